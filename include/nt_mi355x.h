@@ -1,0 +1,184 @@
+/*
+ * nt_mi355x.h — C ABI of the MI355X (gfx950) kernel library libnt_mi355x.so.
+ *
+ * This library stands where the reference's generated launchers stand: the
+ * Triton launch_<name> (reference src/ninetoothed/backends/emitters/triton.py:683-693)
+ * and the CUDA backend's `extern "C" int launch_<name>(ptrs..., int64 dims..., stream)`
+ * (reference src/ninetoothed/backends/emitters/cuda.py:362-380), bound from Python
+ * with ctypes exactly as reference src/ninetoothed/backends/materializers/cuda.py:96-130
+ * binds its library.
+ *
+ * Conventions shared by every entry point:
+ *   - device pointers are `const void*` (inputs) and `void*` (outputs);
+ *   - sizes and strides are int64_t and counted in ELEMENTS, not bytes;
+ *     4-D strides are passed as a host pointer to four int64_t values;
+ *   - the stream is the last argument and every launch is asynchronous on it;
+ *   - the return value is a hipError_t as int: 0 = success, a launch or runtime
+ *     error otherwise, and NT_ERR_INVALID (= hipErrorInvalidValue) when the
+ *     arguments are rejected before anything is launched (null pointers,
+ *     negative sizes, unsupported dtype codes, index ranges beyond int32 where a
+ *     kernel indexes in 32 bits);
+ *   - an empty problem (any size 0) launches nothing and returns 0, as the
+ *     reference's runtime does (reference src/ninetoothed/compiler/runtime.py:1411-1422);
+ *   - the library never allocates device memory: callers own every buffer,
+ *     including the optional conv2d workspace.
+ */
+#ifndef NT_MI355X_H
+#define NT_MI355X_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NT_ABI_VERSION 1
+#define NT_ERR_INVALID 1
+
+/* Element type codes for arguments whose type differs from the entry point's. */
+#define NT_DTYPE_NONE (-1)
+#define NT_DTYPE_F32 0
+#define NT_DTYPE_F16 1
+#define NT_DTYPE_BF16 2
+
+/* Manifest check: returns NT_ABI_VERSION. Replaces the reference's ABI field of
+ * its built manifest (reference src/ninetoothed/compiler/runtime.py:1485-1503). */
+int nt_abi_version(void);
+
+/* ---------------------------------------------------------------------------
+ * Elementwise add: out[i] = lhs[i] + rhs[i] for i < n, each operand addressed as
+ * base + i * stride.  Replaces the launcher of the `add_kernel` application
+ * (reference tests/test_add.py:9-24; elementwise-grid program,
+ * src/ninetoothed/backends/emitters/triton.py:518, 592-594).
+ * ------------------------------------------------------------------------- */
+int nt_add_f32(const void* lhs, int64_t lhs_stride, const void* rhs, int64_t rhs_stride,
+               void* out, int64_t out_stride, int64_t n, hipStream_t stream);
+int nt_add_f16(const void* lhs, int64_t lhs_stride, const void* rhs, int64_t rhs_stride,
+               void* out, int64_t out_stride, int64_t n, hipStream_t stream);
+int nt_add_bf16(const void* lhs, int64_t lhs_stride, const void* rhs, int64_t rhs_stride,
+                void* out, int64_t out_stride, int64_t n, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Row softmax over segments: every row of the [rows, cols] input is cut into
+ * segments of `block` columns (the application's BLOCK_SIZE constexpr) and each
+ * segment is normalised on its own: y = exp(x - max) / sum(exp(x - max)), with
+ * columns past the row end taking the value -inf.  block >= cols gives the usual
+ * full-row softmax.  Math in fp32, result rounded to the element type.
+ * Replaces the launcher of `softmax_kernel` (reference tests/test_softmax.py:10-27;
+ * row-vector schedule, src/ninetoothed/materializers/triton.py:1299-1314).
+ * The column stride must be 1.
+ * ------------------------------------------------------------------------- */
+int nt_softmax_f32(const void* x, int64_t x_row_stride, int64_t x_col_stride,
+                   void* y, int64_t y_row_stride, int64_t y_col_stride,
+                   int64_t rows, int64_t cols, int64_t block, hipStream_t stream);
+int nt_softmax_f16(const void* x, int64_t x_row_stride, int64_t x_col_stride,
+                   void* y, int64_t y_row_stride, int64_t y_col_stride,
+                   int64_t rows, int64_t cols, int64_t block, hipStream_t stream);
+int nt_softmax_bf16(const void* x, int64_t x_row_stride, int64_t x_col_stride,
+                    void* y, int64_t y_row_stride, int64_t y_col_stride,
+                    int64_t rows, int64_t cols, int64_t block, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * 2-D max pooling on an N-C-H-W indexed input:
+ *   y[n,c,p,q] = max over r < kh, s < kw of x[n, c, p*sh - ph + r*dh, q*sw - pw + s*dw],
+ * where positions outside [0,H) x [0,W) read -inf (the arrangement's
+ * `other=float("-inf")`).  Bit-exact: max involves no rounding.
+ * Replaces the launcher of the max_pool2d application
+ * (reference tests/test_max_pool2d.py:13-36; tile(..., floor_mode) semantics
+ * src/ninetoothed/tensor.py:200-286).
+ * ------------------------------------------------------------------------- */
+int nt_max_pool2d_f32(const void* x, const int64_t* x_strides, void* y, const int64_t* y_strides,
+                      int64_t N, int64_t C, int64_t H, int64_t W, int64_t P, int64_t Q,
+                      int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
+                      int64_t dh, int64_t dw, hipStream_t stream);
+int nt_max_pool2d_f16(const void* x, const int64_t* x_strides, void* y, const int64_t* y_strides,
+                      int64_t N, int64_t C, int64_t H, int64_t W, int64_t P, int64_t Q,
+                      int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
+                      int64_t dh, int64_t dw, hipStream_t stream);
+int nt_max_pool2d_bf16(const void* x, const int64_t* x_strides, void* y, const int64_t* y_strides,
+                       int64_t N, int64_t C, int64_t H, int64_t W, int64_t P, int64_t Q,
+                       int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
+                       int64_t dh, int64_t dw, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * GEMM with the addmm epilogue, fp32 accumulation:
+ *   acc[m,n]  = sum_k a[m,k] * b[k,n]
+ *   out[m,n]  = cast_out(beta * c[m,n] + alpha * round(acc[m,n]))     (fp32 math)
+ * `round` rounds acc to `round_dtype` first (NT_DTYPE_NONE = no rounding); it is
+ * the application's `accumulator.to(ntl.float16)` (reference tests/test_matmul.py:47).
+ * c may be NULL (then beta is ignored); c and out have element type `out_dtype`.
+ * Plain matmul is alpha = 1, c = NULL.  Replaces the launchers of the matmul and
+ * addmm applications (reference tests/test_matmul.py:14-47, tests/test_addmm.py:13-38;
+ * blocked-linalg schedule, src/ninetoothed/compiler/passes.py:1070-1084).
+ * a is [M,K] with strides (sa_m, sa_k); b is [K,N] with (sb_k, sb_n); c and out are
+ * [M,N] with (sc_m, sc_n) and (so_m, so_n).  Any strides are accepted; unit
+ * stride along k for a and along n for b takes the vectorised path.
+ * ------------------------------------------------------------------------- */
+int nt_gemm_f16(const void* a, int64_t sa_m, int64_t sa_k, const void* b, int64_t sb_k, int64_t sb_n,
+                const void* c, int64_t sc_m, int64_t sc_n, void* out, int64_t so_m, int64_t so_n,
+                int out_dtype, int64_t M, int64_t N, int64_t K, float alpha, float beta,
+                int round_dtype, hipStream_t stream);
+int nt_gemm_bf16(const void* a, int64_t sa_m, int64_t sa_k, const void* b, int64_t sb_k, int64_t sb_n,
+                 const void* c, int64_t sc_m, int64_t sc_n, void* out, int64_t so_m, int64_t so_n,
+                 int out_dtype, int64_t M, int64_t N, int64_t K, float alpha, float beta,
+                 int round_dtype, hipStream_t stream);
+int nt_gemm_f32(const void* a, int64_t sa_m, int64_t sa_k, const void* b, int64_t sb_k, int64_t sb_n,
+                const void* c, int64_t sc_m, int64_t sc_n, void* out, int64_t so_m, int64_t so_n,
+                int out_dtype, int64_t M, int64_t N, int64_t K, float alpha, float beta,
+                int round_dtype, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * 2-D convolution as an implicit GEMM (cross-correlation, as F.conv2d):
+ *   y[n,k,p,q] = cast_y(round(sum_{c,r,s} x[n,c,p*sh - ph + r*dh, q*sw - pw + s*dw] * w[k,c,r,s]))
+ * with zero outside the input.  The GEMM view is M = N*P*Q, N = K, K = C*R*S, as the
+ * conv2d arrangement builds it (reference tests/test_conv2d.py:14-49, pad
+ * src/ninetoothed/tensor.py:538-563); the body is the matmul application, so
+ * `round_dtype` carries its fp16 cast.  `workspace` (may be NULL) lets the library
+ * re-lay the input and filter for vector loads; nt_conv2d_workspace_size() gives
+ * the bytes it wants for a shape (0 = not used).  With too small a workspace
+ * the direct path runs.
+ * ------------------------------------------------------------------------- */
+int64_t nt_conv2d_workspace_size(int64_t N, int64_t C, int64_t H, int64_t W, int64_t K,
+                                 int64_t R, int64_t S, int64_t ph, int64_t pw, int dtype);
+int nt_conv2d_f16(const void* x, const int64_t* x_strides, const void* w, const int64_t* w_strides,
+                  void* y, const int64_t* y_strides, int y_dtype,
+                  int64_t N, int64_t C, int64_t H, int64_t W, int64_t K, int64_t R, int64_t S,
+                  int64_t P, int64_t Q, int64_t ph, int64_t pw, int64_t sh, int64_t sw,
+                  int64_t dh, int64_t dw, int round_dtype, void* workspace,
+                  int64_t workspace_bytes, hipStream_t stream);
+int nt_conv2d_bf16(const void* x, const int64_t* x_strides, const void* w, const int64_t* w_strides,
+                   void* y, const int64_t* y_strides, int y_dtype,
+                   int64_t N, int64_t C, int64_t H, int64_t W, int64_t K, int64_t R, int64_t S,
+                   int64_t P, int64_t Q, int64_t ph, int64_t pw, int64_t sh, int64_t sw,
+                   int64_t dh, int64_t dw, int round_dtype, void* workspace,
+                   int64_t workspace_bytes, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Fused attention forward (online softmax in base 2), per (b, h):
+ *   qs    = round_in(q * q_scale)                 q_scale = log2(e) * softmax scale
+ *   s_ij  = qs_i . k_j  (fp32),  -inf where j >= Sk or (causal and i < j)
+ *   p_ij  = exp2(s_ij - m_i),  m_i = max_j s_ij,  l_i = sum_j p_ij
+ *   o_i   = cast_o(sum_j round_in(p_ij) * v_j / l_i)
+ * This is the attention application (reference tests/test_attention.py:45-70),
+ * whose q pre-scale is the constant 1.44269504089 and whose causal mask is
+ * q_pos >= k_pos.  Tensors are [B, H, S, D] with arbitrary strides; D <= 128.
+ * ------------------------------------------------------------------------- */
+int nt_attention_f16(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                     const void* v, const int64_t* v_strides, void* o, const int64_t* o_strides,
+                     int o_dtype, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
+                     float q_scale, int causal, hipStream_t stream);
+int nt_attention_bf16(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                      const void* v, const int64_t* v_strides, void* o, const int64_t* o_strides,
+                      int o_dtype, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
+                      float q_scale, int causal, hipStream_t stream);
+int nt_attention_f32(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                     const void* v, const int64_t* v_strides, void* o, const int64_t* o_strides,
+                     int o_dtype, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
+                     float q_scale, int causal, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NT_MI355X_H */

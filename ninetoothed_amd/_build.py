@@ -1,0 +1,91 @@
+"""Build libnt_mi355x.so from the hand-written gfx950 HIP sources in ``csrc/``.
+
+Each ``csrc/*.hip`` file is compiled with ``hipcc --offload-arch=gfx950`` into an
+object in ``_build/`` and the objects are linked into ``libnt_mi355x.so`` next to
+this file.  The library is built in-tree so it travels with the source tree; the
+runtime (``ninetoothed_amd._lib``) only loads what is already built.
+"""
+
+import concurrent.futures
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PACKAGE_DIR = Path(__file__).resolve().parent
+SOURCE_DIR = PACKAGE_DIR / "csrc"
+INCLUDE_DIR = PACKAGE_DIR.parent / "include"
+BUILD_DIR = PACKAGE_DIR / "_build"
+LIBRARY_NAME = "libnt_mi355x.so"
+LIBRARY_PATH = PACKAGE_DIR / LIBRARY_NAME
+OFFLOAD_ARCH = "gfx950"
+
+# Packed-FP32 VALU forms are switched off: hipcc -O3 would otherwise emit them from
+# ordinary float code.
+COMMON_FLAGS = (
+    f"--offload-arch={OFFLOAD_ARCH}",
+    "-O3",
+    "-fPIC",
+    "-std=c++17",
+    "-mcode-object-version=5",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+)
+
+
+def hipcc() -> str:
+    found = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(found).exists():
+        raise RuntimeError("hipcc not found; the ROCm toolchain is required to build libnt_mi355x.so.")
+    return found
+
+
+def sources() -> list[Path]:
+    return sorted(SOURCE_DIR.glob("*.hip"))
+
+
+def _compile(source: Path, extra: tuple[str, ...]) -> Path:
+    obj = BUILD_DIR / (source.stem + ".o")
+    cmd = [
+        hipcc(),
+        *COMMON_FLAGS,
+        *extra,
+        f"-I{INCLUDE_DIR}",
+        f"-I{SOURCE_DIR}",
+        "-c",
+        str(source),
+        "-o",
+        str(obj),
+    ]
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {source.name}:\n{result.stderr}")
+    return obj
+
+
+def build(verbose: bool = False, extra_flags: tuple[str, ...] = (), jobs: int | None = None) -> Path:
+    """Compile every HIP source and link the shared library; returns its path."""
+    BUILD_DIR.mkdir(parents=True, exist_ok=True)
+    srcs = sources()
+    if not srcs:
+        raise RuntimeError(f"no HIP sources under {SOURCE_DIR}")
+    jobs = jobs or min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
+    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
+        objects = list(pool.map(lambda s: _compile(s, tuple(extra_flags)), srcs))
+    tmp = LIBRARY_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"link failed:\n{result.stderr}")
+    os.replace(tmp, LIBRARY_PATH)
+    if verbose:
+        print(f"built {LIBRARY_PATH} from {len(srcs)} sources", file=sys.stderr)
+    return LIBRARY_PATH
+
+
+if __name__ == "__main__":
+    build(verbose=True, extra_flags=tuple(sys.argv[1:]))

@@ -1,0 +1,411 @@
+// Fused attention forward (online softmax in base 2) on the MFMA tile core.
+//
+// One workgroup per (batch, head, block of 128 queries); four waves, each owning 32
+// queries.  Keys and values stream through LDS in tiles of 64.  The kernel works in
+// the transposed frame:
+//   S^T = K . Q^T      (v_mfma_f32_32x32x16: a = K rows from LDS, b = Q^T held in
+//                       registers for the whole key loop)
+//   O^T += V^T . P^T   (a = V^T rows from LDS, b = P^T taken straight from the S^T
+//                       accumulators after exp2 and rounding)
+// In the 32x32 accumulator layout a lane holds one query (lane % 32) and 16 keys, so
+// the per-query max and sum need a single cross-lane exchange (lane ^ 32), the
+// rescale by alpha is a per-lane scalar, and P^T never leaves registers: for the k
+// slice t of 16 keys, slot s of a lane is accumulator register 8*(t%2) + s of key
+// block t/2, i.e. key 16t + (s/4)*8 + (lane/32)*4 + s%4; V^T is fetched with the same
+// key order (two 8-byte LDS reads per fragment).
+// K tiles are stored [d-half][key][64 d] and V^T tiles [d][64 keys], both with the
+// 16-byte chunk swizzle of the MFMA core; V is transposed 8x8 in registers on its way
+// from HBM.  The next key tile is fetched into registers during the current tile's
+// math.  Causal launches stop at the last key tile a query block can see, and the
+// heaviest query blocks are launched first.
+// MFMA-bound: 4 * B * H * Sq * Sk * D flops per launch (half of that when causal).
+#include "mfma_core.h"
+
+namespace nt {
+
+constexpr int AT_BM = 128;  // queries per workgroup
+constexpr int AT_BN = 64;   // keys per tile
+constexpr int AT_THREADS = 256;
+
+struct AttnArgs {
+  const void *q, *k, *v;
+  void* o;
+  int64_t qs[4], ks[4], vs[4], os[4];
+  int64_t B, H, Sq, Sk, D;
+  float q_scale;
+  int causal, o_dtype, q_blocks;
+};
+
+template <typename T, int DM, bool KVEC>  // DM = padded head dim (64 or 128)
+__global__ __launch_bounds__(AT_THREADS) void attention_kernel(AttnArgs g) {
+  typedef typename mfma_traits<T>::frag frag;
+  constexpr int DH = DM / 64;  // 64-wide d halves
+  constexpr int DSUB = DM / 16;
+  constexpr int DBLK = DM / 32;
+  __shared__ __attribute__((aligned(16))) uint16_t sK[DH * AT_BN * TILE_K];
+  __shared__ __attribute__((aligned(16))) uint16_t sVt[DM * TILE_K];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5;
+  // Heaviest (latest) query blocks first.
+  const int qb = g.q_blocks - 1 - (int)(blockIdx.x % g.q_blocks);
+  const int64_t bh = blockIdx.x / g.q_blocks;
+  const int64_t b = bh / g.H, h = bh % g.H;
+  const int64_t q0 = (int64_t)qb * AT_BM;
+  const uint16_t* Q = (const uint16_t*)g.q + b * g.qs[0] + h * g.qs[1];
+  const uint16_t* K = (const uint16_t*)g.k + b * g.ks[0] + h * g.ks[1];
+  const uint16_t* V = (const uint16_t*)g.v + b * g.vs[0] + h * g.vs[1];
+
+  // Q^T fragments of this lane's query, pre-scaled and rounded to the input type.
+  const int64_t qpos = q0 + wave * 32 + (lane & 31);
+  frag qf[DSUB];
+#pragma unroll
+  for (int dd = 0; dd < DSUB; ++dd) {
+    uint16_t tmp[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t d = dd * 16 + half * 8 + u;
+      float x = 0.f;
+      if (qpos < g.Sq && d < g.D) x = elem<T>::to_float(Q[qpos * g.qs[2] + d * g.qs[3]]) * g.q_scale;
+      tmp[u] = elem<T>::from_float(x);
+    }
+    qf[dd] = __builtin_bit_cast(frag, *(const u32x4*)tmp);
+  }
+
+  floatx16 o_acc[DBLK];
+#pragma unroll
+  for (int i = 0; i < DBLK; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o_acc[i][r] = 0.f;
+  float m_i = -INFINITY, l_i = 1.0f;
+
+  int64_t nkt = cdiv(g.Sk, AT_BN);
+  if (g.causal) {
+    const int64_t last = (q0 + AT_BM - 1) / AT_BN + 1;
+    if (last < nkt) nkt = last;
+  }
+
+  // Register staging of one key/value tile.
+  constexpr int K_LOADS = DH * AT_BN * TILE_K / 8 / AT_THREADS;  // 16-byte chunks per lane
+  u32x4 rk[K_LOADS];
+  u32x4 rv[8];
+  const int v_kb = tid & 7;          // key block (8 keys)
+  const int v_db = tid >> 3;         // d block (8 d) ; valid when v_db < DM/8
+  const bool v_active = v_db < DM / 8;
+
+  auto load_tile = [&](int64_t kt) {
+    const int64_t k0 = kt * AT_BN;
+    if (KVEC) {
+#pragma unroll
+      for (int i = 0; i < K_LOADS; ++i) {
+        const int e = i * AT_THREADS + tid;
+        const int key = e / (DM / 8), dch = e % (DM / 8);
+        const int64_t kp = k0 + key;
+        rk[i] = kp < g.Sk ? *(const u32x4*)(K + kp * g.ks[2] + dch * 8) : u32x4{0u, 0u, 0u, 0u};
+      }
+      if (v_active) {
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+          const int64_t kp = k0 + v_kb * 8 + r;
+          rv[r] = kp < g.Sk ? *(const u32x4*)(V + kp * g.vs[2] + v_db * 8) : u32x4{0u, 0u, 0u, 0u};
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < K_LOADS; ++i) {
+        const int e = i * AT_THREADS + tid;
+        const int key = e / (DM / 8), dch = e % (DM / 8);
+        const int64_t kp = k0 + key;
+        uint16_t tmp[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int64_t d = dch * 8 + u;
+          tmp[u] = (kp < g.Sk && d < g.D) ? K[kp * g.ks[2] + d * g.ks[3]] : (uint16_t)0;
+        }
+        rk[i] = *(const u32x4*)tmp;
+      }
+      if (v_active) {
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+          const int64_t kp = k0 + v_kb * 8 + r;
+          uint16_t tmp[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const int64_t d = v_db * 8 + u;
+            tmp[u] = (kp < g.Sk && d < g.D) ? V[kp * g.vs[2] + d * g.vs[3]] : (uint16_t)0;
+          }
+          rv[r] = *(const u32x4*)tmp;
+        }
+      }
+    }
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int i = 0; i < K_LOADS; ++i) {
+      const int e = i * AT_THREADS + tid;
+      const int key = e / (DM / 8), dch = e % (DM / 8);
+      const int hf = dch >> 3, c = dch & 7;
+      *(u32x4*)(sK + hf * AT_BN * TILE_K + key * TILE_K + swz(key, c) * 8) = rk[i];
+    }
+    if (v_active) {
+      u32x4 tv[8];
+      transpose8x8(rv, tv);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int d = v_db * 8 + j;
+        *(u32x4*)(sVt + d * TILE_K + swz(d, v_kb) * 8) = tv[j];
+      }
+    }
+  };
+
+  if (nkt > 0) {
+    load_tile(0);
+    store_tile();
+  }
+  __syncthreads();
+  for (int64_t kt = 0; kt < nkt; ++kt) {
+    if (kt + 1 < nkt) load_tile(kt + 1);
+    const int64_t k0 = kt * AT_BN;
+    // S^T = K . Q^T  (two 32-key blocks)
+    floatx16 s[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[kb][r] = 0.f;
+#pragma unroll
+      for (int dd = 0; dd < DSUB; ++dd) {
+        const int hf = dd >> 2;
+        const int chunk = (dd & 3) * 2 + half;
+        const int row = kb * 32 + (lane & 31);
+        const frag ka = *(const frag*)(sK + hf * AT_BN * TILE_K + row * TILE_K + swz(row, chunk) * 8);
+        s[kb] = mfma_traits<T>::mma(ka, qf[dd], s[kb]);
+      }
+    }
+    // Masks: keys past the end, and keys after the query when causal.
+    const bool need_mask = (k0 + AT_BN > g.Sk) || (g.causal && k0 + AT_BN - 1 > q0 + wave * 32);
+    if (need_mask) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t key = k0 + kb * 32 + acc_row(r, lane);
+          if (key >= g.Sk || (g.causal && qpos < key)) s[kb][r] = -INFINITY;
+        }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_i, mx);
+    float lsum = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = __builtin_amdgcn_exp2f(s[kb][r] - m_new);
+        s[kb][r] = p;
+        lsum += p;
+      }
+    lsum += __shfl_xor(lsum, 32, 64);
+    const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
+    l_i = l_i * alpha + lsum;
+    m_i = m_new;
+#pragma unroll
+    for (int i = 0; i < DBLK; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o_acc[i][r] *= alpha;
+    // O^T += V^T . P^T over four 16-key slices.
+#pragma unroll
+    for (int t = 0; t < AT_BN / 16; ++t) {
+      uint16_t pt[8];
+#pragma unroll
+      for (int sl = 0; sl < 8; ++sl) pt[sl] = elem<T>::from_float(s[t >> 1][8 * (t & 1) + sl]);
+      const frag pf = __builtin_bit_cast(frag, *(const u32x4*)pt);
+#pragma unroll
+      for (int i = 0; i < DBLK; ++i) {
+        const int d = i * 32 + (lane & 31);
+        const uint16_t* rowp = sVt + d * TILE_K;
+        const u32x2 lo = *(const u32x2*)(rowp + swz(d, 2 * t) * 8 + half * 4);
+        const u32x2 hi = *(const u32x2*)(rowp + swz(d, 2 * t + 1) * 8 + half * 4);
+        const frag vf = __builtin_bit_cast(frag, u32x4{lo[0], lo[1], hi[0], hi[1]});
+        o_acc[i] = mfma_traits<T>::mma(vf, pf, o_acc[i]);
+      }
+    }
+    __syncthreads();
+    if (kt + 1 < nkt) {
+      store_tile();
+      __syncthreads();
+    }
+  }
+
+  // o = acc / l
+  if (qpos < g.Sq) {
+    const float inv = 1.0f / l_i;
+    const int64_t obase = b * g.os[0] + h * g.os[1] + qpos * g.os[2];
+#pragma unroll
+    for (int i = 0; i < DBLK; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t d = i * 32 + acc_row(r, lane);
+        if (d < g.D) store_from_float(g.o, obase + d * g.os[3], g.o_dtype, o_acc[i][r] * inv);
+      }
+  }
+}
+
+template <typename T>
+static int attention_launch(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* v,
+                            const int64_t* vs, void* o, const int64_t* os, int o_dtype, int64_t B, int64_t H,
+                            int64_t Sq, int64_t Sk, int64_t D, float q_scale, int causal, hipStream_t stream) {
+  if (B < 0 || H < 0 || Sq < 0 || Sk < 0 || D < 0 || D > 128) return NT_ERR_INVALID;
+  if (!valid_dtype(o_dtype)) return NT_ERR_INVALID;
+  if (B * H * Sq * D == 0) return 0;
+  if (!q || !k || !v || !o || !qs || !ks || !vs || !os) return NT_ERR_INVALID;
+  AttnArgs g{};
+  g.q = q; g.k = k; g.v = v; g.o = o;
+  for (int i = 0; i < 4; ++i) {
+    g.qs[i] = qs[i];
+    g.ks[i] = ks[i];
+    g.vs[i] = vs[i];
+    g.os[i] = os[i];
+  }
+  g.B = B; g.H = H; g.Sq = Sq; g.Sk = Sk; g.D = D;
+  g.q_scale = q_scale;
+  g.causal = causal ? 1 : 0;
+  g.o_dtype = o_dtype;
+  const int64_t qblocks = cdiv(Sq, AT_BM);
+  if (qblocks * B * H > 0x7fffffffLL) return NT_ERR_INVALID;
+  g.q_blocks = (int)qblocks;
+  const dim3 grid((unsigned)(qblocks * B * H)), blk(AT_THREADS);
+  // Vector key/value loads need unit d-stride, 16-byte aligned rows and a full
+  // head dim; the batch/head offsets keep rows aligned when their strides do.
+  auto kvec_ok = [&](int64_t dm) {
+    return ks[3] == 1 && vs[3] == 1 && D == dm && (ks[2] * 2) % 16 == 0 && (vs[2] * 2) % 16 == 0 &&
+           (ks[1] * 2) % 16 == 0 && (vs[1] * 2) % 16 == 0 && (ks[0] * 2) % 16 == 0 && (vs[0] * 2) % 16 == 0 &&
+           (uintptr_t)k % 16 == 0 && (uintptr_t)v % 16 == 0;
+  };
+  if (D <= 64) {
+    if (kvec_ok(64))
+      hipLaunchKernelGGL((attention_kernel<T, 64, true>), grid, blk, 0, stream, g);
+    else
+      hipLaunchKernelGGL((attention_kernel<T, 64, false>), grid, blk, 0, stream, g);
+  } else {
+    if (kvec_ok(128))
+      hipLaunchKernelGGL((attention_kernel<T, 128, true>), grid, blk, 0, stream, g);
+    else
+      hipLaunchKernelGGL((attention_kernel<T, 128, false>), grid, blk, 0, stream, g);
+  }
+  return launch_status();
+}
+
+// fp32 inputs: one lane per query, VALU dot products against key/value tiles staged
+// in LDS (every lane reads the same key, an LDS broadcast).  The q pre-scale and the
+// rounding of p to the value type are exact in fp32.
+constexpr int AF_Q = 64, AF_BN = 32;
+
+__global__ __launch_bounds__(AF_Q) void attention_f32_kernel(AttnArgs g) {
+  __shared__ float sK[AF_BN][128];
+  __shared__ float sV[AF_BN][128];
+  const int tid = threadIdx.x;
+  const int qb = g.q_blocks - 1 - (int)(blockIdx.x % g.q_blocks);
+  const int64_t bh = blockIdx.x / g.q_blocks;
+  const int64_t b = bh / g.H, h = bh % g.H;
+  const int64_t q0 = (int64_t)qb * AF_Q, qpos = q0 + tid;
+  const float* Q = (const float*)g.q + b * g.qs[0] + h * g.qs[1];
+  const float* K = (const float*)g.k + b * g.ks[0] + h * g.ks[1];
+  const float* V = (const float*)g.v + b * g.vs[0] + h * g.vs[1];
+  const int D = (int)g.D;
+  float qv[128], acc[128];
+#pragma unroll
+  for (int d = 0; d < 128; ++d) {
+    qv[d] = (qpos < g.Sq && d < D) ? Q[qpos * g.qs[2] + d * g.qs[3]] * g.q_scale : 0.f;
+    acc[d] = 0.f;
+  }
+  float m_i = -INFINITY, l_i = 1.0f;
+  int64_t nkt = cdiv(g.Sk, AF_BN);
+  if (g.causal) {
+    const int64_t last = (q0 + AF_Q - 1) / AF_BN + 1;
+    if (last < nkt) nkt = last;
+  }
+  for (int64_t kt = 0; kt < nkt; ++kt) {
+    const int64_t k0 = kt * AF_BN;
+    for (int e = tid; e < AF_BN * 128; e += AF_Q) {
+      const int key = e / 128, d = e % 128;
+      const int64_t kp = k0 + key;
+      const bool ok = kp < g.Sk && d < D;
+      sK[key][d] = ok ? K[kp * g.ks[2] + d * g.ks[3]] : 0.f;
+      sV[key][d] = ok ? V[kp * g.vs[2] + d * g.vs[3]] : 0.f;
+    }
+    __syncthreads();
+    float s[AF_BN];
+    float mx = -INFINITY;
+    for (int j = 0; j < AF_BN; ++j) {
+      float dot = 0.f;
+#pragma unroll
+      for (int d = 0; d < 128; ++d) dot = fmaf(qv[d], sK[j][d], dot);
+      const int64_t key = k0 + j;
+      if (key >= g.Sk || (g.causal && qpos < key)) dot = -INFINITY;
+      s[j] = dot;
+      mx = fmaxf(mx, dot);
+    }
+    const float m_new = fmaxf(m_i, mx);
+    const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
+    float lsum = 0.f;
+#pragma unroll
+    for (int d = 0; d < 128; ++d) acc[d] *= alpha;
+    for (int j = 0; j < AF_BN; ++j) {
+      const float p = __builtin_amdgcn_exp2f(s[j] - m_new);
+      lsum += p;
+#pragma unroll
+      for (int d = 0; d < 128; ++d) acc[d] = fmaf(p, sV[j][d], acc[d]);
+    }
+    l_i = l_i * alpha + lsum;
+    m_i = m_new;
+    __syncthreads();
+  }
+  if (qpos < g.Sq) {
+    const float inv = 1.0f / l_i;
+    const int64_t obase = b * g.os[0] + h * g.os[1] + qpos * g.os[2];
+#pragma unroll
+    for (int d = 0; d < 128; ++d)
+      if (d < D) store_from_float(g.o, obase + d * g.os[3], g.o_dtype, acc[d] * inv);
+  }
+}
+
+static int attention_f32_launch(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* v,
+                                const int64_t* vs, void* o, const int64_t* os, int o_dtype, int64_t B, int64_t H,
+                                int64_t Sq, int64_t Sk, int64_t D, float q_scale, int causal, hipStream_t stream) {
+  if (B < 0 || H < 0 || Sq < 0 || Sk < 0 || D < 0 || D > 128) return NT_ERR_INVALID;
+  if (!valid_dtype(o_dtype)) return NT_ERR_INVALID;
+  if (B * H * Sq * D == 0) return 0;
+  if (!q || !k || !v || !o || !qs || !ks || !vs || !os) return NT_ERR_INVALID;
+  AttnArgs g{};
+  g.q = q; g.k = k; g.v = v; g.o = o;
+  for (int i = 0; i < 4; ++i) {
+    g.qs[i] = qs[i];
+    g.ks[i] = ks[i];
+    g.vs[i] = vs[i];
+    g.os[i] = os[i];
+  }
+  g.B = B; g.H = H; g.Sq = Sq; g.Sk = Sk; g.D = D;
+  g.q_scale = q_scale;
+  g.causal = causal ? 1 : 0;
+  g.o_dtype = o_dtype;
+  const int64_t qblocks = cdiv(Sq, AF_Q);
+  if (qblocks * B * H > 0x7fffffffLL) return NT_ERR_INVALID;
+  g.q_blocks = (int)qblocks;
+  hipLaunchKernelGGL(attention_f32_kernel, dim3((unsigned)(qblocks * B * H)), dim3(AF_Q), 0, stream, g);
+  return launch_status();
+}
+
+}  // namespace nt
+
+#define NT_ATTN_PARAMS                                                                                             \
+  const void *q, const int64_t *qs, const void *k, const int64_t *ks, const void *v, const int64_t *vs, void *o,  \
+      const int64_t *os, int o_dtype, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D, float q_scale,     \
+      int causal, hipStream_t stream
+#define NT_ATTN_ARGS q, qs, k, ks, v, vs, o, os, o_dtype, B, H, Sq, Sk, D, q_scale, causal, stream
+
+extern "C" int nt_attention_f16(NT_ATTN_PARAMS) { return nt::attention_launch<nt::f16_t>(NT_ATTN_ARGS); }
+extern "C" int nt_attention_bf16(NT_ATTN_PARAMS) { return nt::attention_launch<nt::bf16_t>(NT_ATTN_ARGS); }
+extern "C" int nt_attention_f32(NT_ATTN_PARAMS) { return nt::attention_f32_launch(NT_ATTN_ARGS); }

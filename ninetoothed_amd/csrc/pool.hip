@@ -1,0 +1,123 @@
+// 2-D max pooling.
+//
+// HBM-bound: every input element of a window grid is read once and every output
+// written once.  Max involves no rounding, so the result is bit-exact for any
+// evaluation order; fp16/bf16 values are compared after an exact widening to fp32.
+//
+// Fast path (the common non-overlapping 2-wide window on 16-bit data, unit inner
+// strides, no padding or dilation): one lane produces 8 consecutive outputs of a
+// row from kh input rows of 16 elements, i.e. 2*kh 16-byte loads and one 16-byte
+// store.  Everything else runs the generic kernel, one lane per output.
+#include "nt_common.h"
+
+namespace nt {
+
+struct PoolShape {
+  int64_t N, C, H, W, P, Q, kh, kw, sh, sw, ph, pw, dh, dw;
+  int64_t xs[4], ys[4];
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void pool_generic_kernel(const typename elem<T>::storage* __restrict__ x,
+                                                           typename elem<T>::storage* __restrict__ y, PoolShape s) {
+  const int64_t total = s.N * s.C * s.P * s.Q;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; o < total; o += stride) {
+    int64_t q = o % s.Q, t = o / s.Q;
+    int64_t p = t % s.P;
+    t /= s.P;
+    int64_t c = t % s.C, n = t / s.C;
+    float m = -INFINITY;
+    const typename elem<T>::storage* xb = x + n * s.xs[0] + c * s.xs[1];
+    for (int64_t r = 0; r < s.kh; ++r) {
+      const int64_t h = p * s.sh - s.ph + r * s.dh;
+      if (h < 0 || h >= s.H) continue;
+      for (int64_t u = 0; u < s.kw; ++u) {
+        const int64_t w = q * s.sw - s.pw + u * s.dw;
+        if (w < 0 || w >= s.W) continue;
+        m = fmaxf(m, elem<T>::to_float(xb[h * s.xs[2] + w * s.xs[3]]));
+      }
+    }
+    y[n * s.ys[0] + c * s.ys[1] + p * s.ys[2] + q * s.ys[3]] = elem<T>::from_float(m);
+  }
+}
+
+// kw == sw == 2, dw == 1, no padding, 16-bit, x/y inner stride 1, Q % 8 == 0,
+// all rows 16-byte aligned, every window inside the input.
+template <typename T>
+__global__ __launch_bounds__(256) void pool_w2_vec_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
+                                                          PoolShape s) {
+  const int64_t qv_per_row = s.Q / 8;
+  const int64_t total = s.N * s.C * s.P * qv_per_row;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t qv = i % qv_per_row;
+    int64_t t = i / qv_per_row;
+    const int64_t p = t % s.P;
+    t /= s.P;
+    const int64_t c = t % s.C, n = t / s.C;
+    const uint16_t* xb = x + n * s.xs[0] + c * s.xs[1] + (p * s.sh) * s.xs[2] + qv * 16;
+    float m[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) m[j] = -INFINITY;
+    for (int64_t r = 0; r < s.kh; ++r) {
+      const uint16_t* row = xb + r * s.dh * s.xs[2];
+      u32x4 a = __builtin_nontemporal_load((const u32x4*)row);
+      u32x4 b = __builtin_nontemporal_load((const u32x4*)(row + 8));
+      const uint16_t* pa = (const uint16_t*)&a;
+      const uint16_t* pb = (const uint16_t*)&b;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        m[j] = fmaxf(m[j], fmaxf(elem<T>::to_float(pa[2 * j]), elem<T>::to_float(pa[2 * j + 1])));
+        m[4 + j] = fmaxf(m[4 + j], fmaxf(elem<T>::to_float(pb[2 * j]), elem<T>::to_float(pb[2 * j + 1])));
+      }
+    }
+    u32x4 out;
+    uint16_t* po = (uint16_t*)&out;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) po[j] = elem<T>::from_float(m[j]);
+    *(u32x4*)(y + n * s.ys[0] + c * s.ys[1] + p * s.ys[2] + qv * 8) = out;
+  }
+}
+
+template <typename T>
+static int pool_launch(const void* x, const int64_t* xs, void* y, const int64_t* ys, int64_t N, int64_t C, int64_t H,
+                       int64_t W, int64_t P, int64_t Q, int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph,
+                       int64_t pw, int64_t dh, int64_t dw, hipStream_t stream) {
+  typedef typename elem<T>::storage S;
+  if (N < 0 || C < 0 || H < 0 || W < 0 || P < 0 || Q < 0 || kh <= 0 || kw <= 0 || sh <= 0 || sw <= 0 || dh <= 0 ||
+      dw <= 0 || ph < 0 || pw < 0)
+    return NT_ERR_INVALID;
+  if (N * C * P * Q == 0) return 0;
+  if (!x || !y || !xs || !ys) return NT_ERR_INVALID;
+  PoolShape s{N, C, H, W, P, Q, kh, kw, sh, sw, ph, pw, dh, dw, {xs[0], xs[1], xs[2], xs[3]}, {ys[0], ys[1], ys[2], ys[3]}};
+  const bool windows_inside = (P - 1) * sh + (kh - 1) * dh < H && (Q - 1) * sw + (kw - 1) * dw < W;
+  const bool fast = sizeof(S) == 2 && kw == 2 && sw == 2 && dw == 1 && ph == 0 && pw == 0 && xs[3] == 1 &&
+                    ys[3] == 1 && Q % 8 == 0 && windows_inside && (uintptr_t)x % 16 == 0 && (uintptr_t)y % 16 == 0 &&
+                    (xs[0] * 2) % 16 == 0 && (xs[1] * 2) % 16 == 0 && (xs[2] * 2) % 16 == 0 &&
+                    (ys[0] * 2) % 16 == 0 && (ys[1] * 2) % 16 == 0 && (ys[2] * 2) % 16 == 0;
+  if (fast) {
+    const int64_t total = N * C * P * (Q / 8);
+    int64_t blocks = cdiv(total, 256);
+    if (blocks > 256 * 32) blocks = 256 * 32;
+    hipLaunchKernelGGL(pool_w2_vec_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, stream, (const uint16_t*)x,
+                       (uint16_t*)y, s);
+  } else {
+    int64_t blocks = cdiv(N * C * P * Q, 256);
+    if (blocks > 256 * 32) blocks = 256 * 32;
+    hipLaunchKernelGGL(pool_generic_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, stream, (const S*)x, (S*)y, s);
+  }
+  return launch_status();
+}
+
+}  // namespace nt
+
+#define NT_POOL_ENTRY(NAME, T)                                                                                      \
+  extern "C" int NAME(const void* x, const int64_t* xs, void* y, const int64_t* ys, int64_t N, int64_t C, int64_t H, \
+                      int64_t W, int64_t P, int64_t Q, int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph,   \
+                      int64_t pw, int64_t dh, int64_t dw, hipStream_t stream) {                                      \
+    return nt::pool_launch<T>(x, xs, y, ys, N, C, H, W, P, Q, kh, kw, sh, sw, ph, pw, dh, dw, stream);              \
+  }
+NT_POOL_ENTRY(nt_max_pool2d_f32, float)
+NT_POOL_ENTRY(nt_max_pool2d_f16, nt::f16_t)
+NT_POOL_ENTRY(nt_max_pool2d_bf16, nt::bf16_t)
