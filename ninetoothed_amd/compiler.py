@@ -1,0 +1,297 @@
+"""Compiler driver: arrangement + application + tensors -> Compilation -> Handle.
+
+Follows the reference's driver (``src/ninetoothed/compiler/driver.py``): ``make``
+(176-216) runs the arrangement on deep copies of the symbolic tensors (283-287),
+lowers the application, asks the selected backend to ``emit`` an ``Artifact``, derives
+the launch ABI (416-495: public arguments in application order, meta/constexpr
+keyword arguments, outputs) and materialises a ``Handle`` through the backend's
+``Materializer``.  ``jit`` takes the arrangement from parameter annotations (272-281).
+
+For the MI355X backend emission does not generate source: it records the program
+(application parameters, arranged tensors, the symbols they use and the schedule
+granularity) and the kernel family is chosen per call-time specialisation, when
+dtypes, shapes, strides and constexpr values are known.
+"""
+
+import copy
+import inspect
+from dataclasses import dataclass, field, replace
+
+from ninetoothed_amd import families, frontend
+from ninetoothed_amd.backends import default_registry
+from ninetoothed_amd.backends.materializers import materializer_for
+from ninetoothed_amd.errors import LoweringError
+from ninetoothed_amd.symbol import default_meta_value
+from ninetoothed_amd.targets import resolve_target_context
+from ninetoothed_amd.tensor import BoundView, Tensor
+
+
+@dataclass(frozen=True)
+class CompileRequest:
+    application: object
+    arrangement: object = None
+    tensors: tuple = None
+    backend: object = None
+    platform: object = None
+    compute_arch: object = None
+    caller: str = "torch"
+    kernel_name: str = None
+    output_dir: object = None
+    num_warps: object = None
+    num_stages: object = None
+    max_num_configs: object = None
+    pipeline: object = None
+    pass_options: object = None
+    backend_options: dict = field(default_factory=dict)
+
+
+@dataclass
+class ParamSpec:
+    name: str
+    source_ndim: int
+    level_ndims: tuple
+    static_shape: tuple
+    dtype: object
+    constexpr: bool
+    shape_symbols: tuple  # (symbol name or None) per source dim
+
+
+@dataclass
+class Compilation:
+    request: CompileRequest
+    kernel: "KernelProgram"
+    artifact: object
+    target: object
+    launch_abi: dict
+
+
+class KernelProgram:
+    """The arranged program, ready to be specialised at call time."""
+
+    def __init__(self, request, params, arranged, specs, symbols, granularity, outputs):
+        self.request = request
+        self.name = request.kernel_name or request.application.__name__
+        self.params = params
+        self.arranged = dict(zip(params, arranged))
+        self.param_specs = specs
+        self.symbols = symbols  # name -> Symbol (meta/constexpr flags)
+        self.granularity = granularity
+        self.outputs = outputs
+
+    @property
+    def meta_args(self):
+        shape_names = {n for s in self.param_specs for n in s.shape_symbols if n}
+        return tuple(sorted(n for n, sym in self.symbols.items() if n not in shape_names and (sym.meta or sym.constexpr)))
+
+    def environment(self, public, meta):
+        env = {}
+        for spec in self.param_specs:
+            if spec.source_ndim == 0:
+                continue
+            for name, size in zip(spec.shape_symbols, public[spec.name].shape):
+                if name is not None:
+                    env[name] = int(size)
+        shape_names = set(env)
+        for name, sym in self.symbols.items():
+            if name in shape_names:
+                continue
+            if name in meta:
+                env[name] = int(meta[name])
+            elif sym.meta:
+                env[name] = default_meta_value(sym)
+            elif sym.constexpr:
+                raise TypeError(f"Missing launch meta-parameter `{name}`.")
+            else:
+                raise TypeError(f"No value for symbol `{name}`.")
+        return env
+
+    def specialize(self, public, meta):
+        env = self.environment(public, meta)
+        views, infos, dtypes = {}, [], {}
+        for spec in self.param_specs:
+            value = public[spec.name]
+            if spec.source_ndim == 0:
+                views[spec.name] = None
+                infos.append(frontend.ParamInfo(spec.name, (), 0, spec.constexpr,
+                                                _plain(value) if spec.constexpr else None))
+                continue
+            view = BoundView(self.arranged[spec.name], env)
+            views[spec.name] = view
+            dtypes[spec.name] = value.dtype
+            infos.append(frontend.ParamInfo(spec.name, tuple(len(s) for s in view.level_shapes[1:]), spec.source_ndim))
+        program = frontend.lower(self.request.application, infos)
+        ctx = families.CallContext(program, views, public, {i.name: i for i in infos}, dtypes)
+        return families.select(ctx)
+
+
+def _plain(v):
+    if hasattr(v, "item"):
+        return v.item()
+    return v
+
+
+def _arrangement_from_annotations(application):
+    sig = inspect.signature(application)
+    annotated = []
+    for name, p in sig.parameters.items():
+        if not isinstance(p.annotation, Tensor):
+            raise LoweringError(f"`jit` needs every parameter annotated with an arranged Tensor (`{name}` is not)")
+        annotated.append(p.annotation)
+
+    def arrangement(*tensors):
+        return tuple(tensors)
+
+    return arrangement, tuple(annotated)
+
+
+def _shape_symbol_names(source):
+    names = []
+    for size in source.shape:
+        names.append(size.name if hasattr(size, "name") and getattr(size, "name", None) else None)
+    return tuple(names)
+
+
+def _discover_outputs(application, params, arranged):
+    """Parameters the application assigns (stores), any constexpr branch included."""
+    infos = []
+    for name, t in zip(params, arranged):
+        if not isinstance(t, Tensor) or t.source.ndim == 0:
+            infos.append(frontend.ParamInfo(name, (), 0, constexpr=bool(getattr(t, "constexpr", False)),
+                                            constexpr_value=_BothBranches()))
+        else:
+            infos.append(frontend.ParamInfo(name, tuple(l.ndim for l in t.levels()[1:]), t.source.ndim))
+    lowerer = _ExploringLowerer(application, infos)
+    program = lowerer.lower()
+    return tuple(n for n in params if n in program.stores), program
+
+
+class _BothBranches:
+    """Marker constexpr value: output discovery walks both arms of an `if`."""
+
+
+class _ExploringLowerer(frontend.Lowerer):
+    def _stmt(self, frame, s):
+        import ast
+
+        if isinstance(s, ast.If):
+            test = self._expr(frame, s.test)
+            if isinstance(test, _BothBranches) or isinstance(test, frontend.Value):
+                self._block(frame, s.body)
+                self._block(frame, s.orelse)
+                return
+        super()._stmt(frame, s)
+
+
+def _granularity(program):
+    """Schedule granularity, in the reference's vocabulary (compiler/passes.py:1070-1084)."""
+    ops = {v.op for value in list(program.stores.values()) + [u for l in program.loops.values() for u in l.update.values()]
+           for v in families._walk(value)}
+    if "dot" in ops and ("math" in ops or "reduce" in ops):
+        return "exp-reduction-dot-region"
+    if "dot" in ops:
+        return "blocked-linalg"
+    if "reduce" in ops:
+        return "parallel-reduction"
+    return "elementwise-grid"
+
+
+def compile_kernel(request):
+    target = resolve_target_context(request.backend, request.platform, request.compute_arch)
+    backend = default_registry().get(target.backend)
+    backend_options = backend.normalize_options(request.backend_options or {})
+    application = request.application
+    params = frontend.parameter_names(application)
+
+    if request.arrangement is None:
+        arrangement, tensors = _arrangement_from_annotations(application)
+    else:
+        arrangement, tensors = request.arrangement, tuple(request.tensors)
+    if len(tensors) != len(params):
+        raise TypeError(f"{len(tensors)} tensors given for an application with {len(params)} parameters")
+    copies = copy.deepcopy(tensors)
+    arranged = arrangement(*copies)
+    if not isinstance(arranged, tuple):
+        arranged = tuple(arranged) if isinstance(arranged, list) else (arranged,)
+    if len(arranged) != len(params):
+        raise LoweringError(f"the arrangement returns {len(arranged)} tensors for {len(params)} application parameters")
+
+    specs, symbols = [], {}
+    for name, original, t in zip(params, tensors, arranged):
+        source = t.source if isinstance(t, Tensor) else t
+        if not isinstance(source, Tensor):
+            raise LoweringError(f"arranged parameter `{name}` is not a Tensor")
+        static = tuple(s if isinstance(s, int) else None for s in source.shape)
+        specs.append(ParamSpec(
+            name=name,
+            source_ndim=source.ndim,
+            level_ndims=tuple(l.ndim for l in t.levels()[1:]) if source.ndim else (),
+            static_shape=static,
+            dtype=source.dtype if isinstance(source.dtype, str) else None,
+            constexpr=bool(source.constexpr),
+            shape_symbols=_shape_symbol_names(source),
+        ))
+        if source.ndim:
+            symbols.update(t.symbols())
+    outputs, explored = _discover_outputs(application, params, arranged)
+    granularity = _granularity(explored)
+    kernel = KernelProgram(request, params, arranged, specs, symbols, granularity, outputs)
+    kernel = backend.prepare_for_emission(kernel)
+    artifact = backend.emit(kernel)
+    abi = {
+        "public_args": tuple(params),
+        "meta_args": kernel.meta_args,
+        "outputs": outputs,
+        "options": dict(backend_options),
+    }
+    return Compilation(request=request, kernel=kernel, artifact=artifact, target=target, launch_abi=abi)
+
+
+class Compiler:
+    def compile(self, request):
+        return compile_kernel(request)
+
+    def materialize(self, request):
+        compilation = self.compile(request)
+        materializer = materializer_for(compilation.target.backend)
+        mode = "jit" if request.caller == "torch" else "aot"
+        if mode == "aot":
+            if request.output_dir is None:
+                raise ValueError("AOT materialization requires an output directory.")
+            return materializer.aot_build(compilation, output_dir=request.output_dir)
+        return materializer.jit_materialize(compilation, output_dir=request.output_dir)
+
+
+DEFAULT_COMPILER = Compiler()
+
+
+def make(arrangement, application, tensors, caller="torch", kernel_name=None, output_dir=None, num_warps=None,
+         num_stages=None, max_num_configs=None, *, backend=None, platform=None, compute_arch=None, pipeline=None,
+         pass_options=None, **backend_options):
+    """``ninetoothed.make`` (reference ``src/ninetoothed/make.py:6-41``) for the MI355X backend.
+
+    ``num_warps``, ``num_stages`` and ``max_num_configs`` are accepted for drop-in
+    compatibility; the hand-written kernels choose their tiles themselves.
+    """
+    return DEFAULT_COMPILER.materialize(CompileRequest(
+        application=application, arrangement=arrangement, tensors=tuple(tensors), backend=backend, platform=platform,
+        compute_arch=compute_arch, caller=caller, kernel_name=kernel_name, output_dir=output_dir, num_warps=num_warps,
+        num_stages=num_stages, max_num_configs=max_num_configs, pipeline=pipeline, pass_options=pass_options,
+        backend_options=backend_options,
+    ))
+
+
+def jit(func=None, *, backend=None, platform=None, compute_arch=None, caller="torch", kernel_name=None, num_warps=None,
+        num_stages=None, max_num_configs=None, pipeline=None, pass_options=None, _prettify=False, **backend_options):
+    """``ninetoothed.jit`` (reference ``src/ninetoothed/compiler/jit.py:6-46``): annotations are the arrangement."""
+    if _prettify:
+        raise NotImplementedError("The legacy `_prettify` source rewrite is not supported.")
+
+    def wrapper(application):
+        return DEFAULT_COMPILER.materialize(CompileRequest(
+            application=application, backend=backend, platform=platform, compute_arch=compute_arch, caller=caller,
+            kernel_name=kernel_name or application.__name__, num_warps=num_warps, num_stages=num_stages,
+            max_num_configs=max_num_configs, pipeline=pipeline, pass_options=pass_options,
+            backend_options=backend_options,
+        ))
+
+    return wrapper if func is None else wrapper(func)

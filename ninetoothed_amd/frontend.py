@@ -1,0 +1,585 @@
+"""Application frontend: a parsed (never executed) application body -> value graph.
+
+Plays the role of the reference's ``from_application``
+(``src/ninetoothed/frontend/python.py:37-91``): the body of an application is parsed
+with ``ast`` and lowered once per specialization (concrete constexpr values fold
+``if`` statements, as the reference's runtime specialization does for non-Triton
+backends, ``src/ninetoothed/compiler/runtime.py:158-243``).  Supported constructs are
+those of the hot-path applications: assignments and augmented assignments, ``for _ in
+range(...)`` loops with loop-carried values, constexpr ``if``, calls to ``ntl``
+functions, ``.to(dtype)``, ``.offsets(dim)``, ``.shape`` / ``.source.shape`` / ``.dtype``,
+level indexing ``x[k]``, broadcasting subscripts ``x[:, None]``, arithmetic and
+comparisons, ``float("-inf")``, and calls to helper applications, which are inlined
+(reference ``_InlineHelperCalls``, ``frontend/python.py:94-306``: a helper that assigns
+to one of its parameters assigns to the caller's variable or tensor it was given).
+
+The result is a graph of hash-consed ``Value`` nodes (structurally equal expressions
+are the same object), plus the loops and the stores (assignments to parameters).
+Family matchers in ``ninetoothed_amd.families`` read this graph.
+"""
+
+import ast
+import builtins
+import inspect
+import math
+import textwrap
+from dataclasses import dataclass, field
+
+from ninetoothed_amd import language as ntl
+from ninetoothed_amd.dtype import normalize_dtype
+from ninetoothed_amd.errors import LoweringError
+
+
+class Value:
+    __slots__ = ("op", "args", "__weakref__")
+
+    def __init__(self, op, args):
+        self.op = op
+        self.args = args
+
+    def __repr__(self):
+        return f"{self.op}({', '.join(_short(a) for a in self.args)})"
+
+
+def _short(a):
+    if isinstance(a, Value):
+        return repr(a) if a.op in ("param", "const", "dtype", "loop_index", "carried") else f"<{a.op}>"
+    return repr(a)
+
+
+VIEW_OPS = ("param", "index")
+
+
+@dataclass
+class Loop:
+    id: int
+    var: str
+    trip: Value
+    init: dict = field(default_factory=dict)
+    update: dict = field(default_factory=dict)
+
+
+@dataclass
+class Program:
+    params: tuple
+    stores: dict  # param name -> stored value (last store)
+    loops: dict  # loop id -> Loop
+    store_order: list
+
+
+@dataclass
+class ParamInfo:
+    """What the frontend needs to know about one application parameter."""
+
+    name: str
+    level_ndims: tuple  # ndim of each level below the program level (level 1 first)
+    source_ndim: int
+    constexpr: bool = False
+    constexpr_value: object = None
+
+
+class _Builder:
+    def __init__(self):
+        self._interned = {}
+
+    def make(self, op, *args):
+        key = (op,) + tuple(id(a) if isinstance(a, Value) else ("#", _freeze(a)) for a in args)
+        v = self._interned.get(key)
+        if v is None:
+            v = Value(op, args)
+            self._interned[key] = v
+        return v
+
+
+def _freeze(a):
+    if isinstance(a, (list, tuple)):
+        return tuple(_freeze(x) for x in a)
+    if isinstance(a, float) and math.isnan(a):
+        return "nan"
+    return a
+
+
+class _Shape:
+    """``x.shape`` of a view or of a value with a known shape."""
+
+    def __init__(self, items):
+        self.items = tuple(items)
+
+    def __getitem__(self, i):
+        return self.items[i]
+
+
+class _Source:
+    def __init__(self, param, ndim):
+        self.param = param
+        self.ndim = ndim
+
+
+class _Method:
+    def __init__(self, name, target):
+        self.name = name
+        self.target = target
+
+
+class _Alias:
+    """A helper parameter bound to the caller's local variable or tensor parameter."""
+
+    def __init__(self, kind, name, frame):
+        self.kind = kind  # "local" | "param"
+        self.name = name
+        self.frame = frame
+
+
+_NTL_BY_ID = {id(getattr(ntl, name)): name for name in ntl._FUNCTIONS}
+_DTYPE_NAMES = {"float16", "bfloat16", "float32", "float64", "int8", "int16", "int32", "int64", "uint8"}
+
+_BINOPS = {ast.Add: "add", ast.Sub: "sub", ast.Mult: "mul", ast.Div: "div", ast.FloorDiv: "floordiv", ast.Mod: "mod"}
+_CMPOPS = {ast.Lt: "lt", ast.LtE: "le", ast.Gt: "gt", ast.GtE: "ge", ast.Eq: "eq", ast.NotEq: "ne"}
+
+
+class _Frame:
+    def __init__(self, func, node, bindings, param_names):
+        self.func = func
+        self.node = node
+        self.env = dict(bindings)
+        self.param_names = set(param_names)
+        self.globals = getattr(func, "__globals__", {})
+        closure = inspect.getclosurevars(func) if func is not None else None
+        self.nonlocals = dict(closure.nonlocals) if closure is not None else {}
+
+
+def parse_function(func):
+    try:
+        source = textwrap.dedent(inspect.getsource(func))
+    except (OSError, TypeError) as exc:
+        raise LoweringError(f"cannot read the source of application `{getattr(func, '__name__', func)}`") from exc
+    module = ast.parse(source)
+    for node in module.body:
+        if isinstance(node, (ast.FunctionDef, ast.AsyncFunctionDef)) and node.name == func.__name__:
+            return node
+    for node in ast.walk(module):
+        if isinstance(node, ast.FunctionDef):
+            return node
+    raise LoweringError(f"no function definition found for `{func.__name__}`")
+
+
+def parameter_names(func):
+    node = parse_function(func)
+    return tuple(a.arg for a in node.args.args)
+
+
+class Lowerer:
+    def __init__(self, application, params):
+        self.b = _Builder()
+        self.params = {p.name: p for p in params}
+        self.loops = {}
+        self.stores = {}
+        self.store_order = []
+        self._loop_ids = 0
+        self.application = application
+
+    # ----------------------------------------------------------------- driver
+    def lower(self):
+        node = parse_function(self.application)
+        names = tuple(a.arg for a in node.args.args)
+        if set(names) != set(self.params):
+            raise LoweringError(f"application parameters {names} do not match the arranged tensors {tuple(self.params)}")
+        bindings = {}
+        for name in names:
+            info = self.params[name]
+            if info.constexpr:
+                bindings[name] = info.constexpr_value
+            else:
+                bindings[name] = self.b.make("param", name)
+        frame = _Frame(self.application, node, bindings, names)
+        self._block(frame, node.body)
+        return Program(names, dict(self.stores), dict(self.loops), list(self.store_order))
+
+    # ----------------------------------------------------------------- values
+    def const(self, v):
+        return self.b.make("const", float(v) if isinstance(v, float) else v)
+
+    def view_level(self, v):
+        if v.op == "param":
+            return 1
+        if v.op == "index":
+            return self.view_level(v.args[0]) + 1
+        raise LoweringError("not a tensor view")
+
+    def view_param(self, v):
+        while v.op == "index":
+            v = v.args[0]
+        return v.args[0]
+
+    def view_ndim(self, v):
+        info = self.params[self.view_param(v)]
+        level = self.view_level(v)
+        if level - 1 >= len(info.level_ndims):
+            return 0
+        return info.level_ndims[level - 1]
+
+    def data(self, v):
+        """A value used as data: tensor views are loaded."""
+        if isinstance(v, Value):
+            if v.op in VIEW_OPS:
+                return self.b.make("load", v)
+            return v
+        if isinstance(v, bool):
+            return self.const(v)
+        if isinstance(v, (int, float)):
+            return self.const(v)
+        raise LoweringError(f"cannot use {v!r} as a tensor value")
+
+    def dtype_value(self, d):
+        if isinstance(d, Value) and d.op in ("dtype_of", "dtype"):
+            return d
+        if isinstance(d, str):
+            name = normalize_dtype(d)
+            if name not in _DTYPE_NAMES:
+                raise LoweringError(f"unknown dtype {d!r}")
+            return self.b.make("dtype", name)
+        raise LoweringError(f"unsupported dtype expression {d!r}")
+
+    # -------------------------------------------------------------- statements
+    def _block(self, frame, stmts):
+        for s in stmts:
+            self._stmt(frame, s)
+
+    def _assign_name(self, frame, name, value):
+        cur = frame.env.get(name)
+        if isinstance(cur, _Alias):
+            if cur.kind == "local":
+                self._assign_name(cur.frame, cur.name, value)
+            else:
+                self._store(cur.name, value)
+            return
+        if name in frame.param_names and isinstance(cur, Value) and cur.op == "param":
+            self._store(cur.args[0], value)
+            return
+        frame.env[name] = value
+
+    def _store(self, param, value):
+        self.stores[param] = self.data(value)
+        self.store_order.append(param)
+
+    def _stmt(self, frame, s):
+        if isinstance(s, ast.Expr):
+            if isinstance(s.value, ast.Constant):
+                return  # docstring
+            self._expr(frame, s.value)
+            return
+        if isinstance(s, ast.Pass):
+            return
+        if isinstance(s, ast.Return):
+            if s.value is not None:
+                raise LoweringError("applications do not return values")
+            return
+        if isinstance(s, ast.Assign):
+            if len(s.targets) != 1:
+                raise LoweringError("chained assignment is not supported")
+            value = self._expr(frame, s.value)
+            self._target(frame, s.targets[0], value)
+            return
+        if isinstance(s, ast.AnnAssign):
+            self._target(frame, s.target, self._expr(frame, s.value))
+            return
+        if isinstance(s, ast.AugAssign):
+            cur = self._expr(frame, s.target)
+            op = _BINOPS.get(type(s.op))
+            if op is None:
+                raise LoweringError(f"unsupported augmented operator {type(s.op).__name__}")
+            self._target(frame, s.target, self._binop(op, cur, self._expr(frame, s.value)))
+            return
+        if isinstance(s, ast.If):
+            test = self._expr(frame, s.test)
+            if isinstance(test, Value):
+                if test.op == "const":
+                    test = test.args[0]
+                else:
+                    raise LoweringError("`if` on run-time data is not supported; branch on constexpr values only")
+            self._block(frame, s.body if test else s.orelse)
+            return
+        if isinstance(s, ast.For):
+            self._for(frame, s)
+            return
+        raise LoweringError(f"unsupported statement `{type(s).__name__}` in an application")
+
+    def _target(self, frame, target, value):
+        if isinstance(target, ast.Name):
+            self._assign_name(frame, target.id, value)
+            return
+        if isinstance(target, ast.Tuple):
+            if not isinstance(value, tuple) or len(value) != len(target.elts):
+                raise LoweringError("tuple unpacking needs a tuple of the same length")
+            for t, v in zip(target.elts, value):
+                self._target(frame, t, v)
+            return
+        raise LoweringError("only simple names can be assigned in an application")
+
+    def _for(self, frame, s):
+        it = s.iter
+        if not (isinstance(it, ast.Call) and isinstance(it.func, ast.Name) and it.func.id == "range" and len(it.args) == 1):
+            raise LoweringError("only `for _ in range(n)` loops are supported")
+        if s.orelse:
+            raise LoweringError("`for ... else` is not supported")
+        if not isinstance(s.target, ast.Name):
+            raise LoweringError("loop variables must be simple names")
+        trip = self.data(self._expr(frame, it.args[0])) if not isinstance(self._expr(frame, it.args[0]), Value) else self._expr(frame, it.args[0])
+        loop_id = self._loop_ids
+        self._loop_ids += 1
+        assigned = _assigned_names(s.body)
+        carried = [n for n in sorted(assigned) if n in frame.env and not isinstance(frame.env[n], (_Alias,))]
+        alias_carried = [n for n in sorted(assigned) if isinstance(frame.env.get(n), _Alias) and frame.env[n].kind == "local"]
+        loop = Loop(loop_id, s.target.id, trip)
+        saved = {}
+        for n in carried:
+            loop.init[n] = frame.env[n]
+            saved[n] = frame.env[n]
+            frame.env[n] = self.b.make("carried", loop_id, n)
+        for n in alias_carried:
+            a = frame.env[n]
+            loop.init[n] = a.frame.env[a.name]
+            a.frame.env[a.name] = self.b.make("carried", loop_id, n)
+        frame.env[s.target.id] = self.b.make("loop_index", loop_id)
+        self._block(frame, s.body)
+        for n in carried:
+            loop.update[n] = frame.env[n]
+            frame.env[n] = self.b.make("loop_out", loop_id, n)
+        for n in alias_carried:
+            a = frame.env[n]
+            loop.update[n] = a.frame.env[a.name]
+            a.frame.env[a.name] = self.b.make("loop_out", loop_id, n)
+        self.loops[loop_id] = loop
+
+    # ------------------------------------------------------------- expressions
+    def _lookup(self, frame, name):
+        if name in frame.env:
+            v = frame.env[name]
+            if isinstance(v, _Alias):
+                if v.kind == "local":
+                    return self._lookup(v.frame, v.name)
+                return v.frame.env[v.name] if v.name in v.frame.env else self.b.make("param", v.name)
+            return v
+        if name in frame.nonlocals:
+            return frame.nonlocals[name]
+        if name in frame.globals:
+            return frame.globals[name]
+        if hasattr(builtins, name):
+            return getattr(builtins, name)
+        raise LoweringError(f"name `{name}` is not defined in the application")
+
+    def _expr(self, frame, e):
+        if isinstance(e, ast.Constant):
+            return e.value
+        if isinstance(e, ast.Name):
+            return self._lookup(frame, e.id)
+        if isinstance(e, ast.Tuple):
+            return tuple(self._expr(frame, x) for x in e.elts)
+        if isinstance(e, ast.Attribute):
+            return self._attribute(frame, self._expr(frame, e.value), e.attr)
+        if isinstance(e, ast.BinOp):
+            op = _BINOPS.get(type(e.op))
+            if op is None:
+                raise LoweringError(f"unsupported operator {type(e.op).__name__}")
+            return self._binop(op, self._expr(frame, e.left), self._expr(frame, e.right))
+        if isinstance(e, ast.UnaryOp):
+            v = self._expr(frame, e.operand)
+            if isinstance(e.op, ast.USub):
+                if isinstance(v, (int, float)):
+                    return -v
+                return self.b.make("neg", self.data(v))
+            if isinstance(e.op, ast.Not) and isinstance(v, (bool, int)):
+                return not v
+            if isinstance(e.op, ast.UAdd):
+                return v
+            raise LoweringError(f"unsupported unary operator {type(e.op).__name__}")
+        if isinstance(e, ast.Compare):
+            if len(e.ops) != 1:
+                raise LoweringError("chained comparisons are not supported")
+            op = _CMPOPS.get(type(e.ops[0]))
+            lhs, rhs = self._expr(frame, e.left), self._expr(frame, e.comparators[0])
+            if not isinstance(lhs, Value) and not isinstance(rhs, Value):
+                return {"lt": lhs < rhs, "le": lhs <= rhs, "gt": lhs > rhs, "ge": lhs >= rhs, "eq": lhs == rhs, "ne": lhs != rhs}[op]
+            return self.b.make(op, self.data(lhs), self.data(rhs))
+        if isinstance(e, ast.BoolOp):
+            vals = [self._expr(frame, x) for x in e.values]
+            if all(not isinstance(v, Value) for v in vals):
+                return all(vals) if isinstance(e.op, ast.And) else any(vals)
+            raise LoweringError("boolean operators on tensors are not supported; use `&` / `|`")
+        if isinstance(e, ast.Subscript):
+            return self._subscript(frame, self._expr(frame, e.value), e.slice)
+        if isinstance(e, ast.Call):
+            return self._call(frame, e)
+        if isinstance(e, ast.List):
+            return tuple(self._expr(frame, x) for x in e.elts)
+        raise LoweringError(f"unsupported expression `{ast.unparse(e)}`")
+
+    def _binop(self, op, lhs, rhs):
+        if not isinstance(lhs, Value) and not isinstance(rhs, Value):
+            return {
+                "add": lambda a, b: a + b, "sub": lambda a, b: a - b, "mul": lambda a, b: a * b,
+                "div": lambda a, b: a / b, "floordiv": lambda a, b: a // b, "mod": lambda a, b: a % b,
+            }[op](lhs, rhs)
+        return self.b.make(op, self.data(lhs), self.data(rhs))
+
+    def _attribute(self, frame, base, attr):
+        if isinstance(base, Value):
+            if attr == "shape":
+                if base.op in VIEW_OPS:
+                    nd = self.view_ndim(base)
+                    return _Shape(self.b.make("shape", base, d) for d in range(nd))
+                if base.op in ("zeros", "full"):
+                    return _Shape(base.args[0])
+                raise LoweringError("`.shape` is only known for tensor parameters and zeros/full values")
+            if attr == "dtype":
+                if base.op in VIEW_OPS:
+                    return self.b.make("dtype_of", base)
+                raise LoweringError("`.dtype` is only supported on tensor parameters")
+            if attr == "source":
+                if base.op != "param":
+                    raise LoweringError("`.source` is only supported on tensor parameters")
+                return _Source(base.args[0], self.params[base.args[0]].source_ndim)
+            if attr in ("to", "offsets"):
+                return _Method(attr, base)
+            raise LoweringError(f"unsupported attribute `.{attr}`")
+        if isinstance(base, _Source):
+            if attr == "shape":
+                return _Shape(self.b.make("source_shape", base.param, d) for d in range(base.ndim))
+            raise LoweringError(f"unsupported attribute `.source.{attr}`")
+        try:
+            return getattr(base, attr)
+        except AttributeError as exc:
+            raise LoweringError(f"`{attr}` not found") from exc
+
+    def _subscript(self, frame, base, sl):
+        if isinstance(base, _Shape):
+            idx = self._expr(frame, sl)
+            if not isinstance(idx, int):
+                raise LoweringError("shape index must be an integer")
+            return base[idx]
+        if isinstance(base, (tuple, list)):
+            return base[self._expr(frame, sl)]
+        if not isinstance(base, Value):
+            raise LoweringError("unsupported subscript")
+        items = sl.elts if isinstance(sl, ast.Tuple) else [sl]
+        if any(isinstance(x, ast.Slice) or (isinstance(x, ast.Constant) and x.value is None) for x in items):
+            pattern = []
+            for x in items:
+                if isinstance(x, ast.Slice):
+                    if x.lower or x.upper or x.step:
+                        raise LoweringError("only `:` and `None` are supported in broadcasting subscripts")
+                    pattern.append(":")
+                elif isinstance(x, ast.Constant) and x.value is None:
+                    pattern.append(None)
+                else:
+                    raise LoweringError("mixed integer/broadcast subscripts are not supported")
+            return self.b.make("bcast", self.data(base), tuple(pattern))
+        if base.op not in VIEW_OPS:
+            raise LoweringError("only tensor parameters can be indexed by level")
+        if len(items) != 1:
+            raise LoweringError("level indexing takes one index")
+        idx = self._expr(frame, items[0])
+        return self.b.make("index", base, self.data(idx) if not isinstance(idx, Value) else idx)
+
+    def _norm_dim(self, d, ndim):
+        if not isinstance(d, int):
+            raise LoweringError("dimension arguments must be integers")
+        return d + ndim if d < 0 else d
+
+    def _call(self, frame, e):
+        func = self._expr(frame, e.func)
+        args = [self._expr(frame, a) for a in e.args]
+        kwargs = {k.arg: self._expr(frame, k.value) for k in e.keywords}
+        if isinstance(func, _Method):
+            t = func.target
+            if func.name == "to":
+                dt = args[0] if args else kwargs.get("dtype")
+                return self.b.make("cast", self.data(t), self.dtype_value(dt))
+            if func.name == "offsets":
+                if t.op not in VIEW_OPS:
+                    raise LoweringError("`.offsets` is only supported on tensor parameters")
+                src_nd = self.params[self.view_param(t)].source_ndim
+                d = self._norm_dim(args[0] if args else kwargs.get("dim", 0), src_nd)
+                return self.b.make("offsets", t, d)
+        if func is float and len(args) == 1 and isinstance(args[0], str):
+            return float(args[0])
+        if func in (float, int, bool, min, max, abs) and all(not isinstance(a, Value) for a in args):
+            return func(*args)
+        name = _NTL_BY_ID.get(id(func))
+        if name is not None:
+            return self._ntl(name, args, kwargs)
+        if inspect.isfunction(func):
+            return self._inline(frame, func, e)
+        raise LoweringError(f"unsupported call `{ast.unparse(e.func)}`")
+
+    def _ntl(self, name, args, kwargs):
+        b = self.b
+        if name in ("zeros", "full"):
+            shape = args[0] if args else kwargs["shape"]
+            if isinstance(shape, _Shape):
+                shape = shape.items
+            shape = tuple(self.data(x) if not isinstance(x, Value) else x for x in shape)
+            if name == "zeros":
+                dt = args[1] if len(args) > 1 else kwargs.get("dtype", "float32")
+                return b.make("zeros", shape, self.dtype_value(dt))
+            value = args[1] if len(args) > 1 else kwargs["value"]
+            dt = args[2] if len(args) > 2 else kwargs.get("dtype", "float32")
+            return b.make("full", shape, float(value), self.dtype_value(dt))
+        if name == "dot":
+            return b.make("dot", self.data(args[0]), self.data(args[1]))
+        if name == "trans":
+            return b.make("trans", self.data(args[0]))
+        if name == "where":
+            return b.make("where", self.data(args[0]), self.data(args[1]), self.data(args[2]))
+        if name in ("max", "min", "sum"):
+            axis = args[1] if len(args) > 1 else kwargs.get("axis")
+            return b.make("reduce", name, self.data(args[0]), axis)
+        if name in ("maximum", "minimum"):
+            return b.make(name, self.data(args[0]), self.data(args[1]))
+        if name in ("exp", "exp2", "log", "log2", "sqrt", "rsqrt", "abs", "sigmoid"):
+            return b.make("math", name, self.data(args[0]))
+        if name == "cast":
+            return b.make("cast", self.data(args[0]), self.dtype_value(args[1] if len(args) > 1 else kwargs["dtype"]))
+        raise LoweringError(f"ntl.{name} is not supported by the MI355X backend")
+
+    def _inline(self, frame, func, call):
+        node = parse_function(func)
+        names = [a.arg for a in node.args.args]
+        if len(call.args) > len(names):
+            raise LoweringError(f"too many arguments for helper `{func.__name__}`")
+        bindings = {}
+        for pname, arg in zip(names, call.args):
+            if isinstance(arg, ast.Name) and arg.id in frame.env:
+                cur = frame.env[arg.id]
+                if isinstance(cur, Value) and cur.op == "param" and arg.id in frame.param_names:
+                    bindings[pname] = _Alias("param", cur.args[0], frame)
+                    continue
+                bindings[pname] = _Alias("local", arg.id, frame)
+            else:
+                bindings[pname] = self._expr(frame, arg)
+        for kw in call.keywords:
+            bindings[kw.arg] = self._expr(frame, kw.value)
+        for pname in names:
+            if pname not in bindings:
+                raise LoweringError(f"missing argument `{pname}` for helper `{func.__name__}`")
+        callee = _Frame(func, node, bindings, names)
+        self._block(callee, node.body)
+        return None
+
+
+def _assigned_names(stmts):
+    out = set()
+    for s in stmts:
+        for node in ast.walk(s):
+            if isinstance(node, (ast.Assign, ast.AugAssign, ast.AnnAssign)):
+                targets = node.targets if isinstance(node, ast.Assign) else [node.target]
+                for t in targets:
+                    for n in ast.walk(t):
+                        if isinstance(n, ast.Name):
+                            out.add(n.id)
+    return out
+
+
+def lower(application, params):
+    """Lower ``application`` for parameters described by ``params`` (ParamInfo list)."""
+    return Lowerer(application, params).lower()

@@ -1,0 +1,131 @@
+"""Handle: the callable that ``make``/``jit`` return, and its call contract.
+
+Mirrors the reference's runtime contract (``src/ninetoothed/compiler/runtime.py``):
+  - ``handle(*public_args, **meta_or_public_kwargs)``, public args in application order;
+  - ``TypeError`` for too many / duplicate / unknown / missing arguments
+    (runtime.py:1147-1185), for rank or static-dim mismatches, for tensors that are not
+    on the GPU (device type ``cuda`` under PyTorch-ROCm) or not all on one GPU
+    (runtime.py:1218-1264), and for dtype mismatches with declared dtypes
+    (runtime.py:1282-1294);
+  - an empty output launches nothing and returns the first output (runtime.py:1411-1422);
+  - otherwise launch on the caller's current stream and return the first output;
+  - a non-zero library status raises ``KernelLaunchError`` (runtime.py:31-35).
+Dtype-less tensors are specialised lazily per call-time key (dtypes, shapes,
+strides, constexpr and meta values), as the reference does for non-Triton backends
+(runtime.py:158-243); each key is matched once to a kernel family and cached.
+"""
+
+import threading
+
+from ninetoothed_amd.dtype import normalize_dtype
+from ninetoothed_amd.errors import KernelLaunchError, LoweringError  # noqa: F401  (re-exported)
+
+
+def _device_type_description(device_types):
+    labels = ["CUDA" if d == "cuda" else d.upper() for d in device_types]
+    return f"a {labels[0]} device" if len(labels) == 1 else f"one of these devices: {', '.join(labels)}"
+
+
+class Handle:
+    """A compiled NineToothed kernel bound to the MI355X backend."""
+
+    def __init__(self, compilation, library_path=None):
+        self._compilation = compilation
+        self._artifact = compilation.artifact
+        self._backend = compilation.target.backend.value
+        self._platform = compilation.target.platform.name
+        self._library = None if library_path is None else str(library_path)
+        self._kernel = compilation.kernel
+        self._abi = compilation.launch_abi
+        self._plans = {}
+        self._lock = threading.Lock()
+        self._device_types = compilation.target.platform.device_types
+
+    # --------------------------------------------------------------- contract
+    def __call__(self, *args, **kwargs):
+        public, meta = self._public_values(args, kwargs)
+        outputs = self._abi["outputs"]
+        if any(hasattr(public.get(n), "numel") and public[n].numel() == 0 for n in outputs):
+            return public[outputs[0]] if outputs else None
+        key = self._key(public, meta)
+        plan = self._plans.get(key)
+        if plan is None:
+            with self._lock:
+                plan = self._plans.get(key)
+                if plan is None:
+                    plan = self._kernel.specialize(public, meta)
+                    self._plans[key] = plan
+        plan.run(public)
+        return public[outputs[0]] if outputs else None
+
+    def _public_values(self, args, kwargs):
+        abi = self._abi
+        names = abi["public_args"]
+        if len(args) > len(names):
+            raise TypeError(f"Expected at most {len(names)} arguments.")
+        positional = names[: len(args)]
+        duplicates = [n for n in positional if n in kwargs]
+        if duplicates:
+            raise TypeError(f"Kernel arguments passed twice: {', '.join(sorted(duplicates))}.")
+        accepted = set(names) | set(abi["meta_args"])
+        unknown = [n for n in kwargs if n not in accepted]
+        if unknown:
+            raise TypeError(f"Unknown kernel arguments: {', '.join(sorted(unknown))}.")
+        values = dict(zip(names, args))
+        meta = {}
+        for k, v in kwargs.items():
+            (values if k in names else meta)[k] = v
+        missing = [n for n in names if n not in values]
+        if missing:
+            raise TypeError(f"Missing kernel arguments: {', '.join(missing)}.")
+        self._validate(values)
+        return values, meta
+
+    def _validate(self, values):
+        expected_device = None
+        for spec in self._kernel.param_specs:
+            value = values[spec.name]
+            if spec.source_ndim == 0:
+                continue
+            shape = getattr(value, "shape", None)
+            if shape is None:
+                raise TypeError(f"Kernel argument `{spec.name}` must be a tensor.")
+            if len(shape) != spec.source_ndim:
+                raise TypeError(f"Kernel argument `{spec.name}` has rank {len(shape)}; expected {spec.source_ndim}.")
+            for axis, (actual, expected) in enumerate(zip(shape, spec.static_shape)):
+                if expected is not None and actual != expected:
+                    raise TypeError(
+                        f"Kernel argument `{spec.name}` has shape {tuple(shape)}; expected dimension {axis} to be {expected}."
+                    )
+            device = getattr(value, "device", None)
+            if device is not None:
+                if device.type not in self._device_types:
+                    raise TypeError(f"Kernel argument `{spec.name}` must be on {_device_type_description(self._device_types)}.")
+                if expected_device is not None and device != expected_device:
+                    raise TypeError("All tensor arguments must use the same CUDA device.")
+                expected_device = expected_device or device
+            if spec.dtype is not None and hasattr(value, "dtype"):
+                actual = str(value.dtype).split(".")[-1]
+                expected = normalize_dtype(spec.dtype)
+                if actual != expected:
+                    raise TypeError(f"Kernel argument `{spec.name}` has dtype {actual}; expected {expected}.")
+
+    def _key(self, public, meta):
+        parts = []
+        for spec in self._kernel.param_specs:
+            v = public[spec.name]
+            if spec.source_ndim == 0:
+                parts.append((spec.name, v if spec.constexpr else type(v).__name__))
+            else:
+                parts.append((spec.name, v.dtype, tuple(v.shape), v.stride()))
+        parts.append(tuple(sorted(meta.items())))
+        return tuple(parts)
+
+    # ---------------------------------------------------------- introspection
+    def plans(self):
+        """Matched kernel families so far, one per specialisation key."""
+        return [p.describe() for p in self._plans.values()]
+
+    @property
+    def library(self):
+        return self._library

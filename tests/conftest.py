@@ -25,3 +25,13 @@ def _seed_per_test(request):
 
 def gpu_available():
     return torch.cuda.is_available()
+
+
+import os
+import sys
+
+# tests/programs.py and the repository root (for `oracle`) on the path.
+_HERE = os.path.dirname(os.path.abspath(__file__))
+for _p in (_HERE, os.path.dirname(_HERE)):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)

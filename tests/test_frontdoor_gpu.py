@@ -1,0 +1,226 @@
+"""The reference's known-answer tests, run through the drop-in ``make``/``jit`` front door.
+
+Each test builds the kernel exactly as a NineToothed user would (arrangement +
+application + symbolic tensors, tests/programs.py), calls it on seeded GPU tensors,
+and checks the result against (a) the reference test's own torch oracle and
+tolerance where that is meaningful on MI355X, and (b) this build's CPU oracle
+(``oracle.apply``, the tile-by-tile restatement of the application) on the same
+inputs.  It also asserts that the call really went through libnt_mi355x.so.
+"""
+
+import functools
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import ninetoothed_amd as ninetoothed
+import programs as pg
+from ninetoothed_amd import _lib
+from oracle import apply
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _gen(seed):
+    g = torch.Generator(device="cpu")
+    g.manual_seed(seed)
+    return g
+
+
+def _randn(shape, dtype, seed, scale=1.0):
+    return (torch.randn(shape, generator=_gen(seed)) * scale).to(dtype).to(DEV)
+
+
+def _rand(shape, dtype, seed, lo=0.0, hi=1.0):
+    return (torch.rand(shape, generator=_gen(seed)) * (hi - lo) + lo).to(dtype).to(DEV)
+
+
+def _np(t):
+    return t.float().cpu().numpy()
+
+
+@pytest.fixture(autouse=True)
+def _no_tf32():
+    torch.backends.cuda.matmul.allow_tf32 = False
+    yield
+
+
+def test_native_library_is_loaded():
+    import ctypes  # noqa: F401
+
+    lib = _lib.load()
+    assert lib.nt_abi_version() == _lib.ABI_VERSION
+    maps = open("/proc/self/maps").read()
+    assert "libnt_mi355x.so" in maps
+
+
+# ------------------------------------------------------------------------ matmul
+def test_matmul_reference_case():
+    m = n = k = 512
+    lhs, rhs = _randn((m, k), torch.float16, 1), _randn((k, n), torch.float16, 2)
+    output = torch.empty((m, n), dtype=torch.float16, device=DEV)
+    kernel = ninetoothed.make(pg.matmul_arrangement, pg.matmul_application, pg.matmul_tensors())
+    assert kernel(lhs, rhs, output) is output
+    expected = torch.matmul(lhs.float(), rhs.float()).half()
+    assert torch.allclose(output, expected, atol=1e-2, rtol=1e-2)
+    ref = apply.matmul(_np(lhs), _np(rhs), "float16", pg.matmul_arrangement, block=(64, 64, 64))
+    assert np.allclose(_np(output), ref, atol=1e-2, rtol=1e-2)
+    assert kernel.plans()[0]["family"] == "gemm"
+
+
+def test_matmul_fp32_readme_case():
+    lhs, rhs = _randn((512, 512), torch.float32, 3), _randn((512, 512), torch.float32, 4)
+    output = torch.empty((512, 512), device=DEV)
+    kernel = ninetoothed.make(pg.matmul_arrangement, pg.matmul_application_fp32, pg.matmul_tensors())
+    kernel(lhs, rhs, output)
+    assert torch.allclose(output, (lhs.double() @ rhs.double()).float(), atol=1e-4, rtol=1e-4)
+
+
+# ------------------------------------------------------------------------- addmm
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+def test_addmm_reference_case(dtype):
+    m = n = k = 512
+    input, mat1, mat2 = _randn((m, n), dtype, 5), _randn((m, k), dtype, 6), _randn((k, n), dtype, 7)
+    beta, alpha = 0.3723, 0.8391
+    output = torch.empty((m, n), dtype=dtype, device=DEV)
+    kernel = ninetoothed.make(pg.addmm_arrangement, pg.addmm_application, pg.addmm_tensors())
+    kernel(input, mat1, mat2, beta, alpha, output)
+    ref = apply.addmm(_np(input), _np(mat1), _np(mat2), beta, alpha, "float16" if dtype == torch.float16 else "bfloat16",
+                      pg.addmm_arrangement, block=(64, 64, 64))
+    assert np.allclose(_np(output), ref, atol=2e-2, rtol=1e-2)
+    if dtype == torch.float16:
+        # The reference test's own oracle and tolerance.
+        assert torch.allclose(output, torch.addmm(input, mat1, mat2, beta=beta, alpha=alpha), atol=0.075)
+
+
+def test_addmm_headline_shape():
+    m = n = k = 4096
+    s = 1.0 / math.sqrt(k)
+    input, mat1, mat2 = (_randn((4096, 4096), torch.float16, 8 + i, s) for i in range(3))
+    output = torch.empty_like(input)
+    kernel = ninetoothed.make(pg.addmm_arrangement, pg.addmm_application, pg.addmm_tensors())
+    kernel(input, mat1, mat2, 0.5, 1.0, output)
+    ref = (0.5 * input.float() + (mat1.float() @ mat2.float()).half().float()).half()
+    assert torch.allclose(output, ref, atol=1e-2, rtol=1e-2)
+
+
+# ------------------------------------------------------------------------ conv2d
+@pytest.mark.parametrize("padding", (0, (1, 1), (0, 1), (2, 0)))
+def test_conv2d_reference_case(padding):
+    x, w = _rand((4, 64, 16, 16), torch.float16, 11), _rand((512, 64, 3, 3), torch.float16, 12)
+    pad = (padding, padding) if isinstance(padding, int) else padding
+    p, q = 16 + 2 * pad[0] - 2, 16 + 2 * pad[1] - 2
+    y = torch.empty((4, 512, p, q), dtype=torch.float16, device=DEV)
+    kernel = pg.make_conv2d()
+    kernel(x, w, y, padding_h=pad[0], padding_w=pad[1])
+    expected = F.conv2d(x.float(), w.float(), padding=pad).half()
+    assert torch.allclose(y, expected, rtol=1e-3, atol=1e-3)  # the reference test's tolerance
+    ref = apply.conv2d(_np(x), _np(w), pad, functools.partial(pg.conv2d_arrangement, enable_padding=True),
+                       block=(64, 64, 64))
+    assert np.allclose(_np(y), ref, rtol=1e-3, atol=1e-3)
+
+
+def test_conv2d_headline_shape():
+    x = _randn((16, 256, 56, 56), torch.float16, 13)
+    w = _randn((256, 256, 3, 3), torch.float16, 14, 1.0 / math.sqrt(256 * 9))
+    y = torch.empty_like(x)
+    pg.make_conv2d()(x, w, y, padding_h=1, padding_w=1)
+    assert torch.allclose(y.float(), F.conv2d(x.float(), w.float(), padding=1), atol=1e-2, rtol=1e-2)
+
+
+# --------------------------------------------------------------------- attention
+@pytest.mark.parametrize("is_causal", (False, True))
+@pytest.mark.parametrize("seq_len", (1024, 1))
+@pytest.mark.parametrize("dtype, tol", ((torch.float32, 0.025), (torch.float16, 0.01)))
+def test_attention_reference_case(is_causal, seq_len, dtype, tol):
+    q, k, v = (_randn((2, 4, seq_len, 64), dtype, 20 + i) for i in range(3))
+    o = torch.empty_like(q)
+    kernel = ninetoothed.make(pg.attention_arrangement, pg.attention_application, pg.attention_tensors())
+    kernel(q, k, v, is_causal, o)
+    expected = F.scaled_dot_product_attention(q.float(), k.float(), v.float(), is_causal=is_causal, scale=1)
+    assert torch.allclose(o.float(), expected, rtol=tol, atol=tol)
+    if dtype == torch.float16 and seq_len == 1024:
+        ref = apply.attention(_np(q[:1, :2]), _np(k[:1, :2]), _np(v[:1, :2]), is_causal, pg.attention_arrangement,
+                              block=(64, 64))
+        assert np.allclose(_np(o[:1, :2]), ref, atol=5e-3, rtol=5e-3)
+
+
+@pytest.mark.parametrize("is_causal", (False, True))
+def test_attention_headline_scaled(is_causal):
+    q, k, v = (_randn((4, 32, 4096, 128), torch.float16, 30 + i) for i in range(3))
+    o = torch.empty_like(q)
+    kernel = ninetoothed.make(pg.attention_arrangement, pg.attention_application_scaled, pg.attention_tensors())
+    kernel(q, k, v, is_causal, o)
+    expected = F.scaled_dot_product_attention(q[:1, :2].float(), k[:1, :2].float(), v[:1, :2].float(),
+                                              is_causal=is_causal, scale=1 / math.sqrt(128))
+    assert torch.allclose(o[:1, :2].float(), expected, atol=1e-2, rtol=1e-2)
+
+
+# ----------------------------------------------------------------------- softmax
+def test_softmax_reference_case():
+    x = _rand((1823, 781), torch.float32, 40)
+    y = pg.make_softmax()
+    out = torch.empty_like(x)
+    y(x, out, BLOCK_SIZE=x.shape[-1])
+    assert torch.allclose(out, torch.softmax(x, dim=-1))
+    assert np.allclose(_np(out), apply.softmax(_np(x), 781), atol=1e-6, rtol=1e-5)
+
+
+def test_softmax_headline_shape():
+    x = _randn((8192, 8192), torch.float16, 41, 2.0)
+    out = torch.empty_like(x)
+    pg.make_softmax()(x, out, BLOCK_SIZE=8192)
+    assert torch.allclose(out.float(), torch.softmax(x.float(), -1), atol=1e-2, rtol=1e-2)
+
+
+def test_softmax_partial_block():
+    x = _randn((33, 1000), torch.float32, 42)
+    out = torch.empty_like(x)
+    pg.make_softmax()(x, out, BLOCK_SIZE=256)
+    assert np.allclose(_np(out), apply.softmax(_np(x), 256), atol=1e-6, rtol=1e-5)
+
+
+# -------------------------------------------------------------------- max_pool2d
+@pytest.mark.parametrize("ceil_mode", (False, True))
+def test_max_pool2d_reference_case(ceil_mode):
+    x = _randn((32, 3, 64, 64), torch.float16, 50)
+    div = (lambda a, b: (a + b - 1) // b) if ceil_mode else (lambda a, b: a // b)
+    p = q = div(64 - 3, 3) + 1
+    y = torch.empty((32, 3, p, q), dtype=torch.float16, device=DEV)
+    kernel = ninetoothed.make(functools.partial(pg.max_pool2d_arrangement, ceil_mode=ceil_mode),
+                              pg.max_pool2d_application, pg.max_pool2d_tensors())
+    kernel(x, y, WINDOW_HEIGHT=3, WINDOW_WIDTH=3)
+    assert torch.equal(y, F.max_pool2d(x, (3, 3), ceil_mode=ceil_mode))
+    ref = apply.max_pool2d(_np(x), (3, 3), ceil_mode, functools.partial(pg.max_pool2d_arrangement, ceil_mode=ceil_mode))
+    assert np.array_equal(_np(y), ref)
+
+
+def test_max_pool2d_headline_shape():
+    x = _rand((32, 128, 112, 112), torch.float16, 51, -1.0, 1.0)
+    y = torch.empty((32, 128, 56, 56), dtype=torch.float16, device=DEV)
+    kernel = ninetoothed.make(functools.partial(pg.max_pool2d_arrangement, ceil_mode=False), pg.max_pool2d_application,
+                              pg.max_pool2d_tensors())
+    kernel(x, y, WINDOW_HEIGHT=2, WINDOW_WIDTH=2)
+    assert torch.equal(y, F.max_pool2d(x, (2, 2)))
+
+
+# --------------------------------------------------------------------------- add
+@pytest.mark.parametrize("size", (98432, 1, 1000003))
+def test_add_reference_case(size):
+    lhs, rhs = _rand((size,), torch.float32, 60), _rand((size,), torch.float32, 61)
+    out = torch.empty_like(lhs)
+    pg.make_add()(lhs, rhs, out)
+    assert torch.allclose(out, lhs + rhs)
+    assert np.array_equal(_np(out), apply.add(_np(lhs), _np(rhs), 64))
+
+
+def test_empty_output_launches_nothing():
+    kernel = ninetoothed.make(pg.matmul_arrangement, pg.matmul_application, pg.matmul_tensors())
+    out = torch.empty((0, 8), dtype=torch.float16, device=DEV)
+    assert kernel(torch.empty((0, 4), dtype=torch.float16, device=DEV),
+                  torch.empty((4, 8), dtype=torch.float16, device=DEV), out) is out

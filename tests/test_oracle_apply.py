@@ -1,0 +1,132 @@
+"""Pin the oracle's tile-by-tile applications to closed forms, invariants and brute force.
+
+Closed forms are torch CPU float64 (matmul, conv2d, softmax, max_pool2d,
+scaled_dot_product_attention) computed from the same rounded inputs; a plausible
+slip in the oracle (a transposed operand, a dropped padding row, a wrong causal
+direction, a missing rescale by alpha, the divisor l) fails one of them.
+"""
+
+import functools
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import programs as pg
+from oracle import apply
+
+
+def _rng(seed):
+    return np.random.default_rng(seed)
+
+
+def _f16(x):
+    return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
+@pytest.mark.parametrize("mnk,block", (((33, 20, 17), (16, 8, 4)), ((64, 48, 40), (16, 16, 16))))
+def test_matmul_closed_form(mnk, block):
+    m, n, k = mnk
+    r = _rng(1)
+    a, b = _f16(r.standard_normal((m, k))), _f16(r.standard_normal((k, n)))
+    got = apply.matmul(a, b, "float16", pg.matmul_arrangement, block=block)
+    ref = _f16(torch.from_numpy(a).double() @ torch.from_numpy(b).double())
+    assert np.allclose(got, ref, atol=1e-2, rtol=1e-3)
+
+
+def test_matmul_fp32_closed_form():
+    r = _rng(2)
+    a, b = r.standard_normal((40, 24)).astype(np.float32), r.standard_normal((24, 36)).astype(np.float32)
+    got = apply.matmul(a, b, "float32", pg.matmul_arrangement, block=(16, 16, 8), round_dtype=None)
+    assert np.allclose(got, a.astype(np.float64) @ b.astype(np.float64), atol=1e-4, rtol=1e-4)
+
+
+def test_addmm_closed_form():
+    r = _rng(3)
+    c, a, b = (_f16(r.standard_normal(s)) for s in ((24, 20), (24, 30), (30, 20)))
+    got = apply.addmm(c, a, b, 0.3, 0.7, "float16", pg.addmm_arrangement, block=(8, 8, 8))
+    ref = torch.addmm(torch.from_numpy(c).double(), torch.from_numpy(a).double(), torch.from_numpy(b).double(),
+                      beta=0.3, alpha=0.7).numpy()
+    assert np.allclose(got, ref, atol=2e-2)
+
+
+@pytest.mark.parametrize("padding", ((0, 0), (1, 1), (0, 1), (2, 0)))
+def test_conv2d_closed_form(padding):
+    r = _rng(4)
+    x = _f16(r.random((2, 5, 7, 6)))
+    w = _f16(r.random((6, 5, 3, 3)))
+    arrangement = functools.partial(pg.conv2d_arrangement, enable_padding=True)
+    got = apply.conv2d(x, w, padding, arrangement, block=(16, 8, 8))
+    ref = F.conv2d(torch.from_numpy(x).double(), torch.from_numpy(w).double(), padding=padding).numpy()
+    assert np.allclose(got, ref, atol=2e-2, rtol=2e-3)
+
+
+def test_conv2d_delta_filter_is_identity():
+    # A 3x3 filter with a single centre tap on channel c -> k is a channel copy (padding 1).
+    r = _rng(5)
+    x = _f16(r.random((1, 2, 5, 5)))
+    w = np.zeros((2, 2, 3, 3), dtype=np.float32)
+    w[0, 1, 1, 1] = 1.0
+    w[1, 0, 1, 1] = 1.0
+    arrangement = functools.partial(pg.conv2d_arrangement, enable_padding=True)
+    got = apply.conv2d(x, w, (1, 1), arrangement, block=(8, 8, 8))
+    assert np.array_equal(got[0, 0], x[0, 1]) and np.array_equal(got[0, 1], x[0, 0])
+
+
+def _sdpa(q, k, v, causal, scale):
+    t = [torch.from_numpy(a).double() for a in (q, k, v)]
+    return F.scaled_dot_product_attention(*t, is_causal=causal, scale=scale).numpy()
+
+
+@pytest.mark.parametrize("causal", (False, True))
+@pytest.mark.parametrize("seq", (19, 1))
+def test_attention_closed_form(seq, causal):
+    r = _rng(6)
+    q, k, v = (_f16(r.standard_normal((1, 2, seq, 8))) for _ in range(3))
+    got = apply.attention(q, k, v, causal, pg.attention_arrangement, block=(8, 4))
+    # The reference constant 1.44269504089 becomes the fp16 1.4423828125: scores are
+    # scaled by c16 / log2(e) in the natural-exp softmax.
+    c16 = float(np.float16(1.44269504089))
+    ref = _sdpa(q, k, v, causal, c16 / math.log2(math.e))
+    assert np.allclose(got, ref, atol=1e-2, rtol=1e-2)
+
+
+def test_attention_invariants():
+    r = _rng(7)
+    q, k = (_f16(r.standard_normal((1, 1, 6, 4))) for _ in range(2))
+    v = _f16(r.standard_normal((1, 1, 6, 4)))
+    out = apply.attention(q, k, v, True, pg.attention_arrangement, block=(4, 2))
+    assert np.allclose(out[0, 0, 0], v[0, 0, 0], atol=1e-3)  # causal row 0 sees only key 0
+    same_keys = np.repeat(k[:, :, :1], 6, axis=2)
+    out2 = apply.attention(q, same_keys, v, False, pg.attention_arrangement, block=(4, 2))
+    assert np.allclose(out2[0, 0], np.broadcast_to(v[0, 0].mean(0), (6, 4)), atol=2e-3)  # equal keys -> mean(v)
+
+
+@pytest.mark.parametrize("block", (781, 128))
+def test_softmax_closed_form(block):
+    r = _rng(8)
+    x = r.random((9, 781)).astype(np.float32)
+    got = apply.softmax(x, block)
+    xp = np.pad(x, ((0, 0), (0, -(-781 // block) * block - 781)), constant_values=-np.inf)
+    ref = torch.softmax(torch.from_numpy(xp).double().view(9, -1, block), -1).view(9, -1)[:, :781].numpy()
+    assert np.allclose(got, ref, atol=1e-7, rtol=1e-5)
+    if block == 781:
+        assert np.allclose(got.sum(1), 1.0, atol=1e-5)
+
+
+@pytest.mark.parametrize("ceil_mode", (False, True))
+def test_max_pool2d_closed_form(ceil_mode):
+    r = _rng(9)
+    x = _f16(r.standard_normal((2, 3, 10, 11)))
+    arrangement = functools.partial(pg.max_pool2d_arrangement, ceil_mode=ceil_mode)
+    got = apply.max_pool2d(x, (3, 3), ceil_mode, arrangement, block=8)
+    ref = F.max_pool2d(torch.from_numpy(x), (3, 3), ceil_mode=ceil_mode).numpy()
+    assert np.array_equal(got, ref)
+
+
+def test_add_closed_form():
+    r = _rng(10)
+    a, b = r.random(1000).astype(np.float32), r.random(1000).astype(np.float32)
+    assert np.array_equal(apply.add(a, b, 256), a + b)
