@@ -37,6 +37,8 @@ def _args():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--only", default="")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="only run a plain 256 MiB device copy K times (scale for rocprofv3 FETCH/WRITE_SIZE)")
     return p.parse_args()
 
 
@@ -187,6 +189,14 @@ def main():
               "(the hot path is single-GPU; see DESIGN.md for how it would shard).", file=sys.stderr)
         sys.exit(2)
     import torch
+
+    if args.calibrate_copy:
+        x = torch.empty(64 * 1024 * 1024, dtype=torch.float32, device="cuda").fill_(1.0)
+        y = torch.empty_like(x)
+        sec, _ = _time(torch, lambda: y.copy_(x), args.steps, args.warmup)
+        print(json.dumps({"calibration": "copy", "bytes_read": x.numel() * 4, "bytes_written": y.numel() * 4,
+                          "ms_per_copy": sec * 1e3}), flush=True)
+        return
 
     import ninetoothed_amd as ninetoothed
     import programs as pg

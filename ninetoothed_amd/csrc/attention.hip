@@ -42,8 +42,11 @@ __global__ __launch_bounds__(AT_THREADS) void attention_kernel(AttnArgs g) {
   constexpr int DH = DM / 64;  // 64-wide d halves
   constexpr int DSUB = DM / 16;
   constexpr int DBLK = DM / 32;
-  __shared__ __attribute__((aligned(16))) uint16_t sK[DH * AT_BN * TILE_K];
-  __shared__ __attribute__((aligned(16))) uint16_t sVt[DM * TILE_K];
+  // K tile, V^T tile; reused at the end to stage the output (32 KiB either way).
+  __shared__ __attribute__((aligned(16))) uint16_t smem[16384];
+  uint16_t* sK = smem;
+  uint16_t* sVt = smem + DH * AT_BN * TILE_K;
+  static_assert(DH * AT_BN * TILE_K + DM * TILE_K <= 16384, "LDS tiles exceed the allocation");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5;
   // Heaviest (latest) query blocks first.
@@ -239,17 +242,44 @@ __global__ __launch_bounds__(AT_THREADS) void attention_kernel(AttnArgs g) {
     }
   }
 
-  // o = acc / l
-  if (qpos < g.Sq) {
+  // o = acc / l, staged through LDS per 64-wide slice of d so that each lane then
+  // writes 4 consecutive d of one query row (lanes 0-15 cover 64 d of a row).
+  {
     const float inv = 1.0f / l_i;
-    const int64_t obase = b * g.os[0] + h * g.os[1] + qpos * g.os[2];
+    float* stage = reinterpret_cast<float*>(smem) + wave * (32 * 64);
+    constexpr int PASSES = (DM + 63) / 64;
 #pragma unroll
-    for (int i = 0; i < DBLK; ++i)
+    for (int ps = 0; ps < PASSES; ++ps) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t d = i * 32 + acc_row(r, lane);
-        if (d < g.D) store_from_float(g.o, obase + d * g.os[3], g.o_dtype, o_acc[i][r] * inv);
+      for (int jb = 0; jb < 2; ++jb) {
+        if (ps * 2 + jb < DBLK) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            stage[(lane & 31) * 64 + jb * 32 + acc_row(r, lane)] = o_acc[ps * 2 + jb][r] * inv;
+        }
       }
+      __syncthreads();
+      for (int e = lane; e < 32 * 16; e += 64) {
+        const int row = e >> 4, grp = (e & 15) * 4;
+        const int64_t qp = q0 + wave * 32 + row;
+        const int d0 = ps * 64 + grp;
+        if (qp >= g.Sq || d0 >= g.D) continue;
+        const float4 v4 = *(const float4*)(stage + row * 64 + grp);
+        const int64_t ob = b * g.os[0] + h * g.os[1] + qp * g.os[2];
+        if (g.o_dtype != NT_DTYPE_F32 && g.os[3] == 1 && d0 + 4 <= g.D && ((ob + d0) & 3) == 0) {
+          uint16_t hv[4];
+          const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            hv[u] = g.o_dtype == NT_DTYPE_F16 ? float_to_f16_bits(vv[u]) : float_to_bf16_bits(vv[u]);
+          *(u32x2*)((uint16_t*)g.o + ob + d0) = *(const u32x2*)hv;
+        } else {
+          const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+          for (int u = 0; u < 4 && d0 + u < g.D; ++u) store_from_float(g.o, ob + (d0 + u) * g.os[3], g.o_dtype, vv[u]);
+        }
+      }
+      __syncthreads();
+    }
   }
 }
 
