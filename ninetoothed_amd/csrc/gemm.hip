@@ -1,9 +1,8 @@
 // GEMM with the addmm epilogue:  out = cast_out(beta * c + alpha * round(sum_k a*b)).
 //
 // fp16 / bf16 (MFMA-bound; 2*M*N*K flops per launch):
-//   workgroup tile 256 x 256 x 64, 256 lanes = 4 waves in a 2 x 2 grid, each wave
-//   owning a 128 x 128 sub-tile as 4 x 4 v_mfma_f32_32x32x16_{f16,bf16} blocks
-//   (256 fp32 accumulators per lane).  Both operands sit in LDS k-contiguous
+//   workgroup tile 256 x 256 x 64 on v_mfma_f32_32x32x16_{f16,bf16}; the fast path runs
+//   8 waves (64 x 128 each), the generic path 4 waves (128 x 128 each).  Both operands sit in LDS k-contiguous
 //   ([m][k] for a, [n][k] for b) so that each lane fetches its 8 k-values for an MFMA
 //   with one ds_read_b128.  b arrives n-contiguous from HBM: each lane loads an
 //   8(k) x 8(n) block with eight 16-byte loads and transposes it in registers
@@ -16,6 +15,8 @@
 // fp32 (config 1, 512^3): 32 x 32 workgroup tiles, four waves each computing a
 //   16 x 16 block with v_mfma_f32_16x16x4f32, k-tiles of 32 staged through LDS.
 #include "mfma_core.h"
+
+#include <type_traits>
 
 namespace nt {
 
@@ -51,6 +52,60 @@ __device__ __forceinline__ void tile_of(int wg, int tiles_m, int tiles_n, int& t
   const int rows_here = min(band, tiles_m - b_id * band);
   tm = b_id * band + in_band % rows_here;
   tn = in_band / rows_here;
+}
+
+// Epilogue shared by the GEMM kernels: out = cast(beta * c + alpha * round(acc)), one
+// 32-row slab per pass staged through LDS (16 KiB per wave), then each lane handles 8
+// consecutive columns: 16-byte loads of c and 16-byte stores of out when both are
+// 16-bit, unit-stride and aligned, element-wise otherwise.
+template <int WI, int WJ>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, const floatx16 (&acc)[WI][WJ], uint16_t* smem,
+                                              int wave, int lane, int64_t row_base, int64_t col_base) {
+  constexpr int COLS = WJ * 32;
+  float* stage = (float*)smem + wave * (32 * COLS);
+  const bool vec16 = g.out_dtype != NT_DTYPE_F32 && g.so_n == 1 && (g.so_m % 8) == 0 && ((uintptr_t)g.out % 16) == 0 &&
+                     (!g.c || (g.sc_n == 1 && (g.sc_m % 8) == 0 && ((uintptr_t)g.c % 16) == 0));
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < WI; ++i) {
+    stage_slab<WJ>(stage, acc[i], lane);
+    __syncthreads();
+    const int64_t row0 = row_base + i * 32;
+    for (int e = lane; e < 32 * (COLS / 8); e += 64) {
+      const int rr = e / (COLS / 8), cg = (e % (COLS / 8)) * 8;
+      const int64_t row = row0 + rr, col = col_base + cg;
+      if (row >= g.M) continue;
+      const float4 v0 = *(const float4*)(stage + rr * COLS + cg);
+      const float4 v1 = *(const float4*)(stage + rr * COLS + cg + 4);
+      float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+      if (vec16 && col + 8 <= g.N) {
+        float cv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (g.c) {
+          const u32x4 craw = *(const u32x4*)((const uint16_t*)g.c + row * g.sc_m + col);
+          const uint16_t* ch = (const uint16_t*)&craw;
+#pragma unroll
+          for (int u = 0; u < 8; ++u)
+            cv[u] = g.out_dtype == NT_DTYPE_F16 ? f16_bits_to_float(ch[u]) : bf16_bits_to_float(ch[u]);
+        }
+        u32x4 oraw;
+        uint16_t* oh = (uint16_t*)&oraw;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const float r = g.alpha * round_through(v[u], g.round_dtype) + g.beta * cv[u];
+          oh[u] = g.out_dtype == NT_DTYPE_F16 ? float_to_f16_bits(r) : float_to_bf16_bits(r);
+        }
+        *(u32x4*)((uint16_t*)g.out + row * g.so_m + col) = oraw;
+      } else {
+        for (int u = 0; u < 8; ++u) {
+          if (col + u >= g.N) break;
+          float r = g.alpha * round_through(v[u], g.round_dtype);
+          if (g.c) r += g.beta * load_as_float(g.c, row * g.sc_m + (col + u) * g.sc_n, g.out_dtype);
+          store_from_float(g.out, row * g.so_m + (col + u) * g.so_n, g.out_dtype, r);
+        }
+      }
+    }
+    __syncthreads();
+  }
 }
 
 template <typename T, bool FAST>
@@ -148,33 +203,134 @@ __global__ __launch_bounds__(G_THREADS) void gemm_mfma_kernel(GemmArgs g) {
     }
   }
 
-  // Epilogue: out = cast(beta * c + alpha * round(acc)), one 32-row slab per pass,
-  // staged through LDS (16 KiB per wave) so that lanes then walk whole rows.
-  __syncthreads();
-  float* stage = (float*)smem + wave * (32 * 128);
+  gemm_epilogue<4, 4>(g, acc, smem, wave, lane, m0 + wm * 128, n0 + wn * 128);
+}
+
+// Fast path (M, N multiples of 256, K of 64, a k-contiguous, b n-contiguous, 16-byte
+// aligned rows): 512 lanes, waves in a 4 (m) x 2 (n) grid, each owning 64 x 128 of the
+// 256 x 256 tile (128 accumulators), so two waves share each SIMD and one's matrix work
+// covers the other's waits.  Two 64 KiB LDS buffers: while tile kt is multiplied out of
+// one, tile kt+1 (already in registers) is stored into the other and tile kt+2 is
+// fetched from HBM, one barrier per k-tile.  a: 4 chunks of 16 bytes per lane; b: a 4(k) x
+// 8(n) block per lane, transposed in registers and stored as eight 8-byte rows.
+__device__ __forceinline__ void transpose4x8(const u32x4 (&in)[4], u32x2 (&out)[8]) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int d = j >> 1;
+    const bool hi = j & 1;
+    uint32_t w[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const uint32_t x0 = in[2 * r][d], x1 = in[2 * r + 1][d];
+      w[r] = hi ? ((x0 >> 16) | (x1 & 0xffff0000u)) : ((x0 & 0xffffu) | (x1 << 16));
+    }
+    out[j] = u32x2{w[0], w[1]};
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(512) void gemm_fast8_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (GB_M + GB_N) * GB_K];
+  constexpr int BUF = (GB_M + GB_N) * GB_K;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;  // 4 x 2
+  int tm, tn;
+  tile_of(blockIdx.x, g.tiles_m, g.tiles_n, tm, tn);
+  const int64_t m0 = (int64_t)tm * GB_M, n0 = (int64_t)tn * GB_N;
+  const int a_row = tid >> 3, a_chunk = tid & 7;  // rows a_row + 64*i
+  const int b_nb = tid & 31, b_kq = tid >> 5;     // 4(k) x 8(n) block: k = 4*b_kq .. +3
+  const uint16_t* A = (const uint16_t*)g.a + (m0 + a_row) * g.sa_m + a_chunk * 8;
+  const uint16_t* B = (const uint16_t*)g.b + (int64_t)(b_kq * 4) * g.sb_k + n0 + b_nb * 8;
+  const int64_t a_step = 64 * g.sa_m;
+  const int nk = (int)(g.K / GB_K);
+
+  floatx16 acc[2][4];
+  zero_acc(acc);
+  u32x4 ra[4], rb[4];
+  u32x2 tb[8];
+  int a_st[4], b_st[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    stage_slab<4>(stage, acc[i], lane);
-    __syncthreads();
-    const int64_t row0 = m0 + wm * 128 + i * 32, col0 = n0 + wn * 128;
-    for (int e = lane; e < 32 * 32; e += 64) {  // 32 rows x 32 groups of 4 columns
-      const int rr = e >> 5, cg = (e & 31) * 4;
-      const int64_t row = row0 + rr;
-      if (row >= g.M) continue;
-      const float4 v4 = *(const float4*)(stage + rr * 128 + cg);
-      const float vals[4] = {v4.x, v4.y, v4.z, v4.w};
+    const int row = i * 64 + a_row;
+    a_st[i] = row * GB_K + swz(row, a_chunk) * 8;
+  }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int64_t col = col0 + cg + u;
-        if (col < g.N) {
-          float v = g.alpha * round_through(vals[u], g.round_dtype);
-          if (g.c) v += g.beta * load_as_float(g.c, row * g.sc_m + col * g.sc_n, g.out_dtype);
-          store_from_float(g.out, row * g.so_m + col * g.so_n, g.out_dtype, v);
-        }
+  for (int j = 0; j < 8; ++j) {
+    const int nrow = b_nb * 8 + j;
+    b_st[j] = GB_M * GB_K + nrow * GB_K + swz(nrow, b_kq >> 1) * 8 + (b_kq & 1) * 4;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ra[i] = *(const u32x4*)(A + i * a_step);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) rb[r] = *(const u32x4*)(B + r * g.sb_k);
+  transpose4x8(rb, tb);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) *(u32x4*)(smem + a_st[i]) = ra[i];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) *(u32x2*)(smem + b_st[j]) = tb[j];
+  if (nk > 1) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ra[i] = *(const u32x4*)(A + i * a_step + GB_K);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) rb[r] = *(const u32x4*)(B + (GB_K + r) * g.sb_k);
+  }
+  __syncthreads();
+
+  typedef typename mfma_traits<T>::frag frag;
+  // One k-tile.  First the staged tile kt+1 (loaded one iteration ago) goes to the other
+  // LDS buffer and the loads of tile kt+2 are issued; the scheduling barrier keeps those
+  // loads here, a whole k-tile of matrix work ahead of their use.
+  auto step = [&](auto has1_c, auto has2_c, int kt) {
+    constexpr bool HAS1 = decltype(has1_c)::value, HAS2 = decltype(has2_c)::value;
+    const uint16_t* sA = smem + (kt & 1) * BUF;
+    const uint16_t* sB = sA + GB_M * GB_K;
+    uint16_t* nxt = smem + ((kt & 1) ^ 1) * BUF;
+    const int64_t k2 = (int64_t)(kt + 2) * GB_K;
+    if constexpr (HAS1) {
+      transpose4x8(rb, tb);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) *(u32x4*)(nxt + a_st[i]) = ra[i];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) *(u32x2*)(nxt + b_st[j]) = tb[j];
+      if constexpr (HAS2) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ra[i] = *(const u32x4*)(A + i * a_step + k2);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) rb[r] = *(const u32x4*)(B + (k2 + r) * g.sb_k);
       }
     }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kk = 0; kk < GB_K / 16; ++kk) {
+      const int chunk = kk * 2 + (lane >> 5);
+      frag fa[2], fb[4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int row = wm * 64 + i * 32 + (lane & 31);
+        fa[i] = *(const frag*)(sA + row * GB_K + swz(row, chunk) * 8);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int row = wn * 128 + j * 32 + (lane & 31);
+        fb[j] = *(const frag*)(sB + row * GB_K + swz(row, chunk) * 8);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma_traits<T>::mma(fa[i], fb[j], acc[i][j]);
+    }
     __syncthreads();
-  }
+  };
+  using T1 = std::integral_constant<bool, true>;
+  using F1 = std::integral_constant<bool, false>;
+  int kt = 0;
+  for (; kt + 2 < nk; ++kt) step(T1{}, T1{}, kt);
+  if (kt + 1 < nk) step(T1{}, F1{}, kt++);
+  step(F1{}, F1{}, kt);
+
+  gemm_epilogue<2, 4>(g, acc, smem, wave, lane, m0 + wm * 64, n0 + wn * 128);
 }
 
 // ----------------------------------------------------------------------------- fp32
@@ -257,7 +413,7 @@ static int gemm16_launch(GemmArgs g, hipStream_t stream) {
                     (g.sb_k * 2) % 16 == 0;
   const dim3 grid((unsigned)(tiles_m * tiles_n)), blk(G_THREADS);
   if (fast)
-    hipLaunchKernelGGL((gemm_mfma_kernel<T, true>), grid, blk, 0, stream, g);
+    hipLaunchKernelGGL((gemm_fast8_kernel<T>), grid, dim3(512), 0, stream, g);
   else
     hipLaunchKernelGGL((gemm_mfma_kernel<T, false>), grid, blk, 0, stream, g);
   return launch_status();

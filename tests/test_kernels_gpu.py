@@ -146,7 +146,8 @@ def _gemm_ref(a, b, c=None, alpha=1.0, beta=0.0, round_dtype=None, out_dtype=Non
 
 
 @pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
-@pytest.mark.parametrize("mnk", ((512, 512, 512), (4096, 4096, 4096), (300, 200, 100), (256, 512, 1000), (1, 1, 1)))
+@pytest.mark.parametrize("mnk", ((512, 512, 512), (4096, 4096, 4096), (300, 200, 100), (256, 512, 1000), (1, 1, 1),
+                                 (256, 256, 64), (256, 512, 128), (512, 256, 192), (768, 1024, 320)))
 def test_gemm16(mnk, dtype):
     m, n, k = mnk
     a = _randn((m, k), dtype, 11)
