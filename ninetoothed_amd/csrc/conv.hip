@@ -14,6 +14,8 @@
 // MFMA-bound in principle (2 * N*P*Q * K * C*R*S flops per launch).
 #include "mfma_core.h"
 
+#include <type_traits>
+
 namespace nt {
 
 constexpr int CB_K = 256;  // output channels per workgroup
@@ -141,13 +143,230 @@ __global__ __launch_bounds__(C_THREADS) void conv_direct_kernel(ConvArgs g) {
   }
 }
 
+
+// ----------------------------------------------------------------------------- N-H-W-C path
+// With a workspace the input is re-laid as zero-padded N-Hp-Wp-C (Hp = H + 2ph, Wp = W + 2pw)
+// and the filter as K-R-S-C.  Reduction index kk = (r*S + s)*C + c then walks channels
+// contiguously, so for a 64-deep k-tile inside one (r, s) every im2col row and every
+// filter row is 128 contiguous bytes: both operands load with 16-byte loads straight
+// into the k-contiguous LDS layout of the MFMA core, no gathers, no transposes, no
+// padding tests.  Needs C % 64 == 0.  Cost of the re-layout: one read and one write of
+// the input (plus the small filter).
+
+// x (N-C-H-W indexed, any strides) -> xp [N][Hp][Wp][C].  One workgroup per (n, hp, 64
+// channels): the 64 x W slab goes through LDS so that reads run along w and writes
+// along c (16 bytes per lane).
+template <typename T>
+__global__ __launch_bounds__(256) void nchw_to_nhwc_pad_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ xp,
+                                                               ConvArgs g, int64_t Hp, int64_t Wp) {
+  __shared__ uint16_t tile[64][64 + 2];
+  const int64_t cblocks = g.C / 64;
+  const int64_t b = blockIdx.x;
+  const int64_t cb = b % cblocks, row = b / cblocks;
+  const int64_t hp = row % Hp, n = row / Hp;
+  const int64_t h = hp - g.ph;
+  const int64_t c0 = cb * 64;
+  uint16_t* out_row = xp + ((n * Hp + hp) * Wp) * g.C + c0;
+  const int tid = threadIdx.x;
+  if (h < 0 || h >= g.H) {
+    for (int64_t e = tid; e < Wp * 8; e += 256) {
+      const int64_t wp = e / 8, ch = e % 8;
+      *(u32x4*)(out_row + wp * g.C + ch * 8) = u32x4{0u, 0u, 0u, 0u};
+    }
+    return;
+  }
+  const uint16_t* xb = x + n * g.xs[0] + c0 * g.xs[1] + h * g.xs[2];
+  for (int64_t w0 = -g.pw; w0 < Wp - g.pw; w0 += 64) {
+    // load 64 channels x 64 positions [w0, w0 + 64)
+    for (int e = tid; e < 64 * 64; e += 256) {
+      const int c = e / 64, wi = e % 64;
+      const int64_t w = w0 + wi;
+      tile[c][wi] = (w >= 0 && w < g.W) ? xb[c * g.xs[1] + w * g.xs[3]] : (uint16_t)0;
+    }
+    __syncthreads();
+    for (int e = tid; e < 64 * 8; e += 256) {
+      const int wi = e / 8, ch = e % 8;
+      const int64_t wp = w0 + g.pw + wi;
+      if (wp < Wp) {
+        uint16_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = tile[ch * 8 + u][wi];
+        *(u32x4*)(out_row + wp * g.C + ch * 8) = *(const u32x4*)v;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// w (K-C-R-S indexed, any strides) -> wt [K][R][S][C].
+template <typename T>
+__global__ __launch_bounds__(256) void filter_krsc_kernel(const uint16_t* __restrict__ w, uint16_t* __restrict__ wt,
+                                                          ConvArgs g) {
+  const int64_t total = g.K * g.KG;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t c = e % g.C;
+    int64_t t = e / g.C;
+    const int64_t s = t % g.S;
+    t /= g.S;
+    const int64_t r = t % g.R, k = t / g.R;
+    wt[e] = w[k * g.ws[0] + c * g.ws[1] + r * g.ws[2] + s * g.ws[3]];
+  }
+}
+
+// Implicit GEMM over the re-laid operands: out^T[k][m] = sum_kk wt[k][kk] * xcol[m][kk].
+// 512 lanes, waves 4 (k) x 2 (m), 256 x 256 tile, two 64 KiB LDS buffers, tile kt+2
+// fetched while kt is multiplied (as the GEMM fast path).
+template <typename T>
+__global__ __launch_bounds__(512) void conv_nhwc_kernel(const uint16_t* __restrict__ xp, const uint16_t* __restrict__ wt,
+                                                        ConvArgs g, int64_t Hp, int64_t Wp) {
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (CB_K + CB_M) * TILE_K];
+  constexpr int BUF = (CB_K + CB_M) * TILE_K;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wk = wave >> 1, wm = wave & 1;
+  const int tk = blockIdx.x % g.tiles_k, tmi = blockIdx.x / g.tiles_k;
+  const int64_t k0t = (int64_t)tk * CB_K, m0t = (int64_t)tmi * CB_M;
+  const int row_in = tid >> 3, chunk = tid & 7;  // rows row_in + 64*i, 16-byte chunk
+  const int64_t KG = g.KG;
+
+  // Per-lane row bases: filter rows k and im2col rows m.
+  const uint16_t* wrow[4];
+  int64_t xrow[4];
+  bool wok[4], xok[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t k = k0t + row_in + 64 * i;
+    wok[i] = k < g.K;
+    wrow[i] = wt + (wok[i] ? k : 0) * KG + chunk * 8;
+    const int64_t m = m0t + row_in + 64 * i;
+    xok[i] = m < g.M;
+    const int64_t mm = xok[i] ? m : 0;
+    const int64_t q = mm % g.Q, t = mm / g.Q;
+    const int64_t p = t % g.P, n = t / g.P;
+    xrow[i] = ((n * Hp + p * g.sh) * Wp + q * g.sw) * g.C + chunk * 8;
+  }
+  int st[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = row_in + 64 * i;
+    st[i] = r * TILE_K + swz(r, chunk) * 8;
+  }
+  const int nk = (int)(KG / TILE_K);
+  u32x4 ra[4], rb[4];
+  auto load = [&](int kt) {
+    const int64_t kk0 = (int64_t)kt * TILE_K;
+    const int64_t rs = kk0 / g.C, c0 = kk0 % g.C;
+    const int64_t r = rs / g.S, s = rs % g.S;
+    const int64_t xoff = (r * g.dh * Wp + s * g.dw) * g.C + c0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      ra[i] = wok[i] ? *(const u32x4*)(wrow[i] + kk0) : u32x4{0u, 0u, 0u, 0u};
+      rb[i] = xok[i] ? *(const u32x4*)(xp + xrow[i] + xoff) : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store = [&](uint16_t* buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      *(u32x4*)(buf + st[i]) = ra[i];
+      *(u32x4*)(buf + CB_K * TILE_K + st[i]) = rb[i];
+    }
+  };
+
+  floatx16 acc[2][4];
+  zero_acc(acc);
+  load(0);
+  store(smem);
+  if (nk > 1) load(1);
+  __syncthreads();
+  typedef typename mfma_traits<T>::frag frag;
+  auto step = [&](auto has1_c, auto has2_c, int kt) {
+    constexpr bool HAS1 = decltype(has1_c)::value, HAS2 = decltype(has2_c)::value;
+    const uint16_t* sW = smem + (kt & 1) * BUF;
+    const uint16_t* sX = sW + CB_K * TILE_K;
+    if constexpr (HAS1) {
+      store(smem + ((kt & 1) ^ 1) * BUF);
+      if constexpr (HAS2) load(kt + 2);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kk = 0; kk < TILE_K / 16; ++kk) {
+      const int ch = kk * 2 + (lane >> 5);
+      frag fa[2], fb[4];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int row = wk * 64 + i * 32 + (lane & 31);
+        fa[i] = *(const frag*)(sW + row * TILE_K + swz(row, ch) * 8);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int row = wm * 128 + j * 32 + (lane & 31);
+        fb[j] = *(const frag*)(sX + row * TILE_K + swz(row, ch) * 8);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma_traits<T>::mma(fa[i], fb[j], acc[i][j]);
+    }
+    __syncthreads();
+  };
+  using T1 = std::integral_constant<bool, true>;
+  using F1 = std::integral_constant<bool, false>;
+  int kt = 0;
+  for (; kt + 2 < nk; ++kt) step(T1{}, T1{}, kt);
+  if (kt + 1 < nk) step(T1{}, F1{}, kt++);
+  step(F1{}, F1{}, kt);
+
+  // Epilogue: slabs of 32 channels x 128 positions staged in LDS; 8 consecutive output
+  // positions per lane, one 16-byte store when they share an output row.
+  float* stage = (float*)smem + wave * (32 * 128);
+  const bool vec = g.y_dtype != NT_DTYPE_F32 && g.ys[3] == 1 && g.Q % 8 == 0 && ((uintptr_t)g.y % 16) == 0 &&
+                   (g.ys[0] % 8) == 0 && (g.ys[1] % 8) == 0 && (g.ys[2] % 8) == 0;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    stage_slab<4>(stage, acc[i], lane);
+    __syncthreads();
+    const int64_t k_0 = k0t + wk * 64 + i * 32, m_0 = m0t + wm * 128;
+    for (int e = lane; e < 32 * 16; e += 64) {
+      const int kr = e >> 4, mg = (e & 15) * 8;
+      const int64_t k = k_0 + kr, mm = m_0 + mg;
+      if (k >= g.K || mm >= g.M) continue;
+      const int64_t q = mm % g.Q, t = mm / g.Q;
+      const int64_t p = t % g.P, n = t / g.P;
+      const float* sv = stage + kr * 128 + mg;
+      if (vec && mm + 8 <= g.M) {
+        u32x4 raw;
+        uint16_t* h = (uint16_t*)&raw;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const float v = round_through(sv[u], g.round_dtype);
+          h[u] = g.y_dtype == NT_DTYPE_F16 ? float_to_f16_bits(v) : float_to_bf16_bits(v);
+        }
+        *(u32x4*)((uint16_t*)g.y + n * g.ys[0] + k * g.ys[1] + p * g.ys[2] + q) = raw;
+      } else {
+        for (int u = 0; u < 8 && mm + u < g.M; ++u) {
+          const int64_t m2 = mm + u;
+          const int64_t q2 = m2 % g.Q, t2 = m2 / g.Q;
+          const int64_t p2 = t2 % g.P, n2 = t2 / g.P;
+          store_from_float(g.y, n2 * g.ys[0] + k * g.ys[1] + p2 * g.ys[2] + q2 * g.ys[3], g.y_dtype,
+                           round_through(sv[u], g.round_dtype));
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+static int64_t nhwc_bytes(int64_t N, int64_t C, int64_t H, int64_t W, int64_t K, int64_t R, int64_t S, int64_t ph,
+                          int64_t pw) {
+  const int64_t xp = N * (H + 2 * ph) * (W + 2 * pw) * C * 2;
+  const int64_t wt = K * R * S * C * 2;
+  return ((xp + 255) / 256) * 256 + wt;
+}
+
 template <typename T>
 static int conv_launch(const void* x, const int64_t* xs, const void* w, const int64_t* ws, void* y, const int64_t* ys,
                        int y_dtype, int64_t N, int64_t C, int64_t H, int64_t W, int64_t K, int64_t R, int64_t S,
                        int64_t P, int64_t Q, int64_t ph, int64_t pw, int64_t sh, int64_t sw, int64_t dh, int64_t dw,
                        int round_dtype, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
-  (void)workspace;
-  (void)workspace_bytes;
   if (N < 0 || C < 0 || H < 0 || W < 0 || K < 0 || R < 0 || S < 0 || P < 0 || Q < 0 || ph < 0 || pw < 0 || sh <= 0 ||
       sw <= 0 || dh <= 0 || dw <= 0)
     return NT_ERR_INVALID;
@@ -171,6 +390,24 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
   if (tiles_k * tiles_m > 0x7fffffffLL) return NT_ERR_INVALID;
   g.tiles_k = (int)tiles_k;
   g.tiles_m = (int)tiles_m;
+  const int64_t need = nhwc_bytes(N, C, H, W, K, R, S, ph, pw);
+  const bool nhwc = workspace != nullptr && workspace_bytes >= need && C % 64 == 0 && (uintptr_t)workspace % 256 == 0 &&
+                    (P - 1) * sh + (R - 1) * dh < H + 2 * ph && (Q - 1) * sw + (S - 1) * dw < W + 2 * pw;
+  if (nhwc) {
+    const int64_t Hp = H + 2 * ph, Wp = W + 2 * pw;
+    uint16_t* xp = (uint16_t*)workspace;
+    uint16_t* wt = (uint16_t*)((char*)workspace + ((N * Hp * Wp * C * 2 + 255) / 256) * 256);
+    const int64_t relayout_blocks = N * Hp * (C / 64);
+    if (relayout_blocks > 0x7fffffffLL) return NT_ERR_INVALID;
+    hipLaunchKernelGGL(nchw_to_nhwc_pad_kernel<T>, dim3((unsigned)relayout_blocks), dim3(256), 0, stream,
+                       (const uint16_t*)x, xp, g, Hp, Wp);
+    int64_t fblocks = cdiv(K * g.KG, 256);
+    if (fblocks > 4096) fblocks = 4096;
+    hipLaunchKernelGGL(filter_krsc_kernel<T>, dim3((unsigned)fblocks), dim3(256), 0, stream, (const uint16_t*)w, wt, g);
+    hipLaunchKernelGGL(conv_nhwc_kernel<T>, dim3((unsigned)(tiles_k * tiles_m)), dim3(512), 0, stream,
+                       (const uint16_t*)xp, (const uint16_t*)wt, g, Hp, Wp);
+    return launch_status();
+  }
   const bool dense_w = ws[3] == 1 && ws[2] == S && ws[1] == R * S && g.KG % TILE_K == 0 && (ws[0] * 2) % 16 == 0 &&
                        (uintptr_t)w % 16 == 0;
   const dim3 grid((unsigned)(tiles_k * tiles_m)), blk(C_THREADS);
@@ -185,8 +422,10 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
 
 extern "C" int64_t nt_conv2d_workspace_size(int64_t N, int64_t C, int64_t H, int64_t W, int64_t K, int64_t R,
                                             int64_t S, int64_t ph, int64_t pw, int dtype) {
-  (void)N; (void)C; (void)H; (void)W; (void)K; (void)R; (void)S; (void)ph; (void)pw; (void)dtype;
-  return 0;
+  if (N <= 0 || C <= 0 || H <= 0 || W <= 0 || K <= 0 || R <= 0 || S <= 0 || ph < 0 || pw < 0) return 0;
+  if (dtype != NT_DTYPE_F16 && dtype != NT_DTYPE_BF16) return 0;
+  if (C % 64 != 0) return 0;
+  return nt::nhwc_bytes(N, C, H, W, K, R, S, ph, pw);
 }
 
 #define NT_CONV_ENTRY(NAME, T)                                                                                       \

@@ -205,25 +205,47 @@ def test_gemm_f32(mnk):
 
 
 # ------------------------------------------------------------------------ conv2d
+def _workspace(x, w, padding):
+    nbytes = kernels.conv2d_workspace_bytes(x, w, padding)
+    return torch.empty(nbytes, dtype=torch.uint8, device=DEV) if nbytes else None
+
+
+@pytest.mark.parametrize("relayout", (False, True))
 @pytest.mark.parametrize("padding", ((0, 0), (1, 1), (0, 1), (2, 0)))
-def test_conv2d_reference_case(padding):
+def test_conv2d_reference_case(padding, relayout):
     x = _rand((4, 64, 16, 16), torch.float16, 23)
     w = _rand((512, 64, 3, 3), torch.float16, 24)
     ph, pw = padding
     p, q = 16 + 2 * ph - 2, 16 + 2 * pw - 2
     y = torch.empty((4, 512, p, q), dtype=torch.float16, device=DEV)
-    kernels.conv2d(x, w, y, padding=padding, round_dtype=torch.float16)
+    ws = _workspace(x, w, padding) if relayout else None
+    assert (ws is not None) == relayout
+    kernels.conv2d(x, w, y, padding=padding, round_dtype=torch.float16, workspace=ws)
     ref = F.conv2d(x.float(), w.float(), padding=padding)
     assert torch.allclose(y.float(), ref, atol=1e-2 * 4, rtol=1e-2)
 
 
-def test_conv2d_headline():
+@pytest.mark.parametrize("relayout", (False, True))
+def test_conv2d_headline(relayout):
     x = _randn((16, 256, 56, 56), torch.float16, 25)
     w = _randn((256, 256, 3, 3), torch.float16, 26, 1.0 / math.sqrt(256 * 9))
     y = torch.empty_like(x)
-    kernels.conv2d(x, w, y, padding=(1, 1), round_dtype=torch.float16)
+    kernels.conv2d(x, w, y, padding=(1, 1), round_dtype=torch.float16,
+                   workspace=_workspace(x, w, (1, 1)) if relayout else None)
     ref = F.conv2d(x.float(), w.float(), padding=1)
     assert torch.allclose(y.float(), ref, atol=1e-2, rtol=1e-2)
+
+
+def test_conv2d_relayout_strided_ragged_bf16():
+    # C = 64 takes the re-laid path; stride 2, dilation 2, K and N*P*Q not multiples of 256.
+    x = _randn((3, 64, 23, 19), torch.bfloat16, 29)
+    w = _randn((72, 64, 3, 2), torch.bfloat16, 30, 0.1)
+    ref = F.conv2d(x.float(), w.float(), padding=(1, 2), stride=(2, 2), dilation=(2, 1))
+    y = torch.empty(ref.shape, dtype=torch.bfloat16, device=DEV)
+    ws = _workspace(x, w, (1, 2))
+    assert ws is not None
+    kernels.conv2d(x, w, y, padding=(1, 2), stride=(2, 2), dilation=(2, 1), workspace=ws)
+    assert torch.allclose(y.float(), ref, atol=3e-2, rtol=1e-2)
 
 
 def test_conv2d_strided_dilated_bf16():
