@@ -36,22 +36,51 @@ struct AttnArgs {
   int causal, o_dtype, q_blocks;
 };
 
+// Workgroup id -> (query block, batch*head).  The dispatcher hands ids to the 8 XCDs
+// round-robin (id % 8), each XCD with its own L2.  When B*H divides by 8, XCD x owns the
+// heads [x*BH/8, (x+1)*BH/8): non-causal launches walk them head by head (a head's 32 KiB
+// K/V tiles stay hot in that L2 while its query blocks run); causal launches walk them
+// heaviest query block first (longest job first) and every XCD gets the same mix of
+// block sizes.  Otherwise: heaviest first, heads fastest.
+__device__ __forceinline__ void block_order(const AttnArgs& g, int64_t id, int& qb, int64_t& bh) {
+  const int64_t BH = g.B * g.H;
+  const int64_t nq = g.q_blocks;
+  if (BH % 8 == 0) {
+    const int64_t per_xcd = BH / 8;
+    const int64_t x = id % 8, local = id / 8;
+    if (g.causal) {
+      qb = (int)(nq - 1 - local / per_xcd);
+      bh = x * per_xcd + local % per_xcd;
+    } else {
+      qb = (int)(local % nq);
+      bh = x * per_xcd + local / nq;
+    }
+    return;
+  }
+  qb = (int)(nq - 1 - id / BH);
+  bh = id % BH;
+}
+
 template <typename T, int DM, bool KVEC>  // DM = padded head dim (64 or 128)
-__global__ __launch_bounds__(AT_THREADS) void attention_kernel(AttnArgs g) {
+__device__ __forceinline__ void attention_body(const AttnArgs& g) {
   typedef typename mfma_traits<T>::frag frag;
   constexpr int DH = DM / 64;  // 64-wide d halves
   constexpr int DSUB = DM / 16;
   constexpr int DBLK = DM / 32;
-  // K tile, V^T tile; reused at the end to stage the output (32 KiB either way).
-  __shared__ __attribute__((aligned(16))) uint16_t smem[16384];
+  // K tile [d-half][key][64 d] (chunk-swizzled) and V^T tile [d][64 keys + 4 pad]; the
+  // pad shifts consecutive d rows by two banks so that the 8-byte fragment reads of 16
+  // rows hit 32 distinct banks.  Reused at the end to stage the output.
+  constexpr int VT_STRIDE = TILE_K + 4;
+  constexpr int SMEM = (DH * AT_BN * TILE_K + DM * VT_STRIDE) > (4 * 32 * 65 * 2) ? (DH * AT_BN * TILE_K + DM * VT_STRIDE)
+                                                                                   : (4 * 32 * 65 * 2);
+  __shared__ __attribute__((aligned(16))) uint16_t smem[SMEM];
   uint16_t* sK = smem;
   uint16_t* sVt = smem + DH * AT_BN * TILE_K;
-  static_assert(DH * AT_BN * TILE_K + DM * TILE_K <= 16384, "LDS tiles exceed the allocation");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5;
-  // Heaviest (latest) query blocks first.
-  const int qb = g.q_blocks - 1 - (int)(blockIdx.x % g.q_blocks);
-  const int64_t bh = blockIdx.x / g.q_blocks;
+  int qb;
+  int64_t bh;
+  block_order(g, blockIdx.x, qb, bh);
   const int64_t b = bh / g.H, h = bh % g.H;
   const int64_t q0 = (int64_t)qb * AT_BM;
   const uint16_t* Q = (const uint16_t*)g.q + b * g.qs[0] + h * g.qs[1];
@@ -64,12 +93,20 @@ __global__ __launch_bounds__(AT_THREADS) void attention_kernel(AttnArgs g) {
 #pragma unroll
   for (int dd = 0; dd < DSUB; ++dd) {
     uint16_t tmp[8];
+    if (KVEC) {  // unit d-stride and 16-byte aligned rows (checked at launch)
+      u32x4 raw = {0u, 0u, 0u, 0u};
+      if (qpos < g.Sq) raw = *(const u32x4*)(Q + qpos * g.qs[2] + dd * 16 + half * 8);
+      const uint16_t* h = (const uint16_t*)&raw;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int64_t d = dd * 16 + half * 8 + u;
-      float x = 0.f;
-      if (qpos < g.Sq && d < g.D) x = elem<T>::to_float(Q[qpos * g.qs[2] + d * g.qs[3]]) * g.q_scale;
-      tmp[u] = elem<T>::from_float(x);
+      for (int u = 0; u < 8; ++u) tmp[u] = elem<T>::from_float(elem<T>::to_float(h[u]) * g.q_scale);
+    } else {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int64_t d = dd * 16 + half * 8 + u;
+        float x = 0.f;
+        if (qpos < g.Sq && d < g.D) x = elem<T>::to_float(Q[qpos * g.qs[2] + d * g.qs[3]]) * g.q_scale;
+        tmp[u] = elem<T>::from_float(x);
+      }
     }
     qf[dd] = __builtin_bit_cast(frag, *(const u32x4*)tmp);
   }
@@ -155,7 +192,9 @@ __global__ __launch_bounds__(AT_THREADS) void attention_kernel(AttnArgs g) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int d = v_db * 8 + j;
-        *(u32x4*)(sVt + d * TILE_K + swz(d, v_kb) * 8) = tv[j];
+        u32x2* dst = (u32x2*)(sVt + d * VT_STRIDE + v_kb * 8);
+        dst[0] = u32x2{tv[j][0], tv[j][1]};
+        dst[1] = u32x2{tv[j][2], tv[j][3]};
       }
     }
   };
@@ -228,9 +267,9 @@ __global__ __launch_bounds__(AT_THREADS) void attention_kernel(AttnArgs g) {
 #pragma unroll
       for (int i = 0; i < DBLK; ++i) {
         const int d = i * 32 + (lane & 31);
-        const uint16_t* rowp = sVt + d * TILE_K;
-        const u32x2 lo = *(const u32x2*)(rowp + swz(d, 2 * t) * 8 + half * 4);
-        const u32x2 hi = *(const u32x2*)(rowp + swz(d, 2 * t + 1) * 8 + half * 4);
+        const uint16_t* rowp = sVt + d * VT_STRIDE;
+        const u32x2 lo = *(const u32x2*)(rowp + (2 * t) * 8 + half * 4);
+        const u32x2 hi = *(const u32x2*)(rowp + (2 * t + 1) * 8 + half * 4);
         const frag vf = __builtin_bit_cast(frag, u32x4{lo[0], lo[1], hi[0], hi[1]});
         o_acc[i] = mfma_traits<T>::mma(vf, pf, o_acc[i]);
       }
@@ -246,7 +285,8 @@ __global__ __launch_bounds__(AT_THREADS) void attention_kernel(AttnArgs g) {
   // writes 4 consecutive d of one query row (lanes 0-15 cover 64 d of a row).
   {
     const float inv = 1.0f / l_i;
-    float* stage = reinterpret_cast<float*>(smem) + wave * (32 * 64);
+    constexpr int ST = 65;  // padded row: lane-per-row writes hit distinct banks
+    float* stage = reinterpret_cast<float*>(smem) + wave * (32 * ST);
     constexpr int PASSES = (DM + 63) / 64;
 #pragma unroll
     for (int ps = 0; ps < PASSES; ++ps) {
@@ -255,7 +295,7 @@ __global__ __launch_bounds__(AT_THREADS) void attention_kernel(AttnArgs g) {
         if (ps * 2 + jb < DBLK) {
 #pragma unroll
           for (int r = 0; r < 16; ++r)
-            stage[(lane & 31) * 64 + jb * 32 + acc_row(r, lane)] = o_acc[ps * 2 + jb][r] * inv;
+            stage[(lane & 31) * ST + jb * 32 + acc_row(r, lane)] = o_acc[ps * 2 + jb][r] * inv;
         }
       }
       __syncthreads();
@@ -264,7 +304,8 @@ __global__ __launch_bounds__(AT_THREADS) void attention_kernel(AttnArgs g) {
         const int64_t qp = q0 + wave * 32 + row;
         const int d0 = ps * 64 + grp;
         if (qp >= g.Sq || d0 >= g.D) continue;
-        const float4 v4 = *(const float4*)(stage + row * 64 + grp);
+        const float* sp = stage + row * ST + grp;
+        const float4 v4 = {sp[0], sp[1], sp[2], sp[3]};
         const int64_t ob = b * g.os[0] + h * g.os[1] + qp * g.os[2];
         if (g.o_dtype != NT_DTYPE_F32 && g.os[3] == 1 && d0 + 4 <= g.D && ((ob + d0) & 3) == 0) {
           uint16_t hv[4];
@@ -281,6 +322,19 @@ __global__ __launch_bounds__(AT_THREADS) void attention_kernel(AttnArgs g) {
       __syncthreads();
     }
   }
+}
+
+// Vector-load variant: two waves per SIMD (two workgroups per CU) so that one
+// workgroup's softmax and LDS traffic overlap the other's matrix work.
+template <typename T, int DM>
+__global__ __launch_bounds__(AT_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_kernel(AttnArgs g) {
+  attention_body<T, DM, true>(g);
+}
+
+// Element-wise loads for unusual strides or head dims.
+template <typename T, int DM>
+__global__ __launch_bounds__(AT_THREADS) void attention_generic_kernel(AttnArgs g) {
+  attention_body<T, DM, false>(g);
 }
 
 template <typename T>
@@ -312,18 +366,19 @@ static int attention_launch(const void* q, const int64_t* qs, const void* k, con
   auto kvec_ok = [&](int64_t dm) {
     return ks[3] == 1 && vs[3] == 1 && D == dm && (ks[2] * 2) % 16 == 0 && (vs[2] * 2) % 16 == 0 &&
            (ks[1] * 2) % 16 == 0 && (vs[1] * 2) % 16 == 0 && (ks[0] * 2) % 16 == 0 && (vs[0] * 2) % 16 == 0 &&
-           (uintptr_t)k % 16 == 0 && (uintptr_t)v % 16 == 0;
+           (uintptr_t)k % 16 == 0 && (uintptr_t)v % 16 == 0 && qs[3] == 1 && (qs[2] * 2) % 16 == 0 &&
+           (qs[1] * 2) % 16 == 0 && (qs[0] * 2) % 16 == 0 && (uintptr_t)q % 16 == 0;
   };
   if (D <= 64) {
     if (kvec_ok(64))
-      hipLaunchKernelGGL((attention_kernel<T, 64, true>), grid, blk, 0, stream, g);
+      hipLaunchKernelGGL((attention_kernel<T, 64>), grid, blk, 0, stream, g);
     else
-      hipLaunchKernelGGL((attention_kernel<T, 64, false>), grid, blk, 0, stream, g);
+      hipLaunchKernelGGL((attention_generic_kernel<T, 64>), grid, blk, 0, stream, g);
   } else {
     if (kvec_ok(128))
-      hipLaunchKernelGGL((attention_kernel<T, 128, true>), grid, blk, 0, stream, g);
+      hipLaunchKernelGGL((attention_kernel<T, 128>), grid, blk, 0, stream, g);
     else
-      hipLaunchKernelGGL((attention_kernel<T, 128, false>), grid, blk, 0, stream, g);
+      hipLaunchKernelGGL((attention_generic_kernel<T, 128>), grid, blk, 0, stream, g);
   }
   return launch_status();
 }
@@ -337,8 +392,9 @@ __global__ __launch_bounds__(AF_Q) void attention_f32_kernel(AttnArgs g) {
   __shared__ float sK[AF_BN][128];
   __shared__ float sV[AF_BN][128];
   const int tid = threadIdx.x;
-  const int qb = g.q_blocks - 1 - (int)(blockIdx.x % g.q_blocks);
-  const int64_t bh = blockIdx.x / g.q_blocks;
+  int qb;
+  int64_t bh;
+  block_order(g, blockIdx.x, qb, bh);
   const int64_t b = bh / g.H, h = bh % g.H;
   const int64_t q0 = (int64_t)qb * AF_Q, qpos = q0 + tid;
   const float* Q = (const float*)g.q + b * g.qs[0] + h * g.qs[1];
