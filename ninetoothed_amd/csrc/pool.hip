@@ -5,9 +5,9 @@
 // evaluation order; fp16/bf16 values are compared after an exact widening to fp32.
 //
 // Fast path (the common non-overlapping 2-wide window on 16-bit data, unit inner
-// strides, no padding or dilation): one lane produces 8 consecutive outputs of a
-// row from kh input rows of 16 elements, i.e. 2*kh 16-byte loads and one 16-byte
-// store.  Everything else runs the generic kernel, one lane per output.
+// strides, no padding or dilation): one workgroup per (n, c) plane; a lane produces 8
+// consecutive outputs of a row from kh input rows of 16 elements, i.e. 2*kh 16-byte
+// loads and one 16-byte store.  Everything else runs the generic kernel, one lane per output.
 #include "nt_common.h"
 
 namespace nt {
@@ -43,27 +43,28 @@ __global__ __launch_bounds__(256) void pool_generic_kernel(const typename elem<T
 }
 
 // kw == sw == 2, dw == 1, no padding, 16-bit, x/y inner stride 1, Q % 8 == 0,
-// all rows 16-byte aligned, every window inside the input.
+// all rows 16-byte aligned, every window inside the input.  One workgroup per (n, c)
+// plane: in-plane indices are 32-bit, and consecutive lanes walk consecutive 16-byte
+// output vectors, so a wave reads one contiguous stretch of input rows.
 template <typename T>
-__global__ __launch_bounds__(256) void pool_w2_vec_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
-                                                          PoolShape s) {
-  const int64_t qv_per_row = s.Q / 8;
-  const int64_t total = s.N * s.C * s.P * qv_per_row;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-    const int64_t qv = i % qv_per_row;
-    int64_t t = i / qv_per_row;
-    const int64_t p = t % s.P;
-    t /= s.P;
-    const int64_t c = t % s.C, n = t / s.C;
-    const uint16_t* xb = x + n * s.xs[0] + c * s.xs[1] + (p * s.sh) * s.xs[2] + qv * 16;
+__global__ __launch_bounds__(256) void pool_w2_plane_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
+                                                            PoolShape s) {
+  const int64_t plane = blockIdx.x;
+  const int64_t c = plane % s.C, n = plane / s.C;
+  const uint16_t* xb = x + n * s.xs[0] + c * s.xs[1];
+  uint16_t* yb = y + n * s.ys[0] + c * s.ys[1];
+  const int qv_per_row = (int)(s.Q / 8);
+  const int total = (int)s.P * qv_per_row;
+  const int xh = (int)s.xs[2], yh = (int)s.ys[2], kh = (int)s.kh, sh = (int)s.sh, dh = (int)s.dh;
+  for (int v = threadIdx.x; v < total; v += 256) {
+    const int p = v / qv_per_row, qv = v - p * qv_per_row;
+    const uint16_t* row = xb + (p * sh) * xh + qv * 16;
     float m[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) m[j] = -INFINITY;
-    for (int64_t r = 0; r < s.kh; ++r) {
-      const uint16_t* row = xb + r * s.dh * s.xs[2];
-      u32x4 a = __builtin_nontemporal_load((const u32x4*)row);
-      u32x4 b = __builtin_nontemporal_load((const u32x4*)(row + 8));
+    for (int r = 0; r < kh; ++r) {
+      const u32x4 a = *(const u32x4*)(row + r * dh * xh);
+      const u32x4 b = *(const u32x4*)(row + r * dh * xh + 8);
       const uint16_t* pa = (const uint16_t*)&a;
       const uint16_t* pb = (const uint16_t*)&b;
 #pragma unroll
@@ -76,7 +77,7 @@ __global__ __launch_bounds__(256) void pool_w2_vec_kernel(const uint16_t* __rest
     uint16_t* po = (uint16_t*)&out;
 #pragma unroll
     for (int j = 0; j < 8; ++j) po[j] = elem<T>::from_float(m[j]);
-    *(u32x4*)(y + n * s.ys[0] + c * s.ys[1] + p * s.ys[2] + qv * 8) = out;
+    *(u32x4*)(yb + p * yh + qv * 8) = out;
   }
 }
 
@@ -95,12 +96,10 @@ static int pool_launch(const void* x, const int64_t* xs, void* y, const int64_t*
   const bool fast = sizeof(S) == 2 && kw == 2 && sw == 2 && dw == 1 && ph == 0 && pw == 0 && xs[3] == 1 &&
                     ys[3] == 1 && Q % 8 == 0 && windows_inside && (uintptr_t)x % 16 == 0 && (uintptr_t)y % 16 == 0 &&
                     (xs[0] * 2) % 16 == 0 && (xs[1] * 2) % 16 == 0 && (xs[2] * 2) % 16 == 0 &&
-                    (ys[0] * 2) % 16 == 0 && (ys[1] * 2) % 16 == 0 && (ys[2] * 2) % 16 == 0;
+                    (ys[0] * 2) % 16 == 0 && (ys[1] * 2) % 16 == 0 && (ys[2] * 2) % 16 == 0 && N * C <= 0x7fffffffLL &&
+                    H * xs[2] <= 0x7fffffffLL && P * ys[2] <= 0x7fffffffLL;
   if (fast) {
-    const int64_t total = N * C * P * (Q / 8);
-    int64_t blocks = cdiv(total, 256);
-    if (blocks > 256 * 32) blocks = 256 * 32;
-    hipLaunchKernelGGL(pool_w2_vec_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, stream, (const uint16_t*)x,
+    hipLaunchKernelGGL(pool_w2_plane_kernel<T>, dim3((unsigned)(N * C)), dim3(256), 0, stream, (const uint16_t*)x,
                        (uint16_t*)y, s);
   } else {
     int64_t blocks = cdiv(N * C * P * Q, 256);
