@@ -13,7 +13,7 @@
 //   multiplied out of LDS.  Workgroups are remapped so that the 8 XCDs (which the
 //   dispatcher fills round-robin) each receive a compact block of output tiles.
 // fp32 (config 1, 512^3): 32 x 32 workgroup tiles, four waves each computing a
-//   16 x 16 block with v_mfma_f32_16x16x4f32, k-tiles of 32 staged through LDS.
+//   16 x 16 block with v_mfma_f32_16x16x4f32, K staged through LDS 256 at a time.
 #include "mfma_core.h"
 
 #include <type_traits>
@@ -334,38 +334,71 @@ __global__ __launch_bounds__(512) void gemm_fast8_kernel(GemmArgs g) {
 }
 
 // ----------------------------------------------------------------------------- fp32
-constexpr int F32_TM = 32, F32_TN = 32, F32_TK = 32;
+constexpr int F32_TM = 32, F32_TN = 32, F32_KC = 256;
+constexpr int F32_AS = F32_KC + 4;  // a chunk row stride (floats): 16-byte aligned rows
+constexpr int F32_BS = F32_TN + 16;  // b chunk row stride: 32 lanes of one read hit 32 banks
 
+// fp32: 32 x 32 output tile per workgroup, four waves of 16 x 16 on
+// v_mfma_f32_16x16x4f32.  K is staged through LDS in chunks of 256 with 16-byte loads
+// (a 512-deep reduction takes two load phases instead of sixteen).
+template <bool VEC>
 __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g) {
-  __shared__ float sA[F32_TM][F32_TK + 1];
-  __shared__ float sB[F32_TK][F32_TN + 1];
+  __shared__ __attribute__((aligned(16))) float sA[F32_TM * F32_AS];
+  __shared__ __attribute__((aligned(16))) float sB[F32_KC * F32_BS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int tm = blockIdx.x / g.tiles_n, tn = blockIdx.x % g.tiles_n;
   const int64_t m0 = (int64_t)tm * F32_TM, n0 = (int64_t)tn * F32_TN;
-  const int wm = wave >> 1, wn = wave & 1;  // 16x16 sub-block of the 32x32 tile
+  const int wm = wave >> 1, wn = wave & 1;
   const float* A = (const float*)g.a;
   const float* B = (const float*)g.b;
-  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int64_t k0 = 0; k0 < g.K; k0 += F32_TK) {
-    for (int e = tid; e < F32_TM * F32_TK; e += 256) {
-      const int r = e / F32_TK, kk = e % F32_TK;
-      const int64_t m = m0 + r, k = k0 + kk;
-      sA[r][kk] = (m < g.M && k < g.K) ? A[m * g.sa_m + k * g.sa_k] : 0.f;
-    }
-    for (int e = tid; e < F32_TK * F32_TN; e += 256) {
-      const int kk = e / F32_TN, cidx = e % F32_TN;
-      const int64_t n = n0 + cidx, k = k0 + kk;
-      sB[kk][cidx] = (n < g.N && k < g.K) ? B[k * g.sb_k + n * g.sb_n] : 0.f;
+  floatx4 acc = {0.f, 0.f, 0.f, 0.f}, acc1 = acc, acc2 = acc, acc3 = acc;
+  for (int64_t k0 = 0; k0 < g.K; k0 += F32_KC) {
+    if (VEC) {  // full tiles, unit inner strides, 16-byte aligned rows
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const int e = it * 256 + tid;  // a: 32 rows x 64 float4
+        const int r = e >> 6, c4 = e & 63;
+        const int64_t k = k0 + c4 * 4;
+        float4 v = {0.f, 0.f, 0.f, 0.f};
+        if (k < g.K) v = *(const float4*)(A + (m0 + r) * g.sa_m + k);
+        *(float4*)(sA + r * F32_AS + c4 * 4) = v;
+      }
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const int e = it * 256 + tid;  // b: 256 rows x 8 float4
+        const int kk = e >> 3, c4 = e & 7;
+        const int64_t k = k0 + kk;
+        float4 v = {0.f, 0.f, 0.f, 0.f};
+        if (k < g.K) v = *(const float4*)(B + k * g.sb_k + n0 + c4 * 4);
+        *(float4*)(sB + kk * F32_BS + c4 * 4) = v;
+      }
+    } else {
+      for (int e = tid; e < F32_TM * F32_KC; e += 256) {
+        const int r = e / F32_KC, kk = e % F32_KC;
+        const int64_t m = m0 + r, k = k0 + kk;
+        sA[r * F32_AS + kk] = (m < g.M && k < g.K) ? A[m * g.sa_m + k * g.sa_k] : 0.f;
+      }
+      for (int e = tid; e < F32_KC * F32_TN; e += 256) {
+        const int kk = e / F32_TN, c = e % F32_TN;
+        const int64_t n = n0 + c, k = k0 + kk;
+        sB[kk * F32_BS + c] = (n < g.N && k < g.K) ? B[k * g.sb_k + n * g.sb_n] : 0.f;
+      }
     }
     __syncthreads();
-#pragma unroll
-    for (int kk = 0; kk < F32_TK; kk += 4) {
-      const float av = sA[wm * 16 + (lane & 15)][kk + (lane >> 4)];
-      const float bv = sB[kk + (lane >> 4)][wn * 16 + (lane & 15)];
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
+    const int kmax = (int)((g.K - k0 < F32_KC) ? (g.K - k0) : F32_KC);
+    const float* ap = sA + (wm * 16 + (lane & 15)) * F32_AS + (lane >> 4);
+    const float* bp = sB + (lane >> 4) * F32_BS + wn * 16 + (lane & 15);
+    int kk = 0;
+    for (; kk + 16 <= kmax; kk += 16) {  // four independent accumulator chains
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ap[kk], bp[kk * F32_BS], acc, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(ap[kk + 4], bp[(kk + 4) * F32_BS], acc1, 0, 0, 0);
+      acc2 = __builtin_amdgcn_mfma_f32_16x16x4f32(ap[kk + 8], bp[(kk + 8) * F32_BS], acc2, 0, 0, 0);
+      acc3 = __builtin_amdgcn_mfma_f32_16x16x4f32(ap[kk + 12], bp[(kk + 12) * F32_BS], acc3, 0, 0, 0);
     }
+    for (; kk < kmax; kk += 4) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ap[kk], bp[kk * F32_BS], acc, 0, 0, 0);
     __syncthreads();
   }
+  acc = (acc + acc1) + (acc2 + acc3);
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int64_t row = m0 + wm * 16 + (lane >> 4) * 4 + r;
@@ -431,7 +464,12 @@ static int gemm32_launch(GemmArgs g, hipStream_t stream) {
   if (tiles_m * tiles_n > 0x7fffffffLL) return NT_ERR_INVALID;
   g.tiles_m = (int)tiles_m;
   g.tiles_n = (int)tiles_n;
-  hipLaunchKernelGGL(gemm_f32_kernel, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, stream, g);
+  const bool vec = g.sa_k == 1 && g.sb_n == 1 && g.M % F32_TM == 0 && g.N % F32_TN == 0 && g.K % 4 == 0 &&
+                   g.sa_m % 4 == 0 && g.sb_k % 4 == 0 && (uintptr_t)g.a % 16 == 0 && (uintptr_t)g.b % 16 == 0;
+  if (vec)
+    hipLaunchKernelGGL(gemm_f32_kernel<true>, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, stream, g);
+  else
+    hipLaunchKernelGGL(gemm_f32_kernel<false>, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, stream, g);
   return launch_status();
 }
 

@@ -193,12 +193,23 @@ def _scalar_value(v):
 
 
 class Plan:
-    """A matched program bound to one kernel launcher; ``run(values)`` launches it."""
+    """A matched program bound to one kernel family.
+
+    ``bind(values, index)`` validates the sample ``values`` (parameter name -> value)
+    against the kernel and returns ``launch(args)``, where ``args`` is a sequence
+    laid out by ``index`` (parameter name -> position).  The launcher stays valid
+    for every call whose tensors agree with the sample in dtype, shape, strides
+    and device, and whose constexpr/meta values are the same.  ``run(values)``
+    binds and launches once."""
 
     family = "?"
 
-    def run(self, values):
+    def bind(self, values, index):
         raise NotImplementedError
+
+    def run(self, values):
+        names = tuple(values)
+        self.bind(values, {n: i for i, n in enumerate(names)})(tuple(values[n] for n in names))
 
     def describe(self):
         return {"family": self.family}
@@ -253,22 +264,47 @@ class GemmPlan(Plan):
         self.round_dtype = round_dtype
 
     @staticmethod
-    def _coef(factors, values):
-        total = 0.0
+    def _coef_fn(factors, index):
+        """args -> sum over terms of the product of its factors (constants or scalar arguments)."""
+        const, terms = 0.0, []
         for term in factors:
-            x = 1.0
+            x, names = 1.0, []
             for f in term:
-                x *= _scalar_value(values[f]) if isinstance(f, str) else f
-            total += x
-        return total
+                if isinstance(f, str):
+                    names.append(index[f])
+                else:
+                    x *= f
+            if names:
+                terms.append((x, tuple(names)))
+            else:
+                const += x
+        if not terms:
+            return lambda args: const
 
-    def run(self, values):
+        def coef(args):
+            total = const
+            for x, positions in terms:
+                for i in positions:
+                    x *= _scalar_value(args[i])
+                total += x
+            return total
+
+        return coef
+
+    def bind(self, values, index):
         from ninetoothed_amd import kernels
 
-        alpha = self._coef(self.alpha_factors, values)
-        beta = self._coef(self.beta_factors, values) if self.c else 0.0
-        kernels.gemm(values[self.a], values[self.b], values[self.out], c=values[self.c] if self.c else None,
-                     alpha=alpha, beta=beta, round_dtype=self.round_dtype)
+        launch = kernels.bind_gemm(values[self.a], values[self.b], values[self.out],
+                                   values[self.c] if self.c else None, round_dtype=self.round_dtype)
+        ia, ib, io = index[self.a], index[self.b], index[self.out]
+        ic = index[self.c] if self.c else None
+        alpha = self._coef_fn(self.alpha_factors, index)
+        beta = self._coef_fn(self.beta_factors, index) if self.c else (lambda args: 0.0)
+
+        def run(args):
+            launch(args[ia], args[ib], args[io], args[ic] if ic is not None else None, alpha(args), beta(args))
+
+        return run
 
     def describe(self):
         return {"family": "gemm", "a": self.a, "b": self.b, "out": self.out, "c": self.c,
@@ -283,18 +319,25 @@ class ConvPlan(Plan):
         self.padding, self.stride, self.dilation = padding, stride, dilation
         self.round_dtype = round_dtype
 
-    def run(self, values):
+    def bind(self, values, index):
+        import torch
+
         from ninetoothed_amd import kernels
 
         x, w, y = values[self.x], values[self.w], values[self.y]
         nbytes = kernels.conv2d_workspace_bytes(x, w, self.padding)
-        workspace = None
-        if nbytes > 0:
-            import torch
+        launch = kernels.bind_conv2d(x, w, y, padding=self.padding, stride=self.stride, dilation=self.dilation,
+                                     round_dtype=self.round_dtype, workspace_bytes=nbytes)
+        ix, iw, iy = index[self.x], index[self.w], index[self.y]
+        device = x.device
 
-            workspace = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
-        kernels.conv2d(x, w, y, padding=self.padding, stride=self.stride, dilation=self.dilation,
-                       round_dtype=self.round_dtype, workspace=workspace)
+        def run(args):
+            # The re-layout workspace comes from torch's stream-ordered caching allocator
+            # on every call, so calls on different streams never share one.
+            workspace = torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes else None
+            launch(args[ix], args[iw], args[iy], workspace)
+
+        return run
 
     def describe(self):
         return {"family": "conv2d", "padding": self.padding, "stride": self.stride, "dilation": self.dilation,
@@ -610,7 +653,7 @@ class AttentionPlan(Plan):
         self.scale = scale
         self.causal = causal
 
-    def run(self, values):
+    def bind(self, values, index):
         import torch
 
         from ninetoothed_amd import kernels
@@ -621,7 +664,14 @@ class AttentionPlan(Plan):
             # A Python float literal in `q * c` takes the tensor's type (weak typing of
             # scalars in the reference's generated kernel): c is rounded to q's dtype.
             scale = float(torch.tensor(scale, dtype=q.dtype))
-        kernels.attention(q, values[self.k], values[self.v], values[self.o], causal=self.causal, q_scale=scale)
+        launch = kernels.bind_attention(q, values[self.k], values[self.v], values[self.o], causal=self.causal,
+                                        q_scale=scale)
+        iq, ik, iv, io = index[self.q], index[self.k], index[self.v], index[self.o]
+
+        def run(args):
+            launch(args[iq], args[ik], args[iv], args[io])
+
+        return run
 
     def describe(self):
         return {"family": "attention", "causal": self.causal, "scale": self.scale}
@@ -683,10 +733,16 @@ class SoftmaxPlan(Plan):
     def __init__(self, x, y, block):
         self.x, self.y, self.block = x, y, block
 
-    def run(self, values):
+    def bind(self, values, index):
         from ninetoothed_amd import kernels
 
-        kernels.softmax(values[self.x], values[self.y], block=self.block)
+        launch = kernels.bind_softmax(values[self.x], values[self.y], block=self.block)
+        ix, iy = index[self.x], index[self.y]
+
+        def run(args):
+            launch(args[ix], args[iy])
+
+        return run
 
     def describe(self):
         return {"family": "softmax", "block": self.block}
@@ -740,11 +796,17 @@ class MaxPoolPlan(Plan):
         self.x, self.y = x, y
         self.window, self.stride, self.padding, self.dilation = window, stride, padding, dilation
 
-    def run(self, values):
+    def bind(self, values, index):
         from ninetoothed_amd import kernels
 
-        kernels.max_pool2d(values[self.x], values[self.y], self.window, stride=self.stride, padding=self.padding,
-                           dilation=self.dilation)
+        launch = kernels.bind_max_pool2d(values[self.x], values[self.y], self.window, stride=self.stride,
+                                         padding=self.padding, dilation=self.dilation)
+        ix, iy = index[self.x], index[self.y]
+
+        def run(args):
+            launch(args[ix], args[iy])
+
+        return run
 
     def describe(self):
         return {"family": "max_pool2d", "window": self.window, "stride": self.stride, "padding": self.padding}
@@ -830,13 +892,21 @@ class AddPlan(Plan):
     def __init__(self, a, b, out):
         self.a, self.b, self.out = a, b, out
 
-    def run(self, values):
+    def bind(self, values, index):
         from ninetoothed_amd import kernels
 
         a, b, o = values[self.a], values[self.b], values[self.out]
         if o.dim() != 1:
+            # Same-shaped operands walked as one flat range: each must be viewable as 1-D
+            # (a view keeps its data pointer, so the launcher takes the original tensors).
             a, b, o = a.view(-1), b.view(-1), o.view(-1)
-        kernels.add(a, b, o)
+        launch = kernels.bind_add(a, b, o)
+        ia, ib, io = index[self.a], index[self.b], index[self.out]
+
+        def run(args):
+            launch(args[ia], args[ib], args[io])
+
+        return run
 
     def describe(self):
         return {"family": "add"}

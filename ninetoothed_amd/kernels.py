@@ -1,14 +1,20 @@
 """Tensor-level launchers over the C ABI of libnt_mi355x.so.
 
-Each function takes PyTorch-ROCm tensors that already live on the GPU, checks
-what the kernel assumes (device, dtype, rank, sizes), and calls the matching
-``nt_*`` entry point on the caller's current stream.  Nothing here computes on the
-CPU and nothing falls back: an unsupported case raises, a non-zero status from the
-library raises :class:`KernelLaunchError` (the reference's error type,
-``src/ninetoothed/compiler/runtime.py:31-35``).
-"""
+Each operation comes in two forms:
 
-import ctypes
+- ``bind_<op>(...)`` takes sample tensors, checks what the kernel assumes (device,
+  dtype, rank, sizes) and returns a launcher closed over everything that depends
+  only on dtypes, shapes and strides (entry point, dims, stride arrays, device).
+  A launcher reads only data pointers, scalar values and the caller's current
+  stream, so a call costs a few microseconds of host time.  Callers re-bind
+  whenever a dtype, shape, stride or device changes (``runtime.Handle`` keys its
+  cache on exactly those).
+- ``<op>(...)`` binds and launches once.
+
+Nothing here computes on the CPU and nothing falls back: an unsupported case
+raises, a non-zero status from the library raises :class:`KernelLaunchError` (the
+reference's error type, ``src/ninetoothed/compiler/runtime.py:31-35``).
+"""
 
 from ninetoothed_amd import _lib
 from ninetoothed_amd.errors import KernelLaunchError
@@ -30,18 +36,28 @@ def _check_device(*tensors):
     return device
 
 
-def _ptr(t):
-    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+def _stream_of(device):
+    """A zero-argument function returning the raw handle of ``device``'s current stream."""
+    import torch
+
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    raw = torch._C._cuda_getCurrentRawStream
+    return lambda: raw(index)
 
 
-def _status(code, name):
-    if code != 0:
-        raise KernelLaunchError(code, name)
+def _entry(prefix, dtype):
+    fn = getattr(_lib.load(), f"{prefix}_{_lib.dtype_suffix(dtype)}")
+    return fn, fn.__name__
 
 
-def add(lhs, rhs, out):
-    """out = lhs + rhs over 1-D tensors of equal length (any strides)."""
-    _check_device(lhs, rhs, out)
+def _raise(code, name):
+    raise KernelLaunchError(code, name)
+
+
+# ------------------------------------------------------------------------- add
+def bind_add(lhs, rhs, out):
+    """launch(lhs, rhs, out): out = lhs + rhs over 1-D tensors of equal length (any strides)."""
+    device = _check_device(lhs, rhs, out)
     if not (lhs.dim() == rhs.dim() == out.dim() == 1):
         raise ValueError("add expects 1-D tensors")
     n = out.shape[0]
@@ -49,37 +65,56 @@ def add(lhs, rhs, out):
         raise ValueError("add operands differ in length")
     if not (lhs.dtype == rhs.dtype == out.dtype):
         raise TypeError("add operands must share one dtype")
-    lib = _lib.load()
-    fn = getattr(lib, f"nt_add_{_lib.dtype_suffix(out.dtype)}")
-    with_stream = _lib.current_stream(out.device)
-    _status(fn(_ptr(lhs), lhs.stride(0), _ptr(rhs), rhs.stride(0), _ptr(out), out.stride(0), n, with_stream), fn.__name__)
+    fn, name = _entry("nt_add", out.dtype)
+    sl, sr, so = lhs.stride(0), rhs.stride(0), out.stride(0)
+    stream = _stream_of(device)
+
+    def launch(lhs, rhs, out):
+        code = fn(lhs.data_ptr(), sl, rhs.data_ptr(), sr, out.data_ptr(), so, n, stream())
+        if code:
+            _raise(code, name)
+
+    return launch
+
+
+def add(lhs, rhs, out):
+    bind_add(lhs, rhs, out)(lhs, rhs, out)
     return out
 
 
-def softmax(x, y, block=None):
-    """Row softmax of a 2-D tensor over segments of ``block`` columns (default: whole rows)."""
-    _check_device(x, y)
+# --------------------------------------------------------------------- softmax
+def bind_softmax(x, y, block=None):
+    """launch(x, y): row softmax of a 2-D tensor over segments of ``block`` columns (default: whole rows)."""
+    device = _check_device(x, y)
     if x.dim() != 2 or y.shape != x.shape:
         raise ValueError("softmax expects matching 2-D tensors")
     if x.dtype != y.dtype:
         raise TypeError("softmax input and output must share one dtype")
     rows, cols = x.shape
-    block = cols if block is None else int(block)
+    block = max(cols if block is None else int(block), 1)
     if cols > 1 and (x.stride(1) != 1 or y.stride(1) != 1):
         raise ValueError("softmax needs unit column stride")
-    lib = _lib.load()
-    fn = getattr(lib, f"nt_softmax_{_lib.dtype_suffix(x.dtype)}")
-    _status(
-        fn(_ptr(x), x.stride(0), x.stride(1), _ptr(y), y.stride(0), y.stride(1), rows, cols, max(block, 1),
-           _lib.current_stream(x.device)),
-        fn.__name__,
-    )
+    fn, name = _entry("nt_softmax", x.dtype)
+    (xr, xc), (yr, yc) = x.stride(), y.stride()
+    stream = _stream_of(device)
+
+    def launch(x, y):
+        code = fn(x.data_ptr(), xr, xc, y.data_ptr(), yr, yc, rows, cols, block, stream())
+        if code:
+            _raise(code, name)
+
+    return launch
+
+
+def softmax(x, y, block=None):
+    bind_softmax(x, y, block)(x, y)
     return y
 
 
-def max_pool2d(x, y, window, stride=None, padding=(0, 0), dilation=(1, 1)):
-    """y = max_pool2d(x) with -inf outside the input (any strides, N-C-H-W indexing)."""
-    _check_device(x, y)
+# ------------------------------------------------------------------ max_pool2d
+def bind_max_pool2d(x, y, window, stride=None, padding=(0, 0), dilation=(1, 1)):
+    """launch(x, y): y = max_pool2d(x) with -inf outside the input (any strides, N-C-H-W indexing)."""
+    device = _check_device(x, y)
     if x.dim() != 4 or y.dim() != 4:
         raise ValueError("max_pool2d expects 4-D tensors")
     if x.dtype != y.dtype:
@@ -92,19 +127,30 @@ def max_pool2d(x, y, window, stride=None, padding=(0, 0), dilation=(1, 1)):
     if y.shape[0] != n or y.shape[1] != c:
         raise ValueError("max_pool2d batch/channel sizes differ")
     p, q = y.shape[2], y.shape[3]
-    lib = _lib.load()
-    fn = getattr(lib, f"nt_max_pool2d_{_lib.dtype_suffix(x.dtype)}")
-    _status(
-        fn(_ptr(x), _lib.int64_array(x.stride()), _ptr(y), _lib.int64_array(y.stride()), n, c, h, w, p, q, kh, kw, sh,
-           sw, ph, pw, dh, dw, _lib.current_stream(x.device)),
-        fn.__name__,
-    )
+    fn, name = _entry("nt_max_pool2d", x.dtype)
+    xs, ys = _lib.int64_array(x.stride()), _lib.int64_array(y.stride())
+    dims = (n, c, h, w, p, q, kh, kw, sh, sw, ph, pw, dh, dw)
+    stream = _stream_of(device)
+
+    def launch(x, y):
+        code = fn(x.data_ptr(), xs, y.data_ptr(), ys, *dims, stream())
+        if code:
+            _raise(code, name)
+
+    return launch
+
+
+def max_pool2d(x, y, window, stride=None, padding=(0, 0), dilation=(1, 1)):
+    bind_max_pool2d(x, y, window, stride, padding, dilation)(x, y)
     return y
 
 
-def gemm(a, b, out, c=None, alpha=1.0, beta=0.0, round_dtype=None):
-    """out = cast(beta * c + alpha * round(a @ b)); fp32 accumulation; any strides."""
-    _check_device(a, b, out, c)
+# ------------------------------------------------------------------------ gemm
+def bind_gemm(a, b, out, c=None, round_dtype=None):
+    """launch(a, b, out, c, alpha, beta): out = cast(beta * c + alpha * round(a @ b)).
+
+    fp32 accumulation; any strides; ``c`` is None exactly when it was None here."""
+    device = _check_device(a, b, out, c)
     if a.dim() != 2 or b.dim() != 2 or out.dim() != 2:
         raise ValueError("gemm expects 2-D tensors")
     m, k = a.shape
@@ -119,21 +165,41 @@ def gemm(a, b, out, c=None, alpha=1.0, beta=0.0, round_dtype=None):
         if c.dtype != out.dtype:
             raise TypeError("gemm bias and output must share one dtype")
     rd = _lib.DTYPE_NONE if round_dtype is None else _lib.dtype_code(round_dtype)
-    lib = _lib.load()
-    fn = getattr(lib, f"nt_gemm_{_lib.dtype_suffix(a.dtype)}")
-    sc = c.stride() if c is not None else (0, 0)
-    _status(
-        fn(_ptr(a), a.stride(0), a.stride(1), _ptr(b), b.stride(0), b.stride(1), _ptr(c), sc[0], sc[1], _ptr(out),
-           out.stride(0), out.stride(1), _lib.dtype_code(out.dtype), m, n, k, float(alpha), float(beta), rd,
-           _lib.current_stream(a.device)),
-        fn.__name__,
-    )
+    fn, name = _entry("nt_gemm", a.dtype)
+    (sa_m, sa_k), (sb_k, sb_n), (so_m, so_n) = a.stride(), b.stride(), out.stride()
+    sc_m, sc_n = c.stride() if c is not None else (0, 0)
+    out_code = _lib.dtype_code(out.dtype)
+    stream = _stream_of(device)
+
+    def launch(a, b, out, c, alpha, beta):
+        code = fn(a.data_ptr(), sa_m, sa_k, b.data_ptr(), sb_k, sb_n, c.data_ptr() if c is not None else None, sc_m,
+                  sc_n, out.data_ptr(), so_m, so_n, out_code, m, n, k, alpha, beta, rd, stream())
+        if code:
+            _raise(code, name)
+
+    return launch
+
+
+def gemm(a, b, out, c=None, alpha=1.0, beta=0.0, round_dtype=None):
+    bind_gemm(a, b, out, c, round_dtype)(a, b, out, c, float(alpha), float(beta))
     return out
 
 
-def conv2d(x, w, y, padding=(0, 0), stride=(1, 1), dilation=(1, 1), round_dtype=None, workspace=None):
-    """y = cast(round(conv2d(x, w))) as an implicit GEMM (cross-correlation, zero padding)."""
-    _check_device(x, w, y, workspace)
+# ---------------------------------------------------------------------- conv2d
+def conv2d_workspace_bytes(x, w, padding=(0, 0)):
+    """Bytes of the workspace that lets conv2d take its re-layout path (0: none needed)."""
+    lib = _lib.load()
+    n, c, h, wd = x.shape
+    k, _, r, s = w.shape
+    return int(lib.nt_conv2d_workspace_size(n, c, h, wd, k, r, s, padding[0], padding[1], _lib.dtype_code(x.dtype)))
+
+
+def bind_conv2d(x, w, y, padding=(0, 0), stride=(1, 1), dilation=(1, 1), round_dtype=None, workspace_bytes=0):
+    """launch(x, w, y, workspace): y = cast(round(conv2d(x, w))) as an implicit GEMM.
+
+    Cross-correlation with zero padding.  ``workspace`` is a device buffer of at
+    least ``workspace_bytes`` bytes, or None when ``workspace_bytes`` is 0."""
+    device = _check_device(x, w, y)
     if x.dim() != 4 or w.dim() != 4 or y.dim() != 4:
         raise ValueError("conv2d expects 4-D tensors")
     if x.dtype != w.dtype:
@@ -147,28 +213,36 @@ def conv2d(x, w, y, padding=(0, 0), stride=(1, 1), dilation=(1, 1), round_dtype=
     sh, sw = stride
     dh, dw = dilation
     rd = _lib.DTYPE_NONE if round_dtype is None else _lib.dtype_code(round_dtype)
-    lib = _lib.load()
-    fn = getattr(lib, f"nt_conv2d_{_lib.dtype_suffix(x.dtype)}")
-    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
-    _status(
-        fn(_ptr(x), _lib.int64_array(x.stride()), _ptr(w), _lib.int64_array(w.stride()), _ptr(y),
-           _lib.int64_array(y.stride()), _lib.dtype_code(y.dtype), n, c, h, wd, k, r, s, p, q, ph, pw, sh, sw, dh, dw,
-           rd, _ptr(workspace), ws_bytes, _lib.current_stream(x.device)),
-        fn.__name__,
-    )
+    fn, name = _entry("nt_conv2d", x.dtype)
+    xs, ws, ys = (_lib.int64_array(t.stride()) for t in (x, w, y))
+    dims = (_lib.dtype_code(y.dtype), n, c, h, wd, k, r, s, p, q, ph, pw, sh, sw, dh, dw, rd)
+    stream = _stream_of(device)
+
+    def launch(x, w, y, workspace):
+        wp = None
+        if workspace is not None:
+            if workspace.device != device:
+                raise TypeError("All tensor arguments must use the same GPU.")
+            wp = workspace.data_ptr()
+        code = fn(x.data_ptr(), xs, w.data_ptr(), ws, y.data_ptr(), ys, *dims, wp, workspace_bytes, stream())
+        if code:
+            _raise(code, name)
+
+    return launch
+
+
+def conv2d(x, w, y, padding=(0, 0), stride=(1, 1), dilation=(1, 1), round_dtype=None, workspace=None):
+    nbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    if workspace is not None:
+        _check_device(x, workspace)
+    bind_conv2d(x, w, y, padding, stride, dilation, round_dtype, nbytes)(x, w, y, workspace)
     return y
 
 
-def conv2d_workspace_bytes(x, w, padding=(0, 0)):
-    lib = _lib.load()
-    n, c, h, wd = x.shape
-    k, _, r, s = w.shape
-    return int(lib.nt_conv2d_workspace_size(n, c, h, wd, k, r, s, padding[0], padding[1], _lib.dtype_code(x.dtype)))
-
-
-def attention(q, k, v, o, causal=False, q_scale=LOG2E):
-    """Flash attention forward of the reference application; q pre-scaled by ``q_scale``."""
-    _check_device(q, k, v, o)
+# ------------------------------------------------------------------- attention
+def bind_attention(q, k, v, o, causal=False, q_scale=LOG2E):
+    """launch(q, k, v, o): flash attention forward of the reference application; q pre-scaled by ``q_scale``."""
+    device = _check_device(q, k, v, o)
     if not (q.dim() == k.dim() == v.dim() == o.dim() == 4):
         raise ValueError("attention expects [B, H, S, D] tensors")
     if not (q.dtype == k.dtype == v.dtype):
@@ -179,12 +253,19 @@ def attention(q, k, v, o, causal=False, q_scale=LOG2E):
         raise ValueError("attention shape mismatch")
     if d > 128:
         raise ValueError("attention head dim must be <= 128")
-    lib = _lib.load()
-    fn = getattr(lib, f"nt_attention_{_lib.dtype_suffix(q.dtype)}")
-    _status(
-        fn(_ptr(q), _lib.int64_array(q.stride()), _ptr(k), _lib.int64_array(k.stride()), _ptr(v),
-           _lib.int64_array(v.stride()), _ptr(o), _lib.int64_array(o.stride()), _lib.dtype_code(o.dtype), bsz, heads,
-           sq, sk, d, float(q_scale), 1 if causal else 0, _lib.current_stream(q.device)),
-        fn.__name__,
-    )
+    fn, name = _entry("nt_attention", q.dtype)
+    qs, ks, vs, os_ = (_lib.int64_array(t.stride()) for t in (q, k, v, o))
+    tail = (_lib.dtype_code(o.dtype), bsz, heads, sq, sk, d, float(q_scale), 1 if causal else 0)
+    stream = _stream_of(device)
+
+    def launch(q, k, v, o):
+        code = fn(q.data_ptr(), qs, k.data_ptr(), ks, v.data_ptr(), vs, o.data_ptr(), os_, *tail, stream())
+        if code:
+            _raise(code, name)
+
+    return launch
+
+
+def attention(q, k, v, o, causal=False, q_scale=LOG2E):
+    bind_attention(q, k, v, o, causal, q_scale)(q, k, v, o)
     return o

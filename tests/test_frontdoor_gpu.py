@@ -224,3 +224,45 @@ def test_empty_output_launches_nothing():
     out = torch.empty((0, 8), dtype=torch.float16, device=DEV)
     assert kernel(torch.empty((0, 4), dtype=torch.float16, device=DEV),
                   torch.empty((4, 8), dtype=torch.float16, device=DEV), out) is out
+
+
+# ----------------------------------------------------------- bound-launcher cache
+def test_repeat_calls_take_new_data_and_scalars():
+    kernel = ninetoothed.make(pg.addmm_arrangement, pg.addmm_application, pg.addmm_tensors())
+    output = torch.empty((256, 192), dtype=torch.float16, device=DEV)
+    for i, (beta, alpha) in enumerate(((0.5, 1.25), (-1.0, 0.25), (0.0, 2.0))):
+        input, mat1, mat2 = _randn((256, 192), torch.float16, 70 + i), _randn((256, 128), torch.float16, 80 + i), \
+            _randn((128, 192), torch.float16, 90 + i)
+        assert kernel(input, mat1, mat2, beta, alpha, output) is output
+        ref = apply.addmm(_np(input), _np(mat1), _np(mat2), beta, alpha, "float16", pg.addmm_arrangement,
+                          block=(64, 64, 64))
+        assert np.allclose(_np(output), ref, atol=2e-2, rtol=1e-2), (beta, alpha)
+    assert len(kernel.plans()) == 1
+
+
+def test_stride_or_shape_change_rebinds():
+    kernel = ninetoothed.make(pg.matmul_arrangement, pg.matmul_application, pg.matmul_tensors())
+    lhs = _randn((192, 320), torch.float16, 100)
+    rhs = _randn((320, 256), torch.float16, 101)
+    rhs_t = _randn((256, 320), torch.float16, 102).t()  # same shape as rhs, k-contiguous
+    for a, b in ((lhs, rhs), (lhs, rhs_t), (lhs[:64], rhs), (lhs, rhs)):
+        out = torch.empty((a.shape[0], b.shape[1]), dtype=torch.float16, device=DEV)
+        kernel(a, b, out)
+        assert torch.allclose(out.float(), a.float() @ b.float(), atol=2e-2, rtol=1e-2)
+    assert len(kernel.plans()) == 3
+
+
+def test_cached_key_still_checks_arguments():
+    kernel = ninetoothed.make(pg.matmul_arrangement, pg.matmul_application, pg.matmul_tensors())
+    lhs, rhs = _randn((64, 64), torch.float16, 103), _randn((64, 64), torch.float16, 104)
+    out = torch.empty((64, 64), dtype=torch.float16, device=DEV)
+    kernel(lhs, rhs, out)
+    with pytest.raises(TypeError):
+        kernel(lhs.cpu(), rhs, out)
+    with pytest.raises(TypeError):
+        kernel(lhs, rhs)
+    with pytest.raises(TypeError):
+        kernel(lhs, rhs, out, output=out)
+    out2 = torch.zeros_like(out)
+    kernel(lhs, rhs, output=out2)  # public argument by keyword: the checked path
+    assert torch.equal(out2, out)

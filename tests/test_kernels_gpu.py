@@ -193,7 +193,7 @@ def test_gemm_transposed_operands():
     assert torch.allclose(out.float(), _gemm_ref(a, b).float(), atol=2e-2, rtol=1e-2)
 
 
-@pytest.mark.parametrize("mnk", ((512, 512, 512), (100, 70, 33)))
+@pytest.mark.parametrize("mnk", ((512, 512, 512), (100, 70, 33), (256, 128, 1000), (64, 32, 260), (64, 64, 514)))
 def test_gemm_f32(mnk):
     m, n, k = mnk
     a = _randn((m, k), torch.float32, 21)
