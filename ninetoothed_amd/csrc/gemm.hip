@@ -1,18 +1,22 @@
 // GEMM with the addmm epilogue:  out = cast_out(beta * c + alpha * round(sum_k a*b)).
 //
-// fp16 / bf16 (MFMA-bound; 2*M*N*K flops per launch):
-//   workgroup tile 256 x 256 x 64 on v_mfma_f32_32x32x16_{f16,bf16}; the fast path runs
-//   8 waves (64 x 128 each), the generic path 4 waves (128 x 128 each).  Both operands sit in LDS k-contiguous
-//   ([m][k] for a, [n][k] for b) so that each lane fetches its 8 k-values for an MFMA
-//   with one ds_read_b128.  b arrives n-contiguous from HBM: each lane loads an
-//   8(k) x 8(n) block with eight 16-byte loads and transposes it in registers
-//   before a 16-byte LDS store.  LDS rows are 128 bytes; the 16-byte chunk index is
-//   XOR-swizzled with (row ^ row >> 3) & 7 so that both the row-wise reads of the
-//   MFMA fetch and the transposed b stores hit 8 distinct chunks per 8 lanes.
-//   The next k-tile is fetched from HBM into registers while the current one is
-//   multiplied out of LDS.  Workgroups are remapped so that the 8 XCDs (which the
-//   dispatcher fills round-robin) each receive a compact block of output tiles.
-// fp32 (config 1, 512^3): 32 x 32 workgroup tiles, four waves each computing a
+// fp16 / bf16 (MFMA-bound; 2*M*N*K flops per launch): workgroup tile 256 x 256 x 64 on
+// v_mfma_f32_32x32x16_{f16,bf16}.  Kernels, fastest first:
+//   gemm_w4_kernel     a k-contiguous, b n-contiguous, M, N multiples of 256, K of 128:
+//                      4 waves of 128 x 128 (one per SIMD, accumulators in the
+//                      accumulator file), a fixed 64-slot issue schedule per k-tile;
+//   gemm_fast8_kernel  same layouts, K a multiple of 64: 8 waves of 64 x 128;
+//   gemm_mfma_kernel   anything else (any strides, ragged edges, zero fill).
+// Both operands sit in LDS k-contiguous ([m][k] for a, [n][k] for b) so that each lane
+// fetches its 8 k-values for an MFMA with one ds_read_b128.  b arrives n-contiguous
+// from HBM: each lane loads an 8(k) x 8(n) block (or 4(k) x 8(n)) with 16-byte loads
+// and transposes it in registers before storing it.  LDS rows are 128 bytes; the
+// 16-byte chunk index is XOR-swizzled with (row ^ row >> 3) & 7 so that both the
+// row-wise fragment reads and the transposed b stores hit 8 distinct chunks per 8
+// lanes.  The next k-tile is fetched from HBM into registers while the current one is
+// multiplied out of LDS (two LDS buffers).  Workgroups are remapped so that the 8 XCDs
+// (which the dispatcher fills round-robin) each receive a compact block of tiles.
+// fp32 (512^3 reference case): 32 x 32 workgroup tiles, four waves each computing a
 //   16 x 16 block with v_mfma_f32_16x16x4f32, K staged through LDS 256 at a time.
 #include "mfma_core.h"
 
@@ -55,56 +59,81 @@ __device__ __forceinline__ void tile_of(int wg, int tiles_m, int tiles_n, int& t
 }
 
 // Epilogue shared by the GEMM kernels: out = cast(beta * c + alpha * round(acc)), one
-// 32-row slab per pass staged through LDS (16 KiB per wave), then each lane handles 8
-// consecutive columns: 16-byte loads of c and 16-byte stores of out when both are
-// 16-bit, unit-stride and aligned, element-wise otherwise.
+// 32-row slab per pass staged through LDS (32 x WJ*32 fp32 per wave), then each lane
+// handles 8 consecutive columns.
+//
+// Fast path (the wave's whole tile in bounds, c and out 16-bit, unit column stride,
+// 16-byte aligned rows): all of a slab's c vectors are loaded at once, the next slab's
+// while the current one is stored, so the epilogue pays the HBM latency about once
+// instead of once per vector; 16-byte loads and stores.  A wave only reads back what it
+// staged itself, so the slabs need no workgroup barrier.  Otherwise element-wise with
+// bounds checks and any strides.
 template <int WI, int WJ>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, const floatx16 (&acc)[WI][WJ], uint16_t* smem,
                                               int wave, int lane, int64_t row_base, int64_t col_base) {
   constexpr int COLS = WJ * 32;
+  constexpr int VPR = COLS / 8;          // 16-byte vectors per row
+  constexpr int VPL = 32 * VPR / 64;     // per lane per slab
   float* stage = (float*)smem + wave * (32 * COLS);
   const bool vec16 = g.out_dtype != NT_DTYPE_F32 && g.so_n == 1 && (g.so_m % 8) == 0 && ((uintptr_t)g.out % 16) == 0 &&
                      (!g.c || (g.sc_n == 1 && (g.sc_m % 8) == 0 && ((uintptr_t)g.c % 16) == 0));
-  __syncthreads();
+  const bool full = vec16 && row_base + WI * 32 <= g.M && col_base + COLS <= g.N;
+  __syncthreads();  // the LDS still holds operand tiles other waves may be reading
+  if (full) {
+    const bool f16 = g.out_dtype == NT_DTYPE_F16;
+    const uint16_t* C = (const uint16_t*)g.c;
+    uint16_t* O = (uint16_t*)g.out;
+    u32x4 cv[2][VPL];
+    auto load_c = [&](int i, int buf) {
+#pragma unroll
+      for (int t = 0; t < VPL; ++t) {
+        const int e = t * 64 + lane, rr = e / VPR, cg = (e % VPR) * 8;
+        cv[buf][t] = *(const u32x4*)(C + (row_base + i * 32 + rr) * g.sc_m + col_base + cg);
+      }
+    };
+    if (g.c) load_c(0, 0);
+#pragma unroll
+    for (int i = 0; i < WI; ++i) {
+      if (g.c && i + 1 < WI) load_c(i + 1, (i + 1) & 1);
+      stage_slab<WJ>(stage, acc[i], lane);
+#pragma unroll
+      for (int t = 0; t < VPL; ++t) {
+        const int e = t * 64 + lane, rr = e / VPR, cg = (e % VPR) * 8;
+        const float4 v0 = *(const float4*)(stage + rr * COLS + cg);
+        const float4 v1 = *(const float4*)(stage + rr * COLS + cg + 4);
+        const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        const uint16_t* ch = (const uint16_t*)&cv[i & 1][t];
+        u32x4 oraw;
+        uint16_t* oh = (uint16_t*)&oraw;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          float r = g.alpha * round_through(v[u], g.round_dtype);
+          if (g.c) r += g.beta * (f16 ? f16_bits_to_float(ch[u]) : bf16_bits_to_float(ch[u]));
+          oh[u] = f16 ? float_to_f16_bits(r) : float_to_bf16_bits(r);
+        }
+        *(u32x4*)(O + (row_base + i * 32 + rr) * g.so_m + col_base + cg) = oraw;
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < WI; ++i) {
     stage_slab<WJ>(stage, acc[i], lane);
-    __syncthreads();
     const int64_t row0 = row_base + i * 32;
-    for (int e = lane; e < 32 * (COLS / 8); e += 64) {
-      const int rr = e / (COLS / 8), cg = (e % (COLS / 8)) * 8;
+    for (int e = lane; e < 32 * VPR; e += 64) {
+      const int rr = e / VPR, cg = (e % VPR) * 8;
       const int64_t row = row0 + rr, col = col_base + cg;
       if (row >= g.M) continue;
       const float4 v0 = *(const float4*)(stage + rr * COLS + cg);
       const float4 v1 = *(const float4*)(stage + rr * COLS + cg + 4);
       float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-      if (vec16 && col + 8 <= g.N) {
-        float cv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        if (g.c) {
-          const u32x4 craw = *(const u32x4*)((const uint16_t*)g.c + row * g.sc_m + col);
-          const uint16_t* ch = (const uint16_t*)&craw;
-#pragma unroll
-          for (int u = 0; u < 8; ++u)
-            cv[u] = g.out_dtype == NT_DTYPE_F16 ? f16_bits_to_float(ch[u]) : bf16_bits_to_float(ch[u]);
-        }
-        u32x4 oraw;
-        uint16_t* oh = (uint16_t*)&oraw;
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const float r = g.alpha * round_through(v[u], g.round_dtype) + g.beta * cv[u];
-          oh[u] = g.out_dtype == NT_DTYPE_F16 ? float_to_f16_bits(r) : float_to_bf16_bits(r);
-        }
-        *(u32x4*)((uint16_t*)g.out + row * g.so_m + col) = oraw;
-      } else {
-        for (int u = 0; u < 8; ++u) {
-          if (col + u >= g.N) break;
-          float r = g.alpha * round_through(v[u], g.round_dtype);
-          if (g.c) r += g.beta * load_as_float(g.c, row * g.sc_m + (col + u) * g.sc_n, g.out_dtype);
-          store_from_float(g.out, row * g.so_m + (col + u) * g.so_n, g.out_dtype, r);
-        }
+      for (int u = 0; u < 8; ++u) {
+        if (col + u >= g.N) break;
+        float r = g.alpha * round_through(v[u], g.round_dtype);
+        if (g.c) r += g.beta * load_as_float(g.c, row * g.sc_m + (col + u) * g.sc_n, g.out_dtype);
+        store_from_float(g.out, row * g.so_m + (col + u) * g.so_n, g.out_dtype, r);
       }
     }
-    __syncthreads();
   }
 }
 
@@ -333,6 +362,228 @@ __global__ __launch_bounds__(512) void gemm_fast8_kernel(GemmArgs g) {
   gemm_epilogue<2, 4>(g, acc, smem, wave, lane, m0 + wm * 64, n0 + wn * 128);
 }
 
+// Fast path, four-wave form: 256 lanes, one wave per SIMD in a 2 x 2 grid, each owning
+// 128 x 128 of the 256 x 256 tile (256 accumulators, kept in the accumulator file).
+// Per 16-deep slice a wave reads 8 KiB of fragments for 16 MFMAs, two thirds of the
+// LDS traffic per flop of a 64 x 128 wave tile.
+//
+// LDS (bytes): a tiles at 0 and 32 Ki, b tiles at 64 Ki and 96 Ki, so with the buffer
+// index static (the k loop is unrolled by two) every LDS access is a per-lane base
+// register plus an immediate offset.  Global operands go through buffer loads whose
+// k-dependent part is a scalar offset, so the loop spends vector ALU only on the b
+// transposes (v_perm_b32).  Each k-tile is a fixed issue schedule of 64 MFMA slots
+// (below): fragments read a slice ahead, tile kt+1 stored into the other buffer and
+// tile kt+2 fetched at an even rate, barrier before the last slice.
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+namespace w4 {
+constexpr int A_BYTES = GB_M * GB_K * 2;  // 32 KiB
+constexpr int B_BASE = 2 * A_BYTES;       // 64 KiB
+
+__device__ __forceinline__ uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel) {
+  return __builtin_amdgcn_perm(s0, s1, sel);
+}
+// 8x8 transpose of 16-bit values, as transpose8x8 but one v_perm_b32 per output dword.
+__device__ __forceinline__ void transpose8x8_perm(const u32x4 (&in)[8], u32x4 (&out)[8]) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int d = j >> 1;
+    const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+    out[j] = u32x4{perm(in[1][d], in[0][d], sel), perm(in[3][d], in[2][d], sel), perm(in[5][d], in[4][d], sel),
+                   perm(in[7][d], in[6][d], sel)};
+  }
+}
+}  // namespace w4
+
+template <typename T>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_w4_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (GB_M + GB_N) * GB_K];
+  char* lds = (char*)smem;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;  // 2 x 2
+  int tm, tn;
+  tile_of(blockIdx.x, g.tiles_m, g.tiles_n, tm, tn);
+  const int64_t m0 = (int64_t)tm * GB_M, n0 = (int64_t)tn * GB_N;
+  const int nk = (int)(g.K / GB_K);
+
+  // Global side: a rows a_row + 32 i (i < 8), one 16-byte chunk each; b an 8(k) x 8(n)
+  // block.  Byte offsets within each operand's panel fit in 32 bits (checked on the host).
+  const int a_row = tid >> 3, a_chunk = tid & 7;
+  const int b_nb = tid & 31, b_kb = tid >> 5;
+  const __amdgpu_buffer_rsrc_t rsA = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const uint16_t*)g.a + m0 * g.sa_m), (short)0, (int)(((GB_M - 1) * g.sa_m + g.K) * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsB = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const uint16_t*)g.b + n0), (short)0, (int)(((g.K - 1) * g.sb_k + GB_N) * 2), 0x00020000);
+  const int va = (int)(a_row * g.sa_m * 2 + a_chunk * 16);
+  const int vb = (int)(b_kb * 8 * g.sb_k * 2 + b_nb * 16);
+  const int a_istep = (int)(32 * g.sa_m * 2);  // bytes between a rows i and i+1
+  const int b_rstep = (int)(g.sb_k * 2);       // bytes between b rows r and r+1
+
+  // LDS side.  Stores: a row i*32 + a_row has the swizzle of i & 1 (rows 64 apart share
+  // it); b row b_nb*8 + j has its own.  Reads: fragment rows of i and i + 2 (j, j + 2)
+  // are 64 rows apart and share a swizzle.
+  int a_st[2], b_st[8], a_rd[4][2], b_rd[4][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int row = i * 32 + a_row;
+    a_st[i] = (row * GB_K + swz(row, a_chunk) * 8) * 2;
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int row = b_nb * 8 + j;
+    b_st[j] = w4::B_BASE + (row * GB_K + swz(row, b_kb) * 8) * 2;
+  }
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int chunk = kk * 2 + (lane >> 5);
+      const int ra_row = wm * 128 + h * 32 + (lane & 31);
+      const int rb_row = wn * 128 + h * 32 + (lane & 31);
+      a_rd[kk][h] = (ra_row * GB_K + swz(ra_row, chunk) * 8) * 2;
+      b_rd[kk][h] = w4::B_BASE + (rb_row * GB_K + swz(rb_row, chunk) * 8) * 2;
+    }
+
+  floatx16 acc[4][4];
+  zero_acc(acc);
+  u32x4 ra[8], rb[8];
+  auto load_a = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ra[i] = __builtin_amdgcn_raw_buffer_load_b128(rsA, va, i * a_istep + kt * 128, 0);
+  };
+  auto load_b = [&](int kt) {
+#pragma unroll
+    for (int r = 0; r < 8; ++r) rb[r] = __builtin_amdgcn_raw_buffer_load_b128(rsB, vb, (kt * 64 + r) * b_rstep, 0);
+  };
+  auto store_a = [&](auto buf_c) {
+    constexpr int OFF = decltype(buf_c)::value * w4::A_BYTES;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) *(u32x4*)(lds + a_st[i & 1] + (i >> 1) * 8192 + OFF) = ra[i];
+  };
+  auto store_b = [&](auto buf_c) {
+    constexpr int OFF = decltype(buf_c)::value * w4::A_BYTES;
+    u32x4 tb[8];
+    w4::transpose8x8_perm(rb, tb);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) *(u32x4*)(lds + b_st[j] + OFF) = tb[j];
+  };
+
+  typedef typename mfma_traits<T>::frag frag;
+  frag fa[2][4], fb[2][4];
+  u32x4 tb[8];
+  // Fragment x of a slice: x < 4 is a row block, x >= 4 a column block.
+  auto read_frag = [&](auto buf_c, int kk, int slot, int x) {
+    constexpr int OFF = decltype(buf_c)::value * w4::A_BYTES;
+    if (x < 4)
+      fa[slot][x] = *(const frag*)(lds + a_rd[kk][x & 1] + (x >> 1) * 8192 + OFF);
+    else
+      fb[slot][x - 4] = *(const frag*)(lds + b_rd[kk][x & 1] + ((x - 4) >> 1) * 8192 + OFF);
+  };
+  auto read_frags = [&](auto buf_c, int kk, int slot) {
+#pragma unroll
+    for (int x = 0; x < 8; ++x) read_frag(buf_c, kk, slot, x);
+  };
+  auto mma1 = [&](int slot, int x) {
+    const int i = x >> 2, j = x & 3;
+    acc[i][j] = mfma_traits<T>::mma(fa[slot][i], fb[slot][j], acc[i][j]);
+  };
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+
+  load_a(0);
+  load_b(0);
+  store_a(B0{});
+  store_b(B0{});
+  if (nk > 1) {
+    load_a(1);
+    load_b(1);
+  }
+  __syncthreads();
+  read_frags(B0{}, 0, 0);
+
+  // Issue schedule of one k-tile: 64 MFMA slots m (slice m / 16, x = m % 16), each
+  // MFMA followed by the memory work of its slot, fenced so the order is kept:
+  //   fragment reads for the next slice: even x in slices 0-1, x < 8 in slices 2-3
+  //     (all done before the barrier / well before use), in the order the next
+  //     slice's MFMAs consume them (a0 b0 b1 b2 b3 a1 a2 a3);
+  //   b of tile kt+1: column j transposed in slot j, stored in slot 3j (0..21);
+  //     row r of tile kt+2 fetched in slot 8 + 3r (after every column is transposed);
+  //   a of tile kt+1: row block i stored in slot 22 + 3i (22..43), refetched for tile
+  //     kt+2 in the same slot;
+  //   barrier before slot 48 (slice 3), whose reads come from the other buffer.
+  // LDS writes are spread one per three MFMAs so four waves never fill the LDS data
+  // queue, and every global load has at least a half k-tile before its use.
+#define NT_FENCE() __builtin_amdgcn_sched_barrier(0)
+  auto step = [&](auto cur_c, auto has1_c, auto has2_c, int kt) {
+    constexpr int CUR = decltype(cur_c)::value;
+    constexpr bool HAS1 = decltype(has1_c)::value, HAS2 = decltype(has2_c)::value;
+    using Cur = std::integral_constant<int, CUR>;
+    using Nxt = std::integral_constant<int, CUR ^ 1>;
+    constexpr int NOFF = (CUR ^ 1) * w4::A_BYTES;
+    const int k2 = kt + 2;
+    static_for<0, 64>([&](auto m_c) {
+      constexpr int m = decltype(m_c)::value;
+      constexpr int slice = m / 16, x = m % 16, slot = slice & 1;
+      if constexpr (m == 48) {
+        NT_FENCE();
+        __syncthreads();
+        NT_FENCE();
+      }
+      mma1(slot, x);
+      NT_FENCE();
+      constexpr bool rd = slice < 2 ? (x % 2 == 0) : (x < 8);
+      if constexpr (rd) {
+        constexpr int f = slice < 2 ? x / 2 : x;
+        constexpr int which = f == 0 ? 0 : (f <= 4 ? f + 3 : f - 4);
+        if constexpr (slice < 3)
+          read_frag(Cur{}, slice + 1, slot ^ 1, which);
+        else if constexpr (HAS1)
+          read_frag(Nxt{}, 0, 0, which);
+      }
+      if constexpr (HAS1) {
+        if constexpr (m < 8) {
+          constexpr int d = m >> 1;
+          constexpr uint32_t sel = (m & 1) ? 0x07060302u : 0x05040100u;
+          tb[m] = u32x4{w4::perm(rb[1][d], rb[0][d], sel), w4::perm(rb[3][d], rb[2][d], sel),
+                        w4::perm(rb[5][d], rb[4][d], sel), w4::perm(rb[7][d], rb[6][d], sel)};
+        }
+        if constexpr (m <= 21 && m % 3 == 0) *(u32x4*)(lds + b_st[m / 3] + NOFF) = tb[m / 3];
+        if constexpr (HAS2 && m >= 8 && m <= 29 && (m - 8) % 3 == 0) {
+          constexpr int r = (m - 8) / 3;
+          rb[r] = __builtin_amdgcn_raw_buffer_load_b128(rsB, vb, (k2 * 64 + r) * b_rstep, 0);
+        }
+        if constexpr (m >= 22 && m <= 43 && (m - 22) % 3 == 0) {
+          constexpr int i = (m - 22) / 3;
+          *(u32x4*)(lds + a_st[i & 1] + (i >> 1) * 8192 + NOFF) = ra[i];
+          if constexpr (HAS2) ra[i] = __builtin_amdgcn_raw_buffer_load_b128(rsA, va, i * a_istep + k2 * 128, 0);
+        }
+      }
+      NT_FENCE();
+    });
+  };
+#undef NT_FENCE
+  using T1 = std::integral_constant<bool, true>;
+  using F1 = std::integral_constant<bool, false>;
+  // nk is even (the launcher checks): pairs of k-tiles, the last pair without prefetch.
+  int kt = 0;
+  for (; kt + 2 < nk; kt += 2) {
+    step(B0{}, T1{}, T1{}, kt);
+    step(B1{}, T1{}, T1{}, kt + 1);
+  }
+  step(B0{}, T1{}, F1{}, kt);
+  step(B1{}, F1{}, F1{}, kt + 1);
+
+  gemm_epilogue<4, 4>(g, acc, smem, wave, lane, m0 + wm * 128, n0 + wn * 128);
+}
+
 // ----------------------------------------------------------------------------- fp32
 constexpr int F32_TM = 32, F32_TN = 32, F32_KC = 256;
 constexpr int F32_AS = F32_KC + 4;  // a chunk row stride (floats): 16-byte aligned rows
@@ -445,7 +696,13 @@ static int gemm16_launch(GemmArgs g, hipStream_t stream) {
                     (uintptr_t)g.a % 16 == 0 && (uintptr_t)g.b % 16 == 0 && (g.sa_m * 2) % 16 == 0 &&
                     (g.sb_k * 2) % 16 == 0;
   const dim3 grid((unsigned)(tiles_m * tiles_n)), blk(G_THREADS);
-  if (fast)
+  // Four-wave kernel: buffer-load offsets are 32-bit and its k loop runs in pairs of
+  // tiles; otherwise the eight-wave kernel.
+  const bool w4_ok = (GB_M - 1) * g.sa_m + g.K <= 0x3fffffffLL && (g.K - 1) * g.sb_k + GB_N <= 0x3fffffffLL &&
+                     (g.K / GB_K) % 2 == 0;
+  if (fast && w4_ok)
+    hipLaunchKernelGGL((gemm_w4_kernel<T>), grid, dim3(256), 0, stream, g);
+  else if (fast)
     hipLaunchKernelGGL((gemm_fast8_kernel<T>), grid, dim3(512), 0, stream, g);
   else
     hipLaunchKernelGGL((gemm_mfma_kernel<T, false>), grid, blk, 0, stream, g);
