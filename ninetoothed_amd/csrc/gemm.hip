@@ -37,6 +37,8 @@ struct GemmArgs {
   float alpha, beta;
   int out_dtype, round_dtype;
   int tiles_m, tiles_n;
+  int c_pre;  // gemm_w4_kernel: 16-bit out (and c) with unit column stride, 16-byte aligned rows,
+              // c panel offsets within 32 bits: c is fetched during the last k-tile
 };
 
 // Map a linear workgroup id to an output tile so that consecutive ids on one XCD
@@ -385,6 +387,8 @@ __device__ __forceinline__ void static_for(F&& f) {
 namespace w4 {
 constexpr int A_BYTES = GB_M * GB_K * 2;  // 32 KiB
 constexpr int B_BASE = 2 * A_BYTES;       // 64 KiB
+constexpr int STAGE_BASE = 4 * A_BYTES;   // 128 KiB: epilogue staging, 8 KiB per wave
+constexpr int STAGE_BYTES = 32768;
 
 __device__ __forceinline__ uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel) {
   return __builtin_amdgcn_perm(s0, s1, sel);
@@ -403,11 +407,11 @@ __device__ __forceinline__ void transpose8x8_perm(const u32x4 (&in)[8], u32x4 (&
 
 template <typename T>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_w4_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (GB_M + GB_N) * GB_K];
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (GB_M + GB_N) * GB_K + w4::STAGE_BYTES / 2];
   char* lds = (char*)smem;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
   const int wm = wave >> 1, wn = wave & 1;  // 2 x 2
   int tm, tn;
   tile_of(blockIdx.x, g.tiles_m, g.tiles_n, tm, tn);
@@ -451,6 +455,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       a_rd[kk][h] = (ra_row * GB_K + swz(ra_row, chunk) * 8) * 2;
       b_rd[kk][h] = w4::B_BASE + (rb_row * GB_K + swz(rb_row, chunk) * 8) * 2;
     }
+
+  // c of this wave's 128 x 128 block, fetched straight into LDS (buffer_load ... lds: lane
+  // l of a load writes bytes 16 l .. 16 l + 15 past the load's LDS address).  Vector x
+  // (slab i = x / 8, t = x % 8) covers rows i * 32 + t * 4 + lane / 16, columns
+  // (lane % 16) * 8 .. + 7, so its 1 KiB lands row-major at c_lds(x) + lane * 16.
+  // Slabs 0, 1 go to LDS buffer 0, slabs 2, 3 to buffer 1, each wave in its own 16 KiB.
+  // Without c (or without the fast epilogue) the resource has no records and the loads
+  // write zeros without touching memory.
+  const int64_t row_base = m0 + wm * 128, col_base = n0 + wn * 128;
+  const bool c_fetch = g.c_pre && g.c;
+  const __amdgpu_buffer_rsrc_t rsC = __builtin_amdgcn_make_buffer_rsrc(
+      c_fetch ? (void*)((const uint16_t*)g.c + row_base * g.sc_m + col_base) : (void*)g.a, (short)0,
+      c_fetch ? (int)((127 * g.sc_m + 128) * 2) : 0, 0x00020000);
+  const int vc = c_fetch ? (int)(((lane >> 4) * g.sc_m + (lane & 15) * 8) * 2) : 0;
+  const int c_rstep = c_fetch ? (int)(g.sc_m * 2) : 0;
+  auto c_lds = [&](int x) { return (wave >> 1) * w4::B_BASE + (x >> 4) * w4::A_BYTES + (wave & 1) * 16384 + (x & 15) * 1024; };
+  auto load_c_lds = [&](int x) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsC, (__attribute__((address_space(3))) void*)(lds + c_lds(x)), 16, vc,
+                                             ((x >> 3) * 32 + (x & 7) * 4) * c_rstep, 0, 0);
+  };
 
   floatx16 acc[4][4];
   zero_acc(acc);
@@ -518,7 +542,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   //     row r of tile kt+2 fetched in slot 8 + 3r (after every column is transposed);
   //   a of tile kt+1: row block i stored in slot 22 + 3i (22..43), refetched for tile
   //     kt+2 in the same slot;
-  //   barrier before slot 48 (slice 3), whose reads come from the other buffer.
+  //   barrier before slot 48 (slice 3), whose reads come from the other buffer;
+  //   last k-tile only: the wave's c vectors 0..15 fetched into LDS buffer 0 in slots
+  //     0..15 and 16..31 into buffer 1 in slots 48..63, so the epilogue's HBM reads
+  //     overlap the last 64 MFMAs.
   // LDS writes are spread one per three MFMAs so four waves never fill the LDS data
   // queue, and every global load has at least a half k-tile before its use.
 #define NT_FENCE() __builtin_amdgcn_sched_barrier(0)
@@ -566,6 +593,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
           if constexpr (HAS2) ra[i] = __builtin_amdgcn_raw_buffer_load_b128(rsA, va, i * a_istep + k2 * 128, 0);
         }
       }
+      // Last k-tile: buffer 0 has been idle since the previous tile's barrier, buffer 1
+      // since this one's (no fragment reads follow it).
+      if constexpr (!HAS1 && m < 16) load_c_lds(m);
+      if constexpr (!HAS1 && m >= 48) load_c_lds(m - 32);
       NT_FENCE();
     });
   };
@@ -581,7 +612,81 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   step(B0{}, T1{}, F1{}, kt);
   step(B1{}, F1{}, F1{}, kt + 1);
 
-  gemm_epilogue<4, 4>(g, acc, smem, wave, lane, m0 + wm * 128, n0 + wn * 128);
+  if (!g.c_pre) {
+    gemm_epilogue<4, 4>(g, acc, smem, wave, lane, row_base, col_base);
+    return;
+  }
+  // Fast epilogue.  The accumulators go through the wave's 8 KiB of the staging area
+  // (which the main loop never touches, so no barrier) 16 rows at a time; the c vectors
+  // are read back from where the last k-tile's loads put them.  The only vector-memory
+  // operations outstanding here are those c loads.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  float* stage = (float*)(lds + w4::STAGE_BASE + wave * 8192);
+  uint16_t* O = (uint16_t*)g.out + row_base * g.so_m + col_base + (lane & 15) * 8;
+  const bool has_c = g.c != nullptr;
+  // Rows 16 h .. 16 h + 15 of slab i come from accumulator registers 8 h .. 8 h + 7.
+  auto stage_half = [&](int i, int h) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 8 * h; r < 8 * h + 8; ++r)
+        stage[(acc_row(r, lane) - 16 * h) * 128 + j * 32 + (lane & 31)] = acc[i][j][r];
+  };
+  // Each lane then finishes 4 vectors of 8 columns (rows t * 4 + lane / 16).
+  auto finish = [&](auto out_f16_c, auto round_c, int i, int h) {
+    constexpr bool OUT_F16 = decltype(out_f16_c)::value;
+    constexpr int ROUND = decltype(round_c)::value;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int rr = t * 4 + (lane >> 4), cg = (lane & 15) * 8;
+      const float4 v0 = *(const float4*)(stage + rr * 128 + cg);
+      const float4 v1 = *(const float4*)(stage + rr * 128 + cg + 4);
+      const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+      u32x4 cw = {0u, 0u, 0u, 0u};
+      if (has_c) cw = *(const u32x4*)(lds + c_lds(i * 8 + h * 4 + t) + lane * 16);
+      u32x4 ow;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        float r[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          float x = v[2 * d + e];
+          if constexpr (ROUND == NT_DTYPE_F16) x = f16_bits_to_float(float_to_f16_bits(x));
+          if constexpr (ROUND == NT_DTYPE_BF16) x = bf16_bits_to_float(float_to_bf16_bits(x));
+          r[e] = g.alpha * x;
+          if (has_c) {
+            const uint16_t cb = (uint16_t)(cw[d] >> (16 * e));
+            r[e] += g.beta * (OUT_F16 ? f16_bits_to_float(cb) : bf16_bits_to_float(cb));
+          }
+        }
+        ow[d] = OUT_F16 ? ((uint32_t)float_to_f16_bits(r[0]) | ((uint32_t)float_to_f16_bits(r[1]) << 16))
+                        : ((uint32_t)float_to_bf16_bits(r[0]) | ((uint32_t)float_to_bf16_bits(r[1]) << 16));
+      }
+      *(u32x4*)(O + (int64_t)(i * 32 + h * 16 + rr) * g.so_m) = ow;
+    }
+  };
+  using OutF16 = std::integral_constant<bool, true>;
+  using OutBF16 = std::integral_constant<bool, false>;
+  using RNone = std::integral_constant<int, NT_DTYPE_NONE>;
+  using RF16 = std::integral_constant<int, NT_DTYPE_F16>;
+  using RBF16 = std::integral_constant<int, NT_DTYPE_BF16>;
+  auto all = [&](auto out_f16_c, auto round_c) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        stage_half(i, h);
+        finish(out_f16_c, round_c, i, h);
+      }
+  };
+  const bool out_f16 = g.out_dtype == NT_DTYPE_F16;
+  if (g.round_dtype == NT_DTYPE_F16) {
+    if (out_f16) all(OutF16{}, RF16{}); else all(OutBF16{}, RF16{});
+  } else if (g.round_dtype == NT_DTYPE_BF16) {
+    if (out_f16) all(OutF16{}, RBF16{}); else all(OutBF16{}, RBF16{});
+  } else {
+    if (out_f16) all(OutF16{}, RNone{}); else all(OutBF16{}, RNone{});
+  }
 }
 
 // ----------------------------------------------------------------------------- fp32
@@ -700,6 +805,12 @@ static int gemm16_launch(GemmArgs g, hipStream_t stream) {
   // tiles; otherwise the eight-wave kernel.
   const bool w4_ok = (GB_M - 1) * g.sa_m + g.K <= 0x3fffffffLL && (g.K - 1) * g.sb_k + GB_N <= 0x3fffffffLL &&
                      (g.K / GB_K) % 2 == 0;
+  // Its fast epilogue: 16-byte out vectors, and c (if any) fetched with 32-bit buffer offsets.
+  const bool out_vec = g.out_dtype != NT_DTYPE_F32 && g.so_n == 1 && g.so_m >= 0 && g.so_m % 8 == 0 &&
+                       (uintptr_t)g.out % 16 == 0;
+  const bool c_vec = !g.c || (g.sc_n == 1 && g.sc_m >= 0 && g.sc_m % 8 == 0 && (uintptr_t)g.c % 16 == 0 &&
+                              127 * g.sc_m + 128 <= 0x3fffffffLL);
+  g.c_pre = fast && w4_ok && out_vec && c_vec;
   if (fast && w4_ok)
     hipLaunchKernelGGL((gemm_w4_kernel<T>), grid, dim3(256), 0, stream, g);
   else if (fast)

@@ -173,6 +173,28 @@ def test_addmm_epilogue():
     assert torch.allclose(out, torch.addmm(c, a, b, beta=beta, alpha=alpha), atol=0.075)
 
 
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+@pytest.mark.parametrize("round_dtype", (None, torch.float16, torch.bfloat16))
+@pytest.mark.parametrize("c_kind", ("dense", "strided", "broadcast", "none"))
+def test_addmm_fast_epilogue_variants(dtype, round_dtype, c_kind):
+    # M, N multiples of 256 and K / 64 even: the four-wave kernel, whose epilogue takes
+    # c through LDS; strided out rows and every kind of c row stride it accepts.
+    m, n, k = 512, 768, 256
+    a = _randn((m, k), dtype, 30)
+    b = _randn((k, n), dtype, 31)
+    c = None
+    if c_kind == "dense":
+        c = _randn((m, n), dtype, 32)
+    elif c_kind == "strided":
+        c = _randn((m, n + 64), dtype, 32)[:, :n]
+    elif c_kind == "broadcast":
+        c = _randn((1, n), dtype, 32).expand(m, n)
+    out = torch.empty((m, n + 128), dtype=dtype, device=DEV)[:, :n]
+    kernels.gemm(a, b, out, c=c, alpha=0.75, beta=-1.25, round_dtype=round_dtype)
+    ref = _gemm_ref(a, b, c, 0.75, -1.25, round_dtype)
+    assert torch.allclose(out.float(), ref.float(), atol=2e-2, rtol=1e-2)
+
+
 def test_addmm_headline_bf16():
     m = n = k = 4096
     g = 1.0 / math.sqrt(k)
