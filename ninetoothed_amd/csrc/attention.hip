@@ -324,6 +324,248 @@ __device__ __forceinline__ void attention_body(const AttnArgs& g) {
   }
 }
 
+// Fast path (unit d-stride, 16-byte aligned rows, D == DM, buffer offsets within 32
+// bits): the same math as attention_body with
+//   - K and V fetched through buffer resources whose range ends at the last key, so
+//     keys past Sk read as zeros with no per-load branch, at scalar per-tile offsets;
+//   - V transposed in 4 (key) x 8 (d) blocks with v_perm_b32, one block per lane;
+//   - two LDS stages, so one barrier per key tile: at the top of tile kt every wave has
+//     finished tile kt - 1 (whose stage now takes tile kt + 1) and stored tile kt;
+//   - lazy rescaling: the running max m used for p = exp2(s - m) is only raised when a
+//     tile's max exceeds it by more than RESCALE_LOG2 (then o, l are rescaled), so p
+//     stays below 2^RESCALE_LOG2 and most tiles skip the rescale; o / l is unchanged
+//     mathematically, and p keeps the input type's relative precision;
+//   - per-lane partial row sums, combined with the partner lane (lane ^ 32) once.
+namespace attn {
+constexpr int VT_STRIDE = TILE_K + 4;
+constexpr float RESCALE_LOG2 = 8.0f;
+template <int DM>
+struct Geo {
+  static constexpr int DH = DM / 64, DSUB = DM / 16, DBLK = DM / 32;
+  static constexpr int K_ELEMS = DH * AT_BN * TILE_K;  // K tile [d-half][key][64 d]
+  static constexpr int BUF = K_ELEMS + DM * VT_STRIDE;  // + V^T tile [d][64 keys + pad]
+  static constexpr int CPR = DM / 8;                    // 16-byte chunks per key row
+  static constexpr int K_LOADS = AT_BN * CPR / AT_THREADS;
+  static constexpr int KEYS_PER_LOAD = AT_THREADS / CPR;
+};
+__device__ __forceinline__ uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel) {
+  return __builtin_amdgcn_perm(s0, s1, sel);
+}
+}  // namespace attn
+
+template <typename T, int DM>
+__global__ __launch_bounds__(AT_THREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void attention_fast_kernel(
+    AttnArgs g) {
+  using G = attn::Geo<DM>;
+  typedef typename mfma_traits<T>::frag frag;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * G::BUF];
+  char* lds = (char*)smem;
+
+  const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  int qb;
+  int64_t bh;
+  block_order(g, blockIdx.x, qb, bh);
+  const int64_t b = bh / g.H, h = bh % g.H;
+  const int q0 = qb * AT_BM;
+  const int Sk = (int)g.Sk;
+  const uint16_t* Q = (const uint16_t*)g.q + b * g.qs[0] + h * g.qs[1];
+
+  // Q^T fragments of this lane's query, pre-scaled and rounded to the input type.
+  const int qpos = q0 + wave * 32 + (lane & 31);
+  frag qf[G::DSUB];
+#pragma unroll
+  for (int dd = 0; dd < G::DSUB; ++dd) {
+    u32x4 raw = {0u, 0u, 0u, 0u};
+    if (qpos < g.Sq) raw = *(const u32x4*)(Q + (int64_t)qpos * g.qs[2] + dd * 16 + half * 8);
+    uint16_t tmp[8];
+    const uint16_t* hv = (const uint16_t*)&raw;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) tmp[u] = elem<T>::from_float(elem<T>::to_float(hv[u]) * g.q_scale);
+    qf[dd] = __builtin_bit_cast(frag, *(const u32x4*)tmp);
+  }
+
+  // K: load i brings key i * KEYS_PER_LOAD + kr, chunk kc.  V: a 4 (key) x 8 (d) block,
+  // keys 4 kq .. 4 kq + 3, d 8 db .. 8 db + 7 (lanes with db >= DM / 8 idle when DM = 64).
+  const int ks2b = (int)g.ks[2] * 2, vs2b = (int)g.vs[2] * 2;
+  const __amdgpu_buffer_rsrc_t rsK = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const uint16_t*)g.k + b * g.ks[0] + h * g.ks[1]), (short)0, (Sk - 1) * ks2b + DM * 2, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsV = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const uint16_t*)g.v + b * g.vs[0] + h * g.vs[1]), (short)0, (Sk - 1) * vs2b + DM * 2, 0x00020000);
+  const int kr = tid / G::CPR, kc = tid % G::CPR;
+  const int vK = kr * ks2b + kc * 16;
+  int k_st[G::K_LOADS];
+#pragma unroll
+  for (int i = 0; i < G::K_LOADS; ++i) {
+    const int key = i * G::KEYS_PER_LOAD + kr;
+    k_st[i] = ((kc >> 3) * AT_BN * TILE_K + key * TILE_K + swz(key, kc & 7) * 8) * 2;
+  }
+  const int kq = tid & 15, db = tid >> 4;
+  const bool v_active = db < DM / 8;
+  const int vV = kq * 4 * vs2b + db * 16;
+  const int v_st = (G::K_ELEMS + db * 8 * attn::VT_STRIDE + kq * 4) * 2;
+
+  u32x4 rk[G::K_LOADS], rv[4];
+  auto load_tile = [&](int kt) {
+    const int k0 = kt * AT_BN;
+#pragma unroll
+    for (int i = 0; i < G::K_LOADS; ++i)
+      rk[i] = __builtin_amdgcn_raw_buffer_load_b128(rsK, vK, (k0 + i * G::KEYS_PER_LOAD) * ks2b, 0);
+    if (v_active) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) rv[r] = __builtin_amdgcn_raw_buffer_load_b128(rsV, vV, (k0 + r) * vs2b, 0);
+    }
+  };
+  auto store_tile = [&](int buf) {
+    char* base = lds + buf * (G::BUF * 2);
+#pragma unroll
+    for (int i = 0; i < G::K_LOADS; ++i) *(u32x4*)(base + k_st[i]) = rk[i];
+    if (v_active) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int d = j >> 1;
+        const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+        *(u32x2*)(base + v_st + j * attn::VT_STRIDE * 2) =
+            u32x2{attn::perm(rv[1][d], rv[0][d], sel), attn::perm(rv[3][d], rv[2][d], sel)};
+      }
+    }
+  };
+
+  floatx16 o_acc[G::DBLK];
+#pragma unroll
+  for (int i = 0; i < G::DBLK; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o_acc[i][r] = 0.f;
+  float m_i = -INFINITY, l_part = 0.5f;  // the two lanes of a query start l at 1 together
+
+  int nkt = (Sk + AT_BN - 1) / AT_BN;
+  if (g.causal) nkt = min(nkt, (q0 + AT_BM - 1) / AT_BN + 1);
+
+  if (nkt > 0) {
+    load_tile(0);
+    store_tile(0);
+    if (nkt > 1) load_tile(1);
+  }
+  for (int kt = 0; kt < nkt; ++kt) {
+    __syncthreads();
+    if (kt + 1 < nkt) {
+      store_tile((kt + 1) & 1);
+      if (kt + 2 < nkt) load_tile(kt + 2);
+    }
+    const int k0 = kt * AT_BN;
+    const uint16_t* sK = smem + (kt & 1) * G::BUF;
+    const uint16_t* sVt = sK + G::K_ELEMS;
+    // S^T = K . Q^T  (two 32-key blocks)
+    floatx16 s[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[kb][r] = 0.f;
+#pragma unroll
+      for (int dd = 0; dd < G::DSUB; ++dd) {
+        const int hf = dd >> 2;
+        const int chunk = (dd & 3) * 2 + half;
+        const int row = kb * 32 + (lane & 31);
+        const frag ka = *(const frag*)(sK + hf * AT_BN * TILE_K + row * TILE_K + swz(row, chunk) * 8);
+        s[kb] = mfma_traits<T>::mma(ka, qf[dd], s[kb]);
+      }
+    }
+    // Masks: keys past the end, and keys after the query when causal.
+    if (k0 + AT_BN > Sk || (g.causal && k0 + AT_BN - 1 > q0 + wave * 32)) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = k0 + kb * 32 + acc_row(r, lane);
+          if (key >= Sk || (g.causal && qpos < key)) s[kb][r] = -INFINITY;
+        }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const bool grow = mx > m_i + attn::RESCALE_LOG2;
+    if (__builtin_amdgcn_ballot_w64(grow)) {
+      const float m_new = grow ? mx : m_i;
+      const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
+      l_part *= alpha;
+#pragma unroll
+      for (int i = 0; i < G::DBLK; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o_acc[i][r] *= alpha;
+      m_i = m_new;
+    }
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = __builtin_amdgcn_exp2f(s[kb][r] - m_i);
+        s[kb][r] = p;
+        l_part += p;
+      }
+    // O^T += V^T . P^T over four 16-key slices.
+#pragma unroll
+    for (int t = 0; t < AT_BN / 16; ++t) {
+      uint16_t pt[8];
+#pragma unroll
+      for (int sl = 0; sl < 8; ++sl) pt[sl] = elem<T>::from_float(s[t >> 1][8 * (t & 1) + sl]);
+      const frag pf = __builtin_bit_cast(frag, *(const u32x4*)pt);
+#pragma unroll
+      for (int i = 0; i < G::DBLK; ++i) {
+        const int d = i * 32 + (lane & 31);
+        const uint16_t* rowp = sVt + d * attn::VT_STRIDE;
+        const u32x2 lo = *(const u32x2*)(rowp + (2 * t) * 8 + half * 4);
+        const u32x2 hi = *(const u32x2*)(rowp + (2 * t + 1) * 8 + half * 4);
+        const frag vf = __builtin_bit_cast(frag, u32x4{lo[0], lo[1], hi[0], hi[1]});
+        o_acc[i] = mfma_traits<T>::mma(vf, pf, o_acc[i]);
+      }
+    }
+  }
+  __syncthreads();  // the output staging below reuses the K/V stages
+
+  // o = acc / l, staged through LDS per 64-wide slice of d so that each lane then
+  // writes 4 consecutive d of one query row (lanes 0-15 cover 64 d of a row).
+  const float l_i = l_part + __shfl_xor(l_part, 32, 64);
+  const float inv = 1.0f / l_i;
+  constexpr int ST = 65;
+  float* stage = reinterpret_cast<float*>(smem) + wave * (32 * ST);
+#pragma unroll
+  for (int ps = 0; ps < DM / 64; ++ps) {
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) stage[(lane & 31) * ST + jb * 32 + acc_row(r, lane)] = o_acc[ps * 2 + jb][r] * inv;
+    __syncthreads();
+#pragma unroll
+    for (int e0 = 0; e0 < 32 * 16; e0 += 64) {
+      const int e = e0 + lane;
+      const int row = e >> 4, grp = (e & 15) * 4;
+      const int qp = q0 + wave * 32 + row;
+      if (qp < g.Sq) {
+        const float* sp = stage + row * ST + grp;
+        const int64_t ob = b * g.os[0] + h * g.os[1] + (int64_t)qp * g.os[2];
+        const int d0 = ps * 64 + grp;
+        if (g.o_dtype != NT_DTYPE_F32 && g.os[3] == 1 && ((ob + d0) & 3) == 0) {
+          const uint32_t w0 = (uint32_t)elem<T>::from_float(sp[0]) | ((uint32_t)elem<T>::from_float(sp[1]) << 16);
+          const uint32_t w1 = (uint32_t)elem<T>::from_float(sp[2]) | ((uint32_t)elem<T>::from_float(sp[3]) << 16);
+          if (g.o_dtype == elem<T>::code) {
+            *(u32x2*)((uint16_t*)g.o + ob + d0) = u32x2{w0, w1};
+          } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) store_from_float(g.o, ob + d0 + u, g.o_dtype, sp[u]);
+          }
+        } else {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) store_from_float(g.o, ob + (d0 + u) * g.os[3], g.o_dtype, sp[u]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
 // Vector-load variant: two waves per SIMD (two workgroups per CU) so that one
 // workgroup's softmax and LDS traffic overlap the other's matrix work.
 template <typename T, int DM>
@@ -369,13 +611,23 @@ static int attention_launch(const void* q, const int64_t* qs, const void* k, con
            (uintptr_t)k % 16 == 0 && (uintptr_t)v % 16 == 0 && qs[3] == 1 && (qs[2] * 2) % 16 == 0 &&
            (qs[1] * 2) % 16 == 0 && (qs[0] * 2) % 16 == 0 && (uintptr_t)q % 16 == 0;
   };
+  // The fast kernel addresses a head's keys with 32-bit buffer offsets (up to 64 keys past
+  // the end) and positions with 32-bit integers.
+  auto fast_ok = [&](int64_t dm) {
+    return kvec_ok(dm) && (Sk + 2 * AT_BN) * ks[2] * 2 < 0x7fffffffLL && (Sk + 2 * AT_BN) * vs[2] * 2 < 0x7fffffffLL &&
+           Sq + AT_BM < 0x7fffffffLL && Sk > 0;
+  };
   if (D <= 64) {
-    if (kvec_ok(64))
+    if (fast_ok(64))
+      hipLaunchKernelGGL((attention_fast_kernel<T, 64>), grid, blk, 0, stream, g);
+    else if (kvec_ok(64))
       hipLaunchKernelGGL((attention_kernel<T, 64>), grid, blk, 0, stream, g);
     else
       hipLaunchKernelGGL((attention_generic_kernel<T, 64>), grid, blk, 0, stream, g);
   } else {
-    if (kvec_ok(128))
+    if (fast_ok(128))
+      hipLaunchKernelGGL((attention_fast_kernel<T, 128>), grid, blk, 0, stream, g);
+    else if (kvec_ok(128))
       hipLaunchKernelGGL((attention_kernel<T, 128>), grid, blk, 0, stream, g);
     else
       hipLaunchKernelGGL((attention_generic_kernel<T, 128>), grid, blk, 0, stream, g);

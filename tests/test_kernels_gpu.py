@@ -308,6 +308,39 @@ def test_attention_d128_scaled(causal, dtype):
     assert torch.allclose(o.float(), _sdpa_ref(q, k, v, causal, scale), atol=tol, rtol=tol)
 
 
+def _attention_ref64(q, k, v, causal, q_scale):
+    # The kernel's arithmetic in float64: q * q_scale rounded to the input type,
+    # s = q . k in base 2, softmax by exp2, p rounded to the input type before p . v.
+    qr = (q.float() * q_scale).to(q.dtype).double()
+    s = qr @ k.double().transpose(-1, -2)
+    if causal:
+        sq, sk = s.shape[-2:]
+        s = s.masked_fill(torch.ones(sq, sk, dtype=torch.bool, device=s.device).triu(1), -math.inf)
+    p = torch.exp2(s - s.amax(-1, keepdim=True))
+    l = p.sum(-1, keepdim=True)
+    return (p.to(q.dtype).double() @ v.double()) / l
+
+
+@pytest.mark.parametrize("d", (64, 128))
+@pytest.mark.parametrize("causal", (False, True))
+@pytest.mark.parametrize("sq, sk", ((700, 700), (300, 700), (129, 65)))
+def test_attention_growing_scores(d, causal, sq, sk):
+    # Scores rise along the keys by ~20 (log2 units) per 64-key tile and spread widely
+    # within a tile, so the running max is raised on nearly every tile and exp2(s - m)
+    # spans the whole range; ragged Sq, Sk exercise the key-range and causal masks.
+    dtype = torch.float16
+    u = _randn((d,), torch.float32, 60) / math.sqrt(d)
+    q = (_randn((1, 2, sq, d), torch.float32, 61) + 2.0 * u).to(dtype)
+    ramp = torch.arange(sk, device=DEV, dtype=torch.float32)[:, None] * (0.11 / math.sqrt(d)) * u * d
+    k = (_randn((1, 2, sk, d), torch.float32, 62) + ramp).to(dtype)
+    v = _randn((1, 2, sk, d), dtype, 63)
+    o = torch.empty_like(q)
+    qs = kernels.LOG2E / math.sqrt(d)
+    kernels.attention(q, k, v, o, causal=causal, q_scale=qs)
+    ref = _attention_ref64(q, k, v, causal, qs)
+    assert torch.allclose(o.double(), ref, atol=1e-2, rtol=1e-2)
+
+
 def test_attention_headline_causal():
     q, k, v = (_randn((4, 32, 4096, 128), torch.float16, 50 + i) for i in range(3))
     o = torch.empty_like(q)
