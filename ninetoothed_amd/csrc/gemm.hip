@@ -376,13 +376,6 @@ __global__ __launch_bounds__(512) void gemm_fast8_kernel(GemmArgs g) {
 // transposes (v_perm_b32).  Each k-tile is a fixed issue schedule of 64 MFMA slots
 // (below): fragments read a slice ahead, tile kt+1 stored into the other buffer and
 // tile kt+2 fetched at an even rate, barrier before the last slice.
-template <int B, int E, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  if constexpr (B < E) {
-    f(std::integral_constant<int, B>{});
-    static_for<B + 1, E>(f);
-  }
-}
 
 namespace w4 {
 constexpr int A_BYTES = GB_M * GB_K * 2;  // 32 KiB

@@ -11,6 +11,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "nt_mi355x.h"
 
 namespace nt {
@@ -101,6 +103,16 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 __host__ __device__ __forceinline__ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Compile-time loop: f(std::integral_constant<int, i>) for i in [B, E), so that every
+// register index inside f is a constant (used for fixed instruction schedules).
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
 
 inline bool valid_dtype(int d) { return d == NT_DTYPE_F32 || d == NT_DTYPE_F16 || d == NT_DTYPE_BF16; }
 inline bool valid_round(int d) { return d == NT_DTYPE_NONE || d == NT_DTYPE_F16 || d == NT_DTYPE_BF16; }
