@@ -213,6 +213,66 @@ __global__ __launch_bounds__(256) void filter_krsc_kernel(const uint16_t* __rest
   }
 }
 
+// One launch for both re-layouts.  Workgroups [0, N * Hp): padded input row (n, hp) of
+// xp; pad rows and pad columns are written as zeros; interior 8 (channel) x 8 (w) blocks
+// go one per lane: eight 16-byte loads along w (one per channel), an 8 x 8 transpose of
+// 16-bit values with v_perm_b32, eight 16-byte stores along c (one per position).  Needs
+// unit w stride, 16-byte aligned input rows and W % 8 == 0.  Workgroups past N * Hp:
+// the filter, element by element into K-R-S-C.
+template <typename T>
+__global__ __launch_bounds__(256) void conv_relayout_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ xp,
+                                                            const uint16_t* __restrict__ w, uint16_t* __restrict__ wt,
+                                                            ConvArgs g, int64_t Hp, int64_t Wp) {
+  const int64_t rows = g.N * Hp;
+  const int tid = threadIdx.x;
+  if ((int64_t)blockIdx.x >= rows) {
+    const int64_t total = g.K * g.KG;
+    const int64_t stride = ((int64_t)gridDim.x - rows) * 256;
+    for (int64_t e = ((int64_t)blockIdx.x - rows) * 256 + tid; e < total; e += stride) {
+      const int64_t c = e % g.C;
+      int64_t t = e / g.C;
+      const int64_t s = t % g.S;
+      t /= g.S;
+      const int64_t r = t % g.R, k = t / g.R;
+      wt[e] = w[k * g.ws[0] + c * g.ws[1] + r * g.ws[2] + s * g.ws[3]];
+    }
+    return;
+  }
+  const int64_t hp = (int64_t)blockIdx.x % Hp, n = (int64_t)blockIdx.x / Hp;
+  const int64_t h = hp - g.ph;
+  const int64_t C = g.C, W = g.W;
+  uint16_t* out_row = xp + ((n * Hp + hp) * Wp) * C;
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+  const int64_t cchunks = C / 8;
+  if (h < 0 || h >= g.H) {
+    for (int64_t e = tid; e < Wp * cchunks; e += 256) *(u32x4*)(out_row + e * 8) = zero;
+    return;
+  }
+  // pad columns
+  for (int64_t e = tid; e < (Wp - W) * cchunks; e += 256) {
+    const int64_t col = e / cchunks, ch = e % cchunks;
+    const int64_t wp = col < g.pw ? col : col + W;
+    *(u32x4*)(out_row + wp * C + ch * 8) = zero;
+  }
+  const uint16_t* xb = x + n * g.xs[0] + h * g.xs[2];
+  const int64_t wblocks = W / 8;
+  for (int64_t e = tid; e < cchunks * wblocks; e += 256) {
+    const int64_t cb = e / wblocks, wb = e % wblocks;  // lanes along w first: loads of one channel row coalesce
+    u32x4 in[8], out[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) in[i] = *(const u32x4*)(xb + (cb * 8 + i) * g.xs[1] + wb * 8);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int d = j >> 1;
+      const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+      out[j] = u32x4{__builtin_amdgcn_perm(in[1][d], in[0][d], sel), __builtin_amdgcn_perm(in[3][d], in[2][d], sel),
+                     __builtin_amdgcn_perm(in[5][d], in[4][d], sel), __builtin_amdgcn_perm(in[7][d], in[6][d], sel)};
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) *(u32x4*)(out_row + (g.pw + wb * 8 + j) * C + cb * 8) = out[j];
+  }
+}
+
 // Implicit GEMM over the re-laid operands: out^T[k][m] = sum_kk wt[k][kk] * xcol[m][kk].
 // 512 lanes, waves 4 (k) x 2 (m), 256 x 256 tile, two 64 KiB LDS buffers, tile kt+2
 // fetched while kt is multiplied (as the GEMM fast path).
@@ -355,6 +415,242 @@ __global__ __launch_bounds__(512) void conv_nhwc_kernel(const uint16_t* __restri
   }
 }
 
+// Four-wave form of conv_nhwc_kernel (the GEMM's gemm_w4_kernel schedule): 256 lanes, one
+// wave per SIMD in a 2 (k) x 2 (m) grid, each owning 128 x 128 of the 256 x 256 tile
+// with its accumulators in the accumulator file.  Both operands are k-contiguous rows
+// (filter rows of the K-R-S-C filter, im2col rows of the padded N-H-W-C input), so both
+// load with 16-byte buffer loads and store to LDS unchanged: a row i * 32 + (lane / 8)
+// per load i, chunk lane % 8.  The im2col rows of a lane have per-lane base offsets; the
+// (r, s, c0) of a k-tile is one scalar offset (a k-tile never crosses an (r, s) block,
+// C % 64 == 0), and rows past M take an offset past the end of the resource so their
+// loads return zeros.  Fixed 64-slot issue schedule per k-tile as in gemm_w4_kernel:
+// fragments read a slice ahead; b (im2col) rows stored in slots 0..21 and a (filter)
+// rows in 22..43, each refetched for tile kt + 2 in the slot it was stored; barrier
+// before slot 48.  Epilogue: 16-row halves of each wave's accumulators staged in a
+// spare 32 KiB of LDS (no barrier), then each lane stores 8 consecutive output
+// positions of one channel (its positions are fixed, so (n, p, q) is computed once).
+namespace cw4 {
+constexpr int A_BYTES = CB_K * TILE_K * 2;  // 32 KiB
+constexpr int B_BASE = 2 * A_BYTES;         // 64 KiB
+constexpr int STAGE_BASE = 4 * A_BYTES;     // 128 KiB
+}  // namespace cw4
+
+template <typename T>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void conv_w4_kernel(
+    const uint16_t* __restrict__ xp, const uint16_t* __restrict__ wt, ConvArgs g, int64_t Hp, int64_t Wp) {
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (CB_K + CB_M) * TILE_K + 16384];
+  char* lds = (char*)smem;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wk = wave >> 1, wm = wave & 1;
+  const int tk = blockIdx.x % g.tiles_k, tmi = blockIdx.x / g.tiles_k;
+  const int k0t = tk * CB_K, m0t = tmi * CB_M;
+  const int KG = (int)g.KG, C = (int)g.C;
+  const int nk = KG / TILE_K;
+
+  const int row_in = tid >> 3, chunk = tid & 7;
+  // Filter: rows k0t + row_in + 32 i; rows past K lie past the resource's end (zeros).
+  const __amdgpu_buffer_rsrc_t rsW = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(wt + (int64_t)k0t * KG), (short)0, (int)((g.K - k0t) * KG * 2), 0x00020000);
+  const int vw = (row_in * KG + chunk * 8) * 2;
+  const int w_istep = 32 * KG * 2;
+  // im2col rows m0t + row_in + 32 i.
+  const int x_bytes = (int)(g.N * Hp * Wp * g.C * 2);
+  const __amdgpu_buffer_rsrc_t rsX = __builtin_amdgcn_make_buffer_rsrc((void*)xp, (short)0, x_bytes, 0x00020000);
+  int vx[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int m = m0t + row_in + 32 * i;
+    if (m < g.M) {
+      const int q = m % (int)g.Q, t = m / (int)g.Q;
+      const int p = t % (int)g.P, n = t / (int)g.P;
+      vx[i] = (((n * (int)Hp + p * (int)g.sh) * (int)Wp + q * (int)g.sw) * C + chunk * 8) * 2;
+    } else {
+      vx[i] = x_bytes;
+    }
+  }
+  // Scalar byte offset of k-tile kt inside an im2col row: (r, s) block and channel c0.
+  auto x_off = [&](int kt) {
+    const int kk0 = kt * TILE_K;
+    const int rs = kk0 / C, c0 = kk0 - rs * C;
+    const int r = rs / (int)g.S, s = rs - r * (int)g.S;
+    return ((r * (int)g.dh * (int)Wp + s * (int)g.dw) * C + c0) * 2;
+  };
+
+  int st[2], a_rd[4][2], b_rd[4][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int row = i * 32 + row_in;
+    st[i] = (row * TILE_K + swz(row, chunk) * 8) * 2;
+  }
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int ch = kk * 2 + (lane >> 5);
+      const int ra = wk * 128 + h * 32 + (lane & 31);
+      const int rb = wm * 128 + h * 32 + (lane & 31);
+      a_rd[kk][h] = (ra * TILE_K + swz(ra, ch) * 8) * 2;
+      b_rd[kk][h] = cw4::B_BASE + (rb * TILE_K + swz(rb, ch) * 8) * 2;
+    }
+
+  floatx16 acc[4][4];
+  zero_acc(acc);
+  u32x4 ra[8], rb[8];
+  auto load_a = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ra[i] = __builtin_amdgcn_raw_buffer_load_b128(rsW, vw, i * w_istep + kt * 128, 0);
+  };
+  auto load_b = [&](int kt) {
+    const int xo = x_off(kt);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) rb[i] = __builtin_amdgcn_raw_buffer_load_b128(rsX, vx[i], xo, 0);
+  };
+  auto store_ab = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      *(u32x4*)(lds + buf * cw4::A_BYTES + st[i & 1] + (i >> 1) * 8192) = ra[i];
+      *(u32x4*)(lds + cw4::B_BASE + buf * cw4::A_BYTES + st[i & 1] + (i >> 1) * 8192) = rb[i];
+    }
+  };
+
+  typedef typename mfma_traits<T>::frag frag;
+  frag fa[2][4], fb[2][4];
+  auto read_frag = [&](auto buf_c, int kk, int slot, int x) {
+    constexpr int OFF = decltype(buf_c)::value * cw4::A_BYTES;
+    if (x < 4)
+      fa[slot][x] = *(const frag*)(lds + a_rd[kk][x & 1] + (x >> 1) * 8192 + OFF);
+    else
+      fb[slot][x - 4] = *(const frag*)(lds + b_rd[kk][x & 1] + ((x - 4) >> 1) * 8192 + OFF);
+  };
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+
+  load_a(0);
+  load_b(0);
+  store_ab(0);
+  if (nk > 1) {
+    load_a(1);
+    load_b(1);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int x = 0; x < 8; ++x) read_frag(B0{}, 0, 0, x);
+
+#define NT_CFENCE() __builtin_amdgcn_sched_barrier(0)
+  auto step = [&](auto cur_c, auto has1_c, auto has2_c, int kt) {
+    constexpr int CUR = decltype(cur_c)::value;
+    constexpr bool HAS1 = decltype(has1_c)::value, HAS2 = decltype(has2_c)::value;
+    using Cur = std::integral_constant<int, CUR>;
+    using Nxt = std::integral_constant<int, CUR ^ 1>;
+    constexpr int NOFF = (CUR ^ 1) * cw4::A_BYTES;
+    const int k2 = kt + 2;
+    const int xo2 = HAS2 ? x_off(k2) : 0;
+    static_for<0, 64>([&](auto m_c) {
+      constexpr int m = decltype(m_c)::value;
+      constexpr int slice = m / 16, x = m % 16, slot = slice & 1;
+      if constexpr (m == 48) {
+        NT_CFENCE();
+        __syncthreads();
+        NT_CFENCE();
+      }
+      {
+        constexpr int i = x >> 2, j = x & 3;
+        acc[i][j] = mfma_traits<T>::mma(fa[slot][i], fb[slot][j], acc[i][j]);
+      }
+      NT_CFENCE();
+      constexpr bool rd = slice < 2 ? (x % 2 == 0) : (x < 8);
+      if constexpr (rd) {
+        constexpr int f = slice < 2 ? x / 2 : x;
+        constexpr int which = f == 0 ? 0 : (f <= 4 ? f + 3 : f - 4);
+        if constexpr (slice < 3)
+          read_frag(Cur{}, slice + 1, slot ^ 1, which);
+        else if constexpr (HAS1)
+          read_frag(Nxt{}, 0, 0, which);
+      }
+      if constexpr (HAS1) {
+        if constexpr (m <= 21 && m % 3 == 0) {
+          constexpr int i = m / 3;
+          *(u32x4*)(lds + cw4::B_BASE + NOFF + st[i & 1] + (i >> 1) * 8192) = rb[i];
+          if constexpr (HAS2) rb[i] = __builtin_amdgcn_raw_buffer_load_b128(rsX, vx[i], xo2, 0);
+        }
+        if constexpr (m >= 22 && m <= 43 && (m - 22) % 3 == 0) {
+          constexpr int i = (m - 22) / 3;
+          *(u32x4*)(lds + NOFF + st[i & 1] + (i >> 1) * 8192) = ra[i];
+          if constexpr (HAS2) ra[i] = __builtin_amdgcn_raw_buffer_load_b128(rsW, vw, i * w_istep + k2 * 128, 0);
+        }
+      }
+      NT_CFENCE();
+    });
+  };
+#undef NT_CFENCE
+  using T1 = std::integral_constant<bool, true>;
+  using F1 = std::integral_constant<bool, false>;
+  // nk is even (the launcher checks): pairs of k-tiles, the last pair without prefetch.
+  int kt = 0;
+  for (; kt + 2 < nk; kt += 2) {
+    step(B0{}, T1{}, T1{}, kt);
+    step(B1{}, T1{}, T1{}, kt + 1);
+  }
+  step(B0{}, T1{}, F1{}, kt);
+  step(B1{}, F1{}, F1{}, kt + 1);
+
+  // Epilogue: this lane's 8 output positions and their (n, p, q).
+  float* stage = (float*)(lds + cw4::STAGE_BASE + wave * 8192);
+  const int cg = (lane & 15) * 8;
+  const int mpos = m0t + wm * 128 + cg;
+  const bool m_ok = mpos < g.M;  // Q % 8 == 0: all 8 positions share one output row
+  int64_t ybase = 0;
+  if (m_ok) {
+    const int q = mpos % (int)g.Q, t = mpos / (int)g.Q;
+    const int p = t % (int)g.P, n = t / (int)g.P;
+    ybase = n * g.ys[0] + p * g.ys[2] + q;
+  }
+  uint16_t* Y = (uint16_t*)g.y;
+  auto finish = [&](auto round_c) {
+    constexpr int ROUND = decltype(round_c)::value;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int r = 8 * h; r < 8 * h + 8; ++r)
+            stage[(acc_row(r, lane) - 16 * h) * 128 + j * 32 + (lane & 31)] = acc[i][j][r];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int rr = t * 4 + (lane >> 4);
+          const int k = k0t + wk * 128 + i * 32 + h * 16 + rr;
+          const float4 v0 = *(const float4*)(stage + rr * 128 + cg);
+          const float4 v1 = *(const float4*)(stage + rr * 128 + cg + 4);
+          const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+          u32x4 ow;
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            float a = v[2 * d], b = v[2 * d + 1];
+            if constexpr (ROUND == NT_DTYPE_F16) {
+              a = f16_bits_to_float(float_to_f16_bits(a));
+              b = f16_bits_to_float(float_to_f16_bits(b));
+            }
+            if constexpr (ROUND == NT_DTYPE_BF16) {
+              a = bf16_bits_to_float(float_to_bf16_bits(a));
+              b = bf16_bits_to_float(float_to_bf16_bits(b));
+            }
+            ow[d] = (uint32_t)elem<T>::from_float(a) | ((uint32_t)elem<T>::from_float(b) << 16);
+          }
+          if (m_ok && k < g.K) *(u32x4*)(Y + ybase + (int64_t)k * g.ys[1]) = ow;
+        }
+      }
+  };
+  if (g.round_dtype == NT_DTYPE_F16)
+    finish(std::integral_constant<int, NT_DTYPE_F16>{});
+  else if (g.round_dtype == NT_DTYPE_BF16)
+    finish(std::integral_constant<int, NT_DTYPE_BF16>{});
+  else
+    finish(std::integral_constant<int, NT_DTYPE_NONE>{});
+}
+
 static int64_t nhwc_bytes(int64_t N, int64_t C, int64_t H, int64_t W, int64_t K, int64_t R, int64_t S, int64_t ph,
                           int64_t pw) {
   const int64_t xp = N * (H + 2 * ph) * (W + 2 * pw) * C * 2;
@@ -397,15 +693,34 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
     const int64_t Hp = H + 2 * ph, Wp = W + 2 * pw;
     uint16_t* xp = (uint16_t*)workspace;
     uint16_t* wt = (uint16_t*)((char*)workspace + ((N * Hp * Wp * C * 2 + 255) / 256) * 256);
-    const int64_t relayout_blocks = N * Hp * (C / 64);
-    if (relayout_blocks > 0x7fffffffLL) return NT_ERR_INVALID;
-    hipLaunchKernelGGL(nchw_to_nhwc_pad_kernel<T>, dim3((unsigned)relayout_blocks), dim3(256), 0, stream,
-                       (const uint16_t*)x, xp, g, Hp, Wp);
     int64_t fblocks = cdiv(K * g.KG, 256);
     if (fblocks > 4096) fblocks = 4096;
-    hipLaunchKernelGGL(filter_krsc_kernel<T>, dim3((unsigned)fblocks), dim3(256), 0, stream, (const uint16_t*)w, wt, g);
-    hipLaunchKernelGGL(conv_nhwc_kernel<T>, dim3((unsigned)(tiles_k * tiles_m)), dim3(512), 0, stream,
-                       (const uint16_t*)xp, (const uint16_t*)wt, g, Hp, Wp);
+    const bool fast_relayout = xs[3] == 1 && W % 8 == 0 && (uintptr_t)x % 16 == 0 && (xs[0] * 2) % 16 == 0 &&
+                               (xs[1] * 2) % 16 == 0 && (xs[2] * 2) % 16 == 0;
+    if (fast_relayout) {
+      if (N * Hp + fblocks > 0x7fffffffLL) return NT_ERR_INVALID;
+      hipLaunchKernelGGL(conv_relayout_kernel<T>, dim3((unsigned)(N * Hp + fblocks)), dim3(256), 0, stream,
+                         (const uint16_t*)x, xp, (const uint16_t*)w, wt, g, Hp, Wp);
+    } else {
+      const int64_t relayout_blocks = N * Hp * (C / 64);
+      if (relayout_blocks > 0x7fffffffLL) return NT_ERR_INVALID;
+      hipLaunchKernelGGL(nchw_to_nhwc_pad_kernel<T>, dim3((unsigned)relayout_blocks), dim3(256), 0, stream,
+                         (const uint16_t*)x, xp, g, Hp, Wp);
+      hipLaunchKernelGGL(filter_krsc_kernel<T>, dim3((unsigned)fblocks), dim3(256), 0, stream, (const uint16_t*)w, wt,
+                         g);
+    }
+    // Four-wave kernel: even number of k-tiles, 32-bit operand offsets, output written as
+    // 16-byte runs of 8 positions of one channel (Q % 8 == 0, y of the input type with
+    // unit q stride and 16-byte aligned rows).
+    const bool w4 = (g.KG / TILE_K) % 2 == 0 && N * Hp * Wp * C * 2 < 0x7fffffffLL &&
+                    K * g.KG * 2 < 0x7fffffffLL && g.M < 0x7fffffffLL && y_dtype == elem<T>::code && Q % 8 == 0 &&
+                    ys[3] == 1 && ys[0] % 8 == 0 && ys[1] % 8 == 0 && ys[2] % 8 == 0 && (uintptr_t)y % 16 == 0;
+    if (w4)
+      hipLaunchKernelGGL(conv_w4_kernel<T>, dim3((unsigned)(tiles_k * tiles_m)), dim3(256), 0, stream,
+                         (const uint16_t*)xp, (const uint16_t*)wt, g, Hp, Wp);
+    else
+      hipLaunchKernelGGL(conv_nhwc_kernel<T>, dim3((unsigned)(tiles_k * tiles_m)), dim3(512), 0, stream,
+                         (const uint16_t*)xp, (const uint16_t*)wt, g, Hp, Wp);
     return launch_status();
   }
   const bool dense_w = ws[3] == 1 && ws[2] == S && ws[1] == R * S && g.KG % TILE_K == 0 && (ws[0] * 2) % 16 == 0 &&
