@@ -177,6 +177,25 @@ int nt_attention_f32(const void* q, const int64_t* q_strides, const void* k, con
                      int o_dtype, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
                      float q_scale, int causal, hipStream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * Generic kernels for programs that match none of the families above.  They replace
+ * the reference's run-time toolchain step for generated sources (nvcc + cuModule in
+ * src/ninetoothed/backends/materializers/cuda.py:96-170, Triton's compile for the
+ * default backend): ninetoothed_amd.generic emits HIP source, these entry points
+ * compile it for gfx950 with hipRTC, load it and launch it.
+ *   nt_rtc_compile: source -> code object (malloc'd; free with nt_rtc_free); on failure
+ *                   NT_ERR_INVALID and the compiler log in `log`.  Needs no GPU.
+ *   nt_rtc_load:    code object -> kernel handle; the module stays loaded for the
+ *                   process.
+ *   nt_rtc_launch:  1-D launch (grid x block threads) with hipModuleLaunchKernel's
+ *                   kernel_params (one pointer per argument value) on `stream`.
+ * ------------------------------------------------------------------------- */
+int nt_rtc_compile(const char* source, const char* name, void** code, int64_t* size, char* log,
+                   int64_t log_cap);
+void nt_rtc_free(void* code);
+int nt_rtc_load(const void* code, const char* kernel_name, void** function);
+int nt_rtc_launch(void* function, uint32_t grid, uint32_t block, void** kernel_params, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -77,7 +77,7 @@ def build(verbose: bool = False, extra_flags: tuple[str, ...] = (), jobs: int | 
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
         objects = list(pool.map(lambda s: _compile(s, tuple(extra_flags)), srcs))
     tmp = LIBRARY_PATH.with_suffix(".so.tmp")
-    cmd = [hipcc(), f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
+    cmd = [hipcc(), f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC", *map(str, objects), "-lhiprtc", "-o", str(tmp)]
     result = subprocess.run(cmd, capture_output=True, text=True)
     if result.returncode != 0:
         raise RuntimeError(f"link failed:\n{result.stderr}")

@@ -58,8 +58,12 @@ _SIGNATURES = {
         f"nt_attention_{t}": (_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _I64, _I64, _I64, _I64, _I64, _F, _I, _P)
         for t in ("f32", "f16", "bf16")
     },
+    "nt_rtc_compile": (ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_P), _I64P, ctypes.c_char_p, _I64),
+    "nt_rtc_free": (_P,),
+    "nt_rtc_load": (_P, ctypes.c_char_p, ctypes.POINTER(_P)),
+    "nt_rtc_launch": (_P, ctypes.c_uint32, ctypes.c_uint32, ctypes.POINTER(_P), _P),
 }
-_RESTYPES = {"nt_conv2d_workspace_size": ctypes.c_int64}
+_RESTYPES = {"nt_conv2d_workspace_size": ctypes.c_int64, "nt_rtc_free": None}
 
 _lock = threading.Lock()
 _library = None

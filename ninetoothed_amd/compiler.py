@@ -205,9 +205,9 @@ def compile_kernel(request):
     if request.arrangement is None:
         arrangement, tensors = _arrangement_from_annotations(application)
     else:
+        # `tensors` are the arrangement's arguments: besides one Tensor per application
+        # parameter they may carry other values the arrangement reads (e.g. slices).
         arrangement, tensors = request.arrangement, tuple(request.tensors)
-    if len(tensors) != len(params):
-        raise TypeError(f"{len(tensors)} tensors given for an application with {len(params)} parameters")
     copies = copy.deepcopy(tensors)
     arranged = arrangement(*copies)
     if not isinstance(arranged, tuple):

@@ -921,6 +921,11 @@ def match_add(ctx):
     if b is None:
         return None
     an, bn = b["a"], b["b"]
+    import torch
+
+    dts = {ctx.dtypes.get(n) for n in (an, bn, out)}
+    if len(dts) != 1 or dts.pop() not in (torch.float32, torch.float16, torch.bfloat16):
+        return None  # mixed or other dtypes: the generic kernels promote as the reference does
     va, vb, vo = ctx.view(an), ctx.view(bn), ctx.view(out)
     _require(va.level_shapes == vo.level_shapes == vb.level_shapes, family, "operands are arranged differently")
     _require(va.source_shape == vb.source_shape == vo.source_shape, family, "operand shapes differ")
@@ -938,18 +943,35 @@ def match_add(ctx):
     return AddPlan(an, bn, out)
 
 
-FAMILIES = (match_attention, match_gemm, match_softmax, match_max_pool2d, match_add)
+def match_generic(ctx):
+    from ninetoothed_amd import generic
+
+    return generic.match_generic(ctx)
+
+
+FAMILIES = (match_attention, match_gemm, match_softmax, match_max_pool2d, match_add, match_generic)
 
 
 def select(ctx):
-    """Return the Plan of the first family whose pattern and geometry fit."""
-    tried = []
+    """Return the Plan of the first family whose pattern and geometry fit.
+
+    A family whose pattern matches but whose geometry does not raises ``LoweringError``;
+    the next families are still tried (an elementwise program the add kernel cannot
+    take runs on the generic kernels) and the reasons are reported if none fits."""
+    tried, reasons = [], []
     for matcher in FAMILIES:
-        plan = matcher(ctx)
+        name = matcher.__name__[len("match_"):]
+        try:
+            plan = matcher(ctx)
+        except LoweringError as exc:
+            reasons.append(f"{name}: {exc}")
+            plan = None
         if plan is not None:
             return plan
-        tried.append(matcher.__name__[len("match_"):])
+        tried.append(name)
+    detail = "; ".join(reasons)
     raise LoweringError(
         "the application matches none of the MI355X kernel families "
         f"({', '.join(tried)}); see ninetoothed_amd.families for the supported programs"
+        + (f" ({detail})" if detail else "")
     )

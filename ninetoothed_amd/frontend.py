@@ -131,6 +131,7 @@ class _Alias:
 
 
 _NTL_BY_ID = {id(getattr(ntl, name)): name for name in ntl._FUNCTIONS}
+_NTL_BY_ID.update({id(getattr(ntl.libdevice, name)): f"libdevice.{name}" for name in ntl.libdevice.FUNCTIONS})
 _DTYPE_NAMES = {"float16", "bfloat16", "float32", "float64", "int8", "int16", "int32", "int64", "uint8"}
 
 _BINOPS = {ast.Add: "add", ast.Sub: "sub", ast.Mult: "mul", ast.Div: "div", ast.FloorDiv: "floordiv", ast.Mod: "mod"}
@@ -540,6 +541,10 @@ class Lowerer:
             return b.make("math", name, self.data(args[0]))
         if name == "cast":
             return b.make("cast", self.data(args[0]), self.dtype_value(args[1] if len(args) > 1 else kwargs["dtype"]))
+        if name.startswith("libdevice."):
+            if kwargs:
+                raise LoweringError(f"{name} takes positional arguments only")
+            return b.make("libm", name[len("libdevice."):], tuple(self.data(a) for a in args))
         raise LoweringError(f"ntl.{name} is not supported by the MI355X backend")
 
     def _inline(self, frame, func, call):

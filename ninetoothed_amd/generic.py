@@ -1,0 +1,515 @@
+"""Generic kernels: element-parallel programs that match no hand-written family.
+
+The reference emits source for any arrangement and application through its backends
+(``src/ninetoothed/emitters/ssa.py``, ``emitters/cuda.py:245-381``) and compiles it at
+run time (``backends/materializers/cuda.py:96-170``).  This module does the same for the
+programs whose work is element by element: every tensor is used at its tile level
+(``load(x)`` of the whole arranged view), the body is arithmetic, comparisons,
+``where``, ``maximum``/``minimum``, casts, ``ntl`` math functions and
+``libdevice`` functions on those values and on 0-d scalar parameters, and the results
+are stored to arranged outputs.  Such a program computes each element independently,
+so the kernel walks the flattened index space of the arranged hierarchy (program grid
+and tile levels together) with one lane per element:
+
+  * index maps: for every tensor, the source offset of every element of that space is
+    evaluated on the host by the same evaluator the families use
+    (``tensor.BoundView.probe``), with the call's strides; masked elements get -1.
+    The tables (int32) are built once per bound launcher (shapes, strides, constexprs).
+  * the body: the application's value graph is emitted as HIP C++ with the reference's
+    typing rules (``src/ninetoothed/frontend/types.py``: ``_promote_dtype``, division
+    promotes to at least float32, math functions keep their operand's type, Python
+    literals are weakly typed); every value is computed in fp32 (fp64 for float64) and
+    rounded to its type after each operation, so fp16/bf16 intermediates round where
+    the reference's program rounds them.  Masked loads read the source's ``other`` (or
+    0); masked outputs are not written.
+  * the source is compiled for gfx950 once per distinct text with hipRTC and launched
+    through ``nt_rtc_*`` of libnt_mi355x.so.
+
+Anything else (reductions, broadcasting subscripts, loops, ``dot``, index arithmetic with
+``offsets``) raises ``LoweringError``.  An arrangement that maps several elements to one
+output element writes it from several lanes (the last write is unspecified), as the
+reference's generated programs would.
+"""
+
+import ctypes
+import hashlib
+import threading
+
+import numpy as np
+
+from ninetoothed_amd import _lib
+from ninetoothed_amd.errors import KernelLaunchError, LoweringError
+from ninetoothed_amd.frontend import Value
+
+MAX_ELEMENTS = 1 << 26  # host-side index tables: at most 64 Mi elements per launch
+
+_ALLOWED = {"load", "const", "param", "add", "sub", "mul", "div", "floordiv", "mod", "neg", "lt", "le", "gt", "ge",
+            "eq", "ne", "where", "maximum", "minimum", "math", "libm", "cast", "dtype", "dtype_of", "zeros",
+            "full"}
+
+_FLOAT = ("float16", "bfloat16", "float32", "float64")
+_INT = ("int8", "int16", "int32", "int64", "uint8")
+_RANK = {"bool": 0, "int8": 1, "uint8": 1, "int16": 2, "int32": 3, "int64": 4, "float16": 6, "bfloat16": 6,
+         "float32": 7, "float64": 8}
+
+# storage C type, working C type, load expression, store expression (of `v`)
+_STORAGE = {
+    "float16": ("unsigned short", "float", "ld_f16({})", "st_f16({})"),
+    "bfloat16": ("unsigned short", "float", "ld_bf16({})", "st_bf16({})"),
+    "float32": ("float", "float", "{}", "{}"),
+    "float64": ("double", "double", "{}", "{}"),
+    "int8": ("signed char", "long long", "(long long){}", "(signed char){}"),
+    "uint8": ("unsigned char", "long long", "(long long){}", "(unsigned char){}"),
+    "int16": ("short", "long long", "(long long){}", "(short){}"),
+    "int32": ("int", "long long", "(long long){}", "(int){}"),
+    "int64": ("long long", "long long", "{}", "{}"),
+    "bool": ("bool", "bool", "{}", "{}"),
+}
+
+_PRELUDE = r"""
+__device__ __forceinline__ float ld_f16(unsigned short b) { return (float)__builtin_bit_cast(_Float16, b); }
+__device__ __forceinline__ unsigned short st_f16(float x) { return __builtin_bit_cast(unsigned short, (_Float16)x); }
+__device__ __forceinline__ float r_f16(float x) { return (float)(_Float16)x; }
+__device__ __forceinline__ float r_bf16(float x) {
+  unsigned u = __builtin_bit_cast(unsigned, x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return __builtin_bit_cast(float, (u | 0x00400000u) & 0xffff0000u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return __builtin_bit_cast(float, u & 0xffff0000u);
+}
+__device__ __forceinline__ float ld_bf16(unsigned short b) { return __builtin_bit_cast(float, (unsigned)b << 16); }
+__device__ __forceinline__ unsigned short st_bf16(float x) { return (unsigned short)(__builtin_bit_cast(unsigned, r_bf16(x)) >> 16); }
+"""
+
+# ntl math functions (unary) and libdevice functions: C names for float / double
+_MATH = {
+    "exp": ("expf", "exp"), "exp2": ("exp2f", "exp2"), "log": ("logf", "log"), "log2": ("log2f", "log2"),
+    "sqrt": ("sqrtf", "sqrt"), "rsqrt": ("rsqrtf", "rsqrt"), "abs": ("fabsf", "fabs"), "expm1": ("expm1f", "expm1"),
+    "log10": ("log10f", "log10"), "log1p": ("log1pf", "log1p"), "sin": ("sinf", "sin"), "cos": ("cosf", "cos"),
+    "tan": ("tanf", "tan"), "tanh": ("tanhf", "tanh"), "sinh": ("sinhf", "sinh"), "cosh": ("coshf", "cosh"),
+    "asin": ("asinf", "asin"), "acos": ("acosf", "acos"), "atan": ("atanf", "atan"), "erf": ("erff", "erf"),
+    "floor": ("floorf", "floor"), "ceil": ("ceilf", "ceil"), "trunc": ("truncf", "trunc"),
+    "round": ("roundf", "round"), "fabs": ("fabsf", "fabs"), "pow": ("powf", "pow"), "atan2": ("atan2f", "atan2"),
+    "fmax": ("fmaxf", "fmax"), "fmin": ("fminf", "fmin"), "fmod": ("fmodf", "fmod"), "hypot": ("hypotf", "hypot"),
+}
+
+
+def _torch_dtype_name(dtype):
+    name = str(dtype).replace("torch.", "")
+    if name == "bool":
+        return "bool"
+    if name not in _RANK:
+        raise LoweringError(f"the generic kernels do not support tensors of dtype {dtype}")
+    return name
+
+
+def _promote(a, b):
+    if a == "weak":
+        return b if b != "weak" else "weak"
+    if b == "weak":
+        return a
+    if a == b:
+        return a
+    if {a, b} == {"float16", "bfloat16"}:
+        return "float32"
+    return a if _RANK[a] >= _RANK[b] else b
+
+
+def _walk(values):
+    """Values reachable from ``values`` (dependencies first)."""
+    order, seen = [], set()
+
+    def visit(v):
+        if not isinstance(v, Value) or id(v) in seen:
+            return
+        seen.add(id(v))
+        for a in v.args:
+            if isinstance(a, tuple):
+                for x in a:
+                    visit(x)
+            else:
+                visit(a)
+        order.append(v)
+
+    for v in values:
+        visit(v)
+    return order
+
+
+class _Emitter:
+    """Typed HIP C++ for the value graph of an element-parallel program."""
+
+    def __init__(self, ctx):
+        self.ctx = ctx
+        self.types = {}  # id(value) -> dtype name, "weak" or "bool"
+        self.names = {}  # id(value) -> C expression / variable
+        self.lines = []
+        self.tensors = []  # loaded tensor params, in argument order
+        self.scalars = []  # 0-d scalar params, in argument order
+
+    def tensor_dtype(self, name):
+        return _torch_dtype_name(self.ctx.dtypes[name])
+
+    def scalar_type(self, name):
+        """0-d run-time parameters: Python ints are int64, everything else float32."""
+        value = self.ctx.values[name]
+        return "int64" if isinstance(value, int) and not isinstance(value, bool) else "float32"
+
+    def dtype_name(self, d):
+        if d.op == "dtype":
+            return d.args[0]
+        view = d.args[0]
+        while view.op == "index":
+            view = view.args[0]
+        return self.tensor_dtype(view.args[0])
+
+    @staticmethod
+    def ctx_const(value):
+        return Value("const", (float(value),))
+
+    def type_of(self, v):
+        if not isinstance(v, Value):
+            return "weak"
+        return self.types[id(v)]
+
+    def work(self, t):
+        return _STORAGE["float32" if t == "weak" else t][1]
+
+    def round_to(self, t, expr):
+        if t == "float16":
+            return f"r_f16({expr})"
+        if t == "bfloat16":
+            return f"r_bf16({expr})"
+        return expr
+
+    def operand(self, v, t):
+        """Operand ``v`` as a value of working type for an operation in type ``t``."""
+        if v.op == "const":
+            c = v.args[0]
+            if isinstance(c, bool):
+                return "true" if c else "false"
+            w = self.work(t)
+            if w == "long long":
+                return f"((long long){int(c)})"
+            if w == "bool":
+                return "true" if c else "false"
+            lit = repr(float(c))
+            if lit in ("inf", "-inf", "nan"):
+                lit = {"inf": "__builtin_huge_valf()", "-inf": "(-__builtin_huge_valf())", "nan": "__builtin_nanf(\"\")"}[lit]
+                if w == "double":
+                    lit = f"((double){lit})"
+            elif w == "float":
+                lit += "f"
+            return self.round_to(t, f"(({w}){lit})")  # weakly typed literal: rounded to the operation's type
+        expr = self.names[id(v)]
+        src = self.types[id(v)]
+        w = self.work(t)
+        if self.work(src) != w:
+            expr = f"(({w}){expr})"
+        return expr
+
+    def define(self, v, t, expr, exact=False):
+        name = f"v{len(self.names)}"
+        self.lines.append(f"    const {self.work(t)} {name} = {expr if exact else self.round_to(t, expr)};")
+        self.names[id(v)] = name
+        self.types[id(v)] = t
+
+    def emit(self, v):
+        op, args = v.op, v.args
+        if op == "const":
+            self.types[id(v)] = "bool" if isinstance(args[0], bool) else "weak"
+            return
+        if op in ("dtype", "dtype_of", "param"):
+            return
+        if op in ("zeros", "full"):
+            t = self.dtype_name(args[-1])
+            fill = 0.0 if op == "zeros" else args[1]
+            self.define(v, t, self.operand(self.ctx_const(fill), t))
+            return
+        if op == "load":
+            view = args[0]
+            if view.op != "param":
+                raise LoweringError("the generic kernels load whole arranged tensors only (no level indexing)")
+            name = view.args[0]
+            info = self.ctx.params[name]
+            if info.source_ndim == 0:
+                if name not in self.scalars:
+                    self.scalars.append(name)
+                self.names[id(v)] = f"s_{name}"
+                self.types[id(v)] = self.scalar_type(name)
+                return
+            if name not in self.tensors:
+                self.tensors.append(name)
+            t = self.tensor_dtype(name)
+            st, w, ld, _ = _STORAGE[t]
+            other = self.ctx.views[name].source.other
+            other = 0.0 if other is None else float(other)
+            o = repr(other) if other == other and abs(other) != float("inf") else (
+                "__builtin_nanf(\"\")" if other != other else ("__builtin_huge_valf()" if other > 0 else "(-__builtin_huge_valf())"))
+            # an element of the tensor, or `other`, is already a value of type t
+            self.define(v, t, f"(i_{name} >= 0 ? ({w}){ld.format(f'p_{name}[i_{name}]')} : ({w}){o})", exact=True)
+            return
+        if op in ("add", "sub", "mul", "div", "floordiv", "mod", "maximum", "minimum"):
+            a, b = args
+            t = _promote(self.type_of(a), self.type_of(b))
+            if t == "weak":
+                t = "float32"
+            if op == "div" and t not in ("float32", "float64"):
+                t = "float32"
+            if t == "bool":
+                raise LoweringError(f"`{op}` on booleans is not supported")
+            x, y = self.operand(a, t), self.operand(b, t)
+            w = self.work(t)
+            if op == "maximum":
+                expr = f"fmax({x}, {y})" if w == "double" else (f"fmaxf({x}, {y})" if w == "float" else f"({x} > {y} ? {x} : {y})")
+            elif op == "minimum":
+                expr = f"fmin({x}, {y})" if w == "double" else (f"fminf({x}, {y})" if w == "float" else f"({x} < {y} ? {x} : {y})")
+            elif op == "floordiv":
+                expr = f"floor({x} / {y})" if w != "long long" else f"({x} / {y})"
+            elif op == "mod":
+                expr = f"fmod({x}, {y})" if w != "long long" else f"({x} % {y})"
+            else:
+                expr = f"({x} {dict(add='+', sub='-', mul='*', div='/')[op]} {y})"
+            self.define(v, t, expr)
+            return
+        if op == "neg":
+            t = self.type_of(args[0])
+            t = "float32" if t == "weak" else t
+            self.define(v, t, f"(-{self.operand(args[0], t)})")
+            return
+        if op in ("lt", "le", "gt", "ge", "eq", "ne"):
+            a, b = args
+            t = _promote(self.type_of(a), self.type_of(b))
+            t = "float32" if t == "weak" else t
+            sym = dict(lt="<", le="<=", gt=">", ge=">=", eq="==", ne="!=")[op]
+            self.define(v, "bool", f"({self.operand(a, t)} {sym} {self.operand(b, t)})")
+            return
+        if op == "where":
+            c, a, b = args
+            t = _promote(self.type_of(a), self.type_of(b))
+            t = "float32" if t == "weak" else t
+            self.define(v, t, f"({self.operand(c, 'bool')} ? {self.operand(a, t)} : {self.operand(b, t)})")
+            return
+        if op == "cast":
+            x, d = args
+            t = self.dtype_name(d)
+            src = self.type_of(x)
+            src = "float32" if src == "weak" else src
+            e = self.operand(x, src)
+            self.define(v, t, f"(({self.work(t)}){e})")
+            return
+        if op in ("math", "libm"):
+            fname = args[0]
+            operands = (args[1],) if op == "math" else args[1]
+            if op == "math" and fname == "sigmoid":
+                t = self.type_of(operands[0])
+                t = "float32" if t in ("weak", "bool") or t not in _FLOAT else t
+                x = self.operand(operands[0], t)
+                one = "1.0" if self.work(t) == "double" else "1.0f"
+                ex = "exp" if self.work(t) == "double" else "expf"
+                self.define(v, t, f"({one} / ({one} + {ex}(-{x})))")
+                return
+            if fname not in _MATH:
+                raise LoweringError(f"math function `{fname}` is not supported by the generic kernels")
+            t = "weak"
+            for o in operands:
+                t = _promote(t, self.type_of(o))
+            if t in ("weak", "bool") or t not in _FLOAT:
+                t = "float32"
+            cf = _MATH[fname][1 if self.work(t) == "double" else 0]
+            self.define(v, t, f"{cf}({', '.join(self.operand(o, t) for o in operands)})")
+            return
+        raise LoweringError(f"operation `{op}` is not supported by the generic kernels")
+
+
+def _analyse(ctx):
+    """(stores, ordered values, output names, loaded names) or None if the program is not element-parallel."""
+    program = ctx.program
+    if program.loops:
+        return None
+    stores = program.stores
+    values = _walk(list(stores.values()))
+    for v in values:
+        if v.op not in _ALLOWED:
+            return None
+        if v.op == "load" and v.args[0].op != "param":
+            return None
+    tensors = [n for n in list(stores) + [v.args[0].args[0] for v in values if v.op == "load"]
+               if ctx.params[n].source_ndim != 0]
+    shapes = {tuple(ctx.views[n].level_shapes) for n in tensors}
+    if len(shapes) > 1:
+        return None
+    for n in stores:
+        if ctx.params[n].source_ndim == 0:
+            return None
+    return stores, values
+
+
+class GenericPlan:
+    """A bound generic kernel (see the module docstring)."""
+
+    family = "generic"
+    _lock = threading.Lock()
+    _functions = {}  # source digest -> loaded kernel handle
+
+    def __init__(self, ctx, stores, values):
+        self.ctx = ctx
+        self.stores = stores
+        em = _Emitter(ctx)
+        for v in values:
+            em.emit(v)
+        self.loaded = list(em.tensors)
+        self.scalars = list(em.scalars)
+        self.outputs = list(stores)
+        lines = []
+        for out, v in stores.items():
+            t = _torch_dtype_name(ctx.dtypes[out])
+            src = em.type_of(v)
+            src = "float32" if src == "weak" else src
+            val = em.operand(v, src) if v.op == "const" else em.names[id(v)]
+            if em.work(src) != em.work(t):
+                val = f"(({em.work(t)}){val})"
+            lines.append(f"    if (o_{out} >= 0) p_{out}[o_{out}] = {_STORAGE[t][3].format(val)};")
+        self.body = em.lines
+        self.store_lines = lines
+        self.index_names = list(dict.fromkeys(self.outputs + self.loaded))
+        params = []
+        for n in self.index_names:
+            params.append(f"const int* __restrict__ t_{n}")
+        for n in self.loaded:
+            if n not in self.outputs:
+                params.append(f"const {_STORAGE[_torch_dtype_name(ctx.dtypes[n])][0]}* __restrict__ p_{n}")
+        for n in self.outputs:
+            params.append(f"{_STORAGE[_torch_dtype_name(ctx.dtypes[n])][0]}* p_{n}")
+        self.scalar_types = {n: em.scalar_type(n) for n in self.scalars}
+        for n in self.scalars:
+            params.append(f"{_STORAGE[self.scalar_types[n]][0]} s_{n}")
+        params.append("long long total")
+        self.params = params
+        self.kernel_name = "nt_generic"
+
+    def source(self, linear=None):
+        """Kernel source; ``linear[name] = n`` marks a tensor whose index table is e for e < n, -1 after."""
+        linear = linear or {}
+
+        def index(n):
+            return f"(e < {linear[n]}LL ? (int)e : -1)" if n in linear else f"t_{n}[e]"
+
+        head = [f"    const int i_{n} = {index(n)};" for n in self.loaded]
+        head += [f"    const int o_{n} = {index(n)};" for n in self.outputs]
+        return (
+            _PRELUDE
+            + f'\nextern "C" __global__ void __launch_bounds__(256) {self.kernel_name}({", ".join(self.params)}) {{\n'
+            + "  for (long long e = (long long)blockIdx.x * 256 + threadIdx.x; e < total;"
+            + " e += (long long)gridDim.x * 256) {\n"
+            + "\n".join(head + self.body + self.store_lines)
+            + "\n  }\n}\n"
+        )
+
+    def describe(self):
+        return {"family": self.family, "outputs": self.outputs, "inputs": self.loaded, "scalars": self.scalars}
+
+    # ------------------------------------------------------------ compile, tables, launch
+    @classmethod
+    def compile(cls, source):
+        """Code object for ``source`` (hipRTC, gfx950); raises LoweringError with the log."""
+        lib = _lib.load()
+        code, size = ctypes.c_void_p(), ctypes.c_int64()
+        log = ctypes.create_string_buffer(16384)
+        status = lib.nt_rtc_compile(source.encode(), b"nt_generic.hip", ctypes.byref(code), ctypes.byref(size), log,
+                                    len(log))
+        if status != 0:
+            raise LoweringError(f"hipRTC could not compile the generic kernel:\n{log.value.decode(errors='replace')}")
+        try:
+            return ctypes.string_at(code, size.value)
+        finally:
+            lib.nt_rtc_free(code)
+
+    def function(self, source):
+        digest = hashlib.sha256(source.encode()).hexdigest()
+        with self._lock:
+            fn = self._functions.get(digest)
+            if fn is None:
+                blob = self.compile(source)
+                handle = ctypes.c_void_p()
+                buf = ctypes.create_string_buffer(blob, len(blob))
+                status = _lib.load().nt_rtc_load(buf, self.kernel_name.encode(), ctypes.byref(handle))
+                if status != 0:
+                    raise KernelLaunchError(status)
+                fn = handle
+                self._functions[digest] = fn
+        return fn
+
+    def _table(self, name, tensor):
+        view = self.ctx.views[name]
+        shape = tuple(s for level in view.level_shapes for s in level)
+        total = int(np.prod(shape)) if shape else 1
+        if total > MAX_ELEMENTS:
+            raise LoweringError(f"the generic kernels index at most {MAX_ELEMENTS} elements per launch ({total} here)")
+        idx, mask = view.probe(view.full_index())
+        off = np.zeros((), dtype=np.int64)
+        for i, st in zip(idx, tensor.stride()):
+            off = off + np.asarray(i, dtype=np.int64) * int(st)
+        off = np.broadcast_to(np.where(mask, off, -1), shape).reshape(-1)
+        if off.size and off.max() >= 2**31:
+            raise LoweringError("the generic kernels address at most 2^31 elements of a tensor")
+        return off.astype(np.int32), total
+
+    def bind(self, values, index):
+        import torch
+
+        if not self.index_names:  # nothing is stored: the program has no effect
+            return lambda args: None
+        device = None
+        tables, linear, total = {}, {}, None
+        for n in self.index_names:
+            t = values[n]
+            device = t.device
+            tab, tot = self._table(n, t)
+            if total is not None and tot != total:
+                raise LoweringError("generic kernel operands do not share one index space")
+            total = tot
+            valid = int(np.count_nonzero(tab >= 0))
+            if np.array_equal(tab[:valid], np.arange(valid, dtype=np.int32)) and not np.any(tab[valid:] >= 0):
+                linear[n] = valid  # e -> e, masked from `valid` on: no table
+            else:
+                tables[n] = torch.from_numpy(tab).to(device)
+        fn = self.function(self.source(linear))
+        ptrs = {n: ctypes.c_void_p() for n in self.index_names}
+        argv = [ctypes.c_void_p(tables[n].data_ptr() if n in tables else None) for n in self.index_names]
+        argv += [ptrs[n] for n in self.loaded if n not in self.outputs]
+        argv += [ptrs[n] for n in self.outputs]
+        svals = {n: ctypes.c_int64() if self.scalar_types[n] == "int64" else ctypes.c_float() for n in self.scalars}
+        argv += [svals[n] for n in self.scalars]
+        argv.append(ctypes.c_int64(total))
+        params = (ctypes.c_void_p * len(argv))(*[ctypes.addressof(a) for a in argv])
+        grid = max(1, min((total + 255) // 256, 256 * 64)) if total else 0
+        lib = _lib.load()
+        positions = {n: index[n] for n in self.index_names}
+        spos = {n: index[n] for n in self.scalars}
+
+        def launch(args):
+            for n, p in positions.items():
+                ptrs[n].value = args[p].data_ptr()
+            for n, p in spos.items():
+                v = args[p]
+                v = v.item() if hasattr(v, "item") else v
+                svals[n].value = int(v) if self.scalar_types[n] == "int64" else float(v)
+            status = lib.nt_rtc_launch(fn, grid, 256, params, ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream))
+            if status != 0:
+                raise KernelLaunchError(status)
+
+        launch.keep = (tables, argv, params)  # device tables and the argument block live with the launcher
+        return launch
+
+    def run(self, values):
+        names = tuple(values)
+        self.bind(values, {n: i for i, n in enumerate(names)})(tuple(values[n] for n in names))
+
+
+def match_generic(ctx):
+    """The generic element-parallel kernel, or None when the program is not element-parallel."""
+    found = _analyse(ctx)
+    if found is None:
+        return None
+    stores, values = found
+    return GenericPlan(ctx, stores, values)

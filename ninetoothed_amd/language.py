@@ -33,4 +33,25 @@ _FUNCTIONS = (
 for _name in _FUNCTIONS:
     globals()[_name] = _parsed_only(_name)
 
-__all__ = list(_FUNCTIONS) + ["float16", "bfloat16", "float32", "float64", "int8", "int16", "int32", "int64", "uint8"]
+
+
+class _LibDevice:
+    """``ntl.libdevice``: device math functions by name (``libdevice.pow(x, y)``), as in
+    the reference's ``ninetoothed.language.libdevice``.  Run by the generic kernels with
+    the device math library of the HIP toolchain."""
+
+    FUNCTIONS = ("pow", "exp", "exp2", "expm1", "log", "log2", "log10", "log1p", "sqrt", "rsqrt", "sin", "cos",
+                 "tan", "tanh", "sinh", "cosh", "asin", "acos", "atan", "atan2", "erf", "floor", "ceil", "trunc",
+                 "round", "fabs", "fmax", "fmin", "fmod", "hypot")
+
+    def __init__(self):
+        for name in self.FUNCTIONS:
+            fn = _parsed_only(f"libdevice.{name}")
+            fn._ntl_name = f"libdevice.{name}"
+            setattr(self, name, fn)
+
+
+libdevice = _LibDevice()
+
+__all__ = list(_FUNCTIONS) + ["float16", "bfloat16", "float32", "float64", "int8", "int16", "int32", "int64", "uint8",
+                              "libdevice"]

@@ -93,9 +93,19 @@ def test_add_matches():
 
 
 # ---------------------------------------------------------------- rejections
-def test_unsupported_math_is_rejected():
+def test_elementwise_program_outside_the_families_is_generic():
     def app(lhs, rhs, output):
         output = ntl.sqrt(lhs) + rhs  # noqa: F841
+
+    bs = Symbol("BS", meta=True)
+    h = ninetoothed.make(lambda a, b, c: (a.tile((bs,)), b.tile((bs,)), c.tile((bs,))), app,
+                         (Tensor(1), Tensor(1), Tensor(1)))
+    assert _specialize(h, torch.empty(10), torch.empty(10), torch.empty(10))["family"] == "generic"
+
+
+def test_unsupported_reduction_is_rejected():
+    def app(lhs, rhs, output):
+        output = ntl.sum(lhs, 0) + rhs  # noqa: F841
 
     bs = Symbol("BS", meta=True)
     h = ninetoothed.make(lambda a, b, c: (a.tile((bs,)), b.tile((bs,)), c.tile((bs,))), app,
@@ -232,7 +242,7 @@ def test_artifact_metadata_contract():
 # ------------------------------------------------------------------ library
 def test_library_exports_every_declared_entry_point():
     header = (Path(__file__).resolve().parents[1] / "include" / "nt_mi355x.h").read_text()
-    declared = set(re.findall(r"^(?:int|int64_t)\s+(nt_\w+)\(", header, re.M))
+    declared = set(re.findall(r"^(?:int|int64_t|void)\s+(nt_\w+)\(", header, re.M))
     assert declared == set(_lib.exported_symbols())
     lib = _lib.load()  # loads without a GPU; no compute call
     for name in declared:

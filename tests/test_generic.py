@@ -1,0 +1,309 @@
+"""The generic element-parallel kernels (programs outside the hand-written families).
+
+CPU: the reference's typing rules in the emitted source, the per-tensor index tables
+(against numpy slicing / transposition of the same tensor), hipRTC compilation of the
+emitted source for gfx950.  GPU: the reference's own elementwise tests (clone
+application 0, ``libdevice.pow``, constant pad, expand of an empty tensor: reference
+tests/test_clone.py, test_pow.py, test_pad.py, test_expand.py) and fp16/bf16 chains,
+scalars, casts, in-place updates and transposed arrangements against torch.
+"""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import ninetoothed_amd as ninetoothed
+import ninetoothed_amd.language as ntl
+from ninetoothed_amd import Symbol, Tensor, block_size
+from ninetoothed_amd.generic import GenericPlan
+
+BS = Symbol("BS", meta=True)
+
+
+def _plan(handle, *args, **meta):
+    names = handle._abi["public_args"]
+    return handle._kernel.specialize(dict(zip(names, args)), meta)
+
+
+def _tiled1(app, n):
+    return ninetoothed.make(lambda *ts: tuple(t.tile((BS,)) for t in ts), app, tuple(Tensor(1) for _ in range(n)))
+
+
+# ------------------------------------------------------------------ applications
+def app_chain(x, y, output):
+    output = ntl.maximum(x * 2 + y, 0.0) - ntl.exp(-x) / (1 + y * y)  # noqa: F841
+
+
+def app_mixed(x, y, output):
+    output = x + y  # noqa: F841
+
+
+def app_div(x, y, output):
+    output = x / y  # noqa: F841
+
+
+def app_where(x, y, output):
+    output = ntl.where(x > y, x, y * 0.5)  # noqa: F841
+
+
+def app_scalars(x, alpha, beta, output):
+    output = x * alpha + beta  # noqa: F841
+
+
+def app_cast(x, output):
+    output = (x > 0).to(ntl.float16) * ntl.sigmoid(x)  # noqa: F841
+
+
+def app_inplace(x):
+    x = x * x + 1  # noqa: F841
+
+
+def app_int(x, y, output):
+    output = x * 3 - y  # noqa: F841
+
+
+def app_pow(input, exponent, output):
+    output = ntl.libdevice.pow(input, exponent)  # noqa: F841
+
+
+def app_copy(input, output):
+    output = input  # noqa: F841
+
+
+# ------------------------------------------------------------------ CPU: typing and source
+def test_typing_follows_the_reference_rules():
+    h = _tiled1(app_chain, 3)
+    src = _plan(h, *(torch.empty(8, dtype=torch.float16) for _ in range(3))).source()
+    # fp16 operations round after every step; the weakly typed literals stay fp16
+    assert "r_f16((v" in src and "float v" in src and "double" not in src.split("nt_generic(")[1]
+    mixed = _plan(_tiled1(app_mixed, 3), torch.empty(8, dtype=torch.float16), torch.empty(8, dtype=torch.bfloat16),
+                  torch.empty(8, dtype=torch.float32)).source()
+    body = mixed.split("nt_generic(")[1]
+    assert "r_f16((v" not in body and "r_bf16((v" not in body  # fp16 + bf16 -> fp32
+    div = _plan(_tiled1(app_div, 3), *(torch.empty(8, dtype=torch.float16) for _ in range(2)),
+                torch.empty(8, dtype=torch.float16)).source()
+    assert "r_f16((v0 / v1))" not in div and "(v0 / v1)" in div  # division promotes to fp32
+    ints = _plan(_tiled1(app_int, 3), *(torch.empty(8, dtype=torch.int32) for _ in range(3))).source()
+    assert "long long v" in ints
+
+
+def test_scalar_parameters_are_typed_by_their_python_type():
+    h = ninetoothed.make(lambda x, a, b, o: (x.tile((BS,)), a, b, o.tile((BS,))), app_scalars,
+                         (Tensor(1), Tensor(0), Tensor(0), Tensor(1)))
+    x = torch.empty(8)
+    src = _plan(h, x, 0.5, 3, x).source()
+    assert "float s_alpha" in src and "long long s_beta" in src
+
+
+def test_index_tables_match_numpy_views():
+    # a transposed, tiled source against numpy's transpose of the same offsets
+    def arrange(src, dst):
+        return src.permute((1, 0)).tile((16, 32)), dst.tile((16, 32))
+
+    h = ninetoothed.make(arrange, app_copy, (Tensor(2), Tensor(2)))
+    src = torch.empty_strided((70, 45), (50, 1))
+    dst = torch.empty(45, 70)
+    plan = _plan(h, src, dst)
+    ts, total = plan._table("input", src)
+    td, _ = plan._table("output", dst)
+    assert total == ts.size == td.size
+    offs = (np.arange(70)[:, None] * 50 + np.arange(45)[None, :]).T  # element (i, j) of the transposed view
+    valid = td >= 0
+    assert np.count_nonzero(valid) == 45 * 70
+    # every output element (i, j) -> input element (j, i)
+    i, j = np.divmod(td[valid], 70)
+    assert np.array_equal(ts[valid], offs[i, j])
+    assert np.all(ts[~valid] == -1)
+
+
+def test_index_tables_of_sliced_arrangements():
+    # reference tests/test_pad.py: input[input_slices] -> output[output_slices]
+    def arrange(input, output, input_slices, output_slices):
+        return input[input_slices], output[output_slices]
+
+    isl, osl = (slice(1, 2), slice(0, 3)), (slice(1, 2), slice(1, 4))
+    h = ninetoothed.make(arrange, app_copy, (Tensor(2), Tensor(2), isl, osl))
+    inp, out = torch.empty(2, 3), torch.empty(3, 6)
+    plan = _plan(h, inp, out)
+    ti, _ = plan._table("input", inp)
+    to, _ = plan._table("output", out)
+    assert np.array_equal(ti, np.arange(6).reshape(2, 3)[isl].ravel())
+    assert np.array_equal(to, np.arange(18).reshape(3, 6)[osl].ravel())
+
+
+def test_tables_agree_with_eval():
+    # ninetoothed.eval gives the contiguous source offset of every element of an arrangement
+    def arrange(x, y):
+        return x.tile((4, 8)), y.tile((4, 8))
+
+    h = ninetoothed.make(arrange, app_copy, (Tensor(2), Tensor(2)))
+    x = torch.empty(10, 20)
+    t, _ = _plan(h, x, x)._table("input", x)
+    src = Tensor(2)
+    assert np.array_equal(t, ninetoothed.eval(src.tile((4, 8)), {src: {"shape": (10, 20)}}).reshape(-1))
+
+
+def test_no_store_program_is_a_no_op():
+    # reference tests/test_expand.py: the application only names its parameter
+    def arrangement(x, BLOCK_SIZE=block_size()):
+        return (x.expand((BLOCK_SIZE,)).tile((BLOCK_SIZE,)),)
+
+    def application(x):
+        x  # noqa: B018
+
+    h = ninetoothed.make(arrangement, application, (Tensor(1),))
+    x = torch.empty((0,))
+    plan = _plan(h, x)
+    assert plan.describe()["family"] == "generic" and plan.describe()["outputs"] == []
+    assert plan.bind({"x": x}, {"x": 0})((x,)) is None
+
+
+@pytest.mark.parametrize("app, n, dtype", ((app_chain, 3, torch.float16), (app_chain, 3, torch.bfloat16),
+                                           (app_where, 3, torch.float32), (app_int, 3, torch.int32),
+                                           (app_pow, 3, torch.float64)))
+def test_emitted_source_compiles(app, n, dtype):
+    plan = _plan(_tiled1(app, n), *(torch.empty(8, dtype=dtype) for _ in range(n)))
+    blob = GenericPlan.compile(plan.source())
+    assert len(blob) > 1000
+    # the variant whose first operand is walked linearly (no index table)
+    assert len(GenericPlan.compile(plan.source({plan.loaded[0]: 5}))) > 1000
+
+
+# ------------------------------------------------------------------ GPU
+@pytest.mark.gpu
+def test_clone_reference_case():
+    # reference tests/test_clone.py:49-70 (application 0)
+    def arrangement(input, output):
+        block_shape = (block_size(), block_size())
+        return input.tile(block_shape), output.tile(block_shape)
+
+    kernel = ninetoothed.make(arrangement, app_copy, (Tensor(2), Tensor(2)))
+    inp = torch.empty_strided((641, 280), (700, 300), device="cuda")
+    inp.copy_(torch.randn(641, 280, device="cuda"))
+    out = torch.empty_like(inp)
+    kernel(inp, out)
+    assert torch.equal(out, inp)
+
+
+@pytest.mark.gpu
+def test_pow_reference_case():
+    # reference tests/test_pow.py:33-42
+    kernel = _tiled1(app_pow, 3)
+    inp = torch.rand(44925, device="cuda")
+    exponent = torch.rand(44925, device="cuda")
+    out = torch.empty_like(inp)
+    kernel(inp, exponent, out)
+    assert torch.allclose(out, torch.pow(inp, exponent), equal_nan=True)
+
+
+def _pad_slices(shape, pad):
+    out_shape, isl, osl = list(shape), [], []
+    for i in range(len(shape)):
+        left, right = pad[2 * (len(shape) - 1 - i)], pad[2 * (len(shape) - 1 - i) + 1]
+        out_shape[i] += left + right
+        isl.append(slice(max(0, -left), min(shape[i], shape[i] + right)))
+        osl.append(slice(max(0, left), out_shape[i] - max(0, right)))
+    return out_shape, tuple(isl), tuple(osl)
+
+
+_PAD_KERNELS = {}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype, atol", ((torch.float32, 1e-8), (torch.float16, 1e-3)))
+@pytest.mark.parametrize("value", (0, 1, -1, float("-inf"), torch.pi, float(torch.sqrt(torch.tensor(2026)))))
+@pytest.mark.parametrize("shape, pad", (((2026, 1207), (-100, 20, 99, -10)), ((2, 3), (1, 1, 1, 2)),
+                                        ((2, 3, 4), (1, 3, 1, 0, 0, 0)), ((2, 3), (-1, -1, 0, 0))))
+def test_pad_reference_cases(shape, pad, value, dtype, atol):
+    # reference tests/test_pad.py:40-58 (arrangement input[slices] -> output[slices])
+    def arrangement(input, output, input_slices, output_slices):
+        return input[input_slices], output[output_slices]
+
+    inp = torch.randn(shape, dtype=dtype, device="cuda")
+    out_shape, isl, osl = _pad_slices(shape, pad)
+    out = torch.full(out_shape, value, dtype=dtype, device="cuda")
+    key = str((len(shape), isl, osl))
+    if key not in _PAD_KERNELS:
+        _PAD_KERNELS[key] = ninetoothed.make(arrangement, app_copy, (Tensor(len(shape)), Tensor(len(shape)), isl, osl))
+    _PAD_KERNELS[key](inp, out)
+    assert torch.allclose(out, F.pad(inp, pad, "constant", value), atol=atol)
+
+
+@pytest.mark.gpu
+def test_expand_of_empty_tensor():
+    # reference tests/test_expand.py:16-22
+    def arrangement(x, BLOCK_SIZE=block_size()):
+        return (x.expand((BLOCK_SIZE,)).tile((BLOCK_SIZE,)),)
+
+    def application(x):
+        x  # noqa: B018
+
+    kernel = ninetoothed.make(arrangement, application, (Tensor(1),))
+    kernel(torch.empty((0,), device="cuda"))
+    torch.cuda.synchronize()
+
+
+def _chain_ref(x, y):
+    x, y = x.float(), y.float()
+    return torch.clamp_min(x * 2 + y, 0.0) - torch.exp(-x) / (1 + y * y)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16, torch.float32))
+@pytest.mark.parametrize("n", (1, 1000, 65537))
+def test_elementwise_chain(dtype, n):
+    kernel = _tiled1(app_chain, 3)
+    g = torch.Generator(device="cuda").manual_seed(n)
+    x = torch.randn(n, device="cuda", generator=g).to(dtype)
+    y = torch.randn(n, device="cuda", generator=g).to(dtype)
+    out = torch.empty(n, dtype=dtype, device="cuda")
+    kernel(x, y, out)
+    tol = 1e-4 if dtype == torch.float32 else 1e-2
+    torch.testing.assert_close(out.float(), _chain_ref(x, y), atol=tol, rtol=tol)
+
+
+@pytest.mark.gpu
+def test_where_scalars_cast_inplace_int():
+    n = 4099
+    x = torch.randn(n, device="cuda")
+    y = torch.randn(n, device="cuda")
+    out = torch.empty_like(x)
+    _tiled1(app_where, 3)(x, y, out)
+    assert torch.equal(out, torch.where(x > y, x, y * 0.5))
+
+    k = ninetoothed.make(lambda x, a, b, o: (x.tile((BS,)), a, b, o.tile((BS,))), app_scalars,
+                         (Tensor(1), Tensor(0), Tensor(0), Tensor(1)))
+    k(x, 0.25, 3, out)
+    torch.testing.assert_close(out, x * 0.25 + 3, atol=1e-6, rtol=1e-6)
+    k(x, -2.0, 5, out)  # same launcher, new scalar values
+    torch.testing.assert_close(out, x * -2.0 + 5, atol=1e-6, rtol=1e-6)
+
+    xh = x.half()
+    oh = torch.empty_like(xh)
+    _tiled1(app_cast, 2)(xh, oh)
+    ref = (xh > 0).half() * torch.sigmoid(xh.float()).half()
+    torch.testing.assert_close(oh.float(), ref.float(), atol=1e-3, rtol=1e-3)
+
+    z = x.clone()
+    ninetoothed.make(lambda t: (t.tile((BS,)),), app_inplace, (Tensor(1),))(z)
+    torch.testing.assert_close(z, x * x + 1, atol=1e-6, rtol=1e-6)
+
+    xi = torch.randint(-1000, 1000, (n,), device="cuda", dtype=torch.int32)
+    yi = torch.randint(-1000, 1000, (n,), device="cuda", dtype=torch.int32)
+    oi = torch.empty_like(xi)
+    _tiled1(app_int, 3)(xi, yi, oi)
+    assert torch.equal(oi, xi * 3 - yi)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", (torch.float16, torch.float32))
+def test_transposed_copy(dtype):
+    def arrange(src, dst):
+        return src.permute((1, 0)).tile((16, 32)), dst.tile((16, 32))
+
+    kernel = ninetoothed.make(arrange, app_copy, (Tensor(2), Tensor(2)))
+    src = torch.randn(300, 257, device="cuda").to(dtype)
+    dst = torch.empty(257, 300, dtype=dtype, device="cuda")
+    kernel(src, dst)
+    assert torch.equal(dst, src.t())
