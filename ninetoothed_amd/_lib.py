@@ -47,7 +47,7 @@ _SIGNATURES = {
     },
     **{
         f"nt_gemm_{t}": (_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I, _I64, _I64, _I64, _F, _F, _I, _P)
-        for t in ("f32", "f16", "bf16")
+        for t in ("f32", "f16", "bf16", "e5m2", "e4m3")
     },
     "nt_conv2d_workspace_size": (_I64,) * 9 + (_I,),
     **{
@@ -120,6 +120,11 @@ def dtype_code(dtype) -> int:
 
 
 def dtype_suffix(dtype) -> str:
+    import torch
+
+    fp8 = {getattr(torch, "float8_e5m2", None): "e5m2", getattr(torch, "float8_e4m3fn", None): "e4m3"}
+    if dtype in fp8 and dtype is not None:
+        return fp8[dtype]
     return {DTYPE_F32: "f32", DTYPE_F16: "f16", DTYPE_BF16: "bf16"}[dtype_code(dtype)]
 
 

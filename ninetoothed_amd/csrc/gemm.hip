@@ -139,7 +139,34 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, const floatx16 
   }
 }
 
-template <typename T, bool FAST>
+// Operand storage of gemm_mfma_kernel's element-wise loader.  16-bit operands are used as
+// they are; fp8 operands are widened exactly to fp16 (every e5m2 and e4m3fn value is an
+// fp16 value) and multiplied on the fp16 matrix core, so the products are exact in fp32
+// as on an fp8 matrix core.
+struct src16 {
+  typedef uint16_t storage;
+  __device__ __forceinline__ static uint16_t widen(uint16_t v) { return v; }
+};
+struct src_e5m2 {  // OCP E5M2: sign, 5 exponent bits (bias 15), 2 mantissa bits = the top byte of an fp16
+  typedef uint8_t storage;
+  __device__ __forceinline__ static uint16_t widen(uint8_t v) { return (uint16_t)((uint16_t)v << 8); }
+};
+struct src_e4m3 {  // OCP E4M3FN: sign, 4 exponent bits (bias 7), 3 mantissa bits, no infinities, S.1111.111 = NaN
+  typedef uint8_t storage;
+  __device__ __forceinline__ static uint16_t widen(uint8_t v) {
+    const uint16_t s = (uint16_t)(v & 0x80) << 8;
+    const int e = (v >> 3) & 0xf, m = v & 7;
+    if (e == 0xf && m == 7) return s | 0x7e00;
+    if (e == 0) {  // m * 2^-9: normalised in fp16 with the leading one of m as the implicit bit
+      if (m == 0) return s;
+      const int lead = m >= 4 ? 2 : (m >= 2 ? 1 : 0);
+      return s | (uint16_t)((lead + 6) << 10) | (uint16_t)((m - (1 << lead)) << (10 - lead));
+    }
+    return s | (uint16_t)((e + 8) << 10) | (uint16_t)(m << 7);
+  }
+};
+
+template <typename T, bool FAST, typename S = src16>
 __global__ __launch_bounds__(G_THREADS) void gemm_mfma_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(16))) uint16_t smem[(GB_M + GB_N) * GB_K];
   uint16_t* sA = smem;
@@ -192,20 +219,22 @@ __global__ __launch_bounds__(G_THREADS) void gemm_mfma_kernel(GemmArgs g) {
     }
   };
   // Generic loader: element-wise, any strides, bounds-checked, zero fill.
+  const typename S::storage* As = (const typename S::storage*)g.a;
+  const typename S::storage* Bs = (const typename S::storage*)g.b;
   auto load_store_generic = [&](int64_t kt) {
     const int64_t k0 = kt * GB_K;
     for (int e = tid; e < GB_M * GB_K; e += G_THREADS) {
       const int row = e / GB_K, kk = e % GB_K;
       const int64_t m = m0 + row, k = k0 + kk;
       uint16_t v = 0;
-      if (m < g.M && k < g.K) v = A[m * g.sa_m + k * g.sa_k];
+      if (m < g.M && k < g.K) v = S::widen(As[m * g.sa_m + k * g.sa_k]);
       sA[lds_index(row, kk)] = v;
     }
     for (int e = tid; e < GB_N * GB_K; e += G_THREADS) {
       const int kk = e / GB_N, col = e % GB_N;
       const int64_t n = n0 + col, k = k0 + kk;
       uint16_t v = 0;
-      if (n < g.N && k < g.K) v = B[k * g.sb_k + n * g.sb_n];
+      if (n < g.N && k < g.K) v = S::widen(Bs[k * g.sb_k + n * g.sb_n]);
       sB[lds_index(col, kk)] = v;
     }
   };
@@ -813,6 +842,25 @@ static int gemm16_launch(GemmArgs g, hipStream_t stream) {
   return launch_status();
 }
 
+// fp8 operands (any strides): the element-wise loader widens them to fp16.
+template <typename S>
+static int gemm8_launch(GemmArgs g, hipStream_t stream) {
+  if (int e = gemm_check(g)) return e;
+  if (g.M == 0 || g.N == 0) return 0;
+  if (!g.a || !g.b || !g.out) return NT_ERR_INVALID;
+  if (g.K == 0) {
+    hipLaunchKernelGGL(gemm_k0_kernel, dim3(1024), dim3(256), 0, stream, g);
+    return launch_status();
+  }
+  const int64_t tiles_m = cdiv(g.M, GB_M), tiles_n = cdiv(g.N, GB_N);
+  if (tiles_m * tiles_n > 0x7fffffffLL) return NT_ERR_INVALID;
+  g.tiles_m = (int)tiles_m;
+  g.tiles_n = (int)tiles_n;
+  hipLaunchKernelGGL((gemm_mfma_kernel<f16_t, false, S>), dim3((unsigned)(tiles_m * tiles_n)), dim3(G_THREADS), 0,
+                     stream, g);
+  return launch_status();
+}
+
 static int gemm32_launch(GemmArgs g, hipStream_t stream) {
   if (int e = gemm_check(g)) return e;
   if (g.M == 0 || g.N == 0) return 0;
@@ -860,3 +908,9 @@ extern "C" int nt_gemm_bf16(NT_GEMM_PARAMS) {
   return nt::gemm16_launch<nt::bf16_t>(nt::make_args(NT_GEMM_ARGS), stream);
 }
 extern "C" int nt_gemm_f32(NT_GEMM_PARAMS) { return nt::gemm32_launch(nt::make_args(NT_GEMM_ARGS), stream); }
+extern "C" int nt_gemm_e5m2(NT_GEMM_PARAMS) {
+  return nt::gemm8_launch<nt::src_e5m2>(nt::make_args(NT_GEMM_ARGS), stream);
+}
+extern "C" int nt_gemm_e4m3(NT_GEMM_PARAMS) {
+  return nt::gemm8_launch<nt::src_e4m3>(nt::make_args(NT_GEMM_ARGS), stream);
+}

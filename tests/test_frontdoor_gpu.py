@@ -73,6 +73,23 @@ def test_matmul_reference_case():
     assert kernel.plans()[0]["family"] == "gemm"
 
 
+@pytest.mark.parametrize("dtype", (torch.float8_e5m2, torch.float8_e4m3fn))
+def test_matmul_fp8_reference_case(dtype):
+    # reference tests/test_matmul.py:64-88: fp8 lhs, column-major fp8 rhs (`other.T.to(dtype)`),
+    # fp16 output, atol 0.125 against torch.matmul on the operands widened to fp16
+    m = n = k = 512
+    lhs = _randn((m, k), torch.float16, 11).to(dtype)
+    rhs = _randn((k, n), torch.float16, 12).T.to(dtype)  # used as the (k, n) operand: column-major
+    assert rhs.stride() == (1, k)
+    output = torch.empty((m, n), dtype=torch.float16, device=DEV)
+    kernel = ninetoothed.make(pg.matmul_arrangement, pg.matmul_application, pg.matmul_tensors())
+    kernel(lhs, rhs, output)
+    expected = torch.matmul(lhs.to(torch.float16), rhs.to(torch.float16))
+    assert torch.allclose(output, expected, atol=0.125)
+    ref = apply.matmul(_np(lhs), _np(rhs), "float16", pg.matmul_arrangement, block=(64, 64, 64))
+    assert np.allclose(_np(output), ref, atol=1e-2, rtol=1e-2)
+
+
 def test_matmul_fp32_readme_case():
     lhs, rhs = _randn((512, 512), torch.float32, 3), _randn((512, 512), torch.float32, 4)
     output = torch.empty((512, 512), device=DEV)

@@ -159,6 +159,37 @@ def test_gemm16(mnk, dtype):
     assert torch.allclose(out.float(), ref.float(), atol=tol, rtol=1e-2)
 
 
+_FP8 = (torch.float8_e5m2, torch.float8_e4m3fn)
+
+
+@pytest.mark.parametrize("dtype", _FP8)
+def test_gemm_fp8_every_finite_value_is_exact(dtype):
+    # a holds every finite byte pattern once (inf/NaN would spread through the zero terms);
+    # b is a one-hot matrix, so out = a exactly: pins the fp8 -> fp16 widening bit for bit
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    vals = codes.view(dtype).float()
+    codes = torch.where(torch.isfinite(vals), codes, torch.zeros_like(codes))
+    a = codes.view(dtype).reshape(4, 64).to(DEV)
+    b = torch.eye(64, dtype=torch.float32).to(dtype).to(DEV)
+    out = torch.empty((4, 64), dtype=torch.float32, device=DEV)
+    kernels.gemm(a, b, out)
+    assert torch.equal(out, a.float())
+
+
+@pytest.mark.parametrize("dtype", _FP8)
+@pytest.mark.parametrize("mnk", ((300, 200, 100), (256, 512, 1000), (1, 1, 1)))
+def test_gemm_fp8_ragged_strided(mnk, dtype):
+    m, n, k = mnk
+    a = _randn((m, k), torch.float16, 21).to(dtype)
+    b = _randn((n, k), torch.float16, 22).to(dtype).t()  # k-contiguous
+    c = _randn((m, n), torch.float16, 23)
+    out = torch.empty((m, n), dtype=torch.float16, device=DEV)
+    kernels.gemm(a, b, out, c=c, alpha=0.5, beta=2.0, round_dtype=torch.float16)
+    ref = _gemm_ref(a.to(torch.float16), b.to(torch.float16), c, 0.5, 2.0, torch.float16)
+    tol = 1e-2 * max(1.0, math.sqrt(k) / 8)
+    assert torch.allclose(out.float(), ref.float(), atol=tol, rtol=1e-2)
+
+
 def test_addmm_epilogue():
     m = n = k = 512
     c = _randn((m, n), torch.float16, 13)
