@@ -541,6 +541,11 @@ class Lowerer:
             return b.make("math", name, self.data(args[0]))
         if name == "cast":
             return b.make("cast", self.data(args[0]), self.dtype_value(args[1] if len(args) > 1 else kwargs["dtype"]))
+        if name in ("rand", "randint", "randn"):
+            # counter-based random numbers: (seed, offset) -> one value per offset element
+            if len(args) != 2 or kwargs:
+                raise LoweringError(f"ntl.{name} takes (seed, offset)")
+            return b.make(name, self.data(args[0]), self.data(args[1]))
         if name.startswith("libdevice."):
             if kwargs:
                 raise LoweringError(f"{name} takes positional arguments only")

@@ -45,7 +45,7 @@ MAX_ELEMENTS = 1 << 26  # host-side index tables: at most 64 Mi elements per lau
 
 _ALLOWED = {"load", "const", "param", "add", "sub", "mul", "div", "floordiv", "mod", "neg", "lt", "le", "gt", "ge",
             "eq", "ne", "where", "maximum", "minimum", "math", "libm", "cast", "dtype", "dtype_of", "zeros",
-            "full"}
+            "full", "offsets", "rand", "randint", "randn"}
 
 _FLOAT = ("float16", "bfloat16", "float32", "float64")
 _INT = ("int8", "int16", "int32", "int64", "uint8")
@@ -75,6 +75,33 @@ __device__ __forceinline__ float r_bf16(float x) {
   if ((u & 0x7fffffffu) > 0x7f800000u) return __builtin_bit_cast(float, (u | 0x00400000u) & 0xffff0000u);
   u += 0x7fffu + ((u >> 16) & 1u);
   return __builtin_bit_cast(float, u & 0xffff0000u);
+}
+// ntl.rand / randint / randn: Philox4x32-10 (Salmon et al., SC'11) on the counter
+// (offset, 0, 0, 0) keyed by the 64-bit seed, as Triton's tl.rand family.
+__device__ __forceinline__ void nt_philox(long long seed, long long offset, unsigned (&c)[4]) {
+  unsigned k0 = (unsigned)(unsigned long long)seed, k1 = (unsigned)((unsigned long long)seed >> 32);
+  c[0] = (unsigned)offset; c[1] = 0u; c[2] = 0u; c[3] = 0u;
+  for (int r = 0; r < 10; ++r) {
+    const unsigned long long p0 = 0xD2511F53ull * c[0], p1 = 0xCD9E8D57ull * c[2];
+    const unsigned n0 = (unsigned)(p1 >> 32) ^ c[1] ^ k0, n2 = (unsigned)(p0 >> 32) ^ c[3] ^ k1;
+    c[1] = (unsigned)p1; c[3] = (unsigned)p0; c[0] = n0; c[2] = n2;
+    k0 += 0x9E3779B9u; k1 += 0xBB67AE85u;
+  }
+}
+__device__ __forceinline__ float nt_uniform(unsigned w) {  // [0, 1): |int32| folded, times ~2^-31
+  const int x = (int)w;
+  return (float)(x < 0 ? ~x : x) * 4.6566127342e-10f;
+}
+__device__ __forceinline__ long long nt_randint(long long seed, long long offset) {
+  unsigned c[4]; nt_philox(seed, offset, c); return (long long)c[0];
+}
+__device__ __forceinline__ float nt_rand(long long seed, long long offset) {
+  unsigned c[4]; nt_philox(seed, offset, c); return nt_uniform(c[0]);
+}
+__device__ __forceinline__ float nt_randn(long long seed, long long offset) {
+  unsigned c[4]; nt_philox(seed, offset, c);
+  const float u1 = fmaxf(nt_uniform(c[0]), 1e-7f), u2 = nt_uniform(c[1]);
+  return sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
 }
 __device__ __forceinline__ float ld_bf16(unsigned short b) { return __builtin_bit_cast(float, (unsigned)b << 16); }
 __device__ __forceinline__ unsigned short st_bf16(float x) { return (unsigned short)(__builtin_bit_cast(unsigned, r_bf16(x)) >> 16); }
@@ -145,6 +172,7 @@ class _Emitter:
         self.lines = []
         self.tensors = []  # loaded tensor params, in argument order
         self.scalars = []  # 0-d scalar params, in argument order
+        self.offsets = []  # (tensor param, source dim) whose per-element offsets the body reads
 
     def tensor_dtype(self, name):
         return _torch_dtype_name(self.ctx.dtypes[name])
@@ -318,6 +346,20 @@ class _Emitter:
             cf = _MATH[fname][1 if self.work(t) == "double" else 0]
             self.define(v, t, f"{cf}({', '.join(self.operand(o, t) for o in operands)})")
             return
+        if op == "offsets":
+            view, d = args
+            if view.op != "param":
+                raise LoweringError("the generic kernels take `offsets` of whole arranged tensors only")
+            key = (view.args[0], int(d))
+            if key not in self.offsets:
+                self.offsets.append(key)
+            self.names[id(v)] = f"q_{key[0]}_{key[1]}"
+            self.types[id(v)] = "int32"
+            return
+        if op in ("rand", "randint", "randn"):
+            seed, off = self.operand(args[0], "int64"), self.operand(args[1], "int64")
+            self.define(v, "int64" if op == "randint" else "float32", f"nt_{op}({seed}, {off})", exact=True)
+            return
         raise LoweringError(f"operation `{op}` is not supported by the generic kernels")
 
 
@@ -333,7 +375,9 @@ def _analyse(ctx):
             return None
         if v.op == "load" and v.args[0].op != "param":
             return None
-    tensors = [n for n in list(stores) + [v.args[0].args[0] for v in values if v.op == "load"]
+        if v.op == "offsets" and v.args[0].op != "param":
+            return None
+    tensors = [n for n in list(stores) + [v.args[0].args[0] for v in values if v.op in ("load", "offsets")]
                if ctx.params[n].source_ndim != 0]
     shapes = {tuple(ctx.views[n].level_shapes) for n in tensors}
     if len(shapes) > 1:
@@ -359,6 +403,7 @@ class GenericPlan:
             em.emit(v)
         self.loaded = list(em.tensors)
         self.scalars = list(em.scalars)
+        self.offsets = list(em.offsets)
         self.outputs = list(stores)
         lines = []
         for out, v in stores.items():
@@ -375,6 +420,8 @@ class GenericPlan:
         params = []
         for n in self.index_names:
             params.append(f"const int* __restrict__ t_{n}")
+        for n, d in self.offsets:
+            params.append(f"const int* __restrict__ f_{n}_{d}")
         for n in self.loaded:
             if n not in self.outputs:
                 params.append(f"const {_STORAGE[_torch_dtype_name(ctx.dtypes[n])][0]}* __restrict__ p_{n}")
@@ -387,8 +434,9 @@ class GenericPlan:
         self.params = params
         self.kernel_name = "nt_generic"
 
-    def source(self, linear=None):
-        """Kernel source; ``linear[name] = n`` marks a tensor whose index table is e for e < n, -1 after."""
+    def source(self, linear=None, linear_offsets=()):
+        """Kernel source; ``linear[name] = n`` marks a tensor whose index table is e for e < n, -1 after;
+        ``linear_offsets`` the (tensor, dim) offsets tables that equal e."""
         linear = linear or {}
 
         def index(n):
@@ -396,6 +444,8 @@ class GenericPlan:
 
         head = [f"    const int i_{n} = {index(n)};" for n in self.loaded]
         head += [f"    const int o_{n} = {index(n)};" for n in self.outputs]
+        head += [f"    const long long q_{n}_{d} = {'e' if (n, d) in linear_offsets else f'(long long)f_{n}_{d}[e]'};"
+                 for n, d in self.offsets]
         return (
             _PRELUDE
             + f'\nextern "C" __global__ void __launch_bounds__(256) {self.kernel_name}({", ".join(self.params)}) {{\n'
@@ -439,13 +489,19 @@ class GenericPlan:
                 self._functions[digest] = fn
         return fn
 
-    def _table(self, name, tensor):
+    def _maps(self, name):
+        """(source index arrays, mask, flattened level shape) of every element of ``name``'s arrangement."""
         view = self.ctx.views[name]
         shape = tuple(s for level in view.level_shapes for s in level)
         total = int(np.prod(shape)) if shape else 1
         if total > MAX_ELEMENTS:
             raise LoweringError(f"the generic kernels index at most {MAX_ELEMENTS} elements per launch ({total} here)")
         idx, mask = view.probe(view.full_index())
+        return idx, mask, shape
+
+    def _table(self, name, tensor, maps=None):
+        idx, mask, shape = maps or self._maps(name)
+        total = int(np.prod(shape)) if shape else 1
         off = np.zeros((), dtype=np.int64)
         for i, st in zip(idx, tensor.stride()):
             off = off + np.asarray(i, dtype=np.int64) * int(st)
@@ -454,6 +510,14 @@ class GenericPlan:
             raise LoweringError("the generic kernels address at most 2^31 elements of a tensor")
         return off.astype(np.int32), total
 
+    def _offsets_table(self, name, dim, maps=None):
+        """Source index along ``dim`` of every element (masked ones included), as ``offsets(dim)`` reads it."""
+        idx, _, shape = maps or self._maps(name)
+        q = np.broadcast_to(np.asarray(idx[dim], dtype=np.int64), shape).reshape(-1)
+        if q.size and (q.max() >= 2**31 or q.min() < -(2**31)):
+            raise LoweringError("the generic kernels take offsets within 32 bits")
+        return q.astype(np.int32)
+
     def bind(self, values, index):
         import torch
 
@@ -461,10 +525,12 @@ class GenericPlan:
             return lambda args: None
         device = None
         tables, linear, total = {}, {}, None
+        maps = {}
         for n in self.index_names:
             t = values[n]
             device = t.device
-            tab, tot = self._table(n, t)
+            maps[n] = self._maps(n)
+            tab, tot = self._table(n, t, maps[n])
             if total is not None and tot != total:
                 raise LoweringError("generic kernel operands do not share one index space")
             total = tot
@@ -473,9 +539,19 @@ class GenericPlan:
                 linear[n] = valid  # e -> e, masked from `valid` on: no table
             else:
                 tables[n] = torch.from_numpy(tab).to(device)
-        fn = self.function(self.source(linear))
+        offset_tables, linear_offsets = {}, set()
+        for n, d in self.offsets:
+            q = self._offsets_table(n, d, maps.get(n))
+            if q.size != total:
+                raise LoweringError("generic kernel operands do not share one index space")
+            if np.array_equal(q, np.arange(q.size, dtype=np.int32)):
+                linear_offsets.add((n, d))
+            else:
+                offset_tables[(n, d)] = torch.from_numpy(q).to(device)
+        fn = self.function(self.source(linear, linear_offsets))
         ptrs = {n: ctypes.c_void_p() for n in self.index_names}
         argv = [ctypes.c_void_p(tables[n].data_ptr() if n in tables else None) for n in self.index_names]
+        argv += [ctypes.c_void_p(offset_tables[k].data_ptr() if k in offset_tables else None) for k in self.offsets]
         argv += [ptrs[n] for n in self.loaded if n not in self.outputs]
         argv += [ptrs[n] for n in self.outputs]
         svals = {n: ctypes.c_int64() if self.scalar_types[n] == "int64" else ctypes.c_float() for n in self.scalars}
@@ -498,7 +574,7 @@ class GenericPlan:
             if status != 0:
                 raise KernelLaunchError(status)
 
-        launch.keep = (tables, argv, params)  # device tables and the argument block live with the launcher
+        launch.keep = (tables, offset_tables, argv, params)  # device tables and the argument block live with the launcher
         return launch
 
     def run(self, values):

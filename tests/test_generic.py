@@ -307,3 +307,74 @@ def test_transposed_copy(dtype):
     dst = torch.empty(257, 300, dtype=dtype, device="cuda")
     kernel(src, dst)
     assert torch.equal(dst, src.t())
+
+
+# ------------------------------------------------------------------ ntl.rand family (dropout)
+def drop_arrangement(input, p, seed, output, BLOCK_SIZE=block_size()):
+    return input.tile((BLOCK_SIZE,)), p, seed, output.tile((BLOCK_SIZE,))
+
+
+def drop_application(input, p, seed, output):
+    # reference tests/test_dropout.py:16-17
+    output = ntl.where(ntl.rand(seed, input.offsets()) > p, input / (1 - p), 0)  # noqa: F841
+
+
+def app_randint(seed, output):
+    output = ntl.randint(seed, output.offsets())  # noqa: F841
+
+
+def app_rand(seed, output):
+    output = ntl.rand(seed, output.offsets())  # noqa: F841
+
+
+def app_randn(seed, output):
+    output = ntl.randn(seed, output.offsets())  # noqa: F841
+
+
+def _rng_kernel(app):
+    return ninetoothed.make(lambda s, o: (s, o.tile((BS,))), app, (Tensor(0), Tensor(1)))
+
+
+def test_dropout_program_compiles():
+    k = ninetoothed.make(drop_arrangement, drop_application, (Tensor(1), Tensor(0), Tensor(0), Tensor(1)))
+    x = torch.empty(349, dtype=torch.float16)
+    plan = _plan(k, x, 0.3, 12345, x)
+    assert plan.offsets == [("input", 0)] and plan.scalar_types == {"seed": "int64", "p": "float32"}
+    assert len(GenericPlan.compile(plan.source())) > 1000
+    q = plan._offsets_table("input", 0)
+    assert np.array_equal(q, np.arange(q.size))  # 1-D tiles: the offset of element e is e
+
+
+@pytest.mark.gpu
+def test_dropout_reference_case():
+    # reference tests/test_dropout.py:33-48, plus the exact mask from the oracle's Philox
+    from oracle import philox
+
+    kernel = ninetoothed.make(drop_arrangement, drop_application, (Tensor(1), Tensor(0), Tensor(0), Tensor(1)))
+    x = torch.randn(349, dtype=torch.float16, device="cuda")
+    p, seed = 0.3, 1_234_567
+    out = torch.empty_like(x)
+    kernel(x, p, seed, out)
+    assert abs(out.nonzero().numel() / x.numel() - (1 - p)) < 0.05
+    assert torch.allclose(out[out != 0], x[out != 0] / (1 - p))
+    keep = philox.rand(seed, np.arange(349)) > np.float32(p)
+    xs = x.float().cpu().numpy()
+    expected = np.where(keep, xs / (np.float32(1.0) - np.float32(p)), 0).astype(np.float16)
+    assert np.array_equal(out.cpu().numpy(), expected)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", (0, 1, 2**31 - 1, 2**40 + 12345))
+def test_random_streams_match_the_oracle(seed):
+    from oracle import philox
+
+    n = 100_003
+    offs = np.arange(n)
+    oi = torch.empty(n, dtype=torch.int64, device="cuda")
+    _rng_kernel(app_randint)(seed, oi)
+    assert np.array_equal(oi.cpu().numpy(), philox.randint(seed, offs).astype(np.int64))
+    of = torch.empty(n, dtype=torch.float32, device="cuda")
+    _rng_kernel(app_rand)(seed, of)
+    assert np.array_equal(of.cpu().numpy(), philox.rand(seed, offs))
+    _rng_kernel(app_randn)(seed, of)
+    assert np.allclose(of.cpu().numpy(), philox.randn(seed, offs), atol=1e-5, rtol=1e-5)

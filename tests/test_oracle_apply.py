@@ -130,3 +130,31 @@ def test_add_closed_form():
     r = _rng(10)
     a, b = r.random(1000).astype(np.float32), r.random(1000).astype(np.float32)
     assert np.array_equal(apply.add(a, b, 256), a + b)
+
+
+# ------------------------------------------------------------------ ntl.rand / randint / randn
+def test_philox_known_answers():
+    # Random123's published known-answer vectors for philox4x32-10 (counter, key -> output)
+    from oracle import philox
+
+    kats = (
+        ((0, 0, 0, 0), (0, 0), (0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8)),
+        ((0xFFFFFFFF,) * 4, (0xFFFFFFFF,) * 2, (0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD)),
+        ((0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344), (0xA4093822, 0x299F31D0),
+         (0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1)),
+    )
+    for counter, key, expected in kats:
+        assert tuple(int(x) for x in philox.philox4x32(counter, key)) == expected
+
+
+def test_uniform_mapping_range_and_extremes():
+    from oracle import philox
+
+    words = np.array([0, 1, 0x7FFFFFFF, 0x80000000, 0xFFFFFFFF], dtype=np.uint32)
+    u = philox.uniform(words)
+    # int32 0 -> 0; 2^31 - 1 and its mirror -2^31 -> the largest value, still below 1
+    assert u[0] == 0.0 and u[4] == 0.0 and u[2] == u[3] and 0.999 < u[2] < 1.0
+    r = philox.rand(1234, np.arange(1 << 16))
+    assert r.min() >= 0.0 and r.max() < 1.0 and abs(r.mean() - 0.5) < 0.01
+    n = philox.randn(1234, np.arange(1 << 16))
+    assert abs(n.mean()) < 0.02 and abs(n.std() - 1.0) < 0.02
