@@ -45,7 +45,7 @@ MAX_ELEMENTS = 1 << 26  # host-side index tables: at most 64 Mi elements per lau
 
 _ALLOWED = {"load", "const", "param", "add", "sub", "mul", "div", "floordiv", "mod", "neg", "lt", "le", "gt", "ge",
             "eq", "ne", "where", "maximum", "minimum", "math", "libm", "cast", "dtype", "dtype_of", "zeros",
-            "full", "offsets", "rand", "randint", "randn"}
+            "full", "offsets", "rand", "randint", "randn", "shape", "source_shape"}
 
 _FLOAT = ("float16", "bfloat16", "float32", "float64")
 _INT = ("int8", "int16", "int32", "int64", "uint8")
@@ -209,10 +209,24 @@ class _Emitter:
             return f"r_bf16({expr})"
         return expr
 
+    def const_value(self, v):
+        """The Python value of a constant, ``x.shape[d]`` or ``x.source.shape[d]``; None otherwise."""
+        if v.op == "const":
+            return v.args[0]
+        if v.op == "shape":
+            view, d = v.args
+            level = 1
+            while view.op == "index":
+                view, level = view.args[0], level + 1
+            return int(self.ctx.views[view.args[0]].level_shapes[level][d])
+        if v.op == "source_shape":
+            return int(self.ctx.views[v.args[0]].source_shape[v.args[1]])
+        return None
+
     def operand(self, v, t):
         """Operand ``v`` as a value of working type for an operation in type ``t``."""
-        if v.op == "const":
-            c = v.args[0]
+        if v.op in ("const", "shape", "source_shape"):
+            c = self.const_value(v)
             if isinstance(c, bool):
                 return "true" if c else "false"
             w = self.work(t)
@@ -243,8 +257,8 @@ class _Emitter:
 
     def emit(self, v):
         op, args = v.op, v.args
-        if op == "const":
-            self.types[id(v)] = "bool" if isinstance(args[0], bool) else "weak"
+        if op in ("const", "shape", "source_shape"):
+            self.types[id(v)] = "bool" if isinstance(self.const_value(v), bool) else "weak"
             return
         if op in ("dtype", "dtype_of", "param"):
             return
@@ -410,7 +424,7 @@ class GenericPlan:
             t = _torch_dtype_name(ctx.dtypes[out])
             src = em.type_of(v)
             src = "float32" if src == "weak" else src
-            val = em.operand(v, src) if v.op == "const" else em.names[id(v)]
+            val = em.operand(v, src) if v.op in ("const", "shape", "source_shape") else em.names[id(v)]
             if em.work(src) != em.work(t):
                 val = f"(({em.work(t)}){val})"
             lines.append(f"    if (o_{out} >= 0) p_{out}[o_{out}] = {_STORAGE[t][3].format(val)};")
@@ -582,10 +596,430 @@ class GenericPlan:
         self.bind(values, {n: i for i, n in enumerate(names)})(tuple(values[n] for n in names))
 
 
-def match_generic(ctx):
-    """The generic element-parallel kernel, or None when the program is not element-parallel."""
-    found = _analyse(ctx)
-    if found is None:
+# ============================================================================ tile programs
+# Programs with reductions (``ntl.sum/max/min``) or broadcasting subscripts run one
+# workgroup per program instance: reductions first, in dependency order, each into an LDS
+# array (groups of G lanes per output element stride the reduced axis and combine with
+# wave64 shuffles), then every output tile element by element.  Values between them are
+# recomputed at the coordinates where they are read (loads through the index tables,
+# reduction results from LDS).  A reduction operand element counts only where the load
+# masks of every tensor it is computed from hold, else it is the reduction's identity
+# (reference src/ninetoothed/backends/emitters/ssa.py:1834-1910, 2180-2210).
+
+_TILE_ALLOWED = _ALLOWED | {"reduce", "bcast"}
+LDS_BYTES = 64 * 1024
+_INT_LIMITS = {"int8": (-128, 127), "uint8": (0, 255), "int16": (-32768, 32767), "int32": (-(2**31), 2**31 - 1),
+               "int64": (-(2**63), 2**63 - 1)}
+
+
+def _value_operands(v):
+    if v.op == "math":
+        return [v.args[1]]
+    if v.op == "libm":
+        return list(v.args[1])
+    if v.op in ("cast", "bcast"):
+        return [v.args[0]]
+    if v.op in ("load", "offsets", "reduce", "const", "shape", "source_shape", "zeros", "full", "param", "dtype",
+                "dtype_of"):
+        return []
+    return [a for a in v.args if isinstance(a, Value)]
+
+
+def _bcast_shapes(*shapes):
+    try:
+        return tuple(int(x) for x in np.broadcast_shapes(*shapes))
+    except ValueError:
+        raise LoweringError(f"shapes {shapes} do not broadcast") from None
+
+
+def _tile_shape(ctx, name):
+    ls = ctx.views[name].level_shapes
+    return tuple(ls[1]) if len(ls) > 1 else ()
+
+
+def _shapes(ctx, values, const_value):
+    """Tile shape of every value: loads have their tensor's tile shape, reductions drop
+    their axis (all axes for ``axis=None``), ``x[:, None]`` inserts unit dims, and
+    elementwise operations broadcast as numpy does (right-aligned)."""
+    shp = {}
+    for v in values:
+        op, a = v.op, v.args
+        if op in ("const", "dtype", "dtype_of", "shape", "source_shape", "param"):
+            s = ()
+        elif op == "load":
+            name = a[0].args[0]
+            s = () if ctx.params[name].source_ndim == 0 else _tile_shape(ctx, name)
+        elif op == "offsets":
+            s = _tile_shape(ctx, a[0].args[0])
+        elif op == "reduce":
+            src, axis = shp[id(a[1])], a[2]
+            if axis is None:
+                s = ()
+            else:
+                ax = axis + len(src) if axis < 0 else axis
+                if not 0 <= ax < len(src):
+                    raise LoweringError(f"reduction axis {axis} of a {len(src)}-D value")
+                s = src[:ax] + src[ax + 1:]
+        elif op == "bcast":
+            src, pattern = list(shp[id(a[0])]), a[1]
+            if sum(1 for x in pattern if x == ":") != len(src):
+                raise LoweringError("a broadcasting subscript needs one `:` per dimension")
+            it = iter(src)
+            s = tuple(next(it) if x == ":" else 1 for x in pattern)
+        elif op in ("zeros", "full"):
+            dims = []
+            for d in a[0]:
+                c = const_value(d) if isinstance(d, Value) else d
+                if not isinstance(c, int):
+                    raise LoweringError("zeros/full need constant shapes")
+                dims.append(c)
+            s = tuple(dims)
+        else:
+            s = _bcast_shapes(*[shp[id(x)] for x in _value_operands(v)]) if _value_operands(v) else ()
+        shp[id(v)] = s
+    return shp
+
+
+def _unravel(idx, shape):
+    """C expressions of the coordinates of row-major element ``idx`` of ``shape``."""
+    coords, stride = [], 1
+    for size in reversed(shape):
+        if size == 1:
+            coords.append("0")
+        else:
+            coords.append(f"(({idx} / {stride}LL) % {size}LL)" if stride > 1 else f"({idx} % {size}LL)")
+        stride *= size
+    return tuple(reversed(coords))
+
+
+def _ravel(coords, shape):
+    terms, stride = [], 1
+    for c, size in zip(reversed(coords), reversed(shape)):
+        if size != 1:
+            terms.append(f"{c} * {stride}LL" if stride > 1 else f"{c}")
+        stride *= size
+    return " + ".join(reversed(terms)) if terms else "0"
+
+
+class _TileEmitter(_Emitter):
+    """Code for one evaluation context: a root value at given coordinates, and every value
+    it is computed from at the coordinates that implies."""
+
+    def __init__(self, plan):
+        super().__init__(plan.ctx)
+        self.plan = plan
+        self.types = plan.types
+        self.shapes = plan.shapes
+
+    def context(self, root, coords, tag):
+        self.names, self.lines, self.coords, self.masks, self.tag = {}, [], {}, {}, tag
+        self._assign(root, tuple(coords))
+        for v in _walk([root]):
+            if id(v) in self.coords:
+                self.emit(v)
+        return self.lines
+
+    def _canon(self, v, coords):
+        return tuple("0" if size == 1 else c for size, c in zip(self.shapes[id(v)], coords))
+
+    def _assign(self, v, coords):
+        coords = self._canon(v, coords)
+        prev = self.coords.get(id(v))
+        if prev is not None:
+            if prev != coords:
+                raise LoweringError("a value is read at two different broadcast positions in one expression")
+            return
+        self.coords[id(v)] = coords
+        if v.op == "bcast":
+            self._assign(v.args[0], tuple(c for c, x in zip(coords, v.args[1]) if x == ":"))
+            return
+        for a in _value_operands(v):
+            sa = self.shapes[id(a)]
+            aligned = coords[len(coords) - len(sa):] if sa else ()
+            self._assign(a, aligned)
+
+    def define(self, v, t, expr, exact=False):
+        name = f"{self.tag}{len(self.names)}"
+        self.lines.append(f"      const {self.work(t)} {name} = {expr if exact else self.round_to(t, expr)};")
+        self.names[id(v)] = name
+        self.types[id(v)] = t
+
+    def emit(self, v):
+        op, args = v.op, v.args
+        if op == "load" and self.ctx.params[args[0].args[0]].source_ndim != 0:
+            name = args[0].args[0]
+            t = self.tensor_dtype(name)
+            st, w, ld, _ = _STORAGE[t]
+            lin = _ravel(self.coords[id(v)], self.shapes[id(v)])
+            ix = f"{self.tag}x{len(self.names)}"
+            self.lines.append(f"      const int {ix} = {self.plan.index_expr(name, lin)};")
+            other = self.ctx.views[name].source.other
+            other = 0.0 if other is None else float(other)
+            o = repr(other) if other == other and abs(other) != float("inf") else (
+                "__builtin_nanf(\"\")" if other != other else ("__builtin_huge_valf()" if other > 0 else "(-__builtin_huge_valf())"))
+            self.define(v, t, f"({ix} >= 0 ? ({w}){ld.format(f'p_{name}[{ix}]')} : ({w}){o})", exact=True)
+            self.masks[id(v)] = frozenset([ix])
+            return
+        if op == "offsets":
+            name, d = args[0].args[0], int(args[1])
+            lin = _ravel(self.coords[id(v)], self.shapes[id(v)])
+            self.names[id(v)] = f"(long long)f_{name}_{d}[pb_{name} + {lin}]"
+            self.types[id(v)] = "int32"
+            self.masks[id(v)] = frozenset()
+            return
+        if op == "reduce":
+            arr, oshape = self.plan.lds[id(v)]
+            self.names[id(v)] = f"{arr}[{_ravel(self.coords[id(v)], oshape)}]"
+            self.masks[id(v)] = frozenset()
+            return
+        if op == "bcast":
+            self.names[id(v)] = self.names[id(args[0])]
+            self.types[id(v)] = self.types[id(args[0])]
+            self.masks[id(v)] = self.masks.get(id(args[0]), frozenset())
+            return
+        if op in ("zeros", "full"):
+            t = self.dtype_name(args[-1])
+            fill = 0.0 if op == "zeros" else args[1]
+            self.define(v, t, self.operand(self.ctx_const(fill), t))
+            self.masks[id(v)] = frozenset()
+            return
+        super().emit(v)
+        m = frozenset()
+        for a in _value_operands(v):
+            m |= self.masks.get(id(a), frozenset())
+        self.masks[id(v)] = m
+
+    def mask_of(self, v):
+        m = sorted(self.masks.get(id(v), frozenset()))
+        return " && ".join(f"({x} >= 0)" for x in m) if m else None
+
+
+def _analyse_tile(ctx):
+    program = ctx.program
+    if program.loops:
         return None
-    stores, values = found
-    return GenericPlan(ctx, stores, values)
+    stores = program.stores
+    values = _walk(list(stores.values()))
+    if not stores:
+        return None
+    for v in values:
+        if v.op not in _TILE_ALLOWED:
+            return None
+        if v.op in ("load", "offsets") and v.args[0].op != "param":
+            return None
+    loaded = {v.args[0].args[0] for v in values if v.op in ("load", "offsets")}
+    tensors = [n for n in list(stores) + sorted(loaded) if ctx.params[n].source_ndim != 0]
+    for n in stores:
+        if ctx.params[n].source_ndim == 0:
+            return None
+    if set(stores) & loaded:
+        raise LoweringError("the generic tile kernels do not update a tensor they also read")
+    for n in tensors:
+        if len(ctx.views[n].level_shapes) > 2:
+            raise LoweringError(f"`{n}` has {len(ctx.views[n].level_shapes)} levels; the generic tile kernels take 2")
+    # one flat program id, unravelled by every tensor over its own outermost level
+    if len({int(np.prod(ctx.views[n].level_shapes[0])) for n in tensors}) > 1:
+        raise LoweringError("the arranged tensors have different numbers of programs")
+    return stores, values
+
+
+class TilePlan(GenericPlan):
+    """A bound generic tile program (see the section comment above)."""
+
+    family = "generic"
+
+    def __init__(self, ctx, stores, values):
+        self.ctx = ctx
+        self.stores = stores
+        probe = _Emitter(ctx)
+        self.shapes = _shapes(ctx, values, probe.const_value)
+        self.types = {}
+        self.outputs = list(stores)
+        self.kernel_name = "nt_generic_tile"
+        grid = tuple(ctx.views[self.outputs[0]].level_shapes[0])
+        self.programs = int(np.prod(grid)) if grid else 1
+        self.lds = {}
+        em = _TileEmitter(self)
+        blocks, lds_bytes, decls = [], 0, []
+        reductions = [v for v in values if v.op == "reduce"]
+        for k, r in enumerate(reductions):
+            kind, operand, axis = r.args
+            sshape = self.shapes[id(operand)]
+            oshape = self.shapes[id(r)]
+            if axis is None:
+                n_out, extent = 1, int(np.prod(sshape)) if sshape else 1
+            else:
+                ax = axis + len(sshape) if axis < 0 else axis
+                n_out, extent = int(np.prod(oshape)) if oshape else 1, sshape[ax]
+            # operand coordinates from (o, l)
+            if axis is None:
+                coords = _unravel("l", sshape)
+            else:
+                oc = list(_unravel("o", oshape))
+                coords = tuple(oc[:ax] + ["l"] + oc[ax:])
+            body = em.context(operand, coords, f"r{k}_")
+            t = em.type_of(operand)
+            t = "float32" if t in ("weak", "bool") else t
+            if kind == "sum" and t in ("int8", "int16", "uint8"):
+                t = "int32"
+            w = em.work(t)
+            if w == "bool":
+                raise LoweringError("reductions of booleans are not supported")
+            ident, comb = self._combine(kind, t, w)
+            val = em.operand(operand, t)
+            mask = em.mask_of(operand)
+            term = f"({mask}) ? {val} : {ident}" if mask else val
+            lanes = 1 if n_out >= 256 else min(64, 1 << int(np.log2(256 // n_out)))
+            lanes = max(1, min(lanes, 1 << int(np.ceil(np.log2(max(extent, 1))))))
+            step = 256 // lanes
+            o_pad = -(-n_out // step) * step
+            arr = f"red{k}"
+            decls.append(f"  __shared__ {w} {arr}[{max(n_out, 1)}];")
+            lds_bytes += max(n_out, 1) * (8 if w in ("double", "long long") else 4)
+            self.lds[id(r)] = (arr, oshape)
+            self.types[id(r)] = t
+            blocks.append("\n".join([
+                f"    {{  // {kind} over {'all axes' if axis is None else f'axis {axis}'}: {n_out} x {extent}",
+                f"      const int g = tid % {lanes};",
+                f"      for (int o = tid / {lanes}; o < {o_pad}; o += {step}) {{",
+                f"        {w} acc = {ident};",
+                f"        if (o < {n_out}) {{",
+                f"          for (long long l = g; l < {extent}LL; l += {lanes}) {{",
+                *["    " + x for x in body],
+                f"            acc = {comb.format(a='acc', b=f'({term})')};",
+                "          }",
+                "        }",
+                *([f"        for (int s = {lanes // 2}; s > 0; s >>= 1) "
+                   f"acc = {comb.format(a='acc', b='__shfl_xor(acc, s, 64)')};"] if lanes > 1 else []),
+                f"        if (g == 0 && o < {n_out}) {arr}[o] = {em.round_to(t, 'acc')};",
+                "      }",
+                "    }",
+                "    __syncthreads();",
+            ]))
+        if lds_bytes > LDS_BYTES:
+            raise LoweringError(f"the reductions of this program need {lds_bytes} bytes of LDS (at most {LDS_BYTES})")
+        for out, v in stores.items():
+            tshape = _tile_shape(ctx, out)
+            sv = self.shapes[id(v)]
+            if _bcast_shapes(sv, tshape) != tshape:
+                raise LoweringError(f"a value of shape {sv} is stored to a tile of shape {tshape}")
+            n_tile = int(np.prod(tshape)) if tshape else 1
+            oc = _unravel("j", tshape)
+            body = em.context(v, oc[len(oc) - len(sv):] if sv else (), f"s{out}_")
+            t = _torch_dtype_name(ctx.dtypes[out])
+            src = em.type_of(v)
+            src = "float32" if src == "weak" else src
+            val = em.operand(v, src) if v.op in ("const", "shape", "source_shape") else em.names[id(v)]
+            if em.work(src) != em.work(t):
+                val = f"(({em.work(t)}){val})"
+            blocks.append("\n".join([
+                f"    for (long long j = tid; j < {n_tile}LL; j += 256) {{",
+                f"      const int oi = {self.index_expr(out, 'j')};",
+                "      if (oi < 0) continue;",
+                *body,
+                f"      p_{out}[oi] = {_STORAGE[t][3].format(val)};",
+                "    }",
+            ]))
+        self.loaded = sorted({v.args[0].args[0] for v in values if v.op == "load"
+                              and ctx.params[v.args[0].args[0]].source_ndim != 0})
+        self.scalars = [v.args[0].args[0] for v in values if v.op == "load"
+                        and ctx.params[v.args[0].args[0]].source_ndim == 0]
+        self.scalars = list(dict.fromkeys(self.scalars))
+        self.offsets = sorted({(v.args[0].args[0], int(v.args[1])) for v in values if v.op == "offsets"})
+        self.index_names = list(dict.fromkeys(self.outputs + self.loaded))
+        self.tile_sizes = {n: int(np.prod(_tile_shape(ctx, n))) if _tile_shape(ctx, n) else 1
+                           for n in set(self.index_names) | {n for n, _ in self.offsets}}
+        self.scalar_types = {n: em.scalar_type(n) for n in self.scalars}
+        params = [f"const int* __restrict__ t_{n}" for n in self.index_names]
+        params += [f"const int* __restrict__ f_{n}_{d}" for n, d in self.offsets]
+        params += [f"const {_STORAGE[_torch_dtype_name(ctx.dtypes[n])][0]}* __restrict__ p_{n}" for n in self.loaded]
+        params += [f"{_STORAGE[_torch_dtype_name(ctx.dtypes[n])][0]}* __restrict__ p_{n}" for n in self.outputs]
+        params += [f"{_STORAGE[self.scalar_types[n]][0]} s_{n}" for n in self.scalars]
+        params.append("long long programs")
+        self.params = params
+        self.decls = decls
+        self.blocks = blocks
+
+    def index_expr(self, name, lin):
+        return f"t_{name}[pb_{name} + {lin}]"
+
+    @staticmethod
+    def _combine(kind, t, w):
+        if kind == "sum":
+            return ("0" if w == "long long" else ("0.0" if w == "double" else "0.0f")), "({a} + {b})"
+        lo, hi = _INT_LIMITS.get(t, (None, None))
+        if w == "long long":
+            ident = f"{lo}LL" if kind == "max" else f"{hi}LL"
+            if t == "int64":
+                ident = "(-9223372036854775807LL - 1)" if kind == "max" else "9223372036854775807LL"
+            return ident, ("({b} > {a} ? {b} : {a})" if kind == "max" else "({b} < {a} ? {b} : {a})")
+        inf = "__builtin_huge_val()" if w == "double" else "__builtin_huge_valf()"
+        f = ("fmax" if kind == "max" else "fmin") + ("" if w == "double" else "f")
+        return (f"(-{inf})" if kind == "max" else inf), f + "({a}, {b})"
+
+    def source(self, linear=None, linear_offsets=()):
+        bases = [f"    const long long pb_{n} = p * {self.tile_sizes[n]}LL;" for n in self.tile_sizes]
+        return (
+            _PRELUDE
+            + f'\nextern "C" __global__ void __launch_bounds__(256) {self.kernel_name}({", ".join(self.params)}) {{\n'
+            + "\n".join(self.decls) + "\n"
+            + "  const int tid = threadIdx.x;\n"
+            + "  for (long long p = blockIdx.x; p < programs; p += gridDim.x) {\n"
+            + "\n".join(bases + self.blocks)
+            + "\n    __syncthreads();\n  }\n}\n"
+        )
+
+    def describe(self):
+        return {"family": self.family, "outputs": self.outputs, "inputs": self.loaded, "scalars": self.scalars,
+                "reductions": len(self.lds)}
+
+    def bind(self, values, index):
+        import torch
+
+        device = values[self.outputs[0]].device
+        tables, offset_tables, maps = {}, {}, {}
+        for n in self.index_names:
+            maps[n] = self._maps(n)
+            tab, _ = self._table(n, values[n], maps[n])
+            tables[n] = torch.from_numpy(tab).to(device)
+        for n, d in self.offsets:
+            offset_tables[(n, d)] = torch.from_numpy(self._offsets_table(n, d, maps.get(n))).to(device)
+        fn = self.function(self.source())
+        ptrs = {n: ctypes.c_void_p() for n in self.index_names}
+        argv = [ctypes.c_void_p(tables[n].data_ptr()) for n in self.index_names]
+        argv += [ctypes.c_void_p(offset_tables[k].data_ptr()) for k in self.offsets]
+        argv += [ptrs[n] for n in self.loaded]
+        argv += [ptrs[n] for n in self.outputs]
+        svals = {n: ctypes.c_int64() if self.scalar_types[n] == "int64" else ctypes.c_float() for n in self.scalars}
+        argv += [svals[n] for n in self.scalars]
+        argv.append(ctypes.c_int64(self.programs))
+        params = (ctypes.c_void_p * len(argv))(*[ctypes.addressof(a) for a in argv])
+        grid = min(self.programs, 256 * 64)
+        lib = _lib.load()
+        positions = {n: index[n] for n in self.index_names}
+        spos = {n: index[n] for n in self.scalars}
+
+        def launch(args):
+            for n, p in positions.items():
+                ptrs[n].value = args[p].data_ptr()
+            for n, p in spos.items():
+                v = args[p]
+                v = v.item() if hasattr(v, "item") else v
+                svals[n].value = int(v) if self.scalar_types[n] == "int64" else float(v)
+            status = lib.nt_rtc_launch(fn, grid, 256, params, ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream))
+            if status != 0:
+                raise KernelLaunchError(status)
+
+        launch.keep = (tables, offset_tables, argv, params)
+        return launch
+
+
+def match_generic(ctx):
+    """A generic kernel for the program, or None when it is neither element-parallel nor a tile program."""
+    found = _analyse(ctx)
+    if found is not None:
+        return GenericPlan(ctx, *found)
+    found = _analyse_tile(ctx)
+    if found is not None:
+        return TilePlan(ctx, *found)
+    return None

@@ -378,3 +378,197 @@ def test_random_streams_match_the_oracle(seed):
     assert np.array_equal(of.cpu().numpy(), philox.rand(seed, offs))
     _rng_kernel(app_randn)(seed, of)
     assert np.allclose(of.cpu().numpy(), philox.randn(seed, offs), atol=1e-5, rtol=1e-5)
+
+
+# ------------------------------------------------------------------ tile programs with reductions
+# The reduction programs of reference tests/test_triton_reduction_schedule.py:18-119,
+# test_cuda_reduction_schedule.py:114-187 and test_triton_block_reductions.py:17-140.
+WIDTH = Symbol("WIDTH", constexpr=True)
+HEIGHT = Symbol("HEIGHT", constexpr=True)
+
+
+def row_arrangement(x, out, WIDTH=WIDTH):
+    return x.tile((1, WIDTH)), out.tile((1, WIDTH))
+
+
+def row_reduced_arrangement(x, out, WIDTH=WIDTH):
+    return x.tile((1, WIDTH)), out.tile((1,))
+
+
+def column_arrangement(x, out, HEIGHT=HEIGHT):
+    return x.tile((HEIGHT, 1)), out.tile((HEIGHT, 1))
+
+
+def row_normalize(x, out):
+    maximum = ntl.max(x, axis=1)
+    numerator = ntl.exp(x - maximum[:, None])
+    out = numerator / ntl.sum(numerator, axis=1)[:, None]  # noqa: F841
+
+
+def row_layernorm(x, out):
+    width = x.shape[1]
+    mean = ntl.sum(x, axis=1) / width
+    mean_square = ntl.sum(x * x, axis=1) / width
+    variance = mean_square - mean * mean
+    out = (x - mean[:, None]) * ntl.rsqrt(variance[:, None] + 1e-5)  # noqa: F841
+
+
+def row_min(x, out):
+    out = ntl.min(x, axis=1)  # noqa: F841
+
+
+def row_sum(x, out):
+    out = ntl.sum(x, axis=1)  # noqa: F841
+
+
+def column_max_broadcast(x, out):
+    out = x + ntl.max(x, axis=0)[None, :]  # noqa: F841
+
+
+def middle_axis_sum(x, out):
+    out = ntl.sum(x, axis=1)  # noqa: F841
+
+
+def separate_reduction_outputs(x, rows, columns):
+    rows = ntl.sum(x, axis=1)  # noqa: F841
+    columns = ntl.max(x, axis=0)  # noqa: F841
+
+
+def block_arrangement(x, out):
+    x = x.tile((1, -1, -1))
+    x.dtype = x.dtype.squeeze(0)
+    out = out.tile((1, -1))
+    out.dtype = out.dtype.squeeze(0)
+    return x, out
+
+
+def block_application(x, out):
+    weights = ntl.sum(x, axis=1)
+    out = ntl.sum(x * weights[:, None], axis=0)  # noqa: F841
+
+
+def independent_arrangement(x, y, out):
+    return x.tile((-1,)), y.tile((-1,)), out.tile((-1,))
+
+
+def independent_application(x, y, out):
+    out = x + ntl.sum(y, axis=0)  # noqa: F841
+
+
+def _reduce_kernel(arrangement, application, *ndims, dtype=None):
+    return ninetoothed.make(arrangement, application, tuple(Tensor(n, dtype=dtype) for n in ndims))
+
+
+def test_tile_programs_compile():
+    cases = ((row_reduced_arrangement, row_min, (2, 1), ((37, 127), (37,)), {"WIDTH": 127}),
+             (row_arrangement, row_normalize, (2, 2), ((41, 781), (41, 781)), {"WIDTH": 781}),
+             (row_arrangement, row_layernorm, (2, 2), ((29, 1127), (29, 1127)), {"WIDTH": 1127}),
+             (column_arrangement, column_max_broadcast, (2, 2), ((193, 41), (193, 41)), {"HEIGHT": 193}),
+             (block_arrangement, block_application, (3, 2), ((3, 8, 16), (3, 16)), {}))
+    for arrangement, application, ndims, shapes, meta in cases:
+        h = _reduce_kernel(arrangement, application, *ndims)
+        plan = _plan(h, *(torch.empty(s) for s in shapes), **meta)
+        assert plan.describe()["family"] == "generic" and plan.describe()["reductions"] >= 1
+        assert len(GenericPlan.compile(plan.source())) > 1000
+
+
+def test_tile_program_rejections():
+    def inplace(x, out):
+        x = x - ntl.max(x, axis=1)[:, None]  # noqa: F841
+        out = x  # noqa: F841
+
+    h = _reduce_kernel(row_arrangement, inplace, 2, 2)
+    with pytest.raises(ninetoothed.LoweringError, match="update a tensor they also read"):
+        _plan(h, torch.empty(4, 8), torch.empty(4, 8), WIDTH=8)
+
+
+@pytest.mark.gpu
+def test_cooperative_reduction_reference_cases():
+    # reference tests/test_cuda_reduction_schedule.py:114-187 (backend-neutral programs, same data shapes)
+    f32, f16, bf16 = ninetoothed.float32, ninetoothed.float16, ninetoothed.bfloat16
+    reduce_min = _reduce_kernel(row_reduced_arrangement, row_min, 2, 1, dtype=f32)
+    base = torch.randn((37, 254), device="cuda")
+    x = base[:, ::2]
+    output = torch.empty((37,), device="cuda")
+    reduce_min(x, output, WIDTH=127)
+    torch.testing.assert_close(output, x.min(dim=1).values)
+
+    normalize = ninetoothed.make(row_arrangement, row_normalize, (Tensor(2, dtype=f16), Tensor(2, dtype=f16)))
+    x = torch.randn((41, 781), device="cuda", dtype=torch.float16)
+    output = torch.empty_like(x)
+    normalize(x, output, WIDTH=781)
+    torch.testing.assert_close(output, torch.softmax(x, dim=1), rtol=2e-3, atol=2e-3)
+
+    layernorm = ninetoothed.make(row_arrangement, row_layernorm, (Tensor(2, dtype=bf16), Tensor(2, dtype=bf16)))
+    x = torch.randn((29, 1127), device="cuda", dtype=torch.bfloat16)
+    output = torch.empty_like(x)
+    layernorm(x, output, WIDTH=1127)
+    torch.testing.assert_close(output, F.layer_norm(x, (1127,)), rtol=2e-2, atol=2e-2)
+
+    reduce_sum = _reduce_kernel(row_reduced_arrangement, row_sum, 2, 1, dtype=f32)
+    x = torch.randn((17, 4097), device="cuda")
+    output = torch.empty((17,), device="cuda")
+    reduce_sum(x, output, WIDTH=4097)
+    torch.testing.assert_close(output, x.sum(dim=1), rtol=1e-4, atol=1e-4)
+
+    column_max = _reduce_kernel(column_arrangement, column_max_broadcast, 2, 2, dtype=f32)
+    x = torch.randn((193, 41), device="cuda")
+    output = torch.empty_like(x)
+    column_max(x, output, HEIGHT=193)
+    torch.testing.assert_close(output, x + x.max(dim=0).values)
+
+    x = torch.empty((0, 127), device="cuda", dtype=torch.float16)
+    output = torch.empty_like(x)
+    normalize(x, output, WIDTH=127)
+    assert output.numel() == 0
+
+
+@pytest.mark.gpu
+def test_block_reduction_reference_cases():
+    # reference tests/test_triton_block_reductions.py:82-140
+    shape = (3, 8, 16)
+    x = torch.randn((*shape[:-1], shape[-1] * 2), device="cuda")[..., ::2]
+    output = torch.empty((shape[0], shape[2]), device="cuda")
+    _reduce_kernel(block_arrangement, block_application, 3, 2)(x, output)
+    expected = (x.double() * x.double().sum(dim=2, keepdim=True)).sum(dim=1)
+    torch.testing.assert_close(output, expected.float(), rtol=2e-5, atol=2e-5)
+
+    x = torch.zeros(8, device="cuda")
+    y = torch.arange(16, device="cuda", dtype=torch.float32)
+    out = torch.empty_like(x)
+    ninetoothed.make(independent_arrangement, independent_application, (Tensor(1), Tensor(1), Tensor(1)))(x, y, out)
+    torch.testing.assert_close(out, torch.full_like(out, 120), rtol=0, atol=0)
+
+
+def mixed_outer_reductions(x, y, out_x, out_y):
+    out_x = ntl.sum(x, axis=1)  # noqa: F841
+    out_y = ntl.sum(y, axis=1)  # noqa: F841
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", (torch.float16, torch.float32))
+def test_more_reduction_programs(dtype):
+    # the other programs of reference tests/test_triton_reduction_schedule.py:43-109
+    tol = 1e-2 if dtype == torch.float16 else 1e-5
+    x = torch.randn((4, 8), device="cuda").to(dtype)
+    rows = torch.empty(4, device="cuda", dtype=dtype)
+    cols = torch.empty(8, device="cuda", dtype=dtype)
+    ninetoothed.make(lambda x, r, c: (x.tile((4, 8)), r.tile((4,)), c.tile((8,))), separate_reduction_outputs,
+                     (Tensor(2), Tensor(1), Tensor(1)))(x, rows, cols)
+    torch.testing.assert_close(rows.float(), x.float().sum(dim=1), rtol=tol, atol=tol)
+    assert torch.equal(cols, x.max(dim=0).values)
+
+    x, y = torch.randn((5, 7), device="cuda").to(dtype), torch.randn((5, 7), device="cuda").to(dtype)
+    ox, oy = torch.empty(5, device="cuda", dtype=dtype), torch.empty(5, device="cuda", dtype=dtype)
+    ninetoothed.make(lambda x, y, a, b: (x.tile((1, 7)), y.tile((1, 7)), a.tile((1,)), b.tile((1,))),
+                     mixed_outer_reductions, (Tensor(2), Tensor(2), Tensor(1), Tensor(1)))(x, y, ox, oy)
+    torch.testing.assert_close(ox.float(), x.float().sum(dim=1), rtol=tol, atol=tol)
+    torch.testing.assert_close(oy.float(), y.float().sum(dim=1), rtol=tol, atol=tol)
+
+    k = ninetoothed.make(lambda x, o: (x.tile((2, 3, 5)), o.tile((2, 5))), middle_axis_sum, (Tensor(3), Tensor(2)))
+    out = torch.empty((6, 10), device="cuda", dtype=dtype)
+    with pytest.raises(ninetoothed.LoweringError):
+        k(torch.randn((6, 9, 10), device="cuda").to(dtype), out)  # 18 programs for x against 6 for out
+    x = torch.randn((6, 3, 10), device="cuda").to(dtype)
+    k(x, out)
+    torch.testing.assert_close(out.float(), x.float().sum(dim=1), rtol=tol, atol=tol)
