@@ -103,15 +103,25 @@ def test_elementwise_program_outside_the_families_is_generic():
     assert _specialize(h, torch.empty(10), torch.empty(10), torch.empty(10))["family"] == "generic"
 
 
-def test_unsupported_reduction_is_rejected():
+def test_reduction_program_is_generic():
     def app(lhs, rhs, output):
         output = ntl.sum(lhs, 0) + rhs  # noqa: F841
 
     bs = Symbol("BS", meta=True)
     h = ninetoothed.make(lambda a, b, c: (a.tile((bs,)), b.tile((bs,)), c.tile((bs,))), app,
                          (Tensor(1), Tensor(1), Tensor(1)))
+    assert _specialize(h, torch.empty(10), torch.empty(10), torch.empty(10))["family"] == "generic"
+
+
+def test_unsupported_program_is_rejected():
+    # a block product without the k loop of a matmul: neither the GEMM family nor the generic kernels
+    def app(lhs, rhs, output):
+        output = ntl.dot(lhs, rhs)  # noqa: F841
+
+    h = ninetoothed.make(lambda a, b, c: (a.tile((16, 16)), b.tile((16, 16)), c.tile((16, 16))), app,
+                         (Tensor(2), Tensor(2), Tensor(2)))
     with pytest.raises(LoweringError, match="matches none"):
-        _specialize(h, torch.empty(10), torch.empty(10), torch.empty(10))
+        _specialize(h, _h((16, 16)), _h((16, 16)), _h((16, 16)))
 
 
 def test_data_dependent_if_is_rejected():
