@@ -54,6 +54,7 @@ class ParamSpec:
     dtype: object
     constexpr: bool
     shape_symbols: tuple  # (symbol name or None) per source dim
+    constexpr_value: object = None  # fixed at definition (``Tensor(0, constexpr=True, value=...)``)
 
 
 @dataclass
@@ -66,7 +67,12 @@ class Compilation:
 
 
 class KernelProgram:
-    """The arranged program, ready to be specialised at call time."""
+    """The arranged program, ready to be specialised at call time.
+
+    The application is lowered once per set of constexpr values (their `if`s fold) and the
+    lowered programs are cached; a program rebuilt from a built artifact (``from_bundle``)
+    carries those lowered programs and needs the application only for constexpr values it
+    was not built with (then it imports it by module and qualified name, if it can)."""
 
     def __init__(self, request, params, arranged, specs, symbols, granularity, outputs):
         self.request = request
@@ -77,6 +83,87 @@ class KernelProgram:
         self.symbols = symbols  # name -> Symbol (meta/constexpr flags)
         self.granularity = granularity
         self.outputs = outputs
+        self.application = request.application
+        self.application_ref = _application_ref(request.application)
+        self._lowered = {}
+
+    # ------------------------------------------------------------ built artifacts
+    def bundle(self):
+        """Everything call-time specialisation needs, as picklable data (no application)."""
+        return {"name": self.name, "params": self.params, "arranged": self.arranged, "specs": self.param_specs,
+                "symbols": self.symbols, "granularity": self.granularity, "outputs": self.outputs,
+                "lowered": dict(self._lowered), "application_ref": self.application_ref}
+
+    @classmethod
+    def from_bundle(cls, bundle):
+        self = cls.__new__(cls)
+        self.request = None
+        self.name = bundle["name"]
+        self.params = bundle["params"]
+        self.arranged = bundle["arranged"]
+        self.param_specs = bundle["specs"]
+        self.symbols = bundle["symbols"]
+        self.granularity = bundle["granularity"]
+        self.outputs = bundle["outputs"]
+        self.application = None
+        self.application_ref = bundle["application_ref"]
+        self._lowered = dict(bundle["lowered"])
+        return self
+
+    def infos(self, public=None):
+        """ParamInfo per parameter; constexpr values from ``public`` or fixed at definition."""
+        infos = []
+        for spec in self.param_specs:
+            if spec.source_ndim == 0:
+                value = public[spec.name] if public is not None and spec.name in public else spec.constexpr_value
+                infos.append(frontend.ParamInfo(spec.name, (), 0, spec.constexpr,
+                                                _plain(value) if spec.constexpr else None))
+            else:
+                infos.append(frontend.ParamInfo(spec.name, spec.level_ndims, spec.source_ndim))
+        return infos
+
+    def lowered(self, infos):
+        key = tuple((i.name, repr(i.constexpr_value)) for i in infos if i.constexpr)
+        program = self._lowered.get(key)
+        if program is None:
+            application = self.application or _import_application(self.application_ref)
+            if application is None:
+                raise LoweringError(
+                    f"`{self.name}` was built for constexpr values {[dict(k) for k in self._lowered] or 'none'}; "
+                    f"{dict(key)} needs its application, which cannot be imported"
+                )
+            program = frontend.lower(application, infos)
+            self._lowered[key] = program
+        return program
+
+    def prelower(self):
+        """Lower for the constexpr values fixed at definition (all of them, or nothing)."""
+        if all(s.constexpr_value is not None for s in self.param_specs if s.constexpr):
+            self.lowered(self.infos())
+
+    def static_values(self):
+        """Meta-device stand-ins for a call, when every shape and dtype is fixed at definition."""
+        import torch
+
+        from ninetoothed_amd.dtype import normalize_dtype
+
+        public = {}
+        for spec in self.param_specs:
+            if spec.source_ndim == 0:
+                if spec.constexpr:
+                    if spec.constexpr_value is None:
+                        return None
+                    public[spec.name] = spec.constexpr_value
+                else:
+                    public[spec.name] = 0.0
+                continue
+            if spec.dtype is None or any(s is None for s in spec.static_shape):
+                return None
+            dtype = getattr(torch, normalize_dtype(spec.dtype), None)
+            if dtype is None:
+                return None
+            public[spec.name] = torch.empty(spec.static_shape, dtype=dtype, device="meta")
+        return public
 
     @property
     def meta_args(self):
@@ -107,19 +194,15 @@ class KernelProgram:
 
     def specialize(self, public, meta):
         env = self.environment(public, meta)
-        views, infos, dtypes = {}, [], {}
+        views, dtypes = {}, {}
         for spec in self.param_specs:
-            value = public[spec.name]
             if spec.source_ndim == 0:
                 views[spec.name] = None
-                infos.append(frontend.ParamInfo(spec.name, (), 0, spec.constexpr,
-                                                _plain(value) if spec.constexpr else None))
                 continue
-            view = BoundView(self.arranged[spec.name], env)
-            views[spec.name] = view
-            dtypes[spec.name] = value.dtype
-            infos.append(frontend.ParamInfo(spec.name, tuple(len(s) for s in view.level_shapes[1:]), spec.source_ndim))
-        program = frontend.lower(self.request.application, infos)
+            views[spec.name] = BoundView(self.arranged[spec.name], env)
+            dtypes[spec.name] = public[spec.name].dtype
+        infos = self.infos(public)
+        program = self.lowered(infos)
         ctx = families.CallContext(program, views, public, {i.name: i for i in infos}, dtypes)
         return families.select(ctx)
 
@@ -128,6 +211,28 @@ def _plain(v):
     if hasattr(v, "item"):
         return v.item()
     return v
+
+
+def _application_ref(application):
+    """(module, qualified name) of an importable application, else None."""
+    module, qualname = getattr(application, "__module__", None), getattr(application, "__qualname__", "")
+    if not module or "<" in qualname:
+        return None
+    return module, qualname
+
+
+def _import_application(ref):
+    if ref is None:
+        return None
+    import importlib
+
+    try:
+        obj = importlib.import_module(ref[0])
+        for part in ref[1].split("."):
+            obj = getattr(obj, part)
+    except (ImportError, AttributeError):
+        return None
+    return obj
 
 
 def _arrangement_from_annotations(application):
@@ -229,6 +334,7 @@ def compile_kernel(request):
             dtype=source.dtype if isinstance(source.dtype, str) else None,
             constexpr=bool(source.constexpr),
             shape_symbols=_shape_symbol_names(source),
+            constexpr_value=source.value if source.constexpr else None,
         ))
         if source.ndim:
             symbols.update(t.symbols())
@@ -250,15 +356,29 @@ class Compiler:
     def compile(self, request):
         return compile_kernel(request)
 
-    def materialize(self, request):
-        compilation = self.compile(request)
+    def materialize(self, request, *, output_dir=None, mode=None):
+        """A Handle for a CompileRequest or an existing Compilation (reference
+        ``compiler/runtime.py:1450-1472``): ``mode`` "jit" or "aot" (default: "jit" for
+        ``caller="torch"``, else "aot"); AOT needs an output directory."""
+        compilation = request if isinstance(request, Compilation) else self.compile(request)
+        req = compilation.request
+        output_dir = output_dir if output_dir is not None else req.output_dir
         materializer = materializer_for(compilation.target.backend)
-        mode = "jit" if request.caller == "torch" else "aot"
+        if mode is None:
+            mode = "jit" if req.caller == "torch" else "aot"
         if mode == "aot":
-            if request.output_dir is None:
+            if output_dir is None:
                 raise ValueError("AOT materialization requires an output directory.")
-            return materializer.aot_build(compilation, output_dir=request.output_dir)
-        return materializer.jit_materialize(compilation, output_dir=request.output_dir)
+            return materializer.aot_build(compilation, output_dir=output_dir)
+        if mode != "jit":
+            raise ValueError(f"Unknown materialization mode `{mode}`.")
+        return materializer.jit_materialize(compilation, output_dir=output_dir)
+
+
+def load_built_artifact(built):
+    """Reload a Handle from a built artifact without the application (reference
+    ``compiler/runtime.py:1475-1481``)."""
+    return materializer_for(built.source.backend).load_built_artifact(built)
 
 
 DEFAULT_COMPILER = Compiler()

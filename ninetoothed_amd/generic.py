@@ -408,6 +408,7 @@ class GenericPlan:
     family = "generic"
     _lock = threading.Lock()
     _functions = {}  # source digest -> loaded kernel handle
+    _blobs = {}  # source digest -> code object (compiled here, or carried by a built artifact)
 
     def __init__(self, ctx, stores, values):
         self.ctx = ctx
@@ -488,12 +489,35 @@ class GenericPlan:
         finally:
             lib.nt_rtc_free(code)
 
+    @staticmethod
+    def digest(source):
+        return hashlib.sha256(source.encode()).hexdigest()
+
+    @classmethod
+    def code_object(cls, source):
+        """The code object of ``source``: from the cache, else compiled (needs no GPU)."""
+        digest = cls.digest(source)
+        with cls._lock:
+            blob = cls._blobs.get(digest)
+        if blob is None:
+            blob = cls.compile(source)
+            with cls._lock:
+                cls._blobs[digest] = blob
+        return blob
+
+    def sources_for(self, values):
+        """The kernel sources a call with ``values`` runs (strides decide the index tables)."""
+        if not self.index_names:
+            return []
+        linear, linear_offsets = self._layout(values)[1:3]
+        return [self.source(linear, linear_offsets)]
+
     def function(self, source):
-        digest = hashlib.sha256(source.encode()).hexdigest()
+        digest = self.digest(source)
+        blob = self.code_object(source)
         with self._lock:
             fn = self._functions.get(digest)
             if fn is None:
-                blob = self.compile(source)
                 handle = ctypes.c_void_p()
                 buf = ctypes.create_string_buffer(blob, len(blob))
                 status = _lib.load().nt_rtc_load(buf, self.kernel_name.encode(), ctypes.byref(handle))
@@ -532,19 +556,13 @@ class GenericPlan:
             raise LoweringError("the generic kernels take offsets within 32 bits")
         return q.astype(np.int32)
 
-    def bind(self, values, index):
-        import torch
-
-        if not self.index_names:  # nothing is stored: the program has no effect
-            return lambda args: None
-        device = None
-        tables, linear, total = {}, {}, None
-        maps = {}
+    def _layout(self, values):
+        """Host index tables, the tensors walked linearly (no table), offsets tables, and the
+        size of the index space."""
+        tables, linear, total, maps = {}, {}, None, {}
         for n in self.index_names:
-            t = values[n]
-            device = t.device
             maps[n] = self._maps(n)
-            tab, tot = self._table(n, t, maps[n])
+            tab, tot = self._table(n, values[n], maps[n])
             if total is not None and tot != total:
                 raise LoweringError("generic kernel operands do not share one index space")
             total = tot
@@ -552,7 +570,7 @@ class GenericPlan:
             if np.array_equal(tab[:valid], np.arange(valid, dtype=np.int32)) and not np.any(tab[valid:] >= 0):
                 linear[n] = valid  # e -> e, masked from `valid` on: no table
             else:
-                tables[n] = torch.from_numpy(tab).to(device)
+                tables[n] = tab
         offset_tables, linear_offsets = {}, set()
         for n, d in self.offsets:
             q = self._offsets_table(n, d, maps.get(n))
@@ -561,7 +579,18 @@ class GenericPlan:
             if np.array_equal(q, np.arange(q.size, dtype=np.int32)):
                 linear_offsets.add((n, d))
             else:
-                offset_tables[(n, d)] = torch.from_numpy(q).to(device)
+                offset_tables[(n, d)] = q
+        return tables, linear, linear_offsets, offset_tables, total
+
+    def bind(self, values, index):
+        import torch
+
+        if not self.index_names:  # nothing is stored: the program has no effect
+            return lambda args: None
+        host_tables, linear, linear_offsets, host_offsets, total = self._layout(values)
+        device = values[self.index_names[0]].device
+        tables = {n: torch.from_numpy(t).to(device) for n, t in host_tables.items()}
+        offset_tables = {k: torch.from_numpy(q).to(device) for k, q in host_offsets.items()}
         fn = self.function(self.source(linear, linear_offsets))
         ptrs = {n: ctypes.c_void_p() for n in self.index_names}
         argv = [ctypes.c_void_p(tables[n].data_ptr() if n in tables else None) for n in self.index_names]
@@ -942,6 +971,9 @@ class TilePlan(GenericPlan):
 
     def index_expr(self, name, lin):
         return f"t_{name}[pb_{name} + {lin}]"
+
+    def sources_for(self, values):
+        return [self.source()]
 
     @staticmethod
     def _combine(kind, t, w):
