@@ -789,6 +789,81 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g) {
   }
 }
 
+// fp32 GEMMs of at most a few hundred 32 x 32 tiles (e.g. 512^3): one tile per
+// workgroup of sixteen waves, each wave multiplying a sixteenth of K with its operands
+// loaded straight into registers (one load phase, all loads in flight together), then
+// the sixteen partial tiles summed through LDS.  MFMA step s of a 32-deep k chunk uses
+// k = 8 t + s in lane group t (the sum is over all k, so any bijection will do), so a
+// lane's a values for the chunk are eight consecutive floats of one row.
+constexpr int F32S_WAVES = 16;
+template <bool AVEC>
+__global__ __launch_bounds__(1024) void gemm_f32_splitk_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(16))) float part[F32S_WAVES * F32_TM * F32_TN];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tm = blockIdx.x / g.tiles_n, tn = blockIdx.x % g.tiles_n;
+  const int64_t m0 = (int64_t)tm * F32_TM, n0 = (int64_t)tn * F32_TN;
+  const float* A = (const float*)g.a;
+  const float* B = (const float*)g.b;
+  const int r16 = lane & 15, t = lane >> 4;
+  const int64_t chunks = (g.K + 31) / 32;
+  const int64_t per = (chunks + F32S_WAVES - 1) / F32S_WAVES;
+  const int64_t c_lo = wave * per, c_hi = min(chunks, c_lo + per);
+  floatx4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int64_t ch = c_lo; ch < c_hi; ++ch) {
+    const int64_t kb = ch * 32 + 8 * t;  // this lane group's eight k values: kb .. kb + 7
+    float a[2][8], b[2][8];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int64_t row = m0 + i * 16 + r16;
+      if (AVEC && row < g.M && kb + 8 <= g.K) {
+        const float4 lo = *(const float4*)(A + row * g.sa_m + kb);
+        const float4 hi = *(const float4*)(A + row * g.sa_m + kb + 4);
+        a[i][0] = lo.x; a[i][1] = lo.y; a[i][2] = lo.z; a[i][3] = lo.w;
+        a[i][4] = hi.x; a[i][5] = hi.y; a[i][6] = hi.z; a[i][7] = hi.w;
+      } else {
+#pragma unroll
+        for (int s = 0; s < 8; ++s) a[i][s] = (row < g.M && kb + s < g.K) ? A[row * g.sa_m + (kb + s) * g.sa_k] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t col = n0 + j * 16 + r16;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) b[j][s] = (col < g.N && kb + s < g.K) ? B[(kb + s) * g.sb_k + col * g.sb_n] : 0.f;
+    }
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][s], b[j][s], acc[i][j], 0, 0, 0);
+  }
+  // 16 x 16 blocks: lane l holds rows 4 (l / 16) + v, column l % 16.
+  float* mine = part + wave * (F32_TM * F32_TN);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) mine[(i * 16 + 4 * t + v) * F32_TN + j * 16 + r16] = acc[i][j][v];
+  __syncthreads();
+  const int e = tid;  // one output element per lane
+  float sum = 0.f;
+#pragma unroll
+  for (int w = 0; w < F32S_WAVES; ++w) sum += part[w * (F32_TM * F32_TN) + e];
+  const int64_t row = m0 + e / F32_TN, col = n0 + e % F32_TN;
+  if (row < g.M && col < g.N) {
+    float v = g.alpha * round_through(sum, g.round_dtype);
+    if (g.c) v += g.beta * load_as_float(g.c, row * g.sc_m + col * g.sc_n, g.out_dtype);
+    store_from_float(g.out, row * g.so_m + col * g.so_n, g.out_dtype, v);
+  }
+}
+
 static int gemm_check(const GemmArgs& g) {
   if (g.M < 0 || g.N < 0 || g.K < 0) return NT_ERR_INVALID;
   if (!valid_dtype(g.out_dtype) || !valid_round(g.round_dtype)) return NT_ERR_INVALID;
@@ -873,6 +948,15 @@ static int gemm32_launch(GemmArgs g, hipStream_t stream) {
   if (tiles_m * tiles_n > 0x7fffffffLL) return NT_ERR_INVALID;
   g.tiles_m = (int)tiles_m;
   g.tiles_n = (int)tiles_n;
+  // At most two tiles per CU: the split-k kernel (its LDS tile sum replaces a second load phase).
+  if (tiles_m * tiles_n <= 512 && g.K >= 64) {
+    const bool avec = g.sa_k == 1 && g.sa_m % 4 == 0 && (uintptr_t)g.a % 16 == 0;
+    if (avec)
+      hipLaunchKernelGGL(gemm_f32_splitk_kernel<true>, dim3((unsigned)(tiles_m * tiles_n)), dim3(1024), 0, stream, g);
+    else
+      hipLaunchKernelGGL(gemm_f32_splitk_kernel<false>, dim3((unsigned)(tiles_m * tiles_n)), dim3(1024), 0, stream, g);
+    return launch_status();
+  }
   const bool vec = g.sa_k == 1 && g.sb_n == 1 && g.M % F32_TM == 0 && g.N % F32_TN == 0 && g.K % 4 == 0 &&
                    g.sa_m % 4 == 0 && g.sb_k % 4 == 0 && (uintptr_t)g.a % 16 == 0 && (uintptr_t)g.b % 16 == 0;
   if (vec)
