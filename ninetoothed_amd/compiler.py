@@ -192,7 +192,17 @@ class KernelProgram:
                 raise TypeError(f"No value for symbol `{name}`.")
         return env
 
-    def specialize(self, public, meta):
+    def specialize(self, public, meta, tune=False):
+        """The kernel plan for a call; with ``tune``, a ``TunedPlan`` over every fitting plan
+        when there are several and the program updates no tensor it reads."""
+        ctx = self.context(public, meta)
+        if tune and not families.updates_an_input(ctx.program):
+            plans = families.candidates(ctx)
+            if len(plans) > 1:
+                return families.TunedPlan(plans, namespace=f"{self.name}:{self.application_ref}")
+        return families.select(ctx)
+
+    def context(self, public, meta):
         env = self.environment(public, meta)
         views, dtypes = {}, {}
         for spec in self.param_specs:
@@ -203,8 +213,7 @@ class KernelProgram:
             dtypes[spec.name] = public[spec.name].dtype
         infos = self.infos(public)
         program = self.lowered(infos)
-        ctx = families.CallContext(program, views, public, {i.name: i for i in infos}, dtypes)
-        return families.select(ctx)
+        return families.CallContext(program, views, public, {i.name: i for i in infos}, dtypes)
 
 
 def _plain(v):

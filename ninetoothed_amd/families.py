@@ -952,6 +952,72 @@ def match_generic(ctx):
 FAMILIES = (match_attention, match_gemm, match_softmax, match_max_pool2d, match_add, match_generic)
 
 
+def candidates(ctx):
+    """Every family plan whose pattern and geometry fit, in the order ``select`` tries them."""
+    plans = []
+    for matcher in FAMILIES:
+        try:
+            plan = matcher(ctx)
+        except LoweringError:
+            plan = None
+        if plan is not None:
+            plans.append(plan)
+    return plans
+
+
+def updates_an_input(program):
+    """Whether the program stores to a tensor it also reads (re-running it changes the result)."""
+    read = set()
+    for value in program.stores.values():
+        for v in _walk(value):
+            if v.op in ("load", "offsets"):
+                t = v.args[0]
+                while t.op == "index":
+                    t = t.args[0]
+                read.add(t.args[0])
+    return bool(read & set(program.stores))
+
+
+class TunedPlan(Plan):
+    """Several fitting plans; each bound call picks the fastest with ``AutoTuner``."""
+
+    family = "tuned"
+
+    def __init__(self, plans, namespace):
+        self.plans = plans
+        self.namespace = namespace
+        self.chosen = {}
+
+    def bind(self, values, index):
+        import json
+
+        from ninetoothed_amd.auto_tuner import AutoTuner
+
+        bound, keys = [], []
+        for plan in self.plans:
+            try:
+                launch = plan.bind(values, index)
+            except (LoweringError, TypeError, ValueError):
+                continue
+            bound.append(launch)
+            keys.append(json.dumps(plan.describe(), sort_keys=True, default=str))
+        if not bound:
+            raise LoweringError("no candidate kernel accepts these arguments")
+        if len(bound) == 1:
+            return bound[0]
+        names = sorted(index, key=index.get)
+        args = tuple(values[n] for n in names)
+        funcs = [lambda *a, _launch=launch: _launch(a) for launch in bound]
+        tuner = AutoTuner(funcs, keys, cache_namespace=self.namespace)
+        best = tuner.best(*args)
+        self.chosen[tuner._make_arg_key(args, {})] = best
+        return bound[keys.index(best)]
+
+    def describe(self):
+        return {"family": "tuned", "candidates": [p.describe() for p in self.plans],
+                "chosen": sorted(set(self.chosen.values()))}
+
+
 def select(ctx):
     """Return the Plan of the first family whose pattern and geometry fit.
 

@@ -56,6 +56,10 @@ class Handle:
         outputs = self._abi["outputs"]
         self._ret = self._index[outputs[0]] if outputs else None
         self._launchers = {}
+        # max_num_configs > 1: pick among every fitting kernel by timing (auto_tuner.AutoTuner)
+        request = compilation.request
+        configs = getattr(request, "max_num_configs", None) if request is not None else None
+        self._tune = isinstance(configs, int) and configs > 1
 
     # --------------------------------------------------------------- contract
     def __call__(self, *args, **kwargs):
@@ -80,7 +84,7 @@ class Handle:
             with self._lock:
                 plan = self._plans.get(plan_key)
                 if plan is None:
-                    plan = self._kernel.specialize(public, meta)
+                    plan = self._kernel.specialize(public, meta, tune=self._tune)
                     self._plans[plan_key] = plan
         if key is not None:
             launch = plan.bind(public, self._index)

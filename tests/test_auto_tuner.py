@@ -1,0 +1,133 @@
+"""AutoTuner (reference tests/test_auto_tuner.py) and tuned Handles.
+
+CPU: the contract of the reference's AutoTuner — every candidate benchmarked once per
+argument key, the selection persisted so a new tuner with the same namespace and
+candidates benchmarks nothing, failing candidates recorded as infinite timings, an error
+naming every reason when all fail.  Programs that update a tensor they read are never
+tuned.  GPU: a Handle made with ``max_num_configs`` > 1 times the fitting kernels (the add
+kernel and the generic kernel) and computes the same result.
+"""
+
+import uuid
+
+import pytest
+import torch
+
+import ninetoothed_amd as ninetoothed
+import ninetoothed_amd.language as ntl
+from ninetoothed_amd import Symbol, Tensor, families
+from ninetoothed_amd.auto_tuner import AutoTuner
+
+
+@pytest.fixture(autouse=True)
+def _cache_dir(tmp_path, monkeypatch):
+    monkeypatch.setenv("NINETOOTHED_AMD_CACHE_DIR", str(tmp_path / "cache"))
+
+
+def _foo(*args, **kwargs):
+    return "foo"
+
+
+def _bar(*args, **kwargs):
+    return "bar"
+
+
+def _deterministic(function, args, kwargs):
+    return {_foo: 2.0, _bar: 1.0}.get(function, 3.0)
+
+
+@pytest.mark.parametrize("kwargs", ({"a": 2, "b": 4}, {"a": 2, "b": 4, "c": 6, "d": 8}))
+@pytest.mark.parametrize("args", ((1,), (1, 3, 5)))
+def test_auto_tuner(args, kwargs):
+    calls = []
+
+    def benchmark(function, a, k):
+        calls.append(function)
+        return _deterministic(function, a, k)
+
+    namespace = f"test_{uuid.uuid4().hex}"
+    tuner = AutoTuner((_foo, _bar), ("_foo", "_bar"), benchmark=benchmark, cache_namespace=namespace)
+    assert not tuner._cache_path.exists()
+    assert tuner(*args, **kwargs) == "bar"
+    assert calls == [_foo, _bar]
+    assert tuner(*args, **kwargs) == "bar" and calls == [_foo, _bar]  # no new benchmarks
+    assert tuner._cache_path.exists() and tuner._get_func_cache_path(_foo).exists()
+
+    again = []
+    cached = AutoTuner((_foo, _bar), ("_foo", "_bar"), benchmark=lambda *c: again.append(c) or 0.0,
+                       cache_namespace=namespace)
+    assert cached(*args, **kwargs) == "bar" and not again
+    # another argument key is benchmarked anew
+    cached(*args, 99, **kwargs)
+    assert len(again) == 2
+
+
+def test_failing_candidates_are_skipped_and_reported():
+    def broken(*a, **k):
+        raise RuntimeError("boom")
+
+    def benchmark(function, a, k):
+        if function is broken:
+            raise RuntimeError("boom")
+        return 1.0
+
+    tuner = AutoTuner((broken, _foo), ("broken", "_foo"), benchmark=benchmark, cache_namespace=uuid.uuid4().hex)
+    assert tuner(1) == "foo"
+    all_broken = AutoTuner((broken,), ("broken",), benchmark=benchmark, cache_namespace=uuid.uuid4().hex)
+    with pytest.raises(RuntimeError, match="All auto-tuning candidates failed: broken: RuntimeError: boom"):
+        all_broken(1)
+
+
+def test_validator_and_key_checks():
+    with pytest.raises(ValueError, match="one key for every candidate"):
+        AutoTuner((_foo, _bar), ("_foo",))
+    seen = []
+    tuner = AutoTuner((_foo,), ("_foo",), benchmark=lambda *c: 1.0, validator=lambda a, k: seen.append(a),
+                      cache_namespace=uuid.uuid4().hex)
+    tuner(3)
+    assert seen == [(3,)]
+    key = AutoTuner._make_arg_key((torch.empty(2, 3),), {"x": 1})
+    assert "shape=(2, 3)" in key and "stride=(3, 1)" in key and "x=1" in key
+
+
+def _add_handle(**options):
+    bs = Symbol("BS", meta=True)
+
+    def app(a, b, out):
+        out = a + b  # noqa: F841
+
+    return ninetoothed.make(lambda a, b, o: (a.tile((bs,)), b.tile((bs,)), o.tile((bs,))), app,
+                            (Tensor(1), Tensor(1), Tensor(1)), **options)
+
+
+def test_candidates_and_in_place_programs():
+    h = _add_handle()
+    v = torch.empty(1000)
+    ctx = h._kernel.context({"a": v, "b": v, "out": v}, {})
+    assert [p.describe()["family"] for p in families.candidates(ctx)] == ["add", "generic"]
+    assert not families.updates_an_input(ctx.program)
+    tuned = h._kernel.specialize({"a": v, "b": v, "out": v}, {}, tune=True)
+    assert tuned.describe()["family"] == "tuned"
+
+    def inplace(x):
+        x = x + 1.0  # noqa: F841
+
+    bs = Symbol("BS", meta=True)
+    k = ninetoothed.make(lambda x: (x.tile((bs,)),), inplace, (Tensor(1),))
+    ctx = k._kernel.context({"x": v}, {})
+    assert families.updates_an_input(ctx.program)
+    assert k._kernel.specialize({"x": v}, {}, tune=True).describe()["family"] == "generic"
+
+
+@pytest.mark.gpu
+def test_tuned_handle_picks_a_kernel_and_computes():
+    h = _add_handle(max_num_configs=4)
+    a, b = torch.randn(100_000, device="cuda"), torch.randn(100_000, device="cuda")
+    out = torch.empty_like(a)
+    h(a, b, out)
+    assert torch.equal(out, a + b)
+    (plan,) = h.plans()
+    assert plan["family"] == "tuned" and len(plan["chosen"]) == 1
+    out2 = torch.empty_like(a)
+    h(a, b, out2)  # the bound winner, no new benchmark
+    assert torch.equal(out2, a + b)
