@@ -284,6 +284,12 @@ class _BothBranches:
 
 
 class _ExploringLowerer(frontend.Lowerer):
+    def data(self, v):
+        # a constexpr used as a value: any constant will do to find the stored parameters
+        if isinstance(v, _BothBranches):
+            return self.const(1)
+        return super().data(v)
+
     def _stmt(self, frame, s):
         import ast
 

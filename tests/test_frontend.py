@@ -258,3 +258,16 @@ def test_library_exports_every_declared_entry_point():
     for name in declared:
         assert callable(getattr(lib, name))
     assert lib.nt_abi_version() == _lib.ABI_VERSION
+
+
+def test_constexpr_used_as_a_value_is_lowered():
+    # reference tests/test_scalar_element_reads.py: a constexpr scalar divides a row sum
+    def app(x, scale, out):
+        mean = ntl.sum(x, axis=1) / scale
+        out = x - mean[:, None]  # noqa: F841
+
+    scalar = Tensor(0, dtype="float32", constexpr=True, value=32.0)
+    h = ninetoothed.make(lambda x, s, o: (x.tile((1, 32)), s, o.tile((1, 32))), app, (Tensor(2), scalar, Tensor(2)))
+    assert h._abi["outputs"] == ("out",)
+    x = torch.empty(3, 32)
+    assert _specialize(h, x, 32.0, x)["family"] == "generic"

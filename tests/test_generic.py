@@ -572,3 +572,21 @@ def test_more_reduction_programs(dtype):
     x = torch.randn((6, 3, 10), device="cuda").to(dtype)
     k(x, out)
     torch.testing.assert_close(out.float(), x.float().sum(dim=1), rtol=tol, atol=tol)
+
+
+def scalar_row_application(x, scale, out):
+    mean = ntl.sum(x, axis=1) / scale
+    out = x - mean[:, None]  # noqa: F841
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("constexpr", (False, True))
+def test_scalar_in_row_expression(constexpr):
+    # reference tests/test_scalar_element_reads.py:9-30
+    scalar = Tensor(0, dtype="float32", constexpr=constexpr, value=32.0 if constexpr else None)
+    kernel = ninetoothed.make(lambda x, s, o: (x.tile((1, 32)), s, o.tile((1, 32))), scalar_row_application,
+                              (Tensor(2), scalar, Tensor(2)), max_num_configs=1)
+    x = torch.randn((3, 32), device="cuda")
+    out = torch.full_like(x, -12345)
+    kernel(x, 32.0, out)
+    torch.testing.assert_close(out, x - x.mean(1, keepdim=True))
