@@ -276,7 +276,8 @@ def _discover_outputs(application, params, arranged):
             infos.append(frontend.ParamInfo(name, tuple(l.ndim for l in t.levels()[1:]), t.source.ndim))
     lowerer = _ExploringLowerer(application, infos)
     program = lowerer.lower()
-    return tuple(n for n in params if n in program.stores), program
+    written = set(program.stores) | set(frontend.effect_targets(program))
+    return tuple(n for n in params if n in written), program
 
 
 class _BothBranches:

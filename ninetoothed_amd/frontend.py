@@ -65,6 +65,9 @@ class Program:
     stores: dict  # param name -> stored value (last store)
     loops: dict  # loop id -> Loop
     store_order: list
+    # side effects outside the arranged tile stores, in program order:
+    # ("src_store", param, indices, value), ("ptr_store", ptr, value), ("atomic_add", ptr, value)
+    effects: list = field(default_factory=list)
 
 
 @dataclass
@@ -176,6 +179,7 @@ class Lowerer:
         self.loops = {}
         self.stores = {}
         self.store_order = []
+        self.effects = []
         self._loop_ids = 0
         self.application = application
 
@@ -194,7 +198,7 @@ class Lowerer:
                 bindings[name] = self.b.make("param", name)
         frame = _Frame(self.application, node, bindings, names)
         self._block(frame, node.body)
-        return Program(names, dict(self.stores), dict(self.loops), list(self.store_order))
+        return Program(names, dict(self.stores), dict(self.loops), list(self.store_order), list(self.effects))
 
     # ----------------------------------------------------------------- values
     def const(self, v):
@@ -315,6 +319,13 @@ class Lowerer:
             for t, v in zip(target.elts, value):
                 self._target(frame, t, v)
             return
+        if isinstance(target, ast.Subscript):
+            base = self._expr(frame, target.value)
+            if isinstance(base, _Source):
+                indices = self._source_indices(frame, base, target.slice)
+                self.effects.append(("src_store", base.param, indices, self.data(value)))
+                self.store_order.append(base.param)
+                return
         raise LoweringError("only simple names can be assigned in an application")
 
     def _for(self, frame, s):
@@ -446,6 +457,8 @@ class Lowerer:
         if isinstance(base, _Source):
             if attr == "shape":
                 return _Shape(self.b.make("source_shape", base.param, d) for d in range(base.ndim))
+            if attr in ("data_ptr", "stride"):
+                return _Method(attr, base)
             raise LoweringError(f"unsupported attribute `.source.{attr}`")
         try:
             return getattr(base, attr)
@@ -460,6 +473,8 @@ class Lowerer:
             return base[idx]
         if isinstance(base, (tuple, list)):
             return base[self._expr(frame, sl)]
+        if isinstance(base, _Source):
+            return self.b.make("src_load", base.param, self._source_indices(frame, base, sl))
         if not isinstance(base, Value):
             raise LoweringError("unsupported subscript")
         items = sl.elts if isinstance(sl, ast.Tuple) else [sl]
@@ -482,6 +497,12 @@ class Lowerer:
         idx = self._expr(frame, items[0])
         return self.b.make("index", base, self.data(idx) if not isinstance(idx, Value) else idx)
 
+    def _source_indices(self, frame, src, sl):
+        items = sl.elts if isinstance(sl, ast.Tuple) else [sl]
+        if len(items) != src.ndim:
+            raise LoweringError(f"`.source[...]` of a {src.ndim}-D tensor takes {src.ndim} indices")
+        return tuple(self.data(self._expr(frame, x)) for x in items)
+
     def _norm_dim(self, d, ndim):
         if not isinstance(d, int):
             raise LoweringError("dimension arguments must be integers")
@@ -491,6 +512,14 @@ class Lowerer:
         func = self._expr(frame, e.func)
         args = [self._expr(frame, a) for a in e.args]
         kwargs = {k.arg: self._expr(frame, k.value) for k in e.keywords}
+        if isinstance(func, _Method) and isinstance(func.target, _Source):
+            src = func.target
+            if func.name == "data_ptr":
+                return self.b.make("ptr", src.param)
+            d = args[0] if args else kwargs.get("dim")
+            if not isinstance(d, int):
+                raise LoweringError("`.source.stride(dim)` needs an integer dimension")
+            return self.b.make("source_stride", src.param, self._norm_dim(d, src.ndim))
         if isinstance(func, _Method):
             t = func.target
             if func.name == "to":
@@ -541,6 +570,16 @@ class Lowerer:
             return b.make("math", name, self.data(args[0]))
         if name == "cast":
             return b.make("cast", self.data(args[0]), self.dtype_value(args[1] if len(args) > 1 else kwargs["dtype"]))
+        if name == "load":
+            if len(args) != 1 or kwargs:
+                raise LoweringError("ntl.load takes one pointer (masks are added by the backend)")
+            return b.make("ptr_load", self.data(args[0]))
+        if name in ("store", "atomic_add"):
+            if len(args) != 2 or kwargs:
+                raise LoweringError(f"ntl.{name} takes (pointer, value)")
+            self.effects.append(("ptr_store" if name == "store" else "atomic_add", self.data(args[0]),
+                                 self.data(args[1])))
+            return None
         if name in ("rand", "randint", "randn"):
             # counter-based random numbers: (seed, offset) -> one value per offset element
             if len(args) != 2 or kwargs:
@@ -587,6 +626,31 @@ def _assigned_names(stmts):
                     for n in ast.walk(t):
                         if isinstance(n, ast.Name):
                             out.add(n.id)
+    return out
+
+
+def pointer_param(v):
+    """The tensor parameter whose ``source.data_ptr()`` a pointer expression starts from."""
+    found = set()
+    stack = [v]
+    while stack:
+        x = stack.pop()
+        if not isinstance(x, Value):
+            continue
+        if x.op == "ptr":
+            found.add(x.args[0])
+        elif x.op in ("add", "sub"):
+            stack.extend(x.args)
+    if len(found) != 1:
+        raise LoweringError("a pointer must be one tensor's `source.data_ptr()` plus integer offsets")
+    return found.pop()
+
+
+def effect_targets(program):
+    """Parameters written by the program's side effects (scatter stores, pointer stores, atomics)."""
+    out = []
+    for eff in program.effects:
+        out.append(eff[1] if eff[0] == "src_store" else pointer_param(eff[1]))
     return out
 
 

@@ -39,9 +39,11 @@ import numpy as np
 
 from ninetoothed_amd import _lib
 from ninetoothed_amd.errors import KernelLaunchError, LoweringError
-from ninetoothed_amd.frontend import Value
+from ninetoothed_amd.frontend import Value, effect_targets
+from ninetoothed_amd.frontend import pointer_param as frontend_pointer_param
 
-MAX_ELEMENTS = 1 << 26  # host-side index tables: at most 64 Mi elements per launch
+MAX_ELEMENTS = 1 << 26
+_CONSTLIKE = ("const", "shape", "source_shape", "source_stride")  # values known at specialisation  # host-side index tables: at most 64 Mi elements per launch
 
 _ALLOWED = {"load", "const", "param", "add", "sub", "mul", "div", "floordiv", "mod", "neg", "lt", "le", "gt", "ge",
             "eq", "ne", "where", "maximum", "minimum", "math", "libm", "cast", "dtype", "dtype_of", "zeros",
@@ -221,11 +223,13 @@ class _Emitter:
             return int(self.ctx.views[view.args[0]].level_shapes[level][d])
         if v.op == "source_shape":
             return int(self.ctx.views[v.args[0]].source_shape[v.args[1]])
+        if v.op == "source_stride":
+            return int(self.ctx.values[v.args[0]].stride(v.args[1]))
         return None
 
     def operand(self, v, t):
         """Operand ``v`` as a value of working type for an operation in type ``t``."""
-        if v.op in ("const", "shape", "source_shape"):
+        if v.op in _CONSTLIKE:
             c = self.const_value(v)
             if isinstance(c, bool):
                 return "true" if c else "false"
@@ -257,7 +261,7 @@ class _Emitter:
 
     def emit(self, v):
         op, args = v.op, v.args
-        if op in ("const", "shape", "source_shape"):
+        if op in _CONSTLIKE:
             self.types[id(v)] = "bool" if isinstance(self.const_value(v), bool) else "weak"
             return
         if op in ("dtype", "dtype_of", "param"):
@@ -380,7 +384,7 @@ class _Emitter:
 def _analyse(ctx):
     """(stores, ordered values, output names, loaded names) or None if the program is not element-parallel."""
     program = ctx.program
-    if program.loops:
+    if program.loops or program.effects:
         return None
     stores = program.stores
     values = _walk(list(stores.values()))
@@ -425,7 +429,7 @@ class GenericPlan:
             t = _torch_dtype_name(ctx.dtypes[out])
             src = em.type_of(v)
             src = "float32" if src == "weak" else src
-            val = em.operand(v, src) if v.op in ("const", "shape", "source_shape") else em.names[id(v)]
+            val = em.operand(v, src) if v.op in _CONSTLIKE else em.names[id(v)]
             if em.work(src) != em.work(t):
                 val = f"(({em.work(t)}){val})"
             lines.append(f"    if (o_{out} >= 0) p_{out}[o_{out}] = {_STORAGE[t][3].format(val)};")
@@ -635,13 +639,19 @@ class GenericPlan:
 # masks of every tensor it is computed from hold, else it is the reduction's identity
 # (reference src/ninetoothed/backends/emitters/ssa.py:1834-1910, 2180-2210).
 
-_TILE_ALLOWED = _ALLOWED | {"reduce", "bcast"}
+_TILE_ALLOWED = _ALLOWED | {"reduce", "bcast", "ptr", "source_stride", "src_load", "ptr_load"}
 LDS_BYTES = 64 * 1024
 _INT_LIMITS = {"int8": (-128, 127), "uint8": (0, 255), "int16": (-32768, 32767), "int32": (-(2**31), 2**31 - 1),
                "int64": (-(2**63), 2**63 - 1)}
 
 
 def _value_operands(v):
+    if v.op == "src_load":
+        return list(v.args[1])
+    if v.op == "ptr_load":
+        return [v.args[0]]
+    if v.op in ("ptr", "source_stride"):
+        return []
     if v.op == "math":
         return [v.args[1]]
     if v.op == "libm":
@@ -673,13 +683,16 @@ def _shapes(ctx, values, const_value):
     shp = {}
     for v in values:
         op, a = v.op, v.args
-        if op in ("const", "dtype", "dtype_of", "shape", "source_shape", "param"):
+        if op in ("const", "dtype", "dtype_of", "shape", "source_shape", "source_stride", "param", "ptr"):
             s = ()
         elif op == "load":
             name = a[0].args[0]
             s = () if ctx.params[name].source_ndim == 0 else _tile_shape(ctx, name)
         elif op == "offsets":
-            s = _tile_shape(ctx, a[0].args[0])
+            tile = _tile_shape(ctx, a[0].args[0])
+            if len(tile) != ctx.params[a[0].args[0]].source_ndim:
+                raise LoweringError("`offsets` in a tile program needs a tile with one dim per source dim")
+            s = (tile[int(a[1])],) if tile else ()
         elif op == "reduce":
             src, axis = shp[id(a[1])], a[2]
             if axis is None:
@@ -740,10 +753,14 @@ class _TileEmitter(_Emitter):
         self.types = plan.types
         self.shapes = plan.shapes
 
-    def context(self, root, coords, tag):
+    def context(self, root, coords, tag, more=()):
+        """Lines computing ``root`` at ``coords`` (and each (value, coords) of ``more``)."""
         self.names, self.lines, self.coords, self.masks, self.tag = {}, [], {}, {}, tag
+        self.ptrs = {}
         self._assign(root, tuple(coords))
-        for v in _walk([root]):
+        for extra, extra_coords in more:
+            self._assign(extra, tuple(extra_coords))
+        for v in _walk([root] + [m[0] for m in more]):
             if id(v) in self.coords:
                 self.emit(v)
         return self.lines
@@ -775,6 +792,22 @@ class _TileEmitter(_Emitter):
 
     def emit(self, v):
         op, args = v.op, v.args
+        if self.emit_pointer(v):
+            return
+        if op == "ptr_load":
+            if not self.is_pointer(args[0]):
+                raise LoweringError("ntl.load needs a `source.data_ptr()` pointer")
+            name, off = self.ptrs[id(args[0])]
+            ox = off  # bounds: inside the tensor's storage extent, else 0
+            self.raw_load(v, name, ox, f"({ox}) >= 0 && ({ox}) < {self.plan.extent(name)}LL")
+            self.masks[id(v)] = frozenset()
+            return
+        if op == "src_load":
+            name, indices = args
+            off, cond = self.source_offset(name, indices)
+            self.raw_load(v, name, off, cond)
+            self.masks[id(v)] = frozenset([f"({cond})"])
+            return
         if op == "load" and self.ctx.params[args[0].args[0]].source_ndim != 0:
             name = args[0].args[0]
             t = self.tensor_dtype(name)
@@ -787,12 +820,12 @@ class _TileEmitter(_Emitter):
             o = repr(other) if other == other and abs(other) != float("inf") else (
                 "__builtin_nanf(\"\")" if other != other else ("__builtin_huge_valf()" if other > 0 else "(-__builtin_huge_valf())"))
             self.define(v, t, f"({ix} >= 0 ? ({w}){ld.format(f'p_{name}[{ix}]')} : ({w}){o})", exact=True)
-            self.masks[id(v)] = frozenset([ix])
+            self.masks[id(v)] = frozenset([f"({ix} >= 0)"])
             return
         if op == "offsets":
             name, d = args[0].args[0], int(args[1])
             lin = _ravel(self.coords[id(v)], self.shapes[id(v)])
-            self.names[id(v)] = f"(long long)f_{name}_{d}[pb_{name} + {lin}]"
+            self.names[id(v)] = f"(long long)f_{name}_{d}[pbo_{name}_{d} + {lin}]"
             self.types[id(v)] = "int32"
             self.masks[id(v)] = frozenset()
             return
@@ -820,7 +853,46 @@ class _TileEmitter(_Emitter):
 
     def mask_of(self, v):
         m = sorted(self.masks.get(id(v), frozenset()))
-        return " && ".join(f"({x} >= 0)" for x in m) if m else None
+        return " && ".join(m) if m else None
+
+    def is_pointer(self, v):
+        return isinstance(v, Value) and id(v) in self.ptrs
+
+    def source_offset(self, name, indices):
+        """(C offset, C bounds condition) of ``source[indices]`` (each index already emitted)."""
+        t = self.ctx.values[name]
+        terms, conds = [], []
+        for d, ix in enumerate(indices):
+            e = self.operand(ix, "int64")
+            terms.append(f"({e}) * {int(t.stride(d))}LL")
+            conds.append(f"({e}) >= 0 && ({e}) < {int(t.shape[d])}LL")
+        return " + ".join(terms) or "0LL", " && ".join(f"({c})" for c in conds) or "true"
+
+    def emit_pointer(self, v):
+        """Pointer arithmetic: record (tensor, C element offset) instead of a value."""
+        if v.op == "ptr":
+            self.ptrs[id(v)] = (v.args[0], "0LL")
+            return True
+        if v.op in ("add", "sub") and any(self.is_pointer(a) for a in v.args):
+            a, b = v.args
+            if v.op == "sub" and self.is_pointer(b):
+                raise LoweringError("a pointer can only be offset, not subtracted from")
+            p, q = (a, b) if self.is_pointer(a) else (b, a)
+            if self.is_pointer(q):
+                raise LoweringError("two pointers cannot be added")
+            name, off = self.ptrs[id(p)]
+            sign = "-" if v.op == "sub" else "+"
+            self.ptrs[id(v)] = (name, f"({off} {sign} {self.operand(q, 'int64')})")
+            return True
+        return False
+
+    def raw_load(self, v, name, off, cond):
+        t = self.tensor_dtype(name)
+        st, w, ld, _ = _STORAGE[t]
+        ox = f"{self.tag}o{len(self.names)}"
+        self.lines.append(f"      const long long {ox} = {off};")
+        self.define(v, t, f"(({cond}) ? ({w}){ld.format(f'p_{name}[{ox}]')} : ({w})0)", exact=True)
+        self.plan.raw_reads.add(name)
 
 
 def _analyse_tile(ctx):
@@ -828,8 +900,11 @@ def _analyse_tile(ctx):
     if program.loops:
         return None
     stores = program.stores
-    values = _walk(list(stores.values()))
-    if not stores:
+    roots = list(stores.values())
+    for eff in program.effects:
+        roots += list(eff[2]) + [eff[3]] if eff[0] == "src_store" else [eff[1], eff[2]]
+    values = _walk(roots)
+    if not stores and not program.effects:
         return None
     for v in values:
         if v.op not in _TILE_ALLOWED:
@@ -837,12 +912,18 @@ def _analyse_tile(ctx):
         if v.op in ("load", "offsets") and v.args[0].op != "param":
             return None
     loaded = {v.args[0].args[0] for v in values if v.op in ("load", "offsets")}
+    read_raw = {v.args[0] for v in values if v.op == "src_load"}
+    read_raw |= {frontend_pointer_param(v.args[0]) for v in values if v.op == "ptr_load"}
     tensors = [n for n in list(stores) + sorted(loaded) if ctx.params[n].source_ndim != 0]
     for n in stores:
         if ctx.params[n].source_ndim == 0:
             return None
-    if set(stores) & loaded:
+    written = set(stores) | set(effect_targets(program))
+    data_read = {v.args[0].args[0] for v in values if v.op == "load"}  # offsets are indices, not data
+    if written & (data_read | read_raw):
         raise LoweringError("the generic tile kernels do not update a tensor they also read")
+    if not tensors:
+        raise LoweringError("a tile program needs an arranged tensor to set its program grid")
     for n in tensors:
         if len(ctx.views[n].level_shapes) > 2:
             raise LoweringError(f"`{n}` has {len(ctx.views[n].level_shapes)} levels; the generic tile kernels take 2")
@@ -865,7 +946,10 @@ class TilePlan(GenericPlan):
         self.types = {}
         self.outputs = list(stores)
         self.kernel_name = "nt_generic_tile"
-        grid = tuple(ctx.views[self.outputs[0]].level_shapes[0])
+        self.raw_reads = set()  # tensors read through source indexing or pointers
+        arranged = self.outputs + sorted({v.args[0].args[0] for v in values if v.op in ("load", "offsets")
+                                          and ctx.params[v.args[0].args[0]].source_ndim != 0})
+        grid = tuple(ctx.views[arranged[0]].level_shapes[0])
         self.programs = int(np.prod(grid)) if grid else 1
         self.lds = {}
         em = _TileEmitter(self)
@@ -938,7 +1022,7 @@ class TilePlan(GenericPlan):
             t = _torch_dtype_name(ctx.dtypes[out])
             src = em.type_of(v)
             src = "float32" if src == "weak" else src
-            val = em.operand(v, src) if v.op in ("const", "shape", "source_shape") else em.names[id(v)]
+            val = em.operand(v, src) if v.op in _CONSTLIKE else em.names[id(v)]
             if em.work(src) != em.work(t):
                 val = f"(({em.work(t)}){val})"
             blocks.append("\n".join([
@@ -949,20 +1033,28 @@ class TilePlan(GenericPlan):
                 f"      p_{out}[oi] = {_STORAGE[t][3].format(val)};",
                 "    }",
             ]))
+        self.raw_writes = []
+        for k, eff in enumerate(ctx.program.effects):
+            blocks.append(self._effect(em, k, eff))
         self.loaded = sorted({v.args[0].args[0] for v in values if v.op == "load"
                               and ctx.params[v.args[0].args[0]].source_ndim != 0})
+        # tensors reached only through pointers or source indexing: a plain pointer argument
+        self.raw = sorted((self.raw_reads | set(self.raw_writes)) - set(self.loaded) - set(self.outputs))
         self.scalars = [v.args[0].args[0] for v in values if v.op == "load"
                         and ctx.params[v.args[0].args[0]].source_ndim == 0]
         self.scalars = list(dict.fromkeys(self.scalars))
         self.offsets = sorted({(v.args[0].args[0], int(v.args[1])) for v in values if v.op == "offsets"})
         self.index_names = list(dict.fromkeys(self.outputs + self.loaded))
         self.tile_sizes = {n: int(np.prod(_tile_shape(ctx, n))) if _tile_shape(ctx, n) else 1
-                           for n in set(self.index_names) | {n for n, _ in self.offsets}}
+                           for n in self.index_names}
+        self.offset_lengths = {(n, d): (_tile_shape(ctx, n)[d] if _tile_shape(ctx, n) else 1) for n, d in self.offsets}
         self.scalar_types = {n: em.scalar_type(n) for n in self.scalars}
         params = [f"const int* __restrict__ t_{n}" for n in self.index_names]
         params += [f"const int* __restrict__ f_{n}_{d}" for n, d in self.offsets]
         params += [f"const {_STORAGE[_torch_dtype_name(ctx.dtypes[n])][0]}* __restrict__ p_{n}" for n in self.loaded]
         params += [f"{_STORAGE[_torch_dtype_name(ctx.dtypes[n])][0]}* __restrict__ p_{n}" for n in self.outputs]
+        params += [("" if n in self.raw_writes else "const ") + f"{_STORAGE[_torch_dtype_name(ctx.dtypes[n])][0]}* p_{n}"
+                   for n in self.raw]
         params += [f"{_STORAGE[self.scalar_types[n]][0]} s_{n}" for n in self.scalars]
         params.append("long long programs")
         self.params = params
@@ -971,6 +1063,58 @@ class TilePlan(GenericPlan):
 
     def index_expr(self, name, lin):
         return f"t_{name}[pb_{name} + {lin}]"
+
+    def extent(self, name):
+        """Elements from a tensor's first to one past its last element (its storage span)."""
+        t = self.ctx.values[name]
+        if t.numel() == 0:
+            return 0
+        return 1 + sum((int(n) - 1) * int(st) for n, st in zip(t.shape, t.stride()))
+
+    _ATOMIC = {"float32": "float", "float64": "double", "int32": "int"}
+
+    def _effect(self, em, k, eff):
+        """One side effect: a scatter into a source, a store or an atomic add through a pointer,
+        element by element over the broadcast shape of its operands, masked to the tensor."""
+        kind = eff[0]
+        if kind == "src_store":
+            name, indices, value = eff[1], eff[2], eff[3]
+            operands = list(indices) + [value]
+        else:
+            ptr, value = eff[1], eff[2]
+            name = frontend_pointer_param(ptr)
+            operands = [ptr, value]
+        shape = _bcast_shapes(*[self.shapes[id(x)] for x in operands])
+        n = int(np.prod(shape)) if shape else 1
+        coords = _unravel("j", shape)
+        roots = [(x, coords[len(coords) - len(self.shapes[id(x)]):] if self.shapes[id(x)] else ())
+                 for x in operands]
+        body = em.context(roots[0][0], roots[0][1], f"e{k}_", more=roots[1:])
+        t = _torch_dtype_name(self.ctx.dtypes[name])
+        src = em.type_of(value)
+        src = "float32" if src in ("weak", "bool") else src
+        val = em.operand(value, t)
+        if kind == "src_store":
+            off, cond = em.source_offset(name, indices)
+        else:
+            pname, off = em.ptrs[id(ptr)]
+            cond = f"({off}) >= 0 && ({off}) < {self.extent(name)}LL"
+        if kind == "atomic_add":
+            ctype = self._ATOMIC.get(t)
+            if ctype is None:
+                raise LoweringError(f"ntl.atomic_add on {t} tensors is not supported (float32, float64, int32 are)")
+            action = f"atomicAdd(p_{name} + o, ({ctype}){val});"
+        else:
+            action = f"p_{name}[o] = {_STORAGE[t][3].format(val)};"
+        self.raw_writes.append(name)
+        return "\n".join([
+            f"    for (long long j = tid; j < {n}LL; j += 256) {{  // {kind} into {name}",
+            *body,
+            f"      const long long o = {off};",
+            f"      if ({cond}) {action}",
+            "    }",
+            "    __syncthreads();",
+        ])
 
     def sources_for(self, values):
         return [self.source()]
@@ -991,6 +1135,7 @@ class TilePlan(GenericPlan):
 
     def source(self, linear=None, linear_offsets=()):
         bases = [f"    const long long pb_{n} = p * {self.tile_sizes[n]}LL;" for n in self.tile_sizes]
+        bases += [f"    const long long pbo_{n}_{d} = p * {self.offset_lengths[(n, d)]}LL;" for n, d in self.offsets]
         return (
             _PRELUDE
             + f'\nextern "C" __global__ void __launch_bounds__(256) {self.kernel_name}({", ".join(self.params)}) {{\n'
@@ -1008,27 +1153,28 @@ class TilePlan(GenericPlan):
     def bind(self, values, index):
         import torch
 
-        device = values[self.outputs[0]].device
+        device = next(values[n].device for n in self.index_names + self.raw + [k[0] for k in self.offsets])
         tables, offset_tables, maps = {}, {}, {}
         for n in self.index_names:
             maps[n] = self._maps(n)
             tab, _ = self._table(n, values[n], maps[n])
             tables[n] = torch.from_numpy(tab).to(device)
         for n, d in self.offsets:
-            offset_tables[(n, d)] = torch.from_numpy(self._offsets_table(n, d, maps.get(n))).to(device)
+            offset_tables[(n, d)] = torch.from_numpy(self._tile_offsets(n, d, maps.get(n))).to(device)
         fn = self.function(self.source())
-        ptrs = {n: ctypes.c_void_p() for n in self.index_names}
+        ptrs = {n: ctypes.c_void_p() for n in self.index_names + self.raw}
         argv = [ctypes.c_void_p(tables[n].data_ptr()) for n in self.index_names]
         argv += [ctypes.c_void_p(offset_tables[k].data_ptr()) for k in self.offsets]
         argv += [ptrs[n] for n in self.loaded]
         argv += [ptrs[n] for n in self.outputs]
+        argv += [ptrs[n] for n in self.raw]
         svals = {n: ctypes.c_int64() if self.scalar_types[n] == "int64" else ctypes.c_float() for n in self.scalars}
         argv += [svals[n] for n in self.scalars]
         argv.append(ctypes.c_int64(self.programs))
         params = (ctypes.c_void_p * len(argv))(*[ctypes.addressof(a) for a in argv])
         grid = min(self.programs, 256 * 64)
         lib = _lib.load()
-        positions = {n: index[n] for n in self.index_names}
+        positions = {n: index[n] for n in self.index_names + self.raw}
         spos = {n: index[n] for n in self.scalars}
 
         def launch(args):
@@ -1044,6 +1190,24 @@ class TilePlan(GenericPlan):
 
         launch.keep = (tables, offset_tables, argv, params)
         return launch
+
+    def _tile_offsets(self, name, dim, maps=None):
+        """``offsets(dim)`` per program: the source index along ``dim`` of the tile's elements
+        along its dim ``dim`` ([programs, tile_shape[dim]]); it may not vary along the other
+        tile dims."""
+        idx, _, shape = maps or self._maps(name)
+        grid = tuple(self.ctx.views[name].level_shapes[0])
+        tile = _tile_shape(self.ctx, name)
+        full = np.broadcast_to(np.asarray(idx[dim], dtype=np.int64), shape).reshape(
+            (int(np.prod(grid)) if grid else 1,) + tile)
+        sel = [slice(None)] + [slice(None) if i == dim else slice(0, 1) for i in range(len(tile))]
+        vec = full[tuple(sel)]
+        if not np.array_equal(np.broadcast_to(vec, full.shape), full):
+            raise LoweringError(f"`{name}.offsets({dim})` varies along other tile dims; tile programs take it as a vector")
+        vec = vec.reshape(full.shape[0], tile[dim] if tile else 1)
+        if vec.size and (vec.max() >= 2**31 or vec.min() < -(2**31)):
+            raise LoweringError("the generic kernels take offsets within 32 bits")
+        return np.ascontiguousarray(vec, dtype=np.int32).reshape(-1)
 
 
 def match_generic(ctx):

@@ -29,7 +29,7 @@ def _parsed_only(name):
 _FUNCTIONS = (
     "zeros", "full", "dot", "trans", "where", "max", "min", "sum", "maximum", "minimum",
     "exp", "exp2", "log", "log2", "sqrt", "rsqrt", "abs", "sigmoid", "cast", "arange",
-    "rand", "randint", "randn",
+    "rand", "randint", "randn", "load", "store", "atomic_add",
 )
 for _name in _FUNCTIONS:
     globals()[_name] = _parsed_only(_name)

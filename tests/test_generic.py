@@ -590,3 +590,66 @@ def test_scalar_in_row_expression(constexpr):
     out = torch.full_like(x, -12345)
     kernel(x, 32.0, out)
     torch.testing.assert_close(out, x - x.mean(1, keepdim=True))
+
+
+# ------------------------------------------------------------------ pointers, source indexing, atomics
+def clone_application_1(input, output):
+    output = ntl.load(  # noqa: F841
+        input.source.data_ptr()
+        + input.offsets(0)[:, None] * input.source.stride(0)
+        + input.offsets(1)[None, :] * input.source.stride(1)
+    )
+
+
+def clone_application_2(input, output):
+    output = input.source[input.offsets(0)[:, None], input.offsets(1)[None, :]]  # noqa: F841
+
+
+def clone_application_3(input, output):
+    output.source[output.offsets(0)[:, None], output.offsets(1)[None, :]] = input
+
+
+def clone_arrangement(input, output):
+    block_shape = (block_size(), block_size())
+    return input.tile(block_shape), output.tile(block_shape)
+
+
+def sum_arrangement(input, output, BLOCK_SIZE=1024):
+    input_arranged = input.tile((BLOCK_SIZE,))
+    return input_arranged, output.tile((-1,)).expand(input_arranged.shape)
+
+
+def sum_application(input, output):
+    ntl.atomic_add(output.source.data_ptr(), ntl.sum(input))
+
+
+@pytest.mark.parametrize("app", (clone_application_1, clone_application_2, clone_application_3))
+def test_pointer_and_source_programs_compile(app):
+    k = ninetoothed.make(clone_arrangement, app, (Tensor(2), Tensor(2)))
+    assert k._abi["outputs"] == ("output",)
+    x = torch.empty_strided((641, 280), (700, 300))
+    plan = _plan(k, x, torch.empty(641, 280))
+    assert plan.describe()["family"] == "generic"
+    assert len(GenericPlan.compile(plan.source())) > 1000
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("app", (clone_application_1, clone_application_2, clone_application_3))
+def test_clone_pointer_applications(app):
+    # reference tests/test_clone.py:22-70 (applications 1-3) on its strided input
+    kernel = ninetoothed.make(clone_arrangement, app, (Tensor(2), Tensor(2)))
+    inp = torch.empty_strided((641, 280), (700, 300), device="cuda")
+    inp.copy_(torch.randn(641, 280, device="cuda"))
+    out = torch.empty_like(inp)
+    kernel(inp, out)
+    assert torch.equal(out, inp)
+
+
+@pytest.mark.gpu
+def test_data_ptr_atomic_sum():
+    # reference tests/test_data_ptr.py:10-42
+    kernel = ninetoothed.make(sum_arrangement, sum_application, (Tensor(1), Tensor(1)))
+    inp = torch.randn(64180, device="cuda")
+    out = torch.zeros(1, dtype=inp.dtype, device="cuda")
+    kernel(inp, out)
+    assert torch.allclose(out[0], torch.sum(inp), rtol=1e-4, atol=1e-3)
