@@ -213,7 +213,12 @@ class KernelProgram:
             dtypes[spec.name] = public[spec.name].dtype
         infos = self.infos(public)
         program = self.lowered(infos)
-        return families.CallContext(program, views, public, {i.name: i for i in infos}, dtypes)
+        ctx = families.CallContext(program, views, public, {i.name: i for i in infos}, dtypes)
+        application = self.application or _import_application(self.application_ref)
+        if application is not None:
+            # the generic kernels re-lower with loops unrolled once trip counts are known
+            ctx.relower = lambda unroll: frontend.lower(application, infos, unroll=unroll)
+        return ctx
 
 
 def _plain(v):

@@ -117,6 +117,7 @@ class CallContext:
         self.values = values  # param name -> runtime value
         self.params = params  # param name -> ParamInfo
         self.dtypes = dtypes  # param name -> torch dtype (tensors only)
+        self.relower = None  # unroll -> Program: the application lowered with loops unrolled
 
     def view(self, name):
         return self.views[name]

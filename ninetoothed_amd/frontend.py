@@ -173,7 +173,8 @@ def parameter_names(func):
 
 
 class Lowerer:
-    def __init__(self, application, params):
+    def __init__(self, application, params, unroll=None):
+        self.unroll = unroll  # trip Value -> int, or None: loops are lowered symbolically
         self.b = _Builder()
         self.params = {p.name: p for p in params}
         self.loops = {}
@@ -321,6 +322,14 @@ class Lowerer:
             return
         if isinstance(target, ast.Subscript):
             base = self._expr(frame, target.value)
+            if isinstance(base, Value) and base.op in VIEW_OPS and not isinstance(target.slice, ast.Slice):
+                # `out[i] = v`: a store into one element (a tile) of a level
+                view = self._subscript(frame, base, target.slice)
+                if not (isinstance(view, Value) and view.op == "index"):
+                    raise LoweringError("only level indexing `out[i] = ...` can be assigned")
+                self.effects.append(("view_store", view, self.data(value)))
+                self.store_order.append(self.view_param(view))
+                return
             if isinstance(base, _Source):
                 indices = self._source_indices(frame, base, target.slice)
                 self.effects.append(("src_store", base.param, indices, self.data(value)))
@@ -337,6 +346,24 @@ class Lowerer:
         if not isinstance(s.target, ast.Name):
             raise LoweringError("loop variables must be simple names")
         trip = self.data(self._expr(frame, it.args[0])) if not isinstance(self._expr(frame, it.args[0]), Value) else self._expr(frame, it.args[0])
+        count = self.unroll(trip) if self.unroll is not None else None
+        if count is not None:
+            # unrolled: the body runs `count` times with the loop variable a constant.  Values
+            # carried from one iteration to the next are wrapped in `unmask` at every boundary:
+            # like the results of a loop, they carry no load mask into later reductions.
+            carried = [n for n in sorted(_assigned_names(s.body)) if isinstance(frame.env.get(n), Value)]
+
+            def boundary():
+                for n in carried:
+                    if isinstance(frame.env.get(n), Value):
+                        frame.env[n] = self.b.make("unmask", frame.env[n])
+
+            for k in range(count):
+                boundary()
+                frame.env[s.target.id] = self.const(k)
+                self._block(frame, s.body)
+            boundary()
+            return
         loop_id = self._loop_ids
         self._loop_ids += 1
         assigned = _assigned_names(s.body)
@@ -442,9 +469,19 @@ class Lowerer:
                     return _Shape(self.b.make("shape", base, d) for d in range(nd))
                 if base.op in ("zeros", "full"):
                     return _Shape(base.args[0])
+                if base.op == "dtype_of":
+                    # the shape of a level below a view (x.dtype.shape, x.dtype.dtype.shape, x[0].dtype.shape)
+                    view, depth = base, 0
+                    while view.op == "dtype_of":
+                        view, depth = view.args[0], depth + 1
+                    param, level = self.view_param(view), self.view_level(view) + depth
+                    ndims = self.params[param].level_ndims
+                    if level - 1 >= len(ndims):
+                        raise LoweringError(f"`{param}` has no level {level}")
+                    return _Shape(self.b.make("level_shape", param, level, d) for d in range(ndims[level - 1]))
                 raise LoweringError("`.shape` is only known for tensor parameters and zeros/full values")
             if attr == "dtype":
-                if base.op in VIEW_OPS:
+                if base.op in VIEW_OPS or base.op == "dtype_of":
                     return self.b.make("dtype_of", base)
                 raise LoweringError("`.dtype` is only supported on tensor parameters")
             if attr == "source":
@@ -623,10 +660,17 @@ def _assigned_names(stmts):
             if isinstance(node, (ast.Assign, ast.AugAssign, ast.AnnAssign)):
                 targets = node.targets if isinstance(node, ast.Assign) else [node.target]
                 for t in targets:
-                    for n in ast.walk(t):
-                        if isinstance(n, ast.Name):
-                            out.add(n.id)
+                    out.update(_bound_names(t))
     return out
+
+
+def _bound_names(target):
+    """Names an assignment target rebinds (``out[i] = v`` and ``x.source[...] = v`` rebind none)."""
+    if isinstance(target, ast.Name):
+        return {target.id}
+    if isinstance(target, (ast.Tuple, ast.List)):
+        return set().union(*(_bound_names(t) for t in target.elts)) if target.elts else set()
+    return set()
 
 
 def pointer_param(v):
@@ -650,10 +694,19 @@ def effect_targets(program):
     """Parameters written by the program's side effects (scatter stores, pointer stores, atomics)."""
     out = []
     for eff in program.effects:
-        out.append(eff[1] if eff[0] == "src_store" else pointer_param(eff[1]))
+        if eff[0] == "src_store":
+            out.append(eff[1])
+        elif eff[0] == "view_store":
+            v = eff[1]
+            while v.op == "index":
+                v = v.args[0]
+            out.append(v.args[0])
+        else:
+            out.append(pointer_param(eff[1]))
     return out
 
 
-def lower(application, params):
-    """Lower ``application`` for parameters described by ``params`` (ParamInfo list)."""
-    return Lowerer(application, params).lower()
+def lower(application, params, unroll=None):
+    """Lower ``application`` for parameters described by ``params`` (ParamInfo list);
+    with ``unroll`` (trip Value -> int or None), loops with a known trip count are unrolled."""
+    return Lowerer(application, params, unroll=unroll).lower()

@@ -31,6 +31,7 @@ output element writes it from several lanes (the last write is unspecified), as 
 reference's generated programs would.
 """
 
+import copy
 import ctypes
 import hashlib
 import threading
@@ -43,11 +44,12 @@ from ninetoothed_amd.frontend import Value, effect_targets
 from ninetoothed_amd.frontend import pointer_param as frontend_pointer_param
 
 MAX_ELEMENTS = 1 << 26
-_CONSTLIKE = ("const", "shape", "source_shape", "source_stride")  # values known at specialisation  # host-side index tables: at most 64 Mi elements per launch
+MAX_UNROLL = 64  # loops of up to this many iterations are unrolled for the tile kernels
+_CONSTLIKE = ("const", "shape", "source_shape", "source_stride", "level_shape")  # values known at specialisation  # host-side index tables: at most 64 Mi elements per launch
 
 _ALLOWED = {"load", "const", "param", "add", "sub", "mul", "div", "floordiv", "mod", "neg", "lt", "le", "gt", "ge",
             "eq", "ne", "where", "maximum", "minimum", "math", "libm", "cast", "dtype", "dtype_of", "zeros",
-            "full", "offsets", "rand", "randint", "randn", "shape", "source_shape"}
+            "full", "offsets", "rand", "randint", "randn", "shape", "source_shape", "level_shape"}
 
 _FLOAT = ("float16", "bfloat16", "float32", "float64")
 _INT = ("int8", "int16", "int32", "int64", "uint8")
@@ -188,7 +190,7 @@ class _Emitter:
         if d.op == "dtype":
             return d.args[0]
         view = d.args[0]
-        while view.op == "index":
+        while view.op in ("index", "dtype_of"):
             view = view.args[0]
         return self.tensor_dtype(view.args[0])
 
@@ -225,6 +227,8 @@ class _Emitter:
             return int(self.ctx.views[v.args[0]].source_shape[v.args[1]])
         if v.op == "source_stride":
             return int(self.ctx.values[v.args[0]].stride(v.args[1]))
+        if v.op == "level_shape":
+            return int(self.ctx.views[v.args[0]].level_shapes[v.args[1]][v.args[2]])
         return None
 
     def operand(self, v, t):
@@ -639,7 +643,7 @@ class GenericPlan:
 # masks of every tensor it is computed from hold, else it is the reduction's identity
 # (reference src/ninetoothed/backends/emitters/ssa.py:1834-1910, 2180-2210).
 
-_TILE_ALLOWED = _ALLOWED | {"reduce", "bcast", "ptr", "source_stride", "src_load", "ptr_load"}
+_TILE_ALLOWED = _ALLOWED | {"reduce", "bcast", "ptr", "source_stride", "src_load", "ptr_load", "index", "unmask"}
 LDS_BYTES = 64 * 1024
 _INT_LIMITS = {"int8": (-128, 127), "uint8": (0, 255), "int16": (-32768, 32767), "int32": (-(2**31), 2**31 - 1),
                "int64": (-(2**63), 2**63 - 1)}
@@ -656,12 +660,26 @@ def _value_operands(v):
         return [v.args[1]]
     if v.op == "libm":
         return list(v.args[1])
-    if v.op in ("cast", "bcast"):
+    if v.op in ("cast", "bcast", "unmask"):
         return [v.args[0]]
-    if v.op in ("load", "offsets", "reduce", "const", "shape", "source_shape", "zeros", "full", "param", "dtype",
-                "dtype_of"):
+    if v.op in ("load", "offsets", "reduce", "const", "shape", "source_shape", "level_shape", "zeros", "full", "param",
+                "dtype", "dtype_of"):
         return []
     return [a for a in v.args if isinstance(a, Value)]
+
+
+def _view_chain(view):
+    """(param, constant level indices) of ``param[k0][k1]...``, or None."""
+    ks = []
+    while view.op == "index":
+        k = view.args[1]
+        if not (isinstance(k, Value) and k.op == "const" and isinstance(k.args[0], int)):
+            return None
+        ks.append(k.args[0])
+        view = view.args[0]
+    if view.op != "param":
+        return None
+    return view.args[0], tuple(reversed(ks))
 
 
 def _bcast_shapes(*shapes):
@@ -683,11 +701,12 @@ def _shapes(ctx, values, const_value):
     shp = {}
     for v in values:
         op, a = v.op, v.args
-        if op in ("const", "dtype", "dtype_of", "shape", "source_shape", "source_stride", "param", "ptr"):
+        if op in ("const", "dtype", "dtype_of", "shape", "source_shape", "source_stride", "level_shape", "param", "ptr"):
             s = ()
         elif op == "load":
-            name = a[0].args[0]
-            s = () if ctx.params[name].source_ndim == 0 else _tile_shape(ctx, name)
+            name, ks = _view_chain(a[0])
+            levels = ctx.views[name].level_shapes if ctx.params[name].source_ndim != 0 else []
+            s = () if not levels else (tuple(levels[1 + len(ks)]) if 1 + len(ks) < len(levels) else ())
         elif op == "offsets":
             tile = _tile_shape(ctx, a[0].args[0])
             if len(tile) != ctx.params[a[0].args[0]].source_ndim:
@@ -808,11 +827,12 @@ class _TileEmitter(_Emitter):
             self.raw_load(v, name, off, cond)
             self.masks[id(v)] = frozenset([f"({cond})"])
             return
-        if op == "load" and self.ctx.params[args[0].args[0]].source_ndim != 0:
-            name = args[0].args[0]
+        chain = _view_chain(args[0]) if op == "load" else None
+        if chain is not None and self.ctx.params[chain[0]].source_ndim != 0:
+            name, ks = chain
             t = self.tensor_dtype(name)
             st, w, ld, _ = _STORAGE[t]
-            lin = _ravel(self.coords[id(v)], self.shapes[id(v)])
+            lin = self.plan.level_lin(name, ks, _ravel(self.coords[id(v)], self.shapes[id(v)]))
             ix = f"{self.tag}x{len(self.names)}"
             self.lines.append(f"      const int {ix} = {self.plan.index_expr(name, lin)};")
             other = self.ctx.views[name].source.other
@@ -838,6 +858,11 @@ class _TileEmitter(_Emitter):
             self.names[id(v)] = self.names[id(args[0])]
             self.types[id(v)] = self.types[id(args[0])]
             self.masks[id(v)] = self.masks.get(id(args[0]), frozenset())
+            return
+        if op == "unmask":  # a loop-carried value: the same value, no load mask
+            self.names[id(v)] = self.names[id(args[0])]
+            self.types[id(v)] = self.types[id(args[0])]
+            self.masks[id(v)] = frozenset()
             return
         if op in ("zeros", "full"):
             t = self.dtype_name(args[-1])
@@ -902,16 +927,26 @@ def _analyse_tile(ctx):
     stores = program.stores
     roots = list(stores.values())
     for eff in program.effects:
-        roots += list(eff[2]) + [eff[3]] if eff[0] == "src_store" else [eff[1], eff[2]]
+        if eff[0] == "src_store":
+            roots += list(eff[2]) + [eff[3]]
+        elif eff[0] == "view_store":
+            if _view_chain(eff[1]) is None:
+                return None
+            roots.append(eff[2])
+        else:
+            roots += [eff[1], eff[2]]
     values = _walk(roots)
     if not stores and not program.effects:
         return None
     for v in values:
         if v.op not in _TILE_ALLOWED:
             return None
-        if v.op in ("load", "offsets") and v.args[0].op != "param":
+        if v.op == "load" and _view_chain(v.args[0]) is None:
             return None
-    loaded = {v.args[0].args[0] for v in values if v.op in ("load", "offsets")}
+        if v.op == "offsets" and v.args[0].op != "param":
+            return None
+    loaded = {_view_chain(v.args[0])[0] for v in values if v.op == "load"}
+    loaded |= {v.args[0].args[0] for v in values if v.op == "offsets"}
     read_raw = {v.args[0] for v in values if v.op == "src_load"}
     read_raw |= {frontend_pointer_param(v.args[0]) for v in values if v.op == "ptr_load"}
     tensors = [n for n in list(stores) + sorted(loaded) if ctx.params[n].source_ndim != 0]
@@ -919,14 +954,18 @@ def _analyse_tile(ctx):
         if ctx.params[n].source_ndim == 0:
             return None
     written = set(stores) | set(effect_targets(program))
-    data_read = {v.args[0].args[0] for v in values if v.op == "load"}  # offsets are indices, not data
+    data_read = {_view_chain(v.args[0])[0] for v in values if v.op == "load"}  # offsets are indices, not data
     if written & (data_read | read_raw):
         raise LoweringError("the generic tile kernels do not update a tensor they also read")
     if not tensors:
         raise LoweringError("a tile program needs an arranged tensor to set its program grid")
+    indexed = {_view_chain(v.args[0])[0] for v in values if v.op == "load" and _view_chain(v.args[0])[1]}
+    indexed |= {_view_chain(e[1])[0] for e in program.effects if e[0] == "view_store"}
+    tensors += sorted({_view_chain(e[1])[0] for e in program.effects if e[0] == "view_store"})
     for n in tensors:
-        if len(ctx.views[n].level_shapes) > 2:
-            raise LoweringError(f"`{n}` has {len(ctx.views[n].level_shapes)} levels; the generic tile kernels take 2")
+        depth = len(ctx.views[n].level_shapes)
+        if depth > 3 or (depth == 3 and n not in indexed):
+            raise LoweringError(f"`{n}` has {depth} levels; the generic tile kernels take 2, or 3 indexed by level")
     # one flat program id, unravelled by every tensor over its own outermost level
     if len({int(np.prod(ctx.views[n].level_shapes[0])) for n in tensors}) > 1:
         raise LoweringError("the arranged tensors have different numbers of programs")
@@ -947,8 +986,11 @@ class TilePlan(GenericPlan):
         self.outputs = list(stores)
         self.kernel_name = "nt_generic_tile"
         self.raw_reads = set()  # tensors read through source indexing or pointers
-        arranged = self.outputs + sorted({v.args[0].args[0] for v in values if v.op in ("load", "offsets")
-                                          and ctx.params[v.args[0].args[0]].source_ndim != 0})
+        arranged = self.outputs + sorted(
+            {_view_chain(e[1])[0] for e in ctx.program.effects if e[0] == "view_store"}
+            | {_view_chain(v.args[0])[0] for v in values if v.op == "load"
+               and ctx.params[_view_chain(v.args[0])[0]].source_ndim != 0}
+            | {v.args[0].args[0] for v in values if v.op == "offsets"})
         grid = tuple(ctx.views[arranged[0]].level_shapes[0])
         self.programs = int(np.prod(grid)) if grid else 1
         self.lds = {}
@@ -1034,25 +1076,28 @@ class TilePlan(GenericPlan):
                 "    }",
             ]))
         self.raw_writes = []
+        self.view_targets = sorted({_view_chain(e[1])[0] for e in ctx.program.effects if e[0] == "view_store"})
         for k, eff in enumerate(ctx.program.effects):
             blocks.append(self._effect(em, k, eff))
-        self.loaded = sorted({v.args[0].args[0] for v in values if v.op == "load"
-                              and ctx.params[v.args[0].args[0]].source_ndim != 0})
+        self.loaded = sorted({_view_chain(v.args[0])[0] for v in values if v.op == "load"
+                              and ctx.params[_view_chain(v.args[0])[0]].source_ndim != 0})
         # tensors reached only through pointers or source indexing: a plain pointer argument
-        self.raw = sorted((self.raw_reads | set(self.raw_writes)) - set(self.loaded) - set(self.outputs))
-        self.scalars = [v.args[0].args[0] for v in values if v.op == "load"
+        self.raw = sorted((self.raw_reads | set(self.raw_writes)) - set(self.loaded) - set(self.outputs)
+                          - set(self.view_targets))
+        self.scalars = [v.args[0].args[0] for v in values if v.op == "load" and v.args[0].op == "param"
                         and ctx.params[v.args[0].args[0]].source_ndim == 0]
         self.scalars = list(dict.fromkeys(self.scalars))
         self.offsets = sorted({(v.args[0].args[0], int(v.args[1])) for v in values if v.op == "offsets"})
-        self.index_names = list(dict.fromkeys(self.outputs + self.loaded))
-        self.tile_sizes = {n: int(np.prod(_tile_shape(ctx, n))) if _tile_shape(ctx, n) else 1
+        self.index_names = list(dict.fromkeys(self.outputs + self.view_targets + self.loaded))
+        self.tile_sizes = {n: int(np.prod([int(np.prod(l)) for l in ctx.views[n].level_shapes[1:]]))
                            for n in self.index_names}
         self.offset_lengths = {(n, d): (_tile_shape(ctx, n)[d] if _tile_shape(ctx, n) else 1) for n, d in self.offsets}
         self.scalar_types = {n: em.scalar_type(n) for n in self.scalars}
         params = [f"const int* __restrict__ t_{n}" for n in self.index_names]
         params += [f"const int* __restrict__ f_{n}_{d}" for n, d in self.offsets]
         params += [f"const {_STORAGE[_torch_dtype_name(ctx.dtypes[n])][0]}* __restrict__ p_{n}" for n in self.loaded]
-        params += [f"{_STORAGE[_torch_dtype_name(ctx.dtypes[n])][0]}* __restrict__ p_{n}" for n in self.outputs]
+        params += [f"{_STORAGE[_torch_dtype_name(ctx.dtypes[n])][0]}* __restrict__ p_{n}"
+                   for n in self.outputs + self.view_targets]
         params += [("" if n in self.raw_writes else "const ") + f"{_STORAGE[_torch_dtype_name(ctx.dtypes[n])][0]}* p_{n}"
                    for n in self.raw]
         params += [f"{_STORAGE[self.scalar_types[n]][0]} s_{n}" for n in self.scalars]
@@ -1063,6 +1108,18 @@ class TilePlan(GenericPlan):
 
     def index_expr(self, name, lin):
         return f"t_{name}[pb_{name} + {lin}]"
+
+    def level_lin(self, name, ks, inner):
+        """Offset, within a program's part of ``name``'s index table, of element ``inner`` of
+        the level reached by the constant level indices ``ks``."""
+        levels = [tuple(l) for l in self.ctx.views[name].level_shapes[1:]]
+        terms = []
+        for i, k in enumerate(ks):
+            if len(levels[i]) != 1 or not 0 <= k < levels[i][0]:
+                raise LoweringError(f"level index {k} of `{name}` needs a 1-D level that holds it")
+            below = int(np.prod([int(np.prod(l)) for l in levels[i + 1:]]))
+            terms.append(f"{k * below}LL")
+        return " + ".join(terms + [inner]) if terms else inner
 
     def extent(self, name):
         """Elements from a tensor's first to one past its last element (its storage span)."""
@@ -1077,6 +1134,32 @@ class TilePlan(GenericPlan):
         """One side effect: a scatter into a source, a store or an atomic add through a pointer,
         element by element over the broadcast shape of its operands, masked to the tensor."""
         kind = eff[0]
+        if kind == "view_store":
+            name, ks = _view_chain(eff[1])
+            value = eff[2]
+            levels = self.ctx.views[name].level_shapes
+            shape = tuple(levels[1 + len(ks)]) if 1 + len(ks) < len(levels) else ()
+            sv = self.shapes[id(value)]
+            if _bcast_shapes(sv, shape) != shape:
+                raise LoweringError(f"a value of shape {sv} is stored to a level of shape {shape}")
+            n = int(np.prod(shape)) if shape else 1
+            coords = _unravel("j", shape)
+            body = em.context(value, coords[len(coords) - len(sv):] if sv else (), f"e{k}_")
+            t = _torch_dtype_name(self.ctx.dtypes[name])
+            src = em.type_of(value)
+            src = "float32" if src == "weak" else src
+            val = em.operand(value, src) if value.op in _CONSTLIKE else em.names[id(value)]
+            if em.work(src) != em.work(t):
+                val = f"(({em.work(t)}){val})"
+            return "\n".join([
+                f"    for (long long j = tid; j < {n}LL; j += 256) {{  // store into {name}{list(ks)}",
+                f"      const int oi = {self.index_expr(name, self.level_lin(name, ks, 'j'))};",
+                "      if (oi < 0) continue;",
+                *body,
+                f"      p_{name}[oi] = {_STORAGE[t][3].format(val)};",
+                "    }",
+                "    __syncthreads();",
+            ])
         if kind == "src_store":
             name, indices, value = eff[1], eff[2], eff[3]
             operands = list(indices) + [value]
@@ -1166,7 +1249,7 @@ class TilePlan(GenericPlan):
         argv = [ctypes.c_void_p(tables[n].data_ptr()) for n in self.index_names]
         argv += [ctypes.c_void_p(offset_tables[k].data_ptr()) for k in self.offsets]
         argv += [ptrs[n] for n in self.loaded]
-        argv += [ptrs[n] for n in self.outputs]
+        argv += [ptrs[n] for n in self.outputs + self.view_targets]
         argv += [ptrs[n] for n in self.raw]
         svals = {n: ctypes.c_int64() if self.scalar_types[n] == "int64" else ctypes.c_float() for n in self.scalars}
         argv += [svals[n] for n in self.scalars]
@@ -1218,4 +1301,19 @@ def match_generic(ctx):
     found = _analyse_tile(ctx)
     if found is not None:
         return TilePlan(ctx, *found)
+    if ctx.program.loops and ctx.relower is not None:
+        # loops whose trip counts are known now: unrolled, the program may be a tile program
+        resolve = _Emitter(ctx).const_value
+
+        def unroll(trip):
+            c = resolve(trip) if isinstance(trip, Value) else trip
+            return c if isinstance(c, int) and not isinstance(c, bool) and 0 <= c <= MAX_UNROLL else None
+
+        program = ctx.relower(unroll)
+        if not program.loops:
+            unrolled = copy.copy(ctx)
+            unrolled.program = program
+            found = _analyse_tile(unrolled)
+            if found is not None:
+                return TilePlan(unrolled, *found)
     return None

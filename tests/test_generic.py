@@ -653,3 +653,50 @@ def test_data_ptr_atomic_sum():
     out = torch.zeros(1, dtype=inp.dtype, device="cuda")
     kernel(inp, out)
     assert torch.allclose(out[0], torch.sum(inp), rtol=1e-4, atol=1e-3)
+
+
+# ------------------------------------------------------------------ loops over tiles (unrolled)
+def tiled_arrangement(x, out):
+    arranged = []
+    for tensor in (x, out):
+        tensor = tensor.tile((1, 256)).tile((1, -1))
+        tensor.dtype = tensor.dtype.squeeze((0,))
+        tensor.dtype.dtype = tensor.dtype.dtype.squeeze((0,))
+        arranged.append(tensor)
+    return tuple(arranged)
+
+
+def tiled_normalize(x, out):
+    # reference tests/test_tiled_reduction_loops.py:22-31
+    accumulator = ntl.zeros(x.dtype.shape, dtype=ntl.float32)
+    for i in range(x.shape[0]):
+        block = ntl.cast(x[i], ntl.float32)
+        accumulator += block * block
+    scale = ntl.rsqrt(ntl.sum(accumulator) / x.source.shape[1] + 1e-5)
+    for i in range(x.shape[0]):
+        out[i] = x[i] * scale
+
+
+def test_tiled_reduction_loop_is_unrolled():
+    k = ninetoothed.make(tiled_arrangement, tiled_normalize, (Tensor(2, other=0), Tensor(2)))
+    assert k._abi["outputs"] == ("out",)
+    x = torch.empty((7, 2050))[:, ::2]
+    plan = _plan(k, x, torch.empty((7, 1025)))
+    assert plan.describe()["family"] == "generic" and plan.describe()["reductions"] == 1
+    src = plan.source()
+    assert src.count("p_out[oi]") == 5  # one level store per column tile
+    assert "acc = (acc + (" in src and ">= 0)) ?" not in src.split("acc = (acc")[1].split("\n")[0]
+    assert len(GenericPlan.compile(src)) > 1000
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", (torch.float16, torch.float32))
+@pytest.mark.parametrize("width", (17, 256, 1025))
+def test_tiled_reduction_loop_runtime(dtype, width):
+    # reference tests/test_tiled_reduction_loops.py:46-68
+    kernel = ninetoothed.make(tiled_arrangement, tiled_normalize, (Tensor(2, other=0), Tensor(2)), max_num_configs=1)
+    x = torch.randn((7, width * 2), device="cuda", dtype=dtype)[:, ::2]
+    out = torch.empty((7, width), device="cuda", dtype=dtype)
+    kernel(x, out)
+    expected = x.float() * torch.rsqrt(x.float().square().mean(dim=1, keepdim=True) + 1e-5)
+    torch.testing.assert_close(out, expected.to(dtype))
