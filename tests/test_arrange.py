@@ -197,3 +197,36 @@ def test_getitem_and_ravel():
     assert r.shape == (2, 2, 2, 3)
     # element (tile row, tile col, i, j) = (2 * tile_row + i) * 6 + 3 * tile_col + j
     assert np.array_equal(r.eval(), np.arange(24).reshape(2, 2, 2, 3).transpose(0, 2, 1, 3))
+
+
+@pytest.mark.parametrize("shape, indices", (
+    # the cases of reference tests/test_getitem.py:7-24, checked against numpy's own indexing
+    ((3, 4, 2), slice(None, None, None)),
+    ((3, 4, 2), slice(0, -1, 2)),
+    ((2, 3, 4, 5), slice(1, None, 2)),
+    ((3, 4, 2), (slice(None), 1, slice(None))),
+    ((3, 4, 2), (1, slice(None), None)),
+    ((3, 4, 2), (slice(None, None, -1), 0, slice(1, -1))),
+    ((3, 4, 2), (..., 1)),
+    ((3, 4, 2), (None, slice(None), 1, slice(None))),
+    ((6, 5), (slice(2, 4, None), slice(1, 4, None))),
+))
+def test_getitem_matches_numpy(shape, indices):
+    out = Tensor(shape=shape)[indices].eval()
+    assert np.array_equal(out, np.arange(int(np.prod(shape))).reshape(shape)[indices])
+
+
+def test_unsqueeze_golden():
+    # the expected arrays of reference tests/test_unsqueeze.py:7-57
+    x = Tensor(1)
+    bm, bn = ninetoothed.block_size(), ninetoothed.block_size()
+    subs = {x: {"shape": (5,)}, bm: 2, bn: 3}
+    u = x.unsqueeze(0)
+    assert np.array_equal(u.eval(subs), np.array([[0, 1, 2, 3, 4]]))
+    ue = u.expand((3, -1))
+    assert np.array_equal(ue.eval(subs), np.array([[0, 1, 2, 3, 4]] * 3))
+    assert np.array_equal(ue.tile((bm, bn)).eval(subs), np.array([
+        [[[0, 1, 2], [0, 1, 2]], [[3, 4, -1], [3, 4, -1]]],
+        [[[0, 1, 2], [-1, -1, -1]], [[3, 4, -1], [-1, -1, -1]]],
+    ]))
+    assert np.array_equal(x.tile((bn,)).unsqueeze(0).eval(subs), np.array([[[0, 1, 2], [3, 4, -1]]]))
