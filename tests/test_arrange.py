@@ -230,3 +230,21 @@ def test_unsqueeze_golden():
         [[[0, 1, 2], [-1, -1, -1]], [[3, 4, -1], [-1, -1, -1]]],
     ]))
     assert np.array_equal(x.tile((bn,)).unsqueeze(0).eval(subs), np.array([[[0, 1, 2], [3, 4, -1]]]))
+
+
+def test_simulate_arrangement_golden():
+    # reference tests/test_debugging.py:14-251: the addmm arrangement's source and target tensors
+    import torch
+
+    from ninetoothed_amd.debugging import simulate_arrangement
+
+    g, targets = _addmm_golden()
+    m, n, k, b = g["m"], g["n"], g["k"], g["block_size"]
+    arrangement = functools.partial(pg.addmm_arrangement, BLOCK_SIZE_M=b, BLOCK_SIZE_N=b, BLOCK_SIZE_K=b)
+    tensors = (Tensor(shape=(m, n)), Tensor(shape=(m, k)), Tensor(shape=(k, n)), Tensor(0), Tensor(0),
+               Tensor(shape=(m, n)))
+    sources, got = simulate_arrangement(arrangement, tensors, device="cpu")
+    for t, expected in zip(sources, g["source_tensors"]):
+        assert torch.equal(t, torch.tensor(expected))
+    for t, expected in zip(got, targets):
+        assert torch.equal(t, torch.from_numpy(expected).to(torch.int64))
