@@ -579,6 +579,15 @@ class GenericPlan:
                 linear[n] = valid  # e -> e, masked from `valid` on: no table
             else:
                 tables[n] = tab
+        if tables and not self.offsets:
+            # Every operand indexed by one table that is a permutation of 0..n-1: an
+            # element-parallel program may visit the elements in memory order instead.
+            ref = next(iter(tables.values()))
+            same = all(np.array_equal(t, ref) for t in tables.values()) and len(tables) == len(self.index_names)
+            if same:
+                valid = ref[ref >= 0]
+                if np.array_equal(np.sort(valid), np.arange(valid.size, dtype=valid.dtype)):
+                    return {}, {n: int(valid.size) for n in self.index_names}, set(), {}, int(valid.size)
         offset_tables, linear_offsets = {}, set()
         for n, d in self.offsets:
             q = self._offsets_table(n, d, maps.get(n))

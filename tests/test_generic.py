@@ -734,3 +734,35 @@ def test_libdevice_call_inside_reduction():
     out = torch.full((3,), -12345.0, device="cuda")
     kernel(x, y, out)
     torch.testing.assert_close(out, torch.fmod(x, y).sum(1))
+
+
+def app_axpy(x, y, out):
+    out = x * 2.0 + y  # noqa: F841
+
+
+def test_same_layout_operands_walk_memory_order():
+    # 2-D tiles of three same-layout tensors: one permutation table for all -> no tables read
+    k = ninetoothed.make(lambda x, y, o: (x.tile((16, 32)), y.tile((16, 32)), o.tile((16, 32))), app_axpy,
+                         (Tensor(2), Tensor(2), Tensor(2)))
+    v = torch.empty(70, 90)
+    plan = _plan(k, v, v, v)
+    (src,) = plan.sources_for({"x": v, "y": v, "out": v})
+    body = src.split("nt_generic(")[1]
+    assert "t_x[e]" not in body and "t_out[e]" not in body and "(e < 6300LL" in body
+    # a transposed operand keeps its table
+    w = torch.empty(90, 70).t()
+    (src,) = plan.sources_for({"x": w, "y": v, "out": v})
+    assert "t_x[e]" in src
+
+
+@pytest.mark.gpu
+def test_two_d_tiled_elementwise():
+    k = ninetoothed.make(lambda x, y, o: (x.tile((16, 32)), y.tile((16, 32)), o.tile((16, 32))), app_axpy,
+                         (Tensor(2), Tensor(2), Tensor(2)))
+    x, y = torch.randn(70, 90, device="cuda"), torch.randn(70, 90, device="cuda")
+    out = torch.empty_like(x)
+    k(x, y, out)
+    assert torch.equal(out, x * 2.0 + y)
+    xt = torch.randn(90, 70, device="cuda").t()
+    k(xt, y, out)
+    assert torch.equal(out, xt * 2.0 + y)
