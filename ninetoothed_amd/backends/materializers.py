@@ -84,13 +84,23 @@ class HipMaterializer(Materializer):
         kernel = compilation.kernel
         kernel.prelower()
         code_objects, plans = {}, []
+        name = compilation.artifact.kernel_name
         static = kernel.static_values()
+        cpp = {"unavailable": "shapes, strides or dtypes are not all fixed at definition"}
         if static is not None:
             plan = kernel.specialize(static, {})
             plans.append(plan.describe())
             for source in getattr(plan, "sources_for", lambda values: [])(static):
                 code_objects[GenericPlan.digest(source)] = GenericPlan.code_object(source)
-        name = compilation.artifact.kernel_name
+            from ninetoothed_amd.backends import cpp_export
+
+            try:
+                code = cpp_export.source(name, plan, kernel, static, set(compilation.launch_abi["outputs"]))
+                library = cpp_export.build(name, code, out)
+                cpp = {"header": str(out / "ninetoothed.h"), "source": str(out / f"{name}.launch.cpp"),
+                       "library": str(library), "symbol": f"launch_{name}"}
+            except cpp_export.Unsupported as exc:
+                cpp = {"unavailable": str(exc)}
         bundle_path = out / f"{name}.program.pkl"
         bundle = {"schema": 1, "abi_version": _lib.ABI_VERSION, "kernel": kernel.bundle(), "code_objects": code_objects}
         bundle_path.write_bytes(pickle.dumps(bundle))
@@ -105,6 +115,7 @@ class HipMaterializer(Materializer):
             "lowered_for": [dict(k) for k in kernel.bundle()["lowered"]],
             "plans": plans,
             "code_objects": sorted(code_objects),
+            "cpp": cpp,
             "abi": {k: list(v) if isinstance(v, tuple) else v for k, v in compilation.launch_abi.items()},
             "artifact": dict(compilation.artifact.metadata),
         }, indent=1, default=str))

@@ -153,3 +153,111 @@ def test_reloaded_handles_compute_the_same(tmp_path):
     handle(x, e, out)
     load_built_artifact(handle._built_artifact)(x, e, out2)
     assert torch.allclose(out, torch.pow(x, e)) and torch.equal(out2, out)
+
+
+# ------------------------------------------------------------------ standalone C++ launchers
+import ctypes  # noqa: E402
+
+
+class NineToothedTensor(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("shape", ctypes.POINTER(ctypes.c_uint64)),
+                ("strides", ctypes.POINTER(ctypes.c_int64))]
+
+
+def _nt_tensor(t, keep):
+    if t.dim() == 0 or not hasattr(t, "data_ptr"):
+        raise TypeError
+    shape = (ctypes.c_uint64 * t.dim())(*t.shape)
+    strides = (ctypes.c_int64 * t.dim())(*t.stride())
+    keep += [shape, strides]
+    return NineToothedTensor(ctypes.c_void_p(t.data_ptr()), shape, strides)
+
+
+def _nt_scalar(value, keep):
+    v = ctypes.c_double(value)
+    keep.append(v)
+    return NineToothedTensor(ctypes.cast(ctypes.pointer(v), ctypes.c_void_p), None, None)
+
+
+def _static_matmul(tmp_path, name="mm_static"):
+    import programs as pg
+
+    f16 = ninetoothed.float16
+    tensors = (Tensor(shape=(256, 512), dtype=f16), Tensor(shape=(512, 128), dtype=f16),
+               Tensor(shape=(256, 128), dtype=f16))
+    c = DEFAULT_COMPILER.compile(CompileRequest(application=pg.matmul_application, arrangement=pg.matmul_arrangement,
+                                                tensors=tensors, kernel_name=name))
+    return DEFAULT_COMPILER.materialize(c, output_dir=tmp_path, mode="aot")
+
+
+def test_cpp_launcher_is_built_and_checks_its_arguments(tmp_path):
+    h = _static_matmul(tmp_path)
+    manifest = json.loads(Path(h._built_artifact.manifest_path).read_text())
+    cpp = manifest["cpp"]
+    assert cpp["symbol"] == "launch_mm_static" and Path(cpp["library"]).is_file()
+    assert "NineToothedTensor" in Path(cpp["header"]).read_text()
+    lib = ctypes.CDLL(cpp["library"])
+    fn = lib.launch_mm_static
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p] + [NineToothedTensor] * 3
+    keep = []
+    a, b, out = torch.empty(256, 512, dtype=torch.float16), torch.empty(512, 128, dtype=torch.float16), \
+        torch.empty(256, 128, dtype=torch.float16)
+    bad = torch.empty(256, 64, dtype=torch.float16)  # wrong shape: rejected before anything is launched
+    assert fn(None, _nt_tensor(a, keep), _nt_tensor(b, keep), _nt_tensor(bad, keep)) == 1
+    nulls = NineToothedTensor(None, _nt_tensor(out, keep).shape, _nt_tensor(out, keep).strides)
+    assert fn(None, _nt_tensor(a, keep), _nt_tensor(b, keep), nulls) == 1
+
+
+def test_cpp_launcher_reasons_are_recorded(tmp_path):
+    # symbolic shapes, and a generic kernel: no launcher, with the reason in the manifest
+    h = ninetoothed.make(lambda x, y, o: (x.tile((64,)), y.tile((64,)), o.tile((64,))), _add_app(), (
+        Tensor(1), Tensor(1), Tensor(1)), caller="hip", output_dir=tmp_path / "sym")
+    assert "not all fixed" in json.loads(Path(h._built_artifact.manifest_path).read_text())["cpp"]["unavailable"]
+    h = DEFAULT_COMPILER.materialize(_pow_kernel(), output_dir=tmp_path / "pow", mode="aot")
+    assert "generic" in json.loads(Path(h._built_artifact.manifest_path).read_text())["cpp"]["unavailable"]
+
+
+def _add_app():
+    def application(input, other, output):
+        output = input + other  # noqa: F841
+
+    return application
+
+
+@pytest.mark.gpu
+def test_cpp_launchers_compute(tmp_path):
+    import programs as pg
+
+    h = _static_matmul(tmp_path / "mm")
+    cpp = json.loads(Path(h._built_artifact.manifest_path).read_text())["cpp"]
+    fn = getattr(ctypes.CDLL(cpp["library"]), cpp["symbol"])
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p] + [NineToothedTensor] * 3
+    a = torch.randn(256, 512, device="cuda", dtype=torch.float16)
+    b = torch.randn(512, 128, device="cuda", dtype=torch.float16)
+    out = torch.empty(256, 128, device="cuda", dtype=torch.float16)
+    keep = []
+    stream = torch.cuda.current_stream().cuda_stream
+    assert fn(stream, _nt_tensor(a, keep), _nt_tensor(b, keep), _nt_tensor(out, keep)) == 0
+    torch.cuda.synchronize()
+    assert torch.allclose(out.float(), (a.float() @ b.float()).half().float(), atol=5e-2, rtol=1e-2)
+
+    # addmm: 0-d alpha/beta are host doubles
+    f16, f64 = ninetoothed.float16, ninetoothed.float64
+    tensors = (Tensor(shape=(256, 128), dtype=f16), Tensor(shape=(256, 512), dtype=f16),
+               Tensor(shape=(512, 128), dtype=f16), Tensor(0, dtype=f64), Tensor(0, dtype=f64),
+               Tensor(shape=(256, 128), dtype=f16))
+    c = DEFAULT_COMPILER.compile(CompileRequest(application=pg.addmm_application, arrangement=pg.addmm_arrangement,
+                                                tensors=tensors, kernel_name="addmm_static"))
+    h = DEFAULT_COMPILER.materialize(c, output_dir=tmp_path / "addmm", mode="aot")
+    cpp = json.loads(Path(h._built_artifact.manifest_path).read_text())["cpp"]
+    fn = getattr(ctypes.CDLL(cpp["library"]), cpp["symbol"])
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p] + [NineToothedTensor] * 6
+    inp = torch.randn(256, 128, device="cuda", dtype=torch.float16)
+    assert fn(stream, _nt_tensor(inp, keep), _nt_tensor(a, keep), _nt_tensor(b, keep), _nt_scalar(0.5, keep),
+              _nt_scalar(2.0, keep), _nt_tensor(out, keep)) == 0
+    torch.cuda.synchronize()
+    ref = 0.5 * inp.float() + 2.0 * (a.float() @ b.float()).half().float()
+    assert torch.allclose(out.float(), ref, atol=1e-1, rtol=1e-2)
