@@ -415,7 +415,7 @@ __global__ __launch_bounds__(512) void conv_nhwc_kernel(const uint16_t* __restri
   }
 }
 
-// Four-wave form of conv_nhwc_kernel (the GEMM's gemm_w4_kernel schedule): 256 lanes, one
+// Four-wave form of conv_nhwc_kernel: 256 lanes, one
 // wave per SIMD in a 2 (k) x 2 (m) grid, each owning 128 x 128 of the 256 x 256 tile
 // with its accumulators in the accumulator file.  Both operands are k-contiguous rows
 // (filter rows of the K-R-S-C filter, im2col rows of the padded N-H-W-C input), so both
@@ -423,11 +423,11 @@ __global__ __launch_bounds__(512) void conv_nhwc_kernel(const uint16_t* __restri
 // per load i, chunk lane % 8.  The im2col rows of a lane have per-lane base offsets; the
 // (r, s, c0) of a k-tile is one scalar offset (a k-tile never crosses an (r, s) block,
 // C % 64 == 0), and rows past M take an offset past the end of the resource so their
-// loads return zeros.  Fixed 64-slot issue schedule per k-tile as in gemm_w4_kernel:
-// fragments read a slice ahead; b (im2col) rows stored in slots 0..21 and a (filter)
+// loads return zeros.  Fixed 64-slot issue schedule per 64-deep k-tile (one MFMA per
+// slot, its memory work fenced after it): fragments read a slice ahead; b (im2col) rows stored in slots 0..21 and a (filter)
 // rows in 22..43, each refetched for tile kt + 2 in the slot it was stored; barrier
 // before slot 48.  Epilogue: 16-row halves of each wave's accumulators staged in a
-// spare 32 KiB of LDS (no barrier), then each lane stores 8 consecutive output
+// spare 32 KiB of LDS (no workgroup barrier: each wave has its own part), then each lane stores 8 consecutive output
 // positions of one channel (its positions are fixed, so (n, p, q) is computed once).
 namespace cw4 {
 constexpr int A_BYTES = CB_K * TILE_K * 2;  // 32 KiB
@@ -613,11 +613,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
+        wave_lds_order();  // the previous half's reads come first
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
           for (int r = 8 * h; r < 8 * h + 8; ++r)
             stage[(acc_row(r, lane) - 16 * h) * 128 + j * 32 + (lane & 31)] = acc[i][j][r];
+        wave_lds_order();  // every lane's writes before any lane reads
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
           const int rr = t * 4 + (lane >> 4);

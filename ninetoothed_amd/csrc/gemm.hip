@@ -2,10 +2,10 @@
 //
 // fp16 / bf16 (MFMA-bound; 2*M*N*K flops per launch): workgroup tile 256 x 256 x 64 on
 // v_mfma_f32_32x32x16_{f16,bf16}.  Kernels, fastest first:
-//   gemm_w4_kernel     a k-contiguous, b n-contiguous, M, N multiples of 256, K of 128:
-//                      4 waves of 128 x 128 (one per SIMD, accumulators in the
-//                      accumulator file), a fixed 64-slot issue schedule per k-tile;
-//   gemm_fast8_kernel  same layouts, K a multiple of 64: 8 waves of 64 x 128;
+//   gemm_dma_kernel    a k-contiguous, b n-contiguous, M, N multiples of 256, K of 64 and at
+//                      least 128: 8 waves of 128 x 64, both operands DMA'd from HBM into a
+//                      four-stage LDS ring (k-tiles of 32), b read with transposing LDS reads;
+//   gemm_fast8_kernel  same layouts, other K multiples of 64: 8 waves of 64 x 128;
 //   gemm_mfma_kernel   anything else (any strides, ragged edges, zero fill).
 // Both operands sit in LDS k-contiguous ([m][k] for a, [n][k] for b) so that each lane
 // fetches its 8 k-values for an MFMA with one ds_read_b128.  b arrives n-contiguous
@@ -37,8 +37,8 @@ struct GemmArgs {
   float alpha, beta;
   int out_dtype, round_dtype;
   int tiles_m, tiles_n;
-  int c_pre;  // gemm_w4_kernel: 16-bit out (and c) with unit column stride, 16-byte aligned rows,
-              // c panel offsets within 32 bits: c is fetched during the last k-tile
+  int c_pre;  // gemm_dma_kernel's fast epilogue: 16-bit out (and c) with unit column stride,
+              // 16-byte aligned rows, out and c panel offsets within 32 bits
 };
 
 // Map a linear workgroup id to an output tile so that consecutive ids on one XCD
@@ -393,298 +393,238 @@ __global__ __launch_bounds__(512) void gemm_fast8_kernel(GemmArgs g) {
   gemm_epilogue<2, 4>(g, acc, smem, wave, lane, m0 + wm * 64, n0 + wn * 128);
 }
 
-// Fast path, four-wave form: 256 lanes, one wave per SIMD in a 2 x 2 grid, each owning
-// 128 x 128 of the 256 x 256 tile (256 accumulators, kept in the accumulator file).
-// Per 16-deep slice a wave reads 8 KiB of fragments for 16 MFMAs, two thirds of the
-// LDS traffic per flop of a 64 x 128 wave tile.
-//
-// LDS (bytes): a tiles at 0 and 32 Ki, b tiles at 64 Ki and 96 Ki, so with the buffer
-// index static (the k loop is unrolled by two) every LDS access is a per-lane base
-// register plus an immediate offset.  Global operands go through buffer loads whose
-// k-dependent part is a scalar offset, so the loop spends vector ALU only on the b
-// transposes (v_perm_b32).  Each k-tile is a fixed issue schedule of 64 MFMA slots
-// (below): fragments read a slice ahead, tile kt+1 stored into the other buffer and
-// tile kt+2 fetched at an even rate, barrier before the last slice.
-
-namespace w4 {
-constexpr int A_BYTES = GB_M * GB_K * 2;  // 32 KiB
-constexpr int B_BASE = 2 * A_BYTES;       // 64 KiB
-constexpr int STAGE_BASE = 4 * A_BYTES;   // 128 KiB: epilogue staging, 8 KiB per wave
-constexpr int STAGE_BYTES = 32768;
-
-__device__ __forceinline__ uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel) {
-  return __builtin_amdgcn_perm(s0, s1, sel);
+// DMA form: 512 lanes, two waves per SIMD in a 2 (m) x 4 (n) grid, each owning 128 x 64 of
+// the 256 x 256 tile (128 accumulators), k-tiles of 32.  Both operands go from HBM straight
+// into LDS (buffer_load ... lds: lane l of a load writes bytes 16 l .. 16 l + 15 past the
+// LDS address in M0), so the k loop holds no staging registers and issues no LDS stores.
+//   a: [m][k] rows of 64 bytes whose four 16-byte chunks are XOR-swizzled by (row / 4) % 4;
+//      each lane fetches the global chunk that belongs at its LDS position; fragments are
+//      ds_read_b128 (16 lanes of one pass hit 16 distinct bank groups).
+//   b: [k][n] as in HBM, rows of 512 bytes whose 64-byte chunks (32 n) are XOR-swizzled by
+//      bsw(k); fragments come from two ds_read_b64_tr_b16 each.  That instruction works on
+//      groups of 16 lanes: lane 4 r + q reads 4 consecutive 16-bit values, and lane j of
+//      the group receives value j % 4 of lanes j / 4, 4 + j / 4, 8 + j / 4, 12 + j / 4.  So if
+//      lane 4 r + q reads row k0 + r at columns 4 q .. 4 q + 3, lane j receives column j at
+//      rows k0 .. k0 + 3: the MFMA's b operand (8 consecutive k of one n) in two reads.
+// Four LDS stages of 32 KiB (a at 16 Ki * stage, b at 64 Ki + 16 Ki * stage) and 32 KiB of
+// epilogue staging at 128 Ki.  Tile kt+3 is fetched during tile kt into the stage of tile
+// kt-1: every read of that stage has completed by then, since LDS operations complete in
+// order and the wave has already waited for a later read of tile kt.  So the one barrier
+// per k-tile (which also publishes tile kt+1, each wave having waited for its own loads)
+// needs no wait for outstanding reads, and a load has two k-tiles to land.
+// The loads are issued from inline assembly: the compiler would otherwise make every LDS
+// read wait for them.  The waves of a SIMD take turns on the matrix core, so one's LDS
+// waits hide behind the other's MFMAs.  Per 32-deep k-tile a wave issues 16 MFMAs, 8
+// ds_read_b128, 8 transposing reads and 4 loads.
+namespace dma {
+constexpr int STAGES = 4, STAGE = 16384, B0 = 65536, EPI = 131072;
+__device__ __forceinline__ int bsw(int k) { return (k & 3) | (((k >> 3) & 1) << 2); }
+__device__ __forceinline__ int asw(int row, int chunk) { return chunk ^ ((row >> 2) & 3); }
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+// Buffer resource: base, no stride, `bytes` records (offsets at or past it read zero).
+__device__ __forceinline__ u32x4 rsrc(const void* base, uint32_t bytes) {
+  const uint64_t p = (uint64_t)base;
+  return u32x4{(uint32_t)p, (uint32_t)(p >> 32) & 0xffffu, bytes, 0x00020000u};
 }
-// 8x8 transpose of 16-bit values, as transpose8x8 but one v_perm_b32 per output dword.
-__device__ __forceinline__ void transpose8x8_perm(const u32x4 (&in)[8], u32x4 (&out)[8]) {
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int d = j >> 1;
-    const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-    out[j] = u32x4{perm(in[1][d], in[0][d], sel), perm(in[3][d], in[2][d], sel), perm(in[5][d], in[4][d], sel),
-                   perm(in[7][d], in[6][d], sel)};
-  }
+// 16 bytes per lane from buffer `rs` at voffset + soffset into LDS at lds_addr + 16 * lane.
+__device__ __forceinline__ void load_lds16(u32x4 rs, uint32_t lds_addr, int voffset, int soffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(lds_addr), "v"(voffset), "s"(rs), "s"(soffset)
+               : "memory", "m0");
 }
-}  // namespace w4
+}  // namespace dma
 
 template <typename T>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_w4_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (GB_M + GB_N) * GB_K + w4::STAGE_BYTES / 2];
-  char* lds = (char*)smem;
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_dma_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(1024))) char lds[dma::EPI + 8 * 4096];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
-  const int wm = wave >> 1, wn = wave & 1;  // 2 x 2
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 2, wn = wave & 3;
   int tm, tn;
   tile_of(blockIdx.x, g.tiles_m, g.tiles_n, tm, tn);
   const int64_t m0 = (int64_t)tm * GB_M, n0 = (int64_t)tn * GB_N;
-  const int nk = (int)(g.K / GB_K);
+  const int nk = (int)(g.K / 32);
 
-  // Global side: a rows a_row + 32 i (i < 8), one 16-byte chunk each; b an 8(k) x 8(n)
-  // block.  Byte offsets within each operand's panel fit in 32 bits (checked on the host).
-  const int a_row = tid >> 3, a_chunk = tid & 7;
-  const int b_nb = tid & 31, b_kb = tid >> 5;
-  const __amdgpu_buffer_rsrc_t rsA = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)((const uint16_t*)g.a + m0 * g.sa_m), (short)0, (int)(((GB_M - 1) * g.sa_m + g.K) * 2), 0x00020000);
-  const __amdgpu_buffer_rsrc_t rsB = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)((const uint16_t*)g.b + n0), (short)0, (int)(((g.K - 1) * g.sb_k + GB_N) * 2), 0x00020000);
-  const int va = (int)(a_row * g.sa_m * 2 + a_chunk * 16);
-  const int vb = (int)(b_kb * 8 * g.sb_k * 2 + b_nb * 16);
-  const int a_istep = (int)(32 * g.sa_m * 2);  // bytes between a rows i and i+1
-  const int b_rstep = (int)(g.sb_k * 2);       // bytes between b rows r and r+1
-
-  // LDS side.  Stores: a row i*32 + a_row has the swizzle of i & 1 (rows 64 apart share
-  // it); b row b_nb*8 + j has its own.  Reads: fragment rows of i and i + 2 (j, j + 2)
-  // are 64 rows apart and share a swizzle.
-  int a_st[2], b_st[8], a_rd[4][2], b_rd[4][2];
+  // Global side (byte offsets within each operand's panel fit in 32 bits; checked on the host).
+  const u32x4 rsA = dma::rsrc((const uint16_t*)g.a + m0 * g.sa_m, (uint32_t)(((GB_M - 1) * g.sa_m + g.K) * 2));
+  const u32x4 rsB = dma::rsrc((const uint16_t*)g.b + n0, (uint32_t)(((g.K - 1) * g.sb_k + GB_N) * 2));
+  // Load q (0, 1) of this wave per k-tile: a rows 32 wave + 16 q + lane / 4, LDS chunk
+  // lane % 4; b rows 4 wave + 2 q + lane / 32, LDS bytes (lane % 32) * 16 of the row.
+  int va[2], vb[2];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int row = i * 32 + a_row;
-    a_st[i] = (row * GB_K + swz(row, a_chunk) * 8) * 2;
+  for (int q = 0; q < 2; ++q) {
+    const int ra = 32 * wave + 16 * q + (lane >> 2);
+    va[q] = (int)(ra * g.sa_m * 2) + dma::asw(ra, lane & 3) * 16;
+    const int kb = 4 * wave + 2 * q + (lane >> 5);
+    const int nb = 32 * (((lane & 31) >> 2) ^ dma::bsw(kb)) + 8 * (lane & 3);
+    vb[q] = (int)(kb * g.sb_k * 2) + nb * 2;
   }
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int row = b_nb * 8 + j;
-    b_st[j] = w4::B_BASE + (row * GB_K + swz(row, b_kb) * 8) * 2;
-  }
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int chunk = kk * 2 + (lane >> 5);
-      const int ra_row = wm * 128 + h * 32 + (lane & 31);
-      const int rb_row = wn * 128 + h * 32 + (lane & 31);
-      a_rd[kk][h] = (ra_row * GB_K + swz(ra_row, chunk) * 8) * 2;
-      b_rd[kk][h] = w4::B_BASE + (rb_row * GB_K + swz(rb_row, chunk) * 8) * 2;
-    }
-
-  // c of this wave's 128 x 128 block, fetched straight into LDS (buffer_load ... lds: lane
-  // l of a load writes bytes 16 l .. 16 l + 15 past the load's LDS address).  Vector x
-  // (slab i = x / 8, t = x % 8) covers rows i * 32 + t * 4 + lane / 16, columns
-  // (lane % 16) * 8 .. + 7, so its 1 KiB lands row-major at c_lds(x) + lane * 16.
-  // Slabs 0, 1 go to LDS buffer 0, slabs 2, 3 to buffer 1, each wave in its own 16 KiB.
-  // Without c (or without the fast epilogue) the resource has no records and the loads
-  // write zeros without touching memory.
-  const int64_t row_base = m0 + wm * 128, col_base = n0 + wn * 128;
-  const bool c_fetch = g.c_pre && g.c;
-  const __amdgpu_buffer_rsrc_t rsC = __builtin_amdgcn_make_buffer_rsrc(
-      c_fetch ? (void*)((const uint16_t*)g.c + row_base * g.sc_m + col_base) : (void*)g.a, (short)0,
-      c_fetch ? (int)((127 * g.sc_m + 128) * 2) : 0, 0x00020000);
-  const int vc = c_fetch ? (int)(((lane >> 4) * g.sc_m + (lane & 15) * 8) * 2) : 0;
-  const int c_rstep = c_fetch ? (int)(g.sc_m * 2) : 0;
-  auto c_lds = [&](int x) { return (wave >> 1) * w4::B_BASE + (x >> 4) * w4::A_BYTES + (wave & 1) * 16384 + (x & 15) * 1024; };
-  auto load_c_lds = [&](int x) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsC, (__attribute__((address_space(3))) void*)(lds + c_lds(x)), 16, vc,
-                                             ((x >> 3) * 32 + (x & 7) * 4) * c_rstep, 0, 0);
-  };
-
-  floatx16 acc[4][4];
-  zero_acc(acc);
-  u32x4 ra[8], rb[8];
-  auto load_a = [&](int kt) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) ra[i] = __builtin_amdgcn_raw_buffer_load_b128(rsA, va, i * a_istep + kt * 128, 0);
-  };
-  auto load_b = [&](int kt) {
-#pragma unroll
-    for (int r = 0; r < 8; ++r) rb[r] = __builtin_amdgcn_raw_buffer_load_b128(rsB, vb, (kt * 64 + r) * b_rstep, 0);
-  };
-  auto store_a = [&](auto buf_c) {
-    constexpr int OFF = decltype(buf_c)::value * w4::A_BYTES;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) *(u32x4*)(lds + a_st[i & 1] + (i >> 1) * 8192 + OFF) = ra[i];
-  };
-  auto store_b = [&](auto buf_c) {
-    constexpr int OFF = decltype(buf_c)::value * w4::A_BYTES;
-    u32x4 tb[8];
-    w4::transpose8x8_perm(rb, tb);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) *(u32x4*)(lds + b_st[j] + OFF) = tb[j];
-  };
-
-  typedef typename mfma_traits<T>::frag frag;
-  frag fa[2][4], fb[2][4];
-  u32x4 tb[8];
-  // Fragment x of a slice: x < 4 is a row block, x >= 4 a column block.
-  auto read_frag = [&](auto buf_c, int kk, int slot, int x) {
-    constexpr int OFF = decltype(buf_c)::value * w4::A_BYTES;
-    if (x < 4)
-      fa[slot][x] = *(const frag*)(lds + a_rd[kk][x & 1] + (x >> 1) * 8192 + OFF);
+  const int b_kstep = (int)(32 * g.sb_k * 2);
+  // Load u (0..3) of tile kt into its stage: a q0, b q0, a q1, b q1.
+  auto load_unit = [&](int u, int kt) {
+    const int st = (kt % dma::STAGES) * dma::STAGE, q = u >> 1;
+    if ((u & 1) == 0)
+      dma::load_lds16(rsA, lds0 + st + 2048 * wave + 1024 * q, va[q], kt * 64);
     else
-      fb[slot][x - 4] = *(const frag*)(lds + b_rd[kk][x & 1] + ((x - 4) >> 1) * 8192 + OFF);
+      dma::load_lds16(rsB, lds0 + dma::B0 + st + 2048 * wave + 1024 * q, vb[q], kt * b_kstep);
   };
-  auto read_frags = [&](auto buf_c, int kk, int slot) {
+
+  // Fragment reads.  a: row 128 wm + 32 i + lane % 32, chunk 2 s + lane / 32 (the swizzle
+  // depends on lane % 32 only).  b (two reads per fragment): lane (group g = lane / 16, r, q)
+  // reads row 16 s + 8 (g / 2) + 4 half + r at columns 64 wn + 32 j + 16 (g % 2) + 4 q .. + 3.
+  int a_rd[2], b_rd[2];
 #pragma unroll
-    for (int x = 0; x < 8; ++x) read_frag(buf_c, kk, slot, x);
-  };
-  auto mma1 = [&](int slot, int x) {
-    const int i = x >> 2, j = x & 3;
-    acc[i][j] = mfma_traits<T>::mma(fa[slot][i], fb[slot][j], acc[i][j]);
-  };
-  using B0 = std::integral_constant<int, 0>;
-  using B1 = std::integral_constant<int, 1>;
-
-  load_a(0);
-  load_b(0);
-  store_a(B0{});
-  store_b(B0{});
-  if (nk > 1) {
-    load_a(1);
-    load_b(1);
+  for (int s2 = 0; s2 < 2; ++s2) {
+    const int row = wm * 128 + (lane & 31);
+    a_rd[s2] = row * 64 + dma::asw(row, 2 * s2 + (lane >> 5)) * 16;
   }
-  __syncthreads();
-  read_frags(B0{}, 0, 0);
+  {
+    const int gq = lane >> 4, r = (lane & 15) >> 2, q = lane & 3;
+    const int f = r | ((gq >> 1) << 2);  // bsw of every row this lane reads
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      b_rd[j] = dma::B0 + (8 * (gq >> 1) + r) * 512 + (((2 * wn + j) ^ f) * 64) + (16 * (gq & 1) + 4 * q) * 2;
+  }
+  typedef typename mfma_traits<T>::frag frag;
+  frag fa[2][4], fb[2][2];
+  // Read unit x (0..5) of slice s2 of the tile in stage byte offset `st`, into slot s2:
+  // a0, b0, b1, a1, a2, a3, the order the slice's MFMAs consume them.
+  auto read_unit = [&](int x, int s2, int st) {
+    if (x == 0 || x >= 3) {
+      const int i = x == 0 ? 0 : x - 2;
+      fa[s2][i] = *(const frag*)(lds + a_rd[s2] + st + i * 2048);
+    } else {
+      const int j = x - 1;
+      const char* p = lds + b_rd[j] + st + s2 * 8192;
+      const dma::v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) dma::v4i16*)p);
+      const dma::v4i16 hi =
+          __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) dma::v4i16*)(p + 2048));
+      const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+      fb[s2][j] = __builtin_bit_cast(frag, u32x4{l2[0], l2[1], h2[0], h2[1]});
+    }
+  };
 
-  // Issue schedule of one k-tile: 64 MFMA slots m (slice m / 16, x = m % 16), each
-  // MFMA followed by the memory work of its slot, fenced so the order is kept:
-  //   fragment reads for the next slice: even x in slices 0-1, x < 8 in slices 2-3
-  //     (all done before the barrier / well before use), in the order the next
-  //     slice's MFMAs consume them (a0 b0 b1 b2 b3 a1 a2 a3);
-  //   b of tile kt+1: column j transposed in slot j, stored in slot 3j (0..21);
-  //     row r of tile kt+2 fetched in slot 8 + 3r (after every column is transposed);
-  //   a of tile kt+1: row block i stored in slot 22 + 3i (22..43), refetched for tile
-  //     kt+2 in the same slot;
-  //   barrier before slot 48 (slice 3), whose reads come from the other buffer;
-  //   last k-tile only: the wave's c vectors 0..15 fetched into LDS buffer 0 in slots
-  //     0..15 and 16..31 into buffer 1 in slots 48..63, so the epilogue's HBM reads
-  //     overlap the last 64 MFMAs.
-  // LDS writes are spread one per three MFMAs so four waves never fill the LDS data
-  // queue, and every global load has at least a half k-tile before its use.
+  floatx16 acc[4][2];
+  zero_acc(acc);
+
+  // nk >= 3 (the launcher checks): tiles 0..2 in flight, wait for tile 0.
+  for (int kt = 0; kt < 3; ++kt)
+    for (int u = 0; u < 4; ++u) load_unit(u, kt);
+  asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+#pragma unroll
+  for (int x = 0; x < 6; ++x) read_unit(x, 0, 0);
+
 #define NT_FENCE() __builtin_amdgcn_sched_barrier(0)
-  auto step = [&](auto cur_c, auto has1_c, auto has2_c, int kt) {
-    constexpr int CUR = decltype(cur_c)::value;
-    constexpr bool HAS1 = decltype(has1_c)::value, HAS2 = decltype(has2_c)::value;
-    using Cur = std::integral_constant<int, CUR>;
-    using Nxt = std::integral_constant<int, CUR ^ 1>;
-    constexpr int NOFF = (CUR ^ 1) * w4::A_BYTES;
-    const int k2 = kt + 2;
-    static_for<0, 64>([&](auto m_c) {
+  // One k-tile.  HAS1: a tile kt+1 exists (read its slice 0 during slice 1); LOAD: fetch
+  // tile kt+3; VM: loads allowed outstanding once tile kt+1 has landed (-1: no wait and no
+  // barrier, the last tile).
+  auto step = [&](auto has1_c, auto load_c, auto vm_c, int kt) {
+    constexpr bool HAS1 = decltype(has1_c)::value, LOAD = decltype(load_c)::value;
+    constexpr int VM = decltype(vm_c)::value;
+    const int st = (kt % dma::STAGES) * dma::STAGE, st1 = ((kt + 1) % dma::STAGES) * dma::STAGE;
+    static_for<0, 16>([&](auto m_c) {
       constexpr int m = decltype(m_c)::value;
-      constexpr int slice = m / 16, x = m % 16, slot = slice & 1;
-      if constexpr (m == 48) {
+      constexpr int s2 = m >> 3, x = m & 7;
+      if constexpr (m == 8 && VM >= 0) {
         NT_FENCE();
-        __syncthreads();
+        if constexpr (VM == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+        if constexpr (VM == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
         NT_FENCE();
       }
-      mma1(slot, x);
+      acc[x >> 1][x & 1] = mfma_traits<T>::mma(fa[s2][x >> 1], fb[s2][x & 1], acc[x >> 1][x & 1]);
       NT_FENCE();
-      constexpr bool rd = slice < 2 ? (x % 2 == 0) : (x < 8);
-      if constexpr (rd) {
-        constexpr int f = slice < 2 ? x / 2 : x;
-        constexpr int which = f == 0 ? 0 : (f <= 4 ? f + 3 : f - 4);
-        if constexpr (slice < 3)
-          read_frag(Cur{}, slice + 1, slot ^ 1, which);
+      if constexpr (x < 6) {
+        if constexpr (s2 == 0)
+          read_unit(x, 1, st);
         else if constexpr (HAS1)
-          read_frag(Nxt{}, 0, 0, which);
+          read_unit(x, 0, st1);
       }
-      if constexpr (HAS1) {
-        if constexpr (m < 8) {
-          constexpr int d = m >> 1;
-          constexpr uint32_t sel = (m & 1) ? 0x07060302u : 0x05040100u;
-          tb[m] = u32x4{w4::perm(rb[1][d], rb[0][d], sel), w4::perm(rb[3][d], rb[2][d], sel),
-                        w4::perm(rb[5][d], rb[4][d], sel), w4::perm(rb[7][d], rb[6][d], sel)};
-        }
-        if constexpr (m <= 21 && m % 3 == 0) *(u32x4*)(lds + b_st[m / 3] + NOFF) = tb[m / 3];
-        if constexpr (HAS2 && m >= 8 && m <= 29 && (m - 8) % 3 == 0) {
-          constexpr int r = (m - 8) / 3;
-          rb[r] = __builtin_amdgcn_raw_buffer_load_b128(rsB, vb, (k2 * 64 + r) * b_rstep, 0);
-        }
-        if constexpr (m >= 22 && m <= 43 && (m - 22) % 3 == 0) {
-          constexpr int i = (m - 22) / 3;
-          *(u32x4*)(lds + a_st[i & 1] + (i >> 1) * 8192 + NOFF) = ra[i];
-          if constexpr (HAS2) ra[i] = __builtin_amdgcn_raw_buffer_load_b128(rsA, va, i * a_istep + k2 * 128, 0);
-        }
-      }
-      // Last k-tile: buffer 0 has been idle since the previous tile's barrier, buffer 1
-      // since this one's (no fragment reads follow it).
-      if constexpr (!HAS1 && m < 16) load_c_lds(m);
-      if constexpr (!HAS1 && m >= 48) load_c_lds(m - 32);
+      if constexpr (s2 == 1 && LOAD && x < 4) load_unit(x, kt + 3);
       NT_FENCE();
     });
   };
 #undef NT_FENCE
   using T1 = std::integral_constant<bool, true>;
   using F1 = std::integral_constant<bool, false>;
-  // nk is even (the launcher checks): pairs of k-tiles, the last pair without prefetch.
+  using V4 = std::integral_constant<int, 4>;
+  using V0 = std::integral_constant<int, 0>;
+  using VN = std::integral_constant<int, -1>;
   int kt = 0;
-  for (; kt + 2 < nk; kt += 2) {
-    step(B0{}, T1{}, T1{}, kt);
-    step(B1{}, T1{}, T1{}, kt + 1);
-  }
-  step(B0{}, T1{}, F1{}, kt);
-  step(B1{}, F1{}, F1{}, kt + 1);
+  for (; kt + 3 < nk; ++kt) step(T1{}, T1{}, V4{}, kt);
+  step(T1{}, F1{}, V4{}, kt);
+  step(T1{}, F1{}, V0{}, kt + 1);
+  step(F1{}, F1{}, VN{}, kt + 2);
 
+  const int64_t row_base = m0 + wm * 128, col_base = n0 + wn * 64;
   if (!g.c_pre) {
-    gemm_epilogue<4, 4>(g, acc, smem, wave, lane, row_base, col_base);
+    gemm_epilogue<4, 2>(g, acc, (uint16_t*)lds, wave, lane, row_base, col_base);
     return;
   }
-  // Fast epilogue.  The accumulators go through the wave's 8 KiB of the staging area
-  // (which the main loop never touches, so no barrier) 16 rows at a time; the c vectors
-  // are read back from where the last k-tile's loads put them.  The only vector-memory
-  // operations outstanding here are those c loads.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  float* stage = (float*)(lds + w4::STAGE_BASE + wave * 8192);
-  uint16_t* O = (uint16_t*)g.out + row_base * g.so_m + col_base + (lane & 15) * 8;
+  // Fast epilogue: the accumulators go through this wave's 4 KiB of staging (never touched
+  // by the k loop: no barrier) 16 rows at a time; a lane finishes rows t * 8 + lane / 8
+  // (t = 0, 1) at columns (lane % 8) * 8 .. + 7.  c is read through a buffer resource (the
+  // host checks its offsets fit 32 bits); c of slab i + 2 is fetched while slab i is
+  // finished.  Without c the resource has no records: the loads return zeros.
   const bool has_c = g.c != nullptr;
-  // Rows 16 h .. 16 h + 15 of slab i come from accumulator registers 8 h .. 8 h + 7.
-  auto stage_half = [&](int i, int h) {
+  const __amdgpu_buffer_rsrc_t rsC = __builtin_amdgcn_make_buffer_rsrc(
+      has_c ? (void*)((const uint16_t*)g.c + row_base * g.sc_m + col_base) : (void*)g.a, (short)0,
+      has_c ? (int)((127 * g.sc_m + 64) * 2) : 0, 0x00020000);
+  const int vc = has_c ? (int)(((lane >> 3) * g.sc_m + (lane & 7) * 8) * 2) : 0;
+  const int c_row = has_c ? (int)(g.sc_m * 2) : 0;
+  // out through plain global stores: a buffer store whose data registers a VALU instruction
+  // rewrote a few instructions later has been seen to store the new values on this target.
+  char* o_lane = (char*)((uint16_t*)g.out + (row_base + (lane >> 3)) * g.so_m + col_base + (lane & 7) * 8);
+  const int64_t o_row = g.so_m * 2;
+  u32x4 cv[2][2][2];
+  auto load_c = [&](int i) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int r = 8 * h; r < 8 * h + 8; ++r)
-        stage[(acc_row(r, lane) - 16 * h) * 128 + j * 32 + (lane & 31)] = acc[i][j][r];
+      for (int t = 0; t < 2; ++t)
+        cv[i & 1][h][t] = __builtin_amdgcn_raw_buffer_load_b128(rsC, vc, (i * 32 + h * 16 + t * 8) * c_row, 0);
   };
-  // Each lane then finishes 4 vectors of 8 columns (rows t * 4 + lane / 16).
+  float* stage = (float*)(lds + dma::EPI + wave * 4096);
   auto finish = [&](auto out_f16_c, auto round_c, int i, int h) {
     constexpr bool OUT_F16 = decltype(out_f16_c)::value;
     constexpr int ROUND = decltype(round_c)::value;
+    wave_lds_order();  // the previous half's reads come first
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int rr = t * 4 + (lane >> 4), cg = (lane & 15) * 8;
-      const float4 v0 = *(const float4*)(stage + rr * 128 + cg);
-      const float4 v1 = *(const float4*)(stage + rr * 128 + cg + 4);
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 8 * h; r < 8 * h + 8; ++r)
+        stage[(acc_row(r, lane) - 16 * h) * 64 + j * 32 + (lane & 31)] = acc[i][j][r];
+    wave_lds_order();  // every lane's writes before any lane reads
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int rr = t * 8 + (lane >> 3), cg = (lane & 7) * 8;
+      const float4 v0 = *(const float4*)(stage + rr * 64 + cg);
+      const float4 v1 = *(const float4*)(stage + rr * 64 + cg + 4);
       const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-      u32x4 cw = {0u, 0u, 0u, 0u};
-      if (has_c) cw = *(const u32x4*)(lds + c_lds(i * 8 + h * 4 + t) + lane * 16);
+      const u32x4 cw = cv[i & 1][h][t];
       u32x4 ow;
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
-        float r[2];
+        float r2[2];
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
           float x = v[2 * d + e];
           if constexpr (ROUND == NT_DTYPE_F16) x = f16_bits_to_float(float_to_f16_bits(x));
           if constexpr (ROUND == NT_DTYPE_BF16) x = bf16_bits_to_float(float_to_bf16_bits(x));
-          r[e] = g.alpha * x;
+          r2[e] = g.alpha * x;
           if (has_c) {
             const uint16_t cb = (uint16_t)(cw[d] >> (16 * e));
-            r[e] += g.beta * (OUT_F16 ? f16_bits_to_float(cb) : bf16_bits_to_float(cb));
+            r2[e] += g.beta * (OUT_F16 ? f16_bits_to_float(cb) : bf16_bits_to_float(cb));
           }
         }
-        ow[d] = OUT_F16 ? ((uint32_t)float_to_f16_bits(r[0]) | ((uint32_t)float_to_f16_bits(r[1]) << 16))
-                        : ((uint32_t)float_to_bf16_bits(r[0]) | ((uint32_t)float_to_bf16_bits(r[1]) << 16));
+        ow[d] = OUT_F16 ? ((uint32_t)float_to_f16_bits(r2[0]) | ((uint32_t)float_to_f16_bits(r2[1]) << 16))
+                        : ((uint32_t)float_to_bf16_bits(r2[0]) | ((uint32_t)float_to_bf16_bits(r2[1]) << 16));
       }
-      *(u32x4*)(O + (int64_t)(i * 32 + h * 16 + rr) * g.so_m) = ow;
+      *(u32x4*)(o_lane + (i * 32 + h * 16 + t * 8) * o_row) = ow;
     }
   };
   using OutF16 = std::integral_constant<bool, true>;
@@ -693,13 +633,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   using RF16 = std::integral_constant<int, NT_DTYPE_F16>;
   using RBF16 = std::integral_constant<int, NT_DTYPE_BF16>;
   auto all = [&](auto out_f16_c, auto round_c) {
+    load_c(0);
+    load_c(1);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 4; ++i) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        stage_half(i, h);
-        finish(out_f16_c, round_c, i, h);
-      }
+      for (int h = 0; h < 2; ++h) finish(out_f16_c, round_c, i, h);
+      if (i + 2 < 4) load_c(i + 2);
+    }
   };
   const bool out_f16 = g.out_dtype == NT_DTYPE_F16;
   if (g.round_dtype == NT_DTYPE_F16) {
@@ -901,7 +842,7 @@ static int gemm16_launch(GemmArgs g, hipStream_t stream) {
   // Four-wave kernel: buffer-load offsets are 32-bit and its k loop runs in pairs of
   // tiles; otherwise the eight-wave kernel.
   const bool w4_ok = (GB_M - 1) * g.sa_m + g.K <= 0x3fffffffLL && (g.K - 1) * g.sb_k + GB_N <= 0x3fffffffLL &&
-                     (g.K / GB_K) % 2 == 0;
+                     g.K >= 3 * 32;
   // Its fast epilogue: 16-byte out vectors, and c (if any) fetched with 32-bit buffer offsets.
   const bool out_vec = g.out_dtype != NT_DTYPE_F32 && g.so_n == 1 && g.so_m >= 0 && g.so_m % 8 == 0 &&
                        (uintptr_t)g.out % 16 == 0;
@@ -909,7 +850,7 @@ static int gemm16_launch(GemmArgs g, hipStream_t stream) {
                               127 * g.sc_m + 128 <= 0x3fffffffLL);
   g.c_pre = fast && w4_ok && out_vec && c_vec;
   if (fast && w4_ok)
-    hipLaunchKernelGGL((gemm_w4_kernel<T>), grid, dim3(256), 0, stream, g);
+    hipLaunchKernelGGL((gemm_dma_kernel<T>), grid, dim3(512), 0, stream, g);
   else if (fast)
     hipLaunchKernelGGL((gemm_fast8_kernel<T>), grid, dim3(512), 0, stream, g);
   else

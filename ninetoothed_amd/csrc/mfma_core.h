@@ -77,15 +77,18 @@ __device__ __forceinline__ void zero_acc(floatx16 (&acc)[WI][WJ]) {
 }
 
 // Write the 32-row slab `acc_i` (WJ blocks of 32 x 32) of one wave into `stage` as
-// fp32 [32][WJ*32], scaled by `scale`.  Every register index is a compile-time
+// fp32 [32][WJ*32], scaled by `scale`, ordered after the wave's earlier reads of `stage`
+// and before its later ones.  Every register index is a compile-time
 // constant, so the accumulators stay in registers; the epilogue that follows reads
 // the slab back with plain runtime loops (and coalesced global accesses).
 template <int WJ>
 __device__ __forceinline__ void stage_slab(float* stage, const floatx16 (&acc_i)[WJ], int lane, float scale = 1.0f) {
+  wave_lds_order();  // reads of the previous slab come first
 #pragma unroll
   for (int j = 0; j < WJ; ++j)
 #pragma unroll
     for (int r = 0; r < 16; ++r) stage[acc_row(r, lane) * (WJ * 32) + j * 32 + (lane & 31)] = acc_i[j][r] * scale;
+  wave_lds_order();  // every lane's writes before any lane reads the slab
 }
 
 // 8x8 transpose of 16-bit values held as 8 rows of 4 dwords (row r, dword d holds

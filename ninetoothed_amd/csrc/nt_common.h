@@ -104,6 +104,13 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 __host__ __device__ __forceinline__ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Lanes of one wave exchanging data through LDS (a lane reads what other lanes wrote): the
+// hardware executes a wave's LDS instructions in program order, but the compiler may move
+// one lane's load above a store whose address it can prove differs for that lane, which
+// lets the load overtake another lane's store.  A call keeps every memory access on its
+// side of it.
+__device__ __forceinline__ void wave_lds_order() { asm volatile("" ::: "memory"); }
+
 // Compile-time loop: f(std::integral_constant<int, i>) for i in [B, E), so that every
 // register index inside f is a constant (used for fixed instruction schedules).
 template <int B, int E, typename F>

@@ -208,8 +208,9 @@ def test_addmm_epilogue():
 @pytest.mark.parametrize("round_dtype", (None, torch.float16, torch.bfloat16))
 @pytest.mark.parametrize("c_kind", ("dense", "strided", "broadcast", "none"))
 def test_addmm_fast_epilogue_variants(dtype, round_dtype, c_kind):
-    # M, N multiples of 256 and K / 64 even: the four-wave kernel, whose epilogue takes
-    # c through LDS; strided out rows and every kind of c row stride it accepts.
+    # M, N multiples of 256 and K a multiple of 64: the DMA kernel, whose fast epilogue
+    # stages the accumulators through LDS and rounds, scales and adds c per variant (six
+    # out x round variants); strided out rows and every kind of c row stride it accepts.
     m, n, k = 512, 768, 256
     a = _randn((m, k), dtype, 30)
     b = _randn((k, n), dtype, 31)
