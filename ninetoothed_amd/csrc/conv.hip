@@ -415,190 +415,165 @@ __global__ __launch_bounds__(512) void conv_nhwc_kernel(const uint16_t* __restri
   }
 }
 
-// Four-wave form of conv_nhwc_kernel: 256 lanes, one
-// wave per SIMD in a 2 (k) x 2 (m) grid, each owning 128 x 128 of the 256 x 256 tile
-// with its accumulators in the accumulator file.  Both operands are k-contiguous rows
-// (filter rows of the K-R-S-C filter, im2col rows of the padded N-H-W-C input), so both
-// load with 16-byte buffer loads and store to LDS unchanged: a row i * 32 + (lane / 8)
-// per load i, chunk lane % 8.  The im2col rows of a lane have per-lane base offsets; the
-// (r, s, c0) of a k-tile is one scalar offset (a k-tile never crosses an (r, s) block,
-// C % 64 == 0), and rows past M take an offset past the end of the resource so their
-// loads return zeros.  Fixed 64-slot issue schedule per 64-deep k-tile (one MFMA per
-// slot, its memory work fenced after it): fragments read a slice ahead; b (im2col) rows stored in slots 0..21 and a (filter)
-// rows in 22..43, each refetched for tile kt + 2 in the slot it was stored; barrier
-// before slot 48.  Epilogue: 16-row halves of each wave's accumulators staged in a
-// spare 32 KiB of LDS (no workgroup barrier: each wave has its own part), then each lane stores 8 consecutive output
-// positions of one channel (its positions are fixed, so (n, p, q) is computed once).
-namespace cw4 {
-constexpr int A_BYTES = CB_K * TILE_K * 2;  // 32 KiB
-constexpr int B_BASE = 2 * A_BYTES;         // 64 KiB
-constexpr int STAGE_BASE = 4 * A_BYTES;     // 128 KiB
-}  // namespace cw4
+// DMA form of the implicit GEMM (the GEMM's gemm_dma_kernel pipeline on two k-contiguous
+// operands): 512 lanes, two waves per SIMD in a 2 (output channels) x 4 (positions) grid,
+// each owning 128 x 64 of the 256 x 256 tile; k-tiles of 32 in a four-stage LDS ring
+// filled by buffer_load ... lds from inline assembly (tile kt+3 into the stage of tile
+// kt-1, one barrier per k-tile, no register staging).  Both operands are stored [row][k]
+// in 64-byte rows whose 16-byte chunks are XOR-swizzled by (row / 4) % 4 and read with
+// ds_read_b128: a = filter rows (K-R-S-C), b = im2col rows of the padded N-H-W-C input,
+// addressed by a per-lane base offset plus one scalar (r, s, c0) offset per k-tile (a
+// k-tile of 32 channels never crosses an (r, s) block: C % 32 == 0); rows past M point
+// past the end of the resource and read zeros.  Epilogue: 16-row halves of each wave's
+// accumulators staged in its own 4 KiB of LDS, each lane storing 8 consecutive
+// positions of one channel (their (n, p, q) computed once).
+namespace cdma {
+constexpr int STAGE = 16384, B0 = 65536, EPI = 131072;
+__device__ __forceinline__ int asw(int row, int chunk) { return chunk ^ ((row >> 2) & 3); }
+__device__ __forceinline__ u32x4 rsrc(const void* base, uint32_t bytes) {
+  const uint64_t p = (uint64_t)base;
+  return u32x4{(uint32_t)p, (uint32_t)(p >> 32) & 0xffffu, bytes, 0x00020000u};
+}
+__device__ __forceinline__ void load_lds16(u32x4 rs, uint32_t lds_addr, int voffset, int soffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(lds_addr), "v"(voffset), "s"(rs), "s"(soffset)
+               : "memory", "m0");
+}
+}  // namespace cdma
 
 template <typename T>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void conv_w4_kernel(
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void conv_dma_kernel(
     const uint16_t* __restrict__ xp, const uint16_t* __restrict__ wt, ConvArgs g, int64_t Hp, int64_t Wp) {
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (CB_K + CB_M) * TILE_K + 16384];
-  char* lds = (char*)smem;
+  __shared__ __attribute__((aligned(1024))) char lds[cdma::EPI + 8 * 4096];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wk = wave >> 1, wm = wave & 1;
+  const int wk = wave >> 2, wm = wave & 3;
   const int tk = blockIdx.x % g.tiles_k, tmi = blockIdx.x / g.tiles_k;
   const int k0t = tk * CB_K, m0t = tmi * CB_M;
   const int KG = (int)g.KG, C = (int)g.C;
-  const int nk = KG / TILE_K;
+  const int nk = KG / 32;
 
-  const int row_in = tid >> 3, chunk = tid & 7;
-  // Filter: rows k0t + row_in + 32 i; rows past K lie past the resource's end (zeros).
-  const __amdgpu_buffer_rsrc_t rsW = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(wt + (int64_t)k0t * KG), (short)0, (int)((g.K - k0t) * KG * 2), 0x00020000);
-  const int vw = (row_in * KG + chunk * 8) * 2;
-  const int w_istep = 32 * KG * 2;
-  // im2col rows m0t + row_in + 32 i.
-  const int x_bytes = (int)(g.N * Hp * Wp * g.C * 2);
-  const __amdgpu_buffer_rsrc_t rsX = __builtin_amdgcn_make_buffer_rsrc((void*)xp, (short)0, x_bytes, 0x00020000);
-  int vx[8];
+  // Load q (0, 1) of this wave per k-tile: rows 32 wave + 16 q + lane / 4 of each operand,
+  // LDS chunk lane % 4.  Filter rows past K lie past the resource's end (zeros).
+  const u32x4 rsW = cdma::rsrc(wt + (int64_t)k0t * KG, (uint32_t)((g.K - k0t) * KG * 2));
+  const uint32_t x_bytes = (uint32_t)(g.N * Hp * Wp * g.C * 2);
+  const u32x4 rsX = cdma::rsrc(xp, x_bytes);
+  int vw[2], vx[2];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int m = m0t + row_in + 32 * i;
+  for (int q = 0; q < 2; ++q) {
+    const int row = 32 * wave + 16 * q + (lane >> 2);
+    const int ch = cdma::asw(row, lane & 3);
+    vw[q] = (row * KG + ch * 8) * 2;
+    const int m = m0t + row;
     if (m < g.M) {
-      const int q = m % (int)g.Q, t = m / (int)g.Q;
+      const int qq = m % (int)g.Q, t = m / (int)g.Q;
       const int p = t % (int)g.P, n = t / (int)g.P;
-      vx[i] = (((n * (int)Hp + p * (int)g.sh) * (int)Wp + q * (int)g.sw) * C + chunk * 8) * 2;
+      vx[q] = (((n * (int)Hp + p * (int)g.sh) * (int)Wp + qq * (int)g.sw) * C + ch * 8) * 2;
     } else {
-      vx[i] = x_bytes;
+      vx[q] = (int)x_bytes;
     }
   }
   // Scalar byte offset of k-tile kt inside an im2col row: (r, s) block and channel c0.
   auto x_off = [&](int kt) {
-    const int kk0 = kt * TILE_K;
+    const int kk0 = kt * 32;
     const int rs = kk0 / C, c0 = kk0 - rs * C;
     const int r = rs / (int)g.S, s = rs - r * (int)g.S;
     return ((r * (int)g.dh * (int)Wp + s * (int)g.dw) * C + c0) * 2;
   };
-
-  int st[2], a_rd[4][2], b_rd[4][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int row = i * 32 + row_in;
-    st[i] = (row * TILE_K + swz(row, chunk) * 8) * 2;
-  }
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int ch = kk * 2 + (lane >> 5);
-      const int ra = wk * 128 + h * 32 + (lane & 31);
-      const int rb = wm * 128 + h * 32 + (lane & 31);
-      a_rd[kk][h] = (ra * TILE_K + swz(ra, ch) * 8) * 2;
-      b_rd[kk][h] = cw4::B_BASE + (rb * TILE_K + swz(rb, ch) * 8) * 2;
-    }
-
-  floatx16 acc[4][4];
-  zero_acc(acc);
-  u32x4 ra[8], rb[8];
-  auto load_a = [&](int kt) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) ra[i] = __builtin_amdgcn_raw_buffer_load_b128(rsW, vw, i * w_istep + kt * 128, 0);
-  };
-  auto load_b = [&](int kt) {
-    const int xo = x_off(kt);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) rb[i] = __builtin_amdgcn_raw_buffer_load_b128(rsX, vx[i], xo, 0);
-  };
-  auto store_ab = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      *(u32x4*)(lds + buf * cw4::A_BYTES + st[i & 1] + (i >> 1) * 8192) = ra[i];
-      *(u32x4*)(lds + cw4::B_BASE + buf * cw4::A_BYTES + st[i & 1] + (i >> 1) * 8192) = rb[i];
-    }
-  };
-
-  typedef typename mfma_traits<T>::frag frag;
-  frag fa[2][4], fb[2][4];
-  auto read_frag = [&](auto buf_c, int kk, int slot, int x) {
-    constexpr int OFF = decltype(buf_c)::value * cw4::A_BYTES;
-    if (x < 4)
-      fa[slot][x] = *(const frag*)(lds + a_rd[kk][x & 1] + (x >> 1) * 8192 + OFF);
+  // Load u (0..3) of tile kt into its stage: filter q0, im2col q0, filter q1, im2col q1.
+  auto load_unit = [&](int u, int kt, int xo) {
+    const int st = (kt & 3) * cdma::STAGE, q = u >> 1;
+    if ((u & 1) == 0)
+      cdma::load_lds16(rsW, lds0 + st + 2048 * wave + 1024 * q, vw[q], kt * 64);
     else
-      fb[slot][x - 4] = *(const frag*)(lds + b_rd[kk][x & 1] + ((x - 4) >> 1) * 8192 + OFF);
+      cdma::load_lds16(rsX, lds0 + cdma::B0 + st + 2048 * wave + 1024 * q, vx[q], xo);
   };
-  using B0 = std::integral_constant<int, 0>;
-  using B1 = std::integral_constant<int, 1>;
 
-  load_a(0);
-  load_b(0);
-  store_ab(0);
-  if (nk > 1) {
-    load_a(1);
-    load_b(1);
-  }
-  __syncthreads();
+  // Fragment reads: filter rows 128 wk + 32 i + lane % 32, im2col rows 64 wm + 32 j + lane % 32,
+  // chunk 2 s + lane / 32 (the swizzle depends on lane % 32 only).
+  int a_rd[2], b_rd[2];
 #pragma unroll
-  for (int x = 0; x < 8; ++x) read_frag(B0{}, 0, 0, x);
+  for (int s2 = 0; s2 < 2; ++s2) {
+    const int ra = wk * 128 + (lane & 31), rb = wm * 64 + (lane & 31);
+    a_rd[s2] = ra * 64 + cdma::asw(ra, 2 * s2 + (lane >> 5)) * 16;
+    b_rd[s2] = cdma::B0 + rb * 64 + cdma::asw(rb, 2 * s2 + (lane >> 5)) * 16;
+  }
+  typedef typename mfma_traits<T>::frag frag;
+  frag fa[2][4], fb[2][2];
+  // Read unit x (0..5) of slice s2 of the tile at stage byte offset st: a0, b0, b1, a1, a2, a3.
+  auto read_unit = [&](int x, int s2, int st) {
+    if (x == 0 || x >= 3) {
+      const int i = x == 0 ? 0 : x - 2;
+      fa[s2][i] = *(const frag*)(lds + a_rd[s2] + st + i * 2048);
+    } else {
+      const int j = x - 1;
+      fb[s2][j] = *(const frag*)(lds + b_rd[s2] + st + j * 2048);
+    }
+  };
+
+  floatx16 acc[4][2];
+  zero_acc(acc);
+
+  // nk >= 3 (the launcher checks): tiles 0..2 in flight, wait for tile 0.
+  for (int kt = 0; kt < 3; ++kt) {
+    const int xo = x_off(kt);
+    for (int u = 0; u < 4; ++u) load_unit(u, kt, xo);
+  }
+  asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+#pragma unroll
+  for (int x = 0; x < 6; ++x) read_unit(x, 0, 0);
 
 #define NT_CFENCE() __builtin_amdgcn_sched_barrier(0)
-  auto step = [&](auto cur_c, auto has1_c, auto has2_c, int kt) {
-    constexpr int CUR = decltype(cur_c)::value;
-    constexpr bool HAS1 = decltype(has1_c)::value, HAS2 = decltype(has2_c)::value;
-    using Cur = std::integral_constant<int, CUR>;
-    using Nxt = std::integral_constant<int, CUR ^ 1>;
-    constexpr int NOFF = (CUR ^ 1) * cw4::A_BYTES;
-    const int k2 = kt + 2;
-    const int xo2 = HAS2 ? x_off(k2) : 0;
-    static_for<0, 64>([&](auto m_c) {
+  // One k-tile, as gemm_dma_kernel's: HAS1 reads slice 0 of tile kt+1 during slice 1, LOAD
+  // fetches tile kt+3, VM is the number of loads allowed outstanding once tile kt+1 has
+  // landed (-1: the last tile, no wait and no barrier).
+  auto step = [&](auto has1_c, auto load_c, auto vm_c, int kt) {
+    constexpr bool HAS1 = decltype(has1_c)::value, LOAD = decltype(load_c)::value;
+    constexpr int VM = decltype(vm_c)::value;
+    const int st = (kt & 3) * cdma::STAGE, st1 = ((kt + 1) & 3) * cdma::STAGE;
+    const int xo3 = LOAD ? x_off(kt + 3) : 0;
+    static_for<0, 16>([&](auto m_c) {
       constexpr int m = decltype(m_c)::value;
-      constexpr int slice = m / 16, x = m % 16, slot = slice & 1;
-      if constexpr (m == 48) {
+      constexpr int s2 = m >> 3, x = m & 7;
+      if constexpr (m == 8 && VM >= 0) {
         NT_CFENCE();
-        __syncthreads();
+        if constexpr (VM == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+        if constexpr (VM == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
         NT_CFENCE();
       }
-      {
-        constexpr int i = x >> 2, j = x & 3;
-        acc[i][j] = mfma_traits<T>::mma(fa[slot][i], fb[slot][j], acc[i][j]);
-      }
+      acc[x >> 1][x & 1] = mfma_traits<T>::mma(fa[s2][x >> 1], fb[s2][x & 1], acc[x >> 1][x & 1]);
       NT_CFENCE();
-      constexpr bool rd = slice < 2 ? (x % 2 == 0) : (x < 8);
-      if constexpr (rd) {
-        constexpr int f = slice < 2 ? x / 2 : x;
-        constexpr int which = f == 0 ? 0 : (f <= 4 ? f + 3 : f - 4);
-        if constexpr (slice < 3)
-          read_frag(Cur{}, slice + 1, slot ^ 1, which);
+      if constexpr (x < 6) {
+        if constexpr (s2 == 0)
+          read_unit(x, 1, st);
         else if constexpr (HAS1)
-          read_frag(Nxt{}, 0, 0, which);
+          read_unit(x, 0, st1);
       }
-      if constexpr (HAS1) {
-        if constexpr (m <= 21 && m % 3 == 0) {
-          constexpr int i = m / 3;
-          *(u32x4*)(lds + cw4::B_BASE + NOFF + st[i & 1] + (i >> 1) * 8192) = rb[i];
-          if constexpr (HAS2) rb[i] = __builtin_amdgcn_raw_buffer_load_b128(rsX, vx[i], xo2, 0);
-        }
-        if constexpr (m >= 22 && m <= 43 && (m - 22) % 3 == 0) {
-          constexpr int i = (m - 22) / 3;
-          *(u32x4*)(lds + NOFF + st[i & 1] + (i >> 1) * 8192) = ra[i];
-          if constexpr (HAS2) ra[i] = __builtin_amdgcn_raw_buffer_load_b128(rsW, vw, i * w_istep + k2 * 128, 0);
-        }
-      }
+      if constexpr (s2 == 1 && LOAD && x < 4) load_unit(x, kt + 3, xo3);
       NT_CFENCE();
     });
   };
 #undef NT_CFENCE
   using T1 = std::integral_constant<bool, true>;
   using F1 = std::integral_constant<bool, false>;
-  // nk is even (the launcher checks): pairs of k-tiles, the last pair without prefetch.
+  using V4 = std::integral_constant<int, 4>;
+  using V0 = std::integral_constant<int, 0>;
+  using VN = std::integral_constant<int, -1>;
   int kt = 0;
-  for (; kt + 2 < nk; kt += 2) {
-    step(B0{}, T1{}, T1{}, kt);
-    step(B1{}, T1{}, T1{}, kt + 1);
-  }
-  step(B0{}, T1{}, F1{}, kt);
-  step(B1{}, F1{}, F1{}, kt + 1);
+  for (; kt + 3 < nk; ++kt) step(T1{}, T1{}, V4{}, kt);
+  step(T1{}, F1{}, V4{}, kt);
+  step(T1{}, F1{}, V0{}, kt + 1);
+  step(F1{}, F1{}, VN{}, kt + 2);
 
-  // Epilogue: this lane's 8 output positions and their (n, p, q).
-  float* stage = (float*)(lds + cw4::STAGE_BASE + wave * 8192);
-  const int cg = (lane & 15) * 8;
-  const int mpos = m0t + wm * 128 + cg;
+  // Epilogue: this lane's 8 output positions (columns (lane % 8) * 8 .. + 7 of the wave's 64)
+  // and their (n, p, q); channels rows t * 8 + lane / 8 of each 16-row half.
+  float* stage = (float*)(lds + cdma::EPI + wave * 4096);
+  const int cg = (lane & 7) * 8;
+  const int mpos = m0t + wm * 64 + cg;
   const bool m_ok = mpos < g.M;  // Q % 8 == 0: all 8 positions share one output row
   int64_t ybase = 0;
   if (m_ok) {
@@ -615,17 +590,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       for (int h = 0; h < 2; ++h) {
         wave_lds_order();  // the previous half's reads come first
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
           for (int r = 8 * h; r < 8 * h + 8; ++r)
-            stage[(acc_row(r, lane) - 16 * h) * 128 + j * 32 + (lane & 31)] = acc[i][j][r];
+            stage[(acc_row(r, lane) - 16 * h) * 64 + j * 32 + (lane & 31)] = acc[i][j][r];
         wave_lds_order();  // every lane's writes before any lane reads
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const int rr = t * 4 + (lane >> 4);
+        for (int t = 0; t < 2; ++t) {
+          const int rr = t * 8 + (lane >> 3);
           const int k = k0t + wk * 128 + i * 32 + h * 16 + rr;
-          const float4 v0 = *(const float4*)(stage + rr * 128 + cg);
-          const float4 v1 = *(const float4*)(stage + rr * 128 + cg + 4);
+          const float4 v0 = *(const float4*)(stage + rr * 64 + cg);
+          const float4 v1 = *(const float4*)(stage + rr * 64 + cg + 4);
           const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
           u32x4 ow;
 #pragma unroll
@@ -711,14 +686,14 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
       hipLaunchKernelGGL(filter_krsc_kernel<T>, dim3((unsigned)fblocks), dim3(256), 0, stream, (const uint16_t*)w, wt,
                          g);
     }
-    // Four-wave kernel: even number of k-tiles, 32-bit operand offsets, output written as
-    // 16-byte runs of 8 positions of one channel (Q % 8 == 0, y of the input type with
+    // DMA kernel: at least three 32-deep k-tiles, 32-bit operand offsets, output written
+    // as 16-byte runs of 8 positions of one channel (Q % 8 == 0, y of the input type with
     // unit q stride and 16-byte aligned rows).
-    const bool w4 = (g.KG / TILE_K) % 2 == 0 && N * Hp * Wp * C * 2 < 0x7fffffffLL &&
-                    K * g.KG * 2 < 0x7fffffffLL && g.M < 0x7fffffffLL && y_dtype == elem<T>::code && Q % 8 == 0 &&
-                    ys[3] == 1 && ys[0] % 8 == 0 && ys[1] % 8 == 0 && ys[2] % 8 == 0 && (uintptr_t)y % 16 == 0;
-    if (w4)
-      hipLaunchKernelGGL(conv_w4_kernel<T>, dim3((unsigned)(tiles_k * tiles_m)), dim3(256), 0, stream,
+    const bool dma = g.KG >= 3 * 32 && g.KG % 32 == 0 && N * Hp * Wp * C * 2 < 0x7fffffffLL &&
+                     K * g.KG * 2 < 0x7fffffffLL && g.M < 0x7fffffffLL && y_dtype == elem<T>::code && Q % 8 == 0 &&
+                     ys[3] == 1 && ys[0] % 8 == 0 && ys[1] % 8 == 0 && ys[2] % 8 == 0 && (uintptr_t)y % 16 == 0;
+    if (dma)
+      hipLaunchKernelGGL(conv_dma_kernel<T>, dim3((unsigned)(tiles_k * tiles_m)), dim3(512), 0, stream,
                          (const uint16_t*)xp, (const uint16_t*)wt, g, Hp, Wp);
     else
       hipLaunchKernelGGL(conv_nhwc_kernel<T>, dim3((unsigned)(tiles_k * tiles_m)), dim3(512), 0, stream,

@@ -304,18 +304,20 @@ def test_conv2d_relayout_strided_ragged_bf16():
 
 @pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
 @pytest.mark.parametrize("case", (
-    # (N, C, H, W), (K, R, S), padding, stride, dilation: Q % 8 == 0 and C*R*S / 64 even,
-    # the four-wave re-laid kernel; M and K not multiples of its 256 x 256 tile.
+    # (N, C, H, W), (K, R, S), padding, stride, dilation: Q % 8 == 0 and C*R*S >= 96, the
+    # re-laid DMA kernel; M and K not multiples of its 256 x 256 tile, 4, 6 and 36 k-tiles
+    # of 32 (the pipeline's shortest and an odd count of 64-deep ones included).
     ((3, 128, 20, 16), (200, 3, 3), (1, 1), (1, 1), (1, 1)),
     ((2, 128, 33, 31), (64, 3, 3), (2, 2), (2, 2), (2, 2)),
     ((1, 64, 9, 45), (320, 1, 2), (0, 1), (1, 3), (1, 1)),
+    ((2, 64, 12, 24), (96, 3, 1), (1, 0), (1, 1), (1, 1)),
 ))
-def test_conv2d_relayout_four_wave(case, dtype):
+def test_conv2d_relayout_dma(case, dtype):
     (n, c, h, w_), (k, r, s), padding, stride, dilation = case
     x = _randn((n, c, h, w_), dtype, 33)
     w = _randn((k, c, r, s), dtype, 34, 1.0 / math.sqrt(c * r * s))
     ref = F.conv2d(x.float(), w.float(), padding=padding, stride=stride, dilation=dilation)
-    assert ref.shape[3] % 8 == 0 and (c * r * s // 64) % 2 == 0
+    assert ref.shape[3] % 8 == 0 and c * r * s >= 96
     y = torch.empty(ref.shape, dtype=dtype, device=DEV)
     kernels.conv2d(x, w, y, padding=padding, stride=stride, dilation=dilation, round_dtype=torch.float16,
                    workspace=_workspace(x, w, padding))
