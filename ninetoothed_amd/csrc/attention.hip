@@ -527,7 +527,13 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
     store_tile(0);
     if (nkt > 1) load_tile(1);
   }
-  for (int kt = 0; kt < nkt; ++kt) {
+  // Causal: tiles whose first key follows every query of this wave would only add masked
+  // scores (p = 0), so the wave computes up to its own last tile nkt_w and then only takes
+  // its part in the workgroup's loads and barriers (a separate loop, so the main one
+  // carries no branch around its body).
+  const int nkt_w = g.causal ? min(nkt, (qw + WQ - 1) / AT_BN + 1) : nkt;
+  int kt = 0;
+  for (; kt < nkt_w; ++kt) {
     __syncthreads();
     if (kt + 1 < nkt) {
       store_tile((kt + 1) & 1);
@@ -636,6 +642,13 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
       }
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) l_acc[qb] = mfma_traits<T>::mma(ones, pf[qb][t], l_acc[qb]);
+    }
+  }
+  for (; kt < nkt; ++kt) {
+    __syncthreads();
+    if (kt + 1 < nkt) {
+      store_tile((kt + 1) & 1);
+      if (kt + 2 < nkt) load_tile(kt + 2);
     }
   }
   __syncthreads();  // the output staging below reuses the K/V stages
