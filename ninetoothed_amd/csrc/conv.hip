@@ -202,14 +202,14 @@ __global__ __launch_bounds__(256) void nchw_to_nhwc_pad_kernel(const uint16_t* _
 template <typename T>
 __global__ __launch_bounds__(256) void filter_krsc_kernel(const uint16_t* __restrict__ w, uint16_t* __restrict__ wt,
                                                           ConvArgs g) {
-  const int64_t total = g.K * g.KG;
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t c = e % g.C;
-    int64_t t = e / g.C;
-    const int64_t s = t % g.S;
-    t /= g.S;
+  // One (k, r, s) row of C channels per workgroup and step (index arithmetic once per row).
+  const int64_t krs = g.K * g.R * g.S;
+  for (int64_t row = blockIdx.x; row < krs; row += gridDim.x) {
+    const int64_t s = row % g.S, t = row / g.S;
     const int64_t r = t % g.R, k = t / g.R;
-    wt[e] = w[k * g.ws[0] + c * g.ws[1] + r * g.ws[2] + s * g.ws[3]];
+    const uint16_t* src = w + k * g.ws[0] + r * g.ws[2] + s * g.ws[3];
+    uint16_t* dst = wt + row * g.C;
+    for (int64_t c = threadIdx.x; c < g.C; c += blockDim.x) dst[c] = src[c * g.ws[1]];
   }
 }
 
@@ -218,7 +218,7 @@ __global__ __launch_bounds__(256) void filter_krsc_kernel(const uint16_t* __rest
 // go one per lane: eight 16-byte loads along w (one per channel), an 8 x 8 transpose of
 // 16-bit values with v_perm_b32, eight 16-byte stores along c (one per position).  Needs
 // unit w stride, 16-byte aligned input rows and W % 8 == 0.  Workgroups past N * Hp:
-// the filter, element by element into K-R-S-C.
+// the filter into K-R-S-C, one (k, r, s) row of C channels at a time.
 template <typename T>
 __global__ __launch_bounds__(256) void conv_relayout_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ xp,
                                                             const uint16_t* __restrict__ w, uint16_t* __restrict__ wt,
@@ -226,15 +226,15 @@ __global__ __launch_bounds__(256) void conv_relayout_kernel(const uint16_t* __re
   const int64_t rows = g.N * Hp;
   const int tid = threadIdx.x;
   if ((int64_t)blockIdx.x >= rows) {
-    const int64_t total = g.K * g.KG;
-    const int64_t stride = ((int64_t)gridDim.x - rows) * 256;
-    for (int64_t e = ((int64_t)blockIdx.x - rows) * 256 + tid; e < total; e += stride) {
-      const int64_t c = e % g.C;
-      int64_t t = e / g.C;
-      const int64_t s = t % g.S;
-      t /= g.S;
+    // Filter: one (k, r, s) row of C channels per workgroup and step, its index arithmetic
+    // done once per row (workgroup-uniform), lanes along c (coalesced stores).
+    const int64_t krs = g.K * g.R * g.S, nb = (int64_t)gridDim.x - rows;
+    for (int64_t row = (int64_t)blockIdx.x - rows; row < krs; row += nb) {
+      const int64_t s = row % g.S, t = row / g.S;
       const int64_t r = t % g.R, k = t / g.R;
-      wt[e] = w[k * g.ws[0] + c * g.ws[1] + r * g.ws[2] + s * g.ws[3]];
+      const uint16_t* src = w + k * g.ws[0] + r * g.ws[2] + s * g.ws[3];
+      uint16_t* dst = wt + row * g.C;
+      for (int64_t c = tid; c < g.C; c += 256) dst[c] = src[c * g.ws[1]];
     }
     return;
   }
@@ -670,7 +670,7 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
     const int64_t Hp = H + 2 * ph, Wp = W + 2 * pw;
     uint16_t* xp = (uint16_t*)workspace;
     uint16_t* wt = (uint16_t*)((char*)workspace + ((N * Hp * Wp * C * 2 + 255) / 256) * 256);
-    int64_t fblocks = cdiv(K * g.KG, 256);
+    int64_t fblocks = K * R * S;  // filter rows of the fast re-layout (at most 4096 workgroups)
     if (fblocks > 4096) fblocks = 4096;
     const bool fast_relayout = xs[3] == 1 && W % 8 == 0 && (uintptr_t)x % 16 == 0 && (xs[0] * 2) % 16 == 0 &&
                                (xs[1] * 2) % 16 == 0 && (xs[2] * 2) % 16 == 0;
