@@ -227,6 +227,22 @@ def test_addmm_fast_epilogue_variants(dtype, round_dtype, c_kind):
     assert torch.allclose(out.float(), ref.float(), atol=2e-2, rtol=1e-2)
 
 
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+@pytest.mark.parametrize("k", (128, 192, 576))
+def test_gemm_dma_padded_leading_dims(k, dtype):
+    # The DMA kernel's operand offsets come from the row strides: a, b, c and out as views
+    # of wider buffers (row strides K + 64, N + 128, N + 32, N + 64), K with 4, 6 and 18
+    # k-tiles of 32.
+    m, n = 512, 768
+    a = _randn((m, k + 64), dtype, 40)[:, :k]
+    b = _randn((k, n + 128), dtype, 41)[:, :n]
+    c = _randn((m, n + 32), dtype, 42)[:, :n]
+    out = torch.empty((m, n + 64), dtype=dtype, device=DEV)[:, :n]
+    kernels.gemm(a, b, out, c=c, alpha=1.5, beta=0.25, round_dtype=None)
+    ref = _gemm_ref(a, b, c, 1.5, 0.25, None)
+    assert torch.allclose(out.float(), ref.float(), atol=2e-2, rtol=1e-2)
+
+
 def test_addmm_headline_bf16():
     m = n = k = 4096
     g = 1.0 / math.sqrt(k)
