@@ -839,17 +839,18 @@ static int gemm16_launch(GemmArgs g, hipStream_t stream) {
                     (uintptr_t)g.a % 16 == 0 && (uintptr_t)g.b % 16 == 0 && (g.sa_m * 2) % 16 == 0 &&
                     (g.sb_k * 2) % 16 == 0;
   const dim3 grid((unsigned)(tiles_m * tiles_n)), blk(G_THREADS);
-  // Four-wave kernel: buffer-load offsets are 32-bit and its k loop runs in pairs of
-  // tiles; otherwise the eight-wave kernel.
-  const bool w4_ok = (GB_M - 1) * g.sa_m + g.K <= 0x3fffffffLL && (g.K - 1) * g.sb_k + GB_N <= 0x3fffffffLL &&
-                     g.K >= 3 * 32;
+  // DMA kernel: operand panel offsets fit its 32-bit buffer offsets and K holds at least the
+  // three 32-deep k-tiles its pipeline keeps in flight; otherwise the register-staged
+  // eight-wave kernel.
+  const bool dma_ok = (GB_M - 1) * g.sa_m + g.K <= 0x3fffffffLL && (g.K - 1) * g.sb_k + GB_N <= 0x3fffffffLL &&
+                      g.K >= 3 * 32;
   // Its fast epilogue: 16-byte out vectors, and c (if any) fetched with 32-bit buffer offsets.
   const bool out_vec = g.out_dtype != NT_DTYPE_F32 && g.so_n == 1 && g.so_m >= 0 && g.so_m % 8 == 0 &&
                        (uintptr_t)g.out % 16 == 0;
   const bool c_vec = !g.c || (g.sc_n == 1 && g.sc_m >= 0 && g.sc_m % 8 == 0 && (uintptr_t)g.c % 16 == 0 &&
                               127 * g.sc_m + 128 <= 0x3fffffffLL);
-  g.c_pre = fast && w4_ok && out_vec && c_vec;
-  if (fast && w4_ok)
+  g.c_pre = fast && dma_ok && out_vec && c_vec;
+  if (fast && dma_ok)
     hipLaunchKernelGGL((gemm_dma_kernel<T>), grid, dim3(512), 0, stream, g);
   else if (fast)
     hipLaunchKernelGGL((gemm_fast8_kernel<T>), grid, dim3(512), 0, stream, g);
