@@ -49,6 +49,11 @@ _SIGNATURES = {
         f"nt_gemm_{t}": (_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I, _I64, _I64, _I64, _F, _F, _I, _P)
         for t in ("f32", "f16", "bf16", "e5m2", "e4m3")
     },
+    **{
+        f"nt_gemm_config_{t}": (_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I, _I64, _I64, _I64, _F,
+                                _F, _I, _I, _P)
+        for t in ("f16", "bf16")
+    },
     "nt_conv2d_workspace_size": (_I64,) * 9 + (_I,),
     **{
         f"nt_conv2d_{t}": (_P, _I64P, _P, _I64P, _P, _I64P, _I) + (_I64,) * 15 + (_I, _P, _I64, _P)

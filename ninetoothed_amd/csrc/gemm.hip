@@ -822,8 +822,12 @@ __global__ void gemm_k0_kernel(GemmArgs g) {
   }
 }
 
+// config: 0 = the fastest kernel whose conditions hold; 1 = the DMA kernel, 2 = the
+// register-staged eight-wave kernel, 3 = the element-wise loader kernel (any strides): a
+// forced kernel whose conditions do not hold is rejected before anything is launched.
 template <typename T>
-static int gemm16_launch(GemmArgs g, hipStream_t stream) {
+static int gemm16_launch(GemmArgs g, hipStream_t stream, int config = 0) {
+  if (config < 0 || config > 3) return NT_ERR_INVALID;
   if (int e = gemm_check(g)) return e;
   if (g.M == 0 || g.N == 0) return 0;
   if (!g.a || !g.b || !g.out) return NT_ERR_INVALID;
@@ -849,10 +853,13 @@ static int gemm16_launch(GemmArgs g, hipStream_t stream) {
                        (uintptr_t)g.out % 16 == 0;
   const bool c_vec = !g.c || (g.sc_n == 1 && g.sc_m >= 0 && g.sc_m % 8 == 0 && (uintptr_t)g.c % 16 == 0 &&
                               127 * g.sc_m + 128 <= 0x3fffffffLL);
-  g.c_pre = fast && dma_ok && out_vec && c_vec;
-  if (fast && dma_ok)
+  if ((config == 1 && !(fast && dma_ok)) || (config == 2 && !fast)) return NT_ERR_INVALID;
+  const bool use_dma = config == 0 ? fast && dma_ok : config == 1;
+  const bool use_fast8 = config == 0 ? fast && !dma_ok : config == 2;
+  g.c_pre = use_dma && out_vec && c_vec;
+  if (use_dma)
     hipLaunchKernelGGL((gemm_dma_kernel<T>), grid, dim3(512), 0, stream, g);
-  else if (fast)
+  else if (use_fast8)
     hipLaunchKernelGGL((gemm_fast8_kernel<T>), grid, dim3(512), 0, stream, g);
   else
     hipLaunchKernelGGL((gemm_mfma_kernel<T, false>), grid, blk, 0, stream, g);
@@ -932,6 +939,18 @@ static GemmArgs make_args(const void* a, int64_t sa_m, int64_t sa_k, const void*
 extern "C" int nt_gemm_f16(NT_GEMM_PARAMS) { return nt::gemm16_launch<nt::f16_t>(nt::make_args(NT_GEMM_ARGS), stream); }
 extern "C" int nt_gemm_bf16(NT_GEMM_PARAMS) {
   return nt::gemm16_launch<nt::bf16_t>(nt::make_args(NT_GEMM_ARGS), stream);
+}
+extern "C" int nt_gemm_config_f16(const void* a, int64_t sa_m, int64_t sa_k, const void* b, int64_t sb_k,
+                                  int64_t sb_n, const void* c, int64_t sc_m, int64_t sc_n, void* out, int64_t so_m,
+                                  int64_t so_n, int out_dtype, int64_t M, int64_t N, int64_t K, float alpha, float beta,
+                                  int round_dtype, int config, hipStream_t stream) {
+  return nt::gemm16_launch<nt::f16_t>(nt::make_args(NT_GEMM_ARGS), stream, config);
+}
+extern "C" int nt_gemm_config_bf16(const void* a, int64_t sa_m, int64_t sa_k, const void* b, int64_t sb_k,
+                                   int64_t sb_n, const void* c, int64_t sc_m, int64_t sc_n, void* out, int64_t so_m,
+                                   int64_t so_n, int out_dtype, int64_t M, int64_t N, int64_t K, float alpha, float beta,
+                                   int round_dtype, int config, hipStream_t stream) {
+  return nt::gemm16_launch<nt::bf16_t>(nt::make_args(NT_GEMM_ARGS), stream, config);
 }
 extern "C" int nt_gemm_f32(NT_GEMM_PARAMS) { return nt::gemm32_launch(nt::make_args(NT_GEMM_ARGS), stream); }
 extern "C" int nt_gemm_e5m2(NT_GEMM_PARAMS) {

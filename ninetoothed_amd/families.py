@@ -259,10 +259,15 @@ def _lin_epilogue(v, acc_out, out_param, scalar_params):
 class GemmPlan(Plan):
     family = "gemm"
 
-    def __init__(self, a, b, out, c, alpha_factors, beta_factors, round_dtype):
+    def __init__(self, a, b, out, c, alpha_factors, beta_factors, round_dtype, config=0):
         self.a, self.b, self.out, self.c = a, b, out, c
         self.alpha_factors, self.beta_factors = alpha_factors, beta_factors
         self.round_dtype = round_dtype
+        self.config = config  # 0: the library picks the kernel; else one forced kernel
+
+    def with_config(self, config):
+        return GemmPlan(self.a, self.b, self.out, self.c, self.alpha_factors, self.beta_factors, self.round_dtype,
+                        config)
 
     @staticmethod
     def _coef_fn(factors, index):
@@ -296,7 +301,8 @@ class GemmPlan(Plan):
         from ninetoothed_amd import kernels
 
         launch = kernels.bind_gemm(values[self.a], values[self.b], values[self.out],
-                                   values[self.c] if self.c else None, round_dtype=self.round_dtype)
+                                   values[self.c] if self.c else None, round_dtype=self.round_dtype,
+                                   config=self.config)
         ia, ib, io = index[self.a], index[self.b], index[self.out]
         ic = index[self.c] if self.c else None
         alpha = self._coef_fn(self.alpha_factors, index)
@@ -308,8 +314,10 @@ class GemmPlan(Plan):
         return run
 
     def describe(self):
-        return {"family": "gemm", "a": self.a, "b": self.b, "out": self.out, "c": self.c,
-                "round": str(self.round_dtype)}
+        d = {"family": "gemm", "a": self.a, "b": self.b, "out": self.out, "c": self.c, "round": str(self.round_dtype)}
+        if self.config:
+            d["config"] = self.config
+        return d
 
 
 class ConvPlan(Plan):
@@ -954,14 +962,22 @@ FAMILIES = (match_attention, match_gemm, match_softmax, match_max_pool2d, match_
 
 
 def candidates(ctx):
-    """Every family plan whose pattern and geometry fit, in the order ``select`` tries them."""
+    """Every family plan whose pattern and geometry fit, in the order ``select`` tries them.
+
+    A GEMM plan stands for each of the 16-bit GEMM's kernel configurations (the DMA kernel,
+    the register-staged one, the element-wise loader one): configurations the call's
+    operands do not admit fail when bound or launched and drop out of the timing."""
+    from ninetoothed_amd import kernels
+
     plans = []
     for matcher in FAMILIES:
         try:
             plan = matcher(ctx)
         except LoweringError:
             plan = None
-        if plan is not None:
+        if isinstance(plan, GemmPlan) and not plan.config:
+            plans.extend(plan.with_config(cfg) for cfg in kernels.GEMM_CONFIGS)
+        elif plan is not None:
             plans.append(plan)
     return plans
 

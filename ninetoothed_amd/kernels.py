@@ -146,10 +146,18 @@ def max_pool2d(x, y, window, stride=None, padding=(0, 0), dilation=(1, 1)):
 
 
 # ------------------------------------------------------------------------ gemm
-def bind_gemm(a, b, out, c=None, round_dtype=None):
+# Kernel configurations of the 16-bit GEMM that ``config`` can force (0: the fastest whose
+# conditions hold): the DMA kernel, the register-staged eight-wave kernel, the element-wise
+# loader kernel.
+GEMM_CONFIGS = (1, 2, 3)
+
+
+def bind_gemm(a, b, out, c=None, round_dtype=None, config=0):
     """launch(a, b, out, c, alpha, beta): out = cast(beta * c + alpha * round(a @ b)).
 
-    fp32 accumulation; any strides; ``c`` is None exactly when it was None here."""
+    fp32 accumulation; any strides; ``c`` is None exactly when it was None here.  A nonzero
+    ``config`` (fp16/bf16 operands only) forces one kernel; a call its conditions do not
+    admit raises ``KernelLaunchError`` without launching."""
     device = _check_device(a, b, out, c)
     if a.dim() != 2 or b.dim() != 2 or out.dim() != 2:
         raise ValueError("gemm expects 2-D tensors")
@@ -165,7 +173,14 @@ def bind_gemm(a, b, out, c=None, round_dtype=None):
         if c.dtype != out.dtype:
             raise TypeError("gemm bias and output must share one dtype")
     rd = _lib.DTYPE_NONE if round_dtype is None else _lib.dtype_code(round_dtype)
-    fn, name = _entry("nt_gemm", a.dtype)
+    if config:
+        if config not in GEMM_CONFIGS or _lib.dtype_suffix(a.dtype) not in ("f16", "bf16"):
+            raise TypeError(f"gemm config {config} needs fp16/bf16 operands and one of {GEMM_CONFIGS}")
+        fn, name = _entry("nt_gemm_config", a.dtype)
+        extra = (int(config),)
+    else:
+        fn, name = _entry("nt_gemm", a.dtype)
+        extra = ()
     (sa_m, sa_k), (sb_k, sb_n), (so_m, so_n) = a.stride(), b.stride(), out.stride()
     sc_m, sc_n = c.stride() if c is not None else (0, 0)
     out_code = _lib.dtype_code(out.dtype)
@@ -173,15 +188,15 @@ def bind_gemm(a, b, out, c=None, round_dtype=None):
 
     def launch(a, b, out, c, alpha, beta):
         code = fn(a.data_ptr(), sa_m, sa_k, b.data_ptr(), sb_k, sb_n, c.data_ptr() if c is not None else None, sc_m,
-                  sc_n, out.data_ptr(), so_m, so_n, out_code, m, n, k, alpha, beta, rd, stream())
+                  sc_n, out.data_ptr(), so_m, so_n, out_code, m, n, k, alpha, beta, rd, *extra, stream())
         if code:
             _raise(code, name)
 
     return launch
 
 
-def gemm(a, b, out, c=None, alpha=1.0, beta=0.0, round_dtype=None):
-    bind_gemm(a, b, out, c, round_dtype)(a, b, out, c, float(alpha), float(beta))
+def gemm(a, b, out, c=None, alpha=1.0, beta=0.0, round_dtype=None, config=0):
+    bind_gemm(a, b, out, c, round_dtype, config)(a, b, out, c, float(alpha), float(beta))
     return out
 
 

@@ -15,6 +15,7 @@ import torch
 
 import ninetoothed_amd as ninetoothed
 import ninetoothed_amd.language as ntl
+import programs as pg
 from ninetoothed_amd import Symbol, Tensor, families
 from ninetoothed_amd.auto_tuner import AutoTuner
 
@@ -131,3 +132,25 @@ def test_tuned_handle_picks_a_kernel_and_computes():
     out2 = torch.empty_like(a)
     h(a, b, out2)  # the bound winner, no new benchmark
     assert torch.equal(out2, a + b)
+
+
+def test_gemm_plans_expand_into_kernel_configs():
+    h = ninetoothed.make(pg.matmul_arrangement, pg.matmul_application, pg.matmul_tensors())
+    t = torch.empty(512, 512, dtype=torch.float16)
+    ctx = h._kernel.context({"lhs": t, "rhs": t, "output": t}, {})
+    described = [p.describe() for p in families.candidates(ctx)]
+    assert [d["family"] for d in described] == ["gemm"] * 3
+    assert [d["config"] for d in described] == [1, 2, 3]
+    assert "config" not in families.select(ctx).describe()  # untuned: the library picks
+
+
+@pytest.mark.gpu
+def test_tuned_matmul_picks_a_kernel_config():
+    h = ninetoothed.make(pg.matmul_arrangement, pg.matmul_application, pg.matmul_tensors(), max_num_configs=4)
+    g = torch.Generator().manual_seed(5)
+    a, b = (torch.randn(512, 512, generator=g).half().cuda() for _ in range(2))
+    out = torch.empty(512, 512, dtype=torch.float16, device="cuda")
+    h(a, b, out)
+    assert torch.allclose(out.float(), (a.float() @ b.float()).half().float(), atol=2e-2, rtol=1e-2)
+    (plan,) = h.plans()
+    assert plan["family"] == "tuned" and len(plan["chosen"]) == 1 and '"config"' in plan["chosen"][0]

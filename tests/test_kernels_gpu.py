@@ -243,6 +243,32 @@ def test_gemm_dma_padded_leading_dims(k, dtype):
     assert torch.allclose(out.float(), ref.float(), atol=2e-2, rtol=1e-2)
 
 
+@pytest.mark.parametrize("config", (1, 2, 3))
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+def test_gemm_kernel_configs(config, dtype):
+    # Each forced kernel configuration (DMA, register-staged eight-wave, element-wise
+    # loader) on a call all three admit.
+    m, n, k = 512, 768, 256
+    a, b, c = _randn((m, k), dtype, 50), _randn((k, n), dtype, 51), _randn((m, n), dtype, 52)
+    out = torch.empty((m, n), dtype=dtype, device=DEV)
+    kernels.gemm(a, b, out, c=c, alpha=0.5, beta=2.0, round_dtype=torch.float16, config=config)
+    ref = _gemm_ref(a, b, c, 0.5, 2.0, torch.float16)
+    assert torch.allclose(out.float(), ref.float(), atol=2e-2, rtol=1e-2)
+
+
+def test_gemm_forced_config_rejects_unfit_call():
+    from ninetoothed_amd.errors import KernelLaunchError
+
+    a, b = _randn((300, 100), torch.float16, 53), _randn((100, 200), torch.float16, 54)
+    out = torch.full((300, 200), 7.0, dtype=torch.float16, device=DEV)
+    for config in (1, 2):  # M, N not multiples of 256: rejected before launching
+        with pytest.raises(KernelLaunchError):
+            kernels.gemm(a, b, out, config=config)
+    assert torch.all(out == 7.0)
+    kernels.gemm(a, b, out, config=3)
+    assert torch.allclose(out.float(), _gemm_ref(a, b).float(), atol=2e-2, rtol=1e-2)
+
+
 def test_addmm_headline_bf16():
     m = n = k = 4096
     g = 1.0 / math.sqrt(k)
