@@ -616,7 +616,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             }
             ow[d] = (uint32_t)elem<T>::from_float(a) | ((uint32_t)elem<T>::from_float(b) << 16);
           }
-          if (m_ok && k < g.K) *(u32x4*)(Y + ybase + (int64_t)k * g.ys[1]) = ow;
+          if (m_ok && k < g.K) __builtin_nontemporal_store(ow, (u32x4*)(Y + ybase + (int64_t)k * g.ys[1]));
         }
       }
   };

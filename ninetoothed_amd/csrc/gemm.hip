@@ -624,7 +624,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         ow[d] = OUT_F16 ? ((uint32_t)float_to_f16_bits(r2[0]) | ((uint32_t)float_to_f16_bits(r2[1]) << 16))
                         : ((uint32_t)float_to_bf16_bits(r2[0]) | ((uint32_t)float_to_bf16_bits(r2[1]) << 16));
       }
-      *(u32x4*)(o_lane + (i * 32 + h * 16 + t * 8) * o_row) = ow;
+      __builtin_nontemporal_store(ow, (u32x4*)(o_lane + (i * 32 + h * 16 + t * 8) * o_row));  // not re-read: no L2 allocation
     }
   };
   using OutF16 = std::integral_constant<bool, true>;
