@@ -181,6 +181,28 @@ int nt_conv2d_bf16(const void* x, const int64_t* x_strides, const void* w, const
                    int64_t dh, int64_t dw, int round_dtype, void* workspace,
                    int64_t workspace_bytes, hipStream_t stream);
 
+/* One path of the 16-bit convolution, for the auto-tuner: the arguments of
+ * nt_conv2d_f16/bf16 plus `config` (0 = the fastest path whose conditions hold, as
+ * nt_conv2d_*; 1 = the re-laid input through the DMA kernel: a workspace of
+ * nt_conv2d_workspace_size bytes, C % 64 == 0, C*R*S >= 128, Q % 8 == 0, y of the input
+ * type with unit q stride; 2 = the re-laid input through the N-H-W-C kernel: the
+ * workspace and C % 64 == 0; 3 = the direct kernel, no workspace).  A forced path whose
+ * conditions do not hold returns NT_ERR_INVALID before launching.  Replaces the
+ * per-configuration launchers the reference's auto-tuner times
+ * (src/ninetoothed/compiler/driver.py:975-1031, tests/test_conv2d.py:109-113). */
+int nt_conv2d_config_f16(const void* x, const int64_t* x_strides, const void* w, const int64_t* w_strides,
+                         void* y, const int64_t* y_strides, int y_dtype,
+                         int64_t N, int64_t C, int64_t H, int64_t W, int64_t K, int64_t R, int64_t S,
+                         int64_t P, int64_t Q, int64_t ph, int64_t pw, int64_t sh, int64_t sw,
+                         int64_t dh, int64_t dw, int round_dtype, void* workspace,
+                         int64_t workspace_bytes, int config, hipStream_t stream);
+int nt_conv2d_config_bf16(const void* x, const int64_t* x_strides, const void* w, const int64_t* w_strides,
+                          void* y, const int64_t* y_strides, int y_dtype,
+                          int64_t N, int64_t C, int64_t H, int64_t W, int64_t K, int64_t R, int64_t S,
+                          int64_t P, int64_t Q, int64_t ph, int64_t pw, int64_t sh, int64_t sw,
+                          int64_t dh, int64_t dw, int round_dtype, void* workspace,
+                          int64_t workspace_bytes, int config, hipStream_t stream);
+
 /* ---------------------------------------------------------------------------
  * Fused attention forward (online softmax in base 2), per (b, h):
  *   qs    = round_in(q * q_scale)                 q_scale = log2(e) * softmax scale

@@ -60,6 +60,10 @@ _SIGNATURES = {
         for t in ("f16", "bf16")
     },
     **{
+        f"nt_conv2d_config_{t}": (_P, _I64P, _P, _I64P, _P, _I64P, _I) + (_I64,) * 15 + (_I, _P, _I64, _I, _P)
+        for t in ("f16", "bf16")
+    },
+    **{
         f"nt_attention_{t}": (_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _I64, _I64, _I64, _I64, _I64, _F, _I, _P)
         for t in ("f32", "f16", "bf16")
     },

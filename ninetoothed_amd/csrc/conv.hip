@@ -639,7 +639,12 @@ template <typename T>
 static int conv_launch(const void* x, const int64_t* xs, const void* w, const int64_t* ws, void* y, const int64_t* ys,
                        int y_dtype, int64_t N, int64_t C, int64_t H, int64_t W, int64_t K, int64_t R, int64_t S,
                        int64_t P, int64_t Q, int64_t ph, int64_t pw, int64_t sh, int64_t sw, int64_t dh, int64_t dw,
-                       int round_dtype, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+                       int round_dtype, void* workspace, int64_t workspace_bytes, hipStream_t stream,
+                       int config = 0) {
+  // config: 0 = the fastest path whose conditions hold; 1 = re-laid input through the DMA
+  // kernel, 2 = re-laid input through conv_nhwc_kernel, 3 = the direct kernel (no
+  // workspace).  A forced path whose conditions do not hold is rejected before launching.
+  if (config < 0 || config > 3) return NT_ERR_INVALID;
   if (N < 0 || C < 0 || H < 0 || W < 0 || K < 0 || R < 0 || S < 0 || P < 0 || Q < 0 || ph < 0 || pw < 0 || sh <= 0 ||
       sw <= 0 || dh <= 0 || dw <= 0)
     return NT_ERR_INVALID;
@@ -664,10 +669,19 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
   g.tiles_k = (int)tiles_k;
   g.tiles_m = (int)tiles_m;
   const int64_t need = nhwc_bytes(N, C, H, W, K, R, S, ph, pw);
-  const bool nhwc = workspace != nullptr && workspace_bytes >= need && C % 64 == 0 && (uintptr_t)workspace % 256 == 0 &&
-                    (P - 1) * sh + (R - 1) * dh < H + 2 * ph && (Q - 1) * sw + (S - 1) * dw < W + 2 * pw;
+  const bool nhwc = config != 3 && workspace != nullptr && workspace_bytes >= need && C % 64 == 0 &&
+                    (uintptr_t)workspace % 256 == 0 && (P - 1) * sh + (R - 1) * dh < H + 2 * ph &&
+                    (Q - 1) * sw + (S - 1) * dw < W + 2 * pw;
+  if ((config == 1 || config == 2) && !nhwc) return NT_ERR_INVALID;
   if (nhwc) {
     const int64_t Hp = H + 2 * ph, Wp = W + 2 * pw;
+    // DMA kernel: at least three 32-deep k-tiles, 32-bit operand offsets, output written
+    // as 16-byte runs of 8 positions of one channel (Q % 8 == 0, y of the input type with
+    // unit q stride and 16-byte aligned rows).
+    const bool dma = g.KG >= 3 * 32 && g.KG % 32 == 0 && N * Hp * Wp * C * 2 < 0x7fffffffLL &&
+                     K * g.KG * 2 < 0x7fffffffLL && g.M < 0x7fffffffLL && y_dtype == elem<T>::code && Q % 8 == 0 &&
+                     ys[3] == 1 && ys[0] % 8 == 0 && ys[1] % 8 == 0 && ys[2] % 8 == 0 && (uintptr_t)y % 16 == 0;
+    if (config == 1 && !dma) return NT_ERR_INVALID;
     uint16_t* xp = (uint16_t*)workspace;
     uint16_t* wt = (uint16_t*)((char*)workspace + ((N * Hp * Wp * C * 2 + 255) / 256) * 256);
     int64_t fblocks = K * R * S;  // filter rows of the fast re-layout (at most 4096 workgroups)
@@ -686,13 +700,7 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
       hipLaunchKernelGGL(filter_krsc_kernel<T>, dim3((unsigned)fblocks), dim3(256), 0, stream, (const uint16_t*)w, wt,
                          g);
     }
-    // DMA kernel: at least three 32-deep k-tiles, 32-bit operand offsets, output written
-    // as 16-byte runs of 8 positions of one channel (Q % 8 == 0, y of the input type with
-    // unit q stride and 16-byte aligned rows).
-    const bool dma = g.KG >= 3 * 32 && g.KG % 32 == 0 && N * Hp * Wp * C * 2 < 0x7fffffffLL &&
-                     K * g.KG * 2 < 0x7fffffffLL && g.M < 0x7fffffffLL && y_dtype == elem<T>::code && Q % 8 == 0 &&
-                     ys[3] == 1 && ys[0] % 8 == 0 && ys[1] % 8 == 0 && ys[2] % 8 == 0 && (uintptr_t)y % 16 == 0;
-    if (dma)
+    if (config == 0 ? dma : config == 1)
       hipLaunchKernelGGL(conv_dma_kernel<T>, dim3((unsigned)(tiles_k * tiles_m)), dim3(512), 0, stream,
                          (const uint16_t*)xp, (const uint16_t*)wt, g, Hp, Wp);
     else
@@ -730,3 +738,14 @@ extern "C" int64_t nt_conv2d_workspace_size(int64_t N, int64_t C, int64_t H, int
   }
 NT_CONV_ENTRY(nt_conv2d_f16, nt::f16_t)
 NT_CONV_ENTRY(nt_conv2d_bf16, nt::bf16_t)
+
+#define NT_CONV_CONFIG_ENTRY(NAME, T)                                                                                \
+  extern "C" int NAME(const void* x, const int64_t* xs, const void* w, const int64_t* ws, void* y, const int64_t* ys, \
+                      int y_dtype, int64_t N, int64_t C, int64_t H, int64_t W, int64_t K, int64_t R, int64_t S,       \
+                      int64_t P, int64_t Q, int64_t ph, int64_t pw, int64_t sh, int64_t sw, int64_t dh, int64_t dw,   \
+                      int round_dtype, void* workspace, int64_t workspace_bytes, int config, hipStream_t stream) {   \
+    return nt::conv_launch<T>(x, xs, w, ws, y, ys, y_dtype, N, C, H, W, K, R, S, P, Q, ph, pw, sh, sw, dh, dw,       \
+                              round_dtype, workspace, workspace_bytes, stream, config);                              \
+  }
+NT_CONV_CONFIG_ENTRY(nt_conv2d_config_f16, nt::f16_t)
+NT_CONV_CONFIG_ENTRY(nt_conv2d_config_bf16, nt::bf16_t)

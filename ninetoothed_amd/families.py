@@ -323,10 +323,14 @@ class GemmPlan(Plan):
 class ConvPlan(Plan):
     family = "conv2d"
 
-    def __init__(self, x, w, y, padding, stride, dilation, round_dtype):
+    def __init__(self, x, w, y, padding, stride, dilation, round_dtype, config=0):
         self.x, self.w, self.y = x, w, y
         self.padding, self.stride, self.dilation = padding, stride, dilation
         self.round_dtype = round_dtype
+        self.config = config  # 0: the library picks the path; else one forced path
+
+    def with_config(self, config):
+        return ConvPlan(self.x, self.w, self.y, self.padding, self.stride, self.dilation, self.round_dtype, config)
 
     def bind(self, values, index):
         import torch
@@ -334,9 +338,9 @@ class ConvPlan(Plan):
         from ninetoothed_amd import kernels
 
         x, w, y = values[self.x], values[self.w], values[self.y]
-        nbytes = kernels.conv2d_workspace_bytes(x, w, self.padding)
+        nbytes = 0 if self.config == 3 else kernels.conv2d_workspace_bytes(x, w, self.padding)
         launch = kernels.bind_conv2d(x, w, y, padding=self.padding, stride=self.stride, dilation=self.dilation,
-                                     round_dtype=self.round_dtype, workspace_bytes=nbytes)
+                                     round_dtype=self.round_dtype, workspace_bytes=nbytes, config=self.config)
         ix, iw, iy = index[self.x], index[self.w], index[self.y]
         device = x.device
 
@@ -349,8 +353,11 @@ class ConvPlan(Plan):
         return run
 
     def describe(self):
-        return {"family": "conv2d", "padding": self.padding, "stride": self.stride, "dilation": self.dilation,
-                "round": str(self.round_dtype)}
+        d = {"family": "conv2d", "padding": self.padding, "stride": self.stride, "dilation": self.dilation,
+             "round": str(self.round_dtype)}
+        if self.config:
+            d["config"] = self.config
+        return d
 
 
 def _torch_dtype(name):
@@ -965,8 +972,10 @@ def candidates(ctx):
     """Every family plan whose pattern and geometry fit, in the order ``select`` tries them.
 
     A GEMM plan stands for each of the 16-bit GEMM's kernel configurations (the DMA kernel,
-    the register-staged one, the element-wise loader one): configurations the call's
-    operands do not admit fail when bound or launched and drop out of the timing."""
+    the register-staged one, the element-wise loader one) and a conv2d plan for each of the
+    convolution's paths (re-laid input through the DMA or the N-H-W-C kernel, the direct
+    kernel): configurations the call's operands do not admit fail when bound or launched
+    and drop out of the timing."""
     from ninetoothed_amd import kernels
 
     plans = []
@@ -977,6 +986,8 @@ def candidates(ctx):
             plan = None
         if isinstance(plan, GemmPlan) and not plan.config:
             plans.extend(plan.with_config(cfg) for cfg in kernels.GEMM_CONFIGS)
+        elif isinstance(plan, ConvPlan) and not plan.config:
+            plans.extend(plan.with_config(cfg) for cfg in kernels.CONV_CONFIGS)
         elif plan is not None:
             plans.append(plan)
     return plans

@@ -209,11 +209,20 @@ def conv2d_workspace_bytes(x, w, padding=(0, 0)):
     return int(lib.nt_conv2d_workspace_size(n, c, h, wd, k, r, s, padding[0], padding[1], _lib.dtype_code(x.dtype)))
 
 
-def bind_conv2d(x, w, y, padding=(0, 0), stride=(1, 1), dilation=(1, 1), round_dtype=None, workspace_bytes=0):
+# Paths of the 16-bit convolution that ``config`` can force (0: the fastest whose conditions
+# hold): re-laid input through the DMA kernel, re-laid input through the N-H-W-C kernel,
+# the direct kernel (no workspace).
+CONV_CONFIGS = (1, 2, 3)
+
+
+def bind_conv2d(x, w, y, padding=(0, 0), stride=(1, 1), dilation=(1, 1), round_dtype=None, workspace_bytes=0,
+                config=0):
     """launch(x, w, y, workspace): y = cast(round(conv2d(x, w))) as an implicit GEMM.
 
     Cross-correlation with zero padding.  ``workspace`` is a device buffer of at
-    least ``workspace_bytes`` bytes, or None when ``workspace_bytes`` is 0."""
+    least ``workspace_bytes`` bytes, or None when ``workspace_bytes`` is 0.  A nonzero
+    ``config`` forces one path; a call its conditions do not admit raises
+    ``KernelLaunchError`` without launching."""
     device = _check_device(x, w, y)
     if x.dim() != 4 or w.dim() != 4 or y.dim() != 4:
         raise ValueError("conv2d expects 4-D tensors")
@@ -228,7 +237,14 @@ def bind_conv2d(x, w, y, padding=(0, 0), stride=(1, 1), dilation=(1, 1), round_d
     sh, sw = stride
     dh, dw = dilation
     rd = _lib.DTYPE_NONE if round_dtype is None else _lib.dtype_code(round_dtype)
-    fn, name = _entry("nt_conv2d", x.dtype)
+    if config:
+        if config not in CONV_CONFIGS:
+            raise TypeError(f"conv2d config {config} is not one of {CONV_CONFIGS}")
+        fn, name = _entry("nt_conv2d_config", x.dtype)
+        extra = (int(config),)
+    else:
+        fn, name = _entry("nt_conv2d", x.dtype)
+        extra = ()
     xs, ws, ys = (_lib.int64_array(t.stride()) for t in (x, w, y))
     dims = (_lib.dtype_code(y.dtype), n, c, h, wd, k, r, s, p, q, ph, pw, sh, sw, dh, dw, rd)
     stream = _stream_of(device)
@@ -239,18 +255,18 @@ def bind_conv2d(x, w, y, padding=(0, 0), stride=(1, 1), dilation=(1, 1), round_d
             if workspace.device != device:
                 raise TypeError("All tensor arguments must use the same GPU.")
             wp = workspace.data_ptr()
-        code = fn(x.data_ptr(), xs, w.data_ptr(), ws, y.data_ptr(), ys, *dims, wp, workspace_bytes, stream())
+        code = fn(x.data_ptr(), xs, w.data_ptr(), ws, y.data_ptr(), ys, *dims, wp, workspace_bytes, *extra, stream())
         if code:
             _raise(code, name)
 
     return launch
 
 
-def conv2d(x, w, y, padding=(0, 0), stride=(1, 1), dilation=(1, 1), round_dtype=None, workspace=None):
+def conv2d(x, w, y, padding=(0, 0), stride=(1, 1), dilation=(1, 1), round_dtype=None, workspace=None, config=0):
     nbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     if workspace is not None:
         _check_device(x, workspace)
-    bind_conv2d(x, w, y, padding, stride, dilation, round_dtype, nbytes)(x, w, y, workspace)
+    bind_conv2d(x, w, y, padding, stride, dilation, round_dtype, nbytes, config)(x, w, y, workspace)
     return y
 
 

@@ -154,3 +154,30 @@ def test_tuned_matmul_picks_a_kernel_config():
     assert torch.allclose(out.float(), (a.float() @ b.float()).half().float(), atol=2e-2, rtol=1e-2)
     (plan,) = h.plans()
     assert plan["family"] == "tuned" and len(plan["chosen"]) == 1 and '"config"' in plan["chosen"][0]
+
+
+def test_conv_plans_expand_into_paths():
+    h = pg.make_conv2d()
+    x = torch.empty(2, 64, 16, 16, dtype=torch.float16)
+    w = torch.empty(96, 64, 3, 3, dtype=torch.float16)
+    y = torch.empty(2, 96, 16, 16, dtype=torch.float16)
+    names = list(h._kernel.params)
+    ctx = h._kernel.context(dict(zip(names, (x, w, y))), {"padding_h": 1, "padding_w": 1})
+    described = [p.describe() for p in families.candidates(ctx)]
+    assert [(d["family"], d["config"]) for d in described] == [("conv2d", 1), ("conv2d", 2), ("conv2d", 3)]
+
+
+@pytest.mark.gpu
+def test_tuned_conv_picks_a_path():
+    import torch.nn.functional as F
+
+    h = pg.make_conv2d(max_num_configs=4)
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(2, 64, 16, 16, generator=g).half().cuda()
+    w = (torch.randn(96, 64, 3, 3, generator=g) / 24).half().cuda()
+    y = torch.empty(2, 96, 16, 16, dtype=torch.float16, device="cuda")
+    h(x, w, y, padding_h=1, padding_w=1)
+    ref = F.conv2d(x.float(), w.float(), padding=1).half().float()
+    assert torch.allclose(y.float(), ref, atol=2e-2, rtol=1e-2)
+    (plan,) = h.plans()
+    assert plan["family"] == "tuned" and len(plan["chosen"]) == 1 and '"config"' in plan["chosen"][0]

@@ -366,6 +366,31 @@ def test_conv2d_relayout_dma(case, dtype):
     assert torch.allclose(y.float(), ref.to(torch.float16).float(), atol=2e-2, rtol=1e-2)
 
 
+@pytest.mark.parametrize("config", (1, 2, 3))
+def test_conv2d_paths(config):
+    # Each forced path (re-laid + DMA kernel, re-laid + N-H-W-C kernel, direct kernel) on a
+    # call all three admit.
+    x = _randn((2, 64, 16, 16), torch.float16, 60)
+    w = _randn((96, 64, 3, 3), torch.float16, 61, 1.0 / math.sqrt(64 * 9))
+    y = torch.empty((2, 96, 16, 16), dtype=torch.float16, device=DEV)
+    ws = _workspace(x, w, (1, 1)) if config != 3 else None
+    kernels.conv2d(x, w, y, padding=(1, 1), round_dtype=torch.float16, workspace=ws, config=config)
+    ref = F.conv2d(x.float(), w.float(), padding=1)
+    assert torch.allclose(y.float(), ref.to(torch.float16).float(), atol=2e-2, rtol=1e-2)
+
+
+def test_conv2d_forced_path_rejects_unfit_call():
+    from ninetoothed_amd.errors import KernelLaunchError
+
+    x = _randn((2, 24, 16, 16), torch.float16, 62)  # C % 64 != 0: no re-laid path
+    w = _randn((40, 24, 3, 3), torch.float16, 63, 0.1)
+    y = torch.full((2, 40, 14, 14), 7.0, dtype=torch.float16, device=DEV)
+    for config in (1, 2):
+        with pytest.raises(KernelLaunchError):
+            kernels.conv2d(x, w, y, config=config)
+    assert torch.all(y == 7.0)
+
+
 def test_conv2d_strided_dilated_bf16():
     x = _randn((2, 24, 21, 19), torch.bfloat16, 27)
     w = _randn((40, 24, 3, 5), torch.bfloat16, 28, 0.1)
