@@ -33,6 +33,15 @@ struct ConvArgs {
   int tiles_k, tiles_m;
 };
 
+// Workgroups are dispatched to the eight XCDs round-robin (b to XCD b % 8), each XCD with
+// its own L2.  This order hands XCD x the consecutive indices [x q + min(x, r), ...) of
+// `total` = 8 q + r, so neighbouring image rows of the re-layout, which share the cache
+// lines where one row of a channel plane runs into the next, meet in one L2.
+__device__ __forceinline__ int64_t xcd_order(int64_t b, int64_t total) {
+  const int64_t x = b % 8, q = total / 8, r = total % 8;
+  return x * q + (x < r ? x : r) + b / 8;
+}
+
 template <typename T, bool DENSE_W>
 __global__ __launch_bounds__(C_THREADS) void conv_direct_kernel(ConvArgs g) {
   __shared__ __attribute__((aligned(16))) uint16_t smem[(CB_K + CB_M) * TILE_K];
@@ -238,7 +247,8 @@ __global__ __launch_bounds__(256) void conv_relayout_kernel(const uint16_t* __re
     }
     return;
   }
-  const int64_t hp = (int64_t)blockIdx.x % Hp, n = (int64_t)blockIdx.x / Hp;
+  const int64_t rb = xcd_order(blockIdx.x, rows);
+  const int64_t hp = rb % Hp, n = rb / Hp;
   const int64_t h = hp - g.ph;
   const int64_t C = g.C, W = g.W;
   uint16_t* out_row = xp + ((n * Hp + hp) * Wp) * C;
