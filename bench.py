@@ -27,7 +27,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.join(ROOT, "tests"))
 
-PEAK = {"hbm": 8.0e12, "fp16": 2.5e15, "bf16": 2.5e15, "fp32": 157.3e12}
+PEAK = {"hbm": 8.0e12, "fp16": 2.5e15, "bf16": 2.5e15, "fp8": 5.0e15, "fp32": 157.3e12}
 
 
 def _args():
@@ -78,6 +78,19 @@ def _configs(torch, ninetoothed, pg):
 
     out.append(dict(name="matmul_fp32_512", workload="fp32 matmul C=A@B, M=N=K=512, N(0,1)", setup=matmul32,
                     work=2 * 512**3, unit="TFLOP/s", bound="mfma", peak=PEAK["fp32"], dtype="fp32"))
+
+    def matmul_e5m2():
+        # the reference's fp8 case (tests/test_matmul.py:64-88) at 4096^3: e5m2 lhs, column-major
+        # e5m2 rhs, fp16 output
+        a = randn((4096, 4096), torch.float16).to(torch.float8_e5m2)
+        b = randn((4096, 4096), torch.float16).T.to(torch.float8_e5m2)
+        o = torch.empty((4096, 4096), dtype=torch.float16, device=dev)
+        k = ninetoothed.make(pg.matmul_arrangement, pg.matmul_application, pg.matmul_tensors())
+        return lambda: k(a, b, o)
+
+    out.append(dict(name="matmul_e5m2_4096", workload="fp8 e5m2 matmul C=A@B (B column-major), fp16 out, M=N=K=4096, "
+                    "N(0,1)", setup=matmul_e5m2, work=2 * 4096**3, unit="TFLOP/s", bound="mfma", peak=PEAK["fp8"],
+                    dtype="e5m2"))
 
     def softmax():
         x = randn((8192, 8192), torch.float16, 2.0)

@@ -145,7 +145,8 @@ int nt_gemm_f32(const void* a, int64_t sa_m, int64_t sa_k, const void* b, int64_
                 int round_dtype, hipStream_t stream);
 /* fp8 operands (OCP float8_e5m2 / float8_e4m3fn, one byte per element, any strides); c and
  * out are f32/f16/bf16 as above.  The reference's float8_e5m2 matmul case,
- * tests/test_matmul.py:64-88 (a row-major, b column-major, fp16 out). */
+ * tests/test_matmul.py:64-88 (a row-major, b column-major, fp16 out), runs at the fp8
+ * matrix rate when M and N are multiples of 256 and K a multiple of 64 (at least 192). */
 int nt_gemm_e5m2(const void* a, int64_t sa_m, int64_t sa_k, const void* b, int64_t sb_k, int64_t sb_n,
                  const void* c, int64_t sc_m, int64_t sc_n, void* out, int64_t so_m, int64_t so_n,
                  int out_dtype, int64_t M, int64_t N, int64_t K, float alpha, float beta,

@@ -867,6 +867,130 @@ static int gemm16_launch(GemmArgs g, hipStream_t stream, int config = 0) {
 }
 
 // fp8 operands (any strides): the element-wise loader widens them to fp16.
+// fp8 operands at the fp8 matrix rate: v_mfma_scale_f32_32x32x64_f8f6f4 with unit scales
+// (E8M0 127), FMT 0 = e4m3fn, 1 = e5m2 (the OCP formats the instruction takes).  a [m][k]
+// and b^T [n][k] both k-contiguous (b column-major), M and N multiples of 256, K of 64 and
+// at least 192.  The structure of gemm_dma_kernel with 64-byte k-tiles (64 elements): the
+// same four-stage LDS ring filled by DMA, a and b^T rows alike with the XOR chunk swizzle.
+// An MFMA operand lane holds row (column) lane % 32 at k = 32 (lane / 32) .. + 31 (checked
+// on the device against an integer product), i.e. two ds_read_b128 of LDS chunks
+// 2 (lane / 32) and 2 (lane / 32) + 1.  Per k-tile a wave issues eight MFMAs (its 4 x 2
+// blocks of 32 x 32); the next tile's b fragments go to a second set, its a fragments
+// replace each a fragment right after the tile's last MFMA that reads it.
+template <int FMT>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_f8_dma_kernel(GemmArgs g) {
+  typedef int v8i __attribute__((ext_vector_type(8)));
+  __shared__ __attribute__((aligned(1024))) char lds[dma::EPI];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 2, wn = wave & 3;
+  int tm, tn;
+  tile_of(blockIdx.x, g.tiles_m, g.tiles_n, tm, tn);
+  const int64_t m0 = (int64_t)tm * GB_M, n0 = (int64_t)tn * GB_N;
+  const int nk = (int)(g.K / 64);
+
+  // Global side: byte offsets within each operand's 256-row panel fit in 32 bits (checked on
+  // the host).  Load q (0, 1) of this wave per k-tile: rows 32 wave + 16 q + lane / 4 of
+  // each operand, LDS chunk lane % 4 holding global chunk asw(row, lane % 4).
+  const u32x4 rsA = dma::rsrc((const uint8_t*)g.a + m0 * g.sa_m, (uint32_t)((GB_M - 1) * g.sa_m + g.K));
+  const u32x4 rsB = dma::rsrc((const uint8_t*)g.b + n0 * g.sb_n, (uint32_t)((GB_N - 1) * g.sb_n + g.K));
+  int va[2], vb[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int r = 32 * wave + 16 * q + (lane >> 2);
+    const int ch = dma::asw(r, lane & 3) * 16;
+    va[q] = (int)(r * g.sa_m) + ch;
+    vb[q] = (int)(r * g.sb_n) + ch;
+  }
+  // Load u (0..3) of tile kt into its stage: a q0, b q0, a q1, b q1.
+  auto load_unit = [&](int u, int kt) {
+    const int st = (kt % dma::STAGES) * dma::STAGE, q = u >> 1;
+    if ((u & 1) == 0)
+      dma::load_lds16(rsA, lds0 + st + 2048 * wave + 1024 * q, va[q], kt * 64);
+    else
+      dma::load_lds16(rsB, lds0 + dma::B0 + st + 2048 * wave + 1024 * q, vb[q], kt * 64);
+  };
+
+  // Fragment reads: a rows 128 wm + 32 i + lane % 32, b^T rows 64 wn + 32 j + lane % 32, the
+  // lane's chunks 2 (lane / 32) + c (the swizzle depends on lane % 32 only, so block i or j
+  // is 2048 bytes further).
+  int a_rd[2], b_rd[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int ra = wm * 128 + (lane & 31), rb = wn * 64 + (lane & 31);
+    a_rd[c] = ra * 64 + dma::asw(ra, 2 * (lane >> 5) + c) * 16;
+    b_rd[c] = dma::B0 + rb * 64 + dma::asw(rb, 2 * (lane >> 5) + c) * 16;
+  }
+  auto frag = [&](const int (&rd)[2], int st, int blk) {
+    const u32x4 lo = *(const u32x4*)(lds + rd[0] + st + blk * 2048);
+    const u32x4 hi = *(const u32x4*)(lds + rd[1] + st + blk * 2048);
+    return v8i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+  };
+  v8i fa[4], fb[2], fbn[2];
+  floatx16 acc[4][2];
+  zero_acc(acc);
+
+  // nk >= 3 (the launcher checks): tiles 0..2 in flight, wait for tile 0.
+  for (int kt = 0; kt < 3; ++kt)
+    for (int u = 0; u < 4; ++u) load_unit(u, kt);
+  asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) fa[i] = frag(a_rd, 0, i);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) fb[j] = frag(b_rd, 0, j);
+
+#define NT_F8FENCE() __builtin_amdgcn_sched_barrier(0)
+  // One k-tile.  HAS1: tile kt+1 exists (its fragments are read during this tile); LOAD:
+  // fetch tile kt+3 (into the stage of tile kt-1, whose fragments were all read during
+  // tile kt-2); VM: loads allowed outstanding once tile kt+1 has landed (-1: the last
+  // tile, no wait and no barrier).
+  auto step = [&](auto has1_c, auto load_c, auto vm_c, int kt) {
+    constexpr bool HAS1 = decltype(has1_c)::value, LOAD = decltype(load_c)::value;
+    constexpr int VM = decltype(vm_c)::value;
+    const int st1 = ((kt + 1) % dma::STAGES) * dma::STAGE;
+    static_for<0, 8>([&](auto m_c) {
+      constexpr int m = decltype(m_c)::value;
+      constexpr int i = m >> 1, j = m & 1;
+      if constexpr (m == 0 && VM >= 0) {
+        NT_F8FENCE();
+        if constexpr (VM == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+        if constexpr (VM == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        NT_F8FENCE();
+      }
+      acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[i], fb[j], acc[i][j], FMT, FMT, 0, 127, 0, 127);
+      NT_F8FENCE();
+      if constexpr (HAS1) {
+        if constexpr (m == 0) fbn[0] = frag(b_rd, st1, 0);
+        if constexpr (m == 1) fbn[1] = frag(b_rd, st1, 1);
+        if constexpr (j == 1) fa[i] = frag(a_rd, st1, i);
+      }
+      if constexpr (LOAD && m >= 1 && m <= 4) load_unit(m - 1, kt + 3);
+      NT_F8FENCE();
+    });
+    if constexpr (HAS1) {
+      fb[0] = fbn[0];
+      fb[1] = fbn[1];
+    }
+  };
+#undef NT_F8FENCE
+  using T1 = std::integral_constant<bool, true>;
+  using F1 = std::integral_constant<bool, false>;
+  using V4 = std::integral_constant<int, 4>;
+  using V0 = std::integral_constant<int, 0>;
+  using VN = std::integral_constant<int, -1>;
+  int kt = 0;
+  for (; kt + 3 < nk; ++kt) step(T1{}, T1{}, V4{}, kt);
+  step(T1{}, F1{}, V4{}, kt);
+  step(T1{}, F1{}, V0{}, kt + 1);
+  step(F1{}, F1{}, VN{}, kt + 2);
+
+  gemm_epilogue<4, 2>(g, acc, (uint16_t*)lds, wave, lane, m0 + wm * 128, n0 + wn * 64);
+}
+
 template <typename S>
 static int gemm8_launch(GemmArgs g, hipStream_t stream) {
   if (int e = gemm_check(g)) return e;
@@ -880,6 +1004,18 @@ static int gemm8_launch(GemmArgs g, hipStream_t stream) {
   if (tiles_m * tiles_n > 0x7fffffffLL) return NT_ERR_INVALID;
   g.tiles_m = (int)tiles_m;
   g.tiles_n = (int)tiles_n;
+  // The fp8-rate kernel: a k-contiguous, b column-major (b^T k-contiguous), whole 256 x 256
+  // tiles, 64-deep k-tiles (at least the three its pipeline keeps in flight), 16-byte
+  // aligned rows and 32-bit panel offsets.
+  const bool f8dma = g.sa_k == 1 && g.sb_k == 1 && g.M % GB_M == 0 && g.N % GB_N == 0 && g.K % 64 == 0 &&
+                     g.K >= 3 * 64 && g.sa_m >= 0 && g.sb_n >= 0 && g.sa_m % 16 == 0 && g.sb_n % 16 == 0 &&
+                     (uintptr_t)g.a % 16 == 0 && (uintptr_t)g.b % 16 == 0 &&
+                     (GB_M - 1) * g.sa_m + g.K <= 0x3fffffffLL && (GB_N - 1) * g.sb_n + g.K <= 0x3fffffffLL;
+  if (f8dma) {
+    constexpr int fmt = std::is_same<S, src_e4m3>::value ? 0 : 1;
+    hipLaunchKernelGGL((gemm_f8_dma_kernel<fmt>), dim3((unsigned)(tiles_m * tiles_n)), dim3(512), 0, stream, g);
+    return launch_status();
+  }
   hipLaunchKernelGGL((gemm_mfma_kernel<f16_t, false, S>), dim3((unsigned)(tiles_m * tiles_n)), dim3(G_THREADS), 0,
                      stream, g);
   return launch_status();

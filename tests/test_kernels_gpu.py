@@ -190,6 +190,44 @@ def test_gemm_fp8_ragged_strided(mnk, dtype):
     assert torch.allclose(out.float(), ref.float(), atol=tol, rtol=1e-2)
 
 
+@pytest.mark.parametrize("dtype", _FP8)
+def test_gemm_fp8_rate_kernel_every_finite_value(dtype):
+    # a k-contiguous, b column-major, M, N multiples of 256 and K of 64 (at least 192): the
+    # fp8-rate kernel (the matrix core multiplies the fp8 bytes themselves).  a is one-hot
+    # (row m selects k = m % 192) and b^T holds every finite byte pattern many times, so
+    # out = b[m % 192, :] exactly, which pins the operand lane layout and the format codes.
+    m, n, k = 512, 256, 192
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    finite = codes[torch.isfinite(codes.view(dtype).float())]
+    idx = torch.arange(n * k) % finite.numel()
+    bt = finite[idx].reshape(n, k).view(dtype).to(DEV)
+    b = bt.t()
+    a = torch.zeros((m, k), dtype=torch.float32)
+    a[torch.arange(m), torch.arange(m) % k] = 1.0
+    a = a.to(dtype).to(DEV)
+    out = torch.empty((m, n), dtype=torch.float32, device=DEV)
+    kernels.gemm(a, b, out)
+    assert torch.equal(out, b.float()[torch.arange(m, device=DEV) % k])
+
+
+@pytest.mark.parametrize("dtype", _FP8)
+@pytest.mark.parametrize("k", (192, 320, 1024))
+@pytest.mark.parametrize("padded", (False, True))
+def test_gemm_fp8_rate_kernel(k, padded, dtype):
+    # The fp8-rate kernel on random data with the addmm epilogue; padded: a and b^T as views
+    # of wider buffers (row strides K + 64 and K + 128), the kernel's offsets come from them.
+    m, n = 512, 768
+    pa, pb = (64, 128) if padded else (0, 0)
+    a = _randn((m, k + pa), torch.float16, 24).to(dtype)[:, :k]
+    b = _randn((n, k + pb), torch.float16, 25).to(dtype)[:, :k].t()
+    c = _randn((m, n), torch.float16, 26)
+    out = torch.empty((m, n), dtype=torch.float16, device=DEV)
+    kernels.gemm(a, b, out, c=c, alpha=0.5, beta=2.0, round_dtype=torch.float16)
+    ref = _gemm_ref(a.to(torch.float16), b.to(torch.float16), c, 0.5, 2.0, torch.float16)
+    tol = 1e-2 * max(1.0, math.sqrt(k) / 8)
+    assert torch.allclose(out.float(), ref.float(), atol=tol, rtol=1e-2)
+
+
 def test_addmm_epilogue():
     m = n = k = 512
     c = _randn((m, n), torch.float16, 13)
