@@ -3,20 +3,33 @@
 A step is one call of the hot path (one kernel through the drop-in ``make``/``jit``
 Handle) on inputs already resident in HBM.  The headline line is configs[1]: fp16
 addmm out = 0.5*C + 1.0*(A@B), M=N=K=4096.  The same JSON line carries every other
-configuration under "configs", each with its own roofline fraction.
+configuration under "configs", each with its own roofline fraction and CPU baseline.
 
-For each configuration: W untimed warm-up steps, then exactly K steps bracketed by
-torch.cuda.synchronize(), timed with HIP events recorded on the stream the kernels
-are launched on (torch's current stream, which the launchers pass to the library).
-roofline.achieved = algorithmic work per launch / average launch duration; peaks are
-MI355X's published figures (HBM 8 TB/s; dense fp16/bf16 MFMA 2.5 PFLOP/s; fp32 157.3
-TFLOP/s).  cpu_baseline: the CPU oracle (tile-by-tile numpy restatement of the
-application) timed on this host on a bounded sample; torch_cpu: torch's fp32 CPU op.
+Per configuration: max(W, 10) untimed warm-up steps; then exactly K steps bracketed by
+torch.cuda.synchronize(), timed with HIP events recorded on the stream the kernels are
+launched on (torch's current stream, which the launchers pass to the library) ->
+``ms_per_step`` and ``value``; then max(K, 50) further steps, each between its own pair
+of events -> ``median_ms`` and the 10th/90th percentiles (the spread).  The bandwidth-bound
+configurations (softmax, max_pool2d, add) rotate through buffer sets whose total exceeds
+the 256 MB Infinity Cache, so every step reads its inputs from HBM.
+
+roofline.achieved = algorithmic work per launch / average launch duration over the K
+steps; peaks are MI355X's published figures (HBM 8 TB/s; dense fp16/bf16 MFMA 2.5 PFLOP/s,
+fp8 5.0; fp32 157.3 TFLOP/s).  roofline.traffic is the HBM bytes per launch from the
+rocprofv3 FETCH_SIZE/WRITE_SIZE runs recorded in profiles/hbm_traffic.json (its
+``source`` says which run), not measured by this process.
+
+cpu_baseline (per configuration): the CPU oracle -- a tile-by-tile numpy restatement of
+the arrange-and-apply program (kind "port") -- timed on this host on a bounded sample of
+the configuration; torch_cpu: the torch fp32 CPU op the reference tests compare against,
+median of 3 runs after one warm-up.  The reference's own kernels under the Triton CPU
+interpreter are not available on the GPU box (the reference does not travel there).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only name,...] [--no-cpu]
 """
 
 import argparse
+import functools
 import json
 import math
 import os
@@ -28,6 +41,7 @@ sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 PEAK = {"hbm": 8.0e12, "fp16": 2.5e15, "bf16": 2.5e15, "fp8": 5.0e15, "fp32": 157.3e12}
+CACHE_BYTES = 256 * 2**20  # MI355X Infinity Cache
 
 
 def _args():
@@ -42,9 +56,163 @@ def _args():
     return p.parse_args()
 
 
-def _configs(torch, ninetoothed, pg):
-    import functools
+def _sets(set_bytes):
+    """Buffer sets to rotate so that their total exceeds the Infinity Cache (at least 2)."""
+    return max(2, math.ceil(1.5 * CACHE_BYTES / set_bytes))
 
+
+# ------------------------------------------------------------------ CPU baselines
+def _host():
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return model
+
+
+def _blas_threads():
+    try:
+        import threadpoolctl
+
+        return max(int(i.get("num_threads", 1)) for i in threadpoolctl.threadpool_info()) or 1
+    except Exception:  # pragma: no cover
+        return 1
+
+
+def _oracle_rate(fn, work, unit, sample, budget_s=3.0):
+    """Repeat the oracle call for about budget_s; work units per second."""
+    reps, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s or reps == 0:
+        fn()
+        reps += 1
+    dt = time.perf_counter() - t0
+    scale = 1e12 if unit == "TFLOP/s" else 1e9
+    return {"value": work * reps / dt / scale, "unit": unit, "cores": _blas_threads(), "kind": "port",
+            "sample": f"{sample}; {reps} run(s) in {dt:.1f} s"}
+
+
+def _torch_rate(torch, fn, work, unit, sample):
+    fn()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    scale = 1e12 if unit == "TFLOP/s" else 1e9
+    return {"value": work / times[1] / scale, "unit": unit, "threads": torch.get_num_threads(),
+            "sample": f"{sample}; median of 3 runs after one warm-up ({times[1] * 1e3:.1f} ms)"}
+
+
+def _cpu_cases(torch, pg):
+    """name -> (oracle sample, torch sample): each a zero-argument function returning its dict."""
+    import numpy as np
+    import torch.nn.functional as F
+
+    from oracle import apply
+
+    r = np.random.default_rng(0)
+
+    def nrm(shape, scale=1.0):
+        return np.asarray(r.standard_normal(shape) * scale, dtype=np.float32)
+
+    def tg(*shape, scale=1.0):
+        return torch.randn(*shape, generator=torch.Generator().manual_seed(0)) * scale
+
+    cases = {}
+
+    def addmm_case(name, rd):
+        n = 1024
+        c, a, b = (nrm((n, n), n**-0.5) for _ in range(3))
+        N = 2048
+        C, A, B = (tg(N, N, scale=N**-0.5) for _ in range(3))
+        cases[name] = (
+            lambda: _oracle_rate(lambda: apply.addmm(c, a, b, 0.5, 1.0, rd, pg.addmm_arrangement, block=(128, 128, 128)),
+                                 2 * n**3, "TFLOP/s", f"oracle addmm ({rd} rounding) {n}^3, 128^3 tiles"),
+            lambda: _torch_rate(torch, lambda: torch.addmm(C, A, B, beta=0.5, alpha=1.0), 2 * N**3, "TFLOP/s",
+                                f"torch.addmm fp32 {N}^3"))
+
+    addmm_case("addmm_fp16_4096", "float16")
+    addmm_case("addmm_bf16_4096", "bfloat16")
+
+    a32, b32 = nrm((512, 512)), nrm((512, 512))
+    A32, B32 = tg(512, 512), tg(512, 512)
+    cases["matmul_fp32_512"] = (
+        lambda: _oracle_rate(lambda: apply.matmul(a32, b32, "float32", pg.matmul_arrangement, block=(64, 64, 64),
+                                                  round_dtype=None), 2 * 512**3, "TFLOP/s",
+                             "oracle matmul fp32 512^3 (the full configuration), 64^3 tiles"),
+        lambda: _torch_rate(torch, lambda: torch.matmul(A32, B32), 2 * 512**3, "TFLOP/s", "torch.matmul fp32 512^3"))
+
+    f8 = torch.float8_e5m2
+    a8 = torch.from_numpy(nrm((1024, 1024))).to(f8).float().numpy()
+    b8 = torch.from_numpy(nrm((1024, 1024))).to(f8).float().numpy()
+    A8, B8 = tg(2048, 2048).to(f8).float(), tg(2048, 2048).to(f8).float()
+    cases["matmul_e5m2_4096"] = (
+        lambda: _oracle_rate(lambda: apply.matmul(a8, b8, "float16", pg.matmul_arrangement, block=(128, 128, 128)),
+                             2 * 1024**3, "TFLOP/s", "oracle matmul on e5m2 values 1024^3, fp16 out, 128^3 tiles"),
+        lambda: _torch_rate(torch, lambda: torch.matmul(A8, B8), 2 * 2048**3, "TFLOP/s",
+                            "torch.matmul fp32 2048^3 on e5m2 values"))
+
+    xs = nrm((1024, 8192), 2.0)
+    XS = tg(8192, 8192, scale=2.0)
+    cases["softmax_fp16_8192"] = (
+        lambda: _oracle_rate(lambda: apply.softmax(xs, 8192, "float16"), 2 * 1024 * 8192 * 2, "GB/s",
+                             "oracle softmax fp16 [1024, 8192] (fp16 bytes)"),
+        lambda: _torch_rate(torch, lambda: torch.softmax(XS, -1), 2 * 8192 * 8192 * 4, "GB/s",
+                            "torch.softmax fp32 [8192, 8192] (fp32 bytes)"))
+
+    xp = np.asarray(r.uniform(-1, 1, (2, 128, 112, 112)), dtype=np.float32)
+    XP = torch.rand(32, 128, 112, 112, generator=torch.Generator().manual_seed(0)) * 2 - 1
+    pool_arr = functools.partial(pg.max_pool2d_arrangement, ceil_mode=False)
+    cases["max_pool2d_fp16"] = (
+        lambda: _oracle_rate(lambda: apply.max_pool2d(xp, (2, 2), False, pool_arr, block=256),
+                             (2 * 128 * 112 * 112 + 2 * 128 * 56 * 56) * 2, "GB/s",
+                             "oracle max_pool2d [2, 128, 112, 112] 2x2 (fp16 bytes)"),
+        lambda: _torch_rate(torch, lambda: F.max_pool2d(XP, 2), (32 * 128 * 112 * 112 + 32 * 128 * 56 * 56) * 4, "GB/s",
+                            "F.max_pool2d fp32 [32, 128, 112, 112] 2x2 (fp32 bytes)"))
+
+    xc, wc = nrm((1, 128, 56, 56)), nrm((128, 128, 3, 3), (128 * 9) ** -0.5)
+    XC, WC = tg(4, 256, 56, 56), tg(256, 256, 3, 3, scale=(256 * 9) ** -0.5)
+    conv_arr = functools.partial(pg.conv2d_arrangement, enable_padding=True)
+    cases["conv2d_fp16"] = (
+        lambda: _oracle_rate(lambda: apply.conv2d(xc, wc, (1, 1), conv_arr, block=(128, 128, 128)),
+                             2 * 56 * 56 * 128 * 128 * 9, "TFLOP/s", "oracle conv2d [1, 128, 56, 56] * [128, 128, 3, 3]"),
+        lambda: _torch_rate(torch, lambda: F.conv2d(XC, WC, padding=1), 2 * 4 * 56 * 56 * 256 * 256 * 9, "TFLOP/s",
+                            "F.conv2d fp32 [4, 256, 56, 56] * [256, 256, 3, 3] (a quarter of the batch)"))
+
+    for causal in (False, True):
+        qa = nrm((1, 2, 1024, 128))
+        QA = tg(1, 8, 4096, 128)
+        div = 2 if causal else 1
+        name = f"attention_fp16_{'causal' if causal else 'noncausal'}"
+        cases[name] = (
+            functools.partial(
+                _oracle_rate,
+                functools.partial(apply.attention, qa, qa, qa, causal, pg.attention_arrangement, block=(64, 64)),
+                4 * 2 * 1024 * 1024 * 128 // div, "TFLOP/s", f"oracle attention [1, 2, 1024, 128] causal={causal}"),
+            functools.partial(
+                _torch_rate, torch,
+                functools.partial(F.scaled_dot_product_attention, QA, QA, QA, is_causal=causal, scale=128**-0.5),
+                4 * 8 * 4096 * 4096 * 128 // div, "TFLOP/s",
+                f"F.scaled_dot_product_attention fp32 [1, 8, 4096, 128] causal={causal} (a sixteenth of the heads)"))
+
+    va = nrm((1 << 22,))
+    VA = tg(1 << 27)
+    cases["add_fp16"] = (
+        lambda: _oracle_rate(lambda: apply.add(va, va, 1024, "float16"), 3 * (1 << 22) * 2, "GB/s",
+                             "oracle add fp16 2^22 elements (fp16 bytes)"),
+        lambda: _torch_rate(torch, lambda: torch.add(VA, VA), 3 * (1 << 27) * 4, "GB/s",
+                            "torch.add fp32 2^27 elements (fp32 bytes)"))
+    return cases
+
+
+# ------------------------------------------------------------------ GPU configurations
+def _configs(torch, ninetoothed, pg):
     dev = "cuda"
     g = torch.Generator().manual_seed(1234)
 
@@ -62,7 +230,7 @@ def _configs(torch, ninetoothed, pg):
             c, a, b = (randn((4096, 4096), dtype, s) for _ in range(3))
             o = torch.empty_like(c)
             k = ninetoothed.make(pg.addmm_arrangement, pg.addmm_application, pg.addmm_tensors())
-            return lambda: k(c, a, b, 0.5, 1.0, o)
+            return [lambda: k(c, a, b, 0.5, 1.0, o)]
 
         out.append(dict(name=name, workload=label, setup=setup, work=2 * 4096**3, unit="TFLOP/s", bound="mfma",
                         peak=PEAK["fp16"], dtype="fp16" if dtype == torch.float16 else "bf16"))
@@ -74,7 +242,7 @@ def _configs(torch, ninetoothed, pg):
         a, b = randn((512, 512), torch.float32), randn((512, 512), torch.float32)
         o = torch.empty((512, 512), device=dev)
         k = ninetoothed.make(pg.matmul_arrangement, pg.matmul_application_fp32, pg.matmul_tensors())
-        return lambda: k(a, b, o)
+        return [lambda: k(a, b, o)]
 
     out.append(dict(name="matmul_fp32_512", workload="fp32 matmul C=A@B, M=N=K=512, N(0,1)", setup=matmul32,
                     work=2 * 512**3, unit="TFLOP/s", bound="mfma", peak=PEAK["fp32"], dtype="fp32"))
@@ -86,38 +254,45 @@ def _configs(torch, ninetoothed, pg):
         b = randn((4096, 4096), torch.float16).T.to(torch.float8_e5m2)
         o = torch.empty((4096, 4096), dtype=torch.float16, device=dev)
         k = ninetoothed.make(pg.matmul_arrangement, pg.matmul_application, pg.matmul_tensors())
-        return lambda: k(a, b, o)
+        return [lambda: k(a, b, o)]
 
     out.append(dict(name="matmul_e5m2_4096", workload="fp8 e5m2 matmul C=A@B (B column-major), fp16 out, M=N=K=4096, "
                     "N(0,1)", setup=matmul_e5m2, work=2 * 4096**3, unit="TFLOP/s", bound="mfma", peak=PEAK["fp8"],
                     dtype="e5m2"))
 
     def softmax():
-        x = randn((8192, 8192), torch.float16, 2.0)
-        y = torch.empty_like(x)
         k = pg.make_softmax()
-        return lambda: k(x, y, BLOCK_SIZE=8192)
+        fns = []
+        for _ in range(_sets(2 * 8192 * 8192 * 2)):
+            x = randn((8192, 8192), torch.float16, 2.0)
+            y = torch.empty_like(x)
+            fns.append(lambda x=x, y=y: k(x, y, BLOCK_SIZE=8192))
+        return fns
 
     out.append(dict(name="softmax_fp16_8192", workload="fp16 row softmax [8192, 8192], N(0,4)", setup=softmax,
                     work=2 * 8192 * 8192 * 2, unit="GB/s", bound="hbm", peak=PEAK["hbm"], dtype="fp16"))
 
+    pool_bytes = (32 * 128 * 112 * 112 + 32 * 128 * 56 * 56) * 2
+
     def pool():
-        x = rand((32, 128, 112, 112), torch.float16, -1.0, 1.0)
-        y = torch.empty((32, 128, 56, 56), dtype=torch.float16, device=dev)
         k = ninetoothed.make(functools.partial(pg.max_pool2d_arrangement, ceil_mode=False), pg.max_pool2d_application,
                              pg.max_pool2d_tensors())
-        return lambda: k(x, y, WINDOW_HEIGHT=2, WINDOW_WIDTH=2)
+        fns = []
+        for _ in range(_sets(pool_bytes)):
+            x = rand((32, 128, 112, 112), torch.float16, -1.0, 1.0)
+            y = torch.empty((32, 128, 56, 56), dtype=torch.float16, device=dev)
+            fns.append(lambda x=x, y=y: k(x, y, WINDOW_HEIGHT=2, WINDOW_WIDTH=2))
+        return fns
 
     out.append(dict(name="max_pool2d_fp16", workload="fp16 max_pool2d 2x2 s2, NCHW [32,128,112,112], U(-1,1)",
-                    setup=pool, work=(32 * 128 * 112 * 112 + 32 * 128 * 56 * 56) * 2, unit="GB/s", bound="hbm",
-                    peak=PEAK["hbm"], dtype="fp16"))
+                    setup=pool, work=pool_bytes, unit="GB/s", bound="hbm", peak=PEAK["hbm"], dtype="fp16"))
 
     def conv():
         x = randn((16, 256, 56, 56), torch.float16)
         w = randn((256, 256, 3, 3), torch.float16, 1.0 / math.sqrt(256 * 9))
         y = torch.empty_like(x)
         k = pg.make_conv2d()
-        return lambda: k(x, w, y, padding_h=1, padding_w=1)
+        return [lambda: k(x, w, y, padding_h=1, padding_w=1)]
 
     out.append(dict(name="conv2d_fp16", workload="fp16 conv2d [16,256,56,56] * [256,256,3,3], pad 1 (implicit GEMM)",
                     setup=conv, work=2 * (16 * 56 * 56) * 256 * (256 * 9), unit="TFLOP/s", bound="mfma",
@@ -128,7 +303,7 @@ def _configs(torch, ninetoothed, pg):
             q, k_, v = (randn((4, 32, 4096, 128), torch.float16) for _ in range(3))
             o = torch.empty_like(q)
             k = ninetoothed.make(pg.attention_arrangement, pg.attention_application_scaled, pg.attention_tensors())
-            return lambda: k(q, k_, v, causal, o)
+            return [lambda: k(q, k_, v, causal, o)]
 
         return setup
 
@@ -138,61 +313,48 @@ def _configs(torch, ninetoothed, pg):
                         workload=f"fp16 SDPA B=4 H=32 S=4096 D=128 scale 1/sqrt(128), causal={causal}",
                         setup=attention(causal), work=flops, unit="TFLOP/s", bound="mfma", peak=PEAK["fp16"],
                         dtype="fp16"))
+
+    n_add = 1 << 27
+    add_bytes = 3 * n_add * 2
+
+    def add():
+        k = pg.make_add()
+        fns = []
+        for _ in range(_sets(add_bytes)):
+            a, b = randn((n_add,), torch.float16), randn((n_add,), torch.float16)
+            o = torch.empty_like(a)
+            fns.append(lambda a=a, b=b, o=o: k(a, b, o))
+        return fns
+
+    out.append(dict(name="add_fp16", workload="fp16 elementwise add, 2^27 elements, N(0,1) (reference tests/test_add.py "
+                    "program)", setup=add, work=add_bytes, unit="GB/s", bound="hbm", peak=PEAK["hbm"], dtype="fp16"))
     return out
 
 
-def _time(torch, fn, steps, warmup):
-    for _ in range(warmup):
-        fn()
+def _time(torch, fns, steps, warmup, samples):
+    """(seconds per step over exactly `steps` steps, sorted per-step seconds of `samples` more)."""
+    n = len(fns)
+    for i in range(warmup):
+        fns[i % n]()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start.record(stream)
-    for _ in range(steps):
-        fn()
+    for i in range(steps):
+        fns[i % n]()
     stop.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    return start.elapsed_time(stop) / 1e3 / steps, wall / steps
-
-
-def _cpu_baseline(torch, pg, budget_s=12.0):
-    """The oracle addmm (fp16 in, fp32 accumulate) on a 1024^3 instance, repeated for ~budget_s."""
-    import numpy as np
-
-    from oracle import apply
-
-    try:
-        import threadpoolctl
-
-        cores = max(int(i.get("num_threads", 1)) for i in threadpoolctl.threadpool_info()) or 1
-    except Exception:  # pragma: no cover
-        cores = os.cpu_count() or 1
-    r = np.random.default_rng(0)
-    n = 1024
-    s = 1.0 / math.sqrt(n)
-    c, a, b = (np.asarray(r.standard_normal((n, n)) * s, dtype=np.float32).astype(np.float16).astype(np.float32)
-               for _ in range(3))
-    reps, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < budget_s or reps == 0:
-        apply.addmm(c, a, b, 0.5, 1.0, "float16", pg.addmm_arrangement, block=(128, 128, 128))
-        reps += 1
-    dt = time.perf_counter() - t0
-    oracle = {"value": 2 * n**3 * reps / dt / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
-              "sample": f"oracle addmm fp16 {n}x{n}x{n} (tile-by-tile numpy, 128^3 tiles), {reps} runs in {dt:.1f}s"}
-    # torch's fp32 CPU addmm at the full 4096^3 shape (the reference tests' CPU-side oracle).
-    torch.set_num_threads(os.cpu_count() or 1)
-    g = torch.Generator().manual_seed(0)
-    C, A, B = (torch.randn(4096, 4096, generator=g) for _ in range(3))
-    torch.addmm(C[:256], A[:256], B, beta=0.5, alpha=1.0)
-    t0 = time.perf_counter()
-    torch.addmm(C, A, B, beta=0.5, alpha=1.0)
-    dt = time.perf_counter() - t0
-    torch_cpu = {"value": 2 * 4096**3 / dt / 1e12, "unit": "TFLOP/s", "threads": torch.get_num_threads(),
-                 "sample": "torch.addmm fp32 4096^3 on CPU, one run"}
-    return oracle, torch_cpu
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(samples)]
+    for i, (a, b) in enumerate(events):
+        a.record(stream)
+        fns[i % n]()
+        b.record(stream)
+    torch.cuda.synchronize()
+    each = sorted(a.elapsed_time(b) / 1e3 for a, b in events)
+    return start.elapsed_time(stop) / 1e3 / steps, wall / steps, each
 
 
 def main():
@@ -206,7 +368,7 @@ def main():
     if args.calibrate_copy:
         x = torch.empty(64 * 1024 * 1024, dtype=torch.float32, device="cuda").fill_(1.0)
         y = torch.empty_like(x)
-        sec, _ = _time(torch, lambda: y.copy_(x), args.steps, args.warmup)
+        sec, _, _ = _time(torch, [lambda: y.copy_(x)], args.steps, args.warmup, 1)
         print(json.dumps({"calibration": "copy", "bytes_read": x.numel() * 4, "bytes_written": y.numel() * 4,
                           "ms_per_copy": sec * 1e3}), flush=True)
         return
@@ -216,35 +378,41 @@ def main():
 
     configs = _configs(torch, ninetoothed, pg)
     only = set(filter(None, args.only.split(",")))
+    traffic = _traffic()
+    warmup, samples = max(args.warmup, 10), max(args.steps, 50)
     results = []
     for cfg in configs:
         if only and cfg["name"] not in only:
             continue
-        fn = cfg["setup"]()
-        sec, wall = _time(torch, fn, args.steps, args.warmup)
+        fns = cfg["setup"]()
+        sec, wall, each = _time(torch, fns, args.steps, warmup, samples)
         scale = 1e12 if cfg["unit"] == "TFLOP/s" else 1e9
         achieved = cfg["work"] / sec
+        pct = lambda q: each[min(len(each) - 1, int(q * len(each)))] * 1e3  # noqa: E731
+        entry = traffic.get(cfg["name"], {})
         results.append({
             "name": cfg["name"], "workload": cfg["workload"], "dtype": cfg["dtype"],
             "value": achieved / scale, "unit": cfg["unit"], "ms_per_step": sec * 1e3,
-            "host_ms_per_step": wall * 1e3,
+            "median_ms": pct(0.5), "p10_ms": pct(0.1), "p90_ms": pct(0.9), "samples": samples,
+            "host_ms_per_step": wall * 1e3, "buffer_sets": len(fns),
             "roofline": {"bound": cfg["bound"], "achieved": achieved / scale, "peak": cfg["peak"] / scale,
-                         "unit": cfg["unit"], "frac": achieved / cfg["peak"]},
+                         "unit": cfg["unit"], "frac": achieved / cfg["peak"],
+                         "traffic": entry.get("bytes"), "traffic_source": entry.get("source")},
         })
-        del fn
+        del fns
         torch.cuda.empty_cache()
         print(f"# {cfg['name']}: {achieved / scale:.1f} {cfg['unit']} ({achieved / cfg['peak'] * 100:.1f}% of peak), "
-              f"{sec * 1e3:.3f} ms/step", file=sys.stderr, flush=True)
+              f"{sec * 1e3:.4f} ms/step, median {pct(0.5):.4f} ms (p10 {pct(0.1):.4f}, p90 {pct(0.9):.4f})",
+              file=sys.stderr, flush=True)
 
     head = next((r for r in results if r["name"] == "addmm_fp16_4096"), results[0] if results else None)
-    traffic = _traffic()
     line = {
         "metric": "TFLOP/s (matmul/conv/attn) and GB/s (softmax) + % of MI355X roofline, 1 GPU",
         "value": head["value"] if head else None,
         "unit": head["unit"] if head else None,
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": args.warmup,
+        "warmup": warmup,
         "ms_per_step": head["ms_per_step"] if head else None,
         "higher_is_better": True,
         "scaling": "weak",
@@ -252,13 +420,24 @@ def main():
         "dtype": head["dtype"] if head else None,
         "data": "synthetic (seeded CPU generator, moved to the GPU before timing)",
         "config": {"workload": head["workload"] if head else None, "entry": "ninetoothed_amd.make (drop-in Handle)"},
-        "roofline": dict(head["roofline"], traffic=traffic.get(head["name"]) if head else None) if head else None,
+        "roofline": dict(head["roofline"]) if head else None,
         "configs": results,
     }
     if not args.no_cpu:
-        oracle, torch_cpu = _cpu_baseline(torch, pg)
-        line["cpu_baseline"] = oracle
-        line["torch_cpu"] = torch_cpu
+        cases = _cpu_cases(torch, pg)
+        for r in results:
+            if r["name"] in cases:
+                oracle_fn, torch_fn = cases[r["name"]]
+                r["cpu_baseline"] = oracle_fn()
+                r["torch_cpu"] = torch_fn()
+                print(f"# cpu {r['name']}: oracle {r['cpu_baseline']['value']:.4g} {r['cpu_baseline']['unit']}, "
+                      f"torch {r['torch_cpu']['value']:.4g}", file=sys.stderr, flush=True)
+        if head is not None and "cpu_baseline" in head:
+            line["cpu_baseline"] = head["cpu_baseline"]
+            line["torch_cpu"] = head["torch_cpu"]
+        line["host"] = {"cpu_model": _host(), "os_cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads(),
+                        "blas_threads": _blas_threads(),
+                        "reference_interpreter": "unavailable on the GPU box (the reference does not travel there)"}
     print(json.dumps(line), flush=True)
 
 
@@ -267,9 +446,11 @@ def _traffic():
     path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
     try:
         with open(path) as f:
-            return json.load(f)
+            data = json.load(f)
     except (OSError, ValueError):
         return {}
+    source = data.get("source")
+    return {k: {"bytes": v, "source": source} for k, v in data.get("bytes_per_launch", {}).items()}
 
 
 if __name__ == "__main__":

@@ -41,6 +41,8 @@ extern "C" {
 #define NT_DTYPE_F32 0
 #define NT_DTYPE_F16 1
 #define NT_DTYPE_BF16 2
+#define NT_DTYPE_E5M2 3 /* GEMM bias (c) only: OCP float8_e5m2 */
+#define NT_DTYPE_E4M3 4 /* GEMM bias (c) only: OCP float8_e4m3fn */
 
 /* Manifest check: returns NT_ABI_VERSION. Replaces the reference's ABI field of
  * its built manifest (reference src/ninetoothed/compiler/runtime.py:1485-1503). */
@@ -107,7 +109,10 @@ int nt_max_pool2d_bf16(const void* x, const int64_t* x_strides, void* y, const i
  *   out[m,n]  = cast_out(beta * c[m,n] + alpha * round(acc[m,n]))     (fp32 math)
  * `round` rounds acc to `round_dtype` first (NT_DTYPE_NONE = no rounding); it is
  * the application's `accumulator.to(ntl.float16)` (reference tests/test_matmul.py:47).
- * c may be NULL (then beta is ignored); c and out have element type `out_dtype`.
+ * c may be NULL (then beta is ignored).  `out_dtype` packs two codes: bits 0-7 are
+ * out's element type (NT_DTYPE_F32/F16/BF16); bits 8-15 are c's type + 1, or 0 when
+ * c has out's type.  c may be fp8 (NT_DTYPE_E5M2/E4M3, widened exactly), as in the
+ * reference's float8_e5m2 addmm case (tests/test_addmm.py:65-85: fp8 input, fp16 out).
  * Plain matmul is alpha = 1, c = NULL.  Replaces the launchers of the matmul and
  * addmm applications (reference tests/test_matmul.py:14-47, tests/test_addmm.py:13-38;
  * blocked-linalg schedule, src/ninetoothed/compiler/passes.py:1070-1084).

@@ -23,6 +23,8 @@ DTYPE_NONE = -1
 DTYPE_F32 = 0
 DTYPE_F16 = 1
 DTYPE_BF16 = 2
+DTYPE_E5M2 = 3  # GEMM bias (c) only
+DTYPE_E4M3 = 4
 
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
@@ -126,6 +128,16 @@ def dtype_code(dtype) -> int:
         return codes[dtype]
     except KeyError:
         raise TypeError(f"dtype {dtype} is not supported by the MI355X kernels") from None
+
+
+def bias_dtype_code(dtype) -> int:
+    """Element-type code of a GEMM's c operand: the float codes plus the fp8 formats."""
+    import torch
+
+    fp8 = {getattr(torch, "float8_e5m2", None): DTYPE_E5M2, getattr(torch, "float8_e4m3fn", None): DTYPE_E4M3}
+    if dtype in fp8 and dtype is not None:
+        return fp8[dtype]
+    return dtype_code(dtype)
 
 
 def dtype_suffix(dtype) -> str:

@@ -1,19 +1,32 @@
-"""Auto-tuning: pick the fastest of several candidate launchers per argument key.
+"""Auto-tuning: time every candidate launcher of a call once, then always run the fastest.
 
-The reference's contract (``src/ninetoothed/auto_tuner.py:14-202``): ``AutoTuner(funcs,
-keys, *, benchmark=None, cache_namespace=None, validator=None)``; a call validates the
-arguments, looks up the best candidate for their key (shapes, strides, dtypes, devices
-and the other values), benchmarks every candidate the first time a key is seen — a
-candidate that raises gets an infinite timing and the reason is kept — and runs the
-winner.  Timings persist per candidate and per selection in JSON files under the cache
-directory (``$NINETOOTHED_AMD_CACHE_DIR``, default ``~/.cache/ninetoothed_amd``), in a
-folder named by a digest of the namespace and the candidate keys, so a new process
-reuses them without benchmarking.
+Public contract (the reference's constructor and call, ``src/ninetoothed/auto_tuner.py:14-30``):
+``AutoTuner(funcs, keys, *, benchmark=None, cache_namespace=None, validator=None)`` with one
+key per candidate; ``tuner(*args, **kwargs)`` runs ``validator(args, kwargs)`` if given,
+chooses a candidate for the call's signature and returns that candidate's result.  A
+candidate whose benchmark raises is never chosen; when all of them raise, ``RuntimeError``
+names every candidate with its reason.  ``benchmark(func, args, kwargs)`` returns a time
+(any unit, smaller is better).
+
+How it is organised here:
+
+* **Signature** of a call (``signature``): a JSON string of each argument's description.
+  Tensors are described by dtype, shape, strides, device and whether the data pointer is
+  16-byte aligned (kernels with vector loads accept only aligned operands, so an aligned
+  and a misaligned call of one shape are different tuning problems); other values by
+  their ``repr``.
+* **Timing book** (``TimingBook``): one JSON file per (namespace, candidate keys) under
+  ``$NINETOOTHED_AMD_CACHE_DIR/tuning`` (default ``~/.cache/ninetoothed_amd``), holding
+  ``{signature: {candidate label: milliseconds or "error: ..."}}``.  Entries are merged
+  into the file under a process-wide lock and written atomically, so several tuners and
+  processes share what was measured and a new process re-times nothing it finds there.
+* **Election**: the first call with a new signature fills in the missing entries of its
+  row by benchmarking those candidates, takes the smallest time, runs the winner, and
+  remembers it in memory only once that run returned (a winner that raises is not kept).
 
 Handles use it when ``make``/``jit`` get ``max_num_configs`` > 1: the candidates are the
-kernel plans of every family whose pattern and geometry fit the call (e.g. the
-elementwise add kernel and the generic kernel), never for programs that update a tensor
-they also read.
+kernel plans (and kernel configurations) that fit the call; programs that update a tensor
+they read are never tuned, since timing them would change their output.
 """
 
 import hashlib
@@ -24,155 +37,170 @@ import threading
 import time
 from pathlib import Path
 
+_BOOK_LOCK = threading.Lock()
+
 
 def cache_dir():
     root = os.environ.get("NINETOOTHED_AMD_CACHE_DIR")
     return Path(root) if root else Path.home() / ".cache" / "ninetoothed_amd"
 
 
-def _digest(obj):
-    return hashlib.sha256(json.dumps(obj, sort_keys=True, default=str).encode()).hexdigest()[:24]
+def _describe(value):
+    if hasattr(value, "shape") and hasattr(value, "dtype"):
+        stride = list(value.stride()) if hasattr(value, "stride") else None
+        pointer = value.data_ptr() if hasattr(value, "data_ptr") else 0
+        return ["tensor", str(value.dtype).replace("torch.", ""), list(value.shape), stride,
+                str(getattr(value, "device", "")), pointer % 16 == 0]
+    return repr(value)
 
 
-def _read(path):
-    try:
-        return json.loads(Path(path).read_text())
-    except (OSError, ValueError):
-        return None
+def signature(args, kwargs):
+    """The tuning key of a call: what a kernel's speed and admissibility depend on."""
+    return json.dumps([[_describe(a) for a in args], [[k, _describe(v)] for k, v in sorted(kwargs.items())]],
+                      separators=(",", ":"))
 
 
-def _write(path, data):
-    path = Path(path)
-    tmp = path.with_suffix(f".{os.getpid()}.{threading.get_ident()}.tmp")
-    tmp.write_text(json.dumps(data, indent=1, sort_keys=True))
-    os.replace(tmp, path)
-
-
-def _candidate_id(key):
+def _label(key):
     return key if isinstance(key, str) else json.dumps(key, sort_keys=True, default=str)
 
 
-class AutoTuner:
-    """Select a runtime candidate using an injectable benchmark strategy."""
+class TimingBook:
+    """Measured times per call signature and candidate label, persisted as one JSON file."""
 
-    _process_lock = threading.Lock()
+    def __init__(self, namespace, labels):
+        ident = json.dumps({"namespace": namespace, "labels": list(labels)}, sort_keys=True)
+        digest = hashlib.sha256(ident.encode()).hexdigest()[:20]
+        self.path = cache_dir() / "tuning" / f"{digest}.json"
+        self.rows = {}
+
+    def _load(self):
+        try:
+            data = json.loads(self.path.read_text())
+        except (OSError, ValueError):
+            return {}
+        return data.get("rows", {}) if isinstance(data, dict) else {}
+
+    def row(self, sig):
+        """What is known for ``sig`` (re-reading the file when this process knows nothing yet)."""
+        if sig not in self.rows:
+            stored = self._load().get(sig)
+            if stored:
+                self.rows[sig] = dict(stored)
+        return dict(self.rows.get(sig, {}))
+
+    def record(self, sig, entries):
+        with _BOOK_LOCK:
+            rows = self._load()
+            merged = dict(rows.get(sig, {}))
+            merged.update(entries)
+            rows[sig] = merged
+            self.rows[sig] = merged
+            self.path.parent.mkdir(parents=True, exist_ok=True)
+            tmp = self.path.with_name(f"{self.path.name}.{os.getpid()}.{threading.get_ident()}")
+            tmp.write_text(json.dumps({"rows": rows}, indent=1, sort_keys=True))
+            os.replace(tmp, self.path)
+
+
+def _time_of(entry):
+    return float(entry) if isinstance(entry, (int, float)) else math.inf
+
+
+class AutoTuner:
+    """Run the fastest of several interchangeable launchers, timed once per call signature."""
 
     def __init__(self, funcs, keys, *, benchmark=None, cache_namespace=None, validator=None):
-        self._funcs = tuple(funcs)
-        self._keys = tuple(keys)
-        if not self._funcs or len(self._funcs) != len(self._keys):
+        funcs, keys = tuple(funcs), tuple(keys)
+        if not funcs or len(funcs) != len(keys):
             raise ValueError("AutoTuner requires one key for every candidate.")
-        self._benchmark = benchmark or _default_benchmark
+        self.candidates = funcs
+        self.labels = tuple(_label(k) for k in keys)
+        self.keys = keys
+        self.book = TimingBook(cache_namespace or "default", self.labels)
+        self._measure = benchmark or default_benchmark
         self._validator = validator
+        self._winners = {}  # signature -> candidate index, kept once the winner has run
         self._lock = threading.Lock()
-        self._key_ids = tuple(_candidate_id(k) for k in self._keys)
-        self._func_to_key = dict(zip(self._funcs, self._key_ids))
-        namespace = cache_namespace or "default"
-        self._cache_dir = cache_dir() / "auto_tuning" / _digest(
-            {"schema": 1, "namespace": namespace, "candidate_ids": self._key_ids})
-        self._cache_dir.mkdir(parents=True, exist_ok=True)
-        self._cache_path = self._cache_dir / "selection.json"
-        self._selection_timings = dict((_read(self._cache_path) or {}).get("timings", {}))
-        self._candidate_timings = {k: {} for k in self._key_ids}
-        self._best_func = {}
 
     def __call__(self, *args, **kwargs):
         if self._validator is not None:
             self._validator(args, kwargs)
-        arg_key = self._make_arg_key(args, kwargs)
+        sig = signature(args, kwargs)
+        index = self._winners.get(sig)
+        if index is not None:
+            return self.candidates[index](*args, **kwargs)
         with self._lock:
-            best = self._best_func.get(arg_key)
-            if best is None:
-                timings = self._get_timings(args, kwargs)
-                if all(math.isinf(t) for t in timings):
-                    raise RuntimeError(self._all_candidates_failed_message(arg_key))
-                best = self._funcs[timings.index(min(timings))]
-                self._best_func[arg_key] = best
-        return best(*args, **kwargs)
+            index = self._elect(sig, args, kwargs)
+            result = self.candidates[index](*args, **kwargs)
+            self._winners[sig] = index
+        return result
 
-    def best(self, *args, **kwargs):
-        """The candidate key chosen for these arguments (benchmarking them if needed)."""
-        arg_key = self._make_arg_key(args, kwargs)
+    def choose(self, *args, **kwargs):
+        """Index of the candidate chosen for these arguments (timing them if needed), without running it."""
+        sig = signature(args, kwargs)
         with self._lock:
-            timings = self._get_timings(args, kwargs)
-        return self._keys[timings.index(min(timings))]
+            return self._elect(sig, args, kwargs)
 
-    def _get_timings(self, args, kwargs):
-        arg_key = self._make_arg_key(args, kwargs)
-        with self._process_lock:
-            self._selection_timings.update((_read(self._cache_path) or {}).get("timings", {}))
-            cached = self._selection_timings.get(arg_key)
-            if cached is not None and not all(math.isinf(t) for t in cached):
-                return list(cached)
-            timings = [self._get_timing(f, args, kwargs) for f in self._funcs]
-            self._selection_timings[arg_key] = timings
-            _write(self._cache_path, {"schema": 1, "timings": self._selection_timings})
-        return timings
+    def timings(self, *args, **kwargs):
+        """Candidate label -> recorded time or error for these arguments (empty before any election)."""
+        return self.book.row(signature(args, kwargs))
 
-    def _get_timing(self, func, args, kwargs):
-        key_id = self._func_to_key[func]
-        data = self._candidate_timings[key_id]
-        arg_key = self._make_arg_key(args, kwargs)
-        if arg_key in data and not math.isinf(data[arg_key]):
-            return data[arg_key]
-        path = self._get_func_cache_path(func)
-        manifest = _read(path) or {}
-        data.update(manifest.get("timings", {}))
-        if arg_key in data and not math.isinf(data[arg_key]):
-            return data[arg_key]
-        failures = dict(manifest.get("failures", {}))
-        try:
-            timing = float(self._benchmark(func, args, kwargs))
-            failures.pop(arg_key, None)
-        except Exception as exc:  # noqa: BLE001  (a failing candidate is recorded, not raised)
-            timing = float("inf")
-            failures[arg_key] = f"{type(exc).__name__}: {exc}"
-        data[arg_key] = timing
-        _write(path, {"schema": 1, "timings": data, "failures": failures})
-        return timing
-
-    def _get_func_cache_path(self, func):
-        return self._cache_dir / f"{_digest({'schema': 1, 'candidate_id': self._func_to_key[func]})}.json"
-
-    def _all_candidates_failed_message(self, arg_key):
-        reasons = []
-        for func, key_id in zip(self._funcs, self._key_ids):
-            manifest = _read(self._get_func_cache_path(func)) or {}
-            reasons.append(f"{key_id}: " + manifest.get("failures", {}).get(arg_key,
-                                                                              "benchmark returned an infinite timing"))
-        return "All auto-tuning candidates failed: " + "; ".join(reasons)
-
-    @staticmethod
-    def _make_arg_key(args, kwargs):
-        def one(a):
-            if hasattr(a, "shape") and hasattr(a, "dtype"):
-                stride = tuple(a.stride()) if hasattr(a, "stride") else None
-                return (f"tensor(shape={tuple(a.shape)}, stride={stride}, dtype={str(a.dtype).split('.')[-1]}, "
-                        f"device={getattr(a, 'device', None)})")
-            return str(a)
-
-        parts = [one(a) for a in args] + [f"{k}={one(v)}" for k, v in sorted(kwargs.items())]
-        return ", ".join(parts)
+    def _elect(self, sig, args, kwargs):
+        row = self.book.row(sig)
+        fresh = {}
+        for func, label in zip(self.candidates, self.labels):
+            if label in row:
+                continue
+            try:
+                fresh[label] = float(self._measure(func, args, kwargs))
+            except Exception as exc:  # noqa: BLE001  (a failing candidate is recorded, not raised)
+                fresh[label] = f"error: {type(exc).__name__}: {exc}"
+        if fresh:
+            self.book.record(sig, fresh)
+            row.update(fresh)
+        times = [_time_of(row.get(label)) for label in self.labels]
+        best = min(range(len(times)), key=times.__getitem__)
+        if math.isinf(times[best]):
+            reasons = "; ".join(f"{label}: {_reason(row.get(label))}" for label in self.labels)
+            raise RuntimeError(f"All auto-tuning candidates failed: {reasons}")
+        return best
 
 
-def _default_benchmark(function, args, kwargs, *, warmup=2, repeat=10):
-    """Median time in milliseconds of ``function(*args, **kwargs)`` on the current stream."""
+def _reason(entry):
+    if isinstance(entry, str) and entry.startswith("error: "):
+        return entry[len("error: "):]
+    return f"no finite timing ({entry})"
+
+
+def default_benchmark(func, args, kwargs, *, target_ms=20.0, max_calls=200):
+    """Milliseconds per call of ``func(*args, **kwargs)``.
+
+    On a GPU: one untimed call, one timed call to size the batch, then a batch of calls
+    lasting about ``target_ms`` timed with events on the current stream (the stream the
+    launchers use).  Without a GPU: wall clock over a batch of the same size."""
     import torch
 
     if not torch.cuda.is_available():
+        func(*args, **kwargs)
         start = time.perf_counter()
-        for _ in range(repeat):
-            function(*args, **kwargs)
-        return (time.perf_counter() - start) * 1e3 / repeat
-    for _ in range(warmup):
-        function(*args, **kwargs)
-    times = []
-    for _ in range(repeat):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        function(*args, **kwargs)
-        e1.record()
-        e1.synchronize()
-        times.append(e0.elapsed_time(e1))
-    times.sort()
-    return times[len(times) // 2]
+        func(*args, **kwargs)
+        once = max(time.perf_counter() - start, 1e-6) * 1e3
+        calls = max(1, min(max_calls, int(target_ms / once)))
+        start = time.perf_counter()
+        for _ in range(calls):
+            func(*args, **kwargs)
+        return (time.perf_counter() - start) * 1e3 / calls
+    stream = torch.cuda.current_stream()
+    func(*args, **kwargs)
+    begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    begin.record(stream)
+    func(*args, **kwargs)
+    end.record(stream)
+    end.synchronize()
+    once = max(begin.elapsed_time(end), 1e-3)
+    calls = max(3, min(max_calls, int(target_ms / once)))
+    begin.record(stream)
+    for _ in range(calls):
+        func(*args, **kwargs)
+    end.record(stream)
+    end.synchronize()
+    return begin.elapsed_time(end) / calls

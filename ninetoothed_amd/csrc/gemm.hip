@@ -36,6 +36,7 @@ struct GemmArgs {
   int64_t M, N, K;
   float alpha, beta;
   int out_dtype, round_dtype;
+  int c_dtype;  // c's element type: out's, or an fp8 format (widened exactly)
   int tiles_m, tiles_n;
   int c_pre;  // gemm_dma_kernel's fast epilogue: 16-bit out (and c) with unit column stride,
               // 16-byte aligned rows, out and c panel offsets within 32 bits
@@ -60,6 +61,45 @@ __device__ __forceinline__ void tile_of(int wg, int tiles_m, int tiles_n, int& t
   tn = in_band / rows_here;
 }
 
+// Operand storage of gemm_mfma_kernel's element-wise loader.  16-bit operands are used as
+// they are; fp8 operands are widened exactly to fp16 (every e5m2 and e4m3fn value is an
+// fp16 value) and multiplied on the fp16 matrix core, so the products are exact in fp32
+// as on an fp8 matrix core.
+struct src16 {
+  typedef uint16_t storage;
+  __device__ __forceinline__ static uint16_t widen(uint16_t v) { return v; }
+};
+struct src_e5m2 {  // OCP E5M2: sign, 5 exponent bits (bias 15), 2 mantissa bits = the top byte of an fp16
+  typedef uint8_t storage;
+  __device__ __forceinline__ static uint16_t widen(uint8_t v) { return (uint16_t)((uint16_t)v << 8); }
+};
+struct src_e4m3 {  // OCP E4M3FN: sign, 4 exponent bits (bias 7), 3 mantissa bits, no infinities, S.1111.111 = NaN
+  typedef uint8_t storage;
+  __device__ __forceinline__ static uint16_t widen(uint8_t v) {
+    const uint16_t s = (uint16_t)(v & 0x80) << 8;
+    const int e = (v >> 3) & 0xf, m = v & 7;
+    if (e == 0xf && m == 7) return s | 0x7e00;
+    if (e == 0) {  // m * 2^-9: normalised in fp16 with the leading one of m as the implicit bit
+      if (m == 0) return s;
+      const int lead = m >= 4 ? 2 : (m >= 2 ? 1 : 0);
+      return s | (uint16_t)((lead + 6) << 10) | (uint16_t)((m - (1 << lead)) << (10 - lead));
+    }
+    return s | (uint16_t)((e + 8) << 10) | (uint16_t)(m << 7);
+  }
+};
+
+// One element of c as fp32: f32/f16/bf16, or (C8: kernels of fp8 operands, whose c may be
+// fp8 too) an fp8 value widened exactly through fp16.  The 16- and 32-bit launchers reject
+// an fp8 c, so their kernels carry no fp8 code.
+template <bool C8>
+__device__ __forceinline__ float load_c(const GemmArgs& g, int64_t i) {
+  if constexpr (C8) {
+    if (g.c_dtype == NT_DTYPE_E5M2) return f16_bits_to_float(src_e5m2::widen(((const uint8_t*)g.c)[i]));
+    if (g.c_dtype == NT_DTYPE_E4M3) return f16_bits_to_float(src_e4m3::widen(((const uint8_t*)g.c)[i]));
+  }
+  return load_as_float(g.c, i, g.c_dtype);
+}
+
 // Epilogue shared by the GEMM kernels: out = cast(beta * c + alpha * round(acc)), one
 // 32-row slab per pass staged through LDS (32 x WJ*32 fp32 per wave), then each lane
 // handles 8 consecutive columns.
@@ -70,7 +110,7 @@ __device__ __forceinline__ void tile_of(int wg, int tiles_m, int tiles_n, int& t
 // instead of once per vector; 16-byte loads and stores.  A wave only reads back what it
 // staged itself, so the slabs need no workgroup barrier.  Otherwise element-wise with
 // bounds checks and any strides.
-template <int WI, int WJ>
+template <int WI, int WJ, bool C8 = false>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, const floatx16 (&acc)[WI][WJ], uint16_t* smem,
                                               int wave, int lane, int64_t row_base, int64_t col_base) {
   constexpr int COLS = WJ * 32;
@@ -78,7 +118,8 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, const floatx16 
   constexpr int VPL = 32 * VPR / 64;     // per lane per slab
   float* stage = (float*)smem + wave * (32 * COLS);
   const bool vec16 = g.out_dtype != NT_DTYPE_F32 && g.so_n == 1 && (g.so_m % 8) == 0 && ((uintptr_t)g.out % 16) == 0 &&
-                     (!g.c || (g.sc_n == 1 && (g.sc_m % 8) == 0 && ((uintptr_t)g.c % 16) == 0));
+                     (!g.c || (g.c_dtype == g.out_dtype && g.sc_n == 1 && (g.sc_m % 8) == 0 &&
+                               ((uintptr_t)g.c % 16) == 0));
   const bool full = vec16 && row_base + WI * 32 <= g.M && col_base + COLS <= g.N;
   __syncthreads();  // the LDS still holds operand tiles other waves may be reading
   if (full) {
@@ -132,39 +173,12 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, const floatx16 
       for (int u = 0; u < 8; ++u) {
         if (col + u >= g.N) break;
         float r = g.alpha * round_through(v[u], g.round_dtype);
-        if (g.c) r += g.beta * load_as_float(g.c, row * g.sc_m + (col + u) * g.sc_n, g.out_dtype);
+        if (g.c) r += g.beta * load_c<C8>(g, row * g.sc_m + (col + u) * g.sc_n);
         store_from_float(g.out, row * g.so_m + (col + u) * g.so_n, g.out_dtype, r);
       }
     }
   }
 }
-
-// Operand storage of gemm_mfma_kernel's element-wise loader.  16-bit operands are used as
-// they are; fp8 operands are widened exactly to fp16 (every e5m2 and e4m3fn value is an
-// fp16 value) and multiplied on the fp16 matrix core, so the products are exact in fp32
-// as on an fp8 matrix core.
-struct src16 {
-  typedef uint16_t storage;
-  __device__ __forceinline__ static uint16_t widen(uint16_t v) { return v; }
-};
-struct src_e5m2 {  // OCP E5M2: sign, 5 exponent bits (bias 15), 2 mantissa bits = the top byte of an fp16
-  typedef uint8_t storage;
-  __device__ __forceinline__ static uint16_t widen(uint8_t v) { return (uint16_t)((uint16_t)v << 8); }
-};
-struct src_e4m3 {  // OCP E4M3FN: sign, 4 exponent bits (bias 7), 3 mantissa bits, no infinities, S.1111.111 = NaN
-  typedef uint8_t storage;
-  __device__ __forceinline__ static uint16_t widen(uint8_t v) {
-    const uint16_t s = (uint16_t)(v & 0x80) << 8;
-    const int e = (v >> 3) & 0xf, m = v & 7;
-    if (e == 0xf && m == 7) return s | 0x7e00;
-    if (e == 0) {  // m * 2^-9: normalised in fp16 with the leading one of m as the implicit bit
-      if (m == 0) return s;
-      const int lead = m >= 4 ? 2 : (m >= 2 ? 1 : 0);
-      return s | (uint16_t)((lead + 6) << 10) | (uint16_t)((m - (1 << lead)) << (10 - lead));
-    }
-    return s | (uint16_t)((e + 8) << 10) | (uint16_t)(m << 7);
-  }
-};
 
 template <typename T, bool FAST, typename S = src16>
 __global__ __launch_bounds__(G_THREADS) void gemm_mfma_kernel(GemmArgs g) {
@@ -263,7 +277,7 @@ __global__ __launch_bounds__(G_THREADS) void gemm_mfma_kernel(GemmArgs g) {
     }
   }
 
-  gemm_epilogue<4, 4>(g, acc, smem, wave, lane, m0 + wm * 128, n0 + wn * 128);
+  gemm_epilogue<4, 4, !std::is_same<S, src16>::value>(g, acc, smem, wave, lane, m0 + wm * 128, n0 + wn * 128);
 }
 
 // Fast path (M, N multiples of 256, K of 64, a k-contiguous, b n-contiguous, 16-byte
@@ -435,7 +449,103 @@ __device__ __forceinline__ void load_lds16(u32x4 rs, uint32_t lds_addr, int voff
 }
 }  // namespace dma
 
-template <typename T>
+// The DMA kernels' fast epilogue (16-bit out, c absent or of out's type, unit column
+// stride, 16-byte aligned rows; the launcher's c_pre).  acc holds a wave's 128 x 64 block as
+// 4 x 2 tiles of 32 x 32 (the 32x32 MFMA accumulator layout); lds + EPI + 4 KiB * wave is
+// the wave's staging.
+__device__ __forceinline__ void dma_fast_epilogue(const GemmArgs& g, const floatx16 (&acc)[4][2], char* lds, int wave,
+                                                  int lane, int64_t row_base, int64_t col_base) {
+  // Fast epilogue: the accumulators go through this wave's 4 KiB of staging (never touched
+  // by the k loop: no barrier) 16 rows at a time; a lane finishes rows t * 8 + lane / 8
+  // (t = 0, 1) at columns (lane % 8) * 8 .. + 7.  c is read through a buffer resource (the
+  // host checks its offsets fit 32 bits); c of slab i + 2 is fetched while slab i is
+  // finished.  Without c the resource has no records: the loads return zeros.
+  const bool has_c = g.c != nullptr;
+  const __amdgpu_buffer_rsrc_t rsC = __builtin_amdgcn_make_buffer_rsrc(
+      has_c ? (void*)((const uint16_t*)g.c + row_base * g.sc_m + col_base) : (void*)g.a, (short)0,
+      has_c ? (int)((127 * g.sc_m + 64) * 2) : 0, 0x00020000);
+  const int vc = has_c ? (int)(((lane >> 3) * g.sc_m + (lane & 7) * 8) * 2) : 0;
+  const int c_row = has_c ? (int)(g.sc_m * 2) : 0;
+  // out through plain global stores: a buffer store whose data registers a VALU instruction
+  // rewrote a few instructions later has been seen to store the new values on this target.
+  char* o_lane = (char*)((uint16_t*)g.out + (row_base + (lane >> 3)) * g.so_m + col_base + (lane & 7) * 8);
+  const int64_t o_row = g.so_m * 2;
+  u32x4 cv[2][2][2];
+  auto load_c = [&](int i) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+        cv[i & 1][h][t] = __builtin_amdgcn_raw_buffer_load_b128(rsC, vc, (i * 32 + h * 16 + t * 8) * c_row, 0);
+  };
+  float* stage = (float*)(lds + dma::EPI + wave * 4096);
+  auto finish = [&](auto out_f16_c, auto round_c, int i, int h) {
+    constexpr bool OUT_F16 = decltype(out_f16_c)::value;
+    constexpr int ROUND = decltype(round_c)::value;
+    wave_lds_order();  // the previous half's reads come first
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 8 * h; r < 8 * h + 8; ++r)
+        stage[(acc_row(r, lane) - 16 * h) * 64 + j * 32 + (lane & 31)] = acc[i][j][r];
+    wave_lds_order();  // every lane's writes before any lane reads
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int rr = t * 8 + (lane >> 3), cg = (lane & 7) * 8;
+      const float4 v0 = *(const float4*)(stage + rr * 64 + cg);
+      const float4 v1 = *(const float4*)(stage + rr * 64 + cg + 4);
+      const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+      const u32x4 cw = cv[i & 1][h][t];
+      u32x4 ow;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        float r2[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          float x = v[2 * d + e];
+          if constexpr (ROUND == NT_DTYPE_F16) x = f16_bits_to_float(float_to_f16_bits(x));
+          if constexpr (ROUND == NT_DTYPE_BF16) x = bf16_bits_to_float(float_to_bf16_bits(x));
+          r2[e] = g.alpha * x;
+          if (has_c) {
+            const uint16_t cb = (uint16_t)(cw[d] >> (16 * e));
+            r2[e] += g.beta * (OUT_F16 ? f16_bits_to_float(cb) : bf16_bits_to_float(cb));
+          }
+        }
+        ow[d] = OUT_F16 ? ((uint32_t)float_to_f16_bits(r2[0]) | ((uint32_t)float_to_f16_bits(r2[1]) << 16))
+                        : ((uint32_t)float_to_bf16_bits(r2[0]) | ((uint32_t)float_to_bf16_bits(r2[1]) << 16));
+      }
+      __builtin_nontemporal_store(ow, (u32x4*)(o_lane + (i * 32 + h * 16 + t * 8) * o_row));  // not re-read: no L2 allocation
+    }
+  };
+  using OutF16 = std::integral_constant<bool, true>;
+  using OutBF16 = std::integral_constant<bool, false>;
+  using RNone = std::integral_constant<int, NT_DTYPE_NONE>;
+  using RF16 = std::integral_constant<int, NT_DTYPE_F16>;
+  using RBF16 = std::integral_constant<int, NT_DTYPE_BF16>;
+  auto all = [&](auto out_f16_c, auto round_c) {
+    load_c(0);
+    load_c(1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) finish(out_f16_c, round_c, i, h);
+      if (i + 2 < 4) load_c(i + 2);
+    }
+  };
+  const bool out_f16 = g.out_dtype == NT_DTYPE_F16;
+  if (g.round_dtype == NT_DTYPE_F16) {
+    if (out_f16) all(OutF16{}, RF16{}); else all(OutBF16{}, RF16{});
+  } else if (g.round_dtype == NT_DTYPE_BF16) {
+    if (out_f16) all(OutF16{}, RBF16{}); else all(OutBF16{}, RBF16{});
+  } else {
+    if (out_f16) all(OutF16{}, RNone{}); else all(OutBF16{}, RNone{});
+  }
+}
+
+// FAST_EPI: the launcher's c_pre condition holds (16-bit out and c of one type, unit column
+// stride, aligned rows); the other instance finishes through the element-wise epilogue.  Two
+// instances so that the fast one holds no code of the other (whose registers would spill).
+template <typename T, bool FAST_EPI>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_dma_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) char lds[dma::EPI + 8 * 4096];
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
@@ -561,95 +671,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   step(F1{}, F1{}, VN{}, kt + 2);
 
   const int64_t row_base = m0 + wm * 128, col_base = n0 + wn * 64;
-  if (!g.c_pre) {
+  if constexpr (!FAST_EPI) {
     gemm_epilogue<4, 2>(g, acc, (uint16_t*)lds, wave, lane, row_base, col_base);
     return;
   }
-  // Fast epilogue: the accumulators go through this wave's 4 KiB of staging (never touched
-  // by the k loop: no barrier) 16 rows at a time; a lane finishes rows t * 8 + lane / 8
-  // (t = 0, 1) at columns (lane % 8) * 8 .. + 7.  c is read through a buffer resource (the
-  // host checks its offsets fit 32 bits); c of slab i + 2 is fetched while slab i is
-  // finished.  Without c the resource has no records: the loads return zeros.
-  const bool has_c = g.c != nullptr;
-  const __amdgpu_buffer_rsrc_t rsC = __builtin_amdgcn_make_buffer_rsrc(
-      has_c ? (void*)((const uint16_t*)g.c + row_base * g.sc_m + col_base) : (void*)g.a, (short)0,
-      has_c ? (int)((127 * g.sc_m + 64) * 2) : 0, 0x00020000);
-  const int vc = has_c ? (int)(((lane >> 3) * g.sc_m + (lane & 7) * 8) * 2) : 0;
-  const int c_row = has_c ? (int)(g.sc_m * 2) : 0;
-  // out through plain global stores: a buffer store whose data registers a VALU instruction
-  // rewrote a few instructions later has been seen to store the new values on this target.
-  char* o_lane = (char*)((uint16_t*)g.out + (row_base + (lane >> 3)) * g.so_m + col_base + (lane & 7) * 8);
-  const int64_t o_row = g.so_m * 2;
-  u32x4 cv[2][2][2];
-  auto load_c = [&](int i) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-        cv[i & 1][h][t] = __builtin_amdgcn_raw_buffer_load_b128(rsC, vc, (i * 32 + h * 16 + t * 8) * c_row, 0);
-  };
-  float* stage = (float*)(lds + dma::EPI + wave * 4096);
-  auto finish = [&](auto out_f16_c, auto round_c, int i, int h) {
-    constexpr bool OUT_F16 = decltype(out_f16_c)::value;
-    constexpr int ROUND = decltype(round_c)::value;
-    wave_lds_order();  // the previous half's reads come first
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 8 * h; r < 8 * h + 8; ++r)
-        stage[(acc_row(r, lane) - 16 * h) * 64 + j * 32 + (lane & 31)] = acc[i][j][r];
-    wave_lds_order();  // every lane's writes before any lane reads
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int rr = t * 8 + (lane >> 3), cg = (lane & 7) * 8;
-      const float4 v0 = *(const float4*)(stage + rr * 64 + cg);
-      const float4 v1 = *(const float4*)(stage + rr * 64 + cg + 4);
-      const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-      const u32x4 cw = cv[i & 1][h][t];
-      u32x4 ow;
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        float r2[2];
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          float x = v[2 * d + e];
-          if constexpr (ROUND == NT_DTYPE_F16) x = f16_bits_to_float(float_to_f16_bits(x));
-          if constexpr (ROUND == NT_DTYPE_BF16) x = bf16_bits_to_float(float_to_bf16_bits(x));
-          r2[e] = g.alpha * x;
-          if (has_c) {
-            const uint16_t cb = (uint16_t)(cw[d] >> (16 * e));
-            r2[e] += g.beta * (OUT_F16 ? f16_bits_to_float(cb) : bf16_bits_to_float(cb));
-          }
-        }
-        ow[d] = OUT_F16 ? ((uint32_t)float_to_f16_bits(r2[0]) | ((uint32_t)float_to_f16_bits(r2[1]) << 16))
-                        : ((uint32_t)float_to_bf16_bits(r2[0]) | ((uint32_t)float_to_bf16_bits(r2[1]) << 16));
-      }
-      __builtin_nontemporal_store(ow, (u32x4*)(o_lane + (i * 32 + h * 16 + t * 8) * o_row));  // not re-read: no L2 allocation
-    }
-  };
-  using OutF16 = std::integral_constant<bool, true>;
-  using OutBF16 = std::integral_constant<bool, false>;
-  using RNone = std::integral_constant<int, NT_DTYPE_NONE>;
-  using RF16 = std::integral_constant<int, NT_DTYPE_F16>;
-  using RBF16 = std::integral_constant<int, NT_DTYPE_BF16>;
-  auto all = [&](auto out_f16_c, auto round_c) {
-    load_c(0);
-    load_c(1);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h) finish(out_f16_c, round_c, i, h);
-      if (i + 2 < 4) load_c(i + 2);
-    }
-  };
-  const bool out_f16 = g.out_dtype == NT_DTYPE_F16;
-  if (g.round_dtype == NT_DTYPE_F16) {
-    if (out_f16) all(OutF16{}, RF16{}); else all(OutBF16{}, RF16{});
-  } else if (g.round_dtype == NT_DTYPE_BF16) {
-    if (out_f16) all(OutF16{}, RBF16{}); else all(OutBF16{}, RBF16{});
-  } else {
-    if (out_f16) all(OutF16{}, RNone{}); else all(OutBF16{}, RNone{});
-  }
+  dma_fast_epilogue(g, acc, lds, wave, lane, row_base, col_base);
 }
 
 // ----------------------------------------------------------------------------- fp32
@@ -724,7 +750,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g) {
     const int64_t col = n0 + wn * 16 + (lane & 15);
     if (row < g.M && col < g.N) {
       float v = g.alpha * round_through(acc[r], g.round_dtype);
-      if (g.c) v += g.beta * load_as_float(g.c, row * g.sc_m + col * g.sc_n, g.out_dtype);
+      if (g.c) v += g.beta * load_c<false>(g, row * g.sc_m + col * g.sc_n);
       store_from_float(g.out, row * g.so_m + col * g.so_n, g.out_dtype, v);
     }
   }
@@ -800,7 +826,7 @@ __global__ __launch_bounds__(1024) void gemm_f32_splitk_kernel(GemmArgs g) {
   const int64_t row = m0 + e / F32_TN, col = n0 + e % F32_TN;
   if (row < g.M && col < g.N) {
     float v = g.alpha * round_through(sum, g.round_dtype);
-    if (g.c) v += g.beta * load_as_float(g.c, row * g.sc_m + col * g.sc_n, g.out_dtype);
+    if (g.c) v += g.beta * load_c<false>(g, row * g.sc_m + col * g.sc_n);
     store_from_float(g.out, row * g.so_m + col * g.so_n, g.out_dtype, v);
   }
 }
@@ -808,6 +834,7 @@ __global__ __launch_bounds__(1024) void gemm_f32_splitk_kernel(GemmArgs g) {
 static int gemm_check(const GemmArgs& g) {
   if (g.M < 0 || g.N < 0 || g.K < 0) return NT_ERR_INVALID;
   if (!valid_dtype(g.out_dtype) || !valid_round(g.round_dtype)) return NT_ERR_INVALID;
+  if (!valid_dtype(g.c_dtype) && g.c_dtype != NT_DTYPE_E5M2 && g.c_dtype != NT_DTYPE_E4M3) return NT_ERR_INVALID;
   return 0;
 }
 
@@ -817,7 +844,7 @@ __global__ void gemm_k0_kernel(GemmArgs g) {
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
     const int64_t row = e / g.N, col = e % g.N;
     float v = 0.f;
-    if (g.c) v += g.beta * load_as_float(g.c, row * g.sc_m + col * g.sc_n, g.out_dtype);
+    if (g.c) v += g.beta * load_c<true>(g, row * g.sc_m + col * g.sc_n);
     store_from_float(g.out, row * g.so_m + col * g.so_n, g.out_dtype, v);
   }
 }
@@ -829,6 +856,7 @@ template <typename T>
 static int gemm16_launch(GemmArgs g, hipStream_t stream, int config = 0) {
   if (config < 0 || config > 3) return NT_ERR_INVALID;
   if (int e = gemm_check(g)) return e;
+  if (!valid_dtype(g.c_dtype)) return NT_ERR_INVALID;  // an fp8 c goes with fp8 operands
   if (g.M == 0 || g.N == 0) return 0;
   if (!g.a || !g.b || !g.out) return NT_ERR_INVALID;
   if (g.K == 0) {
@@ -851,14 +879,16 @@ static int gemm16_launch(GemmArgs g, hipStream_t stream, int config = 0) {
   // Its fast epilogue: 16-byte out vectors, and c (if any) fetched with 32-bit buffer offsets.
   const bool out_vec = g.out_dtype != NT_DTYPE_F32 && g.so_n == 1 && g.so_m >= 0 && g.so_m % 8 == 0 &&
                        (uintptr_t)g.out % 16 == 0;
-  const bool c_vec = !g.c || (g.sc_n == 1 && g.sc_m >= 0 && g.sc_m % 8 == 0 && (uintptr_t)g.c % 16 == 0 &&
+  const bool c_vec = !g.c || (g.c_dtype == g.out_dtype && g.sc_n == 1 && g.sc_m >= 0 && g.sc_m % 8 == 0 && (uintptr_t)g.c % 16 == 0 &&
                               127 * g.sc_m + 128 <= 0x3fffffffLL);
   if ((config == 1 && !(fast && dma_ok)) || (config == 2 && !fast)) return NT_ERR_INVALID;
   const bool use_dma = config == 0 ? fast && dma_ok : config == 1;
   const bool use_fast8 = config == 0 ? fast && !dma_ok : config == 2;
   g.c_pre = use_dma && out_vec && c_vec;
-  if (use_dma)
-    hipLaunchKernelGGL((gemm_dma_kernel<T>), grid, dim3(512), 0, stream, g);
+  if (use_dma && g.c_pre)
+    hipLaunchKernelGGL((gemm_dma_kernel<T, true>), grid, dim3(512), 0, stream, g);
+  else if (use_dma)
+    hipLaunchKernelGGL((gemm_dma_kernel<T, false>), grid, dim3(512), 0, stream, g);
   else if (use_fast8)
     hipLaunchKernelGGL((gemm_fast8_kernel<T>), grid, dim3(512), 0, stream, g);
   else
@@ -877,10 +907,11 @@ static int gemm16_launch(GemmArgs g, hipStream_t stream, int config = 0) {
 // 2 (lane / 32) and 2 (lane / 32) + 1.  Per k-tile a wave issues eight MFMAs (its 4 x 2
 // blocks of 32 x 32); the next tile's b fragments go to a second set, its a fragments
 // replace each a fragment right after the tile's last MFMA that reads it.
-template <int FMT>
+// FAST_EPI as in gemm_dma_kernel (the 32 KiB past the operand stages are its staging).
+template <int FMT, bool FAST_EPI>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_f8_dma_kernel(GemmArgs g) {
   typedef int v8i __attribute__((ext_vector_type(8)));
-  __shared__ __attribute__((aligned(1024))) char lds[dma::EPI];
+  __shared__ __attribute__((aligned(1024))) char lds[dma::EPI + (FAST_EPI ? 8 * 4096 : 0)];
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -988,7 +1019,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   step(T1{}, F1{}, V0{}, kt + 1);
   step(F1{}, F1{}, VN{}, kt + 2);
 
-  gemm_epilogue<4, 2>(g, acc, (uint16_t*)lds, wave, lane, m0 + wm * 128, n0 + wn * 64);
+  if constexpr (FAST_EPI)
+    dma_fast_epilogue(g, acc, lds, wave, lane, m0 + wm * 128, n0 + wn * 64);
+  else
+    gemm_epilogue<4, 2, true>(g, acc, (uint16_t*)lds, wave, lane, m0 + wm * 128, n0 + wn * 64);
 }
 
 template <typename S>
@@ -1013,7 +1047,17 @@ static int gemm8_launch(GemmArgs g, hipStream_t stream) {
                      (GB_M - 1) * g.sa_m + g.K <= 0x3fffffffLL && (GB_N - 1) * g.sb_n + g.K <= 0x3fffffffLL;
   if (f8dma) {
     constexpr int fmt = std::is_same<S, src_e4m3>::value ? 0 : 1;
-    hipLaunchKernelGGL((gemm_f8_dma_kernel<fmt>), dim3((unsigned)(tiles_m * tiles_n)), dim3(512), 0, stream, g);
+    // The fast epilogue: 16-bit out with unit column stride and aligned rows; c absent or of
+    // out's type, fetched with 32-bit buffer offsets.
+    const bool fast_epi = g.out_dtype != NT_DTYPE_F32 && g.so_n == 1 && g.so_m >= 0 && g.so_m % 8 == 0 &&
+                          (uintptr_t)g.out % 16 == 0 &&
+                          (!g.c || (g.c_dtype == g.out_dtype && g.sc_n == 1 && g.sc_m >= 0 && g.sc_m % 8 == 0 &&
+                                    (uintptr_t)g.c % 16 == 0 && 127 * g.sc_m + 128 <= 0x3fffffffLL));
+    const dim3 grid((unsigned)(tiles_m * tiles_n));
+    if (fast_epi)
+      hipLaunchKernelGGL((gemm_f8_dma_kernel<fmt, true>), grid, dim3(512), 0, stream, g);
+    else
+      hipLaunchKernelGGL((gemm_f8_dma_kernel<fmt, false>), grid, dim3(512), 0, stream, g);
     return launch_status();
   }
   hipLaunchKernelGGL((gemm_mfma_kernel<f16_t, false, S>), dim3((unsigned)(tiles_m * tiles_n)), dim3(G_THREADS), 0,
@@ -1023,6 +1067,7 @@ static int gemm8_launch(GemmArgs g, hipStream_t stream) {
 
 static int gemm32_launch(GemmArgs g, hipStream_t stream) {
   if (int e = gemm_check(g)) return e;
+  if (!valid_dtype(g.c_dtype)) return NT_ERR_INVALID;  // an fp8 c goes with fp8 operands
   if (g.M == 0 || g.N == 0) return 0;
   if (!g.a || !g.b || !g.out) return NT_ERR_INVALID;
   if (g.K == 0) {
@@ -1060,7 +1105,11 @@ static GemmArgs make_args(const void* a, int64_t sa_m, int64_t sa_k, const void*
   g.sc_m = sc_m; g.sc_n = sc_n; g.so_m = so_m; g.so_n = so_n;
   g.M = M; g.N = N; g.K = K;
   g.alpha = alpha; g.beta = beta;
-  g.out_dtype = out_dtype; g.round_dtype = round_dtype;
+  // out_dtype: bits 0-7 out's type; bits 8-15 c's type + 1 (0: c has out's type).
+  const int c_field = (out_dtype >> 8) & 0xff;
+  g.out_dtype = (out_dtype < 0 || (out_dtype >> 16)) ? -2 : (out_dtype & 0xff);  // -2: rejected by gemm_check
+  g.c_dtype = c_field ? c_field - 1 : g.out_dtype;
+  g.round_dtype = round_dtype;
   return g;
 }
 

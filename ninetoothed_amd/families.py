@@ -1019,7 +1019,7 @@ class TunedPlan(Plan):
     def bind(self, values, index):
         import json
 
-        from ninetoothed_amd.auto_tuner import AutoTuner
+        from ninetoothed_amd.auto_tuner import AutoTuner, signature
 
         bound, keys = [], []
         for plan in self.plans:
@@ -1037,9 +1037,9 @@ class TunedPlan(Plan):
         args = tuple(values[n] for n in names)
         funcs = [lambda *a, _launch=launch: _launch(a) for launch in bound]
         tuner = AutoTuner(funcs, keys, cache_namespace=self.namespace)
-        best = tuner.best(*args)
-        self.chosen[tuner._make_arg_key(args, {})] = best
-        return bound[keys.index(best)]
+        best = tuner.choose(*args)
+        self.chosen[signature(args, {})] = keys[best]
+        return bound[best]
 
     def describe(self):
         return {"family": "tuned", "candidates": [p.describe() for p in self.plans],

@@ -25,10 +25,12 @@ and tile levels together) with one lane per element:
   * the source is compiled for gfx950 once per distinct text with hipRTC and launched
     through ``nt_rtc_*`` of libnt_mi355x.so.
 
-Anything else (reductions, broadcasting subscripts, loops, ``dot``, index arithmetic with
-``offsets``) raises ``LoweringError``.  An arrangement that maps several elements to one
-output element writes it from several lanes (the last write is unspecified), as the
-reference's generated programs would.
+Programs with reductions (``ntl.sum/max/min``), broadcasting subscripts, ``offsets``
+index vectors, source pointers and gathers, or loops over tile levels run as tile programs
+(``TilePlan``, below): one workgroup per program instance, reductions through LDS and
+wave64 shuffles.  What neither form takes raises ``LoweringError``.  An arrangement that
+maps several elements to one output element writes it from several lanes (the last write
+is unspecified), as the reference's generated programs would.
 """
 
 import copy

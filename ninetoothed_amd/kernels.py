@@ -167,11 +167,17 @@ def bind_gemm(a, b, out, c=None, round_dtype=None, config=0):
     n = b.shape[1]
     if a.dtype != b.dtype:
         raise TypeError("gemm operands must share one dtype")
+    out_code = _lib.dtype_code(out.dtype)
     if c is not None:
         if tuple(c.shape) != (m, n):
             raise ValueError("gemm bias shape mismatch")
         if c.dtype != out.dtype:
-            raise TypeError("gemm bias and output must share one dtype")
+            # c of another type (e.g. the reference's fp8 addmm input with an fp16 output) is
+            # read in its own type: its code + 1 in bits 8-15 of the output-type argument.
+            c_code = _lib.bias_dtype_code(c.dtype)
+            if c_code in (_lib.DTYPE_E5M2, _lib.DTYPE_E4M3) and _lib.dtype_suffix(a.dtype) not in ("e5m2", "e4m3"):
+                raise TypeError("an fp8 gemm bias needs fp8 operands")
+            out_code |= (c_code + 1) << 8
     rd = _lib.DTYPE_NONE if round_dtype is None else _lib.dtype_code(round_dtype)
     if config:
         if config not in GEMM_CONFIGS or _lib.dtype_suffix(a.dtype) not in ("f16", "bf16"):
@@ -183,7 +189,6 @@ def bind_gemm(a, b, out, c=None, round_dtype=None, config=0):
         extra = ()
     (sa_m, sa_k), (sb_k, sb_n), (so_m, so_n) = a.stride(), b.stride(), out.stride()
     sc_m, sc_n = c.stride() if c is not None else (0, 0)
-    out_code = _lib.dtype_code(out.dtype)
     stream = _stream_of(device)
 
     def launch(a, b, out, c, alpha, beta):

@@ -15,7 +15,7 @@ strides, constexpr and meta values), as the reference does for non-Triton backen
 (runtime.py:158-243); each key is matched once to a kernel family and cached.
 
 A call with every public argument given positionally goes through a second cache
-keyed on (dtype, shape, strides, device) of each tensor, the value of each
+keyed on (dtype, shape, strides, device, data-pointer alignment) of each tensor, the value of each
 constexpr, the type of each other scalar and the meta keywords.  A key enters it
 only after a call with that key passed every check above, so a hit goes straight
 to the bound launcher (which reads data pointers, scalars and the current stream).
@@ -95,8 +95,11 @@ class Handle:
         return public[outputs[0]] if outputs else None
 
     def _fast_key(self, args, kwargs):
+        # A tensor's data-pointer alignment is part of the key: a launcher bound (or tuned)
+        # for 16-byte aligned operands may have chosen a kernel that needs them.
         key = tuple([
-            (v.dtype, v.shape, v.stride(), v.device) if kind == 0 else (v if kind == 1 else type(v))
+            (v.dtype, v.shape, v.stride(), v.device, v.data_ptr() & 15) if kind == 0
+            else (v if kind == 1 else type(v))
             for v, kind in zip(args, self._kinds)
         ])
         if kwargs:

@@ -17,7 +17,7 @@ import ninetoothed_amd as ninetoothed
 import ninetoothed_amd.language as ntl
 import programs as pg
 from ninetoothed_amd import Symbol, Tensor, families
-from ninetoothed_amd.auto_tuner import AutoTuner
+from ninetoothed_amd.auto_tuner import AutoTuner, signature
 
 
 @pytest.fixture(autouse=True)
@@ -48,19 +48,23 @@ def test_auto_tuner(args, kwargs):
 
     namespace = f"test_{uuid.uuid4().hex}"
     tuner = AutoTuner((_foo, _bar), ("_foo", "_bar"), benchmark=benchmark, cache_namespace=namespace)
-    assert not tuner._cache_path.exists()
+    assert not tuner.book.path.exists()
     assert tuner(*args, **kwargs) == "bar"
     assert calls == [_foo, _bar]
     assert tuner(*args, **kwargs) == "bar" and calls == [_foo, _bar]  # no new benchmarks
-    assert tuner._cache_path.exists() and tuner._get_func_cache_path(_foo).exists()
+    assert tuner.book.path.exists()
+    assert tuner.timings(*args, **kwargs) == {"_foo": 2.0, "_bar": 1.0}
 
     again = []
     cached = AutoTuner((_foo, _bar), ("_foo", "_bar"), benchmark=lambda *c: again.append(c) or 0.0,
                        cache_namespace=namespace)
-    assert cached(*args, **kwargs) == "bar" and not again
-    # another argument key is benchmarked anew
+    assert cached(*args, **kwargs) == "bar" and not again  # a new tuner reads the book
+    # another argument signature is benchmarked anew, and only that one
     cached(*args, 99, **kwargs)
     assert len(again) == 2
+    # other candidate keys or another namespace are another book
+    assert AutoTuner((_foo, _bar), ("x", "y"), cache_namespace=namespace).book.path != tuner.book.path
+    assert AutoTuner((_foo, _bar), ("_foo", "_bar"), cache_namespace="other").book.path != tuner.book.path
 
 
 def test_failing_candidates_are_skipped_and_reported():
@@ -74,9 +78,22 @@ def test_failing_candidates_are_skipped_and_reported():
 
     tuner = AutoTuner((broken, _foo), ("broken", "_foo"), benchmark=benchmark, cache_namespace=uuid.uuid4().hex)
     assert tuner(1) == "foo"
-    all_broken = AutoTuner((broken,), ("broken",), benchmark=benchmark, cache_namespace=uuid.uuid4().hex)
-    with pytest.raises(RuntimeError, match="All auto-tuning candidates failed: broken: RuntimeError: boom"):
+    assert tuner.timings(1)["broken"].startswith("error: RuntimeError: boom")
+    all_broken = AutoTuner((broken, broken), ("first", "second"), benchmark=benchmark,
+                           cache_namespace=uuid.uuid4().hex)
+    with pytest.raises(RuntimeError, match="All auto-tuning candidates failed: first: RuntimeError: boom; "
+                                           "second: RuntimeError: boom"):
         all_broken(1)
+
+
+def test_winner_that_raises_is_not_kept():
+    def fails(*a, **k):
+        raise RuntimeError("Winner invocation failed.")
+
+    tuner = AutoTuner((fails,), ("winner",), benchmark=lambda *c: 1.0, cache_namespace=uuid.uuid4().hex)
+    with pytest.raises(RuntimeError, match="Winner invocation failed"):
+        tuner(1)
+    assert tuner._winners == {}
 
 
 def test_validator_and_key_checks():
@@ -87,8 +104,18 @@ def test_validator_and_key_checks():
                       cache_namespace=uuid.uuid4().hex)
     tuner(3)
     assert seen == [(3,)]
-    key = AutoTuner._make_arg_key((torch.empty(2, 3),), {"x": 1})
-    assert "shape=(2, 3)" in key and "stride=(3, 1)" in key and "x=1" in key
+    sig = signature((torch.empty(2, 3),), {"x": 1})
+    assert "[2,3]" in sig and "[3,1]" in sig and '"x"' in sig
+
+
+def test_signature_tells_alignment_apart():
+    # A launcher tuned on aligned operands may have chosen a kernel that needs them: a
+    # misaligned view of the same shape and strides is a different signature.
+    base = torch.empty(1025, dtype=torch.float16)
+    aligned, shifted = base[:1024], base[1:]
+    assert aligned.shape == shifted.shape and aligned.stride() == shifted.stride()
+    assert signature((aligned,), {}) != signature((shifted,), {})
+    assert signature((aligned,), {}) == signature((base[:1024].clone(),), {})
 
 
 def _add_handle(**options):
@@ -154,6 +181,29 @@ def test_tuned_matmul_picks_a_kernel_config():
     assert torch.allclose(out.float(), (a.float() @ b.float()).half().float(), atol=2e-2, rtol=1e-2)
     (plan,) = h.plans()
     assert plan["family"] == "tuned" and len(plan["chosen"]) == 1 and '"config"' in plan["chosen"][0]
+
+
+def test_handle_key_tells_alignment_apart():
+    h = ninetoothed.make(pg.matmul_arrangement, pg.matmul_application, pg.matmul_tensors())
+    base = torch.empty(512 * 512 + 8, dtype=torch.float16)
+    aligned, shifted = base[:512 * 512].view(512, 512), base[1:512 * 512 + 1].view(512, 512)
+    assert aligned.stride() == shifted.stride()
+    assert h._fast_key((aligned,) * 3, {}) != h._fast_key((shifted,) * 3, {})
+
+
+@pytest.mark.gpu
+def test_tuned_matmul_then_misaligned_view():
+    # The aligned call may bind a kernel that needs 16-byte aligned operands; a later call
+    # with the same shapes and strides but a misaligned view must not reuse that launcher.
+    h = ninetoothed.make(pg.matmul_arrangement, pg.matmul_application, pg.matmul_tensors(), max_num_configs=4)
+    g = torch.Generator().manual_seed(6)
+    base = torch.randn(2, 512 * 512 + 8, generator=g).half().cuda()
+    a, b = base[0, :512 * 512].view(512, 512), base[1, :512 * 512].view(512, 512)
+    a1, b1 = base[0, 1:512 * 512 + 1].view(512, 512), base[1, 1:512 * 512 + 1].view(512, 512)
+    for x, y in ((a, b), (a1, b1)):
+        out = torch.empty(512, 512, dtype=torch.float16, device="cuda")
+        h(x, y, out)
+        assert torch.allclose(out.float(), (x.float() @ y.float()).half().float(), atol=2e-2, rtol=1e-2)
 
 
 def test_conv_plans_expand_into_paths():

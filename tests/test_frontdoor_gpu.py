@@ -115,6 +115,28 @@ def test_addmm_reference_case(dtype):
         assert torch.allclose(output, torch.addmm(input, mat1, mat2, beta=beta, alpha=alpha), atol=0.075)
 
 
+@pytest.mark.parametrize("dtype", (torch.float8_e5m2, torch.float8_e4m3fn))
+def test_addmm_fp8_reference_case(dtype):
+    # reference tests/test_addmm.py:57-90 (float8_e5m2 case): fp8 input and mat1, column-major
+    # fp8 mat2 (`mat2.T.to(dtype)`), fp16 output, atol 0.125 against torch.addmm on the
+    # operands widened to fp16
+    m = n = k = 512
+    input = _randn((m, n), torch.float16, 15).to(dtype)
+    mat1 = _randn((m, k), torch.float16, 16).to(dtype)
+    mat2 = _randn((k, n), torch.float16, 17).T.to(dtype)
+    assert mat2.stride() == (1, k)
+    beta, alpha = 0.6180, 0.4142
+    output = torch.empty((m, n), dtype=torch.float16, device=DEV)
+    kernel = ninetoothed.make(pg.addmm_arrangement, pg.addmm_application, pg.addmm_tensors())
+    kernel(input, mat1, mat2, beta, alpha, output)
+    f16 = torch.float16
+    expected = torch.addmm(input.to(f16), mat1.to(f16), mat2.to(f16), beta=beta, alpha=alpha)
+    assert torch.allclose(output, expected, atol=0.125)
+    ref = apply.addmm(_np(input), _np(mat1), _np(mat2), beta, alpha, "float16", pg.addmm_arrangement,
+                      block=(64, 64, 64))
+    assert np.allclose(_np(output), ref, atol=1e-2, rtol=1e-2)
+
+
 def test_addmm_headline_shape():
     m = n = k = 4096
     s = 1.0 / math.sqrt(k)
@@ -173,9 +195,42 @@ def test_attention_headline_scaled(is_causal):
     o = torch.empty_like(q)
     kernel = ninetoothed.make(pg.attention_arrangement, pg.attention_application_scaled, pg.attention_tensors())
     kernel(q, k, v, is_causal, o)
-    expected = F.scaled_dot_product_attention(q[:1, :2].float(), k[:1, :2].float(), v[:1, :2].float(),
-                                              is_causal=is_causal, scale=1 / math.sqrt(128))
-    assert torch.allclose(o[:1, :2].float(), expected, atol=1e-2, rtol=1e-2)
+    _check_every_head(q, k, v, o, is_causal, 1 / math.sqrt(128))
+
+
+def _check_every_head(q, k, v, o, causal, scale, tol=1e-2):
+    """Compare every (batch, head) slice with an fp32 restatement of attention, one head at a time.
+
+    The output comes from torch.empty, so a head the kernel's work order skips or writes
+    twice fails here whichever XCD or head group it belongs to."""
+    sq, sk = q.shape[2], k.shape[2]
+    mask = None
+    if causal:
+        mask = torch.ones(sq, sk, dtype=torch.bool, device=q.device).tril().logical_not()  # key j <= query i
+    bad = []
+    for b in range(q.shape[0]):
+        for h in range(q.shape[1]):
+            s = torch.matmul(q[b, h].float(), k[b, h].float().t().contiguous()) * scale
+            if mask is not None:
+                s.masked_fill_(mask, float("-inf"))
+            ref = torch.matmul(torch.softmax(s, dim=-1), v[b, h].float())
+            if not torch.allclose(o[b, h].float(), ref, atol=tol, rtol=tol):
+                bad.append((b, h, float((o[b, h].float() - ref).abs().max())))
+    assert not bad, f"heads outside tolerance (b, h, max error): {bad[:8]}"
+
+
+# B*H = 64 and 24: with 64 (8 heads per XCD, two groups of four) both the grouped causal
+# order and the per-XCD non-causal order run with every head checked; with 24 (3 heads per
+# XCD) the causal launch takes the ungrouped per-XCD order; B*H = 6 takes the plain order.
+@pytest.mark.parametrize("is_causal", (False, True))
+@pytest.mark.parametrize("shape", ((2, 32, 1024, 128), (3, 8, 640, 64), (2, 3, 333, 128)))
+def test_attention_work_orders_every_head(is_causal, shape):
+    q, k, v = (_randn(shape, torch.float16, 70 + i) for i in range(3))
+    o = torch.empty_like(q)
+    kernel = ninetoothed.make(pg.attention_arrangement, pg.attention_application_scaled, pg.attention_tensors())
+    kernel(q, k, v, is_causal, o)
+    torch.cuda.synchronize()
+    _check_every_head(q, k, v, o, is_causal, 1 / math.sqrt(128))  # the application's constant scale
 
 
 # ----------------------------------------------------------------------- softmax
