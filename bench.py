@@ -8,7 +8,7 @@ configuration under "configs", each with its own roofline fraction and CPU basel
 Per configuration: max(W, 10) untimed warm-up steps; then exactly K steps bracketed by
 torch.cuda.synchronize(), timed with HIP events recorded on the stream the kernels are
 launched on (torch's current stream, which the launchers pass to the library) ->
-``ms_per_step`` and ``value``; then max(K, 50) further steps, each between its own pair
+``ms_per_step`` and ``value``; then max(K, S) further steps (S = --samples, default 50), each between its own pair
 of events -> ``median_ms`` and the 10th/90th percentiles (the spread).  The bandwidth-bound
 configurations (softmax, max_pool2d, add) rotate through buffer sets whose total exceeds
 the 256 MB Infinity Cache, so every step reads its inputs from HBM.
@@ -25,7 +25,7 @@ the configuration; torch_cpu: the torch fp32 CPU op the reference tests compare 
 median of 3 runs after one warm-up.  The reference's own kernels under the Triton CPU
 interpreter are not available on the GPU box (the reference does not travel there).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only name,...] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only name,...] [--no-cpu] [--samples S]
 """
 
 import argparse
@@ -51,6 +51,8 @@ def _args():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--only", default="")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--samples", type=int, default=50,
+                   help="launches timed one by one for the median (at least --steps)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="only run a plain 256 MiB device copy K times (scale for rocprofv3 FETCH/WRITE_SIZE)")
     return p.parse_args()
@@ -379,7 +381,7 @@ def main():
     configs = _configs(torch, ninetoothed, pg)
     only = set(filter(None, args.only.split(",")))
     traffic = _traffic()
-    warmup, samples = max(args.warmup, 10), max(args.steps, 50)
+    warmup, samples = max(args.warmup, 10), max(args.steps, args.samples)
     results = []
     for cfg in configs:
         if only and cfg["name"] not in only:

@@ -1,11 +1,12 @@
 """ninetoothed_amd: an MI355X-native (gfx950) backend for NineToothed's arrange-and-apply kernels.
 
 Drop-in surface of ``ninetoothed`` for the hot path (``import ninetoothed_amd as
-ninetoothed``): ``make``, ``jit``, ``Tensor``, ``Symbol``, ``block_size``, the dtype
+ninetoothed``): ``make``, ``jit``, ``build``, ``Tensor``, ``Symbol``, ``block_size``, the dtype
 aliases, ``eval`` and ``subs``; application bodies use ``ninetoothed_amd.language``
 as ``ntl``.  Kernels run from the prebuilt ``libnt_mi355x.so``.
 """
 
+from ninetoothed_amd.build import build
 from ninetoothed_amd.compiler import jit, make
 from ninetoothed_amd.dtype import (
     bfloat16,
@@ -34,6 +35,7 @@ __all__ = [
     "Tensor",
     "bfloat16",
     "block_size",
+    "build",
     "eval",
     "float16",
     "float32",

@@ -125,7 +125,10 @@ def _call_for(plan, values, scalar_expr, index):
         cl.ptr(plan.c if plan.c else None)
         cl.i(c.stride(0) if c is not None else 0), cl.i(c.stride(1) if c is not None else 0)
         cl.ptr(plan.out), cl.i(out.stride(0)), cl.i(out.stride(1))
-        cl.args.append(str(_lib.dtype_code(out.dtype)))
+        out_code = _lib.dtype_code(out.dtype)
+        if c is not None and c.dtype != out.dtype:  # c in its own type (e.g. fp8), as kernels.bind_gemm passes it
+            out_code |= (_lib.bias_dtype_code(c.dtype) + 1) << 8
+        cl.args.append(str(out_code))
         cl.i(m), cl.i(n), cl.i(k)
         cl.f(_coef(plan.alpha_factors, scalar_expr))
         cl.f(_coef(plan.beta_factors, scalar_expr) if plan.c else "0.0")
