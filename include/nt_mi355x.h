@@ -208,6 +208,28 @@ int nt_conv2d_config_bf16(const void* x, const int64_t* x_strides, const void* w
                           int64_t P, int64_t Q, int64_t ph, int64_t pw, int64_t sh, int64_t sw,
                           int64_t dh, int64_t dw, int round_dtype, void* workspace,
                           int64_t workspace_bytes, int config, hipStream_t stream);
+/* Allocation-free conv2d.  No counterpart in the reference: for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  The arguments of nt_conv2d_f16/bf16 without the workspace: the
+ * re-layout workspace is a file-scope device array of NT_CONV2D_SCRATCH_BYTES per GPU
+ * (held from the library's first such call on that GPU until the process ends).  A shape
+ * whose re-layout needs more (nt_conv2d_workspace_size() > NT_CONV2D_SCRATCH_BYTES)
+ * returns NT_ERR_SCRATCH before launching anything.  Nothing is allocated.  All calls on
+ * one GPU share its array: calls that overlap on one GPU (different streams, or host
+ * threads without ordering) race; calls ordered on one stream do not.  Each call writes
+ * every scratch byte it reads, so nothing carries over between calls. */
+#define NT_CONV2D_SCRATCH_BYTES (32LL << 20)
+#define NT_ERR_SCRATCH 2 /* = hipErrorOutOfMemory: the shape needs more than the static scratch */
+int nt_conv2d_noalloc_f16(const void* x, const int64_t* x_strides, const void* w, const int64_t* w_strides,
+                          void* y, const int64_t* y_strides, int y_dtype,
+                          int64_t N, int64_t C, int64_t H, int64_t W, int64_t K, int64_t R, int64_t S,
+                          int64_t P, int64_t Q, int64_t ph, int64_t pw, int64_t sh, int64_t sw,
+                          int64_t dh, int64_t dw, int round_dtype, hipStream_t stream);
+int nt_conv2d_noalloc_bf16(const void* x, const int64_t* x_strides, const void* w, const int64_t* w_strides,
+                           void* y, const int64_t* y_strides, int y_dtype,
+                           int64_t N, int64_t C, int64_t H, int64_t W, int64_t K, int64_t R, int64_t S,
+                           int64_t P, int64_t Q, int64_t ph, int64_t pw, int64_t sh, int64_t sw,
+                           int64_t dh, int64_t dw, int round_dtype, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Fused attention forward (online softmax in base 2), per (b, h):

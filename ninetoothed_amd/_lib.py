@@ -58,6 +58,10 @@ _SIGNATURES = {
     },
     "nt_conv2d_workspace_size": (_I64,) * 9 + (_I,),
     **{
+        f"nt_conv2d_noalloc_{t}": (_P, _I64P, _P, _I64P, _P, _I64P, _I) + (_I64,) * 15 + (_I, _P)
+        for t in ("f16", "bf16")
+    },
+    **{
         f"nt_conv2d_{t}": (_P, _I64P, _P, _I64P, _P, _I64P, _I) + (_I64,) * 15 + (_I, _P, _I64, _P)
         for t in ("f16", "bf16")
     },

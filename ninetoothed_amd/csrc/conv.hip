@@ -14,6 +14,8 @@
 // MFMA-bound in principle (2 * N*P*Q * K * C*R*S flops per launch).
 #include "mfma_core.h"
 
+#include <atomic>
+#include <mutex>
 #include <type_traits>
 
 namespace nt {
@@ -759,3 +761,51 @@ NT_CONV_ENTRY(nt_conv2d_bf16, nt::bf16_t)
   }
 NT_CONV_CONFIG_ENTRY(nt_conv2d_config_f16, nt::f16_t)
 NT_CONV_CONFIG_ENTRY(nt_conv2d_config_bf16, nt::bf16_t)
+
+// ----------------------------------------------------------------------------- allocation-free entry
+// The re-layout workspace of nt_conv2d_* as a file-scope device array (one per GPU the library
+// runs on).  In host code `scratch` names a host-side stand-in, not device memory: its device
+// address comes from hipGetSymbolAddress, looked up once per device on the first call with
+// that device current and kept in scratch_ptr.
+static __device__ __align__(256) char scratch[NT_CONV2D_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<void*> scratch_ptr[kMaxDevices];
+std::mutex scratch_mutex;
+
+// The current device's scratch address, or a nonzero status.
+int current_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return NT_ERR_INVALID;
+  void* p = scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(scratch_mutex);
+    p = scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return (int)e;
+      if (p == nullptr || (uintptr_t)p % 256 != 0) return NT_ERR_INVALID;
+      scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return 0;
+}
+}  // namespace
+
+#define NT_CONV_NOALLOC_ENTRY(NAME, T, CODE)                                                                         \
+  extern "C" int NAME(const void* x, const int64_t* xs, const void* w, const int64_t* ws, void* y, const int64_t* ys, \
+                      int y_dtype, int64_t N, int64_t C, int64_t H, int64_t W, int64_t K, int64_t R, int64_t S,       \
+                      int64_t P, int64_t Q, int64_t ph, int64_t pw, int64_t sh, int64_t sw, int64_t dh, int64_t dw,   \
+                      int round_dtype, hipStream_t stream) {                                                          \
+    if (nt_conv2d_workspace_size(N, C, H, W, K, R, S, ph, pw, CODE) > NT_CONV2D_SCRATCH_BYTES) return NT_ERR_SCRATCH; \
+    void* ws_ptr = nullptr;                                                                                          \
+    if (int e = current_scratch(&ws_ptr)) return e;                                                                  \
+    return nt::conv_launch<T>(x, xs, w, ws, y, ys, y_dtype, N, C, H, W, K, R, S, P, Q, ph, pw, sh, sw, dh, dw,       \
+                              round_dtype, ws_ptr, NT_CONV2D_SCRATCH_BYTES, stream);                                 \
+  }
+NT_CONV_NOALLOC_ENTRY(nt_conv2d_noalloc_f16, nt::f16_t, NT_DTYPE_F16)
+NT_CONV_NOALLOC_ENTRY(nt_conv2d_noalloc_bf16, nt::bf16_t, NT_DTYPE_BF16)
