@@ -254,6 +254,24 @@ int nt_attention_f32(const void* q, const int64_t* q_strides, const void* k, con
                      int o_dtype, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
                      float q_scale, int causal, hipStream_t stream);
 
+/* One kernel configuration of the 16-bit attention, for the auto-tuner: the arguments
+ * of nt_attention_f16/bf16 plus `config` (0 = the fastest kernel whose conditions hold,
+ * as nt_attention_f16/bf16 choose; 1 = the one-wave-per-SIMD pipelined kernel, head dim
+ * 128 with unit d-stride and 16-byte aligned rows; 2 = the eight-wave kernel, same
+ * conditions, head dim 64 or 128; 3 = the four-wave kernels, any strides).  A forced
+ * configuration whose conditions do not hold returns NT_ERR_INVALID before launching.
+ * Replaces the per-configuration launchers the reference's auto-tuner times over
+ * BLOCK_SIZE_M/N (reference tests/test_attention.py:10-11,
+ * src/ninetoothed/compiler/driver.py:975-1031). */
+int nt_attention_config_f16(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                            const void* v, const int64_t* v_strides, void* o, const int64_t* o_strides,
+                            int o_dtype, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
+                            float q_scale, int causal, hipStream_t stream, int config);
+int nt_attention_config_bf16(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                             const void* v, const int64_t* v_strides, void* o, const int64_t* o_strides,
+                             int o_dtype, int64_t B, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
+                             float q_scale, int causal, hipStream_t stream, int config);
+
 /* ---------------------------------------------------------------------------
  * Generic kernels for programs that match none of the families above.  They replace
  * the reference's run-time toolchain step for generated sources (nvcc + cuModule in

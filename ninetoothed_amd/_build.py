@@ -37,6 +37,13 @@ COMMON_FLAGS = (
 )
 
 
+# Per-source flags.  attention.hip: builtin MFMAs keep their accumulators in VGPRs (its
+# one-wave-per-SIMD kernel puts only the output accumulators in AGPRs, through inline
+# assembly); without this the compiler would move every MFMA to AGPRs in that kernel and
+# copy the scores back and forth.
+FILE_FLAGS = {"attention.hip": ("-mllvm", "-amdgpu-mfma-vgpr-form=1")}
+
+
 def hipcc() -> str:
     found = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(found).exists():
@@ -53,6 +60,7 @@ def _compile(source: Path, extra: tuple[str, ...]) -> Path:
     cmd = [
         hipcc(),
         *COMMON_FLAGS,
+        *FILE_FLAGS.get(source.name, ()),
         *extra,
         f"-I{INCLUDE_DIR}",
         f"-I{SOURCE_DIR}",

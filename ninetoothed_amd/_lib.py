@@ -73,6 +73,11 @@ _SIGNATURES = {
         f"nt_attention_{t}": (_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _I64, _I64, _I64, _I64, _I64, _F, _I, _P)
         for t in ("f32", "f16", "bf16")
     },
+    **{
+        f"nt_attention_config_{t}": (_P, _I64P, _P, _I64P, _P, _I64P, _P, _I64P, _I, _I64, _I64, _I64, _I64, _I64, _F, _I,
+                                     _P, _I)
+        for t in ("f16", "bf16")
+    },
     "nt_rtc_compile": (ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(_P), _I64P, ctypes.c_char_p, _I64),
     "nt_rtc_free": (_P,),
     "nt_rtc_load": (_P, ctypes.c_char_p, ctypes.POINTER(_P)),

@@ -690,6 +690,462 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
   }
 }
 
+// Pipelined kernel (head dim 128, 16-bit, the fast path's conditions; configuration 1, a
+// tuning candidate: on MI355X it runs 5-12 % slower than attention_fast_kernel at the
+// B=4, H=32, S=4096 shape, because one wave alone on a SIMD cannot issue the softmax's
+// VALU work fast enough beside its MFMAs).  Four waves per workgroup, one per SIMD, each
+// owning 64 queries (two blocks of 32), so every K and V^T fragment read from LDS feeds two
+// MFMAs and the LDS reads per MFMA halve against the eight-wave kernel.  A wave alone on
+// its SIMD has 512 registers (the O^T accumulators and Q live in AGPRs) and overlaps its
+// own softmax with its matrix work: iteration j issues
+//   phase A: S^T_{j+1} = K_{j+1} . Q^T (16 MFMAs)  beside  P_j = exp2(S_j), row sums
+//   phase B: O^T += V_j^T . P_j^T   (16 MFMAs)     beside  the max of S_{j+1} (mask, lazy
+//                                                          rescale check)
+// so the VALU work of one key tile runs under the MFMAs of the next.  Key tiles of 32,
+// in pairs, come from HBM straight into a four-stage LDS ring (one stage per pair, K and V
+// in separate halves of LDS) by DMA (buffer_load ... lds), two pairs ahead, one barrier per
+// pair:
+//   K tile  [key][128 d], 256-byte rows whose 16-byte chunks are XOR-swizzled by key % 16:
+//           the S^T operand (32 keys x 8 d per lane) is one ds_read_b128;
+//   V tile  [key][128 d] as in HBM, 64-byte chunks XOR-swizzled by key % 4: the O^T
+//           operand V^T (32 d x 8 keys per lane) is two ds_read_b64_tr_b16, each giving
+//           a lane 4 consecutive keys of its d (lane 4 r + q of a 16-lane group reads key
+//           k0 + r at d0 + 4 q .. + 3; lane j receives d0 + j at keys k0 .. k0 + 3).
+// The key order inside a 16-key slice is the one of P^T's register slots (slot s of lane
+// half h is key 8 (s / 4) + 4 h + s % 4), as in the other kernels.  Row sums of the rounded
+// p on the VALU with v_dot2 (two products by one per instruction, fp32 accumulation).
+// Math, lazy rescaling and rounding points are those of attention_fast_kernel.
+namespace ap {
+constexpr int NW = 4;               // waves per workgroup (one per SIMD)
+constexpr int WQ = 64;              // queries per wave: two blocks of 32
+constexpr int BM = NW * WQ;         // queries per workgroup
+constexpr int BN = 32;              // keys per tile (the unit of the math)
+constexpr int ROW = 256;            // bytes per key row (128 d)
+constexpr int KV = BN * ROW;        // one K or V tile: 8 KiB
+constexpr int STAGE = 2 * KV;       // a stage holds a pair of tiles (64 keys) of K, or of V
+constexpr int STAGES = 4;
+constexpr int VREG = STAGES * STAGE;       // V stages follow the K stages
+constexpr int LDS_BYTES = 2 * VREG;        // 128 KiB
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+// 16 bytes per lane from buffer `rs` at voffset + soffset into LDS at lds_addr + 16 * lane.
+__device__ __forceinline__ void load_lds16(u32x4 rs, uint32_t lds_addr, int voffset, int soffset) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voffset), "s"(rs),
+                 "s"(__builtin_amdgcn_readfirstlane(soffset))
+               : "memory", "m0");
+}
+// Buffer resource (uniform: every word read from the first lane, so it lives in SGPRs).
+__device__ __forceinline__ u32x4 rsrc(const void* base, uint32_t bytes) {
+  const uint64_t p = (uint64_t)base;
+  return u32x4{(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)p),
+               (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(p >> 32) & 0xffffu),
+               (uint32_t)__builtin_amdgcn_readfirstlane(bytes), 0x00020000u};
+}
+// Row sum of two rounded p values packed in w, accumulated in fp32.
+template <typename T>
+__device__ __forceinline__ float dot_ones(uint32_t w, float acc);
+// Volatile inline assembly so that the compiler keeps each at its place in the schedule
+// (as a plain builtin it would sink the row sums past the rescale branch, out of the
+// matrix work they are meant to overlap).
+template <>
+__device__ __forceinline__ float dot_ones<f16_t>(uint32_t w, float acc) {
+  asm volatile("v_dot2c_f32_f16 %0, %1, %2" : "+v"(acc) : "v"(w), "v"(0x3c003c00u));
+  return acc;
+}
+template <>
+__device__ __forceinline__ float dot_ones<bf16_t>(uint32_t w, float acc) {
+  asm volatile("v_dot2c_f32_bf16 %0, %1, %2" : "+v"(acc) : "v"(w), "v"(0x3f803f80u));
+  return acc;
+}
+// x of lane l ^ 32 (v_permlane32_swap on two copies of x: afterwards the first holds the
+// low half's values in both halves and the second the high half's).  Inline assembly: the
+// builtin with equal operands has been folded to a wrong result.  s_nop 1: the VALU write
+// of an operand needs wait states before v_permlane32_swap reads it.
+__device__ __forceinline__ void halves(float x, float& lo, float& hi) {
+  lo = x;
+  hi = x;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(lo), "+v"(hi));
+}
+__device__ __forceinline__ float max_halves(float x) {
+  float lo, hi;
+  halves(x, lo, hi);
+  return fmaxf(lo, hi);
+}
+__device__ __forceinline__ float sum_halves(float x) {
+  float lo, hi;
+  halves(x, lo, hi);
+  return lo + hi;
+}
+// O^T += V^T . P^T with the accumulator in AGPRs (the scores stay in VGPRs).  Written as
+// inline assembly, so the compiler neither sees it as an MFMA nor inserts its wait
+// states: the callers do (nop_after_valu before the first of a group whose operands the
+// VALU just wrote, nop_after_mfma before the VALU reads an accumulator).
+template <typename T>
+__device__ __forceinline__ void pv_mma(floatx16& acc, typename mfma_traits<T>::frag a, typename mfma_traits<T>::frag b);
+template <>
+__device__ __forceinline__ void pv_mma<f16_t>(floatx16& acc, half8 a, half8 b) {
+  asm("v_mfma_f32_32x32x16_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+template <>
+__device__ __forceinline__ void pv_mma<bf16_t>(floatx16& acc, bf16x8 a, bf16x8 b) {
+  asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+// Moves of an accumulator between AGPRs and VGPRs, as inline assembly so that every
+// definition of an O^T accumulator is an AGPR one (otherwise the register allocator may
+// give the loop-carried accumulators VGPRs and copy them around every iteration).
+__device__ __forceinline__ floatx16 to_agpr(floatx16 v) {
+  floatx16 r;
+  asm volatile("" : "=a"(r) : "0"(v));
+  return r;
+}
+template <typename F>
+__device__ __forceinline__ F frag_to_agpr(F v) {
+  F r;
+  asm volatile("" : "=a"(r) : "0"(v));
+  return r;
+}
+__device__ __forceinline__ floatx16 from_agpr(floatx16 a) {
+  floatx16 r;
+  asm volatile("" : "=v"(r) : "0"(a));
+  return r;
+}
+// Wait states: a VALU write read by an MFMA needs 2; an 8-pass MFMA's result read by the
+// VALU (or v_accvgpr_read) needs 11.  Both with margin.
+__device__ __forceinline__ void nop_after_valu() { asm volatile("s_nop 4"); }
+__device__ __forceinline__ void nop_after_mfma() { asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 4"); }
+// Scheduling group masks of __builtin_amdgcn_sched_group_barrier.
+constexpr int SG_VALU = 0x0002 | 0x0400, SG_MFMA = 0x0008, SG_DSR = 0x0100;
+}  // namespace ap
+
+template <typename T>
+__global__ __launch_bounds__(ap::NW * 64) __attribute__((amdgpu_waves_per_eu(1, 1))) void attention_pipe_kernel(
+    AttnArgs g) {
+  typedef typename mfma_traits<T>::frag frag;
+  __shared__ __attribute__((aligned(1024))) char lds[ap::LDS_BYTES];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
+  const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  int qb_id;
+  int64_t bh;
+  block_order(g, blockIdx.x, qb_id, bh);
+  const int b = (int)(bh / g.H), h = (int)(bh % g.H);
+  const int q0 = qb_id * ap::BM;
+  const int qw = q0 + wave * ap::WQ;  // first query of this wave
+  const int Sk = (int)g.Sk, Sq = (int)g.Sq;
+  const bool causal = g.causal != 0;
+
+  // Tiles: the workgroup's (up to its last wave's last visible key when causal) and this
+  // wave's own (the others only take part in loads and barriers).
+  int nkt = (Sk + ap::BN - 1) / ap::BN;
+  if (causal) nkt = min(nkt, (q0 + ap::BM - 1) / ap::BN + 1);
+  const int nkt_w = causal ? min(nkt, (qw + ap::WQ - 1) / ap::BN + 1) : nkt;
+  // First tile holding a key past Sk or, causal, past one of this wave's queries.
+  const int first_mask = causal ? min(qw / ap::BN, Sk / ap::BN) : Sk / ap::BN;
+
+  // DMA, per pair of tiles (64 keys, one stage of K and one of V): wave w brings chunks
+  // 4 w .. 4 w + 3 (1 KiB each: keys 4 i .. 4 i + 3) of both.
+  const int ks2b = (int)g.ks[2] * 2, vs2b = (int)g.vs[2] * 2;
+  const u32x4 rsK =
+      ap::rsrc((const uint16_t*)g.k + b * g.ks[0] + h * g.ks[1], (uint32_t)((Sk - 1) * ks2b + ap::ROW));
+  const u32x4 rsV =
+      ap::rsrc((const uint16_t*)g.v + b * g.vs[0] + h * g.vs[1], (uint32_t)((Sk - 1) * vs2b + ap::ROW));
+  int vk[4], vv[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int key = 4 * (4 * wave + u) + (lane >> 4), p = lane & 15;
+    vk[u] = key * ks2b + (p ^ (key & 15)) * 16;
+    vv[u] = key * vs2b + ((((p >> 2) ^ (key & 3)) << 2) | (p & 3)) * 16;
+  }
+  const int kstep = 2 * ap::BN * ks2b, vstep = 2 * ap::BN * vs2b;
+  const int npair = (nkt + 1) / 2;  // tile pairs of the workgroup
+  auto issue = [&](int tp) {        // tile pair tp into stage tp % 4
+    const uint32_t st = lds0 + (uint32_t)((tp & 3) * ap::STAGE) + (uint32_t)(4 * wave * 1024);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      ap::load_lds16(rsK, st + u * 1024, vk[u], tp * kstep);
+      ap::load_lds16(rsV, st + ap::VREG + u * 1024, vv[u], tp * vstep);
+    }
+  };
+  issue(0);
+  if (npair > 1) issue(1);
+  if (npair > 2) issue(2);
+
+  // Q^T fragments of this lane's two queries, pre-scaled and rounded to the input type.
+  frag qf[2][8];
+  int qpos[2];
+  {
+    const uint16_t* Q = (const uint16_t*)g.q + b * g.qs[0] + h * g.qs[1];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      qpos[qb] = qw + qb * 32 + (lane & 31);
+#pragma unroll
+      for (int dd = 0; dd < 8; ++dd) {
+        u32x4 raw = {0u, 0u, 0u, 0u};
+        if (qpos[qb] < Sq) raw = *(const u32x4*)(Q + (int64_t)qpos[qb] * g.qs[2] + dd * 16 + half * 8);
+        uint16_t tmp[8];
+        const uint16_t* hv = (const uint16_t*)&raw;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) tmp[u] = elem<T>::from_float(elem<T>::to_float(hv[u]) * g.q_scale);
+        qf[qb][dd] = ap::frag_to_agpr(__builtin_bit_cast(frag, *(const u32x4*)tmp));  // MFMA b operands from AGPRs
+      }
+    }
+  }
+  // Output addressing, computed now so the key loop carries no 64-bit arguments.
+  uint16_t* const obase = (uint16_t*)g.o + (int64_t)b * g.os[0] + (int64_t)h * g.os[1];
+  const int64_t os2 = g.os[2], os3 = g.os[3];
+  const int o_dtype = g.o_dtype;
+
+  // LDS read addresses (bytes, stage 0).  K fragment dd: key lane % 32, chunk 2 dd + half.
+  // V^T fragment of d block i: lane (group gq, r, q) at key 4 (gq / 2) + r (+ 16 t + 8 R),
+  // d 32 i + 16 (gq % 2) + 4 q; key % 4 = r picks the 64-byte chunk i ^ r.
+  int k_rd[8], v_rd[4];
+#pragma unroll
+  for (int dd = 0; dd < 8; ++dd) k_rd[dd] = (lane & 31) * ap::ROW + (((2 * dd + half) ^ (lane & 15)) * 16);
+  {
+    const int gq = lane >> 4, r = (lane & 15) >> 2, q = lane & 3;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      v_rd[i] = ap::VREG + (4 * (gq >> 1) + r) * ap::ROW + ((i ^ r) * 64) + (16 * (gq & 1) + 4 * q) * 2;
+  }
+
+  floatx16 o[2][4];  // O^T accumulators, in AGPRs
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[qb][i] = ap::to_agpr(floatx16{});
+  floatx16 s[2][2];  // [buffer][query block]: S^T of a tile, shifted by -m
+  floatx16 negm[2];  // -m in every register: the first MFMA's accumulator input
+  float m[2], ls[2];
+  u32x4 pw[2][2];  // [query block][16-key slice]: P^T, two rounded values per word
+
+  // Masking through the accumulator's starting value: for a tile that holds a key past Sk
+  // or (causal) past one of this wave's queries, the first MFMA of its scores starts from
+  // -inf at those positions (base elsewhere), so the scores come out masked.
+  auto masked_start = [&](floatx16 (&c)[2], const float (&base)[2], int k0) {
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const int lim = (causal ? min(qpos[qb] + 1, Sk) : Sk) - k0 - half * 4;  // keys below lim stay
+#pragma unroll
+      for (int r = 0; r < 16; ++r) c[qb][r] = (r >> 2) * 8 + (r & 3) < lim ? base[qb] : -INFINITY;
+    }
+  };
+  // Top of an odd iteration j = 2 tp - 1: tile pair tp (tiles j + 1, j + 2) landed (own
+  // loads, then everyone's: the barrier), and every wave is done with pair tp - 2, whose
+  // stage takes pair tp + 2.
+  auto sync_pair = [&](int tp) {
+    if (tp + 1 < npair)
+      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("s_barrier" ::: "memory");
+    if (tp + 2 < npair) issue(tp + 2);
+  };
+  // Stage moves of the fragment read addresses (to the stage of pair tp from tp - 1).
+  auto stage_delta = [](int tp) { return ((tp & 3) - ((tp - 1) & 3)) * ap::STAGE; };
+
+  // Tile 0: scores, exact max.
+  if (npair > 2)
+    asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+  else if (npair > 1)
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  asm volatile("s_barrier" ::: "memory");
+  {
+    floatx16 start[2] = {};
+    if (first_mask == 0) masked_start(start, {0.f, 0.f}, 0);
+#pragma unroll
+    for (int dd = 0; dd < 8; ++dd) {
+      const frag kf = *(const frag*)(lds + k_rd[dd]);
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) s[0][qb] = mfma_traits<T>::mma(kf, qf[qb][dd], dd == 0 ? start[qb] : s[0][qb]);
+    }
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      float mx = s[0][qb][0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[0][qb][r]);
+      mx = ap::max_halves(mx);
+      m[qb] = mx;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[0][qb][r] -= mx;
+        negm[qb][r] = -mx;
+      }
+      ls[qb] = 0.f;
+    }
+  }
+
+  // P^T item w (0..15): the pair of rounded p in word sl of slice t of query block qb,
+  // from the scores of buffer B.
+  auto p_item = [&](auto b_c, auto w_c) {
+    constexpr int B = decltype(b_c)::value, W = decltype(w_c)::value;
+    // items 0-3: query block 0, slice 0; 4-7: block 1, slice 0; 8-11: block 0, slice 1; 12-15: block 1, slice 1
+    constexpr int QB = (W >> 2) & 1, TT = W >> 3, SL = W & 3;
+    constexpr int r0 = 8 * TT + 2 * SL;
+    pw[QB][TT][SL] = attn::pack2<T>(__builtin_amdgcn_exp2f(s[B][QB][r0]), __builtin_amdgcn_exp2f(s[B][QB][r0 + 1]));
+  };
+  auto sum_item = [&](auto w_c) {
+    constexpr int W = decltype(w_c)::value;
+    constexpr int QB = (W >> 2) & 1, TT = W >> 3, SL = W & 3;
+    ls[QB] = ap::dot_ones<T>(pw[QB][TT][SL], ls[QB]);
+  };
+
+  // Iteration j (P = j % 2; S_j in buffer P).  Tile t lives in stage (t / 2) % 4 at
+  // KV * (t % 2); k_rd points at the stage of K_{j+1}, v_rd at that of V_j.  The last
+  // iteration of a wave (no tile j + 1) computes scores from whatever the stage holds and
+  // leaves them unused: its max takes no part in the rescale check, nothing reads them.
+  auto iter = [&](auto p_c, int j) {
+    constexpr int P = decltype(p_c)::value;
+    constexpr int CUR = P, NXT = P ^ 1;
+    constexpr int OFF_K1 = P == 0 ? ap::KV : 0, OFF_V = P == 0 ? 0 : ap::KV;
+    const bool has_next = j + 1 < nkt_w;
+    if constexpr (P == 1) {
+      const int tp = (j + 1) / 2;
+      sync_pair(tp);
+      const int dlt = stage_delta(tp);
+#pragma unroll
+      for (int dd = 0; dd < 8; ++dd) k_rd[dd] += dlt;
+    } else if (j > 0) {
+      const int dlt = stage_delta(j / 2);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v_rd[i] += dlt;
+    }
+    // Tiles from first_mask on are the last of the wave: negm takes -inf at their masked
+    // positions from here on (a rescale resets it, and the next iteration sets it again).
+    if (j + 1 >= first_mask && has_next) masked_start(negm, {-m[0], -m[1]}, (j + 1) * ap::BN);
+    __builtin_amdgcn_sched_barrier(0);
+    // Phase A: all eight K fragments of tile j + 1 read at once, then eight groups of two
+    // MFMAs of S_{j+1}, with P^T items 0..11 of tile j spread over them (1.5 per group)
+    // and one V^T fragment of tile j read per group for phase B.
+    auto v_frag = [&](int t, int i) {
+      const char* p = lds + v_rd[i] + OFF_V + t * 16 * ap::ROW;
+      const ap::v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) ap::v4i16*)p);
+      const ap::v4i16 hi =
+          __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) ap::v4i16*)(p + 8 * ap::ROW));
+      const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+      return __builtin_bit_cast(frag, u32x4{l2[0], l2[1], h2[0], h2[1]});
+    };
+    frag kf[8], vf[8];
+#pragma unroll
+    for (int dd = 0; dd < 8; ++dd) kf[dd] = *(const frag*)(lds + k_rd[dd] + OFF_K1);
+    __builtin_amdgcn_sched_barrier(0);
+    static_for<0, 8>([&](auto dd_c) {
+      constexpr int DD = decltype(dd_c)::value;
+      static_for<0, 12>([&](auto w_c) {
+        constexpr int W = decltype(w_c)::value;
+        if constexpr (W * 2 / 3 == DD && W % 3 == 0) p_item(std::integral_constant<int, CUR>{}, w_c);
+      });
+      s[NXT][0] = mfma_traits<T>::mma(kf[DD], qf[0][DD], DD == 0 ? negm[0] : s[NXT][0]);
+      vf[DD] = v_frag(DD >> 2, DD & 3);
+      static_for<0, 12>([&](auto w_c) {
+        constexpr int W = decltype(w_c)::value;
+        if constexpr (W * 2 / 3 == DD && W % 3 != 0) p_item(std::integral_constant<int, CUR>{}, w_c);
+      });
+      s[NXT][1] = mfma_traits<T>::mma(kf[DD], qf[1][DD], DD == 0 ? negm[1] : s[NXT][1]);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    __builtin_amdgcn_sched_barrier(0);
+    // Phase B: eight groups (slice t, d block i) of two MFMAs of O^T += V_j^T . P_j^T; P^T
+    // items 12..15 in groups 0..3, the row sums and the max of S_{j+1} in the rest.
+    float mx[2] = {-INFINITY, -INFINITY};
+    static_for<0, 8>([&](auto g_c) {
+      constexpr int G = decltype(g_c)::value, t = G >> 2, i = G & 3;
+      if constexpr (G == 0) ap::nop_after_valu();
+      ap::pv_mma<T>(o[0][i], vf[G], __builtin_bit_cast(frag, pw[0][t]));
+      if constexpr (G < 4) p_item(std::integral_constant<int, CUR>{}, std::integral_constant<int, 12 + G>{});
+      if constexpr (G >= 4) {
+        constexpr int R = 4 * (G - 4);
+        mx[0] = fmaxf(fmaxf(mx[0], s[NXT][0][R]), s[NXT][0][R + 1]);
+        mx[0] = fmaxf(fmaxf(mx[0], s[NXT][0][R + 2]), s[NXT][0][R + 3]);
+      }
+      if constexpr (G == 3) ap::nop_after_valu();
+      ap::pv_mma<T>(o[1][i], vf[G], __builtin_bit_cast(frag, pw[1][t]));
+      if constexpr (G >= 4) {
+        constexpr int R = 4 * (G - 4);
+        mx[1] = fmaxf(fmaxf(mx[1], s[NXT][1][R]), s[NXT][1][R + 1]);
+        mx[1] = fmaxf(fmaxf(mx[1], s[NXT][1][R + 2]), s[NXT][1][R + 3]);
+        static_for<0, 4>([&](auto u_c) { sum_item(std::integral_constant<int, 4 * (G - 4) + decltype(u_c)::value>{}); });
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    });
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) mx[qb] = ap::max_halves(mx[qb]);
+    // Lazy rescale: raise m only where tile j + 1's max passes it by RESCALE_LOG2.
+    const bool grow0 = has_next && mx[0] > attn::RESCALE_LOG2, grow1 = has_next && mx[1] > attn::RESCALE_LOG2;
+    if (__builtin_amdgcn_ballot_w64(grow0 || grow1)) {
+      ap::nop_after_mfma();
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        const float delta = (qb == 0 ? grow0 : grow1) ? mx[qb] : 0.f;
+        const float alpha = __builtin_amdgcn_exp2f(-delta);
+        ls[qb] *= alpha;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[qb][i] = ap::to_agpr(ap::from_agpr(o[qb][i]) * alpha);
+        m[qb] += delta;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          s[NXT][qb][r] -= delta;
+          negm[qb][r] = -m[qb];
+        }
+      }
+    }
+  };
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
+  for (int j = 0;; j += 2) {
+    iter(P0{}, j);
+    if (j + 1 >= nkt_w) break;
+    iter(P1{}, j + 1);
+    if (j + 2 >= nkt_w) break;
+  }
+  // Tiles of later waves (causal): loads and barriers only.
+  for (int jj = nkt_w; jj < nkt; ++jj)
+    if (jj & 1) sync_pair((jj + 1) / 2);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  asm volatile("s_barrier" ::: "memory");  // the output staging reuses the stages
+  ap::nop_after_mfma();
+
+  // o = acc / l, staged per wave through LDS 64 d at a time; each lane then writes 4
+  // consecutive d of one query row.
+  constexpr int STR = 65;
+  float* stage = reinterpret_cast<float*>(lds) + wave * (32 * STR);
+  const bool ovec = o_dtype == elem<T>::code && os3 == 1;
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const float inv = 1.0f / ap::sum_halves(ls[qb]);
+#pragma unroll
+    for (int ps = 0; ps < 2; ++ps) {
+      wave_lds_order();
+#pragma unroll
+      for (int jb = 0; jb < 2; ++jb) {
+        const floatx16 ov = ap::from_agpr(o[qb][ps * 2 + jb]);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) stage[(lane & 31) * STR + jb * 32 + acc_row(r, lane)] = ov[r] * inv;
+      }
+      wave_lds_order();
+#pragma unroll
+      for (int e0 = 0; e0 < 32 * 16; e0 += 64) {
+        const int e = e0 + lane;
+        const int row = e >> 4, grp = (e & 15) * 4;
+        const int qp = qw + qb * 32 + row;
+        if (qp < Sq) {
+          const float* sp = stage + row * STR + grp;
+          const int64_t ob = (int64_t)qp * os2;
+          const int d0 = ps * 64 + grp;
+          if (ovec && (((uintptr_t)(obase + ob + d0)) & 7) == 0) {
+            *(u32x2*)(obase + ob + d0) = u32x2{attn::pack2<T>(sp[0], sp[1]), attn::pack2<T>(sp[2], sp[3])};
+          } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) store_from_float(obase, ob + (d0 + u) * os3, o_dtype, sp[u]);
+          }
+        }
+      }
+    }
+  }
+}
+
 // Vector-load variant: two waves per SIMD (two workgroups per CU) so that one
 // workgroup's softmax and LDS traffic overlap the other's matrix work.
 template <typename T, int DM>
@@ -703,10 +1159,17 @@ __global__ __launch_bounds__(AT_THREADS) void attention_generic_kernel(AttnArgs 
   attention_body<T, DM, false>(g);
 }
 
+// config: 0 = attention_fast_kernel where its conditions hold, else the four-wave kernels;
+// 1 = attention_pipe_kernel (head dim 128, the fast conditions); 2 = attention_fast_kernel
+// (the fast conditions); 3 = the four-wave kernels (attention_kernel, or
+// attention_generic_kernel for other strides).
+// A forced configuration whose conditions do not hold returns NT_ERR_INVALID unlaunched.
 template <typename T>
 static int attention_launch(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* v,
                             const int64_t* vs, void* o, const int64_t* os, int o_dtype, int64_t B, int64_t H,
-                            int64_t Sq, int64_t Sk, int64_t D, float q_scale, int causal, hipStream_t stream) {
+                            int64_t Sq, int64_t Sk, int64_t D, float q_scale, int causal, hipStream_t stream,
+                            int config = 0) {
+  if (config < 0 || config > 3) return NT_ERR_INVALID;
   if (B < 0 || H < 0 || Sq < 0 || Sk < 0 || D < 0 || D > 128) return NT_ERR_INVALID;
   if (!valid_dtype(o_dtype)) return NT_ERR_INVALID;
   if (B * H * Sq * D == 0) return 0;
@@ -739,13 +1202,21 @@ static int attention_launch(const void* q, const int64_t* qs, const void* k, con
            Sq + NW * 32 < 0x7fffffffLL && Sk > 0;
   };
   const int64_t dm = D <= 64 ? 64 : 128;
-  const bool fast = fast_ok(dm);
-  const int64_t bm = fast ? NW * 32 : AT_BM;
+  const bool fast_fits = fast_ok(dm), pipe_fits = dm == 128 && fast_fits;
+  if ((config == 1 && !pipe_fits) || (config == 2 && !fast_fits)) return NT_ERR_INVALID;
+  // The eight-wave kernel is the default: measured on MI355X at B=4, H=32, S=4096, D=128
+  // it runs 1,090-1,130 us non-causal against 1,140-1,270 us for the pipelined kernel.
+  const bool pipe = config == 1;
+  const bool fast = config == 2 || (config == 0 && fast_fits);
+  static_assert(ap::BM == NW * 32, "both fast kernels take 256 queries per workgroup");
+  const int64_t bm = pipe || fast ? NW * 32 : AT_BM;
   const int64_t qblocks = cdiv(Sq, bm);
   if (qblocks * B * H > 0x7fffffffLL) return NT_ERR_INVALID;
   g.q_blocks = (int)qblocks;
   const dim3 grid((unsigned)(qblocks * B * H)), blk(AT_THREADS);
-  if (fast) {
+  if (pipe) {
+    hipLaunchKernelGGL((attention_pipe_kernel<T>), grid, dim3(ap::NW * 64), 0, stream, g);
+  } else if (fast) {
     if (dm == 64)
       hipLaunchKernelGGL((attention_fast_kernel<T, 64, NW>), grid, dim3(NW * 64), 0, stream, g);
     else
@@ -876,3 +1347,9 @@ static int attention_f32_launch(const void* q, const int64_t* qs, const void* k,
 extern "C" int nt_attention_f16(NT_ATTN_PARAMS) { return nt::attention_launch<nt::f16_t>(NT_ATTN_ARGS); }
 extern "C" int nt_attention_bf16(NT_ATTN_PARAMS) { return nt::attention_launch<nt::bf16_t>(NT_ATTN_ARGS); }
 extern "C" int nt_attention_f32(NT_ATTN_PARAMS) { return nt::attention_f32_launch(NT_ATTN_ARGS); }
+extern "C" int nt_attention_config_f16(NT_ATTN_PARAMS, int config) {
+  return nt::attention_launch<nt::f16_t>(NT_ATTN_ARGS, config);
+}
+extern "C" int nt_attention_config_bf16(NT_ATTN_PARAMS, int config) {
+  return nt::attention_launch<nt::bf16_t>(NT_ATTN_ARGS, config);
+}

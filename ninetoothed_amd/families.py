@@ -664,10 +664,14 @@ def match_attention(ctx):
 class AttentionPlan(Plan):
     family = "attention"
 
-    def __init__(self, q, k, v, o, scale, causal):
+    def __init__(self, q, k, v, o, scale, causal, config=0):
         self.q, self.k, self.v, self.o = q, k, v, o
         self.scale = scale
         self.causal = causal
+        self.config = config  # 0: the library picks the kernel; else one forced kernel
+
+    def with_config(self, config):
+        return AttentionPlan(self.q, self.k, self.v, self.o, self.scale, self.causal, config)
 
     def bind(self, values, index):
         import torch
@@ -681,7 +685,7 @@ class AttentionPlan(Plan):
             # scalars in the reference's generated kernel): c is rounded to q's dtype.
             scale = float(torch.tensor(scale, dtype=q.dtype))
         launch = kernels.bind_attention(q, values[self.k], values[self.v], values[self.o], causal=self.causal,
-                                        q_scale=scale)
+                                        q_scale=scale, config=self.config)
         iq, ik, iv, io = index[self.q], index[self.k], index[self.v], index[self.o]
 
         def run(args):
@@ -690,7 +694,10 @@ class AttentionPlan(Plan):
         return run
 
     def describe(self):
-        return {"family": "attention", "causal": self.causal, "scale": self.scale}
+        d = {"family": "attention", "causal": self.causal, "scale": self.scale}
+        if self.config:
+            d["config"] = self.config
+        return d
 
 
 def _fit_attention(ctx, qn, kn, vn, on):
@@ -972,10 +979,11 @@ def candidates(ctx):
     """Every family plan whose pattern and geometry fit, in the order ``select`` tries them.
 
     A GEMM plan stands for each of the 16-bit GEMM's kernel configurations (the DMA kernel,
-    the register-staged one, the element-wise loader one) and a conv2d plan for each of the
+    the register-staged one, the element-wise loader one), a conv2d plan for each of the
     convolution's paths (re-laid input through the DMA or the N-H-W-C kernel, the direct
-    kernel): configurations the call's operands do not admit fail when bound or launched
-    and drop out of the timing."""
+    kernel) and an attention plan for each attention
+    kernel (pipelined one-wave-per-SIMD, eight-wave, four-wave): configurations the call's
+    operands do not admit fail when bound or launched and drop out of the timing."""
     from ninetoothed_amd import kernels
 
     plans = []
@@ -988,6 +996,8 @@ def candidates(ctx):
             plans.extend(plan.with_config(cfg) for cfg in kernels.GEMM_CONFIGS)
         elif isinstance(plan, ConvPlan) and not plan.config:
             plans.extend(plan.with_config(cfg) for cfg in kernels.CONV_CONFIGS)
+        elif isinstance(plan, AttentionPlan) and not plan.config:
+            plans.extend(plan.with_config(cfg) for cfg in kernels.ATTENTION_CONFIGS)
         elif plan is not None:
             plans.append(plan)
     return plans

@@ -276,8 +276,17 @@ def conv2d(x, w, y, padding=(0, 0), stride=(1, 1), dilation=(1, 1), round_dtype=
 
 
 # ------------------------------------------------------------------- attention
-def bind_attention(q, k, v, o, causal=False, q_scale=LOG2E):
-    """launch(q, k, v, o): flash attention forward of the reference application; q pre-scaled by ``q_scale``."""
+# Kernel configurations of the 16-bit attention that ``config`` can force (0: the eight-wave
+# kernel where its conditions hold): the one-wave-per-SIMD pipelined kernel (head dim 128),
+# the eight-wave kernel, the four-wave kernels (any strides).
+ATTENTION_CONFIGS = (1, 2, 3)
+
+
+def bind_attention(q, k, v, o, causal=False, q_scale=LOG2E, config=0):
+    """launch(q, k, v, o): flash attention forward of the reference application; q pre-scaled by ``q_scale``.
+
+    A nonzero ``config`` (fp16/bf16 only) forces one kernel; a call its conditions do not
+    admit raises ``KernelLaunchError`` without launching."""
     device = _check_device(q, k, v, o)
     if not (q.dim() == k.dim() == v.dim() == o.dim() == 4):
         raise ValueError("attention expects [B, H, S, D] tensors")
@@ -289,19 +298,26 @@ def bind_attention(q, k, v, o, causal=False, q_scale=LOG2E):
         raise ValueError("attention shape mismatch")
     if d > 128:
         raise ValueError("attention head dim must be <= 128")
-    fn, name = _entry("nt_attention", q.dtype)
+    if config:
+        if config not in ATTENTION_CONFIGS or _lib.dtype_suffix(q.dtype) not in ("f16", "bf16"):
+            raise TypeError(f"attention config {config} needs fp16/bf16 operands and one of {ATTENTION_CONFIGS}")
+        fn, name = _entry("nt_attention_config", q.dtype)
+        extra = (int(config),)
+    else:
+        fn, name = _entry("nt_attention", q.dtype)
+        extra = ()
     qs, ks, vs, os_ = (_lib.int64_array(t.stride()) for t in (q, k, v, o))
     tail = (_lib.dtype_code(o.dtype), bsz, heads, sq, sk, d, float(q_scale), 1 if causal else 0)
     stream = _stream_of(device)
 
     def launch(q, k, v, o):
-        code = fn(q.data_ptr(), qs, k.data_ptr(), ks, v.data_ptr(), vs, o.data_ptr(), os_, *tail, stream())
+        code = fn(q.data_ptr(), qs, k.data_ptr(), ks, v.data_ptr(), vs, o.data_ptr(), os_, *tail, stream(), *extra)
         if code:
             _raise(code, name)
 
     return launch
 
 
-def attention(q, k, v, o, causal=False, q_scale=LOG2E):
-    bind_attention(q, k, v, o, causal, q_scale)(q, k, v, o)
+def attention(q, k, v, o, causal=False, q_scale=LOG2E, config=0):
+    bind_attention(q, k, v, o, causal, q_scale, config)(q, k, v, o)
     return o

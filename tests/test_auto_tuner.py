@@ -231,3 +231,30 @@ def test_tuned_conv_picks_a_path():
     assert torch.allclose(y.float(), ref, atol=2e-2, rtol=1e-2)
     (plan,) = h.plans()
     assert plan["family"] == "tuned" and len(plan["chosen"]) == 1 and '"config"' in plan["chosen"][0]
+
+
+def test_attention_plans_expand_into_kernels():
+    h = ninetoothed.make(pg.attention_arrangement, pg.attention_application_scaled, pg.attention_tensors())
+    q = torch.empty(1, 2, 256, 128, dtype=torch.float16)
+    names = list(h._kernel.params)
+    ctx = h._kernel.context(dict(zip(names, (q, q, q, True, q))), {})
+    described = [p.describe() for p in families.candidates(ctx)]
+    assert [(d["family"], d["config"]) for d in described] == [("attention", 1), ("attention", 2), ("attention", 3)]
+
+
+@pytest.mark.gpu
+def test_tuned_attention_picks_a_kernel():
+    import math
+
+    import torch.nn.functional as F
+
+    h = ninetoothed.make(pg.attention_arrangement, pg.attention_application_scaled, pg.attention_tensors(),
+                         max_num_configs=4)
+    g = torch.Generator().manual_seed(7)
+    q, k, v = (torch.randn(1, 4, 512, 128, generator=g).half().cuda() for _ in range(3))
+    o = torch.empty_like(q)
+    h(q, k, v, True, o)
+    ref = F.scaled_dot_product_attention(q.float(), k.float(), v.float(), is_causal=True, scale=1 / math.sqrt(128))
+    assert torch.allclose(o.float(), ref, atol=1e-2, rtol=1e-2)
+    (plan,) = h.plans()
+    assert plan["family"] == "tuned" and len(plan["chosen"]) == 1 and '"attention"' in plan["chosen"][0]

@@ -18,7 +18,7 @@ import torch.nn.functional as F
 
 import ninetoothed_amd as ninetoothed
 import programs as pg
-from ninetoothed_amd import _lib
+from ninetoothed_amd import _lib, kernels
 from oracle import apply
 
 pytestmark = pytest.mark.gpu
@@ -231,6 +231,10 @@ def test_attention_work_orders_every_head(is_causal, shape):
     kernel(q, k, v, is_causal, o)
     torch.cuda.synchronize()
     _check_every_head(q, k, v, o, is_causal, 1 / math.sqrt(128))  # the application's constant scale
+    if shape[3] == 128:  # the pipelined kernel's work order too (same block order, its own grid)
+        o.fill_(float("nan"))
+        kernels.attention(q, k, v, o, causal=is_causal, q_scale=kernels.LOG2E / math.sqrt(128), config=1)
+        _check_every_head(q, k, v, o, is_causal, 1 / math.sqrt(128))
 
 
 # ----------------------------------------------------------------------- softmax

@@ -514,3 +514,51 @@ def test_attention_headline_causal():
             if not torch.allclose(o[b:b + 1, h:h + 1].float(), ref, atol=1e-2, rtol=1e-2):
                 bad.append((b, h))
     assert not bad, f"heads outside tolerance: {bad[:8]}"
+
+
+# Every kernel configuration of the 16-bit attention (config 1: one-wave-per-SIMD pipelined
+# kernel, D = 128; 2: eight-wave kernel; 3: four-wave kernels) on ragged and causal shapes,
+# with scores that rise along the keys (the lazy rescale fires on nearly every tile) and on
+# random data, against the float64 restatement of the kernels' arithmetic.
+@pytest.mark.parametrize("config", (1, 2, 3))
+@pytest.mark.parametrize("causal", (False, True))
+@pytest.mark.parametrize("sq, sk", ((700, 700), (300, 700), (129, 65), (64, 32), (257, 1000)))
+def test_attention_configs(config, causal, sq, sk):
+    d, dtype = 128, torch.float16
+    u = _randn((d,), torch.float32, 80) / math.sqrt(d)
+    q = (_randn((1, 3, sq, d), torch.float32, 81) + 2.0 * u).to(dtype)
+    ramp = torch.arange(sk, device=DEV, dtype=torch.float32)[:, None] * (0.11 / math.sqrt(d)) * u * d
+    k = (_randn((1, 3, sk, d), torch.float32, 82) + ramp).to(dtype)
+    v = _randn((1, 3, sk, d), dtype, 83)
+    qs = kernels.LOG2E / math.sqrt(d)
+    for qq, kk in ((q, k), (_randn((1, 3, sq, d), dtype, 84), _randn((1, 3, sk, d), dtype, 85))):
+        o = torch.empty_like(qq)
+        kernels.attention(qq, kk, v, o, causal=causal, q_scale=qs, config=config)
+        ref = _attention_ref64(qq, kk, v, causal, qs)
+        assert torch.allclose(o.double(), ref, atol=1e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("causal", (False, True))
+def test_attention_pipe_bf16_against_eight_wave(causal):
+    q, k, v = (_randn((2, 5, 613, 128), torch.bfloat16, 90 + i) for i in range(3))
+    o1, o2 = torch.empty_like(q), torch.empty_like(q)
+    scale = 1.0 / math.sqrt(128)
+    kernels.attention(q, k, v, o1, causal=causal, q_scale=kernels.LOG2E * scale, config=1)
+    kernels.attention(q, k, v, o2, causal=causal, q_scale=kernels.LOG2E * scale, config=2)
+    ref = _sdpa_ref(q, k, v, causal, scale)
+    assert torch.allclose(o1.float(), ref, atol=2e-2, rtol=2e-2)
+    assert torch.allclose(o1.float(), o2.float(), atol=2e-2, rtol=2e-2)
+
+
+def test_attention_config_conditions_are_checked():
+    from ninetoothed_amd.errors import KernelLaunchError
+
+    q, k, v = (_randn((1, 2, 100, 64), torch.float16, 95 + i) for i in range(3))
+    o = torch.empty_like(q)
+    with pytest.raises(KernelLaunchError):  # the pipelined kernel takes head dim 128 only
+        kernels.attention(q, k, v, o, q_scale=kernels.LOG2E, config=1)
+    qt = q.transpose(2, 3).contiguous().transpose(2, 3)  # d-stride != 1: four-wave kernels only
+    with pytest.raises(KernelLaunchError):
+        kernels.attention(qt, k, v, o, q_scale=kernels.LOG2E, config=2)
+    kernels.attention(qt, k, v, o, q_scale=kernels.LOG2E, config=3)
+    assert torch.allclose(o.float(), _sdpa_ref(q, k, v, False, 1.0), atol=1e-2, rtol=1e-2)
