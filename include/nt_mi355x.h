@@ -81,6 +81,22 @@ int nt_softmax_bf16(const void* x, int64_t x_row_stride, int64_t x_col_stride,
                     void* y, int64_t y_row_stride, int64_t y_col_stride,
                     int64_t rows, int64_t cols, int64_t block, hipStream_t stream);
 
+/* One kernel configuration of the softmax, for the auto-tuner: the arguments of
+ * nt_softmax_* plus `config` (0 = as nt_softmax_* choose; 1, 2, 3 = the register path
+ * with workgroups of four, eight, one wave, when the segment fits it; 4 = the two-sweep
+ * kernel).  A forced configuration that does not fit returns NT_ERR_INVALID before
+ * launching.  Replaces the reference's tuning over num_warps 4, 8, 1
+ * (reference src/ninetoothed/backends/triton.py:151-155). */
+int nt_softmax_config_f32(const void* x, int64_t x_row_stride, int64_t x_col_stride,
+                          void* y, int64_t y_row_stride, int64_t y_col_stride,
+                          int64_t rows, int64_t cols, int64_t block, hipStream_t stream, int config);
+int nt_softmax_config_f16(const void* x, int64_t x_row_stride, int64_t x_col_stride,
+                          void* y, int64_t y_row_stride, int64_t y_col_stride,
+                          int64_t rows, int64_t cols, int64_t block, hipStream_t stream, int config);
+int nt_softmax_config_bf16(const void* x, int64_t x_row_stride, int64_t x_col_stride,
+                           void* y, int64_t y_row_stride, int64_t y_col_stride,
+                           int64_t rows, int64_t cols, int64_t block, hipStream_t stream, int config);
+
 /* ---------------------------------------------------------------------------
  * 2-D max pooling on an N-C-H-W indexed input:
  *   y[n,c,p,q] = max over r < kh, s < kw of x[n, c, p*sh - ph + r*dh, q*sw - pw + s*dw],
@@ -102,6 +118,26 @@ int nt_max_pool2d_bf16(const void* x, const int64_t* x_strides, void* y, const i
                        int64_t N, int64_t C, int64_t H, int64_t W, int64_t P, int64_t Q,
                        int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
                        int64_t dh, int64_t dw, hipStream_t stream);
+
+/* One kernel configuration of max_pool2d, for the auto-tuner: the arguments of
+ * nt_max_pool2d_* plus `config` (0 = as nt_max_pool2d_* choose; 1 = the plane kernel:
+ * 16-bit, 2-wide windows of stride 2 inside the input, unit inner strides, 16-byte aligned
+ * rows, Q a multiple of 8; 2 = the element-wise kernel, any shape).  A forced plane kernel
+ * whose conditions do not hold returns NT_ERR_INVALID before launching.  Replaces the
+ * per-configuration launchers of the reference's auto-tuner for the max_pool2d
+ * application (reference tests/test_max_pool2d.py:13-64). */
+int nt_max_pool2d_config_f32(const void* x, const int64_t* x_strides, void* y, const int64_t* y_strides,
+                             int64_t N, int64_t C, int64_t H, int64_t W, int64_t P, int64_t Q,
+                             int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
+                             int64_t dh, int64_t dw, hipStream_t stream, int config);
+int nt_max_pool2d_config_f16(const void* x, const int64_t* x_strides, void* y, const int64_t* y_strides,
+                             int64_t N, int64_t C, int64_t H, int64_t W, int64_t P, int64_t Q,
+                             int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
+                             int64_t dh, int64_t dw, hipStream_t stream, int config);
+int nt_max_pool2d_config_bf16(const void* x, const int64_t* x_strides, void* y, const int64_t* y_strides,
+                              int64_t N, int64_t C, int64_t H, int64_t W, int64_t P, int64_t Q,
+                              int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
+                              int64_t dh, int64_t dw, hipStream_t stream, int config);
 
 /* ---------------------------------------------------------------------------
  * GEMM with the addmm epilogue, fp32 accumulation:

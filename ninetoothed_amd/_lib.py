@@ -44,7 +44,15 @@ _SIGNATURES = {
         for t in ("f32", "f16", "bf16")
     },
     **{
+        f"nt_softmax_config_{t}": (_P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _I)
+        for t in ("f32", "f16", "bf16")
+    },
+    **{
         f"nt_max_pool2d_{t}": (_P, _I64P, _P, _I64P) + (_I64,) * 14 + (_P,)
+        for t in ("f32", "f16", "bf16")
+    },
+    **{
+        f"nt_max_pool2d_config_{t}": (_P, _I64P, _P, _I64P) + (_I64,) * 14 + (_P, _I)
         for t in ("f32", "f16", "bf16")
     },
     **{

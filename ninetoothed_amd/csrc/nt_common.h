@@ -114,7 +114,7 @@ __device__ __forceinline__ void wave_lds_order() { asm volatile("" ::: "memory")
 // Compile-time loop: f(std::integral_constant<int, i>) for i in [B, E), so that every
 // register index inside f is a constant (used for fixed instruction schedules).
 template <int B, int E, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
+__host__ __device__ __forceinline__ void static_for(F&& f) {
   if constexpr (B < E) {
     f(std::integral_constant<int, B>{});
     static_for<B + 1, E>(f);

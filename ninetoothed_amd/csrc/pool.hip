@@ -81,11 +81,15 @@ __global__ __launch_bounds__(256) void pool_w2_plane_kernel(const uint16_t* __re
   }
 }
 
+// config: 0 = the plane kernel where its conditions hold, else the element-wise kernel;
+// 1 = plane kernel; 2 = element-wise kernel.  A forced plane kernel whose conditions do not
+// hold returns NT_ERR_INVALID unlaunched.
 template <typename T>
 static int pool_launch(const void* x, const int64_t* xs, void* y, const int64_t* ys, int64_t N, int64_t C, int64_t H,
                        int64_t W, int64_t P, int64_t Q, int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph,
-                       int64_t pw, int64_t dh, int64_t dw, hipStream_t stream) {
+                       int64_t pw, int64_t dh, int64_t dw, hipStream_t stream, int config = 0) {
   typedef typename elem<T>::storage S;
+  if (config < 0 || config > 2) return NT_ERR_INVALID;
   if (N < 0 || C < 0 || H < 0 || W < 0 || P < 0 || Q < 0 || kh <= 0 || kw <= 0 || sh <= 0 || sw <= 0 || dh <= 0 ||
       dw <= 0 || ph < 0 || pw < 0)
     return NT_ERR_INVALID;
@@ -98,7 +102,8 @@ static int pool_launch(const void* x, const int64_t* xs, void* y, const int64_t*
                     (xs[0] * 2) % 16 == 0 && (xs[1] * 2) % 16 == 0 && (xs[2] * 2) % 16 == 0 &&
                     (ys[0] * 2) % 16 == 0 && (ys[1] * 2) % 16 == 0 && (ys[2] * 2) % 16 == 0 && N * C <= 0x7fffffffLL &&
                     H * xs[2] <= 0x7fffffffLL && P * ys[2] <= 0x7fffffffLL;
-  if (fast) {
+  if (config == 1 && !fast) return NT_ERR_INVALID;
+  if (fast && config != 2) {
     hipLaunchKernelGGL(pool_w2_plane_kernel<T>, dim3((unsigned)(N * C)), dim3(256), 0, stream, (const uint16_t*)x,
                        (uint16_t*)y, s);
   } else {
@@ -120,3 +125,12 @@ static int pool_launch(const void* x, const int64_t* xs, void* y, const int64_t*
 NT_POOL_ENTRY(nt_max_pool2d_f32, float)
 NT_POOL_ENTRY(nt_max_pool2d_f16, nt::f16_t)
 NT_POOL_ENTRY(nt_max_pool2d_bf16, nt::bf16_t)
+#define NT_POOL_CONFIG_ENTRY(NAME, T)                                                                               \
+  extern "C" int NAME(const void* x, const int64_t* xs, void* y, const int64_t* ys, int64_t N, int64_t C, int64_t H, \
+                      int64_t W, int64_t P, int64_t Q, int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph,   \
+                      int64_t pw, int64_t dh, int64_t dw, hipStream_t stream, int config) {                          \
+    return nt::pool_launch<T>(x, xs, y, ys, N, C, H, W, P, Q, kh, kw, sh, sw, ph, pw, dh, dw, stream, config);      \
+  }
+NT_POOL_CONFIG_ENTRY(nt_max_pool2d_config_f32, float)
+NT_POOL_CONFIG_ENTRY(nt_max_pool2d_config_f16, nt::f16_t)
+NT_POOL_CONFIG_ENTRY(nt_max_pool2d_config_bf16, nt::bf16_t)

@@ -753,13 +753,17 @@ def _fit_attention(ctx, qn, kn, vn, on):
 class SoftmaxPlan(Plan):
     family = "softmax"
 
-    def __init__(self, x, y, block):
+    def __init__(self, x, y, block, config=0):
         self.x, self.y, self.block = x, y, block
+        self.config = config  # 0: the library picks the kernel; else one forced kernel
+
+    def with_config(self, config):
+        return SoftmaxPlan(self.x, self.y, self.block, config)
 
     def bind(self, values, index):
         from ninetoothed_amd import kernels
 
-        launch = kernels.bind_softmax(values[self.x], values[self.y], block=self.block)
+        launch = kernels.bind_softmax(values[self.x], values[self.y], block=self.block, config=self.config)
         ix, iy = index[self.x], index[self.y]
 
         def run(args):
@@ -768,7 +772,10 @@ class SoftmaxPlan(Plan):
         return run
 
     def describe(self):
-        return {"family": "softmax", "block": self.block}
+        d = {"family": "softmax", "block": self.block}
+        if self.config:
+            d["config"] = self.config
+        return d
 
 
 def match_softmax(ctx):
@@ -815,15 +822,19 @@ def match_softmax(ctx):
 class MaxPoolPlan(Plan):
     family = "max_pool2d"
 
-    def __init__(self, x, y, window, stride, padding, dilation):
+    def __init__(self, x, y, window, stride, padding, dilation, config=0):
         self.x, self.y = x, y
         self.window, self.stride, self.padding, self.dilation = window, stride, padding, dilation
+        self.config = config  # 0: the library picks the kernel; else one forced kernel
+
+    def with_config(self, config):
+        return MaxPoolPlan(self.x, self.y, self.window, self.stride, self.padding, self.dilation, config)
 
     def bind(self, values, index):
         from ninetoothed_amd import kernels
 
         launch = kernels.bind_max_pool2d(values[self.x], values[self.y], self.window, stride=self.stride,
-                                         padding=self.padding, dilation=self.dilation)
+                                         padding=self.padding, dilation=self.dilation, config=self.config)
         ix, iy = index[self.x], index[self.y]
 
         def run(args):
@@ -832,7 +843,10 @@ class MaxPoolPlan(Plan):
         return run
 
     def describe(self):
-        return {"family": "max_pool2d", "window": self.window, "stride": self.stride, "padding": self.padding}
+        d = {"family": "max_pool2d", "window": self.window, "stride": self.stride, "padding": self.padding}
+        if self.config:
+            d["config"] = self.config
+        return d
 
 
 def match_max_pool2d(ctx):
@@ -981,8 +995,10 @@ def candidates(ctx):
     A GEMM plan stands for each of the 16-bit GEMM's kernel configurations (the DMA kernel,
     the register-staged one, the element-wise loader one), a conv2d plan for each of the
     convolution's paths (re-laid input through the DMA or the N-H-W-C kernel, the direct
-    kernel) and an attention plan for each attention
-    kernel (pipelined one-wave-per-SIMD, eight-wave, four-wave): configurations the call's
+    kernel), an attention plan for each attention kernel (pipelined one-wave-per-SIMD,
+    eight-wave, four-wave), a softmax plan for each softmax kernel (register path with four,
+    eight or one wave per workgroup, two-sweep) and a max_pool2d plan for each pooling kernel
+    (plane, element-wise): configurations the call's
     operands do not admit fail when bound or launched and drop out of the timing."""
     from ninetoothed_amd import kernels
 
@@ -998,6 +1014,10 @@ def candidates(ctx):
             plans.extend(plan.with_config(cfg) for cfg in kernels.CONV_CONFIGS)
         elif isinstance(plan, AttentionPlan) and not plan.config:
             plans.extend(plan.with_config(cfg) for cfg in kernels.ATTENTION_CONFIGS)
+        elif isinstance(plan, SoftmaxPlan) and not plan.config:
+            plans.extend(plan.with_config(cfg) for cfg in kernels.SOFTMAX_CONFIGS)
+        elif isinstance(plan, MaxPoolPlan) and not plan.config:
+            plans.extend(plan.with_config(cfg) for cfg in kernels.POOL_CONFIGS)
         elif plan is not None:
             plans.append(plan)
     return plans

@@ -83,8 +83,18 @@ def add(lhs, rhs, out):
 
 
 # --------------------------------------------------------------------- softmax
-def bind_softmax(x, y, block=None):
-    """launch(x, y): row softmax of a 2-D tensor over segments of ``block`` columns (default: whole rows)."""
+# Kernel configurations of the softmax that ``config`` can force (0: the four-wave register
+# path where the segment fits, else the two-sweep kernel): the register path with workgroups
+# of four, eight or one wave (the reference's num_warps candidates 4, 8, 1), the two-sweep
+# kernel.
+SOFTMAX_CONFIGS = (1, 2, 3, 4)
+
+
+def bind_softmax(x, y, block=None, config=0):
+    """launch(x, y): row softmax of a 2-D tensor over segments of ``block`` columns (default: whole rows).
+
+    A nonzero ``config`` forces one kernel; a call it does not admit raises
+    ``KernelLaunchError`` without launching."""
     device = _check_device(x, y)
     if x.dim() != 2 or y.shape != x.shape:
         raise ValueError("softmax expects matching 2-D tensors")
@@ -94,26 +104,41 @@ def bind_softmax(x, y, block=None):
     block = max(cols if block is None else int(block), 1)
     if cols > 1 and (x.stride(1) != 1 or y.stride(1) != 1):
         raise ValueError("softmax needs unit column stride")
-    fn, name = _entry("nt_softmax", x.dtype)
+    if config:
+        if config not in SOFTMAX_CONFIGS:
+            raise TypeError(f"softmax config {config} is not one of {SOFTMAX_CONFIGS}")
+        fn, name = _entry("nt_softmax_config", x.dtype)
+        extra = (int(config),)
+    else:
+        fn, name = _entry("nt_softmax", x.dtype)
+        extra = ()
     (xr, xc), (yr, yc) = x.stride(), y.stride()
     stream = _stream_of(device)
 
     def launch(x, y):
-        code = fn(x.data_ptr(), xr, xc, y.data_ptr(), yr, yc, rows, cols, block, stream())
+        code = fn(x.data_ptr(), xr, xc, y.data_ptr(), yr, yc, rows, cols, block, stream(), *extra)
         if code:
             _raise(code, name)
 
     return launch
 
 
-def softmax(x, y, block=None):
-    bind_softmax(x, y, block)(x, y)
+def softmax(x, y, block=None, config=0):
+    bind_softmax(x, y, block, config)(x, y)
     return y
 
 
 # ------------------------------------------------------------------ max_pool2d
-def bind_max_pool2d(x, y, window, stride=None, padding=(0, 0), dilation=(1, 1)):
-    """launch(x, y): y = max_pool2d(x) with -inf outside the input (any strides, N-C-H-W indexing)."""
+# Kernel configurations of max_pool2d that ``config`` can force (0: the plane kernel where
+# its conditions hold, else the element-wise one): the plane kernel, the element-wise kernel.
+POOL_CONFIGS = (1, 2)
+
+
+def bind_max_pool2d(x, y, window, stride=None, padding=(0, 0), dilation=(1, 1), config=0):
+    """launch(x, y): y = max_pool2d(x) with -inf outside the input (any strides, N-C-H-W indexing).
+
+    A nonzero ``config`` forces one kernel; a call it does not admit raises
+    ``KernelLaunchError`` without launching."""
     device = _check_device(x, y)
     if x.dim() != 4 or y.dim() != 4:
         raise ValueError("max_pool2d expects 4-D tensors")
@@ -127,21 +152,28 @@ def bind_max_pool2d(x, y, window, stride=None, padding=(0, 0), dilation=(1, 1)):
     if y.shape[0] != n or y.shape[1] != c:
         raise ValueError("max_pool2d batch/channel sizes differ")
     p, q = y.shape[2], y.shape[3]
-    fn, name = _entry("nt_max_pool2d", x.dtype)
+    if config:
+        if config not in POOL_CONFIGS:
+            raise TypeError(f"max_pool2d config {config} is not one of {POOL_CONFIGS}")
+        fn, name = _entry("nt_max_pool2d_config", x.dtype)
+        extra = (int(config),)
+    else:
+        fn, name = _entry("nt_max_pool2d", x.dtype)
+        extra = ()
     xs, ys = _lib.int64_array(x.stride()), _lib.int64_array(y.stride())
     dims = (n, c, h, w, p, q, kh, kw, sh, sw, ph, pw, dh, dw)
     stream = _stream_of(device)
 
     def launch(x, y):
-        code = fn(x.data_ptr(), xs, y.data_ptr(), ys, *dims, stream())
+        code = fn(x.data_ptr(), xs, y.data_ptr(), ys, *dims, stream(), *extra)
         if code:
             _raise(code, name)
 
     return launch
 
 
-def max_pool2d(x, y, window, stride=None, padding=(0, 0), dilation=(1, 1)):
-    bind_max_pool2d(x, y, window, stride, padding, dilation)(x, y)
+def max_pool2d(x, y, window, stride=None, padding=(0, 0), dilation=(1, 1), config=0):
+    bind_max_pool2d(x, y, window, stride, padding, dilation, config)(x, y)
     return y
 
 

@@ -191,10 +191,10 @@ def attention_tensors():
 
 
 # -------------------------------------------------------------- softmax (reference tests/test_softmax.py:10-27)
-def make_softmax():
+def make_softmax(**jit_options):
     BLOCK_SIZE = Symbol("BLOCK_SIZE", constexpr=True)
 
-    @ninetoothed.jit
+    @ninetoothed.jit(**jit_options)
     def softmax_kernel(
         input_row: Tensor(2, other=float("-inf")).tile((1, BLOCK_SIZE)),
         output_row: Tensor(2).tile((1, BLOCK_SIZE)),

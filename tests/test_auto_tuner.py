@@ -258,3 +258,44 @@ def test_tuned_attention_picks_a_kernel():
     assert torch.allclose(o.float(), ref, atol=1e-2, rtol=1e-2)
     (plan,) = h.plans()
     assert plan["family"] == "tuned" and len(plan["chosen"]) == 1 and '"attention"' in plan["chosen"][0]
+
+
+def test_softmax_and_pool_plans_expand_into_kernels():
+    import functools
+
+    sm = pg.make_softmax()
+    x = torch.empty(8, 300)
+    ctx = sm._kernel.context(dict(zip(list(sm._kernel.params), (x, x))), {"BLOCK_SIZE": 300})
+    described = [p.describe() for p in families.candidates(ctx)]
+    assert [(d["family"], d.get("config")) for d in described] == [
+        ("softmax", 1), ("softmax", 2), ("softmax", 3), ("softmax", 4), ("generic", None)]
+    pool = ninetoothed.make(functools.partial(pg.max_pool2d_arrangement, ceil_mode=False), pg.max_pool2d_application,
+                            pg.max_pool2d_tensors())
+    xi, yo = torch.empty(2, 3, 16, 16, dtype=torch.float16), torch.empty(2, 3, 8, 8, dtype=torch.float16)
+    ctx = pool._kernel.context(dict(zip(list(pool._kernel.params), (xi, yo))), {"WINDOW_HEIGHT": 2, "WINDOW_WIDTH": 2})
+    described = [p.describe() for p in families.candidates(ctx)]
+    assert [(d["family"], d.get("config")) for d in described][:2] == [("max_pool2d", 1), ("max_pool2d", 2)]
+
+
+@pytest.mark.gpu
+def test_tuned_softmax_and_pool_pick_a_kernel():
+    import functools
+
+    import torch.nn.functional as F
+
+    sm = pg.make_softmax(max_num_configs=5)
+    g = torch.Generator().manual_seed(8)
+    x = (torch.randn(64, 3000, generator=g) * 2).half().cuda()
+    y = torch.empty_like(x)
+    sm(x, y, BLOCK_SIZE=3000)
+    assert torch.allclose(y.float(), torch.softmax(x.float(), -1), atol=1e-2, rtol=1e-2)
+    (plan,) = sm.plans()
+    assert plan["family"] == "tuned" and len(plan["chosen"]) == 1
+    pool = ninetoothed.make(functools.partial(pg.max_pool2d_arrangement, ceil_mode=False), pg.max_pool2d_application,
+                            pg.max_pool2d_tensors(), max_num_configs=3)
+    xi = (torch.rand(4, 8, 64, 64, generator=g) * 2 - 1).half().cuda()
+    yo = torch.empty(4, 8, 32, 32, dtype=torch.float16, device="cuda")
+    pool(xi, yo, WINDOW_HEIGHT=2, WINDOW_WIDTH=2)
+    assert torch.equal(yo, F.max_pool2d(xi, (2, 2)))
+    (plan,) = pool.plans()
+    assert plan["family"] == "tuned" and len(plan["chosen"]) == 1

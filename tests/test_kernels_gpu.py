@@ -562,3 +562,52 @@ def test_attention_config_conditions_are_checked():
         kernels.attention(qt, k, v, o, q_scale=kernels.LOG2E, config=2)
     kernels.attention(qt, k, v, o, q_scale=kernels.LOG2E, config=3)
     assert torch.allclose(o.float(), _sdpa_ref(q, k, v, False, 1.0), atol=1e-2, rtol=1e-2)
+
+
+# Softmax kernel configurations (1, 2, 3: register path with four, eight, one wave per
+# workgroup; 4: two-sweep kernel) on whole rows, segments, an unaligned view and the
+# headline width; a configuration whose register path cannot hold the segment is refused.
+@pytest.mark.parametrize("config", (1, 2, 3, 4))
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16, torch.float32))
+@pytest.mark.parametrize("cols, block", ((8192, None), (1000, None), (33, None), (1000, 128), (5000, 777)))
+def test_softmax_configs(config, dtype, cols, block):
+    from ninetoothed_amd.errors import KernelLaunchError
+
+    x = _randn((24, cols), dtype, 11, scale=2.0)
+    blk = cols if block is None else block
+    nseg = -(-cols // blk)
+    xp = F.pad(x.float(), (0, nseg * blk - cols), value=float("-inf")).view(24, nseg, blk)
+    ref = torch.softmax(xp, dim=-1).view(24, nseg * blk)[:, :cols]
+    tol = TOL[dtype]
+    for view in (x, _randn((24, cols + 1), dtype, 12, scale=2.0)[:, 1:]):  # aligned, then off by one element
+        if view is not x:
+            xp = F.pad(view.float(), (0, nseg * blk - cols), value=float("-inf")).view(24, nseg, blk)
+            ref = torch.softmax(xp, dim=-1).view(24, nseg * blk)[:, :cols]
+        y = torch.empty(24, cols, dtype=dtype, device=DEV)
+        lanes = {1: 256, 2: 512, 3: 64}.get(config)
+        vpt_max = 16 if view is x and (cols * x.element_size()) % 16 == 0 and (blk * x.element_size()) % 16 == 0 else 8
+        if lanes is not None and min(blk, cols) > lanes * (16 // x.element_size()) * vpt_max:
+            with pytest.raises(KernelLaunchError):
+                kernels.softmax(view, y, block=block, config=config)
+            continue
+        kernels.softmax(view, y, block=block, config=config)
+        assert torch.allclose(y.float(), ref, atol=tol, rtol=tol)
+
+
+@pytest.mark.parametrize("config", (1, 2))
+def test_max_pool2d_configs(config):
+    from ninetoothed_amd.errors import KernelLaunchError
+
+    x = _rand((4, 16, 112, 112), torch.float16, 13, -1.0, 1.0)
+    y = torch.empty((4, 16, 56, 56), dtype=torch.float16, device=DEV)
+    kernels.max_pool2d(x, y, (2, 2), config=config)
+    assert torch.equal(y, F.max_pool2d(x, (2, 2)))
+    x2 = _randn((2, 5, 17, 19), torch.float16, 14)
+    ref = F.max_pool2d(x2, (3, 2), stride=(2, 3), padding=(1, 1))
+    y2 = torch.empty_like(ref)
+    if config == 1:  # the plane kernel takes 2-wide windows of stride 2 only
+        with pytest.raises(KernelLaunchError):
+            kernels.max_pool2d(x2, y2, (3, 2), stride=(2, 3), padding=(1, 1), config=1)
+    else:
+        kernels.max_pool2d(x2, y2, (3, 2), stride=(2, 3), padding=(1, 1), config=2)
+        assert torch.equal(y2, ref)
