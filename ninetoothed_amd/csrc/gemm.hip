@@ -450,50 +450,56 @@ __device__ __forceinline__ void load_lds16(u32x4 rs, uint32_t lds_addr, int voff
 }  // namespace dma
 
 // The DMA kernels' fast epilogue (16-bit out, c absent or of out's type, unit column
-// stride, 16-byte aligned rows; the launcher's c_pre).  acc holds a wave's 128 x 64 block as
-// 4 x 2 tiles of 32 x 32 (the 32x32 MFMA accumulator layout); lds + EPI + 4 KiB * wave is
-// the wave's staging.
-__device__ __forceinline__ void dma_fast_epilogue(const GemmArgs& g, const floatx16 (&acc)[4][2], char* lds, int wave,
+// stride, 16-byte aligned rows; the launcher's c_pre).  acc holds a wave's 128 x (32 WJ)
+// block as 4 x WJ tiles of 32 x 32 (the 32x32 MFMA accumulator layout); lds + EPI +
+// 2 KiB * WJ * wave is the wave's staging.
+template <int WJ = 2>
+__device__ __forceinline__ void dma_fast_epilogue(const GemmArgs& g, const floatx16 (&acc)[4][WJ], char* lds, int wave,
                                                   int lane, int64_t row_base, int64_t col_base) {
-  // Fast epilogue: the accumulators go through this wave's 4 KiB of staging (never touched
-  // by the k loop: no barrier) 16 rows at a time; a lane finishes rows t * 8 + lane / 8
-  // (t = 0, 1) at columns (lane % 8) * 8 .. + 7.  c is read through a buffer resource (the
-  // host checks its offsets fit 32 bits); c of slab i + 2 is fetched while slab i is
-  // finished.  Without c the resource has no records: the loads return zeros.
+  // Fast epilogue: the accumulators go through this wave's staging (never touched by the k
+  // loop: no barrier) 16 rows at a time; a lane finishes rows t * (64 / CPR) + lane / CPR
+  // (CPR = 4 WJ lanes per row, t < WJ) at columns (lane % CPR) * 8 .. + 7.  c is read
+  // through a buffer resource (the host checks its offsets fit 32 bits); c of slab i + 2 is
+  // fetched while slab i is finished.  Without c the resource has no records: the loads
+  // return zeros.
+  static_assert(WJ == 2 || WJ == 4, "two or four 32-wide column blocks");
+  constexpr int COLS = 32 * WJ, CPR = COLS / 8, RPP = 64 / CPR;  // lanes per row, rows per pass
+  constexpr int CPR_LOG2 = WJ == 2 ? 3 : 4;
+  const int lrow = lane >> CPR_LOG2, lcol = lane & (CPR - 1);
   const bool has_c = g.c != nullptr;
   const __amdgpu_buffer_rsrc_t rsC = __builtin_amdgcn_make_buffer_rsrc(
       has_c ? (void*)((const uint16_t*)g.c + row_base * g.sc_m + col_base) : (void*)g.a, (short)0,
-      has_c ? (int)((127 * g.sc_m + 64) * 2) : 0, 0x00020000);
-  const int vc = has_c ? (int)(((lane >> 3) * g.sc_m + (lane & 7) * 8) * 2) : 0;
+      has_c ? (int)((127 * g.sc_m + COLS) * 2) : 0, 0x00020000);
+  const int vc = has_c ? (int)((lrow * g.sc_m + lcol * 8) * 2) : 0;
   const int c_row = has_c ? (int)(g.sc_m * 2) : 0;
   // out through plain global stores: a buffer store whose data registers a VALU instruction
   // rewrote a few instructions later has been seen to store the new values on this target.
-  char* o_lane = (char*)((uint16_t*)g.out + (row_base + (lane >> 3)) * g.so_m + col_base + (lane & 7) * 8);
+  char* o_lane = (char*)((uint16_t*)g.out + (row_base + lrow) * g.so_m + col_base + lcol * 8);
   const int64_t o_row = g.so_m * 2;
-  u32x4 cv[2][2][2];
+  u32x4 cv[2][2][WJ];
   auto load_c = [&](int i) {
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
-        cv[i & 1][h][t] = __builtin_amdgcn_raw_buffer_load_b128(rsC, vc, (i * 32 + h * 16 + t * 8) * c_row, 0);
+      for (int t = 0; t < WJ; ++t)
+        cv[i & 1][h][t] = __builtin_amdgcn_raw_buffer_load_b128(rsC, vc, (i * 32 + h * 16 + t * RPP) * c_row, 0);
   };
-  float* stage = (float*)(lds + dma::EPI + wave * 4096);
+  float* stage = (float*)(lds + dma::EPI + wave * (2048 * WJ));
   auto finish = [&](auto out_f16_c, auto round_c, int i, int h) {
     constexpr bool OUT_F16 = decltype(out_f16_c)::value;
     constexpr int ROUND = decltype(round_c)::value;
     wave_lds_order();  // the previous half's reads come first
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < WJ; ++j)
 #pragma unroll
       for (int r = 8 * h; r < 8 * h + 8; ++r)
-        stage[(acc_row(r, lane) - 16 * h) * 64 + j * 32 + (lane & 31)] = acc[i][j][r];
+        stage[(acc_row(r, lane) - 16 * h) * COLS + j * 32 + (lane & 31)] = acc[i][j][r];
     wave_lds_order();  // every lane's writes before any lane reads
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int rr = t * 8 + (lane >> 3), cg = (lane & 7) * 8;
-      const float4 v0 = *(const float4*)(stage + rr * 64 + cg);
-      const float4 v1 = *(const float4*)(stage + rr * 64 + cg + 4);
+    for (int t = 0; t < WJ; ++t) {
+      const int rr = t * RPP + lrow, cg = lcol * 8;
+      const float4 v0 = *(const float4*)(stage + rr * COLS + cg);
+      const float4 v1 = *(const float4*)(stage + rr * COLS + cg + 4);
       const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
       const u32x4 cw = cv[i & 1][h][t];
       u32x4 ow;
@@ -514,7 +520,7 @@ __device__ __forceinline__ void dma_fast_epilogue(const GemmArgs& g, const float
         ow[d] = OUT_F16 ? ((uint32_t)float_to_f16_bits(r2[0]) | ((uint32_t)float_to_f16_bits(r2[1]) << 16))
                         : ((uint32_t)float_to_bf16_bits(r2[0]) | ((uint32_t)float_to_bf16_bits(r2[1]) << 16));
       }
-      __builtin_nontemporal_store(ow, (u32x4*)(o_lane + (i * 32 + h * 16 + t * 8) * o_row));  // not re-read: no L2 allocation
+      __builtin_nontemporal_store(ow, (u32x4*)(o_lane + (i * 32 + h * 16 + t * RPP) * o_row));  // not re-read: no L2 allocation
     }
   };
   using OutF16 = std::integral_constant<bool, true>;

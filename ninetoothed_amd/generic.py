@@ -931,10 +931,72 @@ class _TileEmitter(_Emitter):
         self.plan.raw_reads.add(name)
 
 
+def _lower_dots(program):
+    """The program with every ``ntl.dot`` of two tiles rewritten as an fp32 reduction.
+
+    ``dot(x, y)`` of an [m, k] and a [k, n] tile is ``sum(x[:, :, None] * y[None, :, :],
+    axis=1)`` with both operands first cast to float32 (the reference's ``tl.dot``
+    accumulates in fp32 and returns fp32 for 16- and 32-bit floats: reference
+    src/ninetoothed/backends/emitters/ssa.py:1455-1542).  A transposed operand takes the
+    product in another axis order, so that no value is transposed: ``dot(x, trans(w))``
+    with w [n, k] is ``sum(x[:, None, :] * w[None, :, :], axis=2)`` and ``dot(trans(u), y)``
+    with u [k, m] is ``sum(u[:, :, None] * y[:, None, :], axis=0)``.  ``dot`` of two
+    transposed operands raises ``LoweringError``."""
+    roots = list(program.stores.values())
+    for eff in program.effects:
+        roots += [a for a in eff[1:] if isinstance(a, Value)] + [x for a in eff[1:] if isinstance(a, tuple)
+                                                                    for x in a if isinstance(x, Value)]
+    if not any(v.op == "dot" for v in _walk(roots)):
+        return program
+    f32 = Value("dtype", ("float32",))
+    done = {}
+
+    def rebuild(v):
+        if not isinstance(v, Value):
+            if isinstance(v, tuple):
+                return tuple(rebuild(x) for x in v)
+            return v
+        if id(v) in done:
+            return done[id(v)]
+        if v.op == "dot":
+            x, y = v.args
+            tx, ty = x.op == "trans", y.op == "trans"
+            if tx and ty:
+                raise LoweringError("`dot` of two transposed tiles is not supported by the generic kernels")
+            cx = Value("cast", (rebuild(x.args[0] if tx else x), f32))
+            cy = Value("cast", (rebuild(y.args[0] if ty else y), f32))
+            if ty:
+                prod = Value("mul", (Value("bcast", (cx, (":", None, ":"))), Value("bcast", (cy, (None, ":", ":")))))
+                axis = 2
+            elif tx:
+                prod = Value("mul", (Value("bcast", (cx, (":", ":", None))), Value("bcast", (cy, (":", None, ":")))))
+                axis = 0
+            else:
+                prod = Value("mul", (Value("bcast", (cx, (":", ":", None))), Value("bcast", (cy, (None, ":", ":")))))
+                axis = 1
+            out = Value("reduce", ("sum", prod, axis))
+        else:
+            args = tuple(rebuild(a) for a in v.args)
+            out = v if all(a is b for a, b in zip(args, v.args)) else Value(v.op, args)
+        done[id(v)] = out
+        return out
+
+    lowered = copy.copy(program)
+    lowered.stores = {k: rebuild(v) for k, v in program.stores.items()}
+    lowered.effects = [tuple(rebuild(a) for a in eff) for eff in program.effects]
+    return lowered
+
+
 def _analyse_tile(ctx):
+    """(ctx, stores, values) of a tile program (ctx a copy whose program has its dots
+    lowered, when it has any), or None."""
     program = ctx.program
     if program.loops:
         return None
+    program = _lower_dots(program)
+    if program is not ctx.program:
+        ctx = copy.copy(ctx)
+        ctx.program = program
     stores = program.stores
     roots = list(stores.values())
     for eff in program.effects:
@@ -980,7 +1042,7 @@ def _analyse_tile(ctx):
     # one flat program id, unravelled by every tensor over its own outermost level
     if len({int(np.prod(ctx.views[n].level_shapes[0])) for n in tensors}) > 1:
         raise LoweringError("the arranged tensors have different numbers of programs")
-    return stores, values
+    return ctx, stores, values
 
 
 class TilePlan(GenericPlan):
@@ -1311,7 +1373,7 @@ def match_generic(ctx):
         return GenericPlan(ctx, *found)
     found = _analyse_tile(ctx)
     if found is not None:
-        return TilePlan(ctx, *found)
+        return TilePlan(*found)
     if ctx.program.loops and ctx.relower is not None:
         # loops whose trip counts are known now: unrolled, the program may be a tile program
         resolve = _Emitter(ctx).const_value
@@ -1326,5 +1388,5 @@ def match_generic(ctx):
             unrolled.program = program
             found = _analyse_tile(unrolled)
             if found is not None:
-                return TilePlan(unrolled, *found)
+                return TilePlan(*found)
     return None

@@ -766,3 +766,65 @@ def test_two_d_tiled_elementwise():
     xt = torch.randn(90, 70, device="cuda").t()
     k(xt, y, out)
     assert torch.equal(out, xt * 2.0 + y)
+
+
+# ------------------------------------------------------------------ dot in tile programs
+# ``ntl.dot`` outside a GEMM loop: a tile program runs it as an fp32 reduction over the
+# shared axis of a broadcast product (as the reference's ``tl.dot``, fp32 accumulation).
+DOT_BM = Symbol("DOT_BM", constexpr=True)
+
+
+def dot_arrangement(x, w, o):
+    xt = x.tile((DOT_BM, -1))
+    return xt, w.tile((-1, -1)).expand((xt.shape[0], -1)), o.tile((DOT_BM, -1))
+
+
+def dot_rows_arrangement(x, w, o):
+    xt = x.tile((DOT_BM, -1))
+    return xt, w.tile((-1, -1)).expand((xt.shape[0], -1)), o.tile((DOT_BM,))
+
+
+def dot_application(x, w, o):
+    o = ntl.dot(x, w)  # noqa: F841
+
+
+def dot_trans_application(x, w, o):
+    o = ntl.dot(x, ntl.trans(w)) * 0.5 + 1.0  # noqa: F841
+
+
+def dot_row_sum_application(x, w, o):
+    o = ntl.sum(ntl.dot(x, w), axis=1)  # noqa: F841
+
+
+def test_dot_tile_programs_compile():
+    cases = ((dot_arrangement, dot_application, ((64, 40), (40, 24), (64, 24))),
+             (dot_arrangement, dot_trans_application, ((64, 40), (24, 40), (64, 24))),
+             (dot_rows_arrangement, dot_row_sum_application, ((64, 40), (40, 24), (64,))))
+    for arrangement, application, shapes in cases:
+        h = ninetoothed.make(arrangement, application, tuple(Tensor(len(s)) for s in shapes))
+        plan = _plan(h, *(torch.empty(s) for s in shapes), DOT_BM=16)
+        assert plan.describe()["family"] == "generic" and plan.describe()["reductions"] >= 1
+        assert len(GenericPlan.compile(plan.source())) > 1000
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16, torch.float32))
+def test_dot_tile_programs(dtype):
+    tol = 1e-2 if dtype != torch.float32 else 1e-4
+    g = torch.Generator().manual_seed(21)
+    x = (torch.randn(64, 40, generator=g) / 4).to(dtype).cuda()
+    w = (torch.randn(40, 24, generator=g) / 4).to(dtype).cuda()
+    ref = x.float() @ w.float()
+    # dot alone, and with an epilogue on a transposed operand
+    o = torch.empty(64, 24, dtype=dtype, device="cuda")
+    ninetoothed.make(dot_arrangement, dot_application, (Tensor(2), Tensor(2), Tensor(2)))(x, w, o, DOT_BM=16)
+    torch.testing.assert_close(o.float(), ref, rtol=tol, atol=tol)
+    wt = w.t().contiguous()
+    o2 = torch.empty(64, 24, dtype=torch.float32, device="cuda")
+    ninetoothed.make(dot_arrangement, dot_trans_application, (Tensor(2), Tensor(2), Tensor(2)))(x, wt, o2, DOT_BM=32)
+    torch.testing.assert_close(o2, ref * 0.5 + 1.0, rtol=tol, atol=tol)
+    # dot then a reduction of its result (row sums)
+    rows = torch.empty(64, dtype=torch.float32, device="cuda")
+    ninetoothed.make(dot_rows_arrangement, dot_row_sum_application, (Tensor(2), Tensor(2), Tensor(1)))(x, w, rows,
+                                                                                                      DOT_BM=16)
+    torch.testing.assert_close(rows, ref.sum(dim=1), rtol=tol, atol=tol * 8)
