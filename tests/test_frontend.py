@@ -113,14 +113,26 @@ def test_reduction_program_is_generic():
     assert _specialize(h, torch.empty(10), torch.empty(10), torch.empty(10))["family"] == "generic"
 
 
-def test_unsupported_program_is_rejected():
-    # a block product without the k loop of a matmul: neither the GEMM family nor the generic kernels
+def test_block_product_without_k_loop_is_a_tile_program():
+    # a block product without the k loop of a matmul is no GEMM; the generic tile kernels
+    # take it (ntl.dot as an fp32 reduction)
     def app(lhs, rhs, output):
         output = ntl.dot(lhs, rhs)  # noqa: F841
 
     h = ninetoothed.make(lambda a, b, c: (a.tile((16, 16)), b.tile((16, 16)), c.tile((16, 16))), app,
                          (Tensor(2), Tensor(2), Tensor(2)))
-    with pytest.raises(LoweringError, match="matches none"):
+    described = _specialize(h, _h((16, 16)), _h((16, 16)), _h((16, 16)))
+    assert described["family"] == "generic" and described["reductions"] == 1
+
+
+def test_unsupported_program_is_rejected():
+    # dot of two transposed tiles: neither the GEMM family nor the generic kernels
+    def app(lhs, rhs, output):
+        output = ntl.dot(ntl.trans(lhs), ntl.trans(rhs))  # noqa: F841
+
+    h = ninetoothed.make(lambda a, b, c: (a.tile((16, 16)), b.tile((16, 16)), c.tile((16, 16))), app,
+                         (Tensor(2), Tensor(2), Tensor(2)))
+    with pytest.raises(LoweringError, match="two transposed"):
         _specialize(h, _h((16, 16)), _h((16, 16)), _h((16, 16)))
 
 
@@ -165,9 +177,14 @@ def test_overlapping_k_tiles_are_rejected():
         rt.dtype = rt.dtype.squeeze(1)
         return lt, rt, out
 
+    from ninetoothed_amd import families
+
     h = ninetoothed.make(overlap, pg.matmul_application, pg.matmul_tensors())
+    ctx = h._kernel.context(dict(zip(h._abi["public_args"], (_h((32, 48)), _h((48, 64)), _h((32, 64))))), {})
     with pytest.raises(LoweringError, match="exactly once|disagree"):
-        _specialize(h, _h((32, 48)), _h((48, 64)), _h((32, 64)))
+        families.match_gemm(ctx)
+    # the generic tile kernels take it as written (the loop unrolled, each dot a reduction)
+    assert _specialize(h, _h((32, 48)), _h((48, 64)), _h((32, 64)))["family"] == "generic"
 
 
 # ---------------------------------------------------------------- call contract

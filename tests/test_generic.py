@@ -828,3 +828,31 @@ def test_dot_tile_programs(dtype):
     ninetoothed.make(dot_rows_arrangement, dot_row_sum_application, (Tensor(2), Tensor(2), Tensor(1)))(x, w, rows,
                                                                                                       DOT_BM=16)
     torch.testing.assert_close(rows, ref.sum(dim=1), rtol=tol, atol=tol * 8)
+
+
+@pytest.mark.gpu
+def test_overlapping_k_tiles_matmul_runs_as_written():
+    # k-tiles of size 16 at stride 8 (each k visited twice, the last tiles masked past K):
+    # not a GEMM, so the generic kernels run the loop as the program states.
+    import programs as pg
+
+    def overlap(lhs, rhs, output, BM=16, BN=16, BK=16):
+        out = output.tile((BM, BN))
+        lt = lhs.tile((BM, BK), strides=(-1, 8)).tile((1, -1)).expand((-1, out.shape[1]))
+        lt.dtype = lt.dtype.squeeze(0)
+        rt = rhs.tile((BK, BN), strides=(8, -1)).tile((-1, 1)).expand((out.shape[0], -1))
+        rt.dtype = rt.dtype.squeeze(1)
+        return lt, rt, out
+
+    g = torch.Generator().manual_seed(22)
+    a = (torch.randn(32, 48, generator=g) / 4).half().cuda()
+    b = (torch.randn(48, 64, generator=g) / 4).half().cuda()
+    out = torch.empty(32, 64, dtype=torch.float16, device="cuda")
+    ninetoothed.make(overlap, pg.matmul_application, pg.matmul_tensors())(a, b, out)
+    from oracle import apply
+
+    # the oracle evaluates the same arrangement: five k-tiles, at k = 0, 8, ..., 32
+    ref = apply.matmul(a.float().cpu().numpy(), b.float().cpu().numpy(), "float16", overlap, block=(16, 16, 16))
+    torch.testing.assert_close(out.float().cpu(), torch.from_numpy(ref), rtol=1e-2, atol=1e-2)
+    five = sum(a[:, 8 * t:8 * t + 16].float() @ b[8 * t:8 * t + 16, :].float() for t in range(5))
+    torch.testing.assert_close(out.float(), five.half().float(), rtol=1e-2, atol=1e-2)
