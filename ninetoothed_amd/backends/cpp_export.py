@@ -11,8 +11,14 @@ application's parameter order; 0-d parameters point at a host scalar of their de
 dtype (``double`` for floating types).  The launcher checks every rank, shape and stride
 against the specialisation (the plan was fitted to them) and returns NT_ERR_INVALID before
 launching anything when one differs; an empty output returns 0.  It then calls the plan's
-entry point of ``libnt_mi355x.so``, which it links.  The generic kernels (compiled at run
-time) are not exported.
+entry point of ``libnt_mi355x.so``, which it links.
+
+A generic kernel's launcher embeds its code object (compiled for gfx950 by hipRTC at build
+time) and its index tables (fixed by the specialisation's shapes and strides).  On its first
+call on a device it loads the code object (``nt_rtc_load``) and copies the tables to that
+device once (they stay allocated until the process ends); every call then launches through
+``nt_rtc_launch`` with the kernel arguments the Python binding passes.  Tables above
+MAX_TABLE_BYTES are not embedded (no launcher).
 """
 
 import math
@@ -60,6 +66,9 @@ typedef int NineToothedResult;
 
 _SCALAR_C = {"float16": "double", "bfloat16": "double", "float32": "double", "float64": "double",
              "int8": "int8_t", "int16": "int16_t", "int32": "int32_t", "int64": "int64_t", "uint8": "uint8_t"}
+
+
+MAX_TABLE_BYTES = 16 << 20
 
 
 class Unsupported(Exception):
@@ -220,19 +229,82 @@ def source(kernel_name, plan, kernel, values, outputs):
         nulls.append(f"{t}.data == nullptr")
         if name in outputs and math.prod(v.shape) == 0:
             empty.append("true")
-    call = _call_for(plan, values, scalar_expr, index)
     params = ", ".join(["NineToothedStream stream"] + [f"NineToothedTensor tensor_{i}" for i in range(len(names))])
     body = [f"  if ({c}) return NT_ERR_INVALID;" for c in checks]
     if empty:
         body.append("  return 0;  // an empty output: nothing to launch")
     body.append(f"  if ({' || '.join(nulls) or 'false'}) return NT_ERR_INVALID;")
-    body += reads + call.arrays
-    body.append(f"  return {call.entry}({', '.join(call.args + ['static_cast<hipStream_t>(stream)'])});")
+    body += reads
+    prelude = ""
+    if plan.describe()["family"] == "generic":
+        prelude, launch = _generic_launch(plan, values, index)
+        body += launch
+    else:
+        call = _call_for(plan, values, scalar_expr, index)
+        body += call.arrays
+        body.append(f"  return {call.entry}({', '.join(call.args + ['static_cast<hipStream_t>(stream)'])});")
     return (
         "// Standalone launcher of an AOT-built NineToothed kernel for the MI355X backend.\n"
-        '#include "ninetoothed.h"\n#include "nt_mi355x.h"\n\n'
-        f'extern "C" NineToothedResult launch_{kernel_name}({params}) {{\n' + "\n".join(body) + "\n}\n"
+        '#include "ninetoothed.h"\n#include "nt_mi355x.h"\n\n' + prelude
+        + f'extern "C" NineToothedResult launch_{kernel_name}({params}) {{\n' + "\n".join(body) + "\n}\n"
     )
+
+
+def _bytes_c(data, per_line=24):
+    items = [f"0x{b:02x}" for b in data]
+    return ",\n".join(", ".join(items[i:i + per_line]) for i in range(0, len(items), per_line))
+
+
+def _generic_launch(plan, values, index):
+    """(file-scope code, launcher body lines) of a generic kernel plan on the static ``values``."""
+    from ninetoothed_amd.generic import GenericPlan
+
+    spec = plan.launch_spec(values)
+    if spec is None:
+        return "", ["  return 0;  // the program stores nothing"]
+    source, grid, args = spec
+    tables = [a[1] for a in args if a[0] == "table" and a[1] is not None]
+    if sum(t.nbytes for t in tables) > MAX_TABLE_BYTES:
+        raise Unsupported(f"the generic kernel's index tables exceed {MAX_TABLE_BYTES} bytes")
+    code = GenericPlan.code_object(source)
+    lines = ["#include <hip/hip_runtime.h>", "#include <mutex>", "", "namespace {",
+             f"const unsigned char kCode[{len(code)}] = {{\n{_bytes_c(code)}}};"]
+    for i, t in enumerate(tables):
+        vals = ", ".join(str(int(x)) for x in t.tolist())
+        lines.append(f"const int32_t kTable{i}[{t.size}] = {{{vals}}};")
+    n_tab = len(tables)
+    lines += [
+        "// Per device: the loaded kernel and the device copies of the tables (kept until exit).",
+        "struct Loaded {", "  void* fn = nullptr;", f"  void* tab[{max(n_tab, 1)}] = {{}};", "  int status = -1;", "};",
+        "Loaded g_loaded[64];", "std::mutex g_lock;", "int prepare(Loaded& d) {",
+        f'  int s = nt_rtc_load(kCode, "{plan.kernel_name}", &d.fn);', "  if (s) return s;"]
+    for i, t in enumerate(tables):
+        lines += [f"  s = (int)hipMalloc(&d.tab[{i}], sizeof(kTable{i}));", "  if (s) return s;",
+                  f"  s = (int)hipMemcpy(d.tab[{i}], kTable{i}, sizeof(kTable{i}), hipMemcpyHostToDevice);",
+                  "  if (s) return s;"]
+    lines += ["  return 0;", "}", "}  // namespace", ""]
+    body = ["  int dev = 0;", "  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return NT_ERR_INVALID;",
+            "  Loaded& d = g_loaded[dev];", "  {", "    std::lock_guard<std::mutex> guard(g_lock);",
+            "    if (d.status < 0) d.status = prepare(d);", "  }", "  if (d.status) return d.status;"]
+    names, k = [], 0
+    for i, a in enumerate(args):
+        if a[0] == "table":
+            if a[1] is None:
+                body.append(f"  void* k{i} = nullptr;")
+            else:
+                body.append(f"  void* k{i} = d.tab[{k}];")
+                k += 1
+        elif a[0] == "tensor":
+            body.append(f"  void* k{i} = tensor_{index[a[1]]}.data;")
+        elif a[0] == "scalar":
+            ctype = "long long" if a[2] == "int64" else "float"
+            body.append(f"  {ctype} k{i} = ({ctype})s_{a[1]};")
+        else:
+            body.append(f"  long long k{i} = {int(a[1])}LL;")
+        names.append(f"&k{i}")
+    body.append(f"  void* argv[] = {{{', '.join(names)}}};")
+    body.append(f"  return nt_rtc_launch(d.fn, {int(grid)}u, 256u, argv, static_cast<hipStream_t>(stream));")
+    return "\n".join(lines) + "\n", body
 
 
 def build(kernel_name, code, output_dir):

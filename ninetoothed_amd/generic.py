@@ -601,42 +601,63 @@ class GenericPlan:
                 offset_tables[(n, d)] = q
         return tables, linear, linear_offsets, offset_tables, total
 
+    def launch_spec(self, values):
+        """One launch of this plan on ``values``: (kernel source, grid, kernel arguments in
+        parameter order), or None when the program stores nothing.  An argument is ("table",
+        int32 array, or None for a tensor walked linearly), ("tensor", name), ("scalar", name,
+        "int64" or "float32") or ("i64", value)."""
+        if not self.index_names:
+            return None
+        host_tables, linear, linear_offsets, host_offsets, total = self._layout(values)
+        args = [("table", host_tables.get(n)) for n in self.index_names]
+        args += [("table", host_offsets.get(k)) for k in self.offsets]
+        args += [("tensor", n) for n in self.loaded if n not in self.outputs]
+        args += [("tensor", n) for n in self.outputs]
+        args += [("scalar", n, "int64" if self.scalar_types[n] == "int64" else "float32") for n in self.scalars]
+        args.append(("i64", total))
+        grid = max(1, min((total + 255) // 256, 256 * 64)) if total else 0
+        return self.source(linear, linear_offsets), grid, args
+
     def bind(self, values, index):
         import torch
 
-        if not self.index_names:  # nothing is stored: the program has no effect
+        spec = self.launch_spec(values)
+        if spec is None:  # nothing is stored: the program has no effect
             return lambda args: None
-        host_tables, linear, linear_offsets, host_offsets, total = self._layout(values)
-        device = values[self.index_names[0]].device
-        tables = {n: torch.from_numpy(t).to(device) for n, t in host_tables.items()}
-        offset_tables = {k: torch.from_numpy(q).to(device) for k, q in host_offsets.items()}
-        fn = self.function(self.source(linear, linear_offsets))
-        ptrs = {n: ctypes.c_void_p() for n in self.index_names}
-        argv = [ctypes.c_void_p(tables[n].data_ptr() if n in tables else None) for n in self.index_names]
-        argv += [ctypes.c_void_p(offset_tables[k].data_ptr() if k in offset_tables else None) for k in self.offsets]
-        argv += [ptrs[n] for n in self.loaded if n not in self.outputs]
-        argv += [ptrs[n] for n in self.outputs]
-        svals = {n: ctypes.c_int64() if self.scalar_types[n] == "int64" else ctypes.c_float() for n in self.scalars}
-        argv += [svals[n] for n in self.scalars]
-        argv.append(ctypes.c_int64(total))
+        source, grid, spec_args = spec
+        device = next(values[a[1]].device for a in spec_args if a[0] == "tensor")
+        fn = self.function(source)
+        tables, argv, ptrs, svals = [], [], [], {}
+        for a in spec_args:
+            if a[0] == "table":
+                t = torch.from_numpy(a[1]).to(device) if a[1] is not None else None
+                tables.append(t)
+                argv.append(ctypes.c_void_p(t.data_ptr() if t is not None else None))
+            elif a[0] == "tensor":
+                slot = ctypes.c_void_p()
+                ptrs.append((index[a[1]], slot))
+                argv.append(slot)
+            elif a[0] == "scalar":
+                slot = ctypes.c_int64() if a[2] == "int64" else ctypes.c_float()
+                svals[a[1]] = (index[a[1]], slot, a[2])
+                argv.append(slot)
+            else:
+                argv.append(ctypes.c_int64(a[1]))
         params = (ctypes.c_void_p * len(argv))(*[ctypes.addressof(a) for a in argv])
-        grid = max(1, min((total + 255) // 256, 256 * 64)) if total else 0
         lib = _lib.load()
-        positions = {n: index[n] for n in self.index_names}
-        spos = {n: index[n] for n in self.scalars}
 
         def launch(args):
-            for n, p in positions.items():
-                ptrs[n].value = args[p].data_ptr()
-            for n, p in spos.items():
+            for p, slot in ptrs:
+                slot.value = args[p].data_ptr()
+            for p, slot, kind in svals.values():
                 v = args[p]
                 v = v.item() if hasattr(v, "item") else v
-                svals[n].value = int(v) if self.scalar_types[n] == "int64" else float(v)
+                slot.value = int(v) if kind == "int64" else float(v)
             status = lib.nt_rtc_launch(fn, grid, 256, params, ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream))
             if status != 0:
                 raise KernelLaunchError(status)
 
-        launch.keep = (tables, offset_tables, argv, params)  # device tables and the argument block live with the launcher
+        launch.keep = (tables, argv, params)  # device tables and the argument block live with the launcher
         return launch
 
     def run(self, values):
@@ -1306,46 +1327,20 @@ class TilePlan(GenericPlan):
         return {"family": self.family, "outputs": self.outputs, "inputs": self.loaded, "scalars": self.scalars,
                 "reductions": len(self.lds)}
 
-    def bind(self, values, index):
-        import torch
-
-        device = next(values[n].device for n in self.index_names + self.raw + [k[0] for k in self.offsets])
-        tables, offset_tables, maps = {}, {}, {}
+    def launch_spec(self, values):
+        """As GenericPlan.launch_spec: the tables, the tensors (loaded, stored, read through
+        pointers), the scalars and the number of programs."""
+        maps, args = {}, []
         for n in self.index_names:
             maps[n] = self._maps(n)
-            tab, _ = self._table(n, values[n], maps[n])
-            tables[n] = torch.from_numpy(tab).to(device)
-        for n, d in self.offsets:
-            offset_tables[(n, d)] = torch.from_numpy(self._tile_offsets(n, d, maps.get(n))).to(device)
-        fn = self.function(self.source())
-        ptrs = {n: ctypes.c_void_p() for n in self.index_names + self.raw}
-        argv = [ctypes.c_void_p(tables[n].data_ptr()) for n in self.index_names]
-        argv += [ctypes.c_void_p(offset_tables[k].data_ptr()) for k in self.offsets]
-        argv += [ptrs[n] for n in self.loaded]
-        argv += [ptrs[n] for n in self.outputs + self.view_targets]
-        argv += [ptrs[n] for n in self.raw]
-        svals = {n: ctypes.c_int64() if self.scalar_types[n] == "int64" else ctypes.c_float() for n in self.scalars}
-        argv += [svals[n] for n in self.scalars]
-        argv.append(ctypes.c_int64(self.programs))
-        params = (ctypes.c_void_p * len(argv))(*[ctypes.addressof(a) for a in argv])
-        grid = min(self.programs, 256 * 64)
-        lib = _lib.load()
-        positions = {n: index[n] for n in self.index_names + self.raw}
-        spos = {n: index[n] for n in self.scalars}
-
-        def launch(args):
-            for n, p in positions.items():
-                ptrs[n].value = args[p].data_ptr()
-            for n, p in spos.items():
-                v = args[p]
-                v = v.item() if hasattr(v, "item") else v
-                svals[n].value = int(v) if self.scalar_types[n] == "int64" else float(v)
-            status = lib.nt_rtc_launch(fn, grid, 256, params, ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream))
-            if status != 0:
-                raise KernelLaunchError(status)
-
-        launch.keep = (tables, offset_tables, argv, params)
-        return launch
+            args.append(("table", self._table(n, values[n], maps[n])[0]))
+        args += [("table", self._tile_offsets(n, d, maps.get(n))) for n, d in self.offsets]
+        args += [("tensor", n) for n in self.loaded]
+        args += [("tensor", n) for n in self.outputs + self.view_targets]
+        args += [("tensor", n) for n in self.raw]
+        args += [("scalar", n, "int64" if self.scalar_types[n] == "int64" else "float32") for n in self.scalars]
+        args.append(("i64", self.programs))
+        return self.source(), min(self.programs, 256 * 64), args
 
     def _tile_offsets(self, name, dim, maps=None):
         """``offsets(dim)`` per program: the source index along ``dim`` of the tile's elements

@@ -210,12 +210,24 @@ def test_cpp_launcher_is_built_and_checks_its_arguments(tmp_path):
 
 
 def test_cpp_launcher_reasons_are_recorded(tmp_path):
-    # symbolic shapes, and a generic kernel: no launcher, with the reason in the manifest
+    # symbolic shapes: no launcher, with the reason in the manifest
     h = ninetoothed.make(lambda x, y, o: (x.tile((64,)), y.tile((64,)), o.tile((64,))), _add_app(), (
         Tensor(1), Tensor(1), Tensor(1)), caller="hip", output_dir=tmp_path / "sym")
     assert "not all fixed" in json.loads(Path(h._built_artifact.manifest_path).read_text())["cpp"]["unavailable"]
+
+
+def test_generic_kernel_launcher_is_built_and_checks_its_arguments(tmp_path):
+    # a generic kernel's launcher embeds its code object (and index tables, if any)
     h = DEFAULT_COMPILER.materialize(_pow_kernel(), output_dir=tmp_path / "pow", mode="aot")
-    assert "generic" in json.loads(Path(h._built_artifact.manifest_path).read_text())["cpp"]["unavailable"]
+    cpp = json.loads(Path(h._built_artifact.manifest_path).read_text())["cpp"]
+    assert cpp["symbol"] == "launch_pow_static" and Path(cpp["library"]).is_file()
+    assert "kCode[" in Path(cpp["source"]).read_text()
+    fn = getattr(ctypes.CDLL(cpp["library"]), cpp["symbol"])
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p] + [NineToothedTensor] * 3
+    keep = []
+    x, bad = torch.empty(1000), torch.empty(999)
+    assert fn(None, _nt_tensor(x, keep), _nt_tensor(x, keep), _nt_tensor(bad, keep)) == 1  # rejected unlaunched
 
 
 def _add_app():
@@ -261,3 +273,46 @@ def test_cpp_launchers_compute(tmp_path):
     torch.cuda.synchronize()
     ref = 0.5 * inp.float() + 2.0 * (a.float() @ b.float()).half().float()
     assert torch.allclose(out.float(), ref, atol=1e-1, rtol=1e-2)
+
+
+@pytest.mark.gpu
+def test_generic_kernel_launchers_compute(tmp_path):
+    # an element-parallel program (libdevice.pow) and a tile program with index tables
+    # (dot + a reduction), each through its standalone launcher
+    h = DEFAULT_COMPILER.materialize(_pow_kernel(), output_dir=tmp_path / "pow", mode="aot")
+    cpp = json.loads(Path(h._built_artifact.manifest_path).read_text())["cpp"]
+    fn = getattr(ctypes.CDLL(cpp["library"]), cpp["symbol"])
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p] + [NineToothedTensor] * 3
+    x, e = torch.rand(1000, device="cuda"), torch.rand(1000, device="cuda")
+    out = torch.empty_like(x)
+    keep = []
+    stream = torch.cuda.current_stream().cuda_stream
+    assert fn(stream, _nt_tensor(x, keep), _nt_tensor(e, keep), _nt_tensor(out, keep)) == 0
+    torch.cuda.synchronize()
+    assert torch.allclose(out, torch.pow(x, e))
+
+    def arrangement(x, w, o):
+        xt = x.tile((16, -1))
+        return xt, w.tile((-1, -1)).expand((xt.shape[0], -1)), o.tile((16,))
+
+    def application(x, w, o):
+        o = ntl.sum(ntl.dot(x, w), axis=1)  # noqa: F841
+
+    f16, f32 = ninetoothed.float16, ninetoothed.float32
+    tensors = (Tensor(shape=(64, 40), dtype=f16), Tensor(shape=(40, 24), dtype=f16), Tensor(shape=(64,), dtype=f32))
+    h = DEFAULT_COMPILER.materialize(_compile(application, arrangement, tensors, "dot_rows_static"),
+                                     output_dir=tmp_path / "dot", mode="aot")
+    cpp = json.loads(Path(h._built_artifact.manifest_path).read_text())["cpp"]
+    assert "kTable0" in Path(cpp["source"]).read_text()
+    fn = getattr(ctypes.CDLL(cpp["library"]), cpp["symbol"])
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p] + [NineToothedTensor] * 3
+    a = (torch.randn(64, 40, device="cuda") / 4).half()
+    w = (torch.randn(40, 24, device="cuda") / 4).half()
+    rows = torch.empty(64, device="cuda")
+    for _ in range(2):  # the second call reuses the loaded kernel and the device tables
+        rows.fill_(float("nan"))
+        assert fn(stream, _nt_tensor(a, keep), _nt_tensor(w, keep), _nt_tensor(rows, keep)) == 0
+        torch.cuda.synchronize()
+        assert torch.allclose(rows, (a.float() @ w.float()).sum(dim=1), atol=1e-3, rtol=1e-3)
