@@ -999,7 +999,8 @@ def candidates(ctx):
     eight-wave, four-wave), a softmax plan for each softmax kernel (register path with four,
     eight or one wave per workgroup, two-sweep) and a max_pool2d plan for each pooling kernel
     (plane, element-wise): configurations the call's
-    operands do not admit fail when bound or launched and drop out of the timing."""
+    operands do not admit fail when bound or launched and drop out of the timing.  A generic
+    tile program with real loops is a candidate only where no other plan fits."""
     from ninetoothed_amd import kernels
 
     plans = []
@@ -1020,6 +1021,10 @@ def candidates(ctx):
             plans.extend(plan.with_config(cfg) for cfg in kernels.POOL_CONFIGS)
         elif plan is not None:
             plans.append(plan)
+    # a generic tile program that runs real loops is the fallback for programs no hand-written
+    # kernel fits; beside one it is no candidate (timing it would only slow the tuning down)
+    if any(p.family != "generic" for p in plans):
+        plans = [p for p in plans if getattr(p, "nest", None) is None]
     return plans
 
 

@@ -57,6 +57,8 @@ class Loop:
     trip: Value
     init: dict = field(default_factory=dict)
     update: dict = field(default_factory=dict)
+    parent: int = None  # id of the symbolic loop whose body holds this one
+    effects: tuple = (0, 0)  # [start, end) of the program's effects recorded in the body
 
 
 @dataclass
@@ -182,6 +184,7 @@ class Lowerer:
         self.store_order = []
         self.effects = []
         self._loop_ids = 0
+        self._loop_stack = []  # ids of the symbolic loops being lowered, outermost first
         self.application = application
 
     # ----------------------------------------------------------------- driver
@@ -369,7 +372,7 @@ class Lowerer:
         assigned = _assigned_names(s.body)
         carried = [n for n in sorted(assigned) if n in frame.env and not isinstance(frame.env[n], (_Alias,))]
         alias_carried = [n for n in sorted(assigned) if isinstance(frame.env.get(n), _Alias) and frame.env[n].kind == "local"]
-        loop = Loop(loop_id, s.target.id, trip)
+        loop = Loop(loop_id, s.target.id, trip, parent=self._loop_stack[-1] if self._loop_stack else None)
         saved = {}
         for n in carried:
             loop.init[n] = frame.env[n]
@@ -380,7 +383,13 @@ class Lowerer:
             loop.init[n] = a.frame.env[a.name]
             a.frame.env[a.name] = self.b.make("carried", loop_id, n)
         frame.env[s.target.id] = self.b.make("loop_index", loop_id)
-        self._block(frame, s.body)
+        start = len(self.effects)
+        self._loop_stack.append(loop_id)
+        try:
+            self._block(frame, s.body)
+        finally:
+            self._loop_stack.pop()
+        loop.effects = (start, len(self.effects))
         for n in carried:
             loop.update[n] = frame.env[n]
             frame.env[n] = self.b.make("loop_out", loop_id, n)

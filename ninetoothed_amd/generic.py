@@ -25,16 +25,21 @@ and tile levels together) with one lane per element:
   * the source is compiled for gfx950 once per distinct text with hipRTC and launched
     through ``nt_rtc_*`` of libnt_mi355x.so.
 
-Programs with reductions (``ntl.sum/max/min``), broadcasting subscripts, ``offsets``
-index vectors, source pointers and gathers, or loops over tile levels run as tile programs
-(``TilePlan``, below): one workgroup per program instance, reductions through LDS and
-wave64 shuffles.  What neither form takes raises ``LoweringError``.  An arrangement that
+Programs with reductions (``ntl.sum/max/min``), ``ntl.dot``, broadcasting subscripts,
+``offsets`` index vectors, source pointers and gathers, or loops over tile levels run as
+tile programs (``TilePlan``, below): one workgroup per program instance, reductions through
+LDS and wave64 shuffles.  Loops with up to ``MAX_UNROLL`` iterations known at the call are
+unrolled; longer ones, and those whose trip counts are run-time scalars, run as loops in
+the kernel, each loop-carried tile in two LDS buffers (iteration k reads buffer k % 2 and
+writes the other), level indices by the loop variable guarded against the level's extent.
+What neither form takes raises ``LoweringError``.  An arrangement that
 maps several elements to one output element writes it from several lanes (the last write
 is unspecified), as the reference's generated programs would.
 """
 
 import copy
 import ctypes
+import dataclasses
 import hashlib
 import threading
 
@@ -46,7 +51,7 @@ from ninetoothed_amd.frontend import Value, effect_targets
 from ninetoothed_amd.frontend import pointer_param as frontend_pointer_param
 
 MAX_ELEMENTS = 1 << 26
-MAX_UNROLL = 64  # loops of up to this many iterations are unrolled for the tile kernels
+MAX_UNROLL = 64  # loops of up to this many known iterations are unrolled for the tile kernels; longer ones loop
 _CONSTLIKE = ("const", "shape", "source_shape", "source_stride", "level_shape")  # values known at specialisation  # host-side index tables: at most 64 Mi elements per launch
 
 _ALLOWED = {"load", "const", "param", "add", "sub", "mul", "div", "floordiv", "mod", "neg", "lt", "le", "gt", "ge",
@@ -675,7 +680,8 @@ class GenericPlan:
 # masks of every tensor it is computed from hold, else it is the reduction's identity
 # (reference src/ninetoothed/backends/emitters/ssa.py:1834-1910, 2180-2210).
 
-_TILE_ALLOWED = _ALLOWED | {"reduce", "bcast", "ptr", "source_stride", "src_load", "ptr_load", "index", "unmask"}
+_TILE_ALLOWED = _ALLOWED | {"reduce", "bcast", "ptr", "source_stride", "src_load", "ptr_load", "index", "unmask",
+                            "loop_index", "carried", "loop_out"}
 LDS_BYTES = 64 * 1024
 _INT_LIMITS = {"int8": (-128, 127), "uint8": (0, 255), "int16": (-32768, 32767), "int32": (-(2**31), 2**31 - 1),
                "int64": (-(2**63), 2**63 - 1)}
@@ -694,20 +700,24 @@ def _value_operands(v):
         return list(v.args[1])
     if v.op in ("cast", "bcast", "unmask"):
         return [v.args[0]]
-    if v.op in ("load", "offsets", "reduce", "const", "shape", "source_shape", "level_shape", "zeros", "full", "param",
-                "dtype", "dtype_of"):
+    if v.op == "load":  # the level indices that are values
+        chain = _view_chain(v.args[0])
+        return [k for k in chain[1] if isinstance(k, Value)] if chain else []
+    if v.op in ("offsets", "reduce", "const", "shape", "source_shape", "level_shape", "zeros", "full", "param",
+                "dtype", "dtype_of", "loop_index", "carried", "loop_out"):
         return []
     return [a for a in v.args if isinstance(a, Value)]
 
 
 def _view_chain(view):
-    """(param, constant level indices) of ``param[k0][k1]...``, or None."""
+    """(param, level indices) of ``param[k0][k1]...``, or None: constant indices as ints,
+    the others (a loop index, a scalar parameter, an expression of them) as their values."""
     ks = []
     while view.op == "index":
         k = view.args[1]
-        if not (isinstance(k, Value) and k.op == "const" and isinstance(k.args[0], int)):
+        if not isinstance(k, Value):
             return None
-        ks.append(k.args[0])
+        ks.append(k.args[0] if k.op == "const" and isinstance(k.args[0], int) else k)
         view = view.args[0]
     if view.op != "param":
         return None
@@ -726,15 +736,19 @@ def _tile_shape(ctx, name):
     return tuple(ls[1]) if len(ls) > 1 else ()
 
 
-def _shapes(ctx, values, const_value):
+def _shapes(ctx, values, const_value, carried=None):
     """Tile shape of every value: loads have their tensor's tile shape, reductions drop
     their axis (all axes for ``axis=None``), ``x[:, None]`` inserts unit dims, and
-    elementwise operations broadcast as numpy does (right-aligned)."""
+    elementwise operations broadcast as numpy does (right-aligned).  ``carried[(loop, name)]``
+    is the shape of a loop-carried value (and of the loop's result)."""
     shp = {}
     for v in values:
         op, a = v.op, v.args
-        if op in ("const", "dtype", "dtype_of", "shape", "source_shape", "source_stride", "level_shape", "param", "ptr"):
+        if op in ("const", "dtype", "dtype_of", "shape", "source_shape", "source_stride", "level_shape", "param", "ptr",
+                  "loop_index"):
             s = ()
+        elif op in ("carried", "loop_out"):
+            s = carried[(a[0], a[1])]
         elif op == "load":
             name, ks = _view_chain(a[0])
             levels = ctx.views[name].level_shapes if ctx.params[name].source_ndim != 0 else []
@@ -864,9 +878,9 @@ class _TileEmitter(_Emitter):
             name, ks = chain
             t = self.tensor_dtype(name)
             st, w, ld, _ = _STORAGE[t]
-            lin = self.plan.level_lin(name, ks, _ravel(self.coords[id(v)], self.shapes[id(v)]))
+            entry = self.plan.level_index(name, ks, _ravel(self.coords[id(v)], self.shapes[id(v)]), self)
             ix = f"{self.tag}x{len(self.names)}"
-            self.lines.append(f"      const int {ix} = {self.plan.index_expr(name, lin)};")
+            self.lines.append(f"      const int {ix} = {entry};")
             other = self.ctx.views[name].source.other
             other = 0.0 if other is None else float(other)
             o = repr(other) if other == other and abs(other) != float("inf") else (
@@ -890,6 +904,19 @@ class _TileEmitter(_Emitter):
             self.names[id(v)] = self.names[id(args[0])]
             self.types[id(v)] = self.types[id(args[0])]
             self.masks[id(v)] = self.masks.get(id(args[0]), frozenset())
+            return
+        if op == "loop_index":
+            self.names[id(v)] = f"li{args[0]}"
+            self.types[id(v)] = "int32"
+            self.masks[id(v)] = frozenset()
+            return
+        if op in ("carried", "loop_out"):  # this iteration's buffer, or the one the loop ended in
+            i, n = args
+            arr, size = self.plan.carried_arrays[(i, n)]
+            buffer = f"pp{i}" if op == "carried" else f"po{i}"
+            self.names[id(v)] = f"{arr}[{buffer} * {size}LL + {_ravel(self.coords[id(v)], self.shapes[id(v)])}]"
+            self.types[id(v)] = self.plan.carried_type((i, n))
+            self.masks[id(v)] = frozenset()  # as a loop's values: no load mask
             return
         if op == "unmask":  # a loop-carried value: the same value, no load mask
             self.names[id(v)] = self.names[id(args[0])]
@@ -967,6 +994,8 @@ def _lower_dots(program):
     for eff in program.effects:
         roots += [a for a in eff[1:] if isinstance(a, Value)] + [x for a in eff[1:] if isinstance(a, tuple)
                                                                     for x in a if isinstance(x, Value)]
+    for lp in program.loops.values():
+        roots += [lp.trip] + list(lp.init.values()) + list(lp.update.values())
     if not any(v.op == "dot" for v in _walk(roots)):
         return program
     f32 = Value("dtype", ("float32",))
@@ -1005,30 +1034,122 @@ def _lower_dots(program):
     lowered = copy.copy(program)
     lowered.stores = {k: rebuild(v) for k, v in program.stores.items()}
     lowered.effects = [tuple(rebuild(a) for a in eff) for eff in program.effects]
+    lowered.loops = {i: dataclasses.replace(lp, trip=rebuild(lp.trip), init={n: rebuild(x) for n, x in lp.init.items()},
+                                            update={n: rebuild(x) for n, x in lp.update.items()})
+                     for i, lp in program.loops.items()}
     return lowered
+
+
+def _constants(program):
+    """The program with every loop's trip count, initial and updated values as values
+    (a Python number there becomes a constant)."""
+    if not program.loops:
+        return program
+
+    def val(x):
+        return x if isinstance(x, Value) else Value("const", (x,))
+
+    def trip(x):  # `range(n)` of a scalar parameter names the parameter itself: its value
+        return Value("load", (x,)) if isinstance(x, Value) and x.op in ("param", "index") else val(x)
+
+    out = copy.copy(program)
+    out.loops = {i: dataclasses.replace(lp, trip=trip(lp.trip), init={n: val(x) for n, x in lp.init.items()},
+                                        update={n: val(x) for n, x in lp.update.items()})
+                 for i, lp in program.loops.items()}
+    return out
+
+
+def _effect_roots(eff):
+    """The values a side effect reads (its view, with any level indices that are values)."""
+    if eff[0] == "src_store":
+        return list(eff[2]) + [eff[3]]
+    return [eff[1], eff[2]]
+
+
+class _LoopNest:
+    """Where each value of a program with symbolic loops is computed.
+
+    A value's scope is the innermost loop whose index or carried values it depends on (None:
+    outside every loop); a loop's results belong to the loop's own enclosing scope.  The
+    values a Python scope can see make these dependencies a chain, so the innermost is the
+    deepest of them."""
+
+    def __init__(self, program, values):
+        self.program = program
+        self.loops = program.loops
+        self.depth = {}
+        for i in sorted(self.loops):  # a loop's id is above its enclosing loop's
+            p = self.loops[i].parent
+            self.depth[i] = 0 if p is None else self.depth[p] + 1
+        self.scopes = {}
+        for v in values:  # dependencies first
+            if v.op in ("loop_index", "carried"):
+                sc = v.args[0]
+            elif v.op == "loop_out":
+                sc = self.loops[v.args[0]].parent
+            else:
+                sc = None
+                for a in v.args:
+                    for x in (a if isinstance(a, tuple) else (a,)):
+                        if isinstance(x, Value):
+                            sc = self.deeper(sc, self.scopes[id(x)])
+            self.scopes[id(v)] = sc
+
+    def deeper(self, a, b):
+        if a is None:
+            return b
+        if b is None:
+            return a
+        return a if self.depth[a] >= self.depth[b] else b
+
+    def inside(self, i, outer):
+        """Whether loop ``i`` is ``outer`` or nested in it."""
+        while i is not None:
+            if i == outer:
+                return True
+            i = self.loops[i].parent
+        return False
+
+    def effect_scope(self, e):
+        sc = None
+        for i, lp in self.loops.items():
+            if lp.effects[0] <= e < lp.effects[1]:
+                sc = self.deeper(i, sc)
+        return sc
+
+    def items(self, scope):
+        """The loops and side effects directly in ``scope``, in program order."""
+        keyed = [((lp.effects[0], 0, i), ("loop", i)) for i, lp in self.loops.items() if lp.parent == scope]
+        keyed += [((e, 1, 0), ("effect", e)) for e in range(len(self.program.effects)) if self.effect_scope(e) == scope]
+        return [item for _, item in sorted(keyed)]
+
+    def roots(self, i):
+        """Every value loop ``i`` and the loops nested in it compute or store."""
+        out = []
+        for j, lp in self.loops.items():
+            if self.inside(j, i):
+                out += [lp.trip] + list(lp.init.values()) + list(lp.update.values())
+        s, t = self.loops[i].effects
+        for e in range(s, t):
+            out += _effect_roots(self.program.effects[e])
+        return out
 
 
 def _analyse_tile(ctx):
     """(ctx, stores, values) of a tile program (ctx a copy whose program has its dots
     lowered, when it has any), or None."""
-    program = ctx.program
-    if program.loops:
-        return None
-    program = _lower_dots(program)
+    program = _lower_dots(_constants(ctx.program))
     if program is not ctx.program:
         ctx = copy.copy(ctx)
         ctx.program = program
     stores = program.stores
     roots = list(stores.values())
     for eff in program.effects:
-        if eff[0] == "src_store":
-            roots += list(eff[2]) + [eff[3]]
-        elif eff[0] == "view_store":
-            if _view_chain(eff[1]) is None:
-                return None
-            roots.append(eff[2])
-        else:
-            roots += [eff[1], eff[2]]
+        if eff[0] == "view_store" and _view_chain(eff[1]) is None:
+            return None
+        roots += _effect_roots(eff)
+    for lp in program.loops.values():
+        roots += [lp.trip] + list(lp.init.values()) + list(lp.update.values())
     values = _walk(roots)
     if not stores and not program.effects:
         return None
@@ -1075,104 +1196,34 @@ class TilePlan(GenericPlan):
         self.ctx = ctx
         self.stores = stores
         probe = _Emitter(ctx)
-        self.shapes = _shapes(ctx, values, probe.const_value)
-        self.types = {}
+        program = ctx.program
+        self.nest = _LoopNest(program, values) if program.loops else None
+        self.carried_shapes = self._settle_shapes(values, probe)
+        self.shapes = _shapes(ctx, values, probe.const_value, self.carried_shapes)
         self.outputs = list(stores)
         self.kernel_name = "nt_generic_tile"
-        self.raw_reads = set()  # tensors read through source indexing or pointers
         arranged = self.outputs + sorted(
-            {_view_chain(e[1])[0] for e in ctx.program.effects if e[0] == "view_store"}
+            {_view_chain(e[1])[0] for e in program.effects if e[0] == "view_store"}
             | {_view_chain(v.args[0])[0] for v in values if v.op == "load"
                and ctx.params[_view_chain(v.args[0])[0]].source_ndim != 0}
             | {v.args[0].args[0] for v in values if v.op == "offsets"})
         grid = tuple(ctx.views[arranged[0]].level_shapes[0])
         self.programs = int(np.prod(grid)) if grid else 1
-        self.lds = {}
-        em = _TileEmitter(self)
-        blocks, lds_bytes, decls = [], 0, []
-        reductions = [v for v in values if v.op == "reduce"]
-        for k, r in enumerate(reductions):
-            kind, operand, axis = r.args
-            sshape = self.shapes[id(operand)]
-            oshape = self.shapes[id(r)]
-            if axis is None:
-                n_out, extent = 1, int(np.prod(sshape)) if sshape else 1
-            else:
-                ax = axis + len(sshape) if axis < 0 else axis
-                n_out, extent = int(np.prod(oshape)) if oshape else 1, sshape[ax]
-            # operand coordinates from (o, l)
-            if axis is None:
-                coords = _unravel("l", sshape)
-            else:
-                oc = list(_unravel("o", oshape))
-                coords = tuple(oc[:ax] + ["l"] + oc[ax:])
-            body = em.context(operand, coords, f"r{k}_")
-            t = em.type_of(operand)
-            t = "float32" if t in ("weak", "bool") else t
-            if kind == "sum" and t in ("int8", "int16", "uint8"):
-                t = "int32"
-            w = em.work(t)
-            if w == "bool":
-                raise LoweringError("reductions of booleans are not supported")
-            ident, comb = self._combine(kind, t, w)
-            val = em.operand(operand, t)
-            mask = em.mask_of(operand)
-            term = f"({mask}) ? {val} : {ident}" if mask else val
-            lanes = 1 if n_out >= 256 else min(64, 1 << int(np.log2(256 // n_out)))
-            lanes = max(1, min(lanes, 1 << int(np.ceil(np.log2(max(extent, 1))))))
-            step = 256 // lanes
-            o_pad = -(-n_out // step) * step
-            arr = f"red{k}"
-            decls.append(f"  __shared__ {w} {arr}[{max(n_out, 1)}];")
-            lds_bytes += max(n_out, 1) * (8 if w in ("double", "long long") else 4)
-            self.lds[id(r)] = (arr, oshape)
-            self.types[id(r)] = t
-            blocks.append("\n".join([
-                f"    {{  // {kind} over {'all axes' if axis is None else f'axis {axis}'}: {n_out} x {extent}",
-                f"      const int g = tid % {lanes};",
-                f"      for (int o = tid / {lanes}; o < {o_pad}; o += {step}) {{",
-                f"        {w} acc = {ident};",
-                f"        if (o < {n_out}) {{",
-                f"          for (long long l = g; l < {extent}LL; l += {lanes}) {{",
-                *["    " + x for x in body],
-                f"            acc = {comb.format(a='acc', b=f'({term})')};",
-                "          }",
-                "        }",
-                *([f"        for (int s = {lanes // 2}; s > 0; s >>= 1) "
-                   f"acc = {comb.format(a='acc', b='__shfl_xor(acc, s, 64)')};"] if lanes > 1 else []),
-                f"        if (g == 0 && o < {n_out}) {arr}[o] = {em.round_to(t, 'acc')};",
-                "      }",
-                "    }",
-                "    __syncthreads();",
-            ]))
-        if lds_bytes > LDS_BYTES:
-            raise LoweringError(f"the reductions of this program need {lds_bytes} bytes of LDS (at most {LDS_BYTES})")
-        for out, v in stores.items():
-            tshape = _tile_shape(ctx, out)
-            sv = self.shapes[id(v)]
-            if _bcast_shapes(sv, tshape) != tshape:
-                raise LoweringError(f"a value of shape {sv} is stored to a tile of shape {tshape}")
-            n_tile = int(np.prod(tshape)) if tshape else 1
-            oc = _unravel("j", tshape)
-            body = em.context(v, oc[len(oc) - len(sv):] if sv else (), f"s{out}_")
-            t = _torch_dtype_name(ctx.dtypes[out])
-            src = em.type_of(v)
-            src = "float32" if src == "weak" else src
-            val = em.operand(v, src) if v.op in _CONSTLIKE else em.names[id(v)]
-            if em.work(src) != em.work(t):
-                val = f"(({em.work(t)}){val})"
-            blocks.append("\n".join([
-                f"    for (long long j = tid; j < {n_tile}LL; j += 256) {{",
-                f"      const int oi = {self.index_expr(out, 'j')};",
-                "      if (oi < 0) continue;",
-                *body,
-                f"      p_{out}[oi] = {_STORAGE[t][3].format(val)};",
-                "    }",
-            ]))
-        self.raw_writes = []
-        self.view_targets = sorted({_view_chain(e[1])[0] for e in ctx.program.effects if e[0] == "view_store"})
-        for k, eff in enumerate(ctx.program.effects):
-            blocks.append(self._effect(em, k, eff))
+        if self.nest is not None:
+            for out, v in stores.items():
+                if self.nest.scopes[id(v)] is not None:
+                    raise LoweringError(f"`{out}` is assigned a value computed inside a loop; the generic tile kernels "
+                                        "store a loop's results after it, or a level of the output inside it")
+        # the types of the loop-carried values: the promotion of each one's initial and updated
+        # types, found by emitting until they no longer change
+        self.carried_types = {}
+        for _ in range(8):
+            found = self._emit(values)
+            if found == self.carried_types:
+                break
+            self.carried_types = found
+        else:
+            raise LoweringError("the types of the loop-carried values do not settle")
         self.loaded = sorted({_view_chain(v.args[0])[0] for v in values if v.op == "load"
                               and ctx.params[_view_chain(v.args[0])[0]].source_ndim != 0})
         # tensors reached only through pointers or source indexing: a plain pointer argument
@@ -1186,7 +1237,7 @@ class TilePlan(GenericPlan):
         self.tile_sizes = {n: int(np.prod([int(np.prod(l)) for l in ctx.views[n].level_shapes[1:]]))
                            for n in self.index_names}
         self.offset_lengths = {(n, d): (_tile_shape(ctx, n)[d] if _tile_shape(ctx, n) else 1) for n, d in self.offsets}
-        self.scalar_types = {n: em.scalar_type(n) for n in self.scalars}
+        self.scalar_types = {n: probe.scalar_type(n) for n in self.scalars}
         params = [f"const int* __restrict__ t_{n}" for n in self.index_names]
         params += [f"const int* __restrict__ f_{n}_{d}" for n, d in self.offsets]
         params += [f"const {_STORAGE[_torch_dtype_name(ctx.dtypes[n])][0]}* __restrict__ p_{n}" for n in self.loaded]
@@ -1197,23 +1248,246 @@ class TilePlan(GenericPlan):
         params += [f"{_STORAGE[self.scalar_types[n]][0]} s_{n}" for n in self.scalars]
         params.append("long long programs")
         self.params = params
-        self.decls = decls
-        self.blocks = blocks
+
+    def _settle_shapes(self, values, probe):
+        """Shape of every loop-carried value: its initial value's, broadcast with its updated
+        value's until that no longer changes."""
+        program = self.ctx.program
+        carried = {}
+        for i in sorted(program.loops):  # an initial value sees only enclosing and earlier loops
+            lp = program.loops[i]
+            shp = _shapes(self.ctx, _walk(list(lp.init.values())), probe.const_value, carried)
+            for n, x in lp.init.items():
+                carried[(i, n)] = shp[id(x)]
+        for _ in range(8):
+            shp = _shapes(self.ctx, values, probe.const_value, carried)
+            new = {(i, n): _bcast_shapes(carried[(i, n)], shp[id(u)])
+                   for i, lp in program.loops.items() for n, u in lp.update.items()}
+            if new == carried:
+                return carried
+            carried = new
+        raise LoweringError("the shapes of the loop-carried values do not settle")
+
+    def carried_type(self, key):
+        return self.carried_types.get(key, "float32")
+
+    def _emit(self, values):
+        """Emit the kernel body (``self.blocks``, ``self.decls``) with the current carried
+        types; returns the carried types the emission implies."""
+        ctx, program = self.ctx, self.ctx.program
+        self.types = {}
+        self.lds = {}
+        self.raw_reads = set()  # tensors read through source indexing or pointers
+        self.raw_writes = []
+        self.view_targets = sorted({_view_chain(e[1])[0] for e in program.effects if e[0] == "view_store"})
+        self.decls, self.lds_bytes = [], 0
+        self.carried_arrays = {}
+        for (i, n), shape in sorted(self.carried_shapes.items()):
+            size = int(np.prod(shape)) if shape else 1
+            w = _STORAGE["float32" if self.carried_type((i, n)) == "weak" else self.carried_type((i, n))][1]
+            arr = f"c{i}_{n}"
+            self.decls.append(f"  __shared__ {w} {arr}[{2 * size}];  // loop {i}: `{n}`, two buffers")
+            self.lds_bytes += 2 * size * (8 if w in ("double", "long long") else (1 if w == "bool" else 4))
+            self.carried_arrays[(i, n)] = (arr, size)
+        self.found_types = {}
+        self.red_index = {id(r): k for k, r in enumerate(v for v in values if v.op == "reduce")}
+        self.emitted = set()
+        em = _TileEmitter(self)
+        if self.nest is None:
+            items = [("store", out) for out in self.stores] + [("effect", e) for e in range(len(program.effects))]
+        else:
+            items = self.nest.items(None) + [("store", out) for out in self.stores]
+        self.blocks = self._scope_blocks(em, None, items)
+        if self.lds_bytes > LDS_BYTES:
+            raise LoweringError(f"the reductions and loop-carried values of this program need {self.lds_bytes} bytes "
+                                f"of LDS (at most {LDS_BYTES})")
+        return self.found_types
+
+    def _scope_blocks(self, em, scope, items):
+        """Blocks of the items of one scope, each preceded by the reductions of that scope it
+        needs that no earlier item did."""
+        program = self.ctx.program
+        blocks = []
+        for kind, x in items:
+            if kind == "loop":
+                roots = self.nest.roots(x)
+            elif kind == "effect":
+                roots = _effect_roots(program.effects[x])
+            elif kind == "store":
+                roots = [self.stores[x]]
+            else:  # "update": the carried values of loop x
+                roots = list(program.loops[x].update.values())
+            for v in _walk(roots):
+                if v.op == "reduce" and id(v) not in self.emitted and (
+                        self.nest is None or self.nest.scopes[id(v)] == scope):
+                    self.emitted.add(id(v))
+                    blocks.append(self._reduction_block(em, v))
+            if kind == "loop":
+                blocks += self._loop_blocks(em, x)
+            elif kind == "effect":
+                blocks.append(self._effect(em, x, program.effects[x]))
+            elif kind == "store":
+                blocks.append(self._store_block(em, x, self.stores[x]))
+        return blocks
+
+    def _reduction_block(self, em, r):
+        k = self.red_index[id(r)]
+        kind, operand, axis = r.args
+        sshape = self.shapes[id(operand)]
+        oshape = self.shapes[id(r)]
+        if axis is None:
+            n_out, extent = 1, int(np.prod(sshape)) if sshape else 1
+        else:
+            ax = axis + len(sshape) if axis < 0 else axis
+            n_out, extent = int(np.prod(oshape)) if oshape else 1, sshape[ax]
+        # operand coordinates from (o, l)
+        if axis is None:
+            coords = _unravel("l", sshape)
+        else:
+            oc = list(_unravel("o", oshape))
+            coords = tuple(oc[:ax] + ["l"] + oc[ax:])
+        body = em.context(operand, coords, f"r{k}_")
+        t = em.type_of(operand)
+        t = "float32" if t in ("weak", "bool") else t
+        if kind == "sum" and t in ("int8", "int16", "uint8"):
+            t = "int32"
+        w = em.work(t)
+        if w == "bool":
+            raise LoweringError("reductions of booleans are not supported")
+        ident, comb = self._combine(kind, t, w)
+        val = em.operand(operand, t)
+        mask = em.mask_of(operand)
+        term = f"({mask}) ? {val} : {ident}" if mask else val
+        lanes = 1 if n_out >= 256 else min(64, 1 << int(np.log2(256 // n_out)))
+        lanes = max(1, min(lanes, 1 << int(np.ceil(np.log2(max(extent, 1))))))
+        step = 256 // lanes
+        o_pad = -(-n_out // step) * step
+        arr = f"red{k}"
+        self.decls.append(f"  __shared__ {w} {arr}[{max(n_out, 1)}];")
+        self.lds_bytes += max(n_out, 1) * (8 if w in ("double", "long long") else 4)
+        self.lds[id(r)] = (arr, oshape)
+        self.types[id(r)] = t
+        return "\n".join([
+            f"    {{  // {kind} over {'all axes' if axis is None else f'axis {axis}'}: {n_out} x {extent}",
+            f"      const int g = tid % {lanes};",
+            f"      for (int o = tid / {lanes}; o < {o_pad}; o += {step}) {{",
+            f"        {w} acc = {ident};",
+            f"        if (o < {n_out}) {{",
+            f"          for (long long l = g; l < {extent}LL; l += {lanes}) {{",
+            *["    " + x for x in body],
+            f"            acc = {comb.format(a='acc', b=f'({term})')};",
+            "          }",
+            "        }",
+            *([f"        for (int s = {lanes // 2}; s > 0; s >>= 1) "
+               f"acc = {comb.format(a='acc', b='__shfl_xor(acc, s, 64)')};"] if lanes > 1 else []),
+            f"        if (g == 0 && o < {n_out}) {arr}[o] = {em.round_to(t, 'acc')};",
+            "      }",
+            "    }",
+            "    __syncthreads();",
+        ])
+
+    def _store_block(self, em, out, v):
+        ctx = self.ctx
+        tshape = _tile_shape(ctx, out)
+        sv = self.shapes[id(v)]
+        if _bcast_shapes(sv, tshape) != tshape:
+            raise LoweringError(f"a value of shape {sv} is stored to a tile of shape {tshape}")
+        n_tile = int(np.prod(tshape)) if tshape else 1
+        oc = _unravel("j", tshape)
+        body = em.context(v, oc[len(oc) - len(sv):] if sv else (), f"s{out}_")
+        t = _torch_dtype_name(ctx.dtypes[out])
+        src = em.type_of(v)
+        src = "float32" if src == "weak" else src
+        val = em.operand(v, src) if v.op in _CONSTLIKE else em.names[id(v)]
+        if em.work(src) != em.work(t):
+            val = f"(({em.work(t)}){val})"
+        return "\n".join([
+            f"    for (long long j = tid; j < {n_tile}LL; j += 256) {{",
+            f"      const int oi = {self.index_expr(out, 'j')};",
+            "      if (oi < 0) continue;",
+            *body,
+            f"      p_{out}[oi] = {_STORAGE[t][3].format(val)};",
+            "    }",
+        ])
+
+    def _carried_write(self, em, i, n, v, tag, buffer):
+        """Lines writing value ``v`` to every element of loop ``i``'s carried ``n`` in ``buffer``."""
+        arr, size = self.carried_arrays[(i, n)]
+        shape = self.carried_shapes[(i, n)]
+        t = self.carried_type((i, n))
+        coords = _unravel("j", shape)
+        sv = self.shapes[id(v)]
+        body = em.context(v, coords[len(coords) - len(sv):] if sv else (), tag)
+        val = em.round_to(t, em.operand(v, t))
+        return [
+            f"    for (long long j = tid; j < {size}LL; j += 256) {{",
+            *body,
+            f"      {arr}[{buffer} * {size}LL + j] = {val};",
+            "    }",
+        ]
+
+    @staticmethod
+    def _settled_type(t, v):
+        if t != "weak":
+            return t
+        c = v.args[0] if v.op == "const" else None
+        return "bool" if isinstance(c, bool) else ("int32" if isinstance(c, int) else "float32")
+
+    def _loop_blocks(self, em, i):
+        """A symbolic loop: its carried values in two LDS buffers each (iteration k reads
+        buffer k % 2 and writes the other), one barrier per iteration after the update."""
+        lp = self.ctx.program.loops[i]
+        lines = [f"    // loop {i} (`for {lp.var} in range(...)`)"]
+        trip_lines = em.context(lp.trip, (), f"t{i}_")
+        tt = em.type_of(lp.trip)
+        if tt not in _INT and not (tt == "weak" and isinstance(em.const_value(lp.trip), int)):
+            raise LoweringError("a loop's trip count must be an integer")
+        lines += trip_lines + [f"    const long long n{i} = {em.operand(lp.trip, 'int64')};"]
+        init_types = {}
+        for n, x in sorted(lp.init.items()):
+            lines += self._carried_write(em, i, n, x, f"i{i}_{n}_", "0")
+            init_types[n] = self._settled_type(em.type_of(x), x)
+        lines.append("    __syncthreads();")
+        body = self._scope_blocks(em, i, self.nest.items(i) + [("update", i)])
+        update = []
+        for n, u in sorted(lp.update.items()):
+            update += self._carried_write(em, i, n, u, f"u{i}_{n}_", f"(pp{i} ^ 1)")
+            self.found_types[(i, n)] = _promote(init_types[n], self._settled_type(em.type_of(u), u))
+        inner = [f"    const long long pp{i} = li{i} & 1;", *body, *update, "    __syncthreads();"]
+        lines.append(f"    for (long long li{i} = 0; li{i} < n{i}; ++li{i}) {{")
+        lines += ["  " + x for x in "\n".join(inner).split("\n")]
+        lines.append("    }")
+        lines.append(f"    const long long po{i} = (n{i} > 0 ? n{i} : 0) & 1;")
+        return ["\n".join(lines)]
 
     def index_expr(self, name, lin):
         return f"t_{name}[pb_{name} + {lin}]"
 
-    def level_lin(self, name, ks, inner):
-        """Offset, within a program's part of ``name``'s index table, of element ``inner`` of
-        the level reached by the constant level indices ``ks``."""
+    def level_index(self, name, ks, inner, em):
+        """C index-table entry of element ``inner`` of the level of ``name`` reached by the
+        level indices ``ks`` (ints, or values already emitted by ``em``); -1 (masked) where an
+        index that is a value falls outside its level."""
         levels = [tuple(l) for l in self.ctx.views[name].level_shapes[1:]]
-        terms = []
+        terms, guards = [], []
         for i, k in enumerate(ks):
-            if len(levels[i]) != 1 or not 0 <= k < levels[i][0]:
-                raise LoweringError(f"level index {k} of `{name}` needs a 1-D level that holds it")
+            if len(levels[i]) != 1:
+                raise LoweringError(f"level index {k} of `{name}` needs a 1-D level")
             below = int(np.prod([int(np.prod(l)) for l in levels[i + 1:]]))
-            terms.append(f"{k * below}LL")
-        return " + ".join(terms + [inner]) if terms else inner
+            if isinstance(k, Value):
+                if self.shapes[id(k)] != ():
+                    raise LoweringError(f"a level index of `{name}` must be a scalar")
+                t = em.type_of(k)
+                if t not in _INT and not (t == "weak" and isinstance(em.const_value(k), int)):
+                    raise LoweringError(f"a level index of `{name}` must be an integer")
+                e = em.operand(k, "int64")
+                terms.append(f"({e}) * {below}LL")
+                guards.append(f"({e}) >= 0 && ({e}) < {levels[i][0]}LL")
+            else:
+                if not 0 <= k < levels[i][0]:
+                    raise LoweringError(f"level index {k} of `{name}` needs a 1-D level that holds it")
+                terms.append(f"{k * below}LL")
+        entry = self.index_expr(name, " + ".join(terms + [inner]) if terms else inner)
+        return f"(({' && '.join(guards)}) ? {entry} : -1)" if guards else entry
 
     def extent(self, name):
         """Elements from a tensor's first to one past its last element (its storage span)."""
@@ -1238,7 +1512,8 @@ class TilePlan(GenericPlan):
                 raise LoweringError(f"a value of shape {sv} is stored to a level of shape {shape}")
             n = int(np.prod(shape)) if shape else 1
             coords = _unravel("j", shape)
-            body = em.context(value, coords[len(coords) - len(sv):] if sv else (), f"e{k}_")
+            indices = [(x, ()) for x in ks if isinstance(x, Value)]
+            body = em.context(value, coords[len(coords) - len(sv):] if sv else (), f"e{k}_", more=indices)
             t = _torch_dtype_name(self.ctx.dtypes[name])
             src = em.type_of(value)
             src = "float32" if src == "weak" else src
@@ -1247,7 +1522,7 @@ class TilePlan(GenericPlan):
                 val = f"(({em.work(t)}){val})"
             return "\n".join([
                 f"    for (long long j = tid; j < {n}LL; j += 256) {{  // store into {name}{list(ks)}",
-                f"      const int oi = {self.index_expr(name, self.level_lin(name, ks, 'j'))};",
+                f"      const int oi = {self.level_index(name, ks, 'j', em)};",
                 "      if (oi < 0) continue;",
                 *body,
                 f"      p_{name}[oi] = {_STORAGE[t][3].format(val)};",
@@ -1366,11 +1641,10 @@ def match_generic(ctx):
     found = _analyse(ctx)
     if found is not None:
         return GenericPlan(ctx, *found)
-    found = _analyse_tile(ctx)
-    if found is not None:
-        return TilePlan(*found)
+    refused = None
     if ctx.program.loops and ctx.relower is not None:
-        # loops whose trip counts are known now: unrolled, the program may be a tile program
+        # loops with up to MAX_UNROLL iterations known now are unrolled (no loop-carried
+        # buffers); longer ones, and those whose trip counts are run-time values, stay loops
         resolve = _Emitter(ctx).const_value
 
         def unroll(trip):
@@ -1378,10 +1652,18 @@ def match_generic(ctx):
             return c if isinstance(c, int) and not isinstance(c, bool) and 0 <= c <= MAX_UNROLL else None
 
         program = ctx.relower(unroll)
-        if not program.loops:
+        if len(program.loops) < len(ctx.program.loops):
             unrolled = copy.copy(ctx)
             unrolled.program = program
-            found = _analyse_tile(unrolled)
-            if found is not None:
-                return TilePlan(*found)
+            try:
+                found = _analyse_tile(unrolled)
+                if found is not None:
+                    return TilePlan(*found)
+            except LoweringError as e:  # e.g. unrolled reductions beyond the LDS: try the loops
+                refused = e
+    found = _analyse_tile(ctx)
+    if found is not None:
+        return TilePlan(*found)
+    if refused is not None:
+        raise refused
     return None

@@ -655,7 +655,7 @@ def test_data_ptr_atomic_sum():
     assert torch.allclose(out[0], torch.sum(inp), rtol=1e-4, atol=1e-3)
 
 
-# ------------------------------------------------------------------ loops over tiles (unrolled)
+# ------------------------------------------------------------------ loops over tiles (unrolled up to 64 iterations)
 def tiled_arrangement(x, out):
     arranged = []
     for tensor in (x, out):
@@ -700,6 +700,114 @@ def test_tiled_reduction_loop_runtime(dtype, width):
     kernel(x, out)
     expected = x.float() * torch.rsqrt(x.float().square().mean(dim=1, keepdim=True) + 1e-5)
     torch.testing.assert_close(out, expected.to(dtype))
+
+
+# ------------------------------------------------------------------ loops beyond the unroll limit (real loops)
+def counted_normalize(x, n, out):
+    # a run-time trip count: the first n column tiles of each row, scaled by a weight that
+    # an inner loop counts up (a loop nested in a loop, both with run-time trip counts)
+    accumulator = ntl.zeros(x.dtype.shape, dtype=ntl.float32)
+    for i in range(n):
+        weight = 0.0
+        for j in range(n):
+            weight = weight + 0.5
+        accumulator += ntl.cast(x[i], ntl.float32) * weight
+    total = ntl.sum(accumulator)
+    for i in range(x.shape[0]):
+        out[i] = x[i] * 0 + total
+
+
+def _counted():
+    return ninetoothed.make(lambda x, n, out: (tiled_arrangement(x, out)[0], n, tiled_arrangement(x, out)[1]),
+                            counted_normalize, (Tensor(2, other=0), Tensor(0), Tensor(2)))
+
+
+def test_long_tiled_loop_is_a_loop():
+    # 70 column tiles of 256: beyond the unroll limit, so the kernel loops; the carried
+    # accumulator lives in two LDS buffers, and each row's level stores sit inside the loop
+    k = ninetoothed.make(tiled_arrangement, tiled_normalize, (Tensor(2, other=0), Tensor(2)))
+    plan = _plan(k, torch.empty((3, 256 * 70)), torch.empty((3, 256 * 70)))
+    assert plan.describe()["family"] == "generic" and plan.nest is not None
+    src = plan.source()
+    assert src.count("for (long long li") == 2 and src.count("p_out[oi]") == 1
+    assert "__shared__ float c0_accumulator[512]" in src
+    assert len(GenericPlan.compile(src)) > 1000
+    # up to the limit the loops are unrolled (no carried buffers)
+    plan = _plan(k, torch.empty((3, 256 * 64)), torch.empty((3, 256 * 64)))
+    assert plan.nest is None and "for (long long li" not in plan.source()
+
+
+def test_run_time_trip_counts_and_nested_loops_compile():
+    plan = _plan(_counted(), torch.empty((2, 1000)), 3, torch.empty((2, 1000)))
+    src = plan.source()
+    assert plan.nest is not None and "const long long n0 = s_n;" in src and "const long long n1 = s_n;" in src
+    assert "__shared__ float c1_weight[2]" in src  # the inner loop's scalar, carried in its own buffers
+    assert len(GenericPlan.compile(src)) > 1000
+
+
+def test_loop_rejections():
+    # a value computed inside a loop may not be stored to a whole arranged output
+    def stored_inside(x, out):
+        for i in range(x.shape[0]):
+            y = x[i] * 2
+        out = y  # noqa: F841
+
+    k = ninetoothed.make(lambda x, out: (tiled_arrangement(x, out)[0], out.tile((1, 256))), stored_inside,
+                         (Tensor(2), Tensor(2)))
+    with pytest.raises(ninetoothed.LoweringError):
+        _plan(k, torch.empty((3, 256 * 70)), torch.empty((3, 256)))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", (torch.float16, torch.float32))
+@pytest.mark.parametrize("width", (256 * 64 + 1, 40000))
+def test_long_tiled_reduction_loop_runtime(dtype, width):
+    # the reference's tiled reduction program (tests/test_tiled_reduction_loops.py:46-68) on
+    # rows of 65 and 157 column tiles: real loops, checked against the reference test's formula
+    kernel = ninetoothed.make(tiled_arrangement, tiled_normalize, (Tensor(2, other=0), Tensor(2)), max_num_configs=1)
+    x = torch.randn((7, width * 2), device="cuda", dtype=dtype)[:, ::2]
+    out = torch.empty((7, width), device="cuda", dtype=dtype)
+    kernel(x, out)
+    expected = x.float() * torch.rsqrt(x.float().square().mean(dim=1, keepdim=True) + 1e-5)
+    torch.testing.assert_close(out, expected.to(dtype))
+
+
+@pytest.mark.gpu
+def test_run_time_trip_counts_and_nested_loops():
+    kernel = _counted()
+    x = torch.randn((5, 3000), device="cuda")
+    for n in (0, 1, 4, 14):  # the row has 12 tiles: 14 reads two tiles past it (masked to zero)
+        out = torch.full_like(x, -1.0)
+        kernel(x, n, out)
+        expected = (x[:, :256 * n].sum(dim=1, keepdim=True) * (0.5 * n)).expand_as(x)
+        torch.testing.assert_close(out, expected, rtol=1e-5, atol=1e-3)
+
+
+@pytest.mark.gpu
+def test_long_overlapping_k_loop_matmul():
+    # the overlapping k-tiles program with K = 576: 71 k-tiles, each an fp32 dot, in a real
+    # loop (checked against the oracle's evaluation of the same arrangement)
+    import programs as pg
+
+    def overlap(lhs, rhs, output, BM=16, BN=16, BK=16):
+        out = output.tile((BM, BN))
+        lt = lhs.tile((BM, BK), strides=(-1, 8)).tile((1, -1)).expand((-1, out.shape[1]))
+        lt.dtype = lt.dtype.squeeze(0)
+        rt = rhs.tile((BK, BN), strides=(8, -1)).tile((-1, 1)).expand((out.shape[0], -1))
+        rt.dtype = rt.dtype.squeeze(1)
+        return lt, rt, out
+
+    g = torch.Generator().manual_seed(23)
+    a = (torch.randn(32, 576, generator=g) / 8).half().cuda()
+    b = (torch.randn(576, 48, generator=g) / 8).half().cuda()
+    out = torch.empty(32, 48, dtype=torch.float16, device="cuda")
+    h = ninetoothed.make(overlap, pg.matmul_application, pg.matmul_tensors())
+    assert _plan(h, a, b, out).nest is not None
+    h(a, b, out)
+    from oracle import apply
+
+    ref = apply.matmul(a.float().cpu().numpy(), b.float().cpu().numpy(), "float16", overlap, block=(16, 16, 16))
+    torch.testing.assert_close(out.float().cpu(), torch.from_numpy(ref), rtol=1e-2, atol=1e-2)
 
 
 # ------------------------------------------------------------------ libdevice (reference tests/test_libdevice_calls.py)
