@@ -183,6 +183,7 @@ class Lowerer:
         self.stores = {}
         self.store_order = []
         self.effects = []
+        self.written = {}  # param -> the whole tile last assigned to it
         self._loop_ids = 0
         self._loop_stack = []  # ids of the symbolic loops being lowered, outermost first
         self.application = application
@@ -228,8 +229,12 @@ class Lowerer:
         return info.level_ndims[level - 1]
 
     def data(self, v):
-        """A value used as data: tensor views are loaded."""
+        """A value used as data: tensor views are loaded.  A parameter read after the
+        application assigned it reads back what it stored (the reference loads it after its
+        store, in program order), in the parameter's dtype."""
         if isinstance(v, Value):
+            if v.op == "param" and v.args[0] in self.written:
+                return self.b.make("cast", self.written[v.args[0]], self.b.make("dtype_of", v))
             if v.op in VIEW_OPS:
                 return self.b.make("load", v)
             return v
@@ -270,6 +275,7 @@ class Lowerer:
     def _store(self, param, value):
         self.stores[param] = self.data(value)
         self.store_order.append(param)
+        self.written[param] = self.stores[param]
 
     def _stmt(self, frame, s):
         if isinstance(s, ast.Expr):

@@ -52,7 +52,12 @@ from ninetoothed_amd.frontend import pointer_param as frontend_pointer_param
 
 MAX_ELEMENTS = 1 << 26
 MAX_UNROLL = 64  # loops of up to this many known iterations are unrolled for the tile kernels; longer ones loop
-_CONSTLIKE = ("const", "shape", "source_shape", "source_stride", "level_shape")  # values known at specialisation  # host-side index tables: at most 64 Mi elements per launch
+_CONSTLIKE = ("const", "shape", "source_shape", "source_stride", "level_shape")  # values known at specialisation
+# arithmetic on values known at specialisation is folded with Python's semantics, as the
+# reference's constexpr arithmetic (so ``x.source.shape[1] - 1`` stays an exact integer)
+_FOLD = {"add": lambda a, b: a + b, "sub": lambda a, b: a - b, "mul": lambda a, b: a * b,
+         "div": lambda a, b: a / b, "floordiv": lambda a, b: a // b, "mod": lambda a, b: a % b,
+         "neg": lambda a: -a}
 
 _ALLOWED = {"load", "const", "param", "add", "sub", "mul", "div", "floordiv", "mod", "neg", "lt", "le", "gt", "ge",
             "eq", "ne", "where", "maximum", "minimum", "math", "libm", "cast", "dtype", "dtype_of", "zeros",
@@ -236,11 +241,27 @@ class _Emitter:
             return int(self.ctx.values[v.args[0]].stride(v.args[1]))
         if v.op == "level_shape":
             return int(self.ctx.views[v.args[0]].level_shapes[v.args[1]][v.args[2]])
+        if v.op in _FOLD:
+            memo = self.__dict__.setdefault("_folded", {})
+            if id(v) not in memo:
+                xs = [self.const_value(a) if isinstance(a, Value) else a for a in v.args]
+                c = None
+                if all(isinstance(x, (int, float)) and not isinstance(x, bool) for x in xs):
+                    try:
+                        c = _FOLD[v.op](*xs)
+                    except (ZeroDivisionError, OverflowError):
+                        c = None
+                memo[id(v)] = (v, c)  # the value is kept so that its id stays its own
+            return memo[id(v)][1]
         return None
+
+    def is_const(self, v):
+        """Whether ``v`` is known at specialisation (a constant, a shape, or arithmetic on them)."""
+        return v.op in _CONSTLIKE or (v.op in _FOLD and self.const_value(v) is not None)
 
     def operand(self, v, t):
         """Operand ``v`` as a value of working type for an operation in type ``t``."""
-        if v.op in _CONSTLIKE:
+        if self.is_const(v):
             c = self.const_value(v)
             if isinstance(c, bool):
                 return "true" if c else "false"
@@ -272,7 +293,7 @@ class _Emitter:
 
     def emit(self, v):
         op, args = v.op, v.args
-        if op in _CONSTLIKE:
+        if self.is_const(v):
             self.types[id(v)] = "bool" if isinstance(self.const_value(v), bool) else "weak"
             return
         if op in ("dtype", "dtype_of", "param"):
@@ -440,7 +461,7 @@ class GenericPlan:
             t = _torch_dtype_name(ctx.dtypes[out])
             src = em.type_of(v)
             src = "float32" if src == "weak" else src
-            val = em.operand(v, src) if v.op in _CONSTLIKE else em.names[id(v)]
+            val = em.operand(v, src) if em.is_const(v) else em.names[id(v)]
             if em.work(src) != em.work(t):
                 val = f"(({em.work(t)}){val})"
             lines.append(f"    if (o_{out} >= 0) p_{out}[o_{out}] = {_STORAGE[t][3].format(val)};")
@@ -1168,10 +1189,14 @@ def _analyse_tile(ctx):
     for n in stores:
         if ctx.params[n].source_ndim == 0:
             return None
-    written = set(stores) | set(effect_targets(program))
+    targets = set(effect_targets(program))
     data_read = {_view_chain(v.args[0])[0] for v in values if v.op == "load"}  # offsets are indices, not data
-    if written & (data_read | read_raw):
-        raise LoweringError("the generic tile kernels do not update a tensor they also read")
+    if targets & (data_read | read_raw):
+        raise LoweringError("the generic tile kernels do not scatter into or store through a pointer to a tensor "
+                            "they also read")
+    if set(stores) & (data_read | read_raw) and targets & set(stores):
+        raise LoweringError("a tile program that updates a tensor it reads may not also write its outputs "
+                            "through pointers or level stores")
     if not tensors:
         raise LoweringError("a tile program needs an arranged tensor to set its program grid")
     indexed = {_view_chain(v.args[0])[0] for v in values if v.op == "load" and _view_chain(v.args[0])[1]}
@@ -1198,6 +1223,12 @@ class TilePlan(GenericPlan):
         probe = _Emitter(ctx)
         program = ctx.program
         self.nest = _LoopNest(program, values) if program.loops else None
+        # a tile stored to a tensor the program also reads: every stored value is computed
+        # into LDS before the first write, so that each load sees the tensor as it was
+        read = {_view_chain(v.args[0])[0] for v in values if v.op == "load"}
+        read |= {v.args[0] for v in values if v.op == "src_load"}
+        read |= {frontend_pointer_param(v.args[0]) for v in values if v.op == "ptr_load"}
+        self.inplace = bool(set(stores) & read)
         self.carried_shapes = self._settle_shapes(values, probe)
         self.shapes = _shapes(ctx, values, probe.const_value, self.carried_shapes)
         self.outputs = list(stores)
@@ -1225,7 +1256,7 @@ class TilePlan(GenericPlan):
         else:
             raise LoweringError("the types of the loop-carried values do not settle")
         self.loaded = sorted({_view_chain(v.args[0])[0] for v in values if v.op == "load"
-                              and ctx.params[_view_chain(v.args[0])[0]].source_ndim != 0})
+                              and ctx.params[_view_chain(v.args[0])[0]].source_ndim != 0} - set(stores))
         # tensors reached only through pointers or source indexing: a plain pointer argument
         self.raw = sorted((self.raw_reads | set(self.raw_writes)) - set(self.loaded) - set(self.outputs)
                           - set(self.view_targets))
@@ -1293,7 +1324,10 @@ class TilePlan(GenericPlan):
         self.red_index = {id(r): k for k, r in enumerate(v for v in values if v.op == "reduce")}
         self.emitted = set()
         em = _TileEmitter(self)
-        if self.nest is None:
+        if self.inplace:  # side effects (which read no stored tensor) first, then the staged stores
+            items = (self.nest.items(None) if self.nest is not None
+                     else [("effect", e) for e in range(len(program.effects))]) + [("staged", None)]
+        elif self.nest is None:
             items = [("store", out) for out in self.stores] + [("effect", e) for e in range(len(program.effects))]
         else:
             items = self.nest.items(None) + [("store", out) for out in self.stores]
@@ -1315,6 +1349,8 @@ class TilePlan(GenericPlan):
                 roots = _effect_roots(program.effects[x])
             elif kind == "store":
                 roots = [self.stores[x]]
+            elif kind == "staged":
+                roots = list(self.stores.values())
             else:  # "update": the carried values of loop x
                 roots = list(program.loops[x].update.values())
             for v in _walk(roots):
@@ -1328,6 +1364,8 @@ class TilePlan(GenericPlan):
                 blocks.append(self._effect(em, x, program.effects[x]))
             elif kind == "store":
                 blocks.append(self._store_block(em, x, self.stores[x]))
+            elif kind == "staged":
+                blocks += self._staged_stores(em)
         return blocks
 
     def _reduction_block(self, em, r):
@@ -1386,6 +1424,23 @@ class TilePlan(GenericPlan):
             "    __syncthreads();",
         ])
 
+    def _staged_stores(self, em):
+        """Every stored tile computed into LDS (in its storage type), one barrier, then written."""
+        compute, write = [], []
+        for out, v in self.stores.items():
+            lines = self._store_block(em, out, v).split("\n")
+            st = _STORAGE[_torch_dtype_name(self.ctx.dtypes[out])][0]
+            n_tile = int(np.prod(_tile_shape(self.ctx, out)) or 1)
+            arr = f"stage_{out}"
+            self.decls.append(f"  __shared__ {st} {arr}[{n_tile}];  // `{out}` before it is written")
+            self.lds_bytes += n_tile * {"double": 8, "long long": 8, "float": 4, "int": 4}.get(st, 2 if "short" in st else 1)
+            # the store block's loop with its index lookup moved to the write pass
+            head, lookup, skip, body, last, end = lines[0], lines[1], lines[2], lines[3:-2], lines[-2], lines[-1]
+            value = last.split(" = ", 1)[1]
+            compute.append("\n".join([head, *body, f"      {arr}[j] = {value}", end]))
+            write.append("\n".join([head, lookup, skip, f"      p_{out}[oi] = {arr}[j];", end]))
+        return compute + ["    __syncthreads();"] + write
+
     def _store_block(self, em, out, v):
         ctx = self.ctx
         tshape = _tile_shape(ctx, out)
@@ -1398,7 +1453,7 @@ class TilePlan(GenericPlan):
         t = _torch_dtype_name(ctx.dtypes[out])
         src = em.type_of(v)
         src = "float32" if src == "weak" else src
-        val = em.operand(v, src) if v.op in _CONSTLIKE else em.names[id(v)]
+        val = em.operand(v, src) if em.is_const(v) else em.names[id(v)]
         if em.work(src) != em.work(t):
             val = f"(({em.work(t)}){val})"
         return "\n".join([
@@ -1517,7 +1572,7 @@ class TilePlan(GenericPlan):
             t = _torch_dtype_name(self.ctx.dtypes[name])
             src = em.type_of(value)
             src = "float32" if src == "weak" else src
-            val = em.operand(value, src) if value.op in _CONSTLIKE else em.names[id(value)]
+            val = em.operand(value, src) if em.is_const(value) else em.names[id(value)]
             if em.work(src) != em.work(t):
                 val = f"(({em.work(t)}){val})"
             return "\n".join([

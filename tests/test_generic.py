@@ -472,13 +472,27 @@ def test_tile_programs_compile():
         assert len(GenericPlan.compile(plan.source())) > 1000
 
 
+def inplace_two_outputs(x, out):
+    x = x - ntl.max(x, axis=1)[:, None]  # noqa: F841
+    out = x  # noqa: F841
+
+
 def test_tile_program_rejections():
-    def inplace(x, out):
-        x = x - ntl.max(x, axis=1)[:, None]  # noqa: F841
+    # a program that updates a tensor it reads stages its stores; one that scatters into a
+    # tensor it reads is refused
+    h = _reduce_kernel(row_arrangement, inplace_two_outputs, 2, 2)
+    plan = _plan(h, torch.empty(4, 8), torch.empty(4, 8), WIDTH=8)
+    assert plan.inplace
+    # `out = x` after `x = ...` reads back what was stored (the reference loads x after its
+    # store), in x's dtype: no load of x's memory
+    assert plan.stores["out"].op == "cast" and plan.stores["out"].args[0] is plan.stores["x"]
+
+    def scatter_into_read(x, out):
+        x.source[x.offsets(0)[:, None], x.offsets(1)[None, :]] = x * 2
         out = x  # noqa: F841
 
-    h = _reduce_kernel(row_arrangement, inplace, 2, 2)
-    with pytest.raises(ninetoothed.LoweringError, match="update a tensor they also read"):
+    h = _reduce_kernel(row_arrangement, scatter_into_read, 2, 2)
+    with pytest.raises(ninetoothed.LoweringError, match="scatter into"):
         _plan(h, torch.empty(4, 8), torch.empty(4, 8), WIDTH=8)
 
 
@@ -808,6 +822,49 @@ def test_long_overlapping_k_loop_matmul():
 
     ref = apply.matmul(a.float().cpu().numpy(), b.float().cpu().numpy(), "float16", overlap, block=(16, 16, 16))
     torch.testing.assert_close(out.float().cpu(), torch.from_numpy(ref), rtol=1e-2, atol=1e-2)
+
+
+# ------------------------------------------------------------------ tile programs that update a tensor they read
+def inplace_center(x):
+    x = x - ntl.max(x)  # noqa: F841
+
+
+def inplace_reverse(x):
+    # each element takes its row's mirror element: another lane's, so the loads must all
+    # happen before the first write
+    x = x.source[x.offsets(0)[:, None], (x.source.shape[1] - 1 - x.offsets(1))[None, :]]  # noqa: F841
+
+
+def _rows(app):
+    return ninetoothed.make(lambda x, BW=Symbol("BW", meta=True): (x.tile((1, BW)),), app, (Tensor(2),))
+
+
+def test_inplace_tile_programs_stage_their_stores():
+    for app in (inplace_center, inplace_reverse):
+        plan = _plan(_rows(app), torch.empty((4, 300), dtype=torch.float16), BW=512)
+        src = plan.source()
+        assert plan.inplace and "__shared__ unsigned short stage_x[512]" in src
+        compute, write = src.split("stage_x[j] = ")[1], src.split("p_x[oi] = stage_x[j];")[0]
+        assert "__syncthreads();" in compute.split("p_x[oi]")[0] and "p_x[oi] = st_f16" not in write
+        assert len(GenericPlan.compile(src)) > 1000
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", (torch.float16, torch.float32))
+def test_inplace_tile_programs(dtype):
+    g = torch.Generator().manual_seed(24)
+    x0 = torch.randn(6, 300, generator=g).to(dtype).cuda()
+    x = x0.clone()
+    _rows(inplace_center)(x, BW=512)
+    torch.testing.assert_close(x, (x0.float() - x0.float().max(dim=1, keepdim=True).values).to(dtype))
+    x = x0.clone()
+    _rows(inplace_reverse)(x, BW=512)
+    assert torch.equal(x, x0.flip(1))
+    x, out = x0.clone(), torch.empty_like(x0)
+    _reduce_kernel(row_arrangement, inplace_two_outputs, 2, 2)(x, out, WIDTH=512)
+    centred = (x0.float() - x0.float().max(dim=1, keepdim=True).values).to(dtype)
+    torch.testing.assert_close(x, centred)
+    torch.testing.assert_close(out, centred)
 
 
 # ------------------------------------------------------------------ libdevice (reference tests/test_libdevice_calls.py)
