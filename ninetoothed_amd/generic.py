@@ -120,6 +120,9 @@ __device__ __forceinline__ float nt_randn(long long seed, long long offset) {
   return sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
 }
 __device__ __forceinline__ float ld_bf16(unsigned short b) { return __builtin_bit_cast(float, (unsigned)b << 16); }
+typedef _Float16 nt_half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 nt_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float nt_floatx16 __attribute__((ext_vector_type(16)));
 __device__ __forceinline__ unsigned short st_bf16(float x) { return (unsigned short)(__builtin_bit_cast(unsigned, r_bf16(x)) >> 16); }
 """
 
@@ -701,8 +704,8 @@ class GenericPlan:
 # masks of every tensor it is computed from hold, else it is the reduction's identity
 # (reference src/ninetoothed/backends/emitters/ssa.py:1834-1910, 2180-2210).
 
-_TILE_ALLOWED = _ALLOWED | {"reduce", "bcast", "ptr", "source_stride", "src_load", "ptr_load", "index", "unmask",
-                            "loop_index", "carried", "loop_out"}
+_TILE_ALLOWED = _ALLOWED | {"reduce", "mdot", "bcast", "ptr", "source_stride", "src_load", "ptr_load", "index",
+                            "unmask", "loop_index", "carried", "loop_out"}
 LDS_BYTES = 64 * 1024
 _INT_LIMITS = {"int8": (-128, 127), "uint8": (0, 255), "int16": (-32768, 32767), "int32": (-(2**31), 2**31 - 1),
                "int64": (-(2**63), 2**63 - 1)}
@@ -724,7 +727,7 @@ def _value_operands(v):
     if v.op == "load":  # the level indices that are values
         chain = _view_chain(v.args[0])
         return [k for k in chain[1] if isinstance(k, Value)] if chain else []
-    if v.op in ("offsets", "reduce", "const", "shape", "source_shape", "level_shape", "zeros", "full", "param",
+    if v.op in ("offsets", "reduce", "mdot", "const", "shape", "source_shape", "level_shape", "zeros", "full", "param",
                 "dtype", "dtype_of", "loop_index", "carried", "loop_out"):
         return []
     return [a for a in v.args if isinstance(a, Value)]
@@ -770,6 +773,9 @@ def _shapes(ctx, values, const_value, carried=None):
             s = ()
         elif op in ("carried", "loop_out"):
             s = carried[(a[0], a[1])]
+        elif op == "mdot":  # (x, y, x transposed, y transposed)
+            sx, sy = shp[id(a[0])], shp[id(a[1])]
+            s = ((sx[1] if a[2] else sx[0]), (sy[0] if a[3] else sy[1]))
         elif op == "load":
             name, ks = _view_chain(a[0])
             levels = ctx.views[name].level_shapes if ctx.params[name].source_ndim != 0 else []
@@ -916,7 +922,7 @@ class _TileEmitter(_Emitter):
             self.types[id(v)] = "int32"
             self.masks[id(v)] = frozenset()
             return
-        if op == "reduce":
+        if op in ("reduce", "mdot"):
             arr, oshape = self.plan.lds[id(v)]
             self.names[id(v)] = f"{arr}[{_ravel(self.coords[id(v)], oshape)}]"
             self.masks[id(v)] = frozenset()
@@ -1000,8 +1006,49 @@ class _TileEmitter(_Emitter):
         self.plan.raw_reads.add(name)
 
 
-def _lower_dots(program):
-    """The program with every ``ntl.dot`` of two tiles rewritten as an fp32 reduction.
+def _static_type(ctx, v):
+    """The dtype of a loaded tensor or of a cast, as far as it is known without emitting."""
+    if v.op == "load":
+        chain = _view_chain(v.args[0])
+        if chain is not None and ctx.params[chain[0]].source_ndim != 0:
+            return _torch_dtype_name(ctx.dtypes[chain[0]])
+    if v.op == "cast":
+        d = v.args[1]
+        if d.op == "dtype":
+            return d.args[0]
+        if d.op == "dtype_of":
+            view = d.args[0]
+            while view.op in ("index", "dtype_of"):
+                view = view.args[0]
+            return _torch_dtype_name(ctx.dtypes[view.args[0]]) if view.op == "param" else None
+    return None
+
+
+MDOT_LDS = 48 * 1024  # LDS a matrix-core dot may take (staged operands and the fp32 result)
+
+
+def _mdot_fits(ctx, x, y, tx, ty):
+    """Whether ``dot`` of (inner) operands x, y runs on the matrix core: both 16-bit floats
+    of one type, M and N multiples of 32, K of 16, operands and result within MDOT_LDS."""
+    t = _static_type(ctx, x)
+    if t not in ("float16", "bfloat16") or _static_type(ctx, y) != t:
+        return False
+    try:
+        shp = _shapes(ctx, _walk([x, y]), _Emitter(ctx).const_value, {})
+    except (KeyError, LoweringError):
+        return False
+    sx, sy = shp[id(x)], shp[id(y)]
+    if len(sx) != 2 or len(sy) != 2:
+        return False
+    m, k = (sx[1], sx[0]) if tx else sx
+    k2, n = (sy[1], sy[0]) if ty else sy
+    return (k == k2 and m % 32 == 0 and n % 32 == 0 and k % 16 == 0
+            and (m + n) * (k + 8) * 2 + m * n * 4 <= MDOT_LDS)
+
+
+def _lower_dots(program, ctx=None):
+    """The program with every ``ntl.dot`` of two tiles rewritten: on the matrix core
+    (``mdot``) where ``_mdot_fits``, else as an fp32 reduction.
 
     ``dot(x, y)`` of an [m, k] and a [k, n] tile is ``sum(x[:, :, None] * y[None, :, :],
     axis=1)`` with both operands first cast to float32 (the reference's ``tl.dot``
@@ -1010,7 +1057,9 @@ def _lower_dots(program):
     product in another axis order, so that no value is transposed: ``dot(x, trans(w))``
     with w [n, k] is ``sum(x[:, None, :] * w[None, :, :], axis=2)`` and ``dot(trans(u), y)``
     with u [k, m] is ``sum(u[:, :, None] * y[:, None, :], axis=0)``.  ``dot`` of two
-    transposed operands raises ``LoweringError``."""
+    transposed operands raises ``LoweringError``.  In both forms a product counts only where
+    both operands' load masks hold (the reference's dot emitter masks them the same way:
+    src/ninetoothed/backends/emitters/ssa.py:1455-1542)."""
     roots = list(program.stores.values())
     for eff in program.effects:
         roots += [a for a in eff[1:] if isinstance(a, Value)] + [x for a in eff[1:] if isinstance(a, tuple)
@@ -1034,8 +1083,13 @@ def _lower_dots(program):
             tx, ty = x.op == "trans", y.op == "trans"
             if tx and ty:
                 raise LoweringError("`dot` of two transposed tiles is not supported by the generic kernels")
-            cx = Value("cast", (rebuild(x.args[0] if tx else x), f32))
-            cy = Value("cast", (rebuild(y.args[0] if ty else y), f32))
+            xi, yi = rebuild(x.args[0] if tx else x), rebuild(y.args[0] if ty else y)
+            if ctx is not None and _mdot_fits(ctx, xi, yi, tx, ty):
+                out = Value("mdot", (xi, yi, tx, ty))
+                done[id(v)] = out
+                return out
+            cx = Value("cast", (xi, f32))
+            cy = Value("cast", (yi, f32))
             if ty:
                 prod = Value("mul", (Value("bcast", (cx, (":", None, ":"))), Value("bcast", (cy, (None, ":", ":")))))
                 axis = 2
@@ -1159,7 +1213,7 @@ class _LoopNest:
 def _analyse_tile(ctx):
     """(ctx, stores, values) of a tile program (ctx a copy whose program has its dots
     lowered, when it has any), or None."""
-    program = _lower_dots(_constants(ctx.program))
+    program = _lower_dots(_constants(ctx.program), ctx)
     if program is not ctx.program:
         ctx = copy.copy(ctx)
         ctx.program = program
@@ -1321,7 +1375,7 @@ class TilePlan(GenericPlan):
             self.lds_bytes += 2 * size * (8 if w in ("double", "long long") else (1 if w == "bool" else 4))
             self.carried_arrays[(i, n)] = (arr, size)
         self.found_types = {}
-        self.red_index = {id(r): k for k, r in enumerate(v for v in values if v.op == "reduce")}
+        self.red_index = {id(r): k for k, r in enumerate(v for v in values if v.op in ("reduce", "mdot"))}
         self.emitted = set()
         em = _TileEmitter(self)
         if self.inplace:  # side effects (which read no stored tensor) first, then the staged stores
@@ -1354,10 +1408,10 @@ class TilePlan(GenericPlan):
             else:  # "update": the carried values of loop x
                 roots = list(program.loops[x].update.values())
             for v in _walk(roots):
-                if v.op == "reduce" and id(v) not in self.emitted and (
+                if v.op in ("reduce", "mdot") and id(v) not in self.emitted and (
                         self.nest is None or self.nest.scopes[id(v)] == scope):
                     self.emitted.add(id(v))
-                    blocks.append(self._reduction_block(em, v))
+                    blocks.append(self._reduction_block(em, v) if v.op == "reduce" else self._mdot_block(em, v))
             if kind == "loop":
                 blocks += self._loop_blocks(em, x)
             elif kind == "effect":
@@ -1440,6 +1494,65 @@ class TilePlan(GenericPlan):
             compute.append("\n".join([head, *body, f"      {arr}[j] = {value}", end]))
             write.append("\n".join([head, lookup, skip, f"      p_{out}[oi] = {arr}[j];", end]))
         return compute + ["    __syncthreads();"] + write
+
+    def _mdot_block(self, em, v):
+        """``dot`` on the matrix core: both operands staged into LDS as [row][k] (k
+        contiguous, rows padded by 16 bytes), masked elements as zero; each wave takes 32 x 32
+        output blocks, ``v_mfma_f32_32x32x16`` per 16-deep k slice, into an fp32 LDS array."""
+        k_id = self.red_index[id(v)]
+        x, y, tx, ty = v.args
+        sx, sy = self.shapes[id(x)], self.shapes[id(y)]
+        m, kk = (sx[1], sx[0]) if tx else sx
+        n = sy[0] if ty else sy[1]
+        pitch = kk + 8
+        a, b, arr = f"da{k_id}", f"db{k_id}", f"red{k_id}"
+        lines = [f"    {{  // dot on the matrix core: [{m}, {kk}] x [{kk}, {n}]"]
+        t = None
+        for name, val, rows, trans, tag in ((a, x, m, tx, f"ma{k_id}_"), (b, y, n, not ty, f"mb{k_id}_")):
+            # element j of the staged operand: row j / kk, k j % kk
+            r, c = f"(j / {kk}LL)", f"(j % {kk}LL)"
+            body = em.context(val, (c, r) if trans else (r, c), tag)
+            tv = em.type_of(val)
+            if t is None:
+                t = tv
+            if tv != t or t not in ("float16", "bfloat16"):
+                raise LoweringError("a matrix-core dot needs two operands of one 16-bit float type")
+            st = "st_f16" if t == "float16" else "st_bf16"
+            mask = em.mask_of(val)
+            value = f"{st}({em.operand(val, t)})"
+            if mask:
+                value = f"(({mask}) ? {value} : (unsigned short)0)"
+            lines += [f"      for (long long j = tid; j < {rows * kk}LL; j += 256) {{", *["  " + x for x in body],
+                      f"        {name}[(j / {kk}LL) * {pitch}LL + (j % {kk}LL)] = {value};", "      }"]
+            self.decls.append(f"  __shared__ __attribute__((aligned(16))) unsigned short {name}[{rows * pitch}];")
+            self.lds_bytes += rows * pitch * 2
+        frag = "nt_half8" if t == "float16" else "nt_bf16x8"
+        mfma = "__builtin_amdgcn_mfma_f32_32x32x16_" + ("f16" if t == "float16" else "bf16")
+        nb = n // 32
+        lines += [
+            "      __syncthreads();",
+            "      {",
+            "        const int lane = tid & 63, wave = tid >> 6;",
+            f"        for (int blk = wave; blk < {(m // 32) * nb}; blk += 4) {{",
+            f"          const int bm = blk / {nb}, bn = blk % {nb};",
+            "          nt_floatx16 acc = {};",
+            f"          for (int k0 = 0; k0 < {kk}; k0 += 16) {{",
+            f"            const {frag} fa = *(const {frag}*)({a} + (bm * 32 + (lane & 31)) * {pitch} + k0 + 8 * (lane >> 5));",
+            f"            const {frag} fb = *(const {frag}*)({b} + (bn * 32 + (lane & 31)) * {pitch} + k0 + 8 * (lane >> 5));",
+            f"            acc = {mfma}(fa, fb, acc, 0, 0, 0);",
+            "          }",
+            "          for (int r = 0; r < 16; ++r)",
+            f"            {arr}[(bm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * {n} + bn * 32 + (lane & 31)] = acc[r];",
+            "        }",
+            "      }",
+            "    }",
+            "    __syncthreads();",
+        ]
+        self.decls.append(f"  __shared__ float {arr}[{m * n}];")
+        self.lds_bytes += m * n * 4
+        self.lds[id(v)] = (arr, (m, n))
+        self.types[id(v)] = "float32"
+        return "\n".join(lines)
 
     def _store_block(self, em, out, v):
         ctx = self.ctx

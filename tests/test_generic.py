@@ -995,6 +995,85 @@ def test_dot_tile_programs(dtype):
     torch.testing.assert_close(rows, ref.sum(dim=1), rtol=tol, atol=tol * 8)
 
 
+DOT_K, DOT_N = Symbol("DOT_K", meta=True), Symbol("DOT_N", meta=True)
+
+
+def dot_padded_arrangement(x, w, o):
+    # one k-tile of DOT_K over a K that may be shorter (masked columns of x, rows of w)
+    xt = x.tile((DOT_BM, DOT_K))
+    return xt, w.tile((DOT_K, DOT_N)).expand((xt.shape[0], -1)), o.tile((DOT_BM, DOT_N))
+
+
+def test_matrix_core_dot_programs_compile():
+    # 16-bit operands with M, N multiples of 32 and K of 16: the dot runs on the matrix core
+    cases = ((dot_application, (128, 64), (64, 96), "f16", torch.float16),
+             (dot_trans_application, (128, 64), (96, 64), "bf16", torch.bfloat16))
+    for application, sx, sw, suffix, dtype in cases:
+        h = ninetoothed.make(dot_arrangement, application, (Tensor(2), Tensor(2), Tensor(2)))
+        plan = _plan(h, torch.empty(sx, dtype=dtype), torch.empty(sw, dtype=dtype), torch.empty(128, 96), DOT_BM=32)
+        src = plan.source()
+        assert f"__builtin_amdgcn_mfma_f32_32x32x16_{suffix}" in src and "__shared__ float red0[3072]" in src
+        assert len(GenericPlan.compile(src)) > 1000
+    # fp32 operands, or shapes off the 32 x 32 x 16 grid, keep the fp32 reduction
+    h = ninetoothed.make(dot_arrangement, dot_application, (Tensor(2), Tensor(2), Tensor(2)))
+    for dtype, sw in ((torch.float32, (64, 96)), (torch.float16, (64, 24))):
+        plan = _plan(h, torch.empty((128, 64), dtype=dtype), torch.empty(sw, dtype=dtype), torch.empty(128, sw[1]),
+                     DOT_BM=32)
+        assert "mfma" not in plan.source()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+def test_matrix_core_dot_programs(dtype):
+    g = torch.Generator().manual_seed(25)
+    x = (torch.randn(128, 64, generator=g) / 4).to(dtype).cuda()
+    w = (torch.randn(64, 96, generator=g) / 4).to(dtype).cuda()
+    ref = x.float() @ w.float()
+    o = torch.empty(128, 96, dtype=torch.float32, device="cuda")
+    ninetoothed.make(dot_arrangement, dot_application, (Tensor(2), Tensor(2), Tensor(2)))(x, w, o, DOT_BM=32)
+    torch.testing.assert_close(o, ref, rtol=1e-4, atol=1e-4)  # exact products, fp32 sums
+    o2 = torch.empty(128, 96, dtype=dtype, device="cuda")
+    ninetoothed.make(dot_arrangement, dot_trans_application, (Tensor(2), Tensor(2), Tensor(2)))(
+        x, w.t().contiguous(), o2, DOT_BM=64)
+    torch.testing.assert_close(o2.float(), (ref * 0.5 + 1.0).to(dtype).float(), rtol=1e-2, atol=1e-2)
+    # K = 50 in one 64-deep k-tile: the masked columns of x (other = 1) and rows of w
+    # take no part, as in the reference's dot emitter
+    xp = (torch.randn(96, 50, generator=g) / 4).to(dtype).cuda()
+    wp = (torch.randn(50, 64, generator=g) / 4).to(dtype).cuda()
+    op = torch.empty(96, 64, dtype=torch.float32, device="cuda")
+    ninetoothed.make(dot_padded_arrangement, dot_application, (Tensor(2, other=1.0), Tensor(2, other=1.0), Tensor(2)))(
+        xp, wp, op, DOT_BM=32, DOT_K=64, DOT_N=64)
+    torch.testing.assert_close(op, xp.float() @ wp.float(), rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.gpu
+def test_matrix_core_dot_in_a_long_loop():
+    # the overlapping k-tiles matmul with 32 x 32 x 16 tiles and K = 576: 71 matrix-core dots
+    # in a real loop (checked against the oracle's evaluation of the same arrangement)
+    import programs as pg
+
+    def overlap(lhs, rhs, output, BM=32, BN=32, BK=16):
+        out = output.tile((BM, BN))
+        lt = lhs.tile((BM, BK), strides=(-1, 8)).tile((1, -1)).expand((-1, out.shape[1]))
+        lt.dtype = lt.dtype.squeeze(0)
+        rt = rhs.tile((BK, BN), strides=(8, -1)).tile((-1, 1)).expand((out.shape[0], -1))
+        rt.dtype = rt.dtype.squeeze(1)
+        return lt, rt, out
+
+    g = torch.Generator().manual_seed(26)
+    a = (torch.randn(64, 576, generator=g) / 8).half().cuda()
+    b = (torch.randn(576, 96, generator=g) / 8).half().cuda()
+    out = torch.empty(64, 96, dtype=torch.float16, device="cuda")
+    h = ninetoothed.make(overlap, pg.matmul_application, pg.matmul_tensors())
+    plan = _plan(h, a, b, out)
+    assert plan.nest is not None and "mfma_f32_32x32x16_f16" in plan.source()
+    h(a, b, out)
+    from oracle import apply
+
+    ref = apply.matmul(a.float().cpu().numpy(), b.float().cpu().numpy(), "float16", overlap, block=(32, 32, 16))
+    torch.testing.assert_close(out.float().cpu(), torch.from_numpy(ref), rtol=1e-2, atol=1e-2)
+
+
 @pytest.mark.gpu
 def test_overlapping_k_tiles_matmul_runs_as_written():
     # k-tiles of size 16 at stride 8 (each k visited twice, the last tiles masked past K):
