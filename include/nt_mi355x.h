@@ -120,10 +120,12 @@ int nt_max_pool2d_bf16(const void* x, const int64_t* x_strides, void* y, const i
                        int64_t dh, int64_t dw, hipStream_t stream);
 
 /* One kernel configuration of max_pool2d, for the auto-tuner: the arguments of
- * nt_max_pool2d_* plus `config` (0 = as nt_max_pool2d_* choose; 1 = the plane kernel:
+ * nt_max_pool2d_* plus `config` (0 = as nt_max_pool2d_* choose; 1 = the vector kernels:
  * 16-bit, 2-wide windows of stride 2 inside the input, unit inner strides, 16-byte aligned
- * rows, Q a multiple of 8; 2 = the element-wise kernel, any shape).  A forced plane kernel
- * whose conditions do not hold returns NT_ERR_INVALID before launching.  Replaces the
+ * input rows; 2-high windows with Q a multiple of 4 take the pair-row kernel, others the
+ * per-plane kernel with Q a multiple of 8; 2 = the element-wise kernel, any shape; 3 = the
+ * flat kernel: 2-high windows, Q a multiple of 8).  A forced kernel whose conditions do not
+ * hold returns NT_ERR_INVALID before launching.  Replaces the
  * per-configuration launchers of the reference's auto-tuner for the max_pool2d
  * application (reference tests/test_max_pool2d.py:13-64). */
 int nt_max_pool2d_config_f32(const void* x, const int64_t* x_strides, void* y, const int64_t* y_strides,

@@ -4,12 +4,13 @@
 // written once.  Max involves no rounding, so the result is bit-exact for any
 // evaluation order; fp16/bf16 values are compared after an exact widening to fp32.
 //
-// Fast path (the common non-overlapping 2-wide window on 16-bit data, unit inner
-// strides, no padding or dilation): a lane produces 8 consecutive outputs of a row from
-// kh input rows of 16 elements, i.e. 2*kh 16-byte loads and one 16-byte store.  For 2-high
-// windows the lanes walk the output vectors of all planes in one flat order, four per lane
-// per step with all their loads issued first (pool_w2_flat_kernel); otherwise one
-// workgroup per (n, c) plane.  Everything else runs the generic kernel, one lane per output.
+// Fast paths (the common non-overlapping 2-wide window on 16-bit data, unit inner
+// strides, no padding or dilation).  2-high windows: a lane takes 8 consecutive inputs of a
+// window's first row and the same columns of its second row (4 outputs), consecutive lanes
+// consecutive units over all planes in one flat order, eight per lane per step with all
+// their loads issued first (pool_w2_pair_kernel).  Taller windows: one workgroup per (n, c)
+// plane, a lane producing 8 consecutive outputs from kh input rows of 16 elements
+// (pool_w2_plane_kernel).  Everything else runs the generic kernel, one lane per output.
 #include "nt_common.h"
 
 #include <algorithm>
@@ -85,10 +86,11 @@ __global__ __launch_bounds__(256) void pool_w2_plane_kernel(const uint16_t* __re
   }
 }
 
-// config: 0 = the plane kernel where its conditions hold, else the element-wise kernel;
-// 1 = plane kernel; 2 = element-wise kernel.  A forced plane kernel whose conditions do not
+// config: 0 = the pair kernel for 2-high windows, else the plane kernel, where their
+// conditions hold, else the element-wise kernel; 1 = those vector kernels only; 2 =
+// element-wise kernel; 3 = the flat kernel below.  A forced kernel whose conditions do not
 // hold returns NT_ERR_INVALID unlaunched.
-// kh == 2 form of the plane kernel: output vector g of the flattened (plane, row, vector)
+// Flat kernel (kh == 2 form of the plane kernel): output vector g of the flattened (plane, row, vector)
 // order, U = 4 per lane per grid-stride step, the 16 loads of a step issued before any max
 // (one workgroup per plane left a ragged last pass per plane and only four loads in flight
 // per lane).  Indices fit 32 bits (the launcher checks).
@@ -148,12 +150,64 @@ __global__ __launch_bounds__(256) void pool_w2_flat_kernel(const uint16_t* __res
   }
 }
 
+// 2-wide windows of stride 2 (2-high, any vertical stride and dilation) on 16-bit data: a
+// unit is 8 consecutive inputs of a window's first row and the same columns of its second
+// row, giving 4 outputs.  Consecutive lanes take consecutive units, so each 16-byte load
+// instruction reads contiguous chunks of one row (whole cache lines, where two half-rows
+// per instruction would leave each line half used) and each 8-byte store continues the
+// previous lane's.  U units per lane per step, all loads issued first.
+template <typename T>
+__global__ __launch_bounds__(256) void pool_w2_pair_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
+                                                           PoolShape s, int upp, int upr, int total) {
+  constexpr int U = 8;
+  const int stride = (int)gridDim.x * 256;
+  const int64_t xh = s.xs[2], yh = s.ys[2], sh = s.sh, dh = s.dh, C = s.C;
+  auto locate = [&](int g, const uint16_t*& row, uint16_t*& out) {
+    const int plane = g / upp, within = g - plane * upp;
+    const int p = within / upr, j = within - p * upr;
+    const int64_t n = plane / C, c = plane - n * C;
+    row = x + n * s.xs[0] + c * s.xs[1] + p * sh * xh + j * 8;
+    out = y + n * s.ys[0] + c * s.ys[1] + p * yh + j * 4;
+  };
+  auto finish = [&](const u32x4& a, const u32x4& b, uint16_t* out) {
+    u32x2 o;
+    uint16_t* po = (uint16_t*)&o;
+    const uint16_t* pa = (const uint16_t*)&a;
+    const uint16_t* pb = (const uint16_t*)&b;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      po[j] = elem<T>::from_float(fmaxf(fmaxf(elem<T>::to_float(pa[2 * j]), elem<T>::to_float(pa[2 * j + 1])),
+                                        fmaxf(elem<T>::to_float(pb[2 * j]), elem<T>::to_float(pb[2 * j + 1]))));
+    __builtin_nontemporal_store(o, (u32x2*)out);
+  };
+  int g = (int)blockIdx.x * 256 + (int)threadIdx.x;
+  for (; g + (U - 1) * stride < total; g += U * stride) {  // the launcher keeps total + U * stride within int
+    const uint16_t* row[U];
+    uint16_t* out[U];
+    u32x4 a[U], b[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      locate(g + u * stride, row[u], out[u]);
+      a[u] = *(const u32x4*)row[u];
+      b[u] = *(const u32x4*)(row[u] + dh * xh);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) finish(a[u], b[u], out[u]);
+  }
+  for (; g < total; g += stride) {
+    const uint16_t* row;
+    uint16_t* out;
+    locate(g, row, out);
+    finish(*(const u32x4*)row, *(const u32x4*)(row + dh * xh), out);
+  }
+}
+
 template <typename T>
 static int pool_launch(const void* x, const int64_t* xs, void* y, const int64_t* ys, int64_t N, int64_t C, int64_t H,
                        int64_t W, int64_t P, int64_t Q, int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph,
                        int64_t pw, int64_t dh, int64_t dw, hipStream_t stream, int config = 0) {
   typedef typename elem<T>::storage S;
-  if (config < 0 || config > 2) return NT_ERR_INVALID;
+  if (config < 0 || config > 3) return NT_ERR_INVALID;
   if (N < 0 || C < 0 || H < 0 || W < 0 || P < 0 || Q < 0 || kh <= 0 || kw <= 0 || sh <= 0 || sw <= 0 || dh <= 0 ||
       dw <= 0 || ph < 0 || pw < 0)
     return NT_ERR_INVALID;
@@ -166,13 +220,27 @@ static int pool_launch(const void* x, const int64_t* xs, void* y, const int64_t*
                     (xs[0] * 2) % 16 == 0 && (xs[1] * 2) % 16 == 0 && (xs[2] * 2) % 16 == 0 &&
                     (ys[0] * 2) % 16 == 0 && (ys[1] * 2) % 16 == 0 && (ys[2] * 2) % 16 == 0 && N * C <= 0x7fffffffLL &&
                     H * xs[2] <= 0x7fffffffLL && P * ys[2] <= 0x7fffffffLL;
-  if (config == 1 && !fast) return NT_ERR_INVALID;
+  // the pair kernel: as `fast`, with 4 outputs (8 bytes) per unit instead of 8
+  const bool pair = sizeof(S) == 2 && kh == 2 && kw == 2 && sw == 2 && dw == 1 && ph == 0 && pw == 0 && xs[3] == 1 &&
+                    ys[3] == 1 && Q % 4 == 0 && windows_inside && (uintptr_t)x % 16 == 0 && (uintptr_t)y % 8 == 0 &&
+                    (xs[0] * 2) % 16 == 0 && (xs[1] * 2) % 16 == 0 && (xs[2] * 2) % 16 == 0 &&
+                    (ys[0] * 2) % 8 == 0 && (ys[1] * 2) % 8 == 0 && (ys[2] * 2) % 8 == 0 && N * C <= 0x7fffffffLL &&
+                    H * xs[2] <= 0x7fffffffLL && P * ys[2] <= 0x7fffffffLL;
+  // unit counts stay below 2^31 - 2^24, so a lane's next unit index (at most 8 grid strides of
+  // at most 2^19 lanes further) still fits an int
+  constexpr int64_t MAX_UNITS = 0x7fffffffLL - (1LL << 24);
+  const int64_t upp = P * (Q / 4), total_units = N * C * upp;
+  if ((config == 1 && !fast && !pair) || (config == 3 && !(fast && kh == 2))) return NT_ERR_INVALID;
   const int64_t vpp = P * (Q / 8), total_vec = N * C * vpp;
-  if (fast && config != 2 && kh == 2 && total_vec <= 0x7fffffffLL) {
+  if (pair && (config == 0 || config == 1) && total_units <= MAX_UNITS) {
+    const int64_t blocks = std::min<int64_t>(cdiv(total_units, 256 * 8), 256 * 8);
+    hipLaunchKernelGGL(pool_w2_pair_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, stream, (const uint16_t*)x,
+                       (uint16_t*)y, s, (int)upp, (int)(Q / 4), (int)total_units);
+  } else if (fast && config != 2 && kh == 2 && total_vec <= MAX_UNITS) {
     const int64_t blocks = std::min<int64_t>(cdiv(total_vec, 256 * 4), 256 * 8);
     hipLaunchKernelGGL(pool_w2_flat_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, stream, (const uint16_t*)x,
                        (uint16_t*)y, s, (int)vpp, (int)(Q / 8), (int)total_vec);
-  } else if (fast && config != 2) {
+  } else if (fast && config != 2 && config != 3) {
     hipLaunchKernelGGL(pool_w2_plane_kernel<T>, dim3((unsigned)(N * C)), dim3(256), 0, stream, (const uint16_t*)x,
                        (uint16_t*)y, s);
   } else {

@@ -594,7 +594,7 @@ def test_softmax_configs(config, dtype, cols, block):
         assert torch.allclose(y.float(), ref, atol=tol, rtol=tol)
 
 
-@pytest.mark.parametrize("config", (1, 2))
+@pytest.mark.parametrize("config", (1, 2, 3))
 def test_max_pool2d_configs(config):
     from ninetoothed_amd.errors import KernelLaunchError
 
@@ -602,12 +602,24 @@ def test_max_pool2d_configs(config):
     y = torch.empty((4, 16, 56, 56), dtype=torch.float16, device=DEV)
     kernels.max_pool2d(x, y, (2, 2), config=config)
     assert torch.equal(y, F.max_pool2d(x, (2, 2)))
+    # 2-high windows with Q a multiple of 4 but not of 8 (the pair-row kernel's, not the
+    # flat kernel's), an input one column wider than the windows reach, a strided batch,
+    # bf16, and a unit count that is no multiple of the grid's
+    x3 = _rand((3, 7, 26, 48), torch.bfloat16, 15, -4.0, 4.0)[:, :, :, :41]
+    ref3 = F.max_pool2d(x3, (2, 2))
+    y3 = torch.empty_like(ref3)
+    if config == 3:
+        with pytest.raises(KernelLaunchError):
+            kernels.max_pool2d(x3, y3, (2, 2), config=3)
+    else:
+        kernels.max_pool2d(x3, y3, (2, 2), config=config)
+        assert torch.equal(y3, ref3)
     x2 = _randn((2, 5, 17, 19), torch.float16, 14)
     ref = F.max_pool2d(x2, (3, 2), stride=(2, 3), padding=(1, 1))
     y2 = torch.empty_like(ref)
-    if config == 1:  # the plane kernel takes 2-wide windows of stride 2 only
+    if config in (1, 3):  # the vector kernels take 2-wide windows of stride 2 only
         with pytest.raises(KernelLaunchError):
-            kernels.max_pool2d(x2, y2, (3, 2), stride=(2, 3), padding=(1, 1), config=1)
+            kernels.max_pool2d(x2, y2, (3, 2), stride=(2, 3), padding=(1, 1), config=config)
     else:
         kernels.max_pool2d(x2, y2, (3, 2), stride=(2, 3), padding=(1, 1), config=2)
         assert torch.equal(y2, ref)
