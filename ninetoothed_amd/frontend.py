@@ -287,7 +287,7 @@ class Lowerer:
             return
         if isinstance(s, ast.Return):
             if s.value is not None:
-                raise LoweringError("applications do not return values")
+                raise LoweringError("applications do not return values (a helper may end with `return value`)")
             return
         if isinstance(s, ast.Assign):
             if len(s.targets) != 1:
@@ -664,8 +664,13 @@ class Lowerer:
             if pname not in bindings:
                 raise LoweringError(f"missing argument `{pname}` for helper `{func.__name__}`")
         callee = _Frame(func, node, bindings, names)
-        self._block(callee, node.body)
-        return None
+        body = list(node.body)
+        # a trailing `return value` is the call's value (reference frontend/python.py:226-270)
+        result = body.pop() if body and isinstance(body[-1], ast.Return) else None
+        self._block(callee, body)
+        if result is None or result.value is None:
+            return None
+        return self._expr(callee, result.value)
 
 
 def _assigned_names(stmts):

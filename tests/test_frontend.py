@@ -103,6 +103,22 @@ def test_elementwise_program_outside_the_families_is_generic():
     assert _specialize(h, torch.empty(10), torch.empty(10), torch.empty(10))["family"] == "generic"
 
 
+def _sum_of(a, b):
+    s = a + b
+    return s
+
+
+def test_helper_with_a_trailing_return_is_inlined():
+    # reference frontend/python.py:226-270: a helper's trailing `return value` is the call's value
+    def app(lhs, rhs, output):
+        output = _sum_of(lhs, rhs)  # noqa: F841
+
+    bs = Symbol("BS", meta=True)
+    h = ninetoothed.make(lambda a, b, c: (a.tile((bs,)), b.tile((bs,)), c.tile((bs,))), app,
+                         (Tensor(1), Tensor(1), Tensor(1)))
+    assert _specialize(h, torch.empty(10), torch.empty(10), torch.empty(10))["family"] == "add"
+
+
 def test_reduction_program_is_generic():
     def app(lhs, rhs, output):
         output = ntl.sum(lhs, 0) + rhs  # noqa: F841
