@@ -158,3 +158,27 @@ def test_uniform_mapping_range_and_extremes():
     assert r.min() >= 0.0 and r.max() < 1.0 and abs(r.mean() - 0.5) < 0.01
     n = philox.randn(1234, np.arange(1 << 16))
     assert abs(n.mean()) < 0.02 and abs(n.std() - 1.0) < 0.02
+
+
+def test_random_streams_are_distributed_and_independent():
+    # What the mathematics fixes for the parts the known answers leave open (the seed and
+    # offset -> key and counter mapping, Box-Muller): uniform and normal marginals
+    # (Kolmogorov-Smirnov on 2^18 draws: a Box-Muller fed one word twice, or a uniform
+    # map that drops the sign fold, fails), no correlation between neighbouring offsets or
+    # between seeds that differ only in their high word (a mapping that ignored it, or put
+    # the offset in the key, fails).
+    from scipy import stats
+
+    from oracle import philox
+
+    off = np.arange(1 << 18)
+    r = philox.rand(99, off).astype(np.float64)
+    n = philox.randn(99, off).astype(np.float64)
+    assert stats.kstest(r, "uniform").statistic < 0.005
+    assert stats.kstest(n, "norm").statistic < 0.005
+    assert abs(np.corrcoef(r[:-1], r[1:])[0, 1]) < 0.01
+    hi = philox.rand(99 + (1 << 32), off).astype(np.float64)
+    assert abs(np.corrcoef(r, hi)[0, 1]) < 0.01 and not np.array_equal(r, hi)
+    # the pair (u1, u2) behind randn is not one word twice: normals of neighbouring offsets
+    # are uncorrelated too, and their squares average 1
+    assert abs(np.corrcoef(n[:-1], n[1:])[0, 1]) < 0.01 and abs((n * n).mean() - 1.0) < 0.01
