@@ -363,7 +363,8 @@ def main():
     args = _args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
-              "(the hot path is single-GPU; see DESIGN.md for how it would shard).", file=sys.stderr)
+              "(the hot path runs on one GPU: every family is data-parallel over independent output units, "
+              "so one process per GPU would each take a shard of them).", file=sys.stderr)
         sys.exit(2)
     import torch
 
