@@ -57,6 +57,7 @@ def test_conv2d_geometry_is_recovered(padding):
     d = _specialize(h, _h((4, 64, 16, 16)), _h((512, 64, 3, 3)), _h((4, 512, 14 + 2 * ph, 14 + 2 * pw)),
                     padding_h=ph, padding_w=pw)
     assert d["family"] == "conv2d" and d["padding"] == padding and d["stride"] == (1, 1)
+    assert h._kernel.granularity == "blocked-linalg"  # reference compiler/passes.py:1070-1084: a dot, no exp
 
 
 @pytest.mark.parametrize("causal", (False, True))
@@ -83,6 +84,7 @@ def test_max_pool2d_window(ceil_mode):
     p = (64 - 3 + (2 if ceil_mode else 0)) // 3 + 1
     d = _specialize(h, _h((32, 3, 64, 64)), _h((32, 3, p, p)), WINDOW_HEIGHT=3, WINDOW_WIDTH=3)
     assert d["family"] == "max_pool2d" and d["window"] == (3, 3) and d["stride"] == (3, 3)
+    assert h._kernel.granularity == "parallel-reduction"  # a max reduction, no dot
 
 
 def test_add_matches():
