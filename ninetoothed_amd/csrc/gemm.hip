@@ -965,7 +965,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const u32x4 hi = *(const u32x4*)(lds + rd[1] + st + blk * 2048);
     return v8i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
   };
-  v8i fa[4], fb[2], fbn[2];
+  // The next tile's b fragments and its last-used a fragment (fa[3]) go into spare
+  // registers, so that every read of the next tile is issued two MFMAs before this tile
+  // ends (a read into fa[3] itself would have to follow this tile's last MFMA and leave its
+  // latency exposed at the next tile's first wait).
+  v8i fa[4], fb[2], fbn[2], fa3n;
   floatx16 acc[4][2];
   zero_acc(acc);
 
@@ -1003,7 +1007,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if constexpr (HAS1) {
         if constexpr (m == 0) fbn[0] = frag(b_rd, st1, 0);
         if constexpr (m == 1) fbn[1] = frag(b_rd, st1, 1);
-        if constexpr (j == 1) fa[i] = frag(a_rd, st1, i);
+        if constexpr (m == 2) fa3n = frag(a_rd, st1, 3);
+        if constexpr (j == 1 && i < 3) fa[i] = frag(a_rd, st1, i);
       }
       if constexpr (LOAD && m >= 1 && m <= 4) load_unit(m - 1, kt + 3);
       NT_F8FENCE();
@@ -1011,6 +1016,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if constexpr (HAS1) {
       fb[0] = fbn[0];
       fb[1] = fbn[1];
+      fa[3] = fa3n;
     }
   };
 #undef NT_F8FENCE
