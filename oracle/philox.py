@@ -19,12 +19,11 @@ float32 constant 4.6566127342e-10 (just below 2^-31).  ``randn`` is Box-Muller o
 two words mapped that way: u1 = max(u1, 1e-7), r = sqrt(-2 log u1), r * cos(2 pi u2).
 
 Pinned against the Random123 known-answer vectors for philox4x32-10 in
-tests/test_oracle_apply.py::test_philox_known_answers.  Parity unpinned: the mapping of
-(seed, offset) to key and counter and the Box-Muller composition of ``randn`` follow Triton's
-documented generator, which is not installed here and whose outputs no reference file holds;
-tests/test_oracle_apply.py::test_random_streams_are_distributed_and_independent checks what
-the mathematics fixes for them (uniform and normal marginals, independence of neighbouring
-offsets and of seeds that differ in their high word).
+tests/test_oracle_apply.py::test_philox_known_answers, and end to end (the (seed, offset) ->
+(key, counter) mapping, the uniform map and Box-Muller) against Triton 3.6.0's own outputs in
+tests/golden/triton_random.json (written by tests/golden/make_triton_random.py on Triton's
+CPU interpreter; randint and rand bit for bit, randn to 1e-6) in
+tests/test_oracle_apply.py::test_random_streams_match_tritons_generator.
 """
 
 import numpy as np

@@ -160,6 +160,26 @@ def test_uniform_mapping_range_and_extremes():
     assert abs(n.mean()) < 0.02 and abs(n.std() - 1.0) < 0.02
 
 
+def test_random_streams_match_tritons_generator():
+    # The reference's ntl.rand/randint/randn forward to Triton (reference
+    # src/ninetoothed/language.py:1-26); tests/golden/triton_random.json holds Triton 3.6.0's
+    # own outputs (CPU interpreter) for six seeds (two above 2^32) and 32 offsets up to
+    # 2^31 - 1: the oracle's seed/offset -> key/counter mapping and Box-Muller follow it.
+    import json
+    from pathlib import Path
+
+    from oracle import philox
+
+    fixture = json.loads((Path(__file__).parent / "golden" / "triton_random.json").read_text())
+    for case in fixture["cases"]:
+        off = np.asarray(case["offsets"], dtype=np.int64)
+        got = philox.randint(case["seed"], off).astype(np.uint32).view(np.int32)
+        assert got.tolist() == case["randint"], case["seed"]
+        assert np.array_equal(philox.rand(case["seed"], off), np.asarray(case["rand"], dtype=np.float32))
+        np.testing.assert_allclose(philox.randn(case["seed"], off), np.asarray(case["randn"], dtype=np.float32),
+                                   rtol=1e-6, atol=1e-6)
+
+
 def test_random_streams_are_distributed_and_independent():
     # What the mathematics fixes for the parts the known answers leave open (the seed and
     # offset -> key and counter mapping, Box-Muller): uniform and normal marginals
