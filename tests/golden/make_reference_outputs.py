@@ -10,7 +10,7 @@ The reference runs on Triton's CPU interpreter (TRITON_INTERPRET=1).  Its ``gene
 profile accepts CUDA tensors only (reference src/ninetoothed/targets.py:461-469), so this
 script re-registers that profile for CPU tensors in its own process.  Every program is the
 reference's own, imported from its test modules (tests/test_matmul.py, test_addmm.py,
-test_conv2d.py, test_attention.py, test_add.py), except
+test_conv2d.py, test_attention.py, test_dropout.py, test_add.py), except
 the fp32 matmul of the README (README.md:35-67), whose five-line application is restated
 below.  Kernels are made with one configuration each: the interpreter is too slow to tune.
 """
@@ -37,7 +37,7 @@ from ninetoothed.targets import default_platform_registry  # noqa: E402
 _registry = default_platform_registry()
 _registry.register(dataclasses.replace(_registry.get("generic"), device_types=("cpu",)), replace=True)
 
-from tests import test_add, test_addmm, test_attention, test_conv2d, test_matmul  # noqa: E402
+from tests import test_add, test_addmm, test_attention, test_conv2d, test_dropout, test_matmul  # noqa: E402
 
 
 def _gen(seed):
@@ -121,6 +121,15 @@ def main():
     # not here: Triton 3.6's interpreter fails on the reductions in the kernels the reference
     # generates for them, with an AttributeError inside the interpreter.  max_pool2d is pinned
     # bit for bit by F.max_pool2d; softmax by torch.softmax within tolerance.)
+
+    # dropout fp16, p = 0.3, a fixed seed (tests/test_dropout.py:10-24): ntl.rand through the
+    # whole program, x / (1 - p) in the reference's typing
+    x = _randn((349,), torch.float16, 17)
+    y = torch.empty_like(x)
+    k = ninetoothed.make(test_dropout.arrangement, test_dropout.application,
+                         (Tensor(1), Tensor(0), Tensor(0), Tensor(1)), max_num_configs=1)
+    k(x, 0.3, 1234567, y)
+    out.update(dropout_x=x, dropout_out=y)
 
     # add fp32 (tests/test_add.py:9-24)
     lhs, rhs = _randn((1000,), torch.float32, 15), _randn((1000,), torch.float32, 16)

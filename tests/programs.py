@@ -248,3 +248,14 @@ def make_add():
         output = lhs + rhs  # noqa: F841
 
     return add_kernel
+
+
+# ------------------------------------------------------------------- dropout (reference tests/test_dropout.py:10-24)
+def make_dropout():
+    def arrangement(input, p, seed, output, BLOCK_SIZE=ninetoothed.block_size()):
+        return input.tile((BLOCK_SIZE,)), p, seed, output.tile((BLOCK_SIZE,))
+
+    def application(input, p, seed, output):
+        output = ntl.where(ntl.rand(seed, input.offsets()) > p, input / (1 - p), 0)  # noqa: F841
+
+    return ninetoothed.make(arrangement, application, (Tensor(1), Tensor(0), Tensor(0), Tensor(1)))

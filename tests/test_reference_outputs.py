@@ -4,10 +4,11 @@ tests/golden/reference_outputs.npz holds small seeded inputs and what the refere
 kernels computed from them on Triton's CPU interpreter (written by
 tests/golden/make_reference_outputs.py; the reference's own programs from its test modules,
 the README's fp32 matmul, one configuration each).  CPU: the oracle reproduces them bit for
-bit for matmul (fp32 and fp16), addmm, conv2d and add, and attention to 2 ulp (exp2 and the
-accumulation order).  GPU: the MI355X kernels, through the Handle: fp16 matmul and conv2d to
-1 ulp, addmm to 1 ulp of the rounded product plus 1 of the output, attention to 2 ulps of
-max(|o|, 1) with at least 90 % bit for bit, fp32 matmul to 1e-5, add bit for bit.  (The interpreter cannot run the
+bit for matmul (fp32 and fp16), addmm, conv2d, add and dropout (Philox stream, p = 0.3, a
+seed of 1234567), and attention to 2 ulp (exp2 and the accumulation order).  GPU: the MI355X
+kernels, through the Handle: fp16 matmul and conv2d to 1 ulp, addmm to 1 ulp of the rounded
+product plus 1 of the output, attention to 2 ulps of max(|o|, 1) with at least 90 % bit for
+bit, fp32 matmul to 1e-5, add and dropout bit for bit.  (The interpreter cannot run the
 reference's softmax and max_pool2d kernels; those are pinned by torch closed forms, max_pool2d
 bit for bit.)
 """
@@ -19,9 +20,10 @@ import numpy as np
 import pytest
 
 import programs as pg
-from oracle import apply
+from oracle import apply, philox
 
 _Z = np.load(Path(__file__).parent / "golden" / "reference_outputs.npz")
+DROPOUT_P, DROPOUT_SEED = 0.3, 1234567  # the fixture script's call
 
 
 def _arr(key):
@@ -55,14 +57,20 @@ def _oracle(name):
                             functools.partial(pg.conv2d_arrangement, enable_padding=True), block=(32, 32, 32))
     if name == "add":
         return apply.add(_f32("add_lhs"), _f32("add_rhs"), 64)
+    if name == "dropout":
+        # reference tests/test_dropout.py:16-17: fp16 / fp32 scalar computes in fp32, rounded
+        # to fp16 at the store
+        x = _f32("dropout_x")
+        keep = philox.rand(DROPOUT_SEED, np.arange(x.size)) > np.float32(DROPOUT_P)
+        return np.where(keep, x / (np.float32(1) - np.float32(DROPOUT_P)), np.float32(0)).astype(np.float16)
     causal = name.endswith("1")
     return apply.attention(_f32("attention_q"), _f32("attention_k"), _f32("attention_v"), causal,
                            pg.attention_arrangement, block=(32, 32))
 
 
-_EXACT = ("matmul_fp32", "matmul_fp16", "addmm", "conv2d", "add")
+_EXACT = ("matmul_fp32", "matmul_fp16", "addmm", "conv2d", "add", "dropout")
 _OUT = {"matmul_fp32": "matmul_fp32_out", "matmul_fp16": "matmul_fp16_out", "addmm": "addmm_out",
-        "conv2d": "conv2d_out", "add": "add_out", "attention_causal0": "attention_out_causal0",
+        "conv2d": "conv2d_out", "add": "add_out", "dropout": "dropout_out", "attention_causal0": "attention_out_causal0",
         "attention_causal1": "attention_out_causal1"}
 
 
@@ -132,3 +140,8 @@ def test_kernels_match_the_reference_kernels():
     out = torch.empty_like(lhs)
     pg.make_add()(lhs, rhs, out)
     assert np.array_equal(out.cpu().numpy(), _f32("add_out"))
+    # dropout, bit for bit: the same Philox stream, the same fp32 quotient and rounding
+    x = _cuda("dropout_x")
+    y = torch.empty_like(x)
+    pg.make_dropout()(x, DROPOUT_P, DROPOUT_SEED, y)
+    assert np.array_equal(y.cpu().numpy().view(np.int16), _Z["dropout_out"])
