@@ -55,6 +55,10 @@ def _args():
                    help="launches timed one by one for the median (at least --steps)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="only run a plain 256 MiB device copy K times (scale for rocprofv3 FETCH/WRITE_SIZE)")
+    p.add_argument("--mfma-ceiling", action="store_true",
+                   help="only run the matrix-core ceiling probe (fp16 MFMAs back to back, zero and random operands)")
+    p.add_argument("--ceiling-iters", type=int, default=400_000,
+                   help="loop iterations of the ceiling probe (8 MFMAs per wave each)")
     return p.parse_args()
 
 
@@ -376,6 +380,10 @@ def main():
                           "ms_per_copy": sec * 1e3}), flush=True)
         return
 
+    if args.mfma_ceiling:
+        _mfma_ceiling(torch, args.ceiling_iters, 5)
+        return
+
     import ninetoothed_amd as ninetoothed
     import programs as pg
 
@@ -442,6 +450,91 @@ def main():
                         "blas_threads": _blas_threads(),
                         "reference_interpreter": "unavailable on the GPU box (the reference does not travel there)"}
     print(json.dumps(line), flush=True)
+
+
+# The matrix core's own ceiling on this board: every SIMD issues 32x32x16 fp16 MFMAs back to
+# back (eight independent accumulators, one wave per SIMD, one workgroup of four waves per
+# CU) for about a tenth of a second, with operands read once from memory: all zeros, or
+# random fp16 values rotated through four a and four b fragments so the operand registers
+# change at every instruction, as a GEMM's do.  No LDS, no memory traffic in the loop.
+_CEILING_SRC = r"""
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+extern "C" __global__ void __launch_bounds__(256) NAME(const half8* src, float* out, int iters) {
+  const int lane = threadIdx.x & 63;
+  const long w = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  half8 a[4], b[4];
+  for (int i = 0; i < 4; ++i) {
+    a[i] = src[(w * 8 + i) * 64 + lane];
+    b[i] = src[(w * 8 + 4 + i) * 64 + lane];
+  }
+  floatx16 acc[8];
+  for (int c = 0; c < 8; ++c)
+    for (int r = 0; r < 16; ++r) acc[c][r] = 0.0f;
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+      acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[c & 3], b[(c + (c >> 2)) & 3], acc[c], 0, 0, 0);
+  }
+  float s = 0.0f;
+  for (int c = 0; c < 8; ++c)
+    for (int r = 0; r < 16; ++r) s += acc[c][r];
+  out[w * 64 + lane] = s;
+}
+"""
+_CEILING_WGS = 256  # one per CU
+_CEILING_FLOPS_PER_ITER = _CEILING_WGS * 4 * 8 * 2 * 32 * 32 * 16
+
+
+def _mfma_ceiling(torch, iters, runs):
+    import ctypes
+
+    import ninetoothed_amd._lib as _lib
+    from ninetoothed_amd.generic import GenericPlan
+
+    lib = _lib.load()
+    waves = _CEILING_WGS * 4
+    out = torch.empty(waves * 64, dtype=torch.float32, device="cuda")
+    g = torch.Generator("cpu").manual_seed(0)
+    sources = {"zero": torch.zeros(waves * 8 * 64 * 8, dtype=torch.float16),
+               "random": torch.randn(waves * 8 * 64 * 8, generator=g).to(torch.float16)}
+    stream = torch.cuda.current_stream()
+    lines = []
+    for name, host in sources.items():
+        kernel = f"nt_mfma_ceiling_{name}"
+        blob = GenericPlan.compile(_CEILING_SRC.replace("NAME", kernel))
+        fn = ctypes.c_void_p()
+        buf = ctypes.create_string_buffer(blob, len(blob))
+        if lib.nt_rtc_load(buf, kernel.encode(), ctypes.byref(fn)) != 0:
+            raise RuntimeError("could not load the ceiling probe")
+        src = host.cuda()
+        args = [ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(out.data_ptr()), ctypes.c_int32(iters)]
+        params = (ctypes.c_void_p * 3)(*[ctypes.addressof(a) for a in args])
+
+        def launch():
+            status = lib.nt_rtc_launch(fn, _CEILING_WGS, 256, params, ctypes.c_void_p(stream.cuda_stream))
+            if status != 0:
+                raise RuntimeError(f"ceiling probe launch failed ({status})")
+
+        launch()  # warm-up: brings the board to its loaded clock
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(runs):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            launch()
+            b.record(stream)
+            torch.cuda.synchronize()
+            times.append(a.elapsed_time(b) / 1e3)
+        sec = sorted(times)[len(times) // 2]
+        tflops = _CEILING_FLOPS_PER_ITER * iters / sec / 1e12
+        line = {"probe": "mfma_ceiling", "operands": name, "mfma": "v_mfma_f32_32x32x16_f16", "iters": iters,
+                "median_ms": sec * 1e3, "runs": runs, "tflops": tflops, "frac_of_2.5PF": tflops * 1e12 / PEAK["fp16"],
+                # 1,024 SIMDs x 1,024 fp16 flops per SIMD cycle (32 cycles per 32x32x16 MFMA)
+                "implied_clock_ghz": tflops * 1e12 / (1024 * 1024) / 1e9}
+        print(json.dumps(line), flush=True)
+        lines.append(line)
+    return lines
 
 
 def _traffic():
