@@ -169,12 +169,14 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, const floatx16 
       if (row >= g.M) continue;
       const float4 v0 = *(const float4*)(stage + rr * COLS + cg);
       const float4 v1 = *(const float4*)(stage + rr * COLS + cg + 4);
-      float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-      for (int u = 0; u < 8; ++u) {
-        if (col + u >= g.N) break;
-        float r = g.alpha * round_through(v[u], g.round_dtype);
-        if (g.c) r += g.beta * load_c<C8>(g, row * g.sc_m + (col + u) * g.sc_n);
-        store_from_float(g.out, row * g.so_m + (col + u) * g.so_n, g.out_dtype, r);
+      const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {  // unrolled, so v stays in registers
+        if (col + u < g.N) {
+          float r = g.alpha * round_through(v[u], g.round_dtype);
+          if (g.c) r += g.beta * load_c<C8>(g, row * g.sc_m + (col + u) * g.sc_n);
+          store_from_float(g.out, row * g.so_m + (col + u) * g.so_n, g.out_dtype, r);
+        }
       }
     }
   }
@@ -453,7 +455,7 @@ __device__ __forceinline__ void load_lds16(u32x4 rs, uint32_t lds_addr, int voff
 // stride, 16-byte aligned rows; the launcher's c_pre).  acc holds a wave's 128 x (32 WJ)
 // block as 4 x WJ tiles of 32 x 32 (the 32x32 MFMA accumulator layout); lds + EPI +
 // 2 KiB * WJ * wave is the wave's staging.
-template <int WJ = 2>
+template <int WJ = 2, bool BOUNDED = false>
 __device__ __forceinline__ void dma_fast_epilogue(const GemmArgs& g, const floatx16 (&acc)[4][WJ], char* lds, int wave,
                                                   int lane, int64_t row_base, int64_t col_base) {
   // Fast epilogue: the accumulators go through this wave's staging (never touched by the k
@@ -466,10 +468,22 @@ __device__ __forceinline__ void dma_fast_epilogue(const GemmArgs& g, const float
   constexpr int COLS = 32 * WJ, CPR = COLS / 8, RPP = 64 / CPR;  // lanes per row, rows per pass
   constexpr int CPR_LOG2 = WJ == 2 ? 3 : 4;
   const int lrow = lane >> CPR_LOG2, lcol = lane & (CPR - 1);
+  // BOUNDED: rows and columns of this wave's block inside out (ragged M and N; N is a
+  // multiple of 8, so each lane's 8 columns are all inside or all outside).  Otherwise the
+  // launcher has checked that every tile is whole.
+  int rows_v = 128, cols_v = COLS;
+  if constexpr (BOUNDED) {
+    rows_v = (int)(g.M - row_base < 128 ? g.M - row_base : 128);
+    cols_v = (int)(g.N - col_base < COLS ? g.N - col_base : COLS);
+    if (rows_v <= 0 || cols_v <= 0) return;
+  }
+  const bool col_ok = !BOUNDED || lcol * 8 < cols_v;
   const bool has_c = g.c != nullptr;
+  // c through a buffer resource ending at the block's last valid element: rows past M read
+  // zeros instead of memory past the tensor.
   const __amdgpu_buffer_rsrc_t rsC = __builtin_amdgcn_make_buffer_rsrc(
       has_c ? (void*)((const uint16_t*)g.c + row_base * g.sc_m + col_base) : (void*)g.a, (short)0,
-      has_c ? (int)((127 * g.sc_m + COLS) * 2) : 0, 0x00020000);
+      has_c ? (int)(((rows_v - 1) * g.sc_m + cols_v) * 2) : 0, 0x00020000);
   const int vc = has_c ? (int)((lrow * g.sc_m + lcol * 8) * 2) : 0;
   const int c_row = has_c ? (int)(g.sc_m * 2) : 0;
   // out through plain global stores: a buffer store whose data registers a VALU instruction
@@ -520,7 +534,8 @@ __device__ __forceinline__ void dma_fast_epilogue(const GemmArgs& g, const float
         ow[d] = OUT_F16 ? ((uint32_t)float_to_f16_bits(r2[0]) | ((uint32_t)float_to_f16_bits(r2[1]) << 16))
                         : ((uint32_t)float_to_bf16_bits(r2[0]) | ((uint32_t)float_to_bf16_bits(r2[1]) << 16));
       }
-      __builtin_nontemporal_store(ow, (u32x4*)(o_lane + (i * 32 + h * 16 + t * RPP) * o_row));  // not re-read: no L2 allocation
+      if (!BOUNDED || (col_ok && i * 32 + h * 16 + t * RPP + lrow < rows_v))
+        __builtin_nontemporal_store(ow, (u32x4*)(o_lane + (i * 32 + h * 16 + t * RPP) * o_row));  // not re-read: no L2 allocation
     }
   };
   using OutF16 = std::integral_constant<bool, true>;
@@ -562,18 +577,26 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   int tm, tn;
   tile_of(blockIdx.x, g.tiles_m, g.tiles_n, tm, tn);
   const int64_t m0 = (int64_t)tm * GB_M, n0 = (int64_t)tn * GB_N;
-  const int nk = (int)(g.K / 32);
+  const int nk = (int)((g.K + 31) / 32);
 
   // Global side (byte offsets within each operand's panel fit in 32 bits; checked on the host).
-  const u32x4 rsA = dma::rsrc((const uint16_t*)g.a + m0 * g.sa_m, (uint32_t)(((GB_M - 1) * g.sa_m + g.K) * 2));
-  const u32x4 rsB = dma::rsrc((const uint16_t*)g.b + n0, (uint32_t)(((g.K - 1) * g.sb_k + GB_N) * 2));
+  // Each resource ends at the panel's last valid element, so rows of a past M and rows of b
+  // past K read zeros; columns of b past N read the next row's values, which reach only
+  // outputs past N (never stored).  With K not a multiple of 32, the chunks of a past K in
+  // the last k-tile are fetched from offset a_end (zeros): an a value past K would otherwise
+  // be the next row's, and an infinity there times a zero of b is not zero.
+  const int rows_a = (int)(g.M - m0 < GB_M ? g.M - m0 : GB_M), cols_b = (int)(g.N - n0 < GB_N ? g.N - n0 : GB_N);
+  const uint32_t a_end = (uint32_t)(((rows_a - 1) * g.sa_m + g.K) * 2);
+  const u32x4 rsA = dma::rsrc((const uint16_t*)g.a + m0 * g.sa_m, a_end);
+  const u32x4 rsB = dma::rsrc((const uint16_t*)g.b + n0, (uint32_t)(((g.K - 1) * g.sb_k + cols_b) * 2));
   // Load q (0, 1) of this wave per k-tile: a rows 32 wave + 16 q + lane / 4, LDS chunk
   // lane % 4; b rows 4 wave + 2 q + lane / 32, LDS bytes (lane % 32) * 16 of the row.
-  int va[2], vb[2];
+  int va[2], vb[2], va_last[2];
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
     const int ra = 32 * wave + 16 * q + (lane >> 2);
     va[q] = (int)(ra * g.sa_m * 2) + dma::asw(ra, lane & 3) * 16;
+    va_last[q] = (nk - 1) * 32 + dma::asw(ra, lane & 3) * 8 < g.K ? va[q] : (int)a_end;
     const int kb = 4 * wave + 2 * q + (lane >> 5);
     const int nb = 32 * (((lane & 31) >> 2) ^ dma::bsw(kb)) + 8 * (lane & 3);
     vb[q] = (int)(kb * g.sb_k * 2) + nb * 2;
@@ -583,7 +606,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   auto load_unit = [&](int u, int kt) {
     const int st = (kt % dma::STAGES) * dma::STAGE, q = u >> 1;
     if ((u & 1) == 0)
-      dma::load_lds16(rsA, lds0 + st + 2048 * wave + 1024 * q, va[q], kt * 64);
+      dma::load_lds16(rsA, lds0 + st + 2048 * wave + 1024 * q, kt == nk - 1 ? va_last[q] : va[q], kt * 64);
     else
       dma::load_lds16(rsB, lds0 + dma::B0 + st + 2048 * wave + 1024 * q, vb[q], kt * b_kstep);
   };
@@ -681,7 +704,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     gemm_epilogue<4, 2>(g, acc, (uint16_t*)lds, wave, lane, row_base, col_base);
     return;
   }
-  dma_fast_epilogue(g, acc, lds, wave, lane, row_base, col_base);
+  dma_fast_epilogue<2, true>(g, acc, lds, wave, lane, row_base, col_base);
 }
 
 // ----------------------------------------------------------------------------- fp32
@@ -873,22 +896,23 @@ static int gemm16_launch(GemmArgs g, hipStream_t stream, int config = 0) {
   if (tiles_m * tiles_n > 0x7fffffffLL) return NT_ERR_INVALID;
   g.tiles_m = (int)tiles_m;
   g.tiles_n = (int)tiles_n;
-  const bool fast = g.sa_k == 1 && g.sb_n == 1 && g.M % GB_M == 0 && g.N % GB_N == 0 && g.K % GB_K == 0 &&
-                    (uintptr_t)g.a % 16 == 0 && (uintptr_t)g.b % 16 == 0 && (g.sa_m * 2) % 16 == 0 &&
-                    (g.sb_k * 2) % 16 == 0;
+  const bool aligned = g.sa_k == 1 && g.sb_n == 1 && (uintptr_t)g.a % 16 == 0 && (uintptr_t)g.b % 16 == 0 &&
+                       (g.sa_m * 2) % 16 == 0 && (g.sb_k * 2) % 16 == 0;
+  const bool fast = aligned && g.M % GB_M == 0 && g.N % GB_N == 0 && g.K % GB_K == 0;
   const dim3 grid((unsigned)(tiles_m * tiles_n)), blk(G_THREADS);
   // DMA kernel: operand panel offsets fit its 32-bit buffer offsets and K holds at least the
-  // three 32-deep k-tiles its pipeline keeps in flight; otherwise the register-staged
-  // eight-wave kernel.
-  const bool dma_ok = (GB_M - 1) * g.sa_m + g.K <= 0x3fffffffLL && (g.K - 1) * g.sb_k + GB_N <= 0x3fffffffLL &&
-                      g.K >= 3 * 32;
+  // three 32-deep k-tiles its pipeline keeps in flight.  M may be ragged; N and K must be
+  // multiples of 8, so that every 16-byte operand chunk lies wholly inside or wholly past
+  // the matrix (its buffer resources return zeros past the end, per chunk).
+  const bool dma_ok = aligned && g.N % 8 == 0 && g.K % 8 == 0 && (GB_M - 1) * g.sa_m + g.K <= 0x3fffffffLL &&
+                      (g.K - 1) * g.sb_k + GB_N <= 0x3fffffffLL && g.K >= 3 * 32;
   // Its fast epilogue: 16-byte out vectors, and c (if any) fetched with 32-bit buffer offsets.
   const bool out_vec = g.out_dtype != NT_DTYPE_F32 && g.so_n == 1 && g.so_m >= 0 && g.so_m % 8 == 0 &&
                        (uintptr_t)g.out % 16 == 0;
   const bool c_vec = !g.c || (g.c_dtype == g.out_dtype && g.sc_n == 1 && g.sc_m >= 0 && g.sc_m % 8 == 0 && (uintptr_t)g.c % 16 == 0 &&
                               127 * g.sc_m + 128 <= 0x3fffffffLL);
-  if ((config == 1 && !(fast && dma_ok)) || (config == 2 && !fast)) return NT_ERR_INVALID;
-  const bool use_dma = config == 0 ? fast && dma_ok : config == 1;
+  if ((config == 1 && !dma_ok) || (config == 2 && !fast)) return NT_ERR_INVALID;
+  const bool use_dma = config == 0 ? dma_ok : config == 1;
   const bool use_fast8 = config == 0 ? fast && !dma_ok : config == 2;
   g.c_pre = use_dma && out_vec && c_vec;
   if (use_dma && g.c_pre)

@@ -294,12 +294,67 @@ def test_gemm_kernel_configs(config, dtype):
     assert torch.allclose(out.float(), ref.float(), atol=2e-2, rtol=1e-2)
 
 
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+@pytest.mark.parametrize("mnk", ((1000, 1024, 512), (1920, 1920, 1920), (264, 776, 1000), (300, 264, 104),
+                                 (520, 2056, 96), (4000, 4000, 4096)))
+def test_gemm_dma_ragged(mnk, dtype):
+    # The DMA kernel (forced) on ragged shapes: M anything, N and K multiples of 8; its
+    # buffer resources end at the last valid row and column, the last k-tile takes 8, 16 or
+    # 24 valid k (K = 1000, 104, 1000 % 32 = 8), and the epilogue stores only inside out.
+    m, n, k = mnk
+    a, b, c = _randn((m, k), dtype, 60), _randn((k, n), dtype, 61), _randn((m, n), dtype, 62)
+    rd = torch.float16 if dtype == torch.float16 else None
+    out = torch.full((m, n), 7.0, dtype=dtype, device=DEV)
+    kernels.gemm(a, b, out, c=c, alpha=0.5, beta=2.0, round_dtype=rd, config=1)
+    ref = _gemm_ref(a, b, c, 0.5, 2.0, rd)
+    tol = 1e-2 * max(1.0, math.sqrt(k) / 8)
+    assert torch.allclose(out.float(), ref.float(), atol=tol, rtol=1e-2)
+    # without c, fp32 out (the element-wise epilogue of the same kernel)
+    out32 = torch.empty((m, n), dtype=torch.float32, device=DEV)
+    kernels.gemm(a, b, out32, config=1)
+    assert torch.allclose(out32, a.float() @ b.float(), atol=tol, rtol=1e-3)
+
+
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+def test_gemm_dma_ragged_reads_nothing_past_the_matrix(dtype):
+    # a and b are views of larger buffers filled with inf past K (a's columns, b's rows) and
+    # past N (b's columns); out is a view whose neighbours must stay untouched.  A value
+    # past K reaching the product would give inf * 0 = nan; one past N, a wrong column.
+    m, n, k = 300, 264, 200
+    inf = float("inf")
+    abuf = torch.full((m, k + 8), inf, dtype=dtype, device=DEV)
+    abuf[:, :k] = _randn((m, k), dtype, 63)
+    bbuf = torch.full((k + 8, n + 8), inf, dtype=dtype, device=DEV)
+    bbuf[:k, :n] = _randn((k, n), dtype, 64)
+    a, b = abuf[:, :k], bbuf[:k, :n]
+    obuf = torch.full((m + 1, n + 8), 7.0, dtype=dtype, device=DEV)
+    out = obuf[:m, :n]
+    kernels.gemm(a, b, out, config=1)
+    assert torch.isfinite(out).all()
+    assert torch.allclose(out.float(), a.float() @ b.float(), atol=2e-2, rtol=1e-2)
+    assert torch.all(obuf[:, n:] == 7.0) and torch.all(obuf[m:] == 7.0)
+
+
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+def test_gemm_dma_ragged_broadcast_bias(dtype):
+    # c broadcast along rows (row stride 0) on a ragged shape: the fast epilogue's c resource.
+    m, n, k = 777, 520, 264
+    a, b = _randn((m, k), dtype, 65), _randn((k, n), dtype, 66)
+    c = _randn((n,), dtype, 67).expand(m, n)
+    out = torch.empty((m, n), dtype=dtype, device=DEV)
+    kernels.gemm(a, b, out, c=c, alpha=1.0, beta=0.5, config=1)
+    ref = _gemm_ref(a, b, c, 1.0, 0.5, None)
+    assert torch.allclose(out.float(), ref.float(), atol=2e-2, rtol=1e-2)
+
+
 def test_gemm_forced_config_rejects_unfit_call():
     from ninetoothed_amd.errors import KernelLaunchError
 
     a, b = _randn((300, 100), torch.float16, 53), _randn((100, 200), torch.float16, 54)
     out = torch.full((300, 200), 7.0, dtype=torch.float16, device=DEV)
-    for config in (1, 2):  # M, N not multiples of 256: rejected before launching
+    # K = 100 (rows of a not 16-byte aligned) fits neither the DMA kernel nor (M, N not
+    # multiples of 256) the register-staged one: rejected before launching
+    for config in (1, 2):
         with pytest.raises(KernelLaunchError):
             kernels.gemm(a, b, out, config=config)
     assert torch.all(out == 7.0)
