@@ -167,12 +167,14 @@ int nt_gemm_bf16(const void* a, int64_t sa_m, int64_t sa_k, const void* b, int64
                  int out_dtype, int64_t M, int64_t N, int64_t K, float alpha, float beta,
                  int round_dtype, hipStream_t stream);
 /* One kernel configuration of the 16-bit GEMM, for the auto-tuner: the arguments of
- * nt_gemm_f16/bf16 plus `config` (0 = the fastest kernel whose conditions hold, as
- * nt_gemm_*; 1 = the DMA kernel: a k-contiguous, b n-contiguous, 16-byte aligned rows, any
- * M, N and K multiples of 8, K at least 96; 2 = the register-staged eight-wave kernel: the
- * same layouts with M and N multiples of 256 and K of 64; 3 = the element-wise loader
- * kernel: anything).  A
- * forced configuration whose conditions do not hold returns NT_ERR_INVALID before
+ * nt_gemm_f16/bf16 plus `config`:
+ *   0 = the fastest kernel whose conditions hold, as nt_gemm_*;
+ *   1 = the DMA kernel: a k-contiguous; b n-contiguous (N a multiple of 8) or
+ *       k-contiguous; 16-byte aligned rows; any M; K a multiple of 8 and at least 96;
+ *   2 = the register-staged eight-wave kernel: a k-contiguous, b n-contiguous, M and N
+ *       multiples of 256, K of 64;
+ *   3 = the element-wise loader kernel: anything.
+ * A forced configuration whose conditions do not hold returns NT_ERR_INVALID before
  * launching.  Replaces the per-configuration launchers the reference's auto-tuner times
  * (src/ninetoothed/compiler/driver.py:975-1031, src/ninetoothed/auto_tuner.py:14-202). */
 int nt_gemm_config_f16(const void* a, int64_t sa_m, int64_t sa_k, const void* b, int64_t sb_k, int64_t sb_n,

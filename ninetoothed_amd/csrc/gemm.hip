@@ -566,7 +566,10 @@ __device__ __forceinline__ void dma_fast_epilogue(const GemmArgs& g, const float
 // FAST_EPI: the launcher's c_pre condition holds (16-bit out and c of one type, unit column
 // stride, aligned rows); the other instance finishes through the element-wise epilogue.  Two
 // instances so that the fast one holds no code of the other (whose registers would spill).
-template <typename T, bool FAST_EPI>
+// BT: b is k-contiguous (column-major [K, N], i.e. rows of b^T, the layout of x @ w.t());
+// its tiles then go to LDS exactly as a's do (rows of 64 bytes, XOR chunk swizzle) and its
+// fragments are single ds_read_b128, with no transposing reads.
+template <typename T, bool FAST_EPI, bool BT = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_dma_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) char lds[dma::EPI + 8 * 4096];
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
@@ -588,27 +591,38 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int rows_a = (int)(g.M - m0 < GB_M ? g.M - m0 : GB_M), cols_b = (int)(g.N - n0 < GB_N ? g.N - n0 : GB_N);
   const uint32_t a_end = (uint32_t)(((rows_a - 1) * g.sa_m + g.K) * 2);
   const u32x4 rsA = dma::rsrc((const uint16_t*)g.a + m0 * g.sa_m, a_end);
-  const u32x4 rsB = dma::rsrc((const uint16_t*)g.b + n0, (uint32_t)(((g.K - 1) * g.sb_k + cols_b) * 2));
+  // b^T (BT) ends at its last valid row (column of b) like a; its chunks past K in the last
+  // k-tile read zeros the same way.
+  const uint32_t b_end = BT ? (uint32_t)(((cols_b - 1) * g.sb_n + g.K) * 2) : (uint32_t)(((g.K - 1) * g.sb_k + cols_b) * 2);
+  const u32x4 rsB = dma::rsrc((const uint16_t*)g.b + (BT ? n0 * g.sb_n : n0), b_end);
   // Load q (0, 1) of this wave per k-tile: a rows 32 wave + 16 q + lane / 4, LDS chunk
-  // lane % 4; b rows 4 wave + 2 q + lane / 32, LDS bytes (lane % 32) * 16 of the row.
-  int va[2], vb[2], va_last[2];
+  // lane % 4; b rows 4 wave + 2 q + lane / 32, LDS bytes (lane % 32) * 16 of the row (BT:
+  // b^T rows as a's).
+  int va[2], vb[2], va_last[2], vb_last[2];
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
     const int ra = 32 * wave + 16 * q + (lane >> 2);
     va[q] = (int)(ra * g.sa_m * 2) + dma::asw(ra, lane & 3) * 16;
     va_last[q] = (nk - 1) * 32 + dma::asw(ra, lane & 3) * 8 < g.K ? va[q] : (int)a_end;
-    const int kb = 4 * wave + 2 * q + (lane >> 5);
-    const int nb = 32 * (((lane & 31) >> 2) ^ dma::bsw(kb)) + 8 * (lane & 3);
-    vb[q] = (int)(kb * g.sb_k * 2) + nb * 2;
+    if constexpr (BT) {
+      vb[q] = (int)(ra * g.sb_n * 2) + dma::asw(ra, lane & 3) * 16;
+      vb_last[q] = (nk - 1) * 32 + dma::asw(ra, lane & 3) * 8 < g.K ? vb[q] : (int)b_end;
+    } else {
+      const int kb = 4 * wave + 2 * q + (lane >> 5);
+      const int nb = 32 * (((lane & 31) >> 2) ^ dma::bsw(kb)) + 8 * (lane & 3);
+      vb[q] = (int)(kb * g.sb_k * 2) + nb * 2;
+      vb_last[q] = vb[q];
+    }
   }
-  const int b_kstep = (int)(32 * g.sb_k * 2);
+  const int b_kstep = BT ? 64 : (int)(32 * g.sb_k * 2);
   // Load u (0..3) of tile kt into its stage: a q0, b q0, a q1, b q1.
   auto load_unit = [&](int u, int kt) {
     const int st = (kt % dma::STAGES) * dma::STAGE, q = u >> 1;
     if ((u & 1) == 0)
       dma::load_lds16(rsA, lds0 + st + 2048 * wave + 1024 * q, kt == nk - 1 ? va_last[q] : va[q], kt * 64);
     else
-      dma::load_lds16(rsB, lds0 + dma::B0 + st + 2048 * wave + 1024 * q, vb[q], kt * b_kstep);
+      dma::load_lds16(rsB, lds0 + dma::B0 + st + 2048 * wave + 1024 * q, kt == nk - 1 ? vb_last[q] : vb[q],
+                      kt * b_kstep);
   };
 
   // Fragment reads.  a: row 128 wm + 32 i + lane % 32, chunk 2 s + lane / 32 (the swizzle
@@ -620,7 +634,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int row = wm * 128 + (lane & 31);
     a_rd[s2] = row * 64 + dma::asw(row, 2 * s2 + (lane >> 5)) * 16;
   }
-  {
+  if constexpr (BT) {  // b^T: row 64 wn + 32 j + lane % 32 (j at + 2048 j), as a; indexed by slice
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const int row = wn * 64 + (lane & 31);
+      b_rd[s2] = dma::B0 + row * 64 + dma::asw(row, 2 * s2 + (lane >> 5)) * 16;
+    }
+  } else {
     const int gq = lane >> 4, r = (lane & 15) >> 2, q = lane & 3;
     const int f = r | ((gq >> 1) << 2);  // bsw of every row this lane reads
 #pragma unroll
@@ -635,6 +655,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (x == 0 || x >= 3) {
       const int i = x == 0 ? 0 : x - 2;
       fa[s2][i] = *(const frag*)(lds + a_rd[s2] + st + i * 2048);
+    } else if constexpr (BT) {
+      const int j = x - 1;
+      fb[s2][j] = *(const frag*)(lds + b_rd[s2] + st + j * 2048);
     } else {
       const int j = x - 1;
       const char* p = lds + b_rd[j] + st + s2 * 8192;
@@ -904,8 +927,14 @@ static int gemm16_launch(GemmArgs g, hipStream_t stream, int config = 0) {
   // three 32-deep k-tiles its pipeline keeps in flight.  M may be ragged; N and K must be
   // multiples of 8, so that every 16-byte operand chunk lies wholly inside or wholly past
   // the matrix (its buffer resources return zeros past the end, per chunk).
-  const bool dma_ok = aligned && g.N % 8 == 0 && g.K % 8 == 0 && (GB_M - 1) * g.sa_m + g.K <= 0x3fffffffLL &&
+  const bool dma_nn = aligned && g.N % 8 == 0 && g.K % 8 == 0 && (GB_M - 1) * g.sa_m + g.K <= 0x3fffffffLL &&
                       (g.K - 1) * g.sb_k + GB_N <= 0x3fffffffLL && g.K >= 3 * 32;
+  // ... or with b k-contiguous (b^T rows, as a's): any N.
+  const bool dma_bt = g.sa_k == 1 && g.sb_k == 1 && (uintptr_t)g.a % 16 == 0 && (uintptr_t)g.b % 16 == 0 &&
+                      (g.sa_m * 2) % 16 == 0 && (g.sb_n * 2) % 16 == 0 && g.sb_n > 0 && g.K % 8 == 0 &&
+                      (GB_M - 1) * g.sa_m + g.K <= 0x3fffffffLL && (GB_N - 1) * g.sb_n + g.K <= 0x3fffffffLL &&
+                      g.K >= 3 * 32 && !dma_nn;
+  const bool dma_ok = dma_nn || dma_bt;
   // Its fast epilogue: 16-byte out vectors, and c (if any) fetched with 32-bit buffer offsets.
   const bool out_vec = g.out_dtype != NT_DTYPE_F32 && g.so_n == 1 && g.so_m >= 0 && g.so_m % 8 == 0 &&
                        (uintptr_t)g.out % 16 == 0;
@@ -914,8 +943,13 @@ static int gemm16_launch(GemmArgs g, hipStream_t stream, int config = 0) {
   if ((config == 1 && !dma_ok) || (config == 2 && !fast)) return NT_ERR_INVALID;
   const bool use_dma = config == 0 ? dma_ok : config == 1;
   const bool use_fast8 = config == 0 ? fast && !dma_ok : config == 2;
-  g.c_pre = use_dma && out_vec && c_vec;
-  if (use_dma && g.c_pre)
+  g.c_pre = use_dma && out_vec && c_vec && g.N % 8 == 0;
+  if (use_dma && dma_bt) {
+    if (g.c_pre)
+      hipLaunchKernelGGL((gemm_dma_kernel<T, true, true>), grid, dim3(512), 0, stream, g);
+    else
+      hipLaunchKernelGGL((gemm_dma_kernel<T, false, true>), grid, dim3(512), 0, stream, g);
+  } else if (use_dma && g.c_pre)
     hipLaunchKernelGGL((gemm_dma_kernel<T, true>), grid, dim3(512), 0, stream, g);
   else if (use_dma)
     hipLaunchKernelGGL((gemm_dma_kernel<T, false>), grid, dim3(512), 0, stream, g);

@@ -382,6 +382,39 @@ def test_gemm_transposed_operands():
     assert torch.allclose(out.float(), _gemm_ref(a, b).float(), atol=2e-2, rtol=1e-2)
 
 
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+@pytest.mark.parametrize("mnk", ((4096, 4096, 4096), (1000, 1000, 1000), (300, 777, 104), (256, 256, 96),
+                                 (1920, 4100, 640)))
+def test_gemm_dma_b_transposed(mnk, dtype):
+    # b k-contiguous (b = w.t(), the layout of x @ w.t()) on the DMA kernel (forced): b^T
+    # rows go to LDS as a's; any N (777, 4100: not multiples of 8, the element-wise
+    # epilogue), K multiples of 8 with a partial last k-tile (1000, 104, 640 % 32 = 0).
+    m, n, k = mnk
+    a = _randn((m, k), dtype, 70)
+    b = _randn((n, k), dtype, 71).t()
+    c = _randn((m, n), dtype, 72)
+    rd = torch.float16 if dtype == torch.float16 else None
+    out = torch.full((m, n), 7.0, dtype=dtype, device=DEV)
+    kernels.gemm(a, b, out, c=c, alpha=1.0, beta=0.5, round_dtype=rd, config=1)
+    ref = _gemm_ref(a, b.contiguous(), c, 1.0, 0.5, rd)
+    tol = 1e-2 * max(1.0, math.sqrt(k) / 8)
+    assert torch.allclose(out.float(), ref.float(), atol=tol, rtol=1e-2)
+
+
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+def test_gemm_dma_b_transposed_reads_nothing_past_k(dtype):
+    # b^T rows are a view of a wider buffer holding inf past K: those values must not
+    # reach the product (the last k-tile's chunks past K read zeros).
+    m, n, k = 264, 300, 200
+    bt_buf = torch.full((n, k + 8), float("inf"), dtype=dtype, device=DEV)
+    bt_buf[:, :k] = _randn((n, k), dtype, 73)
+    a, b = _randn((m, k), dtype, 74), bt_buf[:, :k].t()
+    out = torch.empty((m, n), dtype=dtype, device=DEV)
+    kernels.gemm(a, b, out, config=1)
+    assert torch.isfinite(out).all()
+    assert torch.allclose(out.float(), a.float() @ b.float(), atol=2e-2, rtol=1e-2)
+
+
 @pytest.mark.parametrize("mnk", ((512, 512, 512), (100, 70, 33), (256, 128, 1000), (64, 32, 260), (64, 64, 514)))
 def test_gemm_f32(mnk):
     m, n, k = mnk
