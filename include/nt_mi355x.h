@@ -84,7 +84,8 @@ int nt_softmax_bf16(const void* x, int64_t x_row_stride, int64_t x_col_stride,
 /* One kernel configuration of the softmax, for the auto-tuner: the arguments of
  * nt_softmax_* plus `config` (0 = as nt_softmax_* choose; 1, 2, 3 = the register path
  * with workgroups of four, eight, one wave, when the segment fits it; 4 = the two-sweep
- * kernel).  A forced configuration that does not fit returns NT_ERR_INVALID before
+ * kernel; 5 = a group of lanes per segment, up to four 16-byte vectors per lane of one
+ * wave).  A forced configuration that does not fit returns NT_ERR_INVALID before
  * launching.  Replaces the reference's tuning over num_warps 4, 8, 1
  * (reference src/ninetoothed/backends/triton.py:151-155). */
 int nt_softmax_config_f32(const void* x, int64_t x_row_stride, int64_t x_col_stride,

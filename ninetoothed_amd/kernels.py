@@ -83,11 +83,12 @@ def add(lhs, rhs, out):
 
 
 # --------------------------------------------------------------------- softmax
-# Kernel configurations of the softmax that ``config`` can force (0: the four-wave register
+# Kernel configurations of the softmax that ``config`` can force (0: the lane-group kernel for
+# segments of at most four 16-byte vectors per lane of a wave, else the four-wave register
 # path where the segment fits, else the two-sweep kernel): the register path with workgroups
 # of four, eight or one wave (the reference's num_warps candidates 4, 8, 1), the two-sweep
-# kernel.
-SOFTMAX_CONFIGS = (1, 2, 3, 4)
+# kernel, the lane-group kernel.
+SOFTMAX_CONFIGS = (1, 2, 3, 4, 5)
 
 
 def bind_softmax(x, y, block=None, config=0):

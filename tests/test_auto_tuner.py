@@ -268,7 +268,7 @@ def test_softmax_and_pool_plans_expand_into_kernels():
     ctx = sm._kernel.context(dict(zip(list(sm._kernel.params), (x, x))), {"BLOCK_SIZE": 300})
     described = [p.describe() for p in families.candidates(ctx)]
     assert [(d["family"], d.get("config")) for d in described] == [
-        ("softmax", 1), ("softmax", 2), ("softmax", 3), ("softmax", 4), ("generic", None)]
+        ("softmax", 1), ("softmax", 2), ("softmax", 3), ("softmax", 4), ("softmax", 5), ("generic", None)]
     pool = ninetoothed.make(functools.partial(pg.max_pool2d_arrangement, ceil_mode=False), pg.max_pool2d_application,
                             pg.max_pool2d_tensors())
     xi, yo = torch.empty(2, 3, 16, 16, dtype=torch.float16), torch.empty(2, 3, 8, 8, dtype=torch.float16)

@@ -653,9 +653,10 @@ def test_attention_config_conditions_are_checked():
 
 
 # Softmax kernel configurations (1, 2, 3: register path with four, eight, one wave per
-# workgroup; 4: two-sweep kernel) on whole rows, segments, an unaligned view and the
-# headline width; a configuration whose register path cannot hold the segment is refused.
-@pytest.mark.parametrize("config", (1, 2, 3, 4))
+# workgroup; 4: two-sweep kernel; 5: a group of lanes per segment) on whole rows, segments,
+# an unaligned view and the headline width; a configuration whose kernel cannot hold the
+# segment is refused.
+@pytest.mark.parametrize("config", (1, 2, 3, 4, 5))
 @pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16, torch.float32))
 @pytest.mark.parametrize("cols, block", ((8192, None), (1000, None), (33, None), (1000, 128), (5000, 777)))
 def test_softmax_configs(config, dtype, cols, block):
@@ -672,14 +673,47 @@ def test_softmax_configs(config, dtype, cols, block):
             xp = F.pad(view.float(), (0, nseg * blk - cols), value=float("-inf")).view(24, nseg, blk)
             ref = torch.softmax(xp, dim=-1).view(24, nseg * blk)[:, :cols]
         y = torch.empty(24, cols, dtype=dtype, device=DEV)
-        lanes = {1: 256, 2: 512, 3: 64}.get(config)
+        lanes = {1: 256, 2: 512, 3: 64, 5: 64}.get(config)
         vpt_max = 16 if view is x and (cols * x.element_size()) % 16 == 0 and (blk * x.element_size()) % 16 == 0 else 8
+        if config == 5:
+            vpt_max = 4
         if lanes is not None and min(blk, cols) > lanes * (16 // x.element_size()) * vpt_max:
             with pytest.raises(KernelLaunchError):
                 kernels.softmax(view, y, block=block, config=config)
             continue
         kernels.softmax(view, y, block=block, config=config)
         assert torch.allclose(y.float(), ref, atol=tol, rtol=tol)
+
+
+@pytest.mark.parametrize("dtype", (torch.float16, torch.float32))
+@pytest.mark.parametrize("rows, cols, block", ((3000, 128, None), (777, 24, None), (9, 300000, None),
+                                               (700, 6000, 2000), (2, 1 << 20, None), (600, 40000, None)))
+def test_softmax_shapes(rows, cols, block, dtype):
+    # The library's own choice: lane groups for short segments (16 lanes per 128 fp16
+    # columns, 4 segments of 24 per 16 lanes...), the register path, and the two-sweep
+    # kernel with 1024 lanes (few segments) or 256 (many); also one column off alignment.
+    x = _randn((rows, cols + 1), dtype, 14, scale=2.0)
+    for view in (x[:, :cols], x[:, 1:]):
+        blk = cols if block is None else block
+        nseg = -(-cols // blk)
+        xp = F.pad(view.float(), (0, nseg * blk - cols), value=float("-inf")).view(rows, nseg, blk)
+        ref = torch.softmax(xp, dim=-1).view(rows, nseg * blk)[:, :cols]
+        y = torch.empty(rows, cols, dtype=dtype, device=DEV)
+        kernels.softmax(view, y, block=block)
+        assert torch.allclose(y.float(), ref, atol=TOL[dtype], rtol=TOL[dtype]), (rows, cols)
+
+
+def test_softmax_infinite_rows():
+    # -inf entries: a row of -inf but one value, -inf prefixes across whole vectors, in the
+    # lane-group kernel (128 columns) and the two-sweep kernel (300000 columns).
+    for cols in (128, 300000):
+        x = torch.randn(4, cols, device=DEV).half()
+        x[0, :] = float("-inf")
+        x[0, cols - 3] = 1.0
+        x[1, : cols // 2] = float("-inf")
+        y = torch.empty_like(x)
+        kernels.softmax(x, y)
+        assert torch.allclose(y.float(), torch.softmax(x.float(), -1), atol=1e-3, rtol=1e-2), cols
 
 
 @pytest.mark.parametrize("config", (1, 2, 3))
