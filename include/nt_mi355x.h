@@ -300,7 +300,8 @@ int nt_attention_f32(const void* q, const int64_t* q_strides, const void* k, con
  * of nt_attention_f16/bf16 plus `config` (0 = the fastest kernel whose conditions hold,
  * as nt_attention_f16/bf16 choose; 1 = the one-wave-per-SIMD pipelined kernel, head dim
  * 128 with unit d-stride and 16-byte aligned rows; 2 = the eight-wave kernel, same
- * conditions, head dim 64 or 128; 3 = the four-wave kernels, any strides).  A forced
+ * conditions, any head dim up to 128 that is a multiple of 8 (padded with zeros to 64 or
+ * 128); 3 = the four-wave kernels, any strides).  A forced
  * configuration whose conditions do not hold returns NT_ERR_INVALID before launching.
  * Replaces the per-configuration launchers the reference's auto-tuner times over
  * BLOCK_SIZE_M/N (reference tests/test_attention.py:10-11,

@@ -419,6 +419,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
   const int q0 = qb_id * BM;
   const int qw = q0 + wave * WQ;  // first query of this wave
   const int Sk = (int)g.Sk;
+  const int D = (int)g.D;  // DM / 2 < D <= DM, a multiple of 8
   const uint16_t* Q = (const uint16_t*)g.q + b * g.qs[0] + h * g.qs[1];
 
   // Q^T fragments of this lane's queries (one per block), pre-scaled and rounded to the
@@ -431,7 +432,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 #pragma unroll
     for (int dd = 0; dd < G::DSUB; ++dd) {
       u32x4 raw = {0u, 0u, 0u, 0u};
-      if (qpos[qb] < g.Sq) raw = *(const u32x4*)(Q + (int64_t)qpos[qb] * g.qs[2] + dd * 16 + half * 8);
+      if (qpos[qb] < g.Sq && dd * 16 + half * 8 < D) raw = *(const u32x4*)(Q + (int64_t)qpos[qb] * g.qs[2] + dd * 16 + half * 8);
       uint16_t tmp[8];
       const uint16_t* hv = (const uint16_t*)&raw;
 #pragma unroll
@@ -448,11 +449,15 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
   const bool k_role = NW == 4 || wave < 4;
   const bool v_role = (NW == 4 || wave >= 4) && (lt >> 4) < DM / 8;
   const int ks2b = (int)g.ks[2] * 2, vs2b = (int)g.vs[2] * 2;
+  // Both resources end at the last key's D-th element.  A head dim D below DM (a multiple
+  // of 8) leaves K chunks kc >= D / 8 zero (they meet Q's zero padding in the scores); V's
+  // chunks past D reach only output rows d >= D, which are never stored.
   const __amdgpu_buffer_rsrc_t rsK = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)((const uint16_t*)g.k + b * g.ks[0] + h * g.ks[1]), (short)0, (Sk - 1) * ks2b + DM * 2, 0x00020000);
+      (void*)((const uint16_t*)g.k + b * g.ks[0] + h * g.ks[1]), (short)0, (Sk - 1) * ks2b + D * 2, 0x00020000);
   const __amdgpu_buffer_rsrc_t rsV = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)((const uint16_t*)g.v + b * g.vs[0] + h * g.vs[1]), (short)0, (Sk - 1) * vs2b + DM * 2, 0x00020000);
+      (void*)((const uint16_t*)g.v + b * g.vs[0] + h * g.vs[1]), (short)0, (Sk - 1) * vs2b + D * 2, 0x00020000);
   const int kr = lt / G::CPR, kc = lt % G::CPR;
+  const bool k_ok = kc * 8 < D;
   const int vK = kr * ks2b + kc * 16;
   int k_st[G::K_LOADS];
 #pragma unroll
@@ -473,7 +478,8 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
     if (k_role) {
 #pragma unroll
       for (int i = 0; i < G::K_LOADS; ++i)
-        rk[i] = __builtin_amdgcn_raw_buffer_load_b128(rsK, vK, (k0 + i * G::KEYS_PER_LOAD) * ks2b, 0);
+        rk[i] = k_ok ? __builtin_amdgcn_raw_buffer_load_b128(rsK, vK, (k0 + i * G::KEYS_PER_LOAD) * ks2b, 0)
+                     : u32x4{0u, 0u, 0u, 0u};
     }
     if (v_role) {
 #pragma unroll
@@ -673,7 +679,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
         const int e = e0 + lane;
         const int row = e >> 4, grp = (e & 15) * 4;
         const int qp = qw + qb * 32 + row;
-        if (qp < g.Sq) {
+        if (qp < g.Sq && ps * 64 + grp < D) {
           const float* sp = stage + row * ST + grp;
           const int64_t ob = b * g.os[0] + h * g.os[1] + (int64_t)qp * g.os[2];
           const int d0 = ps * 64 + grp;
@@ -1197,12 +1203,20 @@ static int attention_launch(const void* q, const int64_t* qs, const void* k, con
   // The fast kernel addresses a head's keys with 32-bit buffer offsets (up to two tiles
   // past the end) and positions with 32-bit integers.
   constexpr int NW = 8;  // waves of 32 queries per workgroup of the fast kernel
+  // The fast kernel also takes a head dim below its 64 or 128 (a multiple of 8, padded with
+  // zeros): 16-byte row vectors need only unit d-stride and aligned rows.
+  auto rows_ok = [&]() {
+    return ks[3] == 1 && vs[3] == 1 && qs[3] == 1 && D % 8 == 0 && (ks[2] * 2) % 16 == 0 && (vs[2] * 2) % 16 == 0 &&
+           (qs[2] * 2) % 16 == 0 && (ks[1] * 2) % 16 == 0 && (vs[1] * 2) % 16 == 0 && (qs[1] * 2) % 16 == 0 &&
+           (ks[0] * 2) % 16 == 0 && (vs[0] * 2) % 16 == 0 && (qs[0] * 2) % 16 == 0 && (uintptr_t)k % 16 == 0 &&
+           (uintptr_t)v % 16 == 0 && (uintptr_t)q % 16 == 0;
+  };
   auto fast_ok = [&](int64_t dm) {
-    return kvec_ok(dm) && (Sk + 2 * AT_BN) * ks[2] * 2 < 0x7fffffffLL && (Sk + 2 * AT_BN) * vs[2] * 2 < 0x7fffffffLL &&
-           Sq + NW * 32 < 0x7fffffffLL && Sk > 0;
+    return rows_ok() && D <= dm && (Sk + 2 * AT_BN) * ks[2] * 2 < 0x7fffffffLL &&
+           (Sk + 2 * AT_BN) * vs[2] * 2 < 0x7fffffffLL && Sq + NW * 32 < 0x7fffffffLL && Sk > 0;
   };
   const int64_t dm = D <= 64 ? 64 : 128;
-  const bool fast_fits = fast_ok(dm), pipe_fits = dm == 128 && fast_fits;
+  const bool fast_fits = fast_ok(dm), pipe_fits = D == 128 && fast_fits;
   if ((config == 1 && !pipe_fits) || (config == 2 && !fast_fits)) return NT_ERR_INVALID;
   // The eight-wave kernel is the default: measured on MI355X at B=4, H=32, S=4096, D=128
   // it runs 1,090-1,130 us non-causal against 1,140-1,270 us for the pipelined kernel.

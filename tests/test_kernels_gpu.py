@@ -588,6 +588,29 @@ def test_attention_growing_scores(d, causal, sq, sk):
     assert torch.allclose(o.double(), ref, atol=1e-2, rtol=1e-2)
 
 
+@pytest.mark.parametrize("d", (8, 40, 80, 96, 112))
+@pytest.mark.parametrize("causal", (False, True))
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+def test_attention_padded_head_dims(d, causal, dtype):
+    # Head dims below 64 or 128 (multiples of 8) on the eight-wave kernel (forced), padded
+    # with zeros: k, v and o as views of wider rows whose columns past d hold inf (k, v)
+    # and a sentinel (o), so a value past d reaching the scores, or a store past d, shows.
+    sq, sk = 300, 333
+    pad = torch.full((1, 3, sk, d + 8), float("inf"), dtype=dtype, device=DEV)
+    k, v = pad.clone(), pad.clone()
+    k[..., :d] = _randn((1, 3, sk, d), dtype, 64)
+    v[..., :d] = _randn((1, 3, sk, d), dtype, 65)
+    k, v = k[..., :d], v[..., :d]
+    q = _randn((1, 3, sq, d), dtype, 66)
+    obuf = torch.full((1, 3, sq, d + 8), 7.0, dtype=dtype, device=DEV)
+    o = obuf[..., :d]
+    scale = 1.0 / math.sqrt(d)
+    kernels.attention(q, k, v, o, causal=causal, q_scale=kernels.LOG2E * scale, config=2)
+    ref = F.scaled_dot_product_attention(q.float(), k.float(), v.float(), is_causal=causal, scale=scale)
+    assert torch.allclose(o.float(), ref, atol=2e-2, rtol=2e-2)
+    assert torch.all(obuf[..., d:] == 7.0)
+
+
 def test_attention_headline_causal():
     q, k, v = (_randn((4, 32, 4096, 128), torch.float16, 50 + i) for i in range(3))
     o = torch.empty_like(q)
