@@ -210,9 +210,9 @@ int nt_gemm_e4m3(const void* a, int64_t sa_m, int64_t sa_k, const void* b, int64
  * conv2d arrangement builds it (reference tests/test_conv2d.py:14-49, pad
  * src/ninetoothed/tensor.py:538-563); the body is the matmul application, so
  * `round_dtype` carries its fp16 cast.  `workspace` (may be NULL) lets the library
- * re-lay the input and filter for vector loads; nt_conv2d_workspace_size() gives
- * the bytes it wants for a shape (0 = not used).  With too small a workspace
- * the direct path runs.
+ * re-lay the input and filter for vector loads (channels zero-filled up to a multiple
+ * of 32 or 64); nt_conv2d_workspace_size() gives the bytes it wants for a shape (0 =
+ * not used).  With too small a workspace the direct path runs.
  * ------------------------------------------------------------------------- */
 int64_t nt_conv2d_workspace_size(int64_t N, int64_t C, int64_t H, int64_t W, int64_t K,
                                  int64_t R, int64_t S, int64_t ph, int64_t pw, int dtype);
@@ -232,9 +232,9 @@ int nt_conv2d_bf16(const void* x, const int64_t* x_strides, const void* w, const
 /* One path of the 16-bit convolution, for the auto-tuner: the arguments of
  * nt_conv2d_f16/bf16 plus `config` (0 = the fastest path whose conditions hold, as
  * nt_conv2d_*; 1 = the re-laid input through the DMA kernel: a workspace of
- * nt_conv2d_workspace_size bytes, C % 64 == 0, C*R*S >= 128, Q % 8 == 0, y of the input
- * type with unit q stride; 2 = the re-laid input through the N-H-W-C kernel: the
- * workspace and C % 64 == 0; 3 = the direct kernel, no workspace).  A forced path whose
+ * nt_conv2d_workspace_size bytes, C*R*S >= 96 with C rounded up to 32, Q % 8 == 0, y of
+ * the input type with unit q stride; 2 = the re-laid input through the N-H-W-C kernel:
+ * the workspace; 3 = the direct kernel, no workspace).  A forced path whose
  * conditions do not hold returns NT_ERR_INVALID before launching.  Replaces the
  * per-configuration launchers the reference's auto-tuner times
  * (src/ninetoothed/compiler/driver.py:975-1031, tests/test_conv2d.py:109-113). */

@@ -31,6 +31,7 @@ struct ConvArgs {
   int64_t xs[4], ws[4], ys[4];
   int64_t N, C, H, W, K, R, S, P, Q, ph, pw, sh, sw, dh, dw;
   int64_t M, KG;  // N*P*Q, C*R*S
+  int64_t Cr;     // channels of x and w; C is the re-laid layout's (Cr rounded up, zero-filled)
   int y_dtype, round_dtype;
   int tiles_k, tiles_m;
 };
@@ -171,7 +172,7 @@ template <typename T>
 __global__ __launch_bounds__(256) void nchw_to_nhwc_pad_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ xp,
                                                                ConvArgs g, int64_t Hp, int64_t Wp) {
   __shared__ uint16_t tile[64][64 + 2];
-  const int64_t cblocks = g.C / 64;
+  const int64_t cblocks = cdiv(g.C, 64);  // the last block may hold 32 channels
   const int64_t b = blockIdx.x;
   const int64_t cb = b % cblocks, row = b / cblocks;
   const int64_t hp = row % Hp, n = row / Hp;
@@ -182,7 +183,7 @@ __global__ __launch_bounds__(256) void nchw_to_nhwc_pad_kernel(const uint16_t* _
   if (h < 0 || h >= g.H) {
     for (int64_t e = tid; e < Wp * 8; e += 256) {
       const int64_t wp = e / 8, ch = e % 8;
-      *(u32x4*)(out_row + wp * g.C + ch * 8) = u32x4{0u, 0u, 0u, 0u};
+      if (c0 + ch * 8 < g.C) *(u32x4*)(out_row + wp * g.C + ch * 8) = u32x4{0u, 0u, 0u, 0u};
     }
     return;
   }
@@ -192,13 +193,13 @@ __global__ __launch_bounds__(256) void nchw_to_nhwc_pad_kernel(const uint16_t* _
     for (int e = tid; e < 64 * 64; e += 256) {
       const int c = e / 64, wi = e % 64;
       const int64_t w = w0 + wi;
-      tile[c][wi] = (w >= 0 && w < g.W) ? xb[c * g.xs[1] + w * g.xs[3]] : (uint16_t)0;
+      tile[c][wi] = (w >= 0 && w < g.W && c0 + c < g.Cr) ? xb[c * g.xs[1] + w * g.xs[3]] : (uint16_t)0;
     }
     __syncthreads();
     for (int e = tid; e < 64 * 8; e += 256) {
       const int wi = e / 8, ch = e % 8;
       const int64_t wp = w0 + g.pw + wi;
-      if (wp < Wp) {
+      if (wp < Wp && c0 + ch * 8 < g.C) {
         uint16_t v[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) v[u] = tile[ch * 8 + u][wi];
@@ -220,7 +221,7 @@ __global__ __launch_bounds__(256) void filter_krsc_kernel(const uint16_t* __rest
     const int64_t r = t % g.R, k = t / g.R;
     const uint16_t* src = w + k * g.ws[0] + r * g.ws[2] + s * g.ws[3];
     uint16_t* dst = wt + row * g.C;
-    for (int64_t c = threadIdx.x; c < g.C; c += blockDim.x) dst[c] = src[c * g.ws[1]];
+    for (int64_t c = threadIdx.x; c < g.C; c += blockDim.x) dst[c] = c < g.Cr ? src[c * g.ws[1]] : (uint16_t)0;
   }
 }
 
@@ -245,7 +246,7 @@ __global__ __launch_bounds__(256) void conv_relayout_kernel(const uint16_t* __re
       const int64_t r = t % g.R, k = t / g.R;
       const uint16_t* src = w + k * g.ws[0] + r * g.ws[2] + s * g.ws[3];
       uint16_t* dst = wt + row * g.C;
-      for (int64_t c = tid; c < g.C; c += 256) dst[c] = src[c * g.ws[1]];
+      for (int64_t c = tid; c < g.C; c += 256) dst[c] = c < g.Cr ? src[c * g.ws[1]] : (uint16_t)0;
     }
     return;
   }
@@ -272,7 +273,8 @@ __global__ __launch_bounds__(256) void conv_relayout_kernel(const uint16_t* __re
     const int64_t cb = e / wblocks, wb = e % wblocks;  // lanes along w first: loads of one channel row coalesce
     u32x4 in[8], out[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) in[i] = *(const u32x4*)(xb + (cb * 8 + i) * g.xs[1] + wb * 8);
+    for (int i = 0; i < 8; ++i)
+      in[i] = cb * 8 + i < g.Cr ? *(const u32x4*)(xb + (cb * 8 + i) * g.xs[1] + wb * 8) : zero;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int d = j >> 1;
@@ -670,7 +672,7 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
     g.ws[i] = ws[i];
     g.ys[i] = ys[i];
   }
-  g.N = N; g.C = C; g.H = H; g.W = W; g.K = K; g.R = R; g.S = S; g.P = P; g.Q = Q;
+  g.N = N; g.C = C; g.Cr = C; g.H = H; g.W = W; g.K = K; g.R = R; g.S = S; g.P = P; g.Q = Q;
   g.ph = ph; g.pw = pw; g.sh = sh; g.sw = sw; g.dh = dh; g.dw = dw;
   g.M = N * P * Q;
   g.KG = C * R * S;
@@ -680,22 +682,31 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
   if (tiles_k * tiles_m > 0x7fffffffLL) return NT_ERR_INVALID;
   g.tiles_k = (int)tiles_k;
   g.tiles_m = (int)tiles_m;
-  const int64_t need = nhwc_bytes(N, C, H, W, K, R, S, ph, pw);
-  const bool nhwc = config != 3 && workspace != nullptr && workspace_bytes >= need && C % 64 == 0 &&
-                    (uintptr_t)workspace % 256 == 0 && (P - 1) * sh + (R - 1) * dh < H + 2 * ph &&
-                    (Q - 1) * sw + (S - 1) * dw < W + 2 * pw;
-  if ((config == 1 || config == 2) && !nhwc) return NT_ERR_INVALID;
+  const int64_t Hp = H + 2 * ph, Wp = W + 2 * pw;
+  // The re-laid input and filter carry Cl channels: C rounded up to 32 for the DMA kernel
+  // (its 32-deep k-tiles stay inside one filter tap), to 64 for conv_nhwc_kernel (64-deep
+  // ones); the channels past C are zeros, so they add nothing to any sum.
+  // DMA kernel: at least three 32-deep k-tiles, 32-bit operand offsets, output written as
+  // 16-byte runs of 8 positions of one channel (Q % 8 == 0, y of the input type with unit
+  // q stride and 16-byte aligned rows).
+  auto dma_fits = [&](int64_t Cl) {
+    const int64_t KGl = Cl * R * S;
+    return KGl >= 3 * 32 && N * Hp * Wp * Cl * 2 < 0x7fffffffLL && K * KGl * 2 < 0x7fffffffLL && g.M < 0x7fffffffLL &&
+           y_dtype == elem<T>::code && Q % 8 == 0 && ys[3] == 1 && ys[0] % 8 == 0 && ys[1] % 8 == 0 && ys[2] % 8 == 0 &&
+           (uintptr_t)y % 16 == 0;
+  };
+  const int64_t C32 = cdiv(C, 32) * 32, C64 = cdiv(C, 64) * 64;
+  const bool dma = config != 2 && dma_fits(C32);
+  const int64_t Cl = dma ? C32 : C64;
+  const int64_t need = nhwc_bytes(N, Cl, H, W, K, R, S, ph, pw);
+  const bool nhwc = config != 3 && workspace != nullptr && workspace_bytes >= need && (uintptr_t)workspace % 256 == 0 &&
+                    (P - 1) * sh + (R - 1) * dh < Hp && (Q - 1) * sw + (S - 1) * dw < Wp;
+  if ((config == 1 && !(nhwc && dma)) || (config == 2 && !nhwc)) return NT_ERR_INVALID;
   if (nhwc) {
-    const int64_t Hp = H + 2 * ph, Wp = W + 2 * pw;
-    // DMA kernel: at least three 32-deep k-tiles, 32-bit operand offsets, output written
-    // as 16-byte runs of 8 positions of one channel (Q % 8 == 0, y of the input type with
-    // unit q stride and 16-byte aligned rows).
-    const bool dma = g.KG >= 3 * 32 && g.KG % 32 == 0 && N * Hp * Wp * C * 2 < 0x7fffffffLL &&
-                     K * g.KG * 2 < 0x7fffffffLL && g.M < 0x7fffffffLL && y_dtype == elem<T>::code && Q % 8 == 0 &&
-                     ys[3] == 1 && ys[0] % 8 == 0 && ys[1] % 8 == 0 && ys[2] % 8 == 0 && (uintptr_t)y % 16 == 0;
-    if (config == 1 && !dma) return NT_ERR_INVALID;
+    g.C = Cl;
+    g.KG = Cl * R * S;
     uint16_t* xp = (uint16_t*)workspace;
-    uint16_t* wt = (uint16_t*)((char*)workspace + ((N * Hp * Wp * C * 2 + 255) / 256) * 256);
+    uint16_t* wt = (uint16_t*)((char*)workspace + ((N * Hp * Wp * Cl * 2 + 255) / 256) * 256);
     int64_t fblocks = K * R * S;  // filter rows of the fast re-layout (at most 4096 workgroups)
     if (fblocks > 4096) fblocks = 4096;
     const bool fast_relayout = xs[3] == 1 && W % 8 == 0 && (uintptr_t)x % 16 == 0 && (xs[0] * 2) % 16 == 0 &&
@@ -705,14 +716,14 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
       hipLaunchKernelGGL(conv_relayout_kernel<T>, dim3((unsigned)(N * Hp + fblocks)), dim3(256), 0, stream,
                          (const uint16_t*)x, xp, (const uint16_t*)w, wt, g, Hp, Wp);
     } else {
-      const int64_t relayout_blocks = N * Hp * (C / 64);
+      const int64_t relayout_blocks = N * Hp * cdiv(Cl, 64);
       if (relayout_blocks > 0x7fffffffLL) return NT_ERR_INVALID;
       hipLaunchKernelGGL(nchw_to_nhwc_pad_kernel<T>, dim3((unsigned)relayout_blocks), dim3(256), 0, stream,
                          (const uint16_t*)x, xp, g, Hp, Wp);
       hipLaunchKernelGGL(filter_krsc_kernel<T>, dim3((unsigned)fblocks), dim3(256), 0, stream, (const uint16_t*)w, wt,
                          g);
     }
-    if (config == 0 ? dma : config == 1)
+    if (dma)
       hipLaunchKernelGGL(conv_dma_kernel<T>, dim3((unsigned)(tiles_k * tiles_m)), dim3(512), 0, stream,
                          (const uint16_t*)xp, (const uint16_t*)wt, g, Hp, Wp);
     else
@@ -736,8 +747,7 @@ extern "C" int64_t nt_conv2d_workspace_size(int64_t N, int64_t C, int64_t H, int
                                             int64_t S, int64_t ph, int64_t pw, int dtype) {
   if (N <= 0 || C <= 0 || H <= 0 || W <= 0 || K <= 0 || R <= 0 || S <= 0 || ph < 0 || pw < 0) return 0;
   if (dtype != NT_DTYPE_F16 && dtype != NT_DTYPE_BF16) return 0;
-  if (C % 64 != 0) return 0;
-  return nt::nhwc_bytes(N, C, H, W, K, R, S, ph, pw);
+  return nt::nhwc_bytes(N, nt::cdiv(C, 64) * 64, H, W, K, R, S, ph, pw);  // enough for either layout
 }
 
 #define NT_CONV_ENTRY(NAME, T)                                                                                       \

@@ -505,10 +505,35 @@ def test_conv2d_paths(config):
     assert torch.allclose(y.float(), ref.to(torch.float16).float(), atol=2e-2, rtol=1e-2)
 
 
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+@pytest.mark.parametrize("case", (
+    # (N, C, H, W), (K, R, S), padding, config: channel counts that are no multiple of 64,
+    # zero-filled to 32 (DMA kernel, config 1) or 64 (N-H-W-C kernel, config 2) in the
+    # workspace; W % 8 == 0 (the one-launch re-layout) and not (the slab re-layout)
+    ((2, 3, 32, 32), (64, 3, 3), (1, 1), 1),
+    ((2, 3, 30, 30), (16, 7, 7), (3, 3), 2),
+    ((3, 24, 16, 24), (40, 3, 3), (1, 1), 1),
+    ((2, 96, 14, 16), (192, 3, 3), (1, 1), 1),
+    ((2, 96, 14, 14), (100, 3, 3), (1, 1), 2),
+    ((1, 100, 9, 13), (72, 3, 3), (1, 1), 0),
+    ((2, 32, 28, 28), (64, 1, 1), (0, 0), 2),
+))
+def test_conv2d_padded_channels(case, dtype):
+    (n, c, h, w_), (k, r, s), padding, config = case
+    x = _randn((n, c, h, w_), dtype, 35)
+    w = _randn((k, c, r, s), dtype, 36, 1.0 / math.sqrt(c * r * s))
+    ref = F.conv2d(x.float(), w.float(), padding=padding)
+    y = torch.full(ref.shape, 7.0, dtype=dtype, device=DEV)
+    ws = _workspace(x, w, padding)
+    assert ws is not None
+    kernels.conv2d(x, w, y, padding=padding, round_dtype=torch.float16, workspace=ws, config=config)
+    assert torch.allclose(y.float(), ref.to(torch.float16).float(), atol=2e-2, rtol=1e-2)
+
+
 def test_conv2d_forced_path_rejects_unfit_call():
     from ninetoothed_amd.errors import KernelLaunchError
 
-    x = _randn((2, 24, 16, 16), torch.float16, 62)  # C % 64 != 0: no re-laid path
+    x = _randn((2, 24, 16, 16), torch.float16, 62)  # no workspace: no re-laid path
     w = _randn((40, 24, 3, 3), torch.float16, 63, 0.1)
     y = torch.full((2, 40, 14, 14), 7.0, dtype=torch.float16, device=DEV)
     for config in (1, 2):
