@@ -232,8 +232,9 @@ int nt_conv2d_bf16(const void* x, const int64_t* x_strides, const void* w, const
 /* One path of the 16-bit convolution, for the auto-tuner: the arguments of
  * nt_conv2d_f16/bf16 plus `config` (0 = the fastest path whose conditions hold, as
  * nt_conv2d_*; 1 = the re-laid input through the DMA kernel: a workspace of
- * nt_conv2d_workspace_size bytes, C*R*S >= 96 with C rounded up to 32, Q % 8 == 0, y of
- * the input type with unit q stride; 2 = the re-laid input through the N-H-W-C kernel:
+ * nt_conv2d_workspace_size bytes (which also holds the fp32 partials when the kernel splits
+ * the reduction of a small output), C*R*S >= 96 with C rounded up to 32, y of the input
+ * type; 2 = the re-laid input through the N-H-W-C kernel:
  * the workspace; 3 = the direct kernel, no workspace).  A forced path whose
  * conditions do not hold returns NT_ERR_INVALID before launching.  Replaces the
  * per-configuration launchers the reference's auto-tuner times

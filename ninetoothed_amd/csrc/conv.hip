@@ -32,6 +32,12 @@ struct ConvArgs {
   int64_t N, C, H, W, K, R, S, P, Q, ph, pw, sh, sw, dh, dw;
   int64_t M, KG;  // N*P*Q, C*R*S
   int64_t Cr;     // channels of x and w; C is the re-laid layout's (Cr rounded up, zero-filled)
+  // conv_dma_kernel split along the reduction: `splits` workgroups per output tile, each
+  // `kt_per` 32-deep k-tiles, fp32 partial tiles to part[split][K][M] (splits 1: none).
+  int splits, kt_per;
+  float* part;
+  int64_t Mp;  // rows of the partials: M rounded up to 8
+  int qvec;    // Q % 8 == 0 and y's q stride 1: 8 consecutive positions are one 16-byte run
   int y_dtype, round_dtype;
   int tiles_k, tiles_m;
 };
@@ -464,10 +470,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wk = wave >> 2, wm = wave & 3;
-  const int tk = blockIdx.x % g.tiles_k, tmi = blockIdx.x / g.tiles_k;
+  const int ntile = g.tiles_k * g.tiles_m;
+  const int split = (int)blockIdx.x / ntile, tile = (int)blockIdx.x - split * ntile;
+  const int tk = tile % g.tiles_k, tmi = tile / g.tiles_k;
   const int k0t = tk * CB_K, m0t = tmi * CB_M;
   const int KG = (int)g.KG, C = (int)g.C;
-  const int nk = KG / 32;
+  // This workgroup's k-tiles [kt0, kt1): all of them, or one split's (at least 3).
+  const int kt0 = split * g.kt_per, kt1 = min(KG / 32, kt0 + g.kt_per);
 
   // Load q (0, 1) of this wave per k-tile: rows 32 wave + 16 q + lane / 4 of each operand,
   // LDS chunk lane % 4.  Filter rows past K lie past the resource's end (zeros).
@@ -530,15 +539,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   floatx16 acc[4][2];
   zero_acc(acc);
 
-  // nk >= 3 (the launcher checks): tiles 0..2 in flight, wait for tile 0.
-  for (int kt = 0; kt < 3; ++kt) {
+  // kt1 - kt0 >= 3 (the launcher checks): tiles kt0..kt0+2 in flight, wait for kt0.
+  for (int kt = kt0; kt < kt0 + 3; ++kt) {
     const int xo = x_off(kt);
     for (int u = 0; u < 4; ++u) load_unit(u, kt, xo);
   }
   asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
   __builtin_amdgcn_s_barrier();
 #pragma unroll
-  for (int x = 0; x < 6; ++x) read_unit(x, 0, 0);
+  for (int x = 0; x < 6; ++x) read_unit(x, 0, (kt0 & 3) * cdma::STAGE);
 
 #define NT_CFENCE() __builtin_amdgcn_sched_barrier(0)
   // One k-tile, as gemm_dma_kernel's: HAS1 reads slice 0 of tile kt+1 during slice 1, LOAD
@@ -577,8 +586,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   using V4 = std::integral_constant<int, 4>;
   using V0 = std::integral_constant<int, 0>;
   using VN = std::integral_constant<int, -1>;
-  int kt = 0;
-  for (; kt + 3 < nk; ++kt) step(T1{}, T1{}, V4{}, kt);
+  int kt = kt0;
+  for (; kt + 3 < kt1; ++kt) step(T1{}, T1{}, V4{}, kt);
   step(T1{}, F1{}, V4{}, kt);
   step(T1{}, F1{}, V0{}, kt + 1);
   step(F1{}, F1{}, VN{}, kt + 2);
@@ -588,14 +597,52 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   float* stage = (float*)(lds + cdma::EPI + wave * 4096);
   const int cg = (lane & 7) * 8;
   const int mpos = m0t + wm * 64 + cg;
-  const bool m_ok = mpos < g.M;  // Q % 8 == 0: all 8 positions share one output row
+  const bool m_ok = mpos < g.M;
+  // qvec: the 8 positions share one output row (one 16-byte store per channel); otherwise
+  // each position's own offset (they may run across rows), stored element by element.
   int64_t ybase = 0;
+  int64_t yoff[8];
   if (m_ok) {
     const int q = mpos % (int)g.Q, t = mpos / (int)g.Q;
     const int p = t % (int)g.P, n = t / (int)g.P;
     ybase = n * g.ys[0] + p * g.ys[2] + q;
   }
+  if (!g.qvec) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t m = mpos + u;
+      const int64_t q = m % g.Q, t = m / g.Q;
+      yoff[u] = m < g.M ? (t / g.P) * g.ys[0] + (t % g.P) * g.ys[2] + q * g.ys[3] : -1;
+    }
+  }
   uint16_t* Y = (uint16_t*)g.y;
+  if (g.splits > 1) {
+    // A split's partial tile, fp32, unrounded: conv_splitk_reduce_kernel sums the splits.
+    float* P = g.part + (int64_t)split * g.K * g.Mp;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        wave_lds_order();
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r = 8 * h; r < 8 * h + 8; ++r)
+            stage[(acc_row(r, lane) - 16 * h) * 64 + j * 32 + (lane & 31)] = acc[i][j][r];
+        wave_lds_order();
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int rr = t * 8 + (lane >> 3);
+          const int k = k0t + wk * 128 + i * 32 + h * 16 + rr;
+          if (m_ok && k < g.K) {
+            float* dst = P + (int64_t)k * g.Mp + mpos;
+            *(float4*)dst = *(const float4*)(stage + rr * 64 + cg);
+            *(float4*)(dst + 4) = *(const float4*)(stage + rr * 64 + cg + 4);
+          }
+        }
+      }
+    return;
+  }
   auto finish = [&](auto round_c) {
     constexpr int ROUND = decltype(round_c)::value;
 #pragma unroll
@@ -630,7 +677,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             }
             ow[d] = (uint32_t)elem<T>::from_float(a) | ((uint32_t)elem<T>::from_float(b) << 16);
           }
-          if (m_ok && k < g.K) __builtin_nontemporal_store(ow, (u32x4*)(Y + ybase + (int64_t)k * g.ys[1]));
+          if (m_ok && k < g.K) {
+            if (g.qvec) {
+              __builtin_nontemporal_store(ow, (u32x4*)(Y + ybase + (int64_t)k * g.ys[1]));
+            } else {
+#pragma unroll
+              for (int u = 0; u < 8; ++u)
+                if (yoff[u] >= 0) Y[yoff[u] + (int64_t)k * g.ys[1]] = (uint16_t)(ow[u >> 1] >> (16 * (u & 1)));
+            }
+          }
         }
       }
   };
@@ -642,11 +697,72 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     finish(std::integral_constant<int, NT_DTYPE_NONE>{});
 }
 
+// Sum of conv_dma_kernel's split partials: one lane per 8 consecutive output positions of
+// one channel, rounded and stored as one 16-byte vector when they share an output row
+// (qvec), else element by element.
+template <typename T>
+__global__ __launch_bounds__(256) void conv_splitk_reduce_kernel(ConvArgs g) {
+  const int64_t mv = g.Mp / 8, total = g.K * mv;
+  uint16_t* Y = (uint16_t*)g.y;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int64_t k = e / mv, m = (e - k * mv) * 8;
+    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int sp = 0; sp < g.splits; ++sp) {
+      const float* src = g.part + ((int64_t)sp * g.K + k) * g.Mp + m;
+      const float4 a = *(const float4*)src, b = *(const float4*)(src + 4);
+      v[0] += a.x; v[1] += a.y; v[2] += a.z; v[3] += a.w;
+      v[4] += b.x; v[5] += b.y; v[6] += b.z; v[7] += b.w;
+    }
+    u32x4 ow;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const float a = round_through(v[2 * d], g.round_dtype), b = round_through(v[2 * d + 1], g.round_dtype);
+      ow[d] = (uint32_t)elem<T>::from_float(a) | ((uint32_t)elem<T>::from_float(b) << 16);
+    }
+    if (g.qvec) {
+      const int64_t q = m % g.Q, t = m / g.Q;
+      const int64_t p = t % g.P, n = t / g.P;
+      __builtin_nontemporal_store(ow, (u32x4*)(Y + n * g.ys[0] + k * g.ys[1] + p * g.ys[2] + q));
+    } else {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int64_t mu = m + u;
+        if (mu < g.M) {
+          const int64_t q = mu % g.Q, t = mu / g.Q;
+          Y[(t / g.P) * g.ys[0] + k * g.ys[1] + (t % g.P) * g.ys[2] + q * g.ys[3]] =
+              (uint16_t)(ow[u >> 1] >> (16 * (u & 1)));
+        }
+      }
+    }
+  }
+}
+
 static int64_t nhwc_bytes(int64_t N, int64_t C, int64_t H, int64_t W, int64_t K, int64_t R, int64_t S, int64_t ph,
                           int64_t pw) {
   const int64_t xp = N * (H + 2 * ph) * (W + 2 * pw) * C * 2;
   const int64_t wt = K * R * S * C * 2;
   return ((xp + 255) / 256) * 256 + wt;
+}
+
+// Splits of conv_dma_kernel's reduction for an output of `tiles` 256 x 256 tiles and nk
+// 32-deep k-tiles: none when the tiles alone fill the GPU (128 or more), else enough to
+// give about 256 workgroups, at most 16, each with at least 4 k-tiles (the last at least
+// 3), and no more than `room` bytes of fp32 partials (K x M each).  Returns the number of
+// splits and sets *per to the k-tiles of each.
+static int64_t conv_splits(int64_t tiles, int64_t nk, int64_t K, int64_t M, int64_t room, int64_t* per) {
+  *per = nk;
+  if (tiles >= 128) return 1;
+  int64_t sp = cdiv(256, tiles);
+  if (sp > 16) sp = 16;
+  if (sp > nk / 4) sp = nk / 4;
+  for (; sp > 1; --sp) {
+    const int64_t p = cdiv(nk, sp), used = cdiv(nk, p);
+    if (nk - (used - 1) * p >= 3 && used * K * M * 4 <= room && used * tiles <= 0x7fffffffLL) {
+      *per = p;
+      return used;
+    }
+  }
+  return 1;
 }
 
 template <typename T>
@@ -673,6 +789,9 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
     g.ys[i] = ys[i];
   }
   g.N = N; g.C = C; g.Cr = C; g.H = H; g.W = W; g.K = K; g.R = R; g.S = S; g.P = P; g.Q = Q;
+  g.splits = 1;
+  g.kt_per = (int)((C * R * S) / 32);
+  g.part = nullptr;
   g.ph = ph; g.pw = pw; g.sh = sh; g.sw = sw; g.dh = dh; g.dw = dw;
   g.M = N * P * Q;
   g.KG = C * R * S;
@@ -692,9 +811,11 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
   auto dma_fits = [&](int64_t Cl) {
     const int64_t KGl = Cl * R * S;
     return KGl >= 3 * 32 && N * Hp * Wp * Cl * 2 < 0x7fffffffLL && K * KGl * 2 < 0x7fffffffLL && g.M < 0x7fffffffLL &&
-           y_dtype == elem<T>::code && Q % 8 == 0 && ys[3] == 1 && ys[0] % 8 == 0 && ys[1] % 8 == 0 && ys[2] % 8 == 0 &&
-           (uintptr_t)y % 16 == 0;
+           y_dtype == elem<T>::code;
   };
+  // Its output as 16-byte runs of 8 positions of one channel, or else element by element.
+  g.qvec = Q % 8 == 0 && ys[3] == 1 && ys[0] % 8 == 0 && ys[1] % 8 == 0 && ys[2] % 8 == 0 && (uintptr_t)y % 16 == 0;
+  g.Mp = cdiv(g.M, 8) * 8;
   const int64_t C32 = cdiv(C, 32) * 32, C64 = cdiv(C, 64) * 64;
   const bool dma = config != 2 && dma_fits(C32);
   const int64_t Cl = dma ? C32 : C64;
@@ -705,6 +826,13 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
   if (nhwc) {
     g.C = Cl;
     g.KG = Cl * R * S;
+    // Few output tiles: the DMA kernel splits the reduction, partials after the re-layout.
+    const int64_t part_at = cdiv(need, 256) * 256;
+    int64_t per = g.KG / 32;
+    const int64_t sp = dma ? conv_splits(tiles_k * tiles_m, g.KG / 32, K, g.Mp, workspace_bytes - part_at, &per) : 1;
+    g.splits = (int)sp;
+    g.kt_per = (int)per;
+    g.part = sp > 1 ? (float*)((char*)workspace + part_at) : nullptr;
     uint16_t* xp = (uint16_t*)workspace;
     uint16_t* wt = (uint16_t*)((char*)workspace + ((N * Hp * Wp * Cl * 2 + 255) / 256) * 256);
     int64_t fblocks = K * R * S;  // filter rows of the fast re-layout (at most 4096 workgroups)
@@ -723,10 +851,15 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
       hipLaunchKernelGGL(filter_krsc_kernel<T>, dim3((unsigned)fblocks), dim3(256), 0, stream, (const uint16_t*)w, wt,
                          g);
     }
-    if (dma)
-      hipLaunchKernelGGL(conv_dma_kernel<T>, dim3((unsigned)(tiles_k * tiles_m)), dim3(512), 0, stream,
+    if (dma) {
+      hipLaunchKernelGGL(conv_dma_kernel<T>, dim3((unsigned)(sp * tiles_k * tiles_m)), dim3(512), 0, stream,
                          (const uint16_t*)xp, (const uint16_t*)wt, g, Hp, Wp);
-    else
+      if (sp > 1) {
+        const int64_t vecs = K * (g.Mp / 8);
+        hipLaunchKernelGGL(conv_splitk_reduce_kernel<T>, dim3((unsigned)(cdiv(vecs, 256) < 4096 ? cdiv(vecs, 256) : 4096)),
+                           dim3(256), 0, stream, g);
+      }
+    } else
       hipLaunchKernelGGL(conv_nhwc_kernel<T>, dim3((unsigned)(tiles_k * tiles_m)), dim3(512), 0, stream,
                          (const uint16_t*)xp, (const uint16_t*)wt, g, Hp, Wp);
     return launch_status();
@@ -747,7 +880,16 @@ extern "C" int64_t nt_conv2d_workspace_size(int64_t N, int64_t C, int64_t H, int
                                             int64_t S, int64_t ph, int64_t pw, int dtype) {
   if (N <= 0 || C <= 0 || H <= 0 || W <= 0 || K <= 0 || R <= 0 || S <= 0 || ph < 0 || pw < 0) return 0;
   if (dtype != NT_DTYPE_F16 && dtype != NT_DTYPE_BF16) return 0;
-  return nt::nhwc_bytes(N, nt::cdiv(C, 64) * 64, H, W, K, R, S, ph, pw);  // enough for either layout
+  // Enough for either layout (channels rounded up to 64), plus the split partials of the
+  // largest output the shape can have (stride and dilation 1).
+  const int64_t base = nt::cdiv(nt::nhwc_bytes(N, nt::cdiv(C, 64) * 64, H, W, K, R, S, ph, pw), 256) * 256;
+  const int64_t P = H + 2 * ph - R + 1, Q = W + 2 * pw - S + 1;
+  if (P <= 0 || Q <= 0) return base;
+  const int64_t M = nt::cdiv(N * P * Q, 8) * 8;
+  int64_t per = 0;
+  const int64_t sp = nt::conv_splits(nt::cdiv(K, nt::CB_K) * nt::cdiv(M, nt::CB_M), nt::cdiv(C, 32) * 32 * R * S / 32, K,
+                                     M, INT64_MAX, &per);
+  return base + (sp > 1 ? sp * K * M * 4 : 0);
 }
 
 #define NT_CONV_ENTRY(NAME, T)                                                                                       \

@@ -530,6 +530,47 @@ def test_conv2d_padded_channels(case, dtype):
     assert torch.allclose(y.float(), ref.to(torch.float16).float(), atol=2e-2, rtol=1e-2)
 
 
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+@pytest.mark.parametrize("case", (
+    # (N, C, H, W), (K, R, S), padding: outputs of 2 to 50 tiles of 256 x 256, so the DMA
+    # kernel splits the reduction (16 splits of 9 k-tiles; 27 k-tiles in 6 splits, the last
+    # shorter; 1,280 channels) and a second kernel sums the fp32 partials
+    ((2, 512, 8, 8), (512, 3, 3), (1, 1)),
+    ((4, 96, 28, 16), (192, 3, 3), (1, 1)),
+    ((1, 1280, 8, 8), (1280, 3, 3), (1, 1)),
+    ((4, 64, 16, 16), (512, 3, 3), (1, 1)),
+    ((32, 512, 7, 7), (512, 3, 3), (1, 1)),   # Q = 7: partials of M rounded up to 8, stores one by one
+    ((3, 96, 14, 14), (200, 3, 3), (1, 1)),
+))
+def test_conv2d_split_reduction(case, dtype):
+    (n, c, h, w_), (k, r, s), padding = case
+    x = _randn((n, c, h, w_), dtype, 37)
+    w = _randn((k, c, r, s), dtype, 38, 1.0 / math.sqrt(c * r * s))
+    ref = F.conv2d(x.float(), w.float(), padding=padding)
+    y = torch.full(ref.shape, 7.0, dtype=dtype, device=DEV)
+    kernels.conv2d(x, w, y, padding=padding, workspace=_workspace(x, w, padding), config=1)
+    assert torch.allclose(y.float(), ref, atol=2e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+@pytest.mark.parametrize("case", (
+    # (N, C, H, W), (K, R, S), padding, stride: Q no multiple of 8 on the DMA kernel without
+    # a split (the element-by-element epilogue: 8 positions that run across output rows)
+    ((32, 128, 28, 28), (128, 3, 3), (1, 1), (1, 1)),
+    ((16, 64, 15, 17), (300, 3, 3), (1, 1), (2, 2)),
+    ((8, 256, 14, 14), (256, 1, 1), (0, 0), (1, 1)),
+))
+def test_conv2d_dma_any_q(case, dtype):
+    (n, c, h, w_), (k, r, s), padding, stride = case
+    x = _randn((n, c, h, w_), dtype, 39)
+    w = _randn((k, c, r, s), dtype, 40, 1.0 / math.sqrt(c * r * s))
+    ref = F.conv2d(x.float(), w.float(), padding=padding, stride=stride)
+    assert ref.shape[3] % 8 != 0
+    y = torch.full(ref.shape, 7.0, dtype=dtype, device=DEV)
+    kernels.conv2d(x, w, y, padding=padding, stride=stride, workspace=_workspace(x, w, padding), config=1)
+    assert torch.allclose(y.float(), ref, atol=2e-2, rtol=1e-2)
+
+
 def test_conv2d_forced_path_rejects_unfit_call():
     from ninetoothed_amd.errors import KernelLaunchError
 
