@@ -744,6 +744,15 @@ static int64_t nhwc_bytes(int64_t N, int64_t C, int64_t H, int64_t W, int64_t K,
   return ((xp + 255) / 256) * 256 + wt;
 }
 
+// Channels of the DMA kernel's re-laid layout: C rounded up to 32, and far enough that the
+// reduction C*R*S holds the three 32-deep k-tiles its pipeline keeps in flight (a 1 x 1
+// filter over 64 channels runs as 96, the last 32 zero).
+static int64_t dma_channels(int64_t C, int64_t R, int64_t S) {
+  int64_t c = cdiv(C, 32) * 32;
+  if (c * R * S < 96) c = cdiv(cdiv(96, R * S), 32) * 32;
+  return c;
+}
+
 // Splits of conv_dma_kernel's reduction for an output of `tiles` 256 x 256 tiles and nk
 // 32-deep k-tiles: none when the tiles alone fill the GPU (128 or more), else enough to
 // give about 256 workgroups, at most 16, each with at least 4 k-tiles (the last at least
@@ -816,7 +825,7 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
   // Its output as 16-byte runs of 8 positions of one channel, or else element by element.
   g.qvec = Q % 8 == 0 && ys[3] == 1 && ys[0] % 8 == 0 && ys[1] % 8 == 0 && ys[2] % 8 == 0 && (uintptr_t)y % 16 == 0;
   g.Mp = cdiv(g.M, 8) * 8;
-  const int64_t C32 = cdiv(C, 32) * 32, C64 = cdiv(C, 64) * 64;
+  const int64_t C32 = dma_channels(C, R, S), C64 = cdiv(C, 64) * 64;
   const bool dma = config != 2 && dma_fits(C32);
   const int64_t Cl = dma ? C32 : C64;
   const int64_t need = nhwc_bytes(N, Cl, H, W, K, R, S, ph, pw);
@@ -880,15 +889,16 @@ extern "C" int64_t nt_conv2d_workspace_size(int64_t N, int64_t C, int64_t H, int
                                             int64_t S, int64_t ph, int64_t pw, int dtype) {
   if (N <= 0 || C <= 0 || H <= 0 || W <= 0 || K <= 0 || R <= 0 || S <= 0 || ph < 0 || pw < 0) return 0;
   if (dtype != NT_DTYPE_F16 && dtype != NT_DTYPE_BF16) return 0;
-  // Enough for either layout (channels rounded up to 64), plus the split partials of the
-  // largest output the shape can have (stride and dilation 1).
-  const int64_t base = nt::cdiv(nt::nhwc_bytes(N, nt::cdiv(C, 64) * 64, H, W, K, R, S, ph, pw), 256) * 256;
+  // Enough for either layout's channels (rounded up to 64, or the DMA kernel's), plus the
+  // split partials of the largest output the shape can have (stride and dilation 1).
+  const int64_t c64 = nt::cdiv(C, 64) * 64, cd = nt::dma_channels(C, R, S);
+  const int64_t base = nt::cdiv(nt::nhwc_bytes(N, c64 > cd ? c64 : cd, H, W, K, R, S, ph, pw), 256) * 256;
   const int64_t P = H + 2 * ph - R + 1, Q = W + 2 * pw - S + 1;
   if (P <= 0 || Q <= 0) return base;
   const int64_t M = nt::cdiv(N * P * Q, 8) * 8;
   int64_t per = 0;
-  const int64_t sp = nt::conv_splits(nt::cdiv(K, nt::CB_K) * nt::cdiv(M, nt::CB_M), nt::cdiv(C, 32) * 32 * R * S / 32, K,
-                                     M, INT64_MAX, &per);
+  const int64_t sp = nt::conv_splits(nt::cdiv(K, nt::CB_K) * nt::cdiv(M, nt::CB_M), cd * R * S / 32, K, M, INT64_MAX,
+                                     &per);
   return base + (sp > 1 ? sp * K * M * 4 : 0);
 }
 

@@ -559,6 +559,8 @@ def test_conv2d_split_reduction(case, dtype):
     ((32, 128, 28, 28), (128, 3, 3), (1, 1), (1, 1)),
     ((16, 64, 15, 17), (300, 3, 3), (1, 1), (2, 2)),
     ((8, 256, 14, 14), (256, 1, 1), (0, 0), (1, 1)),
+    ((8, 64, 28, 21), (128, 1, 1), (0, 0), (1, 1)),  # C*R*S = 64: re-laid with 96 channels
+    ((4, 40, 9, 11), (72, 1, 1), (0, 0), (1, 1)),
 ))
 def test_conv2d_dma_any_q(case, dtype):
     (n, c, h, w_), (k, r, s), padding, stride = case
