@@ -883,6 +883,102 @@ __global__ __launch_bounds__(1024) void gemm_f32_splitk_kernel(GemmArgs g) {
   }
 }
 
+// fp32 GEMMs of more tiles (1024^2 and up) on v_mfma_f32_32x32x2_f32: 256 lanes in a 2 x 2
+// grid of waves, each owning (32 WI) x (32 WJ) of the (64 WI) x (64 WJ) tile.  K in
+// 16-deep chunks, double-buffered in LDS and staged through registers (the next chunk's
+// 16-byte loads are in flight while this one is multiplied; one barrier per chunk).  MFMA
+// step s of a chunk takes k = 8 h + s in lane half h (the sum runs over all k, so any
+// bijection will do): a lane's a values for the chunk are then 8 consecutive floats of one
+// row (two ds_read_b128), its b values 8 floats of one column (ds_read_b32, consecutive
+// lanes on consecutive banks).  a rows are padded to 20 floats (16 lanes of a 16-byte read
+// on 16 distinct bank quads), b rows to BN + 4 floats (the two lane halves 8 rows apart
+// on different banks).  M, N, K may be ragged; N and K multiples of 4 (16-byte loads).
+constexpr int F32M_KC = 16, F32M_AS = F32M_KC + 4;
+template <int WI, int WJ>
+__global__ __launch_bounds__(256) void gemm_f32_mfma_kernel(GemmArgs g) {
+  constexpr int BM = 64 * WI, BN = 64 * WJ, BS = BN + 4;
+  constexpr int A_F4 = BM * F32M_KC / 4 / 256, B_F4 = F32M_KC * BN / 4 / 256;  // float4 per lane per chunk
+  constexpr int A_ELEMS = BM * F32M_AS, B_ELEMS = F32M_KC * BS;
+  constexpr int EPI_ELEMS = 4 * 32 * WJ * 32;  // gemm_epilogue's staging (fp32)
+  constexpr int LDS_ELEMS = 2 * (A_ELEMS + B_ELEMS) > EPI_ELEMS ? 2 * (A_ELEMS + B_ELEMS) : EPI_ELEMS;
+  __shared__ __attribute__((aligned(16))) float lds[LDS_ELEMS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  int tm, tn;
+  tile_of(blockIdx.x, g.tiles_m, g.tiles_n, tm, tn);
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const float* A = (const float*)g.a;
+  const float* B = (const float*)g.b;
+  const int nk = (int)((g.K + F32M_KC - 1) / F32M_KC);
+
+  float4 ra[A_F4], rb[B_F4];
+  auto load = [&](int kt) {
+    const int64_t k0 = (int64_t)kt * F32M_KC;
+#pragma unroll
+    for (int i = 0; i < A_F4; ++i) {
+      const int e = i * 256 + tid, row = e >> 2, c4 = e & 3;
+      const int64_t m = m0 + row, k = k0 + c4 * 4;
+      ra[i] = (m < g.M && k < g.K) ? *(const float4*)(A + m * g.sa_m + k) : float4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int i = 0; i < B_F4; ++i) {
+      const int e = i * 256 + tid, kk = e / (BN / 4), c4 = e % (BN / 4);
+      const int64_t k = k0 + kk, n = n0 + c4 * 4;
+      rb[i] = (k < g.K && n < g.N) ? *(const float4*)(B + k * g.sb_k + n) : float4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  auto store = [&](int buf) {
+    float* sA = lds + buf * (A_ELEMS + B_ELEMS);
+    float* sB = sA + A_ELEMS;
+#pragma unroll
+    for (int i = 0; i < A_F4; ++i) {
+      const int e = i * 256 + tid, row = e >> 2, c4 = e & 3;
+      *(float4*)(sA + row * F32M_AS + c4 * 4) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_F4; ++i) {
+      const int e = i * 256 + tid, kk = e / (BN / 4), c4 = e % (BN / 4);
+      *(float4*)(sB + kk * BS + c4 * 4) = rb[i];
+    }
+  };
+  floatx16 acc[WI][WJ];
+  zero_acc(acc);
+  const int r32 = lane & 31, hf = lane >> 5;
+  auto compute = [&](int buf) {
+    const float* sA = lds + buf * (A_ELEMS + B_ELEMS);
+    const float* sB = sA + A_ELEMS;
+    float a[WI][8], b[WJ][8];
+#pragma unroll
+    for (int i = 0; i < WI; ++i) {
+      const float* p = sA + (wm * WI * 32 + i * 32 + r32) * F32M_AS + 8 * hf;
+      const float4 lo = *(const float4*)p, hi = *(const float4*)(p + 4);
+      a[i][0] = lo.x; a[i][1] = lo.y; a[i][2] = lo.z; a[i][3] = lo.w;
+      a[i][4] = hi.x; a[i][5] = hi.y; a[i][6] = hi.z; a[i][7] = hi.w;
+    }
+#pragma unroll
+    for (int j = 0; j < WJ; ++j)
+#pragma unroll
+      for (int st = 0; st < 8; ++st) b[j][st] = sB[(8 * hf + st) * BS + wn * WJ * 32 + j * 32 + r32];
+#pragma unroll
+    for (int st = 0; st < 8; ++st)
+#pragma unroll
+      for (int i = 0; i < WI; ++i)
+#pragma unroll
+        for (int j = 0; j < WJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][st], b[j][st], acc[i][j], 0, 0, 0);
+  };
+
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    if (kt + 1 < nk) load(kt + 1);
+    compute(kt & 1);
+    if (kt + 1 < nk) store((kt + 1) & 1);
+    __syncthreads();
+  }
+  gemm_epilogue<WI, WJ>(g, acc, (uint16_t*)lds, wave, lane, m0 + wm * WI * 32, n0 + wn * WJ * 32);
+}
+
 static int gemm_check(const GemmArgs& g) {
   if (g.M < 0 || g.N < 0 || g.K < 0) return NT_ERR_INVALID;
   if (!valid_dtype(g.out_dtype) || !valid_round(g.round_dtype)) return NT_ERR_INVALID;
@@ -1155,6 +1251,22 @@ static int gemm32_launch(GemmArgs g, hipStream_t stream) {
       hipLaunchKernelGGL(gemm_f32_splitk_kernel<true>, dim3((unsigned)(tiles_m * tiles_n)), dim3(1024), 0, stream, g);
     else
       hipLaunchKernelGGL(gemm_f32_splitk_kernel<false>, dim3((unsigned)(tiles_m * tiles_n)), dim3(1024), 0, stream, g);
+    return launch_status();
+  }
+  // More tiles: the MFMA kernel with 128 x 128 tiles when they alone fill the GPU, else 64 x 64.
+  const bool mfma = g.sa_k == 1 && g.sb_n == 1 && g.N % 4 == 0 && g.K % 4 == 0 && g.sa_m % 4 == 0 && g.sb_k % 4 == 0 &&
+                    (uintptr_t)g.a % 16 == 0 && (uintptr_t)g.b % 16 == 0;
+  if (mfma) {
+    const int64_t t128 = cdiv(g.M, 128) * cdiv(g.N, 128);
+    if (t128 >= 256) {
+      g.tiles_m = (int)cdiv(g.M, 128);
+      g.tiles_n = (int)cdiv(g.N, 128);
+      hipLaunchKernelGGL((gemm_f32_mfma_kernel<2, 2>), dim3((unsigned)t128), dim3(256), 0, stream, g);
+    } else {
+      g.tiles_m = (int)cdiv(g.M, 64);
+      g.tiles_n = (int)cdiv(g.N, 64);
+      hipLaunchKernelGGL((gemm_f32_mfma_kernel<1, 1>), dim3((unsigned)(g.tiles_m * g.tiles_n)), dim3(256), 0, stream, g);
+    }
     return launch_status();
   }
   const bool vec = g.sa_k == 1 && g.sb_n == 1 && g.M % F32_TM == 0 && g.N % F32_TN == 0 && g.K % 4 == 0 &&

@@ -415,6 +415,22 @@ def test_gemm_dma_b_transposed_reads_nothing_past_k(dtype):
     assert torch.allclose(out.float(), a.float() @ b.float(), atol=2e-2, rtol=1e-2)
 
 
+@pytest.mark.parametrize("mnk", ((1024, 1024, 1024), (2048, 2048, 256), (1000, 1028, 516), (4096, 64, 100),
+                                 (700, 900, 4)))
+def test_gemm_f32_mfma(mnk):
+    # fp32 on the matrix core (v_mfma_f32_32x32x2_f32): 128 x 128 tiles (2048^2: 256 of
+    # them) or 64 x 64, ragged M, N, K (multiples of 4), with c, alpha and beta, and a and b
+    # as views of wider rows; against fp64.
+    m, n, k = mnk
+    a = _randn((m, k + 4), torch.float32, 23)[:, :k]
+    b = _randn((k, n + 8), torch.float32, 24)[:, :n]
+    c = _randn((m, n), torch.float32, 25)
+    out = torch.empty((m, n), device=DEV)
+    kernels.gemm(a, b, out, c=c, alpha=0.5, beta=2.0)
+    ref = (0.5 * (a.double() @ b.double()) + 2.0 * c.double()).float()
+    assert torch.allclose(out, ref, atol=1e-4 * max(1.0, k ** 0.5 / 8), rtol=1e-4)
+
+
 @pytest.mark.parametrize("mnk", ((512, 512, 512), (100, 70, 33), (256, 128, 1000), (64, 32, 260), (64, 64, 514)))
 def test_gemm_f32(mnk):
     m, n, k = mnk
