@@ -1249,78 +1249,145 @@ static int attention_launch(const void* q, const int64_t* qs, const void* k, con
   return launch_status();
 }
 
-// fp32 inputs: one lane per query, VALU dot products against key/value tiles staged
-// in LDS (every lane reads the same key, an LDS broadcast).  The q pre-scale and the
-// rounding of p to the value type are exact in fp32.
-constexpr int AF_Q = 64, AF_BN = 32;
-
-__global__ __launch_bounds__(AF_Q) void attention_f32_kernel(AttnArgs g) {
-  __shared__ float sK[AF_BN][128];
-  __shared__ float sV[AF_BN][128];
-  const int tid = threadIdx.x;
+constexpr int AF_BN = 32;  // keys per tile
+// fp32 inputs on the VALU: each query is held by LPQ lanes (1 for head dims up to 64, 2 up
+// to 128), every lane with 64 of its dims of q and of the output accumulator, so a lane
+// needs 128 registers for them and two waves fit each SIMD.  A wave's 64 lanes hold
+// 64 / LPQ queries; the KS waves of a workgroup share those queries and take every KS-th
+// 32-key tile each (KS 4 when there are few query blocks, so that short problems still
+// spread over the CUs), then merge their running (max, sum, accumulator) states through
+// LDS.  Each wave stages its own K and V tiles in LDS as [key][DM] rows and reads them
+// with 16-byte broadcasts (4 FMAs per LDS read); the two halves of a query's dot product
+// meet through one lane swap.  The q pre-scale and the rounding of p to the value type
+// (fp32) are exact.
+template <int DM, int KS>
+__global__ __launch_bounds__(64 * KS) void attention_f32_kernel(AttnArgs g) {
+  constexpr int LPQ = DM / 64, QPW = 64 / LPQ;  // lanes per query, queries per workgroup
+  constexpr int TILE = AF_BN * DM;              // floats of one K (or V) tile
+  constexpr int RED = (KS - 1) * 64 * 66;       // merge area: per lane acc[64], m, l
+  constexpr int LDS = 2 * KS * TILE > RED ? 2 * KS * TILE : RED;
+  __shared__ __attribute__((aligned(16))) float lds[LDS];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int qi = lane / LPQ, part = lane % LPQ;  // query of this lane, and which 64 dims
+  float* sK = lds + w * 2 * TILE;
+  float* sV = sK + TILE;
   int qb;
   int64_t bh;
   block_order(g, blockIdx.x, qb, bh);
   const int64_t b = bh / g.H, h = bh % g.H;
-  const int64_t q0 = (int64_t)qb * AF_Q, qpos = q0 + tid;
+  const int64_t q0 = (int64_t)qb * QPW, qpos = q0 + qi;
   const float* Q = (const float*)g.q + b * g.qs[0] + h * g.qs[1];
   const float* K = (const float*)g.k + b * g.ks[0] + h * g.ks[1];
   const float* V = (const float*)g.v + b * g.vs[0] + h * g.vs[1];
-  const int D = (int)g.D;
-  float qv[128], acc[128];
+  const int D = (int)g.D, d0 = part * 64;
+  float qv[64], acc[64];
 #pragma unroll
-  for (int d = 0; d < 128; ++d) {
-    qv[d] = (qpos < g.Sq && d < D) ? Q[qpos * g.qs[2] + d * g.qs[3]] * g.q_scale : 0.f;
+  for (int d = 0; d < 64; ++d) {
+    qv[d] = (qpos < g.Sq && d0 + d < D) ? Q[qpos * g.qs[2] + (d0 + d) * g.qs[3]] * g.q_scale : 0.f;
     acc[d] = 0.f;
   }
-  float m_i = -INFINITY, l_i = 1.0f;
+  float m_i = -INFINITY, l_i = 0.f;
   int64_t nkt = cdiv(g.Sk, AF_BN);
   if (g.causal) {
-    const int64_t last = (q0 + AF_Q - 1) / AF_BN + 1;
+    const int64_t last = (q0 + QPW - 1) / AF_BN + 1;
     if (last < nkt) nkt = last;
   }
-  for (int64_t kt = 0; kt < nkt; ++kt) {
+  const bool kvec = g.ks[3] == 1 && g.vs[3] == 1 && D % 4 == 0 && g.ks[2] % 4 == 0 && g.vs[2] % 4 == 0 &&
+                    ((uintptr_t)K & 15) == 0 && ((uintptr_t)V & 15) == 0;
+  for (int64_t kt = w; kt < nkt; kt += KS) {
     const int64_t k0 = kt * AF_BN;
-    for (int e = tid; e < AF_BN * 128; e += AF_Q) {
-      const int key = e / 128, d = e % 128;
-      const int64_t kp = k0 + key;
-      const bool ok = kp < g.Sk && d < D;
-      sK[key][d] = ok ? K[kp * g.ks[2] + d * g.ks[3]] : 0.f;
-      sV[key][d] = ok ? V[kp * g.vs[2] + d * g.vs[3]] : 0.f;
+    wave_lds_order();  // this wave's reads of the previous tile come first
+    if (kvec) {
+      for (int e = lane; e < AF_BN * DM / 4; e += 64) {
+        const int key = e / (DM / 4), d = (e % (DM / 4)) * 4;
+        const int64_t kp = k0 + key;
+        const bool ok = kp < g.Sk && d < D;
+        *(float4*)(sK + key * DM + d) = ok ? *(const float4*)(K + kp * g.ks[2] + d) : float4{0.f, 0.f, 0.f, 0.f};
+        *(float4*)(sV + key * DM + d) = ok ? *(const float4*)(V + kp * g.vs[2] + d) : float4{0.f, 0.f, 0.f, 0.f};
+      }
+    } else {
+      for (int e = lane; e < AF_BN * DM; e += 64) {
+        const int key = e / DM, d = e % DM;
+        const int64_t kp = k0 + key;
+        const bool ok = kp < g.Sk && d < D;
+        sK[key * DM + d] = ok ? K[kp * g.ks[2] + d * g.ks[3]] : 0.f;
+        sV[key * DM + d] = ok ? V[kp * g.vs[2] + d * g.vs[3]] : 0.f;
+      }
     }
-    __syncthreads();
-    float s[AF_BN];
+    wave_lds_order();  // every lane's writes before any lane reads
+    float sc[AF_BN];
     float mx = -INFINITY;
+#pragma unroll
     for (int j = 0; j < AF_BN; ++j) {
       float dot = 0.f;
 #pragma unroll
-      for (int d = 0; d < 128; ++d) dot = fmaf(qv[d], sK[j][d], dot);
+      for (int d = 0; d < 64; d += 4) {
+        const float4 kv = *(const float4*)(sK + j * DM + d0 + d);
+        dot = fmaf(qv[d], kv.x, dot);
+        dot = fmaf(qv[d + 1], kv.y, dot);
+        dot = fmaf(qv[d + 2], kv.z, dot);
+        dot = fmaf(qv[d + 3], kv.w, dot);
+      }
+      if constexpr (LPQ == 2) dot += __shfl_xor(dot, 1, 64);
       const int64_t key = k0 + j;
       if (key >= g.Sk || (g.causal && qpos < key)) dot = -INFINITY;
-      s[j] = dot;
+      sc[j] = dot;
       mx = fmaxf(mx, dot);
     }
     const float m_new = fmaxf(m_i, mx);
-    const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
-    float lsum = 0.f;
+    if (m_new != -INFINITY) {  // a tile of masked keys (so far) adds nothing
+      const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
+      float lsum = 0.f;
 #pragma unroll
-    for (int d = 0; d < 128; ++d) acc[d] *= alpha;
-    for (int j = 0; j < AF_BN; ++j) {
-      const float p = __builtin_amdgcn_exp2f(s[j] - m_new);
-      lsum += p;
+      for (int d = 0; d < 64; ++d) acc[d] *= alpha;
 #pragma unroll
-      for (int d = 0; d < 128; ++d) acc[d] = fmaf(p, sV[j][d], acc[d]);
+      for (int j = 0; j < AF_BN; ++j) {
+        const float p = __builtin_amdgcn_exp2f(sc[j] - m_new);
+        lsum += p;
+#pragma unroll
+        for (int d = 0; d < 64; d += 4) {
+          const float4 vv = *(const float4*)(sV + j * DM + d0 + d);
+          acc[d] = fmaf(p, vv.x, acc[d]);
+          acc[d + 1] = fmaf(p, vv.y, acc[d + 1]);
+          acc[d + 2] = fmaf(p, vv.z, acc[d + 2]);
+          acc[d + 3] = fmaf(p, vv.w, acc[d + 3]);
+        }
+      }
+      l_i = l_i * alpha + lsum;
+      m_i = m_new;
     }
-    l_i = l_i * alpha + lsum;
-    m_i = m_new;
+  }
+  if constexpr (KS > 1) {
+    // Merge: waves 1.. park their states, wave 0 rescales every state to the common max.
+    __syncthreads();  // every wave is done with its tiles (the area is reused)
+    if (w > 0) {
+      float* r = lds + ((w - 1) * 64 + lane) * 66;
+#pragma unroll
+      for (int d = 0; d < 64; ++d) r[d] = acc[d];
+      r[64] = m_i;
+      r[65] = l_i;
+    }
     __syncthreads();
+    if (w > 0) return;
+#pragma unroll
+    for (int ww = 1; ww < KS; ++ww) {
+      const float* r = lds + ((ww - 1) * 64 + lane) * 66;
+      const float m2 = r[64], l2 = r[65];
+      if (m2 == -INFINITY) continue;  // that wave saw only masked keys
+      const float m = fmaxf(m_i, m2);
+      const float a1 = m_i == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_i - m), a2 = __builtin_amdgcn_exp2f(m2 - m);
+#pragma unroll
+      for (int d = 0; d < 64; ++d) acc[d] = acc[d] * a1 + r[d] * a2;
+      l_i = l_i * a1 + l2 * a2;
+      m_i = m;
+    }
   }
   if (qpos < g.Sq) {
     const float inv = 1.0f / l_i;
     const int64_t obase = b * g.os[0] + h * g.os[1] + qpos * g.os[2];
 #pragma unroll
-    for (int d = 0; d < 128; ++d)
-      if (d < D) store_from_float(g.o, obase + d * g.os[3], g.o_dtype, acc[d] * inv);
+    for (int d = 0; d < 64; ++d)
+      if (d0 + d < D) store_from_float(g.o, obase + (d0 + d) * g.os[3], g.o_dtype, acc[d] * inv);
   }
 }
 
@@ -1343,10 +1410,21 @@ static int attention_f32_launch(const void* q, const int64_t* qs, const void* k,
   g.q_scale = q_scale;
   g.causal = causal ? 1 : 0;
   g.o_dtype = o_dtype;
-  const int64_t qblocks = cdiv(Sq, AF_Q);
+  // Four waves splitting the keys of each query block when there are fewer than 512 blocks.
+  const int64_t lpq = D <= 64 ? 1 : 2;
+  const int64_t qblocks = cdiv(Sq, 64 / lpq);
   if (qblocks * B * H > 0x7fffffffLL) return NT_ERR_INVALID;
   g.q_blocks = (int)qblocks;
-  hipLaunchKernelGGL(attention_f32_kernel, dim3((unsigned)(qblocks * B * H)), dim3(AF_Q), 0, stream, g);
+  const bool split = qblocks * B * H < 512;
+  const dim3 grid((unsigned)(qblocks * B * H));
+  if (D <= 64 && split)
+    hipLaunchKernelGGL((attention_f32_kernel<64, 4>), grid, dim3(256), 0, stream, g);
+  else if (D <= 64)
+    hipLaunchKernelGGL((attention_f32_kernel<64, 1>), grid, dim3(64), 0, stream, g);
+  else if (split)
+    hipLaunchKernelGGL((attention_f32_kernel<128, 4>), grid, dim3(256), 0, stream, g);
+  else
+    hipLaunchKernelGGL((attention_f32_kernel<128, 1>), grid, dim3(64), 0, stream, g);
   return launch_status();
 }
 

@@ -695,6 +695,22 @@ def test_attention_padded_head_dims(d, causal, dtype):
     assert torch.all(obuf[..., d:] == 7.0)
 
 
+@pytest.mark.parametrize("d", (24, 64, 100, 128))
+@pytest.mark.parametrize("causal", (False, True))
+def test_attention_f32(d, causal):
+    # fp32 on the VALU kernel: one lane per query up to 64 dims, two above; ragged Sq, Sk;
+    # k and v also as transposed copies (d stride != 1: element-wise tile loads); fp32 math,
+    # so within 1e-4 of fp64.
+    sq, sk = 130, 300
+    q, k, v = (_randn((2, 3, s_, d), torch.float32, 80 + i) for i, s_ in enumerate((sq, sk, sk)))
+    scale = 1.0 / math.sqrt(d)
+    ref = F.scaled_dot_product_attention(q.double(), k.double(), v.double(), is_causal=causal, scale=scale)
+    for kk, vv in ((k, v), (k.transpose(2, 3).contiguous().transpose(2, 3), v.transpose(2, 3).contiguous().transpose(2, 3))):
+        o = torch.empty_like(q)
+        kernels.attention(q, kk, vv, o, causal=causal, q_scale=kernels.LOG2E * scale)
+        assert torch.allclose(o.double(), ref, atol=1e-4, rtol=1e-4), (d, causal)
+
+
 def test_attention_headline_causal():
     q, k, v = (_randn((4, 32, 4096, 128), torch.float16, 50 + i) for i in range(3))
     o = torch.empty_like(q)
