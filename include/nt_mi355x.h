@@ -125,8 +125,11 @@ int nt_max_pool2d_bf16(const void* x, const int64_t* x_strides, void* y, const i
  * 16-bit, 2-wide windows of stride 2 inside the input, unit inner strides, 16-byte aligned
  * input rows; 2-high windows with Q a multiple of 4 take the pair-row kernel, others the
  * per-plane kernel with Q a multiple of 8; 2 = the element-wise kernel, any shape; 3 = the
- * flat kernel: 2-high windows, Q a multiple of 8).  A forced kernel whose conditions do not
- * hold returns NT_ERR_INVALID before launching.  Replaces the
+ * flat kernel: 2-high windows, Q a multiple of 8; 4 = the LDS kernel: any window, stride,
+ * padding and dilation whose (kh - 1) * dh + 1 input rows fit 16 KiB of LDS, the default for
+ * the shapes the vector kernels do not take when x's rows are contiguous or whole 16-byte
+ * vectors).  A forced kernel whose conditions do not hold returns NT_ERR_INVALID before
+ * launching.  Replaces the
  * per-configuration launchers of the reference's auto-tuner for the max_pool2d
  * application (reference tests/test_max_pool2d.py:13-64). */
 int nt_max_pool2d_config_f32(const void* x, const int64_t* x_strides, void* y, const int64_t* y_strides,

@@ -10,10 +10,12 @@
 // consecutive units over all planes in one flat order, eight per lane per step with all
 // their loads issued first (pool_w2_pair_kernel).  Taller windows: one workgroup per (n, c)
 // plane, a lane producing 8 consecutive outputs from kh input rows of 16 elements
-// (pool_w2_plane_kernel).  Everything else runs the generic kernel, one lane per output.
+// (pool_w2_plane_kernel).  Other windows take strips of input rows through LDS
+// (pool_lds_kernel); what does not fit runs the generic kernel, one lane per output.
 #include "nt_common.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace nt {
 
@@ -86,10 +88,142 @@ __global__ __launch_bounds__(256) void pool_w2_plane_kernel(const uint16_t* __re
   }
 }
 
+// Any window, stride, padding and dilation, through LDS.  A workgroup takes G whole (n, c)
+// planes (G > 1 where planes are small and x and y both plane-contiguous), or one strip of
+// PR output rows of one plane.  It copies the input rows its windows reach into LDS once,
+// then every output takes its window's max out of LDS, consecutive lanes on consecutive
+// outputs.  So each input element is read from HBM once per workgroup (overlapping windows,
+// as 3 x 3 with stride 2, re-read only LDS) instead of once per window covering it.
+// Rows outside the input are not copied and count as padding.
+//   MODE 0: the copied rows are one contiguous range of x (rows of W elements back to back,
+//           and for G > 1 planes back to back): a scalar head up to x's first 16-byte
+//           boundary, 16-byte vectors, a scalar tail.  The tile starts at the range's
+//           address modulo 16 in LDS, so LDS and global addresses share their alignment.
+//   MODE 1: rows strided but each row whole 16-byte vectors (G == 1).
+//   MODE 2: any strides, element by element (G == 1).
+// U loads per lane are issued before their LDS stores.  KH, KW > 0 fix the window at
+// compile time; 0 reads it from the shape.
+#ifndef NT_POOL_LDS_BYTES
+#define NT_POOL_LDS_BYTES 16384
+#endif
+constexpr int POOL_LDS_BYTES = NT_POOL_LDS_BYTES;
+template <typename T, int MODE, int KH, int KW>
+__global__ __launch_bounds__(256) void pool_lds_kernel(const typename elem<T>::storage* __restrict__ x,
+                                                       typename elem<T>::storage* __restrict__ y, PoolShape s, int G,
+                                                       int PR, int strips) {
+  typedef typename elem<T>::storage S;
+  constexpr int V = MODE == 2 ? 1 : 16 / sizeof(S), U = 4;
+  typedef typename std::conditional<MODE == 2, S, u32x4>::type L;
+  extern __shared__ __attribute__((aligned(16))) unsigned char pool_lds[];
+  const int64_t b = blockIdx.x;
+  const int strip = (int)(b % strips);
+  const int64_t g0 = (b / strips) * G;
+  const int gn = (int)(s.N * s.C - g0 < G ? s.N * s.C - g0 : G);
+  const int W = (int)s.W, H = (int)s.H, P = (int)s.P, Q = (int)s.Q;
+  const int kh = KH > 0 ? KH : (int)s.kh, kw = KW > 0 ? KW : (int)s.kw;
+  const int sh = (int)s.sh, sw = (int)s.sw, ph = (int)s.ph, pw = (int)s.pw, dh = (int)s.dh, dw = (int)s.dw;
+  const int p0 = strip * PR, p1 = p0 + PR < P ? p0 + PR : P;
+  // input rows [hv0, hv1) of each plane are in the tile, row h at (h - hv0) * W; a plane
+  // spans ts elements of the tile
+  int hv0 = 0, hv1 = H;
+  if (G == 1) {
+    const int hs = p0 * sh - ph, he = (p1 - 1) * sh - ph + (kh - 1) * dh + 1;
+    hv0 = hs > 0 ? hs : 0;
+    hv1 = he < H ? he : H;
+  }
+  const int nrows = hv1 > hv0 ? hv1 - hv0 : 0, ts = H * W;
+  const int64_t c0 = g0 % s.C, n0 = g0 / s.C;
+  const S* xb = x + n0 * s.xs[0] + c0 * s.xs[1];
+  const int tid = threadIdx.x;
+  S* tile;
+  if (MODE == 0) {
+    const S* src = xb + (int64_t)hv0 * W;
+    const int len = (gn - 1) * ts + nrows * W;
+    const int shift = (int)((uintptr_t)src & 15);
+    tile = (S*)(pool_lds + shift);
+    int head = ((16 - shift) & 15) / (int)sizeof(S);
+    head = head < len ? head : len;
+    const int nv = (len - head) / V, tail0 = head + nv * V;
+    const int nscalar = head + len - tail0;
+    for (int e = tid; e < nscalar; e += 256) {
+      const int t = e < head ? e : tail0 + e - head;
+      tile[t] = src[t];
+    }
+    const u32x4* vs = (const u32x4*)(src + head);
+    u32x4* vt = (u32x4*)(tile + head);
+    for (int e0 = tid; e0 < nv; e0 += 256 * U) {
+      u32x4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (e0 + u * 256 < nv) v[u] = vs[e0 + u * 256];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (e0 + u * 256 < nv) vt[e0 + u * 256] = v[u];
+    }
+  } else {
+    tile = (S*)pool_lds;
+    const int vpr = W / V, n_units = nrows * vpr, xh = (int)s.xs[2], xw = (int)s.xs[3];
+    for (int e0 = tid; e0 < n_units; e0 += 256 * U) {
+      L v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int e = e0 + u * 256;
+        if (e < n_units) {
+          const int r = e / vpr, k = e - r * vpr;
+          v[u] = *(const L*)(xb + (hv0 + r) * xh + k * V * xw);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int e = e0 + u * 256;
+        if (e < n_units) {
+          const int r = e / vpr, k = e - r * vpr;
+          *(L*)(tile + r * W + k * V) = v[u];
+        }
+      }
+    }
+  }
+  __syncthreads();
+  const int np = p1 - p0, per_plane = np * Q;
+  S* yb = y + n0 * s.ys[0] + c0 * s.ys[1];  // for G > 1, y is plane-contiguous: plane g at g * P * Q
+  const int64_t ys2 = s.ys[2], ys3 = s.ys[3];
+  for (int o = tid; o < gn * per_plane; o += 256) {
+    const int g = o / per_plane, rem = o - g * per_plane;
+    const int pp = rem / Q, q = rem - pp * Q;
+    const int tb = g * ts - hv0 * W;  // tile offset of row 0 of plane g (rows below hv0 are never read)
+    const int hb = (p0 + pp) * sh - ph, wb = q * sw - pw;
+    // every tap reads LDS (a tap outside the input reads an address inside the plane's tile
+    // and its value is dropped), so the window's reads issue back to back
+    float m = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < (KH > 0 ? KH : 1); ++r) {
+      for (int rr = r; rr < (KH > 0 ? r + 1 : kh); ++rr) {
+        const int h = hb + rr * dh;
+        const bool hok = h >= hv0 && h < hv1;
+        const int row = tb + (hok ? h : hv0) * W;
+#pragma unroll
+        for (int u = 0; u < (KW > 0 ? KW : 1); ++u) {
+          for (int uu = u; uu < (KW > 0 ? u + 1 : kw); ++uu) {
+            const int w = wb + uu * dw;
+            const bool ok = hok && w >= 0 && w < W;
+            const float v = elem<T>::to_float(tile[row + (ok ? w : 0)]);
+            m = ok ? fmaxf(m, v) : m;
+          }
+        }
+      }
+    }
+    if (G > 1)
+      yb[o] = elem<T>::from_float(m);
+    else
+      yb[(int64_t)(p0 + pp) * ys2 + (int64_t)q * ys3] = elem<T>::from_float(m);
+  }
+}
+
 // config: 0 = the pair kernel for 2-high windows, else the plane kernel, where their
-// conditions hold, else the element-wise kernel; 1 = those vector kernels only; 2 =
-// element-wise kernel; 3 = the flat kernel below.  A forced kernel whose conditions do not
-// hold returns NT_ERR_INVALID unlaunched.
+// conditions hold, else the LDS strip kernel where a strip of one output row fits its LDS,
+// else the element-wise kernel; 1 = those vector kernels only; 2 = element-wise kernel;
+// 3 = the flat kernel below; 4 = the LDS strip kernel.  A forced kernel whose conditions do
+// not hold returns NT_ERR_INVALID unlaunched.
 // Flat kernel (kh == 2 form of the plane kernel): output vector g of the flattened (plane, row, vector)
 // order, U = 4 per lane per grid-stride step, the 16 loads of a step issued before any max
 // (one workgroup per plane left a ragged last pass per plane and only four loads in flight
@@ -207,7 +341,7 @@ static int pool_launch(const void* x, const int64_t* xs, void* y, const int64_t*
                        int64_t W, int64_t P, int64_t Q, int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph,
                        int64_t pw, int64_t dh, int64_t dw, hipStream_t stream, int config = 0) {
   typedef typename elem<T>::storage S;
-  if (config < 0 || config > 3) return NT_ERR_INVALID;
+  if (config < 0 || config > 4) return NT_ERR_INVALID;
   if (N < 0 || C < 0 || H < 0 || W < 0 || P < 0 || Q < 0 || kh <= 0 || kw <= 0 || sh <= 0 || sw <= 0 || dh <= 0 ||
       dw <= 0 || ph < 0 || pw < 0)
     return NT_ERR_INVALID;
@@ -230,9 +364,65 @@ static int pool_launch(const void* x, const int64_t* xs, void* y, const int64_t*
   // at most 2^19 lanes further) still fits an int
   constexpr int64_t MAX_UNITS = 0x7fffffffLL - (1LL << 24);
   const int64_t upp = P * (Q / 4), total_units = N * C * upp;
-  if ((config == 1 && !fast && !pair) || (config == 3 && !(fast && kh == 2))) return NT_ERR_INVALID;
+  // The LDS kernel.  Small planes: G whole planes per workgroup, as many as fit its LDS but
+  // no more than leave the chip 8 workgroups per CU, when x and y are plane-contiguous.
+  // Otherwise one strip of PR output rows of one plane: at most as many as the LDS holds the
+  // input rows of, and fewer where that leaves the chip under 8 workgroups per CU.  In-plane
+  // and in-tile indices are 32-bit; the grid stays under 2^24 workgroups of 256 lanes.
+  constexpr int64_t LDS_TARGET = 256 * 8, LDS_ROOM = POOL_LDS_BYTES - 16;
+  const int64_t per_row = W * (int64_t)sizeof(S), span = (kh - 1) * dh + 1, NC = N * C;
+  const bool rows_flat = xs[3] == 1 && xs[2] == W;
+  const bool planes_flat = rows_flat && xs[1] == H * W && xs[0] == C * H * W && ys[3] == 1 && ys[2] == Q &&
+                           ys[1] == P * Q && ys[0] == C * P * Q;
+  int64_t G = 1, PR = 0;
+  if (W * H <= 0x7fffffffLL && P * Q <= 0x7fffffffLL && P * ys[2] + Q * ys[3] <= 0x7fffffffLL &&
+      H * xs[2] + W * xs[3] <= 0x7fffffffLL) {
+    if (planes_flat && H * per_row <= LDS_ROOM / 2) {
+      G = std::min<int64_t>(LDS_ROOM / (H * per_row), cdiv(NC, LDS_TARGET));
+      G = std::max<int64_t>(G, 1);
+    }
+    if (G > 1) {
+      PR = P;
+    } else if (span * per_row <= LDS_ROOM) {
+      PR = std::min<int64_t>(P, 1 + (LDS_ROOM / per_row - span) / sh);
+      PR = std::max<int64_t>(1, std::min<int64_t>(PR, cdiv(P * NC, LDS_TARGET)));
+      PR = cdiv(P, cdiv(P, PR));  // strips of equal height
+    }
+  }
+  const int64_t strips = PR > 0 ? cdiv(P, PR) : 0, lds_blocks = strips * cdiv(NC, G);
+  const bool lds = PR > 0 && lds_blocks < (1LL << 24) && G * H * W <= 0x7fffffffLL;
+  const int64_t lds_bytes = G > 1 ? G * H * per_row + 16 : ((PR - 1) * sh + span) * per_row + 16;
+  const int lds_mode = rows_flat ? 0
+                       : (xs[3] == 1 && per_row % 16 == 0 && (uintptr_t)x % 16 == 0 &&
+                          (xs[0] * (int64_t)sizeof(S)) % 16 == 0 && (xs[1] * (int64_t)sizeof(S)) % 16 == 0 &&
+                          (xs[2] * (int64_t)sizeof(S)) % 16 == 0)
+                           ? 1
+                           : 2;
+  if ((config == 1 && !fast && !pair) || (config == 3 && !(fast && kh == 2)) || (config == 4 && !lds))
+    return NT_ERR_INVALID;
   const int64_t vpp = P * (Q / 8), total_vec = N * C * vpp;
-  if (pair && (config == 0 || config == 1) && total_units <= MAX_UNITS) {
+  if (config == 4 || (config == 0 && !fast && !pair && lds && lds_mode != 2)) {
+    const dim3 grid((unsigned)lds_blocks);
+    const unsigned shm = (unsigned)lds_bytes;
+    auto go = [&](auto kern) {
+      hipLaunchKernelGGL(kern, grid, dim3(256), shm, stream, (const S*)x, (S*)y, s, (int)G, (int)PR, (int)strips);
+    };
+    auto pick = [&](auto mode) {
+      constexpr int M = decltype(mode)::value;
+      if (kh == 3 && kw == 3)
+        go(pool_lds_kernel<T, M, 3, 3>);
+      else if (kh == 2 && kw == 2)
+        go(pool_lds_kernel<T, M, 2, 2>);
+      else
+        go(pool_lds_kernel<T, M, 0, 0>);
+    };
+    if (lds_mode == 0)
+      pick(std::integral_constant<int, 0>());
+    else if (lds_mode == 1)
+      pick(std::integral_constant<int, 1>());
+    else
+      pick(std::integral_constant<int, 2>());
+  } else if (pair && (config == 0 || config == 1) && total_units <= MAX_UNITS) {
     const int64_t blocks = std::min<int64_t>(cdiv(total_units, 256 * 8), 256 * 8);
     hipLaunchKernelGGL(pool_w2_pair_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, stream, (const uint16_t*)x,
                        (uint16_t*)y, s, (int)upp, (int)(Q / 4), (int)total_units);

@@ -998,7 +998,7 @@ def candidates(ctx):
     kernel), an attention plan for each attention kernel (pipelined one-wave-per-SIMD,
     eight-wave, four-wave), a softmax plan for each softmax kernel (register path with four,
     eight or one wave per workgroup, two-sweep) and a max_pool2d plan for each pooling kernel
-    (pair-row or plane, element-wise, flat): configurations the call's
+    (pair-row or plane, element-wise, flat, LDS strip): configurations the call's
     operands do not admit fail when bound or launched and drop out of the timing.  A generic
     tile program with real loops is a candidate only where no other plan fits."""
     from ninetoothed_amd import kernels

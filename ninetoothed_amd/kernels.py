@@ -132,8 +132,9 @@ def softmax(x, y, block=None, config=0):
 # ------------------------------------------------------------------ max_pool2d
 # Kernel configurations of max_pool2d that ``config`` can force (0: the library's choice):
 # 1 the vector kernels (pair-row kernel for 2-high windows, else one workgroup per plane),
-# 2 the element-wise kernel, 3 the flat kernel (2-high windows, 8 outputs per unit).
-POOL_CONFIGS = (1, 2, 3)
+# 2 the element-wise kernel, 3 the flat kernel (2-high windows, 8 outputs per unit),
+# 4 the LDS strip kernel (any window whose input rows fit 32 KiB of LDS).
+POOL_CONFIGS = (1, 2, 3, 4)
 
 
 def bind_max_pool2d(x, y, window, stride=None, padding=(0, 0), dilation=(1, 1), config=0):

@@ -274,8 +274,8 @@ def test_softmax_and_pool_plans_expand_into_kernels():
     xi, yo = torch.empty(2, 3, 16, 16, dtype=torch.float16), torch.empty(2, 3, 8, 8, dtype=torch.float16)
     ctx = pool._kernel.context(dict(zip(list(pool._kernel.params), (xi, yo))), {"WINDOW_HEIGHT": 2, "WINDOW_WIDTH": 2})
     described = [p.describe() for p in families.candidates(ctx)]
-    assert [(d["family"], d.get("config")) for d in described][:3] == [
-        ("max_pool2d", 1), ("max_pool2d", 2), ("max_pool2d", 3)]
+    assert [(d["family"], d.get("config")) for d in described][:4] == [
+        ("max_pool2d", 1), ("max_pool2d", 2), ("max_pool2d", 3), ("max_pool2d", 4)]
 
 
 @pytest.mark.gpu

@@ -839,7 +839,7 @@ def test_softmax_infinite_rows():
         assert torch.allclose(y.float(), torch.softmax(x.float(), -1), atol=1e-3, rtol=1e-2), cols
 
 
-@pytest.mark.parametrize("config", (1, 2, 3))
+@pytest.mark.parametrize("config", (1, 2, 3, 4))
 def test_max_pool2d_configs(config):
     from ninetoothed_amd.errors import KernelLaunchError
 
@@ -866,5 +866,37 @@ def test_max_pool2d_configs(config):
         with pytest.raises(KernelLaunchError):
             kernels.max_pool2d(x2, y2, (3, 2), stride=(2, 3), padding=(1, 1), config=config)
     else:
-        kernels.max_pool2d(x2, y2, (3, 2), stride=(2, 3), padding=(1, 1), config=2)
+        kernels.max_pool2d(x2, y2, (3, 2), stride=(2, 3), padding=(1, 1), config=config)
         assert torch.equal(y2, ref)
+
+
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16, torch.float32))
+def test_max_pool2d_overlapping_windows(dtype):
+    """Overlapping and padded windows (the LDS strip kernel) against F.max_pool2d, bit-exact:
+    the ResNet stem pool (3x3, stride 2, padding 1) on rows of whole 16-byte vectors, an odd
+    width (element-wise staging), ceil mode, dilation, a strided input, planes split into
+    several strips, and a window too tall for the LDS (the element-wise kernel)."""
+    cases = [
+        ((4, 64, 112, 112), (3, 3), (2, 2), (1, 1), (1, 1), False),
+        ((3, 5, 55, 55), (3, 3), (2, 2), (0, 0), (1, 1), True),
+        ((2, 7, 33, 40), (3, 3), (1, 1), (1, 1), (1, 1), False),
+        ((2, 3, 29, 24), (5, 3), (2, 1), (2, 1), (2, 3), True),
+        ((1, 2, 300, 2048), (3, 3), (2, 2), (1, 1), (1, 1), False),
+        ((1, 2, 40, 4096), (7, 2), (1, 2), (3, 0), (1, 1), False),
+    ]
+    for i, (shape, k, st, pad, dil, ceil) in enumerate(cases):
+        x = _randn(shape, dtype, 40 + i)
+        ref = F.max_pool2d(x, k, st, pad, dil, ceil_mode=ceil)
+        y = torch.empty_like(ref)
+        kernels.max_pool2d(x, y, k, st, pad, dil)
+        assert torch.equal(y, ref), (shape, k, st, pad, dil, ceil)
+        y.fill_(0)
+        kernels.max_pool2d(x, y, k, st, pad, dil, config=2)
+        assert torch.equal(y, ref), (shape, k, st, pad, dil, ceil)
+    base = _randn((3, 8, 60, 64), dtype, 50)
+    for xs in (base[:, ::2, 1:, :], base[:, ::2, 1:, 2:]):  # strided channels, row and column offsets
+        ref = F.max_pool2d(xs, 3, 2, 1)
+        for config in (0, 4):
+            y = torch.empty_like(ref)
+            kernels.max_pool2d(xs, y, (3, 3), (2, 2), (1, 1), config=config)
+            assert torch.equal(y, ref), (xs.shape, config)
