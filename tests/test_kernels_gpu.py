@@ -893,6 +893,18 @@ def test_max_pool2d_overlapping_windows(dtype):
         y.fill_(0)
         kernels.max_pool2d(x, y, k, st, pad, dil, config=2)
         assert torch.equal(y, ref), (shape, k, st, pad, dil, ceil)
+    # many small planes: several whole planes per workgroup, a partial last group, ranges
+    # starting at every 16-byte phase; and the same input into an output that is not
+    # plane-contiguous (one plane per workgroup)
+    x = _randn((3, 1111, 9, 14), dtype, 48)  # ceil mode adds an output column
+    for ceil in (False, True):
+        ref = F.max_pool2d(x, 3, 2, 1, ceil_mode=ceil)
+        y = torch.empty_like(ref)
+        kernels.max_pool2d(x, y, (3, 3), (2, 2), (1, 1))
+        assert torch.equal(y, ref), ceil
+        yt = torch.empty(ref.shape[2], ref.shape[3], 3, 1111, dtype=dtype, device=DEV).permute(2, 3, 0, 1)
+        kernels.max_pool2d(x, yt, (3, 3), (2, 2), (1, 1))
+        assert torch.equal(yt, ref), ceil
     base = _randn((3, 8, 60, 64), dtype, 50)
     for xs in (base[:, ::2, 1:, :], base[:, ::2, 1:, 2:]):  # strided channels, row and column offsets
         ref = F.max_pool2d(xs, 3, 2, 1)
