@@ -375,7 +375,7 @@ static int pool_launch(const void* x, const int64_t* xs, void* y, const int64_t*
   const bool planes_flat = rows_flat && xs[1] == H * W && xs[0] == C * H * W && ys[3] == 1 && ys[2] == Q &&
                            ys[1] == P * Q && ys[0] == C * P * Q;
   int64_t G = 1, PR = 0;
-  if (W * H <= 0x7fffffffLL && P * Q <= 0x7fffffffLL && P * ys[2] + Q * ys[3] <= 0x7fffffffLL &&
+  if (H > 0 && W > 0 && W * H <= 0x7fffffffLL && P * Q <= 0x7fffffffLL && P * ys[2] + Q * ys[3] <= 0x7fffffffLL &&
       H * xs[2] + W * xs[3] <= 0x7fffffffLL) {
     if (planes_flat && H * per_row <= LDS_ROOM / 2) {
       G = std::min<int64_t>(LDS_ROOM / (H * per_row), cdiv(NC, LDS_TARGET));

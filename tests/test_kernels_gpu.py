@@ -870,6 +870,34 @@ def test_max_pool2d_configs(config):
         assert torch.equal(y2, ref)
 
 
+def test_max_pool2d_empty_input_plane():
+    """A zero-width (or zero-height) input whose padding still gives outputs: every window
+    lies in the padding, so every output is -inf (through the C ABI: torch refuses the shape,
+    and an empty tensor has no data pointer).  The kernel choice must not divide by the
+    empty row's size."""
+    import ctypes
+
+    from ninetoothed_amd import _lib
+
+    lib = _lib.load()
+    x = torch.zeros(64, dtype=torch.float16, device=DEV)  # never read: every window is padding
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for h, w, kh, kw, ph, pw, p, q in ((4, 0, 2, 2, 1, 1, 5, 1), (0, 6, 2, 2, 1, 1, 1, 7)):
+        y = torch.zeros(2, 3, p, q, dtype=torch.float16, device=DEV)
+        for config in (0, 2):
+            code = lib.nt_max_pool2d_config_f16(x.data_ptr(), _lib.int64_array((3 * h * w, h * w, w, 1)), y.data_ptr(),
+                                                _lib.int64_array(y.stride()), 2, 3, h, w, p, q, kh, kw, 1, 1, ph, pw,
+                                                1, 1, stream, config)
+            torch.cuda.synchronize()
+            assert code == 0, (h, w, config)
+            assert torch.isneginf(y).all(), (h, w, config)
+            y.zero_()
+        code = lib.nt_max_pool2d_config_f16(x.data_ptr(), _lib.int64_array((3 * h * w, h * w, w, 1)), y.data_ptr(),
+                                            _lib.int64_array(y.stride()), 2, 3, h, w, p, q, kh, kw, 1, 1, ph, pw, 1, 1,
+                                            stream, 4)
+        assert code != 0, (h, w)  # the LDS kernel does not take an empty plane
+
+
 @pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16, torch.float32))
 def test_max_pool2d_overlapping_windows(dtype):
     """Overlapping and padded windows (the LDS strip kernel) against F.max_pool2d, bit-exact:
