@@ -752,7 +752,7 @@ static int64_t nhwc_bytes(int64_t N, int64_t C, int64_t H, int64_t W, int64_t K,
 // filter over 64 channels runs as 96, the last 32 zero).
 static int64_t dma_channels(int64_t C, int64_t R, int64_t S) {
   int64_t c = cdiv(C, 32) * 32;
-  if (c * R * S < 96) c = cdiv(cdiv(96, R * S), 32) * 32;
+  if (R * S > 0 && c * R * S < 96) c = cdiv(cdiv(96, R * S), 32) * 32;
   return c;
 }
 
@@ -832,7 +832,8 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
   const bool dma = config != 2 && dma_fits(C32);
   const int64_t Cl = dma ? C32 : C64;
   const int64_t need = nhwc_bytes(N, Cl, H, W, K, R, S, ph, pw);
-  const bool nhwc = config != 3 && workspace != nullptr && workspace_bytes >= need && (uintptr_t)workspace % 256 == 0 &&
+  // (an empty filter, R or S zero, sums nothing: the direct kernel writes the zeros)
+  const bool nhwc = config != 3 && R * S > 0 && workspace != nullptr && workspace_bytes >= need && (uintptr_t)workspace % 256 == 0 &&
                     (P - 1) * sh + (R - 1) * dh < Hp && (Q - 1) * sw + (S - 1) * dw < Wp;
   if ((config == 1 && !(nhwc && dma)) || (config == 2 && !nhwc)) return NT_ERR_INVALID;
   if (nhwc) {

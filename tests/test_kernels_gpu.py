@@ -589,6 +589,34 @@ def test_conv2d_dma_any_q(case, dtype):
     assert torch.allclose(y.float(), ref, atol=2e-2, rtol=1e-2)
 
 
+def test_conv2d_empty_filter():
+    """A filter with no taps (R or S zero) sums nothing: every output is zero, with or
+    without a workspace (through the C ABI: torch refuses the shape, and an empty tensor has
+    no data pointer).  The kernel choice must not divide by R * S."""
+    import ctypes
+
+    from ninetoothed_amd import _lib
+
+    lib = _lib.load()
+    x = _randn((2, 8, 6, 6), torch.float16, 60)
+    w = torch.zeros(64, dtype=torch.float16, device=DEV)  # never read: the filter has no taps
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device=DEV)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    code16 = _lib.dtype_code(torch.float16)
+    for r, s_ in ((0, 3), (3, 0)):
+        p, q = 6 + 2 - r + 1, 6 + 2 - s_ + 1
+        y = torch.full((2, 4, p, q), float("nan"), dtype=torch.float16, device=DEV)
+        for workspace, nbytes in ((None, 0), (ws.data_ptr(), ws.numel())):
+            y.fill_(float("nan"))
+            code = lib.nt_conv2d_f16(x.data_ptr(), _lib.int64_array(x.stride()), w.data_ptr(),
+                                     _lib.int64_array((8 * r * s_, r * s_, s_, 1)), y.data_ptr(),
+                                     _lib.int64_array(y.stride()), code16, 2, 8, 6, 6, 4, r, s_, p, q, 1, 1, 1, 1, 1, 1,
+                                     code16, workspace, nbytes, stream)
+            torch.cuda.synchronize()
+            assert code == 0, (r, s_, workspace)
+            assert (y == 0).all(), (r, s_, workspace)
+
+
 def test_conv2d_forced_path_rejects_unfit_call():
     from ninetoothed_amd.errors import KernelLaunchError
 
