@@ -286,6 +286,8 @@ int nt_conv2d_noalloc_bf16(const void* x, const int64_t* x_strides, const void* 
  * This is the attention application (reference tests/test_attention.py:45-70),
  * whose q pre-scale is the constant 1.44269504089 and whose causal mask is
  * q_pos >= k_pos.  Tensors are [B, H, S, D] with arbitrary strides; D <= 128.
+ * With no keys (Sk == 0) every output is zero, as torch's scaled_dot_product_attention
+ * gives; q, k and v are then not read and may be null.
  * ------------------------------------------------------------------------- */
 int nt_attention_f16(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
                      const void* v, const int64_t* v_strides, void* o, const int64_t* o_strides,

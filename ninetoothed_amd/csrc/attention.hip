@@ -1170,6 +1170,28 @@ __global__ __launch_bounds__(AT_THREADS) void attention_generic_kernel(AttnArgs 
 // (the fast conditions); 3 = the four-wave kernels (attention_kernel, or
 // attention_generic_kernel for other strides).
 // A forced configuration whose conditions do not hold returns NT_ERR_INVALID unlaunched.
+// No keys: every query's weights are an empty softmax and its output is zero (as torch's
+// scaled_dot_product_attention defines it); o is filled, element by element over its strides.
+__global__ __launch_bounds__(256) void attention_empty_keys_kernel(void* o, AttnArgs g) {
+  const int64_t total = g.B * g.H * g.Sq * g.D;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int64_t d = e % g.D, t = e / g.D;
+    const int64_t s = t % g.Sq, u = t / g.Sq;
+    const int64_t h = u % g.H, b = u / g.H;
+    store_from_float(o, b * g.os[0] + h * g.os[1] + s * g.os[2] + d * g.os[3], g.o_dtype, 0.f);
+  }
+}
+
+static int attention_empty_keys(void* o, const int64_t* os, int o_dtype, int64_t B, int64_t H, int64_t Sq, int64_t D,
+                                hipStream_t stream) {
+  AttnArgs g{};
+  g.B = B; g.H = H; g.Sq = Sq; g.D = D; g.o_dtype = o_dtype;
+  for (int i = 0; i < 4; ++i) g.os[i] = os[i];
+  const int64_t blocks = std::min<int64_t>(cdiv(B * H * Sq * D, 256), 4096);
+  hipLaunchKernelGGL(attention_empty_keys_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, o, g);
+  return launch_status();
+}
+
 template <typename T>
 static int attention_launch(const void* q, const int64_t* qs, const void* k, const int64_t* ks, const void* v,
                             const int64_t* vs, void* o, const int64_t* os, int o_dtype, int64_t B, int64_t H,
@@ -1179,7 +1201,9 @@ static int attention_launch(const void* q, const int64_t* qs, const void* k, con
   if (B < 0 || H < 0 || Sq < 0 || Sk < 0 || D < 0 || D > 128) return NT_ERR_INVALID;
   if (!valid_dtype(o_dtype)) return NT_ERR_INVALID;
   if (B * H * Sq * D == 0) return 0;
-  if (!q || !k || !v || !o || !qs || !ks || !vs || !os) return NT_ERR_INVALID;
+  if (!o || !os) return NT_ERR_INVALID;
+  if (Sk == 0) return attention_empty_keys(o, os, o_dtype, B, H, Sq, D, stream);
+  if (!q || !k || !v || !qs || !ks || !vs) return NT_ERR_INVALID;
   AttnArgs g{};
   g.q = q; g.k = k; g.v = v; g.o = o;
   for (int i = 0; i < 4; ++i) {
@@ -1397,7 +1421,9 @@ static int attention_f32_launch(const void* q, const int64_t* qs, const void* k,
   if (B < 0 || H < 0 || Sq < 0 || Sk < 0 || D < 0 || D > 128) return NT_ERR_INVALID;
   if (!valid_dtype(o_dtype)) return NT_ERR_INVALID;
   if (B * H * Sq * D == 0) return 0;
-  if (!q || !k || !v || !o || !qs || !ks || !vs || !os) return NT_ERR_INVALID;
+  if (!o || !os) return NT_ERR_INVALID;
+  if (Sk == 0) return attention_empty_keys(o, os, o_dtype, B, H, Sq, D, stream);
+  if (!q || !k || !v || !qs || !ks || !vs) return NT_ERR_INVALID;
   AttnArgs g{};
   g.q = q; g.k = k; g.v = v; g.o = o;
   for (int i = 0; i < 4; ++i) {

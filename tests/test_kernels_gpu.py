@@ -723,6 +723,20 @@ def test_attention_padded_head_dims(d, causal, dtype):
     assert torch.all(obuf[..., d:] == 7.0)
 
 
+@pytest.mark.parametrize("dtype", (torch.float16, torch.float32))
+def test_attention_empty_keys(dtype):
+    """No keys: every output is zero, as F.scaled_dot_product_attention gives (the empty key
+    tensors have no data pointer; the launcher needs none)."""
+    q = _randn((2, 3, 5, 64), dtype, 70)
+    k = torch.empty(2, 3, 0, 64, dtype=dtype, device=DEV)
+    for causal in (False, True):
+        o = torch.full_like(q, float("nan"))
+        kernels.attention(q, k, k, o, causal)
+        assert torch.equal(o, torch.zeros_like(q)), causal
+        assert torch.equal(o.float().cpu(), F.scaled_dot_product_attention(q.float().cpu(), k.float().cpu(),
+                                                                           k.float().cpu()))
+
+
 @pytest.mark.parametrize("d", (24, 64, 100, 128))
 @pytest.mark.parametrize("causal", (False, True))
 def test_attention_f32(d, causal):
