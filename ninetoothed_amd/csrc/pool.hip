@@ -103,6 +103,23 @@ __global__ __launch_bounds__(256) void pool_w2_plane_kernel(const uint16_t* __re
 //   MODE 2: any strides, element by element (G == 1).
 // U loads per lane are issued before their LDS stores.  KH, KW > 0 fix the window at
 // compile time; 0 reads it from the shape.
+// Division by a divisor fixed for the launch, for 0 <= n < 2^31: with l = ceil(log2 d) and
+// m = floor(2^32 (2^l - d) / d) + 1, n / d = (mulhi(n, m) + n) >> l (the round-up
+// multiplier method of Granlund and Montgomery, "Division by invariant integers using
+// multiplication", 1994); a few instructions where a runtime 32-bit division takes dozens.
+struct PoolDiv {
+  uint32_t m, l;
+};
+static PoolDiv pool_div(uint32_t d) {
+  uint32_t l = 0;
+  while ((1ull << l) < d) ++l;
+  return PoolDiv{(uint32_t)((((1ull << l) - d) << 32) / d + 1), l};
+}
+__device__ __forceinline__ int pool_divide(int n, PoolDiv f) {
+  const uint32_t t = __umulhi((uint32_t)n, f.m);
+  return (int)((t + (uint32_t)n) >> f.l);  // t <= n < 2^31: the sum fits 32 bits
+}
+
 #ifndef NT_POOL_LDS_BYTES
 #define NT_POOL_LDS_BYTES 16384
 #endif
@@ -110,7 +127,7 @@ constexpr int POOL_LDS_BYTES = NT_POOL_LDS_BYTES;
 template <typename T, int MODE, int KH, int KW>
 __global__ __launch_bounds__(256) void pool_lds_kernel(const typename elem<T>::storage* __restrict__ x,
                                                        typename elem<T>::storage* __restrict__ y, PoolShape s, int G,
-                                                       int PR, int strips) {
+                                                       int PR, int strips, PoolDiv div_q, PoolDiv div_pq) {
   typedef typename elem<T>::storage S;
   constexpr int V = MODE == 2 ? 1 : 16 / sizeof(S), U = 4;
   typedef typename std::conditional<MODE == 2, S, u32x4>::type L;
@@ -188,8 +205,8 @@ __global__ __launch_bounds__(256) void pool_lds_kernel(const typename elem<T>::s
   S* yb = y + n0 * s.ys[0] + c0 * s.ys[1];  // for G > 1, y is plane-contiguous: plane g at g * P * Q
   const int64_t ys2 = s.ys[2], ys3 = s.ys[3];
   for (int o = tid; o < gn * per_plane; o += 256) {
-    const int g = o / per_plane, rem = o - g * per_plane;
-    const int pp = rem / Q, q = rem - pp * Q;
+    const int g = G > 1 ? pool_divide(o, div_pq) : 0, rem = o - g * per_plane;  // G > 1: per_plane = P * Q
+    const int pp = pool_divide(rem, div_q), q = rem - pp * Q;
     const int tb = g * ts - hv0 * W;  // tile offset of row 0 of plane g (rows below hv0 are never read)
     const int hb = (p0 + pp) * sh - ph, wb = q * sw - pw;
     // every tap reads LDS (a tap outside the input reads an address inside the plane's tile
@@ -380,6 +397,7 @@ static int pool_launch(const void* x, const int64_t* xs, void* y, const int64_t*
     if (planes_flat && H * per_row <= LDS_ROOM / 2) {
       G = std::min<int64_t>(LDS_ROOM / (H * per_row), cdiv(NC, LDS_TARGET));
       G = std::max<int64_t>(G, 1);
+      if (G * P * Q > 0x7fffffffLL) G = 1;  // a group's output index stays a 32-bit int
     }
     if (G > 1) {
       PR = P;
@@ -404,8 +422,10 @@ static int pool_launch(const void* x, const int64_t* xs, void* y, const int64_t*
   if (config == 4 || (config == 0 && !fast && !pair && lds && lds_mode != 2)) {
     const dim3 grid((unsigned)lds_blocks);
     const unsigned shm = (unsigned)lds_bytes;
+    const PoolDiv div_q = pool_div((uint32_t)Q), div_pq = pool_div((uint32_t)(G > 1 ? P * Q : 1));
     auto go = [&](auto kern) {
-      hipLaunchKernelGGL(kern, grid, dim3(256), shm, stream, (const S*)x, (S*)y, s, (int)G, (int)PR, (int)strips);
+      hipLaunchKernelGGL(kern, grid, dim3(256), shm, stream, (const S*)x, (S*)y, s, (int)G, (int)PR, (int)strips,
+                         div_q, div_pq);
     };
     auto pick = [&](auto mode) {
       constexpr int M = decltype(mode)::value;
