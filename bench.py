@@ -293,6 +293,24 @@ def _configs(torch, ninetoothed, pg):
     out.append(dict(name="max_pool2d_fp16", workload="fp16 max_pool2d 2x2 s2, NCHW [32,128,112,112], U(-1,1)",
                     setup=pool, work=pool_bytes, unit="GB/s", bound="hbm", peak=PEAK["hbm"], dtype="fp16"))
 
+    # Not in the default run (name it with --only): ResNet's stem pool, overlapping padded
+    # windows (the LDS kernel), through the library's max_pool2d entry point.
+    stem_bytes = (32 * 64 * 112 * 112 + 32 * 64 * 56 * 56) * 2
+
+    def stem_pool():
+        from ninetoothed_amd import kernels
+        fns = []
+        for _ in range(_sets(stem_bytes)):
+            x = rand((32, 64, 112, 112), torch.float16, -1.0, 1.0)
+            y = torch.empty((32, 64, 56, 56), dtype=torch.float16, device=dev)
+            launch = kernels.bind_max_pool2d(x, y, (3, 3), (2, 2), (1, 1))
+            fns.append(lambda x=x, y=y, launch=launch: launch(x, y))
+        return fns
+
+    out.append(dict(name="max_pool2d_3x3s2p1_fp16", workload="fp16 max_pool2d 3x3 s2 pad 1, NCHW [32,64,112,112], U(-1,1)",
+                    setup=stem_pool, work=stem_bytes, unit="GB/s", bound="hbm", peak=PEAK["hbm"], dtype="fp16",
+                    extra=True))
+
     def conv():
         x = randn((16, 256, 56, 56), torch.float16)
         w = randn((256, 256, 3, 3), torch.float16, 1.0 / math.sqrt(256 * 9))
@@ -393,7 +411,7 @@ def main():
     warmup, samples = max(args.warmup, 10), max(args.steps, args.samples)
     results = []
     for cfg in configs:
-        if only and cfg["name"] not in only:
+        if (only and cfg["name"] not in only) or (not only and cfg.get("extra")):
             continue
         fns = cfg["setup"]()
         sec, wall, each = _time(torch, fns, args.steps, warmup, samples)
