@@ -809,14 +809,15 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs g) {
 }
 
 // fp32 GEMMs of at most a few hundred 32 x 32 tiles (e.g. 512^3): one tile per
-// workgroup of sixteen waves, each wave multiplying a sixteenth of K with its operands
-// loaded straight into registers (one load phase, all loads in flight together), then
-// the sixteen partial tiles summed through LDS.  MFMA step s of a 32-deep k chunk uses
-// k = 8 t + s in lane group t (the sum is over all k, so any bijection will do), so a
+// workgroup of eight waves, each wave multiplying an eighth of K with its operands
+// loaded straight into registers, then the eight partial tiles summed through LDS, two
+// outputs per lane.  (Sixteen waves of one 32-deep chunk each measured 10.4 us median at
+// 512^3 against 9.9-10.0 for eight; four were no faster.)  MFMA step s of a 32-deep k chunk
+// uses k = 8 t + s in lane group t (the sum is over all k, so any bijection will do), so a
 // lane's a values for the chunk are eight consecutive floats of one row.
-constexpr int F32S_WAVES = 16;
+constexpr int F32S_WAVES = 8;
 template <bool AVEC>
-__global__ __launch_bounds__(1024) void gemm_f32_splitk_kernel(GemmArgs g) {
+__global__ __launch_bounds__(64 * F32S_WAVES) void gemm_f32_splitk_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(16))) float part[F32S_WAVES * F32_TM * F32_TN];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -871,15 +872,16 @@ __global__ __launch_bounds__(1024) void gemm_f32_splitk_kernel(GemmArgs g) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) mine[(i * 16 + 4 * t + v) * F32_TN + j * 16 + r16] = acc[i][j][v];
   __syncthreads();
-  const int e = tid;  // one output element per lane
-  float sum = 0.f;
+  for (int e = tid; e < F32_TM * F32_TN; e += 64 * F32S_WAVES) {
+    float sum = 0.f;
 #pragma unroll
-  for (int w = 0; w < F32S_WAVES; ++w) sum += part[w * (F32_TM * F32_TN) + e];
-  const int64_t row = m0 + e / F32_TN, col = n0 + e % F32_TN;
-  if (row < g.M && col < g.N) {
-    float v = g.alpha * round_through(sum, g.round_dtype);
-    if (g.c) v += g.beta * load_c<false>(g, row * g.sc_m + col * g.sc_n);
-    store_from_float(g.out, row * g.so_m + col * g.so_n, g.out_dtype, v);
+    for (int w = 0; w < F32S_WAVES; ++w) sum += part[w * (F32_TM * F32_TN) + e];
+    const int64_t row = m0 + e / F32_TN, col = n0 + e % F32_TN;
+    if (row < g.M && col < g.N) {
+      float v = g.alpha * round_through(sum, g.round_dtype);
+      if (g.c) v += g.beta * load_c<false>(g, row * g.sc_m + col * g.sc_n);
+      store_from_float(g.out, row * g.so_m + col * g.so_n, g.out_dtype, v);
+    }
   }
 }
 
@@ -1248,9 +1250,9 @@ static int gemm32_launch(GemmArgs g, hipStream_t stream) {
   if (tiles_m * tiles_n <= 512 && g.K >= 64) {
     const bool avec = g.sa_k == 1 && g.sa_m % 4 == 0 && (uintptr_t)g.a % 16 == 0;
     if (avec)
-      hipLaunchKernelGGL(gemm_f32_splitk_kernel<true>, dim3((unsigned)(tiles_m * tiles_n)), dim3(1024), 0, stream, g);
+      hipLaunchKernelGGL(gemm_f32_splitk_kernel<true>, dim3((unsigned)(tiles_m * tiles_n)), dim3(64 * F32S_WAVES), 0, stream, g);
     else
-      hipLaunchKernelGGL(gemm_f32_splitk_kernel<false>, dim3((unsigned)(tiles_m * tiles_n)), dim3(1024), 0, stream, g);
+      hipLaunchKernelGGL(gemm_f32_splitk_kernel<false>, dim3((unsigned)(tiles_m * tiles_n)), dim3(64 * F32S_WAVES), 0, stream, g);
     return launch_status();
   }
   // More tiles: the MFMA kernel with 128 x 128 tiles when they alone fill the GPU, else 64 x 64.
