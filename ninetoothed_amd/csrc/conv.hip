@@ -237,7 +237,15 @@ __global__ __launch_bounds__(256) void filter_krsc_kernel(const uint16_t* __rest
 // 16-bit values with v_perm_b32, eight 16-byte stores along c (one per position).  Needs
 // unit w stride, 16-byte aligned input rows and W % 8 == 0.  Workgroups past N * Hp:
 // the filter into K-R-S-C, one (k, r, s) row of C channels at a time.
-template <typename T>
+// STAGE (C * W * 2 <= RELAYOUT_STAGE_BYTES): lanes along w for the loads (each load
+// instruction reads runs of one channel row), the transposed chunks into LDS in the output
+// row's order, 16-byte chunk (pos, cb) at pos * C/8 + (cb ^ (pos / 8 & mask)) (mask < 8
+// divides C/8, so the XOR stays inside the row; it spreads one store instruction's chunks,
+// eight positions apart, over the banks), then consecutive lanes copy the W * C values of
+// the row out (each store instruction one contiguous run).  Otherwise lanes along channel
+// chunks, stored straight from registers.
+constexpr int RELAYOUT_STAGE_BYTES = 32768;
+template <typename T, bool STAGE>
 __global__ __launch_bounds__(256) void conv_relayout_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ xp,
                                                             const uint16_t* __restrict__ w, uint16_t* __restrict__ wt,
                                                             ConvArgs g, int64_t Hp, int64_t Wp) {
@@ -275,12 +283,9 @@ __global__ __launch_bounds__(256) void conv_relayout_kernel(const uint16_t* __re
   }
   const uint16_t* xb = x + n * g.xs[0] + h * g.xs[2];
   const int64_t wblocks = W / 8;
-  for (int64_t e = tid; e < cchunks * wblocks; e += 256) {
-    // lanes along channel chunks: each store instruction writes whole runs of a position's
-    // channels (12.6-12.9 us against 13.5-13.8 with lanes along w, whose loads coalesced
-    // instead, at [16,256,56,56])
-    const int64_t wb = e / cchunks, cb = e % cchunks;
-    u32x4 in[8], out[8];
+  // eight channel rows at columns wb*8 .. +7 -> eight positions of channel chunk cb
+  auto transpose = [&](int64_t cb, int64_t wb, u32x4 (&out)[8]) {
+    u32x4 in[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
       in[i] = cb * 8 + i < g.Cr ? *(const u32x4*)(xb + (cb * 8 + i) * g.xs[1] + wb * 8) : zero;
@@ -291,8 +296,35 @@ __global__ __launch_bounds__(256) void conv_relayout_kernel(const uint16_t* __re
       out[j] = u32x4{__builtin_amdgcn_perm(in[1][d], in[0][d], sel), __builtin_amdgcn_perm(in[3][d], in[2][d], sel),
                      __builtin_amdgcn_perm(in[5][d], in[4][d], sel), __builtin_amdgcn_perm(in[7][d], in[6][d], sel)};
     }
+  };
+  if constexpr (STAGE) {
+    __shared__ __attribute__((aligned(16))) u32x4 stage[RELAYOUT_STAGE_BYTES / 16];
+    const int cc = (int)cchunks, wbk = (int)wblocks;
+    const int mask = cc % 8 == 0 ? 7 : cc % 4 == 0 ? 3 : cc % 2 == 0 ? 1 : 0;
+    for (int e = tid; e < cc * wbk; e += 256) {
+      const int cb = e / wbk, wb = e - cb * wbk;
+      u32x4 out[8];
+      transpose(cb, wb, out);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) *(u32x4*)(out_row + (g.pw + wb * 8 + j) * C + cb * 8) = out[j];
+      for (int j = 0; j < 8; ++j) stage[(wb * 8 + j) * cc + (cb ^ (wb & mask))] = out[j];
+    }
+    __syncthreads();
+    u32x4* dst = (u32x4*)(out_row + g.pw * C);  // positions pw .. pw + W - 1: W * C/8 chunks in a row
+    for (int k = tid; k < (int)W * cc; k += 256) {
+      const int pos = k / cc, cb = k - pos * cc;
+      dst[k] = stage[pos * cc + (cb ^ ((pos >> 3) & mask))];
+    }
+  } else {
+    for (int64_t e = tid; e < cchunks * wblocks; e += 256) {
+      // lanes along channel chunks: each store instruction writes whole runs of a position's
+      // channels (12.6-12.9 us against 13.5-13.8 with lanes along w, whose loads coalesced
+      // instead, at [16,256,56,56])
+      const int64_t wb = e / cchunks, cb = e % cchunks;
+      u32x4 out[8];
+      transpose(cb, wb, out);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) *(u32x4*)(out_row + (g.pw + wb * 8 + j) * C + cb * 8) = out[j];
+    }
   }
 }
 
@@ -854,8 +886,12 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
                                (xs[1] * 2) % 16 == 0 && (xs[2] * 2) % 16 == 0;
     if (fast_relayout) {
       if (N * Hp + fblocks > 0x7fffffffLL) return NT_ERR_INVALID;
-      hipLaunchKernelGGL(conv_relayout_kernel<T>, dim3((unsigned)(N * Hp + fblocks)), dim3(256), 0, stream,
-                         (const uint16_t*)x, xp, (const uint16_t*)w, wt, g, Hp, Wp);
+      if (Cl * W * 2 <= RELAYOUT_STAGE_BYTES)
+        hipLaunchKernelGGL((conv_relayout_kernel<T, true>), dim3((unsigned)(N * Hp + fblocks)), dim3(256), 0, stream,
+                           (const uint16_t*)x, xp, (const uint16_t*)w, wt, g, Hp, Wp);
+      else
+        hipLaunchKernelGGL((conv_relayout_kernel<T, false>), dim3((unsigned)(N * Hp + fblocks)), dim3(256), 0, stream,
+                           (const uint16_t*)x, xp, (const uint16_t*)w, wt, g, Hp, Wp);
     } else {
       const int64_t relayout_blocks = N * Hp * cdiv(Cl, 64);
       if (relayout_blocks > 0x7fffffffLL) return NT_ERR_INVALID;
