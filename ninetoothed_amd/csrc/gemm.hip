@@ -1017,7 +1017,9 @@ static int gemm16_launch(GemmArgs g, hipStream_t stream, int config = 0) {
   if (tiles_m * tiles_n > 0x7fffffffLL) return NT_ERR_INVALID;
   g.tiles_m = (int)tiles_m;
   g.tiles_n = (int)tiles_n;
-  const bool aligned = g.sa_k == 1 && g.sb_n == 1 && (uintptr_t)g.a % 16 == 0 && (uintptr_t)g.b % 16 == 0 &&
+  // (row strides non-negative: the DMA kernels address panels with unsigned 32-bit offsets)
+  const bool aligned = g.sa_k == 1 && g.sb_n == 1 && g.sa_m >= 0 && g.sb_k >= 0 && (uintptr_t)g.a % 16 == 0 &&
+                       (uintptr_t)g.b % 16 == 0 &&
                        (g.sa_m * 2) % 16 == 0 && (g.sb_k * 2) % 16 == 0;
   const bool fast = aligned && g.M % GB_M == 0 && g.N % GB_N == 0 && g.K % GB_K == 0;
   const dim3 grid((unsigned)(tiles_m * tiles_n)), blk(G_THREADS);
@@ -1028,7 +1030,7 @@ static int gemm16_launch(GemmArgs g, hipStream_t stream, int config = 0) {
   const bool dma_nn = aligned && g.N % 8 == 0 && g.K % 8 == 0 && (GB_M - 1) * g.sa_m + g.K <= 0x3fffffffLL &&
                       (g.K - 1) * g.sb_k + GB_N <= 0x3fffffffLL && g.K >= 3 * 32;
   // ... or with b k-contiguous (b^T rows, as a's): any N.
-  const bool dma_bt = g.sa_k == 1 && g.sb_k == 1 && (uintptr_t)g.a % 16 == 0 && (uintptr_t)g.b % 16 == 0 &&
+  const bool dma_bt = g.sa_k == 1 && g.sb_k == 1 && g.sa_m >= 0 && (uintptr_t)g.a % 16 == 0 && (uintptr_t)g.b % 16 == 0 &&
                       (g.sa_m * 2) % 16 == 0 && (g.sb_n * 2) % 16 == 0 && g.sb_n > 0 && g.K % 8 == 0 &&
                       (GB_M - 1) * g.sa_m + g.K <= 0x3fffffffLL && (GB_N - 1) * g.sb_n + g.K <= 0x3fffffffLL &&
                       g.K >= 3 * 32 && !dma_nn;

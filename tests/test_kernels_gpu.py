@@ -401,6 +401,31 @@ def test_gemm_dma_b_transposed(mnk, dtype):
     assert torch.allclose(out.float(), ref.float(), atol=tol, rtol=1e-2)
 
 
+def test_gemm_negative_row_strides():
+    """Rows walked backwards through the C ABI (a and out with negative row strides, as a
+    caller may pass for a flipped view; torch itself makes none): the aligned DMA kernels
+    address panels with unsigned offsets, so such a call takes the any-strides kernel and
+    must still match the product of the flipped matrices."""
+    import ctypes
+
+    from ninetoothed_amd import _lib
+
+    lib = _lib.load()
+    m, n, k = 512, 512, 512
+    a = _randn((m, k), torch.float16, 80, 0.1)
+    b = _randn((k, n), torch.float16, 81, 0.1)
+    out = torch.zeros(m, n, dtype=torch.float16, device=DEV)
+    es = a.element_size()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    code = lib.nt_gemm_f16(a.data_ptr() + (m - 1) * k * es, -k, 1, b.data_ptr(), n, 1, None, 0, 0,
+                           out.data_ptr() + (m - 1) * n * es, -n, 1, _lib.dtype_code(torch.float16), m, n, k, 1.0, 0.0,
+                           _lib.dtype_code(torch.float16), stream)
+    torch.cuda.synchronize()
+    assert code == 0
+    ref = (a.float() @ b.float())  # row i of the flipped a times b lands in row i of the flipped out
+    assert torch.allclose(out.float(), ref, atol=1e-2, rtol=1e-2), (out.float() - ref).abs().max()
+
+
 @pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
 def test_gemm_dma_b_transposed_reads_nothing_past_k(dtype):
     # b^T rows are a view of a wider buffer holding inf past K: those values must not
