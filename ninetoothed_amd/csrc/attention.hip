@@ -1229,8 +1229,9 @@ static int attention_launch(const void* q, const int64_t* qs, const void* k, con
   constexpr int NW = 8;  // waves of 32 queries per workgroup of the fast kernel
   // The fast kernel also takes a head dim below its 64 or 128 (a multiple of 8, padded with
   // zeros): 16-byte row vectors need only unit d-stride and aligned rows.
-  auto rows_ok = [&]() {
-    return ks[3] == 1 && vs[3] == 1 && qs[3] == 1 && D % 8 == 0 && (ks[2] * 2) % 16 == 0 && (vs[2] * 2) % 16 == 0 &&
+  auto rows_ok = [&]() {  // (row strides non-negative: a head's keys are addressed with unsigned buffer offsets)
+    return ks[3] == 1 && vs[3] == 1 && qs[3] == 1 && D % 8 == 0 && ks[2] >= 0 && vs[2] >= 0 && qs[2] >= 0 &&
+           (ks[2] * 2) % 16 == 0 && (vs[2] * 2) % 16 == 0 &&
            (qs[2] * 2) % 16 == 0 && (ks[1] * 2) % 16 == 0 && (vs[1] * 2) % 16 == 0 && (qs[1] * 2) % 16 == 0 &&
            (ks[0] * 2) % 16 == 0 && (vs[0] * 2) % 16 == 0 && (qs[0] * 2) % 16 == 0 && (uintptr_t)k % 16 == 0 &&
            (uintptr_t)v % 16 == 0 && (uintptr_t)q % 16 == 0;

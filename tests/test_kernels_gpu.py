@@ -748,6 +748,36 @@ def test_attention_padded_head_dims(d, causal, dtype):
     assert torch.all(obuf[..., d:] == 7.0)
 
 
+def test_attention_negative_row_strides():
+    """Keys, values and queries walked backwards through the C ABI (negative row strides, as
+    a caller may pass for a flipped view; torch itself makes none).  The fast kernels address
+    a head's keys with unsigned buffer offsets, so such a call takes the four-wave kernels and
+    must match attention over the flipped tensors."""
+    import ctypes
+
+    from ninetoothed_amd import _lib
+
+    lib = _lib.load()
+    b_, h_, s_, d_ = 1, 2, 256, 64
+    q, k, v = (_randn((b_, h_, s_, d_), torch.float16, 90 + i) for i in range(3))
+    o = torch.zeros_like(q)
+    es = q.element_size()
+
+    def flipped(t):  # pointer to row s-1 of head 0, row stride -D
+        st = t.stride()
+        return t.data_ptr() + (s_ - 1) * st[2] * es, _lib.int64_array((st[0], st[1], -st[2], st[3]))
+
+    (qp, qs_), (kp, ks_), (vp, vs_), (op, os_) = (flipped(t) for t in (q, k, v, o))
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    code = lib.nt_attention_f16(qp, qs_, kp, ks_, vp, vs_, op, os_, _lib.dtype_code(torch.float16), b_, h_, s_, s_,
+                                d_, 1.4426950408889634 / d_ ** 0.5, 0, stream)
+    torch.cuda.synchronize()
+    assert code == 0
+    # every row reversed in q, k, v and o: the softmax over keys is order-free, so o = attn(q, k, v)
+    ref = F.scaled_dot_product_attention(q.float().cpu(), k.float().cpu(), v.float().cpu())
+    assert torch.allclose(o.float().cpu(), ref, atol=1e-2, rtol=1e-2), (o.float().cpu() - ref).abs().max()
+
+
 @pytest.mark.parametrize("dtype", (torch.float16, torch.float32))
 def test_attention_empty_keys(dtype):
     """No keys: every output is zero, as F.scaled_dot_product_attention gives (the empty key
