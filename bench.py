@@ -5,7 +5,8 @@ Handle) on inputs already resident in HBM.  The headline line is configs[1]: fp1
 addmm out = 0.5*C + 1.0*(A@B), M=N=K=4096.  The same JSON line carries every other
 configuration under "configs", each with its own roofline fraction and CPU baseline.
 
-Per configuration: max(W, 10) untimed warm-up steps; then exactly K steps bracketed by
+Per configuration: W untimed warm-up steps (--warmup, default 10; the first one also binds
+the Handle to its kernel); then exactly K steps bracketed by
 torch.cuda.synchronize(), timed with HIP events recorded on the stream the kernels are
 launched on (torch's current stream, which the launchers pass to the library) ->
 ``ms_per_step`` and ``value``; then max(K, S) further steps (S = --samples, default 50), each between its own pair
@@ -48,7 +49,7 @@ def _args():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--only", default="")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--samples", type=int, default=50,
@@ -408,7 +409,7 @@ def main():
     configs = _configs(torch, ninetoothed, pg)
     only = set(filter(None, args.only.split(",")))
     traffic = _traffic()
-    warmup, samples = max(args.warmup, 10), max(args.steps, args.samples)
+    warmup, samples = args.warmup, max(args.steps, args.samples)
     results = []
     for cfg in configs:
         if (only and cfg["name"] not in only) or (not only and cfg.get("extra")):

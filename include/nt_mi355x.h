@@ -69,7 +69,7 @@ int nt_add_bf16(const void* lhs, int64_t lhs_stride, const void* rhs, int64_t rh
  * full-row softmax.  Math in fp32, result rounded to the element type.
  * Replaces the launcher of `softmax_kernel` (reference tests/test_softmax.py:10-27;
  * row-vector schedule, src/ninetoothed/materializers/triton.py:1299-1314).
- * The column stride must be 1.
+ * Any strides: a column stride other than 1 takes an element-wise kernel.
  * ------------------------------------------------------------------------- */
 int nt_softmax_f32(const void* x, int64_t x_row_stride, int64_t x_col_stride,
                    void* y, int64_t y_row_stride, int64_t y_col_stride,
@@ -85,8 +85,8 @@ int nt_softmax_bf16(const void* x, int64_t x_row_stride, int64_t x_col_stride,
  * nt_softmax_* plus `config` (0 = as nt_softmax_* choose; 1, 2, 3 = the register path
  * with workgroups of four, eight, one wave, when the segment fits it; 4 = the two-sweep
  * kernel; 5 = a group of lanes per segment, up to four 16-byte vectors per lane of one
- * wave).  A forced configuration that does not fit returns NT_ERR_INVALID before
- * launching.  Replaces the reference's tuning over num_warps 4, 8, 1
+ * wave; 6 = the element-wise kernel for any strides).  A forced configuration that does
+ * not fit returns NT_ERR_INVALID before launching.  Replaces the reference's tuning over num_warps 4, 8, 1
  * (reference src/ninetoothed/backends/triton.py:151-155). */
 int nt_softmax_config_f32(const void* x, int64_t x_row_stride, int64_t x_col_stride,
                           void* y, int64_t y_row_stride, int64_t y_col_stride,
@@ -97,6 +97,16 @@ int nt_softmax_config_f16(const void* x, int64_t x_row_stride, int64_t x_col_str
 int nt_softmax_config_bf16(const void* x, int64_t x_row_stride, int64_t x_col_stride,
                            void* y, int64_t y_row_stride, int64_t y_col_stride,
                            int64_t rows, int64_t cols, int64_t block, hipStream_t stream, int config);
+
+/* Softmax with input and output of any two element types (x_dtype, y_dtype: NT_DTYPE_F32,
+ * F16 or BF16): the reference's kernel takes strides as arguments and its store casts the
+ * fp32 quotient to the output's type (reference tests/test_softmax.py:13-21,
+ * src/ninetoothed/frontend/types.py:319-324), so an fp16 input with an fp32 output is a
+ * valid program.  Equal types behave as nt_softmax_*; others take the element-wise
+ * kernel (any strides).  Other arguments as nt_softmax_*. */
+int nt_softmax_cast(const void* x, int x_dtype, int64_t x_row_stride, int64_t x_col_stride,
+                    void* y, int y_dtype, int64_t y_row_stride, int64_t y_col_stride,
+                    int64_t rows, int64_t cols, int64_t block, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * 2-D max pooling on an N-C-H-W indexed input:
@@ -144,6 +154,16 @@ int nt_max_pool2d_config_bf16(const void* x, const int64_t* x_strides, void* y, 
                               int64_t N, int64_t C, int64_t H, int64_t W, int64_t P, int64_t Q,
                               int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
                               int64_t dh, int64_t dw, hipStream_t stream, int config);
+
+/* max_pool2d with input and output of any two element types (x_dtype, y_dtype: NT_DTYPE_F32,
+ * F16 or BF16; the reference's store casts the window max to the output's type,
+ * tests/test_max_pool2d.py:33-36): equal types behave as nt_max_pool2d_*, others take the
+ * element-wise kernel.  Still bit-exact: the max of the widened inputs, rounded once,
+ * equals the rounded max.  Other arguments as nt_max_pool2d_*. */
+int nt_max_pool2d_cast(const void* x, int x_dtype, const int64_t* x_strides, void* y, int y_dtype,
+                       const int64_t* y_strides, int64_t N, int64_t C, int64_t H, int64_t W, int64_t P,
+                       int64_t Q, int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
+                       int64_t dh, int64_t dw, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * GEMM with the addmm epilogue, fp32 accumulation:

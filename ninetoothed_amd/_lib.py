@@ -47,6 +47,8 @@ _SIGNATURES = {
         f"nt_softmax_config_{t}": (_P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _I)
         for t in ("f32", "f16", "bf16")
     },
+    "nt_softmax_cast": (_P, _I, _I64, _I64, _P, _I, _I64, _I64, _I64, _I64, _I64, _P),
+    "nt_max_pool2d_cast": (_P, _I, _I64P, _P, _I, _I64P) + (_I64,) * 14 + (_P,),
     **{
         f"nt_max_pool2d_{t}": (_P, _I64P, _P, _I64P) + (_I64,) * 14 + (_P,)
         for t in ("f32", "f16", "bf16")

@@ -15,14 +15,18 @@ How it is organised here:
   16-byte aligned (kernels with vector loads accept only aligned operands, so an aligned
   and a misaligned call of one shape are different tuning problems); other values by
   their ``repr``.
-* **Timing book** (``TimingBook``): one JSON file per (namespace, candidate keys) under
-  ``$NINETOOTHED_AMD_CACHE_DIR/tuning`` (default ``~/.cache/ninetoothed_amd``), holding
-  ``{signature: {candidate label: milliseconds or "error: ..."}}``.  Entries are merged
-  into the file under a process-wide lock and written atomically, so several tuners and
-  processes share what was measured and a new process re-times nothing it finds there.
-* **Election**: the first call with a new signature fills in the missing entries of its
-  row by benchmarking those candidates, takes the smallest time, runs the winner, and
-  remembers it in memory only once that run returned (a winner that raises is not kept).
+* **Timing book** (``TimingBook``): one JSON file per (namespace, candidate keys, kernel
+  library build) under ``$NINETOOTHED_AMD_CACHE_DIR/tuning`` (default
+  ``~/.cache/ninetoothed_amd``), holding ``{signature: {candidate label: milliseconds or
+  "error: ..."}}``.  The build is a digest of ``libnt_mi355x.so``, so timings of one
+  build never choose among another build's kernels.  Entries are merged into the file
+  under a process-wide lock and written atomically, so several tuners and processes
+  share what was measured and a new process re-times no candidate it finds timed there.
+* **Election**: the first call with a new signature benchmarks every candidate of its row
+  that has no finite time yet (a recorded failure counts as none, as the reference's
+  infinite timing does, so a transient failure or a fixed bug is retried), takes the
+  smallest time, runs the winner, and remembers it in memory only once that run returned
+  (a winner that raises is not kept).
 
 Handles use it when ``make``/``jit`` get ``max_num_configs`` > 1: the candidates are the
 kernel plans (and kernel configurations) that fit the call; programs that update a tensor
@@ -64,11 +68,28 @@ def _label(key):
     return key if isinstance(key, str) else json.dumps(key, sort_keys=True, default=str)
 
 
+_BUILD = None
+
+
+def library_build():
+    """Digest of the kernel library this process loads ("none" when it is not built)."""
+    global _BUILD
+    if _BUILD is None:
+        from ninetoothed_amd import _lib
+
+        try:
+            _BUILD = hashlib.sha256(Path(_lib.LIBRARY_PATH).read_bytes()).hexdigest()[:16]
+        except OSError:
+            _BUILD = "none"
+    return _BUILD
+
+
 class TimingBook:
     """Measured times per call signature and candidate label, persisted as one JSON file."""
 
     def __init__(self, namespace, labels):
-        ident = json.dumps({"namespace": namespace, "labels": list(labels)}, sort_keys=True)
+        ident = json.dumps({"namespace": namespace, "labels": list(labels), "build": library_build()},
+                           sort_keys=True)
         digest = hashlib.sha256(ident.encode()).hexdigest()[:20]
         self.path = cache_dir() / "tuning" / f"{digest}.json"
         self.rows = {}
@@ -148,8 +169,8 @@ class AutoTuner:
         row = self.book.row(sig)
         fresh = {}
         for func, label in zip(self.candidates, self.labels):
-            if label in row:
-                continue
+            if not math.isinf(_time_of(row.get(label))):
+                continue  # timed before; a failure (or no entry) is timed again
             try:
                 fresh[label] = float(self._measure(func, args, kwargs))
             except Exception as exc:  # noqa: BLE001  (a failing candidate is recorded, not raised)

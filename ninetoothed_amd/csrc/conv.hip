@@ -637,6 +637,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // each position's own offset (they may run across rows), stored element by element.
   int64_t ybase = 0;
   int64_t yoff[8];
+  uint32_t yvalid = 0;  // bit u: position mpos + u < M (an offset may be negative for flipped views)
   if (m_ok) {
     const int q = mpos % (int)g.Q, t = mpos / (int)g.Q;
     const int p = t % (int)g.P, n = t / (int)g.P;
@@ -647,7 +648,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int u = 0; u < 8; ++u) {
       const int64_t m = mpos + u;
       const int64_t q = m % g.Q, t = m / g.Q;
-      yoff[u] = m < g.M ? (t / g.P) * g.ys[0] + (t % g.P) * g.ys[2] + q * g.ys[3] : -1;
+      yoff[u] = (t / g.P) * g.ys[0] + (t % g.P) * g.ys[2] + q * g.ys[3];
+      yvalid |= (m < g.M ? 1u : 0u) << u;
     }
   }
   uint16_t* Y = (uint16_t*)g.y;
@@ -718,7 +720,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             } else {
 #pragma unroll
               for (int u = 0; u < 8; ++u)
-                if (yoff[u] >= 0) Y[yoff[u] + (int64_t)k * g.ys[1]] = (uint16_t)(ow[u >> 1] >> (16 * (u & 1)));
+                if ((yvalid >> u) & 1u) Y[yoff[u] + (int64_t)k * g.ys[1]] = (uint16_t)(ow[u >> 1] >> (16 * (u & 1)));
             }
           }
         }

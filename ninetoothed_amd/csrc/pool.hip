@@ -24,9 +24,12 @@ struct PoolShape {
   int64_t xs[4], ys[4];
 };
 
-template <typename T>
+// One lane per output, any strides; the output may be of another element type than the
+// input (the reference's store casts): the max of widened values, rounded once on store,
+// equals the rounded max, since rounding is monotone.
+template <typename T, typename To = T>
 __global__ __launch_bounds__(256) void pool_generic_kernel(const typename elem<T>::storage* __restrict__ x,
-                                                           typename elem<T>::storage* __restrict__ y, PoolShape s) {
+                                                           typename elem<To>::storage* __restrict__ y, PoolShape s) {
   const int64_t total = s.N * s.C * s.P * s.Q;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; o < total; o += stride) {
@@ -45,7 +48,7 @@ __global__ __launch_bounds__(256) void pool_generic_kernel(const typename elem<T
         m = fmaxf(m, elem<T>::to_float(xb[h * s.xs[2] + w * s.xs[3]]));
       }
     }
-    y[n * s.ys[0] + c * s.ys[1] + p * s.ys[2] + q * s.ys[3]] = elem<T>::from_float(m);
+    y[n * s.ys[0] + c * s.ys[1] + p * s.ys[2] + q * s.ys[3]] = elem<To>::from_float(m);
   }
 }
 
@@ -461,7 +464,46 @@ static int pool_launch(const void* x, const int64_t* xs, void* y, const int64_t*
   return launch_status();
 }
 
+// Input and output of any two element types: same types take pool_launch's kernels, others
+// the element-wise kernel.
+template <typename T>
+static int pool_cast_to(const void* x, const int64_t* xs, void* y, int y_dtype, const int64_t* ys, int64_t N,
+                        int64_t C, int64_t H, int64_t W, int64_t P, int64_t Q, int64_t kh, int64_t kw, int64_t sh,
+                        int64_t sw, int64_t ph, int64_t pw, int64_t dh, int64_t dw, hipStream_t stream) {
+  if (y_dtype == elem<T>::code)
+    return pool_launch<T>(x, xs, y, ys, N, C, H, W, P, Q, kh, kw, sh, sw, ph, pw, dh, dw, stream);
+  if (!valid_dtype(y_dtype)) return NT_ERR_INVALID;
+  if (N < 0 || C < 0 || H < 0 || W < 0 || P < 0 || Q < 0 || kh <= 0 || kw <= 0 || sh <= 0 || sw <= 0 || dh <= 0 ||
+      dw <= 0 || ph < 0 || pw < 0)
+    return NT_ERR_INVALID;
+  if (N * C * P * Q == 0) return 0;
+  if (!x || !y || !xs || !ys) return NT_ERR_INVALID;
+  PoolShape s{N, C, H, W, P, Q, kh, kw, sh, sw, ph, pw, dh, dw, {xs[0], xs[1], xs[2], xs[3]}, {ys[0], ys[1], ys[2], ys[3]}};
+  const dim3 grid((unsigned)std::min<int64_t>(cdiv(N * C * P * Q, 256), 256 * 32));
+  typedef typename elem<T>::storage S;
+  if (y_dtype == NT_DTYPE_F32)
+    hipLaunchKernelGGL((pool_generic_kernel<T, float>), grid, dim3(256), 0, stream, (const S*)x, (float*)y, s);
+  else if (y_dtype == NT_DTYPE_F16)
+    hipLaunchKernelGGL((pool_generic_kernel<T, f16_t>), grid, dim3(256), 0, stream, (const S*)x, (uint16_t*)y, s);
+  else
+    hipLaunchKernelGGL((pool_generic_kernel<T, bf16_t>), grid, dim3(256), 0, stream, (const S*)x, (uint16_t*)y, s);
+  return launch_status();
+}
+
 }  // namespace nt
+
+extern "C" int nt_max_pool2d_cast(const void* x, int x_dtype, const int64_t* xs, void* y, int y_dtype,
+                                  const int64_t* ys, int64_t N, int64_t C, int64_t H, int64_t W, int64_t P, int64_t Q,
+                                  int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw, int64_t dh,
+                                  int64_t dw, hipStream_t stream) {
+  if (x_dtype == NT_DTYPE_F32)
+    return nt::pool_cast_to<float>(x, xs, y, y_dtype, ys, N, C, H, W, P, Q, kh, kw, sh, sw, ph, pw, dh, dw, stream);
+  if (x_dtype == NT_DTYPE_F16)
+    return nt::pool_cast_to<nt::f16_t>(x, xs, y, y_dtype, ys, N, C, H, W, P, Q, kh, kw, sh, sw, ph, pw, dh, dw, stream);
+  if (x_dtype == NT_DTYPE_BF16)
+    return nt::pool_cast_to<nt::bf16_t>(x, xs, y, y_dtype, ys, N, C, H, W, P, Q, kh, kw, sh, sw, ph, pw, dh, dw, stream);
+  return NT_ERR_INVALID;
+}
 
 #define NT_POOL_ENTRY(NAME, T)                                                                                      \
   extern "C" int NAME(const void* x, const int64_t* xs, void* y, const int64_t* ys, int64_t N, int64_t C, int64_t H, \

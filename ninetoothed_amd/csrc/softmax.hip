@@ -118,7 +118,8 @@ __device__ __forceinline__ int seg_head(const S* xr, int64_t len) {
 }
 
 // Short segments: a group of LPR lanes (a power of two, at most a wave) per segment, each
-// lane holding VPT vectors of V elements (and a head element), so a 256-lane workgroup
+// lane holding VPT vectors of V elements (and up to HN head elements: the head has at most
+// V - 1 elements, strided over the group's lanes), so a 256-lane workgroup
 // takes 256 / LPR segments (one per 16 lanes for 128 fp16 columns) instead of leaving most
 // of its lanes idle.  The reductions are butterflies inside the group.
 template <int LPR>
@@ -152,9 +153,16 @@ __global__ __launch_bounds__(SM_THREADS) void softmax_rows_kernel(const typename
   const S* xb = xr + head;
   S* yb = yr + head;
   const int64_t blen = len - head;
-  const float hv = gl < head ? elem<T>::to_float(xr[gl]) : -INFINITY;
+  constexpr int HN = (V - 1 + LPR - 1) / LPR;  // head elements gl, gl + LPR, ... per lane
+  float hv[HN];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < HN; ++i) {
+    const int e = gl + i * LPR;
+    hv[i] = e < head ? elem<T>::to_float(xr[e]) : -INFINITY;
+    mx = fmaxf(mx, hv[i]);
+  }
   float v[VPT][V];
-  float mx = hv;
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
     const int64_t e0 = ((int64_t)j * LPR + gl) * V;
@@ -171,8 +179,12 @@ __global__ __launch_bounds__(SM_THREADS) void softmax_rows_kernel(const typename
     for (int u = 0; u < V; ++u) mx = fmaxf(mx, v[j][u]);
   }
   mx = group_max<LPR>(mx);
-  const float he = fast_exp(hv - mx);
-  float sum = gl < head ? he : 0.f;
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < HN; ++i) {
+    hv[i] = fast_exp(hv[i] - mx);
+    if (gl + i * LPR < head) sum += hv[i];
+  }
 #pragma unroll
   for (int j = 0; j < VPT; ++j)
 #pragma unroll
@@ -181,7 +193,9 @@ __global__ __launch_bounds__(SM_THREADS) void softmax_rows_kernel(const typename
       sum += v[j][u];
     }
   const float inv = 1.0f / group_sum<LPR>(sum);
-  if (gl < head) yr[gl] = elem<T>::from_float(he * inv);
+#pragma unroll
+  for (int i = 0; i < HN; ++i)
+    if (gl + i * LPR < head) yr[gl + i * LPR] = elem<T>::from_float(hv[i] * inv);
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
     const int64_t e0 = ((int64_t)j * LPR + gl) * V;
@@ -283,11 +297,76 @@ __global__ __launch_bounds__(NT) void softmax_long_kernel(const typename elem<T>
   }
 }
 
+// Any strides and any pair of element types (the reference passes strides to its kernel and
+// its store casts to the output's type): one 256-lane workgroup per segment, element-wise
+// loads at the column stride, U elements per lane in flight, an online (max, sum) sweep,
+// then a sweep that recomputes exp(x - max) / sum and stores it in the output's type.
+template <typename Ti, typename To>
+__global__ __launch_bounds__(SM_THREADS) void softmax_any_kernel(const typename elem<Ti>::storage* __restrict__ x,
+                                                                 int64_t xs, int64_t xcs,
+                                                                 typename elem<To>::storage* __restrict__ y,
+                                                                 int64_t ys, int64_t ycs, int64_t cols, int64_t block,
+                                                                 int64_t segs_per_row) {
+  constexpr int U = 8;
+  constexpr int64_t STEP = (int64_t)SM_THREADS * U;
+  __shared__ float red[SM_THREADS / 64];
+  const int64_t seg = blockIdx.x;
+  const int64_t row = seg / segs_per_row;
+  const int64_t c0 = (seg % segs_per_row) * block;
+  const int64_t len = (cols - c0 < block) ? (cols - c0) : block;
+  const typename elem<Ti>::storage* xr = x + row * xs + c0 * xcs;
+  typename elem<To>::storage* yr = y + row * ys + c0 * ycs;
+  float m = -INFINITY, s = 0.f;
+  for (int64_t base = 0; base < len; base += STEP) {
+    float v[U];
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      const int64_t e = base + (int64_t)j * SM_THREADS + threadIdx.x;
+      v[j] = e < len ? elem<Ti>::to_float(xr[e * xcs]) : -INFINITY;
+    }
+    float vm = v[0];
+#pragma unroll
+    for (int j = 1; j < U; ++j) vm = fmaxf(vm, v[j]);
+    if (vm != -INFINITY) {
+      const float nm = fmaxf(m, vm);
+      s = (m == -INFINITY) ? 0.f : s * fast_exp(m - nm);
+      m = nm;
+#pragma unroll
+      for (int j = 0; j < U; ++j) s += fast_exp(v[j] - m);
+    }
+  }
+  const float gm = block_max<SM_THREADS / 64>(m, red);
+  const float part = (m == -INFINITY) ? 0.f : s * fast_exp(m - gm);
+  const float inv = 1.0f / block_sum<SM_THREADS / 64>(part, red);
+  for (int64_t base = 0; base < len; base += STEP) {
+    float v[U];
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      const int64_t e = base + (int64_t)j * SM_THREADS + threadIdx.x;
+      v[j] = e < len ? elem<Ti>::to_float(xr[e * xcs]) : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      const int64_t e = base + (int64_t)j * SM_THREADS + threadIdx.x;
+      if (e < len) yr[e * ycs] = elem<To>::from_float(fast_exp(v[j] - gm) * inv);
+    }
+  }
+}
+
+template <typename Ti, typename To>
+static void softmax_any_launch(const void* x, int64_t xs, int64_t xcs, void* y, int64_t ys, int64_t ycs, int64_t cols,
+                               int64_t block, int64_t segs_per_row, int64_t segs, hipStream_t stream) {
+  hipLaunchKernelGGL((softmax_any_kernel<Ti, To>), dim3((unsigned)segs), dim3(SM_THREADS), 0, stream,
+                     (const typename elem<Ti>::storage*)x, xs, xcs, (typename elem<To>::storage*)y, ys, ycs, cols,
+                     block, segs_per_row);
+}
+
 // config: 0 = the lane-group kernel for segments of at most 4 vectors per lane of a wave,
 // else the four-wave register path when the segment fits it (16 vectors of 16 bytes per
 // lane at most), else the two-sweep kernel; 1 = four-wave register path; 2 = eight-wave
 // register path; 3 = one-wave register path; 4 = two-sweep kernel; 5 = lane-group kernel
-// (the reference's auto-tuner times num_warps 4, 8, 1:
+// 6 = the any-strides kernel (the only one for a column stride other than 1, so config 0
+// takes it then) (the reference's auto-tuner times num_warps 4, 8, 1:
 // src/ninetoothed/backends/triton.py:151-155).  A forced kernel whose conditions do not
 // hold returns NT_ERR_INVALID unlaunched.
 template <typename T>
@@ -295,14 +374,19 @@ static int softmax_launch(const void* x, int64_t xs, int64_t xcs, void* y, int64
                           int64_t cols, int64_t block, hipStream_t stream, int config = 0) {
   typedef typename elem<T>::storage S;
   constexpr int V = 16 / sizeof(S);
-  if (config < 0 || config > 5) return NT_ERR_INVALID;
+  if (config < 0 || config > 6) return NT_ERR_INVALID;
   if (rows < 0 || cols < 0 || block <= 0) return NT_ERR_INVALID;
   if (rows == 0 || cols == 0) return 0;
   if (!x || !y) return NT_ERR_INVALID;
-  if (cols > 1 && (xcs != 1 || ycs != 1)) return NT_ERR_INVALID;
   const int64_t segs_per_row = cdiv(cols, block);
   const int64_t segs = rows * segs_per_row;
   if (segs > 0x7fffffffLL) return NT_ERR_INVALID;
+  const bool unit = cols <= 1 || (xcs == 1 && ycs == 1);
+  if (config == 6 || (config == 0 && !unit)) {
+    softmax_any_launch<T, T>(x, xs, xcs, y, ys, ycs, cols, block, segs_per_row, segs, stream);
+    return launch_status();
+  }
+  if (!unit) return NT_ERR_INVALID;
   const int64_t len = block < cols ? block : cols;
   const bool vec = ((uintptr_t)x % 16 == 0) && ((uintptr_t)y % 16 == 0) && ((xs * (int64_t)sizeof(S)) % 16 == 0 || rows == 1) &&
                    ((ys * (int64_t)sizeof(S)) % 16 == 0 || rows == 1) &&
@@ -392,7 +476,38 @@ static int softmax_launch(const void* x, int64_t xs, int64_t xcs, void* y, int64
   return launch_status();
 }
 
+// Input and output of any two element types: same types take softmax_launch's kernels,
+// others the any-strides kernel.
+template <typename Ti>
+static int softmax_cast_to(const void* x, int64_t xs, int64_t xcs, void* y, int y_dtype, int64_t ys, int64_t ycs,
+                           int64_t rows, int64_t cols, int64_t block, hipStream_t stream) {
+  if (y_dtype == elem<Ti>::code) return softmax_launch<Ti>(x, xs, xcs, y, ys, ycs, rows, cols, block, stream);
+  if (!valid_dtype(y_dtype) || rows < 0 || cols < 0 || block <= 0) return NT_ERR_INVALID;
+  if (rows == 0 || cols == 0) return 0;
+  if (!x || !y) return NT_ERR_INVALID;
+  const int64_t segs_per_row = cdiv(cols, block);
+  const int64_t segs = rows * segs_per_row;
+  if (segs > 0x7fffffffLL) return NT_ERR_INVALID;
+  if (y_dtype == NT_DTYPE_F32)
+    softmax_any_launch<Ti, float>(x, xs, xcs, y, ys, ycs, cols, block, segs_per_row, segs, stream);
+  else if (y_dtype == NT_DTYPE_F16)
+    softmax_any_launch<Ti, f16_t>(x, xs, xcs, y, ys, ycs, cols, block, segs_per_row, segs, stream);
+  else
+    softmax_any_launch<Ti, bf16_t>(x, xs, xcs, y, ys, ycs, cols, block, segs_per_row, segs, stream);
+  return launch_status();
+}
+
 }  // namespace nt
+
+extern "C" int nt_softmax_cast(const void* x, int x_dtype, int64_t xs, int64_t xcs, void* y, int y_dtype, int64_t ys,
+                               int64_t ycs, int64_t rows, int64_t cols, int64_t block, hipStream_t stream) {
+  if (x_dtype == NT_DTYPE_F32) return nt::softmax_cast_to<float>(x, xs, xcs, y, y_dtype, ys, ycs, rows, cols, block, stream);
+  if (x_dtype == NT_DTYPE_F16)
+    return nt::softmax_cast_to<nt::f16_t>(x, xs, xcs, y, y_dtype, ys, ycs, rows, cols, block, stream);
+  if (x_dtype == NT_DTYPE_BF16)
+    return nt::softmax_cast_to<nt::bf16_t>(x, xs, xcs, y, y_dtype, ys, ycs, rows, cols, block, stream);
+  return NT_ERR_INVALID;
+}
 
 extern "C" int nt_softmax_f32(const void* x, int64_t xs, int64_t xcs, void* y, int64_t ys, int64_t ycs, int64_t rows,
                               int64_t cols, int64_t block, hipStream_t stream) {

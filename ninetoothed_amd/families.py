@@ -208,6 +208,11 @@ class Plan:
     def bind(self, values, index):
         raise NotImplementedError
 
+    def check(self, values):
+        """Raise ``TypeError`` / ``ValueError`` where the family's kernel would reject the
+        call's dtypes or sizes (the check ``bind`` runs first), touching no device, so that
+        ``select`` can hand such a call to the next family instead."""
+
     def run(self, values):
         names = tuple(values)
         self.bind(values, {n: i for i, n in enumerate(names)})(tuple(values[n] for n in names))
@@ -297,6 +302,12 @@ class GemmPlan(Plan):
 
         return coef
 
+    def check(self, values):
+        from ninetoothed_amd import kernels
+
+        kernels.check_gemm(values[self.a], values[self.b], values[self.out], values[self.c] if self.c else None,
+                           self.round_dtype, self.config)
+
     def bind(self, values, index):
         from ninetoothed_amd import kernels
 
@@ -331,6 +342,11 @@ class ConvPlan(Plan):
 
     def with_config(self, config):
         return ConvPlan(self.x, self.w, self.y, self.padding, self.stride, self.dilation, self.round_dtype, config)
+
+    def check(self, values):
+        from ninetoothed_amd import kernels
+
+        kernels.check_conv2d(values[self.x], values[self.w], values[self.y], self.round_dtype, self.config)
 
     def bind(self, values, index):
         import torch
@@ -673,6 +689,11 @@ class AttentionPlan(Plan):
     def with_config(self, config):
         return AttentionPlan(self.q, self.k, self.v, self.o, self.scale, self.causal, config)
 
+    def check(self, values):
+        from ninetoothed_amd import kernels
+
+        kernels.check_attention(values[self.q], values[self.k], values[self.v], values[self.o], self.config)
+
     def bind(self, values, index):
         import torch
 
@@ -760,6 +781,11 @@ class SoftmaxPlan(Plan):
     def with_config(self, config):
         return SoftmaxPlan(self.x, self.y, self.block, config)
 
+    def check(self, values):
+        from ninetoothed_amd import kernels
+
+        kernels.check_softmax(values[self.x], values[self.y], self.config)
+
     def bind(self, values, index):
         from ninetoothed_amd import kernels
 
@@ -829,6 +855,11 @@ class MaxPoolPlan(Plan):
 
     def with_config(self, config):
         return MaxPoolPlan(self.x, self.y, self.window, self.stride, self.padding, self.dilation, config)
+
+    def check(self, values):
+        from ninetoothed_amd import kernels
+
+        kernels.check_max_pool2d(values[self.x], values[self.y], self.config)
 
     def bind(self, values, index):
         from ninetoothed_amd import kernels
@@ -929,6 +960,12 @@ class AddPlan(Plan):
     def __init__(self, a, b, out):
         self.a, self.b, self.out = a, b, out
 
+    def check(self, values):
+        from ninetoothed_amd import kernels
+
+        a, b, o = values[self.a], values[self.b], values[self.out]
+        kernels.check_add(a.reshape(-1), b.reshape(-1), o.reshape(-1))
+
     def bind(self, values, index):
         from ninetoothed_amd import kernels
 
@@ -1007,7 +1044,9 @@ def candidates(ctx):
     for matcher in FAMILIES:
         try:
             plan = matcher(ctx)
-        except LoweringError:
+            if plan is not None:
+                plan.check(ctx.values)
+        except (LoweringError, TypeError, ValueError):
             plan = None
         if isinstance(plan, GemmPlan) and not plan.config:
             plans.extend(plan.with_config(cfg) for cfg in kernels.GEMM_CONFIGS)
@@ -1021,11 +1060,20 @@ def candidates(ctx):
             plans.extend(plan.with_config(cfg) for cfg in kernels.POOL_CONFIGS)
         elif plan is not None:
             plans.append(plan)
+    plans = [p for p in plans if _admits(p, ctx.values)]
     # a generic tile program that runs real loops is the fallback for programs no hand-written
     # kernel fits; beside one it is no candidate (timing it would only slow the tuning down)
     if any(p.family != "generic" for p in plans):
         plans = [p for p in plans if getattr(p, "nest", None) is None]
     return plans
+
+
+def _admits(plan, values):
+    try:
+        plan.check(values)
+    except (TypeError, ValueError):
+        return False
+    return True
 
 
 def updates_an_input(program):
@@ -1084,15 +1132,18 @@ class TunedPlan(Plan):
 def select(ctx):
     """Return the Plan of the first family whose pattern and geometry fit.
 
-    A family whose pattern matches but whose geometry does not raises ``LoweringError``;
-    the next families are still tried (an elementwise program the add kernel cannot
-    take runs on the generic kernels) and the reasons are reported if none fits."""
+    A family whose pattern matches but whose geometry does not raises ``LoweringError``,
+    and a plan whose kernel would reject the call's dtypes or sizes (``Plan.check``) is
+    declined too; the next families are still tried (an elementwise program the add kernel
+    cannot take runs on the generic kernels) and the reasons are reported if none fits."""
     tried, reasons = [], []
     for matcher in FAMILIES:
         name = matcher.__name__[len("match_"):]
         try:
             plan = matcher(ctx)
-        except LoweringError as exc:
+            if plan is not None:
+                plan.check(ctx.values)  # a call the family's kernel would reject goes on
+        except (LoweringError, TypeError, ValueError) as exc:
             reasons.append(f"{name}: {exc}")
             plan = None
         if plan is not None:

@@ -449,6 +449,9 @@ class GenericPlan:
     _functions = {}  # source digest -> loaded kernel handle
     _blobs = {}  # source digest -> code object (compiled here, or carried by a built artifact)
 
+    def check(self, values):
+        """The generic kernels take every dtype and size their emitter accepted."""
+
     def __init__(self, ctx, stores, values):
         self.ctx = ctx
         self.stores = stores

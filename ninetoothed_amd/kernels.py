@@ -45,8 +45,16 @@ def _stream_of(device):
     return lambda: raw(index)
 
 
-def _entry(prefix, dtype):
-    fn = getattr(_lib.load(), f"{prefix}_{_lib.dtype_suffix(dtype)}")
+def _entry_name(prefix, dtype):
+    """The entry point ``<prefix>_<dtype>``; ``TypeError`` when the library has none for ``dtype``."""
+    name = f"{prefix}_{_lib.dtype_suffix(dtype)}"
+    if name not in _lib.exported_symbols():
+        raise TypeError(f"no {prefix} kernel takes {dtype} operands")
+    return name
+
+
+def _entry(name):
+    fn = getattr(_lib.load(), name)
     return fn, fn.__name__
 
 
@@ -55,9 +63,11 @@ def _raise(code, name):
 
 
 # ------------------------------------------------------------------------- add
-def bind_add(lhs, rhs, out):
-    """launch(lhs, rhs, out): out = lhs + rhs over 1-D tensors of equal length (any strides)."""
-    device = _check_device(lhs, rhs, out)
+# Each ``check_<op>`` validates what the kernels assume about dtypes, ranks and sizes
+# without touching a device or the library (``TypeError`` / ``ValueError``), so a family
+# matcher can decline a call its kernel would reject (``families.select``); ``bind_<op>``
+# runs the same check before it binds.
+def check_add(lhs, rhs, out):
     if not (lhs.dim() == rhs.dim() == out.dim() == 1):
         raise ValueError("add expects 1-D tensors")
     n = out.shape[0]
@@ -65,7 +75,15 @@ def bind_add(lhs, rhs, out):
         raise ValueError("add operands differ in length")
     if not (lhs.dtype == rhs.dtype == out.dtype):
         raise TypeError("add operands must share one dtype")
-    fn, name = _entry("nt_add", out.dtype)
+    return _entry_name("nt_add", out.dtype)
+
+
+def bind_add(lhs, rhs, out):
+    """launch(lhs, rhs, out): out = lhs + rhs over 1-D tensors of equal length (any strides)."""
+    entry = check_add(lhs, rhs, out)
+    device = _check_device(lhs, rhs, out)
+    n = out.shape[0]
+    fn, name = _entry(entry)
     sl, sr, so = lhs.stride(0), rhs.stride(0), out.stride(0)
     stream = _stream_of(device)
 
@@ -85,36 +103,58 @@ def add(lhs, rhs, out):
 # --------------------------------------------------------------------- softmax
 # Kernel configurations of the softmax that ``config`` can force (0: the lane-group kernel for
 # segments of at most four 16-byte vectors per lane of a wave, else the four-wave register
-# path where the segment fits, else the two-sweep kernel): the register path with workgroups
-# of four, eight or one wave (the reference's num_warps candidates 4, 8, 1), the two-sweep
-# kernel, the lane-group kernel.
-SOFTMAX_CONFIGS = (1, 2, 3, 4, 5)
+# path where the segment fits, else the two-sweep kernel; the element-wise kernel for a
+# column stride other than 1 or an output of another dtype): the register path with
+# workgroups of four, eight or one wave (the reference's num_warps candidates 4, 8, 1), the
+# two-sweep kernel, the lane-group kernel, the element-wise kernel.
+SOFTMAX_CONFIGS = (1, 2, 3, 4, 5, 6)
+SOFTMAX_ANY = 6  # the configuration that takes any strides and any output dtype
+
+
+def check_softmax(x, y, config=0):
+    if x.dim() != 2 or y.shape != x.shape:
+        raise ValueError("softmax expects matching 2-D tensors")
+    if config and config not in SOFTMAX_CONFIGS:
+        raise TypeError(f"softmax config {config} is not one of {SOFTMAX_CONFIGS}")
+    cols = x.shape[1]
+    unit = cols <= 1 or (x.stride(1) == 1 and y.stride(1) == 1)
+    if config not in (0, SOFTMAX_ANY):
+        if x.dtype != y.dtype:
+            raise TypeError(f"softmax config {config} needs input and output of one dtype")
+        if not unit:
+            raise ValueError(f"softmax config {config} needs unit column strides")
+    if x.dtype != y.dtype:
+        _lib.dtype_code(x.dtype), _lib.dtype_code(y.dtype)  # TypeError for other dtypes
+        return "nt_softmax_cast"
+    return _entry_name("nt_softmax_config" if config else "nt_softmax", x.dtype)
 
 
 def bind_softmax(x, y, block=None, config=0):
     """launch(x, y): row softmax of a 2-D tensor over segments of ``block`` columns (default: whole rows).
 
-    A nonzero ``config`` forces one kernel; a call it does not admit raises
+    Any strides; ``y`` may have another float dtype than ``x`` (the quotient is stored in
+    y's type, as the reference's store casts it).  A nonzero ``config`` forces one kernel:
+    configurations 1-5 need unit column strides and one dtype (``ValueError`` /
+    ``TypeError`` here otherwise); a call a forced kernel does not admit raises
     ``KernelLaunchError`` without launching."""
+    entry = check_softmax(x, y, config)
     device = _check_device(x, y)
-    if x.dim() != 2 or y.shape != x.shape:
-        raise ValueError("softmax expects matching 2-D tensors")
-    if x.dtype != y.dtype:
-        raise TypeError("softmax input and output must share one dtype")
     rows, cols = x.shape
     block = max(cols if block is None else int(block), 1)
-    if cols > 1 and (x.stride(1) != 1 or y.stride(1) != 1):
-        raise ValueError("softmax needs unit column stride")
-    if config:
-        if config not in SOFTMAX_CONFIGS:
-            raise TypeError(f"softmax config {config} is not one of {SOFTMAX_CONFIGS}")
-        fn, name = _entry("nt_softmax_config", x.dtype)
-        extra = (int(config),)
-    else:
-        fn, name = _entry("nt_softmax", x.dtype)
-        extra = ()
     (xr, xc), (yr, yc) = x.stride(), y.stride()
     stream = _stream_of(device)
+    if x.dtype != y.dtype:
+        fn, name = _entry(entry)
+        xcode, ycode = _lib.dtype_code(x.dtype), _lib.dtype_code(y.dtype)
+
+        def launch(x, y):
+            code = fn(x.data_ptr(), xcode, xr, xc, y.data_ptr(), ycode, yr, yc, rows, cols, block, stream())
+            if code:
+                _raise(code, name)
+
+        return launch
+    fn, name = _entry(entry)
+    extra = (int(config),) if config else ()
 
     def launch(x, y):
         code = fn(x.data_ptr(), xr, xc, y.data_ptr(), yr, yc, rows, cols, block, stream(), *extra)
@@ -135,37 +175,55 @@ def softmax(x, y, block=None, config=0):
 # 2 the element-wise kernel, 3 the flat kernel (2-high windows, 8 outputs per unit),
 # 4 the LDS strip kernel (any window whose input rows fit 32 KiB of LDS).
 POOL_CONFIGS = (1, 2, 3, 4)
+POOL_ANY = 2  # the configuration that takes any strides and any output dtype
+
+
+def check_max_pool2d(x, y, config=0):
+    if x.dim() != 4 or y.dim() != 4:
+        raise ValueError("max_pool2d expects 4-D tensors")
+    if config and config not in POOL_CONFIGS:
+        raise TypeError(f"max_pool2d config {config} is not one of {POOL_CONFIGS}")
+    if x.shape[0] != y.shape[0] or x.shape[1] != y.shape[1]:
+        raise ValueError("max_pool2d batch/channel sizes differ")
+    if x.dtype != y.dtype:
+        if config not in (0, POOL_ANY):
+            raise TypeError(f"max_pool2d config {config} needs input and output of one dtype")
+        _lib.dtype_code(x.dtype), _lib.dtype_code(y.dtype)  # TypeError for other dtypes
+        return "nt_max_pool2d_cast"
+    return _entry_name("nt_max_pool2d_config" if config else "nt_max_pool2d", x.dtype)
 
 
 def bind_max_pool2d(x, y, window, stride=None, padding=(0, 0), dilation=(1, 1), config=0):
     """launch(x, y): y = max_pool2d(x) with -inf outside the input (any strides, N-C-H-W indexing).
 
+    ``y`` may have another float dtype than ``x`` (the window max is stored in y's type, as
+    the reference's store casts it; still exact, rounding is monotone): that takes the
+    element-wise kernel, so configurations other than 0 and 2 raise ``TypeError`` here.
     A nonzero ``config`` forces one kernel; a call it does not admit raises
     ``KernelLaunchError`` without launching."""
+    entry = check_max_pool2d(x, y, config)
     device = _check_device(x, y)
-    if x.dim() != 4 or y.dim() != 4:
-        raise ValueError("max_pool2d expects 4-D tensors")
-    if x.dtype != y.dtype:
-        raise TypeError("max_pool2d input and output must share one dtype")
     kh, kw = window
     sh, sw = stride if stride is not None else window
     ph, pw = padding
     dh, dw = dilation
     n, c, h, w = x.shape
-    if y.shape[0] != n or y.shape[1] != c:
-        raise ValueError("max_pool2d batch/channel sizes differ")
     p, q = y.shape[2], y.shape[3]
-    if config:
-        if config not in POOL_CONFIGS:
-            raise TypeError(f"max_pool2d config {config} is not one of {POOL_CONFIGS}")
-        fn, name = _entry("nt_max_pool2d_config", x.dtype)
-        extra = (int(config),)
-    else:
-        fn, name = _entry("nt_max_pool2d", x.dtype)
-        extra = ()
     xs, ys = _lib.int64_array(x.stride()), _lib.int64_array(y.stride())
     dims = (n, c, h, w, p, q, kh, kw, sh, sw, ph, pw, dh, dw)
     stream = _stream_of(device)
+    if x.dtype != y.dtype:
+        fn, name = _entry(entry)
+        xcode, ycode = _lib.dtype_code(x.dtype), _lib.dtype_code(y.dtype)
+
+        def launch(x, y):
+            code = fn(x.data_ptr(), xcode, xs, y.data_ptr(), ycode, ys, *dims, stream())
+            if code:
+                _raise(code, name)
+
+        return launch
+    fn, name = _entry(entry)
+    extra = (int(config),) if config else ()
 
     def launch(x, y):
         code = fn(x.data_ptr(), xs, y.data_ptr(), ys, *dims, stream(), *extra)
@@ -187,13 +245,8 @@ def max_pool2d(x, y, window, stride=None, padding=(0, 0), dilation=(1, 1), confi
 GEMM_CONFIGS = (1, 2, 3)
 
 
-def bind_gemm(a, b, out, c=None, round_dtype=None, config=0):
-    """launch(a, b, out, c, alpha, beta): out = cast(beta * c + alpha * round(a @ b)).
-
-    fp32 accumulation; any strides; ``c`` is None exactly when it was None here.  A nonzero
-    ``config`` (fp16/bf16 operands only) forces one kernel; a call its conditions do not
-    admit raises ``KernelLaunchError`` without launching."""
-    device = _check_device(a, b, out, c)
+def check_gemm(a, b, out, c=None, round_dtype=None, config=0):
+    """(entry point, out/c type argument, rounding type code) of a GEMM call."""
     if a.dim() != 2 or b.dim() != 2 or out.dim() != 2:
         raise ValueError("gemm expects 2-D tensors")
     m, k = a.shape
@@ -217,11 +270,22 @@ def bind_gemm(a, b, out, c=None, round_dtype=None, config=0):
     if config:
         if config not in GEMM_CONFIGS or _lib.dtype_suffix(a.dtype) not in ("f16", "bf16"):
             raise TypeError(f"gemm config {config} needs fp16/bf16 operands and one of {GEMM_CONFIGS}")
-        fn, name = _entry("nt_gemm_config", a.dtype)
-        extra = (int(config),)
-    else:
-        fn, name = _entry("nt_gemm", a.dtype)
-        extra = ()
+        return _entry_name("nt_gemm_config", a.dtype), out_code, rd
+    return _entry_name("nt_gemm", a.dtype), out_code, rd
+
+
+def bind_gemm(a, b, out, c=None, round_dtype=None, config=0):
+    """launch(a, b, out, c, alpha, beta): out = cast(beta * c + alpha * round(a @ b)).
+
+    fp32 accumulation; any strides; ``c`` is None exactly when it was None here.  A nonzero
+    ``config`` (fp16/bf16 operands only) forces one kernel; a call its conditions do not
+    admit raises ``KernelLaunchError`` without launching."""
+    entry, out_code, rd = check_gemm(a, b, out, c, round_dtype, config)
+    device = _check_device(a, b, out, c)
+    m, k = a.shape
+    n = b.shape[1]
+    fn, name = _entry(entry)
+    extra = (int(config),) if config else ()
     (sa_m, sa_k), (sb_k, sb_n), (so_m, so_n) = a.stride(), b.stride(), out.stride()
     sc_m, sc_n = c.stride() if c is not None else (0, 0)
     stream = _stream_of(device)
@@ -255,6 +319,23 @@ def conv2d_workspace_bytes(x, w, padding=(0, 0)):
 CONV_CONFIGS = (1, 2, 3)
 
 
+def check_conv2d(x, w, y, round_dtype=None, config=0):
+    """(entry point, rounding type code) of a conv2d call (fp16/bf16 input and filter)."""
+    if x.dim() != 4 or w.dim() != 4 or y.dim() != 4:
+        raise ValueError("conv2d expects 4-D tensors")
+    if x.dtype != w.dtype:
+        raise TypeError("conv2d input and filter must share one dtype")
+    n, c = x.shape[:2]
+    k, c2 = w.shape[:2]
+    if c2 != c or y.shape[0] != n or y.shape[1] != k:
+        raise ValueError("conv2d shape mismatch")
+    _lib.dtype_code(y.dtype)
+    rd = _lib.DTYPE_NONE if round_dtype is None else _lib.dtype_code(round_dtype)
+    if config and config not in CONV_CONFIGS:
+        raise TypeError(f"conv2d config {config} is not one of {CONV_CONFIGS}")
+    return _entry_name("nt_conv2d_config" if config else "nt_conv2d", x.dtype), rd
+
+
 def bind_conv2d(x, w, y, padding=(0, 0), stride=(1, 1), dilation=(1, 1), round_dtype=None, workspace_bytes=0,
                 config=0):
     """launch(x, w, y, workspace): y = cast(round(conv2d(x, w))) as an implicit GEMM.
@@ -263,28 +344,16 @@ def bind_conv2d(x, w, y, padding=(0, 0), stride=(1, 1), dilation=(1, 1), round_d
     least ``workspace_bytes`` bytes, or None when ``workspace_bytes`` is 0.  A nonzero
     ``config`` forces one path; a call its conditions do not admit raises
     ``KernelLaunchError`` without launching."""
+    entry, rd = check_conv2d(x, w, y, round_dtype, config)
     device = _check_device(x, w, y)
-    if x.dim() != 4 or w.dim() != 4 or y.dim() != 4:
-        raise ValueError("conv2d expects 4-D tensors")
-    if x.dtype != w.dtype:
-        raise TypeError("conv2d input and filter must share one dtype")
     n, c, h, wd = x.shape
     k, c2, r, s = w.shape
-    if c2 != c or y.shape[0] != n or y.shape[1] != k:
-        raise ValueError("conv2d shape mismatch")
     p, q = y.shape[2], y.shape[3]
     ph, pw = padding
     sh, sw = stride
     dh, dw = dilation
-    rd = _lib.DTYPE_NONE if round_dtype is None else _lib.dtype_code(round_dtype)
-    if config:
-        if config not in CONV_CONFIGS:
-            raise TypeError(f"conv2d config {config} is not one of {CONV_CONFIGS}")
-        fn, name = _entry("nt_conv2d_config", x.dtype)
-        extra = (int(config),)
-    else:
-        fn, name = _entry("nt_conv2d", x.dtype)
-        extra = ()
+    fn, name = _entry(entry)
+    extra = (int(config),) if config else ()
     xs, ws, ys = (_lib.int64_array(t.stride()) for t in (x, w, y))
     dims = (_lib.dtype_code(y.dtype), n, c, h, wd, k, r, s, p, q, ph, pw, sh, sw, dh, dw, rd)
     stream = _stream_of(device)
@@ -317,12 +386,7 @@ def conv2d(x, w, y, padding=(0, 0), stride=(1, 1), dilation=(1, 1), round_dtype=
 ATTENTION_CONFIGS = (1, 2, 3)
 
 
-def bind_attention(q, k, v, o, causal=False, q_scale=LOG2E, config=0):
-    """launch(q, k, v, o): flash attention forward of the reference application; q pre-scaled by ``q_scale``.
-
-    A nonzero ``config`` (fp16/bf16 only) forces one kernel; a call its conditions do not
-    admit raises ``KernelLaunchError`` without launching."""
-    device = _check_device(q, k, v, o)
+def check_attention(q, k, v, o, config=0):
     if not (q.dim() == k.dim() == v.dim() == o.dim() == 4):
         raise ValueError("attention expects [B, H, S, D] tensors")
     if not (q.dtype == k.dtype == v.dtype):
@@ -333,14 +397,25 @@ def bind_attention(q, k, v, o, causal=False, q_scale=LOG2E, config=0):
         raise ValueError("attention shape mismatch")
     if d > 128:
         raise ValueError("attention head dim must be <= 128")
+    _lib.dtype_code(o.dtype)
     if config:
         if config not in ATTENTION_CONFIGS or _lib.dtype_suffix(q.dtype) not in ("f16", "bf16"):
             raise TypeError(f"attention config {config} needs fp16/bf16 operands and one of {ATTENTION_CONFIGS}")
-        fn, name = _entry("nt_attention_config", q.dtype)
-        extra = (int(config),)
-    else:
-        fn, name = _entry("nt_attention", q.dtype)
-        extra = ()
+        return _entry_name("nt_attention_config", q.dtype)
+    return _entry_name("nt_attention", q.dtype)
+
+
+def bind_attention(q, k, v, o, causal=False, q_scale=LOG2E, config=0):
+    """launch(q, k, v, o): flash attention forward of the reference application; q pre-scaled by ``q_scale``.
+
+    A nonzero ``config`` (fp16/bf16 only) forces one kernel; a call its conditions do not
+    admit raises ``KernelLaunchError`` without launching."""
+    entry = check_attention(q, k, v, o, config)
+    device = _check_device(q, k, v, o)
+    bsz, heads, sq, d = q.shape
+    sk = k.shape[2]
+    fn, name = _entry(entry)
+    extra = (int(config),) if config else ()
     qs, ks, vs, os_ = (_lib.int64_array(t.stride()) for t in (q, k, v, o))
     tail = (_lib.dtype_code(o.dtype), bsz, heads, sq, sk, d, float(q_scale), 1 if causal else 0)
     stream = _stream_of(device)

@@ -190,9 +190,10 @@ def attention(q, k, v, is_causal, arrangement, scale_const=1.44269504089, in_dty
 
 
 # ----------------------------------------------------------------------------- softmax
-def softmax(x, block_size, in_dtype="float32"):
+def softmax(x, block_size, in_dtype="float32", out_dtype=None):
     """softmax_kernel (reference tests/test_softmax.py:13-21) over (1, BLOCK_SIZE) tiles with
-    other=-inf: x - max, exp, sum, divide (the divide in fp32)."""
+    other=-inf: x - max, exp, sum, divide (the divide in fp32), stored in ``out_dtype``
+    (default ``in_dtype``; the reference's store casts the fp32 quotient to the output's type)."""
     R, C = x.shape
     xt = OTensor((R, C), other=float("-inf")).tile((1, block_size))
     t, valid = _split_grid(xt, 2)  # (G, 1, BS, 2)
@@ -205,7 +206,7 @@ def softmax(x, block_size, in_dtype="float32"):
     y = num / den
     out = np.zeros((R, C), dtype=np.float32)
     _scatter(out, t, valid, y)
-    return round_to(out, in_dtype)
+    return round_to(out, in_dtype if out_dtype is None else out_dtype)
 
 
 # ----------------------------------------------------------------------------- max_pool2d

@@ -2,8 +2,8 @@
 
 CPU: the contract of the reference's AutoTuner — every candidate benchmarked once per
 argument key, the selection persisted so a new tuner with the same namespace and
-candidates benchmarks nothing, failing candidates recorded as infinite timings, an error
-naming every reason when all fail.  Programs that update a tensor they read are never
+candidates benchmarks nothing, failing candidates recorded as infinite timings (and timed
+again by the next election), an error naming every reason when all fail.  Programs that update a tensor they read are never
 tuned.  GPU: a Handle made with ``max_num_configs`` > 1 times the fitting kernels (the add
 kernel and the generic kernel) and computes the same result.
 """
@@ -84,6 +84,46 @@ def test_failing_candidates_are_skipped_and_reported():
     with pytest.raises(RuntimeError, match="All auto-tuning candidates failed: first: RuntimeError: boom; "
                                            "second: RuntimeError: boom"):
         all_broken(1)
+
+
+def test_failed_candidate_is_retimed_by_a_new_election():
+    # a candidate that failed once (a transient error, a kernel bug fixed since) is timed
+    # again by the next tuner on the same book, and wins when it is now the fastest
+    namespace = uuid.uuid4().hex
+    state = {"fail": True}
+
+    def flaky(*a, **k):
+        return "flaky"
+
+    def benchmark(function, a, k):
+        if function is flaky:
+            if state["fail"]:
+                raise RuntimeError("device busy")
+            return 0.5
+        return 1.0
+
+    first = AutoTuner((flaky, _foo), ("flaky", "_foo"), benchmark=benchmark, cache_namespace=namespace)
+    assert first(1) == "foo"
+    assert first.timings(1)["flaky"].startswith("error: RuntimeError: device busy")
+    state["fail"] = False
+    second = AutoTuner((flaky, _foo), ("flaky", "_foo"), benchmark=benchmark, cache_namespace=namespace)
+    assert second(1) == "flaky"
+    assert second.timings(1) == {"flaky": 0.5, "_foo": 1.0}
+    # a row where every candidate failed is not final either
+    all_failed = uuid.uuid4().hex
+    state["fail"] = True
+    with pytest.raises(RuntimeError, match="All auto-tuning candidates failed"):
+        AutoTuner((flaky,), ("flaky",), benchmark=benchmark, cache_namespace=all_failed)(1)
+    state["fail"] = False
+    assert AutoTuner((flaky,), ("flaky",), benchmark=benchmark, cache_namespace=all_failed)(1) == "flaky"
+
+
+def test_book_is_keyed_by_library_build(monkeypatch):
+    from ninetoothed_amd import auto_tuner
+
+    book = AutoTuner((_foo,), ("_foo",), cache_namespace="ns").book.path
+    monkeypatch.setattr(auto_tuner, "_BUILD", "another-build")
+    assert AutoTuner((_foo,), ("_foo",), cache_namespace="ns").book.path != book
 
 
 def test_winner_that_raises_is_not_kept():
@@ -268,7 +308,16 @@ def test_softmax_and_pool_plans_expand_into_kernels():
     ctx = sm._kernel.context(dict(zip(list(sm._kernel.params), (x, x))), {"BLOCK_SIZE": 300})
     described = [p.describe() for p in families.candidates(ctx)]
     assert [(d["family"], d.get("config")) for d in described] == [
-        ("softmax", 1), ("softmax", 2), ("softmax", 3), ("softmax", 4), ("softmax", 5), ("generic", None)]
+        ("softmax", 1), ("softmax", 2), ("softmax", 3), ("softmax", 4), ("softmax", 5), ("softmax", 6),
+        ("generic", None)]
+    # a transposed input or an output of another dtype: only the element-wise kernel admits it
+    xt = torch.empty(300, 8).t()
+    ctx = sm._kernel.context(dict(zip(list(sm._kernel.params), (xt, x))), {"BLOCK_SIZE": 300})
+    assert [(d["family"], d.get("config")) for d in map(lambda p: p.describe(), families.candidates(ctx))] == [
+        ("softmax", 6), ("generic", None)]
+    ctx = sm._kernel.context(dict(zip(list(sm._kernel.params), (x.half(), x))), {"BLOCK_SIZE": 300})
+    assert [(d["family"], d.get("config")) for d in map(lambda p: p.describe(), families.candidates(ctx))] == [
+        ("softmax", 6), ("generic", None)]
     pool = ninetoothed.make(functools.partial(pg.max_pool2d_arrangement, ceil_mode=False), pg.max_pool2d_application,
                             pg.max_pool2d_tensors())
     xi, yo = torch.empty(2, 3, 16, 16, dtype=torch.float16), torch.empty(2, 3, 8, 8, dtype=torch.float16)
@@ -276,6 +325,11 @@ def test_softmax_and_pool_plans_expand_into_kernels():
     described = [p.describe() for p in families.candidates(ctx)]
     assert [(d["family"], d.get("config")) for d in described][:4] == [
         ("max_pool2d", 1), ("max_pool2d", 2), ("max_pool2d", 3), ("max_pool2d", 4)]
+    ctx = pool._kernel.context(dict(zip(list(pool._kernel.params), (xi, yo.float()))),
+                               {"WINDOW_HEIGHT": 2, "WINDOW_WIDTH": 2})
+    described = [p.describe() for p in families.candidates(ctx)]
+    assert [(d["family"], d.get("config")) for d in described][:1] == [("max_pool2d", 2)]
+    assert all(d["family"] != "max_pool2d" for d in described[1:])
 
 
 @pytest.mark.gpu

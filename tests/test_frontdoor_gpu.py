@@ -261,7 +261,54 @@ def test_softmax_partial_block():
     assert np.allclose(_np(out), apply.softmax(_np(x), 256), atol=1e-6, rtol=1e-5)
 
 
+@pytest.mark.parametrize("layout", ("transposed", "every_other_column"))
+@pytest.mark.parametrize("block", (781, 256))
+def test_softmax_strided_columns(layout, block):
+    # the reference passes strides to its kernel: softmax(x.t(), y) and softmax(x[:, ::2], y) run
+    if layout == "transposed":
+        x = _randn((781, 64), torch.float16, 21, 2.0).t()
+    else:
+        x = _randn((64, 1562), torch.float16, 21, 2.0)[:, ::2]
+    assert x.stride(1) != 1
+    y = torch.full(x.shape, float("nan"), dtype=torch.float16, device=DEV)
+    pg.make_softmax()(x, y, BLOCK_SIZE=block)
+    ref = apply.softmax(_np(x), block, "float16")
+    assert np.allclose(_np(y), ref, atol=1e-3, rtol=1e-2)
+    if block == 781:
+        assert torch.allclose(y.float(), torch.softmax(x.float(), -1), atol=1e-3, rtol=1e-2)
+
+
+@pytest.mark.parametrize("in_dtype, out_dtype", ((torch.float16, torch.float32), (torch.float32, torch.bfloat16),
+                                                 (torch.bfloat16, torch.float16)))
+def test_softmax_output_of_another_dtype(in_dtype, out_dtype):
+    # the reference's store casts the fp32 quotient to the output's type
+    x = _randn((129, 3000), in_dtype, 22, 2.0)
+    y = torch.full(x.shape, float("nan"), dtype=out_dtype, device=DEV)
+    pg.make_softmax()(x, y, BLOCK_SIZE=3000)
+    names = {torch.float16: "float16", torch.bfloat16: "bfloat16", torch.float32: "float32"}
+    ref = apply.softmax(_np(x), 3000, names[in_dtype], out_dtype=names[out_dtype])
+    assert np.allclose(_np(y), ref, atol=1e-3, rtol=1e-2)
+    # fp32 math throughout on the kernel's side: close to torch's float softmax of the same values
+    assert torch.allclose(y.float(), torch.softmax(x.float(), -1).to(out_dtype).float(), atol=1e-5, rtol=1e-2)
+
+
 # -------------------------------------------------------------------- max_pool2d
+@pytest.mark.parametrize("in_dtype, out_dtype", ((torch.float16, torch.float32), (torch.float32, torch.float16),
+                                                 (torch.bfloat16, torch.float32)))
+@pytest.mark.parametrize("ceil_mode", (False, True))
+def test_max_pool2d_output_of_another_dtype(in_dtype, out_dtype, ceil_mode):
+    x = _rand((3, 5, 33, 34), in_dtype, 23, -1.0, 1.0)
+    kernel = ninetoothed.make(functools.partial(pg.max_pool2d_arrangement, ceil_mode=ceil_mode),
+                              pg.max_pool2d_application, pg.max_pool2d_tensors())
+    ref = F.max_pool2d(x, (2, 2), ceil_mode=ceil_mode)
+    y = torch.full(ref.shape, float("nan"), dtype=out_dtype, device=DEV)
+    kernel(x, y, WINDOW_HEIGHT=2, WINDOW_WIDTH=2)
+    assert torch.equal(y, ref.to(out_dtype))  # bit-exact: rounding is monotone
+    oracle = apply.max_pool2d(_np(x), (2, 2), ceil_mode,
+                              functools.partial(pg.max_pool2d_arrangement, ceil_mode=ceil_mode))
+    assert np.array_equal(_np(y), _np(torch.from_numpy(oracle).to(out_dtype)))
+
+
 @pytest.mark.parametrize("ceil_mode", (False, True))
 def test_max_pool2d_reference_case(ceil_mode):
     x = _randn((32, 3, 64, 64), torch.float16, 50)

@@ -96,6 +96,47 @@ def test_softmax_segments():
     assert torch.allclose(y, ref, atol=1e-6, rtol=1e-5)
 
 
+@pytest.mark.parametrize("config", (0, 5))
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16, torch.float32))
+def test_softmax_short_contiguous_widths(dtype, config):
+    # Contiguous rows whose byte length is no multiple of 16: most rows start inside a 16-byte
+    # vector, so the lane-group kernel splits off a head of up to V - 1 elements (7 for
+    # 16-bit types, 3 for fp32), more than a group of 1, 2 or 4 lanes has.  y starts as NaN
+    # so an element the kernel never writes shows.
+    widths = range(2, 32) if dtype != torch.float32 else range(2, 16)
+    for cols in widths:
+        x = _randn((37, cols), dtype, 100 + cols, scale=2.0)
+        y = torch.full_like(x, float("nan"))
+        kernels.softmax(x, y, config=config)
+        ref = torch.softmax(x.float(), dim=-1)
+        assert not torch.isnan(y).any(), f"cols={cols}: unwritten outputs"
+        assert torch.allclose(y.float(), ref, atol=TOL[dtype], rtol=TOL[dtype]), f"cols={cols}"
+
+
+@pytest.mark.parametrize("dtype", (torch.float16, torch.float32))
+@pytest.mark.parametrize("block", (None, 100))
+def test_softmax_any_strides(dtype, block):
+    # column strides other than 1 (a transposed view, every third column, a reversed row)
+    # take the element-wise kernel; the forced vector kernels refuse them before launching
+    base = _randn((450, 300), dtype, 15, scale=2.0)
+    views = (base.t(), base[:, ::3], base.flip(1))
+    for x in views:
+        rows, cols = x.shape
+        blk = cols if block is None else block
+        nseg = -(-cols // blk)
+        xp = F.pad(x.float(), (0, nseg * blk - cols), value=float("-inf")).view(rows, nseg, blk)
+        ref = torch.softmax(xp, dim=-1).view(rows, nseg * blk)[:, :cols]
+        for y in (torch.full((rows, cols), float("nan"), dtype=dtype, device=DEV),
+                  torch.full((cols, rows), float("nan"), dtype=dtype, device=DEV).t()):
+            kernels.softmax(x, y, block=block)
+            assert torch.allclose(y.float(), ref, atol=TOL[dtype], rtol=TOL[dtype])
+            y.fill_(float("nan"))
+            kernels.softmax(x, y, block=block, config=kernels.SOFTMAX_ANY)
+            assert torch.allclose(y.float(), ref, atol=TOL[dtype], rtol=TOL[dtype])
+        with pytest.raises(ValueError):
+            kernels.softmax(x, torch.empty(rows, cols, dtype=dtype, device=DEV), block=block, config=1)
+
+
 def test_softmax_headline_shape():
     x = _randn((8192, 8192), torch.float16, 7, scale=2.0)
     y = torch.empty_like(x)
@@ -612,6 +653,48 @@ def test_conv2d_dma_any_q(case, dtype):
     y = torch.full(ref.shape, 7.0, dtype=dtype, device=DEV)
     kernels.conv2d(x, w, y, padding=padding, stride=stride, workspace=_workspace(x, w, padding), config=1)
     assert torch.allclose(y.float(), ref, atol=2e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("flip", ("w", "h"))
+@pytest.mark.parametrize("config", (0, 1, 3))
+@pytest.mark.parametrize("xshape", ((4, 64, 15, 13), (17, 64, 45, 45)))
+def test_conv2d_flipped_output(flip, config, xshape):
+    """An output flipped along w (q stride -1) or h (p stride -Q) through the C ABI, with
+    Q % 8 != 0 so the DMA kernel stores element by element (the small shape splits the
+    reduction, the large one does not): positions at negative offsets from the data
+    pointer are valid outputs and must be written, on every path."""
+    import ctypes
+
+    from ninetoothed_amd import _lib
+
+    lib = _lib.load()
+    x = _randn(xshape, torch.float16, 64)
+    w = _randn((128, 64, 3, 3), torch.float16, 65, 1.0 / math.sqrt(64 * 9))
+    ref = F.conv2d(x.float(), w.float(), padding=1)
+    n, k, p, q = ref.shape
+    assert q % 8 != 0
+    ybuf = torch.full(ref.shape, float("nan"), dtype=torch.float16, device=DEV)
+    es = ybuf.element_size()
+    if flip == "w":
+        ptr, ys = ybuf.data_ptr() + (q - 1) * es, (k * p * q, p * q, q, -1)
+    else:
+        ptr, ys = ybuf.data_ptr() + (p - 1) * q * es, (k * p * q, p * q, -q, 1)
+    nbytes = kernels.conv2d_workspace_bytes(x, w, (1, 1))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=DEV)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    code16 = _lib.dtype_code(torch.float16)
+    args = (x.data_ptr(), _lib.int64_array(x.stride()), w.data_ptr(), _lib.int64_array(w.stride()), ptr,
+            _lib.int64_array(ys), code16, *xshape, k, 3, 3, p, q, 1, 1, 1, 1, 1, 1, code16,
+            ws.data_ptr() if config != 3 else None, nbytes if config != 3 else 0)
+    if config:
+        code = lib.nt_conv2d_config_f16(*args, config, stream)
+    else:
+        code = lib.nt_conv2d_f16(*args, stream)
+    torch.cuda.synchronize()
+    assert code == 0
+    got = ybuf.flip(3) if flip == "w" else ybuf.flip(2)
+    assert not torch.isnan(got).any()
+    assert torch.allclose(got.float(), ref, atol=2e-2, rtol=1e-2)
 
 
 def test_conv2d_empty_filter():

@@ -116,6 +116,18 @@ def test_softmax_closed_form(block):
         assert np.allclose(got.sum(1), 1.0, atol=1e-5)
 
 
+def test_softmax_fp16_input_fp32_output():
+    # fp16 arithmetic up to the quotient, the quotient stored as fp32 (not rounded to fp16):
+    # within fp16 precision of the float64 softmax, and not on the fp16 grid
+    r = _rng(18)
+    x = _f16(r.standard_normal((5, 300)) * 2)
+    got = apply.softmax(x, 300, "float16", out_dtype="float32")
+    ref = torch.softmax(torch.from_numpy(x).double(), -1).numpy()
+    assert np.allclose(got, ref, atol=2e-4, rtol=4e-3)
+    assert not np.array_equal(got, got.astype(np.float16).astype(np.float32))
+    assert np.array_equal(apply.softmax(x, 300, "float16"), got.astype(np.float16).astype(np.float32))
+
+
 @pytest.mark.parametrize("ceil_mode", (False, True))
 def test_max_pool2d_closed_form(ceil_mode):
     r = _rng(9)
