@@ -300,8 +300,10 @@ _block_size_counter = itertools.count()
 
 
 def block_size(lower_bound=None, upper_bound=None):
-    """A fresh block-size meta symbol (reference ``src/ninetoothed/symbol.py:257-271``)."""
-    return Symbol(f"BLOCK_SIZE_{next(_block_size_counter)}", meta=True, lower_bound=lower_bound, upper_bound=upper_bound)
+    """A fresh block-size meta symbol (reference ``src/ninetoothed/symbol.py:257-271``), named as
+    the reference names generated symbols (``naming.py:4-5``), so a call's meta keywords agree."""
+    return Symbol(f"ninetoothed_BLOCK_SIZE_{next(_block_size_counter)}", meta=True, lower_bound=lower_bound,
+                  upper_bound=upper_bound)
 
 
 def default_meta_value(symbol, preferred=64):

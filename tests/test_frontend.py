@@ -1,6 +1,7 @@
 """Host logic on the CPU: lowering, family matching, launch ABI, call contract, registry."""
 
 import functools
+import json
 import re
 from pathlib import Path
 
@@ -28,12 +29,21 @@ def _h(shape, dtype=torch.float16):
     return torch.empty(shape, dtype=dtype)
 
 
+# The reference's own schedule granularity per program (compiler/passes.py:1070-1084), as its
+# pipeline computed it for its test programs (tests/golden/make_reference_registry.py).
+_REFERENCE = json.loads((Path(__file__).parent / "golden" / "reference_registry.json").read_text())["programs"]
+
+
+def _granularity(program):
+    return _REFERENCE[program]["reference"]["granularity"]
+
+
 # ------------------------------------------------------------------- matching
 def test_matmul_matches_gemm():
     h = ninetoothed.make(pg.matmul_arrangement, pg.matmul_application, pg.matmul_tensors())
     assert h._abi["public_args"] == ("lhs", "rhs", "output")
     assert h._abi["outputs"] == ("output",)
-    assert h._kernel.granularity == "blocked-linalg"
+    assert h._kernel.granularity == _granularity("matmul")
     d = _specialize(h, _h((96, 80)), _h((80, 72)), _h((96, 72)))
     assert d["family"] == "gemm" and d["round"] == "torch.float16" and d["c"] is None
 
@@ -57,13 +67,13 @@ def test_conv2d_geometry_is_recovered(padding):
     d = _specialize(h, _h((4, 64, 16, 16)), _h((512, 64, 3, 3)), _h((4, 512, 14 + 2 * ph, 14 + 2 * pw)),
                     padding_h=ph, padding_w=pw)
     assert d["family"] == "conv2d" and d["padding"] == padding and d["stride"] == (1, 1)
-    assert h._kernel.granularity == "blocked-linalg"  # reference compiler/passes.py:1070-1084: a dot, no exp
+    assert h._kernel.granularity == _granularity("conv2d")
 
 
 @pytest.mark.parametrize("causal", (False, True))
 def test_attention_matches(causal):
     h = ninetoothed.make(pg.attention_arrangement, pg.attention_application, pg.attention_tensors())
-    assert h._kernel.granularity == "exp-reduction-dot-region"
+    assert h._kernel.granularity == _granularity("attention")
     q = _h((2, 4, 100, 64))
     d = _specialize(h, q, q, q, causal, q)
     assert d == {"family": "attention", "causal": causal, "scale": 1.44269504089}
@@ -71,7 +81,7 @@ def test_attention_matches(causal):
 
 def test_softmax_block_size_is_semantic():
     sm = pg.make_softmax()
-    assert sm._kernel.granularity == "parallel-reduction"
+    assert sm._kernel.granularity == _granularity("softmax")
     x = torch.empty(10, 100)
     assert _specialize(sm, x, torch.empty_like(x), BLOCK_SIZE=100)["block"] == 100
     assert _specialize(sm, x, torch.empty_like(x), BLOCK_SIZE=32)["block"] == 32
@@ -84,12 +94,12 @@ def test_max_pool2d_window(ceil_mode):
     p = (64 - 3 + (2 if ceil_mode else 0)) // 3 + 1
     d = _specialize(h, _h((32, 3, 64, 64)), _h((32, 3, p, p)), WINDOW_HEIGHT=3, WINDOW_WIDTH=3)
     assert d["family"] == "max_pool2d" and d["window"] == (3, 3) and d["stride"] == (3, 3)
-    assert h._kernel.granularity == "parallel-reduction"  # a max reduction, no dot
+    assert h._kernel.granularity == _granularity("max_pool2d")
 
 
 def test_add_matches():
     add = pg.make_add()
-    assert add._kernel.granularity == "elementwise-grid"
+    assert add._kernel.granularity == _granularity("add")
     v = torch.empty(98432)
     assert _specialize(add, v, v, v)["family"] == "add"
 
