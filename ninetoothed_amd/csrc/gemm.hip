@@ -563,6 +563,42 @@ __device__ __forceinline__ void dma_fast_epilogue(const GemmArgs& g, const float
   }
 }
 
+// The DMA kernels' element-wise epilogue (any out type, any c type, any strides).  After a
+// barrier the operand ring is free: each wave stages two of its four 32-row slabs there at
+// once (16 KiB per wave), finishes them one element per lane per step (consecutive lanes on
+// consecutive columns, nothing unrolled), then does the same with the other two, so that
+// at most half of the accumulators are live while elements are stored.
+template <int WJ = 2, bool C8 = false>
+__device__ __forceinline__ void dma_any_epilogue(const GemmArgs& g, const floatx16 (&acc)[4][WJ], char* lds, int wave,
+                                                 int lane, int64_t row_base, int64_t col_base) {
+  constexpr int COLS = 32 * WJ;
+  float* stage = (float*)(lds + wave * (2 * 32 * COLS * 4));
+  __syncthreads();  // other waves may still read the last operand stage
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    wave_lds_order();  // the previous pair's reads come first
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < WJ; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          stage[(i * 32 + acc_row(r, lane)) * COLS + j * 32 + (lane & 31)] = acc[2 * p + i][j][r];
+    wave_lds_order();  // every lane's writes before any lane reads
+    const int64_t row0 = row_base + p * 64;
+#pragma unroll 1
+    for (int e = lane; e < 64 * COLS; e += 64) {
+      const int rr = e / COLS, cc = e % COLS;
+      const int64_t row = row0 + rr, col = col_base + cc;
+      if (row < g.M && col < g.N) {
+        float r = g.alpha * round_through(stage[rr * COLS + cc], g.round_dtype);
+        if (g.c) r += g.beta * load_c<C8>(g, row * g.sc_m + col * g.sc_n);
+        store_from_float(g.out, row * g.so_m + col * g.so_n, g.out_dtype, r);
+      }
+    }
+  }
+}
+
 // FAST_EPI: the launcher's c_pre condition holds (16-bit out and c of one type, unit column
 // stride, aligned rows); the other instance finishes through the element-wise epilogue.  Two
 // instances so that the fast one holds no code of the other (whose registers would spill).
@@ -724,7 +760,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   const int64_t row_base = m0 + wm * 128, col_base = n0 + wn * 64;
   if constexpr (!FAST_EPI) {
-    gemm_epilogue<4, 2>(g, acc, (uint16_t*)lds, wave, lane, row_base, col_base);
+    dma_any_epilogue<2>(g, acc, lds, wave, lane, row_base, col_base);
     return;
   }
   dma_fast_epilogue<2, true>(g, acc, lds, wave, lane, row_base, col_base);
@@ -834,34 +870,46 @@ __global__ __launch_bounds__(64 * F32S_WAVES) void gemm_f32_splitk_kernel(GemmAr
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-  for (int64_t ch = c_lo; ch < c_hi; ++ch) {
-    const int64_t kb = ch * 32 + 8 * t;  // this lane group's eight k values: kb .. kb + 7
-    float a[2][8], b[2][8];
+  // Two chunks per step, all their loads issued before the first MFMA: the second chunk's
+  // fetch latency hides behind the first's (512^3: one step per wave; 0.8 us less per call
+  // than loading and multiplying one chunk at a time).  A chunk at or past c_hi reads zeros.
+  for (int64_t ch0 = c_lo; ch0 < c_hi; ch0 += 2) {
+    float a[2][2][8], b[2][2][8];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int64_t row = m0 + i * 16 + r16;
-      if (AVEC && row < g.M && kb + 8 <= g.K) {
-        const float4 lo = *(const float4*)(A + row * g.sa_m + kb);
-        const float4 hi = *(const float4*)(A + row * g.sa_m + kb + 4);
-        a[i][0] = lo.x; a[i][1] = lo.y; a[i][2] = lo.z; a[i][3] = lo.w;
-        a[i][4] = hi.x; a[i][5] = hi.y; a[i][6] = hi.z; a[i][7] = hi.w;
-      } else {
+    for (int h = 0; h < 2; ++h) {
+      const bool live = ch0 + h < c_hi;
+      const int64_t kb = (ch0 + h) * 32 + 8 * t;  // this lane group's eight k values: kb .. kb + 7
 #pragma unroll
-        for (int s = 0; s < 8; ++s) a[i][s] = (row < g.M && kb + s < g.K) ? A[row * g.sa_m + (kb + s) * g.sa_k] : 0.f;
+      for (int i = 0; i < 2; ++i) {
+        const int64_t row = m0 + i * 16 + r16;
+        if (AVEC && live && row < g.M && kb + 8 <= g.K) {
+          const float4 lo = *(const float4*)(A + row * g.sa_m + kb);
+          const float4 hi = *(const float4*)(A + row * g.sa_m + kb + 4);
+          a[h][i][0] = lo.x; a[h][i][1] = lo.y; a[h][i][2] = lo.z; a[h][i][3] = lo.w;
+          a[h][i][4] = hi.x; a[h][i][5] = hi.y; a[h][i][6] = hi.z; a[h][i][7] = hi.w;
+        } else {
+#pragma unroll
+          for (int s = 0; s < 8; ++s)
+            a[h][i][s] = (live && row < g.M && kb + s < g.K) ? A[row * g.sa_m + (kb + s) * g.sa_k] : 0.f;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int64_t col = n0 + j * 16 + r16;
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+          b[h][j][s] = (live && col < g.N && kb + s < g.K) ? B[(kb + s) * g.sb_k + col * g.sb_n] : 0.f;
       }
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int64_t col = n0 + j * 16 + r16;
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int s = 0; s < 8; ++s) b[j][s] = (col < g.N && kb + s < g.K) ? B[(kb + s) * g.sb_k + col * g.sb_n] : 0.f;
-    }
+      for (int s = 0; s < 8; ++s)
 #pragma unroll
-    for (int s = 0; s < 8; ++s)
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][s], b[j][s], acc[i][j], 0, 0, 0);
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[h][i][s], b[h][j][s], acc[i][j], 0, 0, 0);
   }
   // 16 x 16 blocks: lane l holds rows 4 (l / 16) + v, column l % 16.
   float* mine = part + wave * (F32_TM * F32_TN);
@@ -1192,7 +1240,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   if constexpr (FAST_EPI)
     dma_fast_epilogue(g, acc, lds, wave, lane, m0 + wm * 128, n0 + wn * 64);
   else
-    gemm_epilogue<4, 2, true>(g, acc, (uint16_t*)lds, wave, lane, m0 + wm * 128, n0 + wn * 64);
+    dma_any_epilogue<2, true>(g, acc, lds, wave, lane, m0 + wm * 128, n0 + wn * 64);
 }
 
 template <typename S>
