@@ -10,7 +10,10 @@ the Handle to its kernel); then exactly K steps bracketed by
 torch.cuda.synchronize(), timed with HIP events recorded on the stream the kernels are
 launched on (torch's current stream, which the launchers pass to the library) ->
 ``ms_per_step`` and ``value``; then max(K, S) further steps (S = --samples, default 50), each between its own pair
-of events -> ``median_ms`` and the 10th/90th percentiles (the spread).  The bandwidth-bound
+of events -> ``median_ms`` and the 10th/90th percentiles (the spread).  Configurations under
+0.1 ms per step also report ``graph_ms_per_step`` / ``graph_value``: K calls captured once in a
+HIP graph and replayed, i.e. the kernels' rate without the host path of a Handle call (about
+8 us per call, which sets the pace of the direct calls for kernels of a few microseconds).  The bandwidth-bound
 configurations (softmax, max_pool2d, add) rotate through buffer sets whose total exceeds
 the 256 MB Infinity Cache, so every step reads its inputs from HBM.
 
@@ -52,6 +55,9 @@ def _args():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--only", default="")
     p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--no-graph", action="store_true", help="skip the graph-replayed timing (e.g. under a profiler)")
+    p.add_argument("--cold", action="store_true",
+                   help="MFMA configurations rotate buffer sets that exceed the Infinity Cache, as the bandwidth ones do")
     p.add_argument("--samples", type=int, default=50,
                    help="launches timed one by one for the median (at least --steps)")
     p.add_argument("--calibrate-copy", action="store_true",
@@ -219,8 +225,14 @@ def _cpu_cases(torch, pg):
 
 
 # ------------------------------------------------------------------ GPU configurations
-def _configs(torch, ninetoothed, pg):
+def _configs(torch, ninetoothed, pg, cold=False):
+    """The configurations.  ``cold``: the MFMA configurations, too, rotate buffer sets whose
+    total exceeds the Infinity Cache (by default they run on one set, whose operands the
+    256 MB cache may partly hold between steps)."""
     dev = "cuda"
+
+    def nsets(set_bytes):
+        return _sets(set_bytes) if cold else 1
     g = torch.Generator().manual_seed(1234)
 
     def randn(shape, dtype, scale=1.0):
@@ -234,10 +246,13 @@ def _configs(torch, ninetoothed, pg):
     def addmm(dtype, name, label):
         def setup():
             s = 1.0 / math.sqrt(4096)
-            c, a, b = (randn((4096, 4096), dtype, s) for _ in range(3))
-            o = torch.empty_like(c)
             k = ninetoothed.make(pg.addmm_arrangement, pg.addmm_application, pg.addmm_tensors())
-            return [lambda: k(c, a, b, 0.5, 1.0, o)]
+            fns = []
+            for _ in range(nsets(4 * 4096 * 4096 * 2)):
+                c, a, b = (randn((4096, 4096), dtype, s) for _ in range(3))
+                o = torch.empty_like(c)
+                fns.append(lambda c=c, a=a, b=b, o=o: k(c, a, b, 0.5, 1.0, o))
+            return fns
 
         out.append(dict(name=name, workload=label, setup=setup, work=2 * 4096**3, unit="TFLOP/s", bound="mfma",
                         peak=PEAK["fp16"], dtype="fp16" if dtype == torch.float16 else "bf16"))
@@ -257,11 +272,14 @@ def _configs(torch, ninetoothed, pg):
     def matmul_e5m2():
         # the reference's fp8 case (tests/test_matmul.py:64-88) at 4096^3: e5m2 lhs, column-major
         # e5m2 rhs, fp16 output
-        a = randn((4096, 4096), torch.float16).to(torch.float8_e5m2)
-        b = randn((4096, 4096), torch.float16).T.to(torch.float8_e5m2)
-        o = torch.empty((4096, 4096), dtype=torch.float16, device=dev)
         k = ninetoothed.make(pg.matmul_arrangement, pg.matmul_application, pg.matmul_tensors())
-        return [lambda: k(a, b, o)]
+        fns = []
+        for _ in range(nsets(4 * 4096 * 4096)):
+            a = randn((4096, 4096), torch.float16).to(torch.float8_e5m2)
+            b = randn((4096, 4096), torch.float16).T.to(torch.float8_e5m2)
+            o = torch.empty((4096, 4096), dtype=torch.float16, device=dev)
+            fns.append(lambda a=a, b=b, o=o: k(a, b, o))
+        return fns
 
     out.append(dict(name="matmul_e5m2_4096", workload="fp8 e5m2 matmul C=A@B (B column-major), fp16 out, M=N=K=4096, "
                     "N(0,1)", setup=matmul_e5m2, work=2 * 4096**3, unit="TFLOP/s", bound="mfma", peak=PEAK["fp8"],
@@ -313,11 +331,14 @@ def _configs(torch, ninetoothed, pg):
                     extra=True))
 
     def conv():
-        x = randn((16, 256, 56, 56), torch.float16)
-        w = randn((256, 256, 3, 3), torch.float16, 1.0 / math.sqrt(256 * 9))
-        y = torch.empty_like(x)
         k = pg.make_conv2d()
-        return [lambda: k(x, w, y, padding_h=1, padding_w=1)]
+        fns = []
+        for _ in range(nsets(2 * 16 * 256 * 56 * 56 * 2 + 256 * 256 * 9 * 2)):
+            x = randn((16, 256, 56, 56), torch.float16)
+            w = randn((256, 256, 3, 3), torch.float16, 1.0 / math.sqrt(256 * 9))
+            y = torch.empty_like(x)
+            fns.append(lambda x=x, w=w, y=y: k(x, w, y, padding_h=1, padding_w=1))
+        return fns
 
     out.append(dict(name="conv2d_fp16", workload="fp16 conv2d [16,256,56,56] * [256,256,3,3], pad 1 (implicit GEMM)",
                     setup=conv, work=2 * (16 * 56 * 56) * 256 * (256 * 9), unit="TFLOP/s", bound="mfma",
@@ -325,10 +346,13 @@ def _configs(torch, ninetoothed, pg):
 
     def attention(causal):
         def setup():
-            q, k_, v = (randn((4, 32, 4096, 128), torch.float16) for _ in range(3))
-            o = torch.empty_like(q)
             k = ninetoothed.make(pg.attention_arrangement, pg.attention_application_scaled, pg.attention_tensors())
-            return [lambda: k(q, k_, v, causal, o)]
+            fns = []
+            for _ in range(nsets(4 * 4 * 32 * 4096 * 128 * 2)):
+                q, k_, v = (randn((4, 32, 4096, 128), torch.float16) for _ in range(3))
+                o = torch.empty_like(q)
+                fns.append(lambda q=q, k_=k_, v=v, o=o: k(q, k_, v, causal, o))
+            return fns
 
         return setup
 
@@ -382,6 +406,32 @@ def _time(torch, fns, steps, warmup, samples):
     return start.elapsed_time(stop) / 1e3 / steps, wall / steps, each
 
 
+def _graph_time(torch, fns, steps, replays=5):
+    """Seconds per step with `steps` calls captured once in a HIP graph and replayed: the
+    kernels' own rate without the host path of a Handle call (which sets the pace of the
+    direct calls for kernels of a few microseconds).  Reported beside ms_per_step only."""
+    n = len(fns)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(3):
+            fns[i % n]()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            fns[i % n]()
+    graph.replay()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / 1e3 / (replays * steps)
+
+
 def main():
     args = _args()
     if args.gpus != 1:
@@ -406,7 +456,7 @@ def main():
     import ninetoothed_amd as ninetoothed
     import programs as pg
 
-    configs = _configs(torch, ninetoothed, pg)
+    configs = _configs(torch, ninetoothed, pg, cold=args.cold)
     only = set(filter(None, args.only.split(",")))
     traffic = _traffic()
     warmup, samples = args.warmup, max(args.steps, args.samples)
@@ -429,10 +479,20 @@ def main():
                          "unit": cfg["unit"], "frac": achieved / cfg["peak"],
                          "traffic": entry.get("bytes"), "traffic_source": entry.get("source")},
         })
+        if sec < 1e-4 and not args.no_graph:
+            try:
+                gsec = _graph_time(torch, fns, args.steps)
+                results[-1]["graph_ms_per_step"] = gsec * 1e3
+                results[-1]["graph_value"] = cfg["work"] / gsec / scale
+            except Exception as exc:  # noqa: BLE001  (reported, never fatal)
+                results[-1]["graph_ms_per_step"] = None
+                results[-1]["graph_error"] = f"{type(exc).__name__}: {exc}"
         del fns
         torch.cuda.empty_cache()
+        graph = results[-1].get("graph_ms_per_step")
         print(f"# {cfg['name']}: {achieved / scale:.1f} {cfg['unit']} ({achieved / cfg['peak'] * 100:.1f}% of peak), "
-              f"{sec * 1e3:.4f} ms/step, median {pct(0.5):.4f} ms (p10 {pct(0.1):.4f}, p90 {pct(0.9):.4f})",
+              f"{sec * 1e3:.4f} ms/step, median {pct(0.5):.4f} ms (p10 {pct(0.1):.4f}, p90 {pct(0.9):.4f})"
+              + (f", graph-replayed {graph:.4f} ms/step" if graph else ""),
               file=sys.stderr, flush=True)
 
     head = next((r for r in results if r["name"] == "addmm_fp16_4096"), results[0] if results else None)
@@ -449,6 +509,8 @@ def main():
         "vs_baseline": None,
         "dtype": head["dtype"] if head else None,
         "data": "synthetic (seeded CPU generator, moved to the GPU before timing)",
+        "mfma_buffers": ("cold: every configuration rotates buffer sets larger than the Infinity Cache" if args.cold
+                         else "warm: MFMA configurations run on one buffer set, bandwidth ones rotate"),
         "config": {"workload": head["workload"] if head else None, "entry": "ninetoothed_amd.make (drop-in Handle)"},
         "roofline": dict(head["roofline"]) if head else None,
         "configs": results,

@@ -96,9 +96,12 @@ class Handle:
 
     def _fast_key(self, args, kwargs):
         # A tensor's data-pointer alignment is part of the key: a launcher bound (or tuned)
-        # for 16-byte aligned operands may have chosen a kernel that needs them.
+        # for 16-byte aligned operands may have chosen a kernel that needs them.  The device
+        # enters as its index (get_device: -1 off the GPU), which hashes far faster than a
+        # torch.device object and tells the same tensors apart (all GPU tensors here report
+        # one device type).
         key = tuple([
-            (v.dtype, v.shape, v.stride(), v.device, v.data_ptr() & 15) if kind == 0
+            (v.dtype, v.shape, v.stride(), v.get_device(), v.data_ptr() & 15) if kind == 0
             else (v if kind == 1 else type(v))
             for v, kind in zip(args, self._kinds)
         ])
