@@ -11,7 +11,7 @@ torch.cuda.synchronize(), timed with HIP events recorded on the stream the kerne
 launched on (torch's current stream, which the launchers pass to the library) ->
 ``ms_per_step`` and ``value``; then max(K, S) further steps (S = --samples, default 50), each between its own pair
 of events -> ``median_ms`` and the 10th/90th percentiles (the spread).  Configurations under
-0.1 ms per step also report ``graph_ms_per_step`` / ``graph_value``: K calls captured once in a
+30 us per step also report ``graph_ms_per_step`` / ``graph_value``: K calls captured once in a
 HIP graph and replayed, i.e. the kernels' rate without the host path of a Handle call (about
 8 us per call, which sets the pace of the direct calls for kernels of a few microseconds).  The bandwidth-bound
 configurations (softmax, max_pool2d, add) rotate through buffer sets whose total exceeds
@@ -479,7 +479,7 @@ def main():
                          "unit": cfg["unit"], "frac": achieved / cfg["peak"],
                          "traffic": entry.get("bytes"), "traffic_source": entry.get("source")},
         })
-        if sec < 1e-4 and not args.no_graph:
+        if sec < 3e-5 and not args.no_graph:
             try:
                 gsec = _graph_time(torch, fns, args.steps)
                 results[-1]["graph_ms_per_step"] = gsec * 1e3

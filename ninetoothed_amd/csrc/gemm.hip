@@ -933,6 +933,77 @@ __global__ __launch_bounds__(64 * F32S_WAVES) void gemm_f32_splitk_kernel(GemmAr
   }
 }
 
+// gemm_f32_splitk_kernel for whole tiles: M, N multiples of 32, K of 512 (every wave takes
+// an even number of 32-deep chunks, two per step), a and b with unit inner strides and
+// 16-byte aligned a rows, element offsets within 32 bits.  No bounds checks and 32-bit
+// index arithmetic: at 512^3 the general kernel spends more on its checks and 64-bit
+// offsets (sixteen scalar b loads per chunk and lane) than on its MFMAs.
+__global__ __launch_bounds__(64 * F32S_WAVES) void gemm_f32_splitk_full_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(16))) float part[F32S_WAVES * F32_TM * F32_TN];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tm = blockIdx.x / g.tiles_n, tn = blockIdx.x % g.tiles_n;
+  const int m0 = tm * F32_TM, n0 = tn * F32_TN;
+  const int sa = (int)g.sa_m, sb = (int)g.sb_k;
+  const int r16 = lane & 15, t = lane >> 4;
+  const float* A = (const float*)g.a + (int64_t)m0 * sa + r16 * sa + 8 * t;
+  const float* B = (const float*)g.b + n0 + r16 + 8 * t * sb;
+  const int per = (int)(g.K / (32 * F32S_WAVES));
+  floatx4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int ch = wave * per; ch < (wave + 1) * per; ch += 2) {
+    float a[2][2][8], b[2][2][8];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int kb = (ch + h) * 32;  // plus 8 t, folded into A and B
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const float* p = A + i * 16 * sa + kb;
+        const float4 lo = *(const float4*)p, hi = *(const float4*)(p + 4);
+        a[h][i][0] = lo.x; a[h][i][1] = lo.y; a[h][i][2] = lo.z; a[h][i][3] = lo.w;
+        a[h][i][4] = hi.x; a[h][i][5] = hi.y; a[h][i][6] = hi.z; a[h][i][7] = hi.w;
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int s = 0; s < 8; ++s) b[h][j][s] = B[(kb + s) * sb + j * 16];
+    }
+    // every load of both chunks in flight before the first MFMA: left alone, the
+    // scheduler trades them for registers and waits on each load in turn
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[h][i][s], b[h][j][s], acc[i][j], 0, 0, 0);
+  }
+  float* mine = part + wave * (F32_TM * F32_TN);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) mine[(i * 16 + 4 * t + v) * F32_TN + j * 16 + r16] = acc[i][j][v];
+  __syncthreads();
+#pragma unroll
+  for (int e = tid; e < F32_TM * F32_TN; e += 64 * F32S_WAVES) {
+    float sum = 0.f;
+#pragma unroll
+    for (int w = 0; w < F32S_WAVES; ++w) sum += part[w * (F32_TM * F32_TN) + e];
+    const int64_t row = m0 + e / F32_TN, col = n0 + e % F32_TN;
+    float v = g.alpha * round_through(sum, g.round_dtype);
+    if (g.c) v += g.beta * load_c<false>(g, row * g.sc_m + col * g.sc_n);
+    store_from_float(g.out, row * g.so_m + col * g.so_n, g.out_dtype, v);
+  }
+}
+
 // fp32 GEMMs of more tiles (1024^2 and up) on v_mfma_f32_32x32x2_f32: 256 lanes in a 2 x 2
 // grid of waves, each owning (32 WI) x (32 WJ) of the (64 WI) x (64 WJ) tile.  K in
 // 16-deep chunks, double-buffered in LDS and staged through registers (the next chunk's
@@ -1299,7 +1370,13 @@ static int gemm32_launch(GemmArgs g, hipStream_t stream) {
   // At most two tiles per CU: the split-k kernel (its LDS tile sum replaces a second load phase).
   if (tiles_m * tiles_n <= 512 && g.K >= 64) {
     const bool avec = g.sa_k == 1 && g.sa_m % 4 == 0 && (uintptr_t)g.a % 16 == 0;
-    if (avec)
+    const bool full = avec && g.sb_n == 1 && g.M % F32_TM == 0 && g.N % F32_TN == 0 && g.K % 512 == 0 &&
+                      g.sa_m >= 0 && g.sb_k >= 0 && (g.M - 1) * g.sa_m + g.K < 0x7fffffffLL &&
+                      (g.K - 1) * g.sb_k + g.N < 0x7fffffffLL;
+    if (full)
+      hipLaunchKernelGGL(gemm_f32_splitk_full_kernel, dim3((unsigned)(tiles_m * tiles_n)), dim3(64 * F32S_WAVES), 0,
+                         stream, g);
+    else if (avec)
       hipLaunchKernelGGL(gemm_f32_splitk_kernel<true>, dim3((unsigned)(tiles_m * tiles_n)), dim3(64 * F32S_WAVES), 0, stream, g);
     else
       hipLaunchKernelGGL(gemm_f32_splitk_kernel<false>, dim3((unsigned)(tiles_m * tiles_n)), dim3(64 * F32S_WAVES), 0, stream, g);
