@@ -934,55 +934,68 @@ __global__ __launch_bounds__(64 * F32S_WAVES) void gemm_f32_splitk_kernel(GemmAr
 }
 
 // gemm_f32_splitk_kernel for whole tiles: M, N multiples of 32, K of 512 (every wave takes
-// an even number of 32-deep chunks, two per step), a and b with unit inner strides and
-// 16-byte aligned a rows, element offsets within 32 bits.  No bounds checks and 32-bit
-// index arithmetic: at 512^3 the general kernel spends more on its checks and 64-bit
-// offsets (sixteen scalar b loads per chunk and lane) than on its MFMAs.
+// an even number of 32-deep chunks), a and b with unit inner strides, 16-byte aligned a
+// rows, byte offsets within 32 bits.  The tile is (blockIdx.y, blockIdx.x).  This kernel
+// is latency-bound at 512^3 (a few microseconds, a third of it launch and drain), so it
+// keeps to what shortens the path to the first load and from the last MFMA: no bounds
+// checks, scalar address arithmetic, no division for the tile, and (PLAIN:
+// alpha 1, no c, fp32 out without rounding, unit column stride) a bare store.  K512: K is
+// exactly 512, two chunks per wave without a loop.
+template <bool PLAIN, bool K512>
 __global__ __launch_bounds__(64 * F32S_WAVES) void gemm_f32_splitk_full_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(16))) float part[F32S_WAVES * F32_TM * F32_TN];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int tm = blockIdx.x / g.tiles_n, tn = blockIdx.x % g.tiles_n;
-  const int m0 = tm * F32_TM, n0 = tn * F32_TN;
+  const int m0 = blockIdx.y * F32_TM, n0 = blockIdx.x * F32_TN;
   const int sa = (int)g.sa_m, sb = (int)g.sb_k;
-  const int r16 = lane & 15, t = lane >> 4;
-  const float* A = (const float*)g.a + (int64_t)m0 * sa + r16 * sa + 8 * t;
-  const float* B = (const float*)g.b + n0 + r16 + 8 * t * sb;
-  const int per = (int)(g.K / (32 * F32S_WAVES));
+  const int tid = threadIdx.x, lane = tid & 63, r16 = lane & 15, t = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int per = K512 ? 2 : (int)(g.K / (32 * F32S_WAVES));
+  // Buffer loads: the per-lane part of each offset (voffset) is fixed, the part that
+  // varies from load to load is wave-uniform and goes in soffset, so the scalar unit
+  // computes every address and the vector unit only issues loads and MFMAs.
+  const __amdgpu_buffer_rsrc_t rsA = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)g.a, (short)0, (int)(((g.M - 1) * g.sa_m + g.K) * 4), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsB = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)g.b, (short)0, (int)(((g.K - 1) * g.sb_k + g.N) * 4), 0x00020000);
+  const int va = ((m0 + r16) * sa + 8 * t) * 4, vb = (8 * t * sb + n0 + r16) * 4;
   floatx4 acc[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-  for (int ch = wave * per; ch < (wave + 1) * per; ch += 2) {
+  for (int c0 = 0; c0 < per; c0 += 2) {
     float a[2][2][8], b[2][2][8];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int kb = (ch + h) * 32;  // plus 8 t, folded into A and B
+    for (int c = 0; c < 2; ++c) {
+      const int kb = (wave * per + c0 + c) * 32;  // wave-uniform
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        const float* p = A + i * 16 * sa + kb;
-        const float4 lo = *(const float4*)p, hi = *(const float4*)(p + 4);
-        a[h][i][0] = lo.x; a[h][i][1] = lo.y; a[h][i][2] = lo.z; a[h][i][3] = lo.w;
-        a[h][i][4] = hi.x; a[h][i][5] = hi.y; a[h][i][6] = hi.z; a[h][i][7] = hi.w;
+        const int so = (i * 16 * sa + kb) * 4;
+        const u32x4 lo = __builtin_amdgcn_raw_buffer_load_b128(rsA, va, so, 0);
+        const u32x4 hi = __builtin_amdgcn_raw_buffer_load_b128(rsA, va + 16, so, 0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          a[c][i][q] = __uint_as_float(lo[q]);
+          a[c][i][4 + q] = __uint_as_float(hi[q]);
+        }
       }
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int s = 0; s < 8; ++s) b[h][j][s] = B[(kb + s) * sb + j * 16];
+        for (int s = 0; s < 8; ++s)
+          b[c][j][s] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsB, vb + j * 64, (kb + s) * sb * 4, 0));
+      // the loads in issue order, first chunk then second, all ahead of the MFMAs: left
+      // to itself the scheduler trades them for registers and waits on each in turn
+      __builtin_amdgcn_sched_barrier(0);
     }
-    // every load of both chunks in flight before the first MFMA: left alone, the
-    // scheduler trades them for registers and waits on each load in turn
-    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int c = 0; c < 2; ++c)
 #pragma unroll
       for (int s = 0; s < 8; ++s)
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
           for (int j = 0; j < 2; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[h][i][s], b[h][j][s], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[c][i][s], b[c][j][s], acc[i][j], 0, 0, 0);
   }
   float* mine = part + wave * (F32_TM * F32_TN);
 #pragma unroll
@@ -997,10 +1010,14 @@ __global__ __launch_bounds__(64 * F32S_WAVES) void gemm_f32_splitk_full_kernel(G
     float sum = 0.f;
 #pragma unroll
     for (int w = 0; w < F32S_WAVES; ++w) sum += part[w * (F32_TM * F32_TN) + e];
-    const int64_t row = m0 + e / F32_TN, col = n0 + e % F32_TN;
-    float v = g.alpha * round_through(sum, g.round_dtype);
-    if (g.c) v += g.beta * load_c<false>(g, row * g.sc_m + col * g.sc_n);
-    store_from_float(g.out, row * g.so_m + col * g.so_n, g.out_dtype, v);
+    if (PLAIN) {
+      ((float*)g.out)[(m0 + e / F32_TN) * (int)g.so_m + n0 + e % F32_TN] = sum;
+    } else {
+      const int64_t row = m0 + e / F32_TN, col = n0 + e % F32_TN;
+      float v = g.alpha * round_through(sum, g.round_dtype);
+      if (g.c) v += g.beta * load_c<false>(g, row * g.sc_m + col * g.sc_n);
+      store_from_float(g.out, row * g.so_m + col * g.so_n, g.out_dtype, v);
+    }
   }
 }
 
@@ -1370,13 +1387,24 @@ static int gemm32_launch(GemmArgs g, hipStream_t stream) {
   // At most two tiles per CU: the split-k kernel (its LDS tile sum replaces a second load phase).
   if (tiles_m * tiles_n <= 512 && g.K >= 64) {
     const bool avec = g.sa_k == 1 && g.sa_m % 4 == 0 && (uintptr_t)g.a % 16 == 0;
+    // whole-tile instance: byte offsets of a and b (buffer loads) within 32 bits
     const bool full = avec && g.sb_n == 1 && g.M % F32_TM == 0 && g.N % F32_TN == 0 && g.K % 512 == 0 &&
-                      g.sa_m >= 0 && g.sb_k >= 0 && (g.M - 1) * g.sa_m + g.K < 0x7fffffffLL &&
-                      (g.K - 1) * g.sb_k + g.N < 0x7fffffffLL;
-    if (full)
-      hipLaunchKernelGGL(gemm_f32_splitk_full_kernel, dim3((unsigned)(tiles_m * tiles_n)), dim3(64 * F32S_WAVES), 0,
-                         stream, g);
-    else if (avec)
+                      g.sa_m >= 0 && g.sb_k >= 0 && (g.M - 1) * g.sa_m + g.K < (1LL << 30) &&
+                      (g.K - 1) * g.sb_k + g.N < (1LL << 30);
+    if (full) {
+      const bool plain = !g.c && g.alpha == 1.f && g.out_dtype == NT_DTYPE_F32 && g.round_dtype != NT_DTYPE_F16 &&
+                         g.round_dtype != NT_DTYPE_BF16 &&
+                         g.so_n == 1 && g.so_m >= 0 && (g.M - 1) * g.so_m + g.N < 0x7fffffffLL;
+      const dim3 grid((unsigned)tiles_n, (unsigned)tiles_m), block(64 * F32S_WAVES);
+      if (plain && g.K == 512)
+        hipLaunchKernelGGL((gemm_f32_splitk_full_kernel<true, true>), grid, block, 0, stream, g);
+      else if (plain)
+        hipLaunchKernelGGL((gemm_f32_splitk_full_kernel<true, false>), grid, block, 0, stream, g);
+      else if (g.K == 512)
+        hipLaunchKernelGGL((gemm_f32_splitk_full_kernel<false, true>), grid, block, 0, stream, g);
+      else
+        hipLaunchKernelGGL((gemm_f32_splitk_full_kernel<false, false>), grid, block, 0, stream, g);
+    } else if (avec)
       hipLaunchKernelGGL(gemm_f32_splitk_kernel<true>, dim3((unsigned)(tiles_m * tiles_n)), dim3(64 * F32S_WAVES), 0, stream, g);
     else
       hipLaunchKernelGGL(gemm_f32_splitk_kernel<false>, dim3((unsigned)(tiles_m * tiles_n)), dim3(64 * F32S_WAVES), 0, stream, g);

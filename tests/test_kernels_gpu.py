@@ -508,18 +508,24 @@ def test_gemm_f32(mnk):
     assert torch.allclose(out, ref, atol=1e-4, rtol=1e-4)
 
 
+@pytest.mark.parametrize("plain", (False, True))
 @pytest.mark.parametrize("mnk", ((512, 512, 512), (96, 64, 1024), (32, 32, 2048), (64, 128, 512)))
-def test_gemm_f32_whole_tiles(mnk):
-    # the split-k kernel's whole-tile instance (M, N multiples of 32, K of 512, unit inner
-    # strides, 16-byte aligned a rows): a and b as views of wider rows, c, alpha and beta,
-    # and an output that is a slice of wider rows; against fp64.
+def test_gemm_f32_whole_tiles(mnk, plain):
+    # the split-k kernel's whole-tile instances (M, N multiples of 32, K of 512, unit inner
+    # strides, 16-byte aligned a rows; K exactly 512 or a loop; plain: no c, alpha 1): a and
+    # b as views of wider rows, c, alpha and beta, and an output that is a slice of wider
+    # rows; against fp64.
     m, n, k = mnk
     a = _randn((m, k + 4), torch.float32, 26)[:, :k]
     b = _randn((k, n + 8), torch.float32, 27)[:, :n]
     c = _randn((m, n), torch.float32, 28)
     out = torch.full((m, n + 3), 7.0, device=DEV)
-    kernels.gemm(a, b, out[:, 1:n + 1], c=c, alpha=0.5, beta=2.0)
-    ref = (0.5 * (a.double() @ b.double()) + 2.0 * c.double()).float()
+    if plain:
+        kernels.gemm(a, b, out[:, 1:n + 1])
+        ref = (a.double() @ b.double()).float()
+    else:
+        kernels.gemm(a, b, out[:, 1:n + 1], c=c, alpha=0.5, beta=2.0)
+        ref = (0.5 * (a.double() @ b.double()) + 2.0 * c.double()).float()
     assert torch.allclose(out[:, 1:n + 1], ref, atol=1e-4 * max(1.0, k ** 0.5 / 8), rtol=1e-4)
     assert (out[:, 0] == 7.0).all() and (out[:, n + 1:] == 7.0).all()
 
