@@ -66,7 +66,51 @@ def _args():
                    help="only run the matrix-core ceiling probe (fp16 MFMAs back to back, zero and random operands)")
     p.add_argument("--ceiling-iters", type=int, default=400_000,
                    help="loop iterations of the ceiling probe (8 MFMAs per wave each)")
+    p.add_argument("--trace-summary", default="",
+                   help="only summarise a rocprofv3 --kernel-trace CSV of one configuration (--only) run with the "
+                        "same --warmup/--steps: per-kernel durations over the K timed steps (no GPU used)")
     return p.parse_args()
+
+
+def _trace_summary(args):
+    """Markdown rows for one configuration's rocprofv3 kernel trace (a run of this script with
+    --only <config> --no-graph and the same --warmup W and --steps K).  Each kernel of a step
+    is dispatched once per call, so its dispatches W .. W+K-1 in start order are the K timed
+    steps; mean, median, min and max are over those.  A kernel with fewer than W+K dispatches
+    ran while the configuration was built (e.g. torch's dtype conversions of the inputs): it
+    is listed, but left out of ``frac (profile)`` = work / (sum of the step kernels' means) / peak."""
+    import csv
+    import statistics
+
+    import torch
+    import ninetoothed_amd as ninetoothed
+    import programs as pg
+
+    (cfg,) = [c for c in _configs(torch, ninetoothed, pg) if c["name"] == args.only]
+    spans = {}
+    with open(args.trace_summary, newline="") as f:
+        for r in csv.DictReader(f):
+            spans.setdefault(r["Kernel_Name"], []).append((int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
+    w, k = args.warmup, args.steps
+    rows, total = [], 0.0
+    for name, d in spans.items():
+        d.sort()
+        short = name.split("(")[0] if name.startswith(("nt::", "void nt::")) else name[:90]
+        if len(d) >= w + k:
+            us = [(e - s) / 1e3 for s, e in d[w:w + k]]
+            mean = statistics.fmean(us)
+            total += mean
+            rows.append((short, len(d), f"{mean:.2f}", f"{statistics.median(us):.2f}", f"{min(us):.2f}",
+                         f"{max(us):.2f}", "step"))
+        else:
+            us = [(e - s) / 1e3 for s, e in d]
+            rows.append((short, len(d), f"{statistics.fmean(us):.2f}", f"{statistics.median(us):.2f}",
+                         f"{min(us):.2f}", f"{max(us):.2f}", "setup (not a step)"))
+    frac = cfg["work"] / (total * 1e-6) / cfg["peak"] if total else float("nan")
+    for i, (short, n, mean, med, lo, hi, role) in enumerate(rows):
+        head = f"| {cfg['name']} " if i == 0 else "| "
+        tail = f"| {frac:.3f} |" if i == 0 else "| |"
+        print(f"{head}| `{short}` | {role} | {n} | {mean} | {med} | {lo} | {hi} {tail}")
 
 
 def _sets(set_bytes):
@@ -439,6 +483,9 @@ def main():
               "(the hot path runs on one GPU: every family is data-parallel over independent output units, "
               "so one process per GPU would each take a shard of them).", file=sys.stderr)
         sys.exit(2)
+    if args.trace_summary:
+        _trace_summary(args)
+        return
     import torch
 
     if args.calibrate_copy:

@@ -40,6 +40,11 @@ struct ConvArgs {
   int qvec;    // Q % 8 == 0 and y's q stride 1: 8 consecutive positions are one 16-byte run
   int y_dtype, round_dtype;
   int tiles_k, tiles_m;
+  // Reduction order of the re-laid filter (and of the k-tiles that walk it): 1 for the DMA
+  // kernels, (c / 32, r, s, c % 32), so that the nine taps of one 32-channel block come in
+  // consecutive k-tiles and a workgroup's input rows for that block stay in L2 while they
+  // are re-read; 0 for conv_nhwc_kernel, (r, s, c).
+  int cb_order;
 };
 
 // Workgroups are dispatched to the eight XCDs round-robin (b to XCD b % 8), each XCD with
@@ -164,8 +169,8 @@ __global__ __launch_bounds__(C_THREADS) void conv_direct_kernel(ConvArgs g) {
 
 // ----------------------------------------------------------------------------- N-H-W-C path
 // With a workspace the input is re-laid as zero-padded N-Hp-Wp-C (Hp = H + 2ph, Wp = W + 2pw)
-// and the filter as K-R-S-C.  Reduction index kk = (r*S + s)*C + c then walks channels
-// contiguously, so for a 64-deep k-tile inside one (r, s) every im2col row and every
+// and the filter as K-R-S-C (for the DMA kernels K-(C/32)-R-S-32: ConvArgs::cb_order).
+// Reduction index kk = (r*S + s)*C + c then walks channels contiguously, so for a 64-deep k-tile inside one (r, s) every im2col row and every
 // filter row is 128 contiguous bytes: both operands load with 16-byte loads straight
 // into the k-contiguous LDS layout of the MFMA core, no gathers, no transposes, no
 // padding tests.  Needs C % 64 == 0.  Cost of the re-layout: one read and one write of
@@ -226,8 +231,10 @@ __global__ __launch_bounds__(256) void filter_krsc_kernel(const uint16_t* __rest
     const int64_t s = row % g.S, t = row / g.S;
     const int64_t r = t % g.R, k = t / g.R;
     const uint16_t* src = w + k * g.ws[0] + r * g.ws[2] + s * g.ws[3];
-    uint16_t* dst = wt + row * g.C;
-    for (int64_t c = threadIdx.x; c < g.C; c += blockDim.x) dst[c] = c < g.Cr ? src[c * g.ws[1]] : (uint16_t)0;
+    uint16_t* dst = g.cb_order ? wt + k * g.KG + (r * g.S + s) * 32 : wt + row * g.C;
+    const int64_t cb_step = g.R * g.S * 32;
+    for (int64_t c = threadIdx.x; c < g.C; c += blockDim.x)
+      dst[g.cb_order ? (c >> 5) * cb_step + (c & 31) : c] = c < g.Cr ? src[c * g.ws[1]] : (uint16_t)0;
   }
 }
 
@@ -236,7 +243,7 @@ __global__ __launch_bounds__(256) void filter_krsc_kernel(const uint16_t* __rest
 // go one per lane: eight 16-byte loads along w (one per channel), an 8 x 8 transpose of
 // 16-bit values with v_perm_b32, eight 16-byte stores along c (one per position).  Needs
 // unit w stride, 16-byte aligned input rows and W % 8 == 0.  Workgroups past N * Hp:
-// the filter into K-R-S-C, one (k, r, s) row of C channels at a time.
+// the filter into K-R-S-C (or K-(C/32)-R-S-32), one (k, r, s) row of C channels at a time.
 // STAGE (C * W * 2 <= RELAYOUT_STAGE_BYTES): lanes along w for the loads (each load
 // instruction reads runs of one channel row), the transposed chunks into LDS in the output
 // row's order, 16-byte chunk (pos, cb) at pos * C/8 + (cb ^ (pos / 8 & mask)) (mask < 8
@@ -259,8 +266,10 @@ __global__ __launch_bounds__(256) void conv_relayout_kernel(const uint16_t* __re
       const int64_t s = row % g.S, t = row / g.S;
       const int64_t r = t % g.R, k = t / g.R;
       const uint16_t* src = w + k * g.ws[0] + r * g.ws[2] + s * g.ws[3];
-      uint16_t* dst = wt + row * g.C;
-      for (int64_t c = tid; c < g.C; c += 256) dst[c] = c < g.Cr ? src[c * g.ws[1]] : (uint16_t)0;
+      uint16_t* dst = g.cb_order ? wt + k * g.KG + (r * g.S + s) * 32 : wt + row * g.C;
+      const int64_t cb_step = g.R * g.S * 32;
+      for (int64_t c = tid; c < g.C; c += 256)
+        dst[g.cb_order ? (c >> 5) * cb_step + (c & 31) : c] = c < g.Cr ? src[c * g.ws[1]] : (uint16_t)0;
     }
     return;
   }
@@ -325,6 +334,108 @@ __global__ __launch_bounds__(256) void conv_relayout_kernel(const uint16_t* __re
 #pragma unroll
       for (int j = 0; j < 8; ++j) *(u32x4*)(out_row + (g.pw + wb * 8 + j) * C + cb * 8) = out[j];
     }
+  }
+}
+
+// The filter into K-R-S-C, or K-(C/32)-R-S-32 (cb_order), for conv_relayout_pipe_kernel:
+// one output channel k per workgroup and step, lanes along the destination row (coalesced
+// stores), loads gathered from any strides.
+__device__ __forceinline__ void relayout_filter_rows(const uint16_t* __restrict__ w, uint16_t* __restrict__ wt,
+                                                     const ConvArgs& g, int64_t first, int64_t step) {
+  const int RS = (int)(g.R * g.S), S = (int)g.S, C = (int)g.C, KG = (int)g.KG, Cr = (int)g.Cr;
+  for (int64_t k = first; k < g.K; k += step) {
+    const uint16_t* src = w + k * g.ws[0];
+    uint16_t* dst = wt + k * g.KG;
+    for (int d = threadIdx.x; d < KG; d += blockDim.x) {
+      int c, rs;
+      if (g.cb_order) {
+        const int cb = d / (RS * 32), rem = d - cb * RS * 32;
+        rs = rem >> 5;
+        c = cb * 32 + (rem & 31);
+      } else {
+        rs = d / C;
+        c = d - rs * C;
+      }
+      const int r = rs / S, s = rs - r * S;
+      dst[d] = c < Cr ? src[c * g.ws[1] + r * g.ws[2] + s * g.ws[3]] : (uint16_t)0;
+    }
+  }
+}
+
+// conv_relayout_kernel's STAGE form for rows of at most 256 8 x 8 blocks (one per lane),
+// with fewer workgroups than rows: workgroup b takes rows b, b + row_blocks, ... (in
+// xcd_order) and issues the loads of its next row before it transposes, stages and stores
+// the current one, so each CU reads and writes at once.  With one workgroup per row, all of
+// them resident, the GPU read every row before it wrote any: 10.9 us for the rows of
+// [16,256,56,56] against 53.6 MB moved.  Workgroups from row_blocks on re-lay the filter,
+// one output channel at a time (one workgroup per filter row (k, r, s) took 5.3 us alone).
+template <typename T>
+__global__ __launch_bounds__(256) void conv_relayout_pipe_kernel(const uint16_t* __restrict__ x,
+                                                                 uint16_t* __restrict__ xp,
+                                                                 const uint16_t* __restrict__ w,
+                                                                 uint16_t* __restrict__ wt, ConvArgs g, int64_t Hp,
+                                                                 int64_t Wp, int row_blocks) {
+  const int tid = threadIdx.x;
+  if ((int)blockIdx.x >= row_blocks) {
+    relayout_filter_rows(w, wt, g, (int)blockIdx.x - row_blocks, (int)gridDim.x - row_blocks);
+    return;
+  }
+  __shared__ __attribute__((aligned(16))) u32x4 stage[RELAYOUT_STAGE_BYTES / 16];
+  const int64_t rows = g.N * Hp;
+  const int64_t C = g.C, W = g.W;
+  const int cc = (int)(C / 8), wbk = (int)(W / 8);
+  const int mask = cc % 8 == 0 ? 7 : cc % 4 == 0 ? 3 : cc % 2 == 0 ? 1 : 0;
+  const bool active = tid < cc * wbk;
+  const int cb = active ? tid / wbk : 0, wb = active ? tid - cb * wbk : 0;
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+  // Loads of row `it` (xcd_order) into `in`: this lane's 8 (channel) x 8 (w) block.
+  auto load = [&](int64_t it, u32x4 (&in)[8]) {
+    const int64_t rb = xcd_order(it, rows);
+    const int64_t hp = rb % Hp, n = rb / Hp, h = hp - g.ph;
+    if (!active || h < 0 || h >= g.H) return;
+    const uint16_t* xb = x + n * g.xs[0] + h * g.xs[2] + wb * 8;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) in[i] = cb * 8 + i < g.Cr ? *(const u32x4*)(xb + (cb * 8 + i) * g.xs[1]) : zero;
+  };
+  // Row `it` from `cur`, after issuing the loads of row it + row_blocks into `nxt`.
+  auto step = [&](int64_t it, u32x4 (&cur)[8], u32x4 (&nxt)[8]) {
+    if (it + row_blocks < rows) load(it + row_blocks, nxt);
+    const int64_t rb = xcd_order(it, rows);
+    const int64_t hp = rb % Hp, n = rb / Hp, h = hp - g.ph;
+    uint16_t* out_row = xp + ((n * Hp + hp) * Wp) * C;
+    if (h < 0 || h >= g.H) {  // a pad row (workgroup-uniform)
+      for (int64_t e = tid; e < Wp * cc; e += 256) *(u32x4*)(out_row + e * 8) = zero;
+      return;
+    }
+    for (int64_t e = tid; e < (Wp - W) * cc; e += 256) {  // pad columns
+      const int64_t col = e / cc, ch = e % cc;
+      const int64_t wp = col < g.pw ? col : col + W;
+      *(u32x4*)(out_row + wp * C + ch * 8) = zero;
+    }
+    if (active) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int d = j >> 1;
+        const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+        stage[(wb * 8 + j) * cc + (cb ^ (wb & mask))] =
+            u32x4{__builtin_amdgcn_perm(cur[1][d], cur[0][d], sel), __builtin_amdgcn_perm(cur[3][d], cur[2][d], sel),
+                  __builtin_amdgcn_perm(cur[5][d], cur[4][d], sel), __builtin_amdgcn_perm(cur[7][d], cur[6][d], sel)};
+      }
+    }
+    __syncthreads();
+    u32x4* dst = (u32x4*)(out_row + g.pw * C);  // positions pw .. pw + W - 1: W * C/8 chunks in a row
+    for (int k = tid; k < (int)W * cc; k += 256) {
+      const int pos = k / cc, c8 = k - pos * cc;
+      dst[k] = stage[pos * cc + (c8 ^ ((pos >> 3) & mask))];
+    }
+    __syncthreads();  // the stage is rewritten by the next row
+  };
+  u32x4 a[8], b[8];
+  int64_t it = blockIdx.x;
+  if (it < rows) load(it, a);
+  for (; it < rows; it += 2 * (int64_t)row_blocks) {
+    step(it, a, b);
+    if (it + row_blocks < rows) step(it + row_blocks, b, a);
   }
 }
 
@@ -476,9 +587,9 @@ __global__ __launch_bounds__(512) void conv_nhwc_kernel(const uint16_t* __restri
 // filled by buffer_load ... lds from inline assembly (tile kt+3 into the stage of tile
 // kt-1, one barrier per k-tile, no register staging).  Both operands are stored [row][k]
 // in 64-byte rows whose 16-byte chunks are XOR-swizzled by (row / 4) % 4 and read with
-// ds_read_b128: a = filter rows (K-R-S-C), b = im2col rows of the padded N-H-W-C input,
-// addressed by a per-lane base offset plus one scalar (r, s, c0) offset per k-tile (a
-// k-tile of 32 channels never crosses an (r, s) block: C % 32 == 0); rows past M point
+// ds_read_b128: a = filter rows (K-(C/32)-R-S-32), b = im2col rows of the padded N-H-W-C
+// input, addressed by a per-lane base offset plus one scalar (channel block, r, s) offset
+// per k-tile (C % 32 == 0: a k-tile is one tap of one 32-channel block); rows past M point
 // past the end of the resource and read zeros.  Epilogue: 16-row halves of each wave's
 // accumulators staged in its own 4 KiB of LDS, each lane storing 8 consecutive
 // positions of one channel (their (n, p, q) computed once).
@@ -533,12 +644,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       vx[q] = (int)x_bytes;
     }
   }
-  // Scalar byte offset of k-tile kt inside an im2col row: (r, s) block and channel c0.
+  // Scalar byte offset of k-tile kt inside an im2col row: channel block cb, tap (r, s).
   auto x_off = [&](int kt) {
-    const int kk0 = kt * 32;
-    const int rs = kk0 / C, c0 = kk0 - rs * C;
+    const int taps = (int)(g.R * g.S);
+    const int cb = kt / taps, rs = kt - cb * taps;
     const int r = rs / (int)g.S, s = rs - r * (int)g.S;
-    return ((r * (int)g.dh * (int)Wp + s * (int)g.dw) * C + c0) * 2;
+    return ((r * (int)g.dh * (int)Wp + s * (int)g.dw) * C + cb * 32) * 2;
   };
   // Load u (0..3) of tile kt into its stage: filter q0, im2col q0, filter q1, im2col q1.
   auto load_unit = [&](int u, int kt, int xo) {
@@ -734,6 +845,224 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     finish(std::integral_constant<int, NT_DTYPE_NONE>{});
 }
 
+// conv_dma_kernel with tiles of 224 positions (seven 32-position blocks) by 256 channels,
+// for outputs whose 256 x 256 tiles leave CUs idle: [16,256,56,56] has 196 such tiles for
+// 256 CUs, and 224 of these.  Waves w and w + 4 of a workgroup run on one SIMD; wave w
+// (0..3) takes channels 64 w .. 64 w + 63 and positions 0..127 of the tile, wave w + 4
+// the same channels and positions 128..223, so each SIMD issues 8 + 6 MFMAs per 16-deep
+// slice where a 256 x 256 tile takes 16: the workgroup's time scales with its 224
+// positions.  Loads, ring, waits and barriers are conv_dma_kernel's (rows 224..255 of the
+// position operand read zeros); each wave's body is compiled for its own block count, so
+// neither carries a branch per MFMA.  No split reduction.
+constexpr int CB_M224 = 224;
+template <typename T>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void conv_dma224_kernel(
+    const uint16_t* __restrict__ xp, const uint16_t* __restrict__ wt, ConvArgs g, int64_t Hp, int64_t Wp) {
+  __shared__ __attribute__((aligned(1024))) char lds[cdma::EPI + 8 * 4096];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tile = (int)blockIdx.x;
+  const int tk = tile % g.tiles_k, tmi = tile / g.tiles_k;
+  const int k0t = tk * CB_K, m0t = tmi * CB_M224;
+  const int KG = (int)g.KG, C = (int)g.C;
+  const int nkt = KG / 32;
+
+  const u32x4 rsW = cdma::rsrc(wt + (int64_t)k0t * KG, (uint32_t)((g.K - k0t) * KG * 2));
+  const uint32_t x_bytes = (uint32_t)(g.N * Hp * Wp * g.C * 2);
+  const u32x4 rsX = cdma::rsrc(xp, x_bytes);
+  int vw[2], vx[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int row = 32 * wave + 16 * q + (lane >> 2);
+    const int ch = cdma::asw(row, lane & 3);
+    vw[q] = (row * KG + ch * 8) * 2;
+    const int m = m0t + row;
+    if (row < CB_M224 && m < g.M) {
+      const int qq = m % (int)g.Q, t = m / (int)g.Q;
+      const int p = t % (int)g.P, n = t / (int)g.P;
+      vx[q] = (((n * (int)Hp + p * (int)g.sh) * (int)Wp + qq * (int)g.sw) * C + ch * 8) * 2;
+    } else {
+      vx[q] = (int)x_bytes;
+    }
+  }
+  auto x_off = [&](int kt) {
+    const int taps = (int)(g.R * g.S);
+    const int cb = kt / taps, rs = kt - cb * taps;
+    const int r = rs / (int)g.S, s = rs - r * (int)g.S;
+    return ((r * (int)g.dh * (int)Wp + s * (int)g.dw) * C + cb * 32) * 2;
+  };
+  auto load_unit = [&](int u, int kt, int xo) {
+    const int st = (kt & 3) * cdma::STAGE, q = u >> 1;
+    if ((u & 1) == 0)
+      cdma::load_lds16(rsW, lds0 + st + 2048 * wave + 1024 * q, vw[q], kt * 64);
+    else
+      cdma::load_lds16(rsX, lds0 + cdma::B0 + st + 2048 * wave + 1024 * q, vx[q], xo);
+  };
+  const int wk = wave & 3, wm = wave >> 2;
+  uint16_t* Y = (uint16_t*)g.y;
+
+  auto body = [&](auto nb_c) {
+    constexpr int NB = decltype(nb_c)::value;  // 32-position blocks of this wave
+    // Fragment rows: channels 64 wk + 32 i + lane % 32, positions 128 wm + 32 j + lane % 32.
+    int a_rd[2], b_rd[2];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const int ra = wk * 64 + (lane & 31), rb = wm * 128 + (lane & 31);
+      a_rd[s2] = ra * 64 + cdma::asw(ra, 2 * s2 + (lane >> 5)) * 16;
+      b_rd[s2] = cdma::B0 + rb * 64 + cdma::asw(rb, 2 * s2 + (lane >> 5)) * 16;
+    }
+    typedef typename mfma_traits<T>::frag frag;
+    frag fa[2][2], fb[2][NB];
+    // Unit u (0..NB+1) of slice s2 at stage offset st, in the order the slice's MFMAs
+    // (channel block x / NB, position block x % NB) consume them: a0, b0 .. b(NB-1), a1.
+    auto read_unit = [&](int u, int s2, int st) {
+      if (u == 0)
+        fa[s2][0] = *(const frag*)(lds + a_rd[s2] + st);
+      else if (u == NB + 1)
+        fa[s2][1] = *(const frag*)(lds + a_rd[s2] + st + 2048);
+      else
+        fb[s2][u - 1] = *(const frag*)(lds + b_rd[s2] + st + (u - 1) * 2048);
+    };
+    floatx16 acc[2][NB];
+    zero_acc(acc);
+    for (int kt = 0; kt < 3; ++kt) {
+      const int xo = x_off(kt);
+      for (int u = 0; u < 4; ++u) load_unit(u, kt, xo);
+    }
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+#pragma unroll
+    for (int u = 0; u < NB + 2; ++u) read_unit(u, 0, 0);
+
+#define NT_CFENCE() __builtin_amdgcn_sched_barrier(0)
+    auto step = [&](auto has1_c, auto load_c, auto vm_c, int kt) {
+      constexpr bool HAS1 = decltype(has1_c)::value, LOAD = decltype(load_c)::value;
+      constexpr int VM = decltype(vm_c)::value;
+      const int st = (kt & 3) * cdma::STAGE, st1 = ((kt + 1) & 3) * cdma::STAGE;
+      const int xo3 = LOAD ? x_off(kt + 3) : 0;
+      static_for<0, 4 * NB>([&](auto m_c) {
+        constexpr int m = decltype(m_c)::value;
+        constexpr int s2 = m / (2 * NB), x = m % (2 * NB);
+        if constexpr (m == 2 * NB && VM >= 0) {
+          NT_CFENCE();
+          if constexpr (VM == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+          if constexpr (VM == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+          __builtin_amdgcn_s_barrier();
+          NT_CFENCE();
+        }
+        acc[x / NB][x % NB] = mfma_traits<T>::mma(fa[s2][x / NB], fb[s2][x % NB], acc[x / NB][x % NB]);
+        NT_CFENCE();
+        if constexpr (x < NB + 2) {
+          if constexpr (s2 == 0)
+            read_unit(x, 1, st);
+          else if constexpr (HAS1)
+            read_unit(x, 0, st1);
+        }
+        if constexpr (s2 == 1 && LOAD && x < 4) load_unit(x, kt + 3, xo3);
+        NT_CFENCE();
+      });
+    };
+#undef NT_CFENCE
+    using T1 = std::integral_constant<bool, true>;
+    using F1 = std::integral_constant<bool, false>;
+    using V4 = std::integral_constant<int, 4>;
+    using V0 = std::integral_constant<int, 0>;
+    using VN = std::integral_constant<int, -1>;
+    int kt = 0;
+    for (; kt + 3 < nkt; ++kt) step(T1{}, T1{}, V4{}, kt);
+    step(T1{}, F1{}, V4{}, kt);
+    step(T1{}, F1{}, V0{}, kt + 1);
+    step(F1{}, F1{}, VN{}, kt + 2);
+
+    // Epilogue, per 64-position half (blocks 2 ph, 2 ph + 1) of the wave's positions: each
+    // 16-channel half of a channel block staged in the wave's 4 KiB, each lane storing 8
+    // consecutive positions (columns (lane % 8) * 8 .. + 7) of one channel.
+    float* stage = (float*)(lds + cdma::EPI + wave * 4096);
+    const int cg = (lane & 7) * 8;
+    auto finish = [&](auto round_c) {
+      constexpr int ROUND = decltype(round_c)::value;
+      static_for<0, (NB + 1) / 2>([&](auto ph_c) {
+        constexpr int ph = decltype(ph_c)::value;
+        constexpr int JN = NB - 2 * ph < 2 ? NB - 2 * ph : 2;  // blocks in this half
+        const int mpos = m0t + wm * 128 + ph * 64 + cg;
+        const bool m_ok = cg < JN * 32 && mpos < g.M;
+        int64_t ybase = 0;
+        int64_t yoff[8];
+        uint32_t yvalid = 0;
+        if (m_ok) {
+          const int q = mpos % (int)g.Q, t = mpos / (int)g.Q;
+          const int p = t % (int)g.P, n = t / (int)g.P;
+          ybase = n * g.ys[0] + p * g.ys[2] + q;
+        }
+        if (!g.qvec) {
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const int64_t m = mpos + u;
+            const int64_t q = m % g.Q, t = m / g.Q;
+            yoff[u] = (t / g.P) * g.ys[0] + (t % g.P) * g.ys[2] + q * g.ys[3];
+            yvalid |= (m < g.M ? 1u : 0u) << u;
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            wave_lds_order();  // the previous half's reads come first
+#pragma unroll
+            for (int jj = 0; jj < JN; ++jj)
+#pragma unroll
+              for (int r = 8 * h; r < 8 * h + 8; ++r)
+                stage[(acc_row(r, lane) - 16 * h) * 64 + jj * 32 + (lane & 31)] = acc[i][2 * ph + jj][r];
+            wave_lds_order();  // every lane's writes before any lane reads
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+              const int rr = t * 8 + (lane >> 3);
+              const int k = k0t + wk * 64 + i * 32 + h * 16 + rr;
+              const float4 v0 = *(const float4*)(stage + rr * 64 + cg);
+              const float4 v1 = *(const float4*)(stage + rr * 64 + cg + 4);
+              const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+              u32x4 ow;
+#pragma unroll
+              for (int d = 0; d < 4; ++d) {
+                float a = v[2 * d], b = v[2 * d + 1];
+                if constexpr (ROUND == NT_DTYPE_F16) {
+                  a = f16_bits_to_float(float_to_f16_bits(a));
+                  b = f16_bits_to_float(float_to_f16_bits(b));
+                }
+                if constexpr (ROUND == NT_DTYPE_BF16) {
+                  a = bf16_bits_to_float(float_to_bf16_bits(a));
+                  b = bf16_bits_to_float(float_to_bf16_bits(b));
+                }
+                ow[d] = (uint32_t)elem<T>::from_float(a) | ((uint32_t)elem<T>::from_float(b) << 16);
+              }
+              if (m_ok && k < g.K) {
+                if (g.qvec) {
+                  __builtin_nontemporal_store(ow, (u32x4*)(Y + ybase + (int64_t)k * g.ys[1]));
+                } else {
+#pragma unroll
+                  for (int u = 0; u < 8; ++u)
+                    if ((yvalid >> u) & 1u)
+                      Y[yoff[u] + (int64_t)k * g.ys[1]] = (uint16_t)(ow[u >> 1] >> (16 * (u & 1)));
+                }
+              }
+            }
+          }
+      });
+    };
+    if (g.round_dtype == NT_DTYPE_F16)
+      finish(std::integral_constant<int, NT_DTYPE_F16>{});
+    else if (g.round_dtype == NT_DTYPE_BF16)
+      finish(std::integral_constant<int, NT_DTYPE_BF16>{});
+    else
+      finish(std::integral_constant<int, NT_DTYPE_NONE>{});
+  };
+  if (wm == 0)
+    body(std::integral_constant<int, 4>{});
+  else
+    body(std::integral_constant<int, 3>{});
+}
+
 // Sum of conv_dma_kernel's split partials: one lane per 8 consecutive output positions of
 // one channel, rounded and stored as one 16-byte vector when they share an output row
 // (qvec), else element by element.
@@ -819,8 +1148,9 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
                        int config = 0) {
   // config: 0 = the fastest path whose conditions hold; 1 = re-laid input through the DMA
   // kernel, 2 = re-laid input through conv_nhwc_kernel, 3 = the direct kernel (no
-  // workspace).  A forced path whose conditions do not hold is rejected before launching.
-  if (config < 0 || config > 3) return NT_ERR_INVALID;
+  // workspace), 4 = re-laid input through the DMA kernel of 224-position tiles.  A forced
+  // path whose conditions do not hold is rejected before launching.
+  if (config < 0 || config > 4) return NT_ERR_INVALID;
   if (N < 0 || C < 0 || H < 0 || W < 0 || K < 0 || R < 0 || S < 0 || P < 0 || Q < 0 || ph < 0 || pw < 0 || sh <= 0 ||
       sw <= 0 || dh <= 0 || dw <= 0)
     return NT_ERR_INVALID;
@@ -869,14 +1199,21 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
   // (an empty filter, R or S zero, sums nothing: the direct kernel writes the zeros)
   const bool nhwc = config != 3 && R * S > 0 && workspace != nullptr && workspace_bytes >= need && (uintptr_t)workspace % 256 == 0 &&
                     (P - 1) * sh + (R - 1) * dh < Hp && (Q - 1) * sw + (S - 1) * dw < Wp;
-  if ((config == 1 && !(nhwc && dma)) || (config == 2 && !nhwc)) return NT_ERR_INVALID;
+  if (((config == 1 || config == 4) && !(nhwc && dma)) || (config == 2 && !nhwc)) return NT_ERR_INVALID;
   if (nhwc) {
     g.C = Cl;
     g.KG = Cl * R * S;
+    g.cb_order = dma ? 1 : 0;
     // Few output tiles: the DMA kernel splits the reduction, partials after the re-layout.
     const int64_t part_at = cdiv(need, 256) * 256;
     int64_t per = g.KG / 32;
-    const int64_t sp = dma ? conv_splits(tiles_k * tiles_m, g.KG / 32, K, g.Mp, workspace_bytes - part_at, &per) : 1;
+    const int64_t sp = dma && config != 4 ? conv_splits(tiles_k * tiles_m, g.KG / 32, K, g.Mp, workspace_bytes - part_at, &per) : 1;
+    // 224-position tiles when, without a split, they leave fewer CUs idle: per CU and round
+    // of 256 workgroups, a workgroup's time goes with its positions (224 or 256).
+    const int64_t tiles_m224 = cdiv(g.M, CB_M224);
+    const bool m224 = dma && sp == 1 && tiles_k * tiles_m224 <= 0x7fffffffLL &&
+                      (config == 4 || (config == 0 && cdiv(tiles_k * tiles_m224, 256) * 224 * 100 <
+                                                          cdiv(tiles_k * tiles_m, 256) * 256 * 97));
     g.splits = (int)sp;
     g.kt_per = (int)per;
     g.part = sp > 1 ? (float*)((char*)workspace + part_at) : nullptr;
@@ -886,7 +1223,12 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
     if (fblocks > 4096) fblocks = 4096;
     const bool fast_relayout = xs[3] == 1 && W % 8 == 0 && (uintptr_t)x % 16 == 0 && (xs[0] * 2) % 16 == 0 &&
                                (xs[1] * 2) % 16 == 0 && (xs[2] * 2) % 16 == 0;
-    if (fast_relayout) {
+    if (fast_relayout && Cl * W * 2 <= RELAYOUT_STAGE_BYTES && (Cl / 8) * (W / 8) <= 256) {
+      // rows in workgroups that each take several, two per CU; the filter one channel k at a time
+      const int64_t row_blocks = N * Hp < 512 ? N * Hp : 512, kblocks = K < 256 ? K : 256;
+      hipLaunchKernelGGL(conv_relayout_pipe_kernel<T>, dim3((unsigned)(row_blocks + kblocks)), dim3(256), 0, stream,
+                         (const uint16_t*)x, xp, (const uint16_t*)w, wt, g, Hp, Wp, (int)row_blocks);
+    } else if (fast_relayout) {
       if (N * Hp + fblocks > 0x7fffffffLL) return NT_ERR_INVALID;
       if (Cl * W * 2 <= RELAYOUT_STAGE_BYTES)
         hipLaunchKernelGGL((conv_relayout_kernel<T, true>), dim3((unsigned)(N * Hp + fblocks)), dim3(256), 0, stream,
@@ -902,7 +1244,11 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
       hipLaunchKernelGGL(filter_krsc_kernel<T>, dim3((unsigned)fblocks), dim3(256), 0, stream, (const uint16_t*)w, wt,
                          g);
     }
-    if (dma) {
+    if (m224) {
+      g.tiles_m = (int)tiles_m224;
+      hipLaunchKernelGGL(conv_dma224_kernel<T>, dim3((unsigned)(tiles_k * tiles_m224)), dim3(512), 0, stream,
+                         (const uint16_t*)xp, (const uint16_t*)wt, g, Hp, Wp);
+    } else if (dma) {
       hipLaunchKernelGGL(conv_dma_kernel<T>, dim3((unsigned)(sp * tiles_k * tiles_m)), dim3(512), 0, stream,
                          (const uint16_t*)xp, (const uint16_t*)wt, g, Hp, Wp);
       if (sp > 1) {

@@ -583,6 +583,8 @@ def test_conv2d_relayout_strided_ragged_bf16():
     ((2, 128, 33, 31), (64, 3, 3), (2, 2), (2, 2), (2, 2)),
     ((1, 64, 9, 45), (320, 1, 2), (0, 1), (1, 3), (1, 1)),
     ((2, 64, 12, 24), (96, 3, 1), (1, 0), (1, 1), (1, 1)),
+    # 1,664 padded input rows: the re-layout's workgroups take three or four rows each
+    ((64, 64, 24, 24), (64, 3, 3), (1, 1), (1, 1), (1, 1)),
 ))
 def test_conv2d_relayout_dma(case, dtype):
     (n, c, h, w_), (k, r, s), padding, stride, dilation = case
@@ -596,10 +598,10 @@ def test_conv2d_relayout_dma(case, dtype):
     assert torch.allclose(y.float(), ref.to(torch.float16).float(), atol=2e-2, rtol=1e-2)
 
 
-@pytest.mark.parametrize("config", (1, 2, 3))
+@pytest.mark.parametrize("config", (1, 2, 3, 4))
 def test_conv2d_paths(config):
-    # Each forced path (re-laid + DMA kernel, re-laid + N-H-W-C kernel, direct kernel) on a
-    # call all three admit.
+    # Each forced path (re-laid + DMA kernel, re-laid + N-H-W-C kernel, direct kernel,
+    # re-laid + DMA kernel of 224-position tiles) on a call all four admit.
     x = _randn((2, 64, 16, 16), torch.float16, 60)
     w = _randn((96, 64, 3, 3), torch.float16, 61, 1.0 / math.sqrt(64 * 9))
     y = torch.empty((2, 96, 16, 16), dtype=torch.float16, device=DEV)
@@ -677,8 +679,48 @@ def test_conv2d_dma_any_q(case, dtype):
     assert torch.allclose(y.float(), ref, atol=2e-2, rtol=1e-2)
 
 
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+@pytest.mark.parametrize("case", (
+    # (N, C, H, W), (K, R, S), padding, stride, dilation through the DMA kernel of 224-position
+    # tiles: M = N*P*Q no multiple of 224 (the last tile's upper waves wholly past M), K no
+    # multiple of 256, the shortest pipeline (3 k-tiles), Q % 8 != 0 (element-by-element
+    # stores), stride and dilation
+    ((3, 128, 20, 16), (200, 3, 3), (1, 1), (1, 1), (1, 1)),
+    ((2, 64, 12, 24), (96, 3, 1), (1, 0), (1, 1), (1, 1)),
+    ((1, 32, 9, 45), (320, 1, 3), (0, 1), (1, 1), (1, 1)),
+    ((32, 128, 28, 28), (128, 3, 3), (1, 1), (1, 1), (1, 1)),
+    ((16, 64, 15, 17), (300, 3, 3), (1, 1), (2, 2), (1, 1)),
+    ((2, 128, 33, 31), (64, 3, 3), (2, 2), (2, 2), (2, 2)),
+))
+def test_conv2d_dma224(case, dtype):
+    (n, c, h, w_), (k, r, s), padding, stride, dilation = case
+    x = _randn((n, c, h, w_), dtype, 41)
+    w = _randn((k, c, r, s), dtype, 42, 1.0 / math.sqrt(c * r * s))
+    ref = F.conv2d(x.float(), w.float(), padding=padding, stride=stride, dilation=dilation)
+    y = torch.full(ref.shape, 7.0, dtype=dtype, device=DEV)
+    kernels.conv2d(x, w, y, padding=padding, stride=stride, dilation=dilation, workspace=_workspace(x, w, padding),
+                   config=4)
+    assert torch.allclose(y.float(), ref, atol=2e-2, rtol=1e-2)
+
+
+def test_conv2d_headline_takes_224_tiles():
+    # [16,256,56,56] * [256,256,3,3]: 196 tiles of 256 positions or 224 of 224, one round of
+    # 256 CUs either way; the default path takes the 224-position kernel and agrees with
+    # the 256-position one bit for bit (same k order, same fp32 sums).
+    x = _randn((16, 256, 56, 56), torch.float16, 43)
+    w = _randn((256, 256, 3, 3), torch.float16, 44, 1.0 / math.sqrt(256 * 9))
+    ws = _workspace(x, w, (1, 1))
+    y0, y1, y4 = (torch.empty_like(x) for _ in range(3))
+    kernels.conv2d(x, w, y0, padding=(1, 1), workspace=ws)
+    kernels.conv2d(x, w, y1, padding=(1, 1), workspace=ws, config=1)
+    kernels.conv2d(x, w, y4, padding=(1, 1), workspace=ws, config=4)
+    assert torch.equal(y0, y4) and torch.equal(y1, y4)
+    ref = F.conv2d(x.float(), w.float(), padding=1)
+    assert torch.allclose(y4.float(), ref, atol=1e-2, rtol=1e-2)
+
+
 @pytest.mark.parametrize("flip", ("w", "h"))
-@pytest.mark.parametrize("config", (0, 1, 3))
+@pytest.mark.parametrize("config", (0, 1, 3, 4))
 @pytest.mark.parametrize("xshape", ((4, 64, 15, 13), (17, 64, 45, 45)))
 def test_conv2d_flipped_output(flip, config, xshape):
     """An output flipped along w (q stride -1) or h (p stride -Q) through the C ABI, with
@@ -753,7 +795,7 @@ def test_conv2d_forced_path_rejects_unfit_call():
     x = _randn((2, 24, 16, 16), torch.float16, 62)  # no workspace: no re-laid path
     w = _randn((40, 24, 3, 3), torch.float16, 63, 0.1)
     y = torch.full((2, 40, 14, 14), 7.0, dtype=torch.float16, device=DEV)
-    for config in (1, 2):
+    for config in (1, 2, 4):
         with pytest.raises(KernelLaunchError):
             kernels.conv2d(x, w, y, config=config)
     assert torch.all(y == 7.0)
