@@ -258,7 +258,8 @@ int nt_conv2d_bf16(const void* x, const int64_t* x_strides, const void* w, const
  * nt_conv2d_workspace_size bytes (which also holds the fp32 partials when the kernel splits
  * the reduction of a small output), C*R*S >= 96 with C rounded up to 32, y of the input
  * type; 2 = the re-laid input through the N-H-W-C kernel:
- * the workspace; 3 = the direct kernel, no workspace).  A forced path whose
+ * the workspace; 3 = the direct kernel, no workspace; 4 = the re-laid input through the
+ * DMA kernel of 224-position tiles, as 1 but never splitting the reduction).  A forced path whose
  * conditions do not hold returns NT_ERR_INVALID before launching.  Replaces the
  * per-configuration launchers the reference's auto-tuner times
  * (src/ninetoothed/compiler/driver.py:975-1031, tests/test_conv2d.py:109-113). */
