@@ -107,6 +107,7 @@ def _trace_summary(args):
             rows.append((short, len(d), f"{statistics.fmean(us):.2f}", f"{statistics.median(us):.2f}",
                          f"{min(us):.2f}", f"{max(us):.2f}", "setup (not a step)"))
     frac = cfg["work"] / (total * 1e-6) / cfg["peak"] if total else float("nan")
+    rows.sort(key=lambda r: r[-1] != "step")  # the step kernels first, in trace order
     for i, (short, n, mean, med, lo, hi, role) in enumerate(rows):
         head = f"| {cfg['name']} " if i == 0 else "| "
         tail = f"| {frac:.3f} |" if i == 0 else "| |"
