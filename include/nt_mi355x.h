@@ -226,6 +226,19 @@ int nt_gemm_e4m3(const void* a, int64_t sa_m, int64_t sa_k, const void* b, int64
                  int out_dtype, int64_t M, int64_t N, int64_t K, float alpha, float beta,
                  int round_dtype, hipStream_t stream);
 
+/* The GEMM entry points above with all their arguments in one array of 22 int64 values:
+ *   v[0]  entry: 0 nt_gemm_f16, 1 nt_gemm_bf16, 2 nt_gemm_f32, 3 nt_gemm_e5m2, 4 nt_gemm_e4m3;
+ *   v[1..16]  a, sa_m, sa_k, b, sb_k, sb_n, c, sc_m, sc_n, out, so_m, so_n, out_dtype, M, N, K
+ *             (pointers as their address);
+ *   v[17], v[18]  alpha and beta, the bits of each float in the low 32 bits;
+ *   v[19]  round_dtype;  v[20]  config (nonzero: nt_gemm_config_f16/bf16; entries 0 and 1
+ *          only, else NT_ERR_INVALID);  v[21]  the stream.
+ * Same results and status as the entry it selects.  No counterpart in the reference: it is
+ * for bindings whose per-argument call cost is as long as a small GEMM (the Python binding
+ * fills the array once per bound call and rewrites only the data pointers, alpha, beta and
+ * the stream: one argument instead of 20). */
+int nt_gemm_packed(const int64_t* v);
+
 /* ---------------------------------------------------------------------------
  * 2-D convolution as an implicit GEMM (cross-correlation, as F.conv2d):
  *   y[n,k,p,q] = cast_y(round(sum_{c,r,s} x[n,c,p*sh - ph + r*dh, q*sw - pw + s*dw] * w[k,c,r,s]))

@@ -10,6 +10,7 @@ import concurrent.futures
 import os
 import shutil
 import subprocess
+import sysconfig
 import sys
 from pathlib import Path
 
@@ -90,9 +91,37 @@ def build(verbose: bool = False, extra_flags: tuple[str, ...] = (), jobs: int | 
     if result.returncode != 0:
         raise RuntimeError(f"link failed:\n{result.stderr}")
     os.replace(tmp, LIBRARY_PATH)
+    build_fastkey()
     if verbose:
-        print(f"built {LIBRARY_PATH} from {len(srcs)} sources", file=sys.stderr)
+        print(f"built {LIBRARY_PATH} from {len(srcs)} sources, and {fastkey_path().name}", file=sys.stderr)
     return LIBRARY_PATH
+
+
+def fastkey_path() -> Path:
+    return PACKAGE_DIR / ("_fastkey" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def build_fastkey() -> Path:
+    """Compile csrc/fastkey.cpp (the Handle's call key in C++, a CPython module over torch's
+    tensor metadata) with the host compiler against the installed torch."""
+    import torch
+
+    torch_dir = Path(torch.__path__[0])
+    out = fastkey_path()
+    tmp = out.with_name(out.name + ".tmp")
+    cmd = [
+        shutil.which("g++") or "g++", "-O2", "-shared", "-fPIC", "-std=c++17",
+        f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+        f"-I{sysconfig.get_paths()['include']}", f"-I{torch_dir / 'include'}",
+        f"-I{torch_dir / 'include' / 'torch' / 'csrc' / 'api' / 'include'}",
+        str(SOURCE_DIR / "fastkey.cpp"), f"-L{torch_dir / 'lib'}", "-lc10", "-ltorch", "-ltorch_cpu", "-ltorch_python",
+        f"-Wl,-rpath,{torch_dir / 'lib'}", "-o", str(tmp),
+    ]
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"fastkey.cpp failed to build:\n{result.stderr}")
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":

@@ -66,6 +66,7 @@ _SIGNATURES = {
                                 _F, _I, _I, _P)
         for t in ("f16", "bf16")
     },
+    "nt_gemm_packed": (_I64P,),
     "nt_conv2d_workspace_size": (_I64,) * 9 + (_I,),
     **{
         f"nt_conv2d_noalloc_{t}": (_P, _I64P, _P, _I64P, _P, _I64P, _I) + (_I64,) * 15 + (_I, _P)

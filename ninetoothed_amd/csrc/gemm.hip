@@ -20,6 +20,7 @@
 //   16 x 16 block with v_mfma_f32_16x16x4f32, K staged through LDS 256 at a time.
 #include "mfma_core.h"
 
+#include <cstring>
 #include <type_traits>
 
 namespace nt {
@@ -1482,4 +1483,44 @@ extern "C" int nt_gemm_e5m2(NT_GEMM_PARAMS) {
 }
 extern "C" int nt_gemm_e4m3(NT_GEMM_PARAMS) {
   return nt::gemm8_launch<nt::src_e4m3>(nt::make_args(NT_GEMM_ARGS), stream);
+}
+
+// The GEMM entry points with their arguments in one int64 array (see nt_mi355x.h).
+extern "C" int nt_gemm_packed(const int64_t* v) {
+  if (v == nullptr) return NT_ERR_INVALID;
+  auto ptr = [&](int i) { return (void*)(intptr_t)v[i]; };
+  auto flt = [&](int i) {
+    const uint32_t bits = (uint32_t)(uint64_t)v[i];
+    float x;
+    std::memcpy(&x, &bits, sizeof(x));
+    return x;
+  };
+  const void* a = ptr(1);
+  const int64_t sa_m = v[2], sa_k = v[3];
+  const void* b = ptr(4);
+  const int64_t sb_k = v[5], sb_n = v[6];
+  const void* c = ptr(7);
+  const int64_t sc_m = v[8], sc_n = v[9];
+  void* out = ptr(10);
+  const int64_t so_m = v[11], so_n = v[12];
+  const int out_dtype = (int)v[13];
+  const int64_t M = v[14], N = v[15], K = v[16];
+  const float alpha = flt(17), beta = flt(18);
+  const int round_dtype = (int)v[19], config = (int)v[20];
+  hipStream_t stream = (hipStream_t)ptr(21);
+  if (config != 0 && v[0] > 1) return NT_ERR_INVALID;
+  switch (v[0]) {
+    case 0:
+      return config ? nt_gemm_config_f16(NT_GEMM_ARGS, config, stream) : nt_gemm_f16(NT_GEMM_ARGS, stream);
+    case 1:
+      return config ? nt_gemm_config_bf16(NT_GEMM_ARGS, config, stream) : nt_gemm_bf16(NT_GEMM_ARGS, stream);
+    case 2:
+      return nt_gemm_f32(NT_GEMM_ARGS, stream);
+    case 3:
+      return nt_gemm_e5m2(NT_GEMM_ARGS, stream);
+    case 4:
+      return nt_gemm_e4m3(NT_GEMM_ARGS, stream);
+    default:
+      return NT_ERR_INVALID;
+  }
 }

@@ -6,7 +6,8 @@ Each operation comes in two forms:
   dtype, rank, sizes) and returns a launcher closed over everything that depends
   only on dtypes, shapes and strides (entry point, dims, stride arrays, device).
   A launcher reads only data pointers, scalar values and the caller's current
-  stream, so a call costs a few microseconds of host time.  Callers re-bind
+  stream, so a call costs a few microseconds of host time (the GEMM's about one: its
+  constant arguments are packed once for ``nt_gemm_packed``).  Callers re-bind
   whenever a dtype, shape, stride or device changes (``runtime.Handle`` keys its
   cache on exactly those).
 - ``<op>(...)`` binds and launches once.
@@ -15,6 +16,9 @@ Nothing here computes on the CPU and nothing falls back: an unsupported case
 raises, a non-zero status from the library raises :class:`KernelLaunchError` (the
 reference's error type, ``src/ninetoothed/compiler/runtime.py:31-35``).
 """
+
+import ctypes
+import struct
 
 from ninetoothed_amd import _lib
 from ninetoothed_amd.errors import KernelLaunchError
@@ -60,6 +64,38 @@ def _entry(name):
 
 def _raise(code, name):
     raise KernelLaunchError(code, name)
+
+
+try:  # the packed launch (csrc/fastkey.cpp, built by ninetoothed_amd._build); else ctypes per argument
+    from ninetoothed_amd import _fastkey
+except ImportError:
+    _fastkey = None
+
+
+def _packed_address(name):
+    """Address of the packed entry point ``name`` (``int name(const int64_t*)``), or None when
+    the library does not export it or the packed launch module is missing."""
+    if _fastkey is None or name not in _lib.exported_symbols():
+        return None
+    fn = getattr(_lib.load(), name, None)
+    if not isinstance(fn, ctypes._CFuncPtr):
+        return None
+    return ctypes.cast(fn, ctypes.c_void_p).value
+
+
+_F32 = struct.Struct("<f")
+_U32 = struct.Struct("<I")
+_float_bits_seen = {}
+
+
+def _float_bits(x):
+    """The bits of ``x`` as an fp32, as the packed entry points take alpha and beta."""
+    bits = _float_bits_seen.get(x) if x else None  # (0.0 and -0.0 compare equal: not cached)
+    if bits is None:
+        bits = _U32.unpack(_F32.pack(x))[0]
+        if x and len(_float_bits_seen) < 256:
+            _float_bits_seen[x] = bits
+    return bits
 
 
 # ------------------------------------------------------------------------- add
@@ -290,6 +326,23 @@ def bind_gemm(a, b, out, c=None, round_dtype=None, config=0):
     sc_m, sc_n = c.stride() if c is not None else (0, 0)
     stream = _stream_of(device)
 
+    addr = _packed_address("nt_gemm_packed")
+    if addr is not None:
+        # nt_gemm_packed: the constant arguments packed once; per call the C++ helper writes
+        # the four data pointers, alpha, beta and the stream into their slots and calls it.
+        which = _PACKED_GEMM_ENTRY[entry]
+        template = struct.pack("<22q", which, 0, sa_m, sa_k, 0, sb_k, sb_n, 0, sc_m, sc_n, 0, so_m, so_n, out_code, m,
+                               n, k, 0, 0, rd, int(config), 0)
+        call = _fastkey.call
+
+        def launch(a, b, out, c, alpha, beta):
+            code = call(addr, template, _GEMM_POINTER_SLOTS, (a, b, c, out), _GEMM_VALUE_SLOTS,
+                        (_float_bits(alpha), _float_bits(beta), stream() or 0))
+            if code:
+                _raise(code, name)
+
+        return launch
+
     def launch(a, b, out, c, alpha, beta):
         code = fn(a.data_ptr(), sa_m, sa_k, b.data_ptr(), sb_k, sb_n, c.data_ptr() if c is not None else None, sc_m,
                   sc_n, out.data_ptr(), so_m, so_n, out_code, m, n, k, alpha, beta, rd, *extra, stream())
@@ -297,6 +350,13 @@ def bind_gemm(a, b, out, c=None, round_dtype=None, config=0):
             _raise(code, name)
 
     return launch
+
+
+# nt_gemm_packed: v[0] per entry point; slots of a, b, c, out and of alpha, beta, the stream
+_PACKED_GEMM_ENTRY = {"nt_gemm_f16": 0, "nt_gemm_bf16": 1, "nt_gemm_f32": 2, "nt_gemm_e5m2": 3, "nt_gemm_e4m3": 4,
+                      "nt_gemm_config_f16": 0, "nt_gemm_config_bf16": 1}
+_GEMM_POINTER_SLOTS = (1, 4, 7, 10)
+_GEMM_VALUE_SLOTS = (17, 18, 21)
 
 
 def gemm(a, b, out, c=None, alpha=1.0, beta=0.0, round_dtype=None, config=0):

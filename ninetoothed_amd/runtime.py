@@ -16,7 +16,8 @@ strides, constexpr and meta values), as the reference does for non-Triton backen
 
 A call with every public argument given positionally goes through a second cache
 keyed on (dtype, shape, strides, device, data-pointer alignment) of each tensor, the value of each
-constexpr, the type of each other scalar and the meta keywords.  A key enters it
+constexpr, the type of each other scalar and the meta keywords; the tensors' part of that key is
+built in C++ (`_fastkey`, from csrc/fastkey.cpp) where that module is built.  A key enters it
 only after a call with that key passed every check above, so a hit goes straight
 to the bound launcher (which reads data pointers, scalars and the current stream).
 """
@@ -24,6 +25,11 @@ to the bound launcher (which reads data pointers, scalars and the current stream
 import threading
 
 from ninetoothed_amd.dtype import normalize_dtype
+
+try:  # the call key in C++ (csrc/fastkey.cpp, built by ninetoothed_amd._build); else built in Python
+    from ninetoothed_amd import _fastkey
+except ImportError:
+    _fastkey = None
 from ninetoothed_amd.errors import KernelLaunchError, LoweringError  # noqa: F401  (re-exported)
 
 
@@ -55,6 +61,8 @@ class Handle:
         )
         outputs = self._abi["outputs"]
         self._ret = self._index[outputs[0]] if outputs else None
+        self._tensor_pos = tuple(i for i, k in enumerate(self._kinds) if k == 0)
+        self._all_tensors = len(self._tensor_pos) == len(self._kinds)
         self._launchers = {}
         # max_num_configs > 1: pick among every fitting kernel by timing (auto_tuner.AutoTuner)
         request = compilation.request
@@ -100,11 +108,19 @@ class Handle:
         # enters as its index (get_device: -1 off the GPU), which hashes far faster than a
         # torch.device object and tells the same tensors apart (all GPU tensors here report
         # one device type).
-        key = tuple([
-            (v.dtype, v.shape, v.stride(), v.get_device(), v.data_ptr() & 15) if kind == 0
-            else (v if kind == 1 else type(v))
-            for v, kind in zip(args, self._kinds)
-        ])
+        if _fastkey is not None:
+            tensors = args if self._all_tensors else tuple([args[i] for i in self._tensor_pos])
+            key = _fastkey.key(tensors)
+            if key is None:
+                raise TypeError("not a tensor")  # the checks of the full path report it
+            if not self._all_tensors:
+                key = (key, tuple([v if kind == 1 else type(v) for v, kind in zip(args, self._kinds) if kind != 0]))
+        else:
+            key = tuple([
+                (v.dtype, v.shape, v.stride(), v.get_device(), v.data_ptr() & 15) if kind == 0
+                else (v if kind == 1 else type(v))
+                for v, kind in zip(args, self._kinds)
+            ])
         if kwargs:
             key = (key, tuple(sorted(kwargs.items())))
         return key
