@@ -30,6 +30,9 @@ median of 3 runs after one warm-up.  The reference's own kernels under the Trito
 interpreter are not available on the GPU box (the reference does not travel there).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only name,...] [--no-cpu] [--samples S]
+       [--cold] [--no-graph]
+       python bench.py --trace-summary <rocprofv3 kernel_trace.csv> --only <config> --warmup W --steps K
+       (per-kernel durations over the K timed steps of a traced run of that configuration)
 """
 
 import argparse
