@@ -975,80 +975,77 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     step(T1{}, F1{}, V0{}, kt + 1);
     step(F1{}, F1{}, VN{}, kt + 2);
 
-    // Epilogue, per 64-position half (blocks 2 ph, 2 ph + 1) of the wave's positions: each
-    // 16-channel half of a channel block staged in the wave's 4 KiB, each lane storing 8
-    // consecutive positions (columns (lane % 8) * 8 .. + 7) of one channel.
-    float* stage = (float*)(lds + cdma::EPI + wave * 4096);
-    const int cg = (lane & 7) * 8;
+    // Epilogue.  Once every wave has left the loop the LDS ring and the staging area are
+    // free: each wave owns 20 KiB of them and stages one 32-channel block of its tile at a
+    // time (32 rows of its PW positions in fp32; a row stride of PW + 8 floats keeps the two
+    // lane halves, four rows apart, on different banks), then each lane stores 16-byte runs
+    // of 8 positions: positions 8 (lane % 16) .. + 7 of rows lane / 16 + 4 t.  One LDS round
+    // trip per 32 channels, and eight stores per lane issued back to back.
+    __syncthreads();
+    constexpr int PW = NB * 32, SW = PW + 8;
+    float* stage = (float*)(lds + wave * 20480);
+    const int cp = (lane & 15) * 8;
+    const int mpos = m0t + wm * 128 + cp;
+    const bool m_ok = cp < PW && mpos < g.M;
+    int64_t ybase = 0;
+    int64_t yoff[8];
+    uint32_t yvalid = 0;  // bit u: position mpos + u < M (an offset may be negative for flipped views)
+    if (m_ok) {
+      const int q = mpos % (int)g.Q, t = mpos / (int)g.Q;
+      const int p = t % (int)g.P, n = t / (int)g.P;
+      ybase = n * g.ys[0] + p * g.ys[2] + q;
+    }
+    if (!g.qvec) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int64_t m = mpos + u;
+        const int64_t q = m % g.Q, t = m / g.Q;
+        yoff[u] = (t / g.P) * g.ys[0] + (t % g.P) * g.ys[2] + q * g.ys[3];
+        yvalid |= (m < g.M ? 1u : 0u) << u;
+      }
+    }
     auto finish = [&](auto round_c) {
       constexpr int ROUND = decltype(round_c)::value;
-      static_for<0, (NB + 1) / 2>([&](auto ph_c) {
-        constexpr int ph = decltype(ph_c)::value;
-        constexpr int JN = NB - 2 * ph < 2 ? NB - 2 * ph : 2;  // blocks in this half
-        const int mpos = m0t + wm * 128 + ph * 64 + cg;
-        const bool m_ok = cg < JN * 32 && mpos < g.M;
-        int64_t ybase = 0;
-        int64_t yoff[8];
-        uint32_t yvalid = 0;
-        if (m_ok) {
-          const int q = mpos % (int)g.Q, t = mpos / (int)g.Q;
-          const int p = t % (int)g.P, n = t / (int)g.P;
-          ybase = n * g.ys[0] + p * g.ys[2] + q;
-        }
-        if (!g.qvec) {
 #pragma unroll
-          for (int u = 0; u < 8; ++u) {
-            const int64_t m = mpos + u;
-            const int64_t q = m % g.Q, t = m / g.Q;
-            yoff[u] = (t / g.P) * g.ys[0] + (t % g.P) * g.ys[2] + q * g.ys[3];
-            yvalid |= (m < g.M ? 1u : 0u) << u;
+      for (int i = 0; i < 2; ++i) {
+        wave_lds_order();  // the previous block's reads come first
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) stage[acc_row(r, lane) * SW + j * 32 + (lane & 31)] = acc[i][j][r];
+        wave_lds_order();  // every lane's writes before any lane reads
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const int rr = (lane >> 4) + 4 * t;
+          const int k = k0t + wk * 64 + i * 32 + rr;
+          const float4 v0 = *(const float4*)(stage + rr * SW + cp);
+          const float4 v1 = *(const float4*)(stage + rr * SW + cp + 4);
+          const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+          u32x4 ow;
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            float a = v[2 * d], b = v[2 * d + 1];
+            if constexpr (ROUND == NT_DTYPE_F16) {
+              a = f16_bits_to_float(float_to_f16_bits(a));
+              b = f16_bits_to_float(float_to_f16_bits(b));
+            }
+            if constexpr (ROUND == NT_DTYPE_BF16) {
+              a = bf16_bits_to_float(float_to_bf16_bits(a));
+              b = bf16_bits_to_float(float_to_bf16_bits(b));
+            }
+            ow[d] = (uint32_t)elem<T>::from_float(a) | ((uint32_t)elem<T>::from_float(b) << 16);
           }
-        }
+          if (m_ok && k < g.K) {
+            if (g.qvec) {
+              __builtin_nontemporal_store(ow, (u32x4*)(Y + ybase + (int64_t)k * g.ys[1]));
+            } else {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            wave_lds_order();  // the previous half's reads come first
-#pragma unroll
-            for (int jj = 0; jj < JN; ++jj)
-#pragma unroll
-              for (int r = 8 * h; r < 8 * h + 8; ++r)
-                stage[(acc_row(r, lane) - 16 * h) * 64 + jj * 32 + (lane & 31)] = acc[i][2 * ph + jj][r];
-            wave_lds_order();  // every lane's writes before any lane reads
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-              const int rr = t * 8 + (lane >> 3);
-              const int k = k0t + wk * 64 + i * 32 + h * 16 + rr;
-              const float4 v0 = *(const float4*)(stage + rr * 64 + cg);
-              const float4 v1 = *(const float4*)(stage + rr * 64 + cg + 4);
-              const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-              u32x4 ow;
-#pragma unroll
-              for (int d = 0; d < 4; ++d) {
-                float a = v[2 * d], b = v[2 * d + 1];
-                if constexpr (ROUND == NT_DTYPE_F16) {
-                  a = f16_bits_to_float(float_to_f16_bits(a));
-                  b = f16_bits_to_float(float_to_f16_bits(b));
-                }
-                if constexpr (ROUND == NT_DTYPE_BF16) {
-                  a = bf16_bits_to_float(float_to_bf16_bits(a));
-                  b = bf16_bits_to_float(float_to_bf16_bits(b));
-                }
-                ow[d] = (uint32_t)elem<T>::from_float(a) | ((uint32_t)elem<T>::from_float(b) << 16);
-              }
-              if (m_ok && k < g.K) {
-                if (g.qvec) {
-                  __builtin_nontemporal_store(ow, (u32x4*)(Y + ybase + (int64_t)k * g.ys[1]));
-                } else {
-#pragma unroll
-                  for (int u = 0; u < 8; ++u)
-                    if ((yvalid >> u) & 1u)
-                      Y[yoff[u] + (int64_t)k * g.ys[1]] = (uint16_t)(ow[u >> 1] >> (16 * (u & 1)));
-                }
-              }
+              for (int u = 0; u < 8; ++u)
+                if ((yvalid >> u) & 1u) Y[yoff[u] + (int64_t)k * g.ys[1]] = (uint16_t)(ow[u >> 1] >> (16 * (u & 1)));
             }
           }
-      });
+        }
+      }
     };
     if (g.round_dtype == NT_DTYPE_F16)
       finish(std::integral_constant<int, NT_DTYPE_F16>{});
