@@ -799,10 +799,15 @@ def _shapes(ctx, values, const_value, carried=None):
                 s = src[:ax] + src[ax + 1:]
         elif op == "bcast":
             src, pattern = list(shp[id(a[0])]), a[1]
-            if sum(1 for x in pattern if x == ":") != len(src):
-                raise LoweringError("a broadcasting subscript needs one `:` per dimension")
-            it = iter(src)
-            s = tuple(next(it) if x == ":" else 1 for x in pattern)
+            if any(isinstance(x, int) for x in pattern):  # axes named: a broadcast with the axes permuted
+                if sorted(x for x in pattern if x is not None) != list(range(len(src))):
+                    raise LoweringError("a permuting broadcast names every source axis once")
+                s = tuple(src[x] if x is not None else 1 for x in pattern)
+            else:
+                if sum(1 for x in pattern if x == ":") != len(src):
+                    raise LoweringError("a broadcasting subscript needs one `:` per dimension")
+                it = iter(src)
+                s = tuple(next(it) if x == ":" else 1 for x in pattern)
         elif op in ("zeros", "full"):
             dims = []
             for d in a[0]:
@@ -872,7 +877,15 @@ class _TileEmitter(_Emitter):
             return
         self.coords[id(v)] = coords
         if v.op == "bcast":
-            self._assign(v.args[0], tuple(c for c, x in zip(coords, v.args[1]) if x == ":"))
+            pattern = v.args[1]
+            if any(isinstance(x, int) for x in pattern):  # source axis x at this position
+                src = [None] * sum(1 for x in pattern if x is not None)
+                for c, x in zip(coords, pattern):
+                    if x is not None:
+                        src[x] = c
+                self._assign(v.args[0], tuple(src))
+            else:
+                self._assign(v.args[0], tuple(c for c, x in zip(coords, pattern) if x == ":"))
             return
         for a in _value_operands(v):
             sa = self.shapes[id(a)]
@@ -1059,8 +1072,10 @@ def _lower_dots(program, ctx=None):
     src/ninetoothed/backends/emitters/ssa.py:1455-1542).  A transposed operand takes the
     product in another axis order, so that no value is transposed: ``dot(x, trans(w))``
     with w [n, k] is ``sum(x[:, None, :] * w[None, :, :], axis=2)`` and ``dot(trans(u), y)``
-    with u [k, m] is ``sum(u[:, :, None] * y[:, None, :], axis=0)``.  ``dot`` of two
-    transposed operands raises ``LoweringError``.  In both forms a product counts only where
+    with u [k, m] is ``sum(u[:, :, None] * y[:, None, :], axis=0)``; ``dot(trans(u),
+    trans(w))`` is the same sum over a [k, m, n] product whose w factor is broadcast with its
+    axes permuted (a ``bcast`` naming source axes), so again nothing is transposed in memory.
+    In every form a product counts only where
     both operands' load masks hold (the reference's dot emitter masks them the same way:
     src/ninetoothed/backends/emitters/ssa.py:1455-1542)."""
     roots = list(program.stores.values())
@@ -1084,8 +1099,6 @@ def _lower_dots(program, ctx=None):
         if v.op == "dot":
             x, y = v.args
             tx, ty = x.op == "trans", y.op == "trans"
-            if tx and ty:
-                raise LoweringError("`dot` of two transposed tiles is not supported by the generic kernels")
             xi, yi = rebuild(x.args[0] if tx else x), rebuild(y.args[0] if ty else y)
             if ctx is not None and _mdot_fits(ctx, xi, yi, tx, ty):
                 out = Value("mdot", (xi, yi, tx, ty))
@@ -1093,7 +1106,10 @@ def _lower_dots(program, ctx=None):
                 return out
             cx = Value("cast", (xi, f32))
             cy = Value("cast", (yi, f32))
-            if ty:
+            if tx and ty:  # u [k, m], w [n, k]: prod[k, m, n] = u[k, m] * w[n, k]
+                prod = Value("mul", (Value("bcast", (cx, (":", ":", None))), Value("bcast", (cy, (1, None, 0)))))
+                axis = 0
+            elif ty:
                 prod = Value("mul", (Value("bcast", (cx, (":", None, ":"))), Value("bcast", (cy, (None, ":", ":")))))
                 axis = 2
             elif tx:

@@ -995,6 +995,43 @@ def test_dot_tile_programs(dtype):
     torch.testing.assert_close(rows, ref.sum(dim=1), rtol=tol, atol=tol * 8)
 
 
+def dot_tt_arrangement(x, w, o):
+    # x [K, M] in column tiles (programs along M), w [N, K] whole, o [M, N] in row tiles
+    xt = x.tile((-1, DOT_BM)).permute((1, 0))
+    return xt, w.tile((-1, -1)).expand((xt.shape[0], -1)), o.tile((DOT_BM, -1))
+
+
+def dot_tt_application(x, w, o):
+    o = ntl.dot(ntl.trans(x), ntl.trans(w))  # noqa: F841
+
+
+def test_dot_of_two_transposed_tiles_compiles():
+    # fp32 operands: the fp32 reduction over a [k, m, n] product, w's factor broadcast with its
+    # axes permuted; 16-bit operands on the 32 x 32 x 16 grid: the matrix core, both staged by
+    # axis order
+    h = ninetoothed.make(dot_tt_arrangement, dot_tt_application, (Tensor(2), Tensor(2), Tensor(2)))
+    for dtype, mfma in ((torch.float32, False), (torch.float16, True)):
+        plan = _plan(h, torch.empty((64, 128), dtype=dtype), torch.empty((96, 64), dtype=dtype),
+                     torch.empty(128, 96), DOT_BM=32)
+        assert plan.describe()["family"] == "generic"
+        src = plan.source()
+        assert ("mfma" in src) == mfma
+        assert len(GenericPlan.compile(src)) > 1000
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", (torch.float32, torch.float16, torch.bfloat16))
+def test_dot_of_two_transposed_tiles(dtype):
+    g = torch.Generator().manual_seed(27)
+    x = (torch.randn(64, 128, generator=g) / 4).to(dtype).cuda()  # [K, M]
+    w = (torch.randn(96, 64, generator=g) / 4).to(dtype).cuda()   # [N, K]
+    ref = x.float().t() @ w.float().t()
+    o = torch.empty(128, 96, dtype=torch.float32, device="cuda")
+    ninetoothed.make(dot_tt_arrangement, dot_tt_application, (Tensor(2), Tensor(2), Tensor(2)))(x, w, o, DOT_BM=32)
+    tol = 1e-4 if dtype == torch.float32 else 1e-4 * 8
+    torch.testing.assert_close(o, ref, rtol=tol, atol=tol)  # 16-bit products are exact, sums fp32
+
+
 DOT_K, DOT_N = Symbol("DOT_K", meta=True), Symbol("DOT_N", meta=True)
 
 
