@@ -1045,7 +1045,8 @@ MDOT_LDS = 48 * 1024  # LDS a matrix-core dot may take (staged operands and the 
 
 def _mdot_fits(ctx, x, y, tx, ty):
     """Whether ``dot`` of (inner) operands x, y runs on the matrix core: both 16-bit floats
-    of one type, M and N multiples of 32, K of 16, operands and result within MDOT_LDS."""
+    of one type, and the operands padded to M, N multiples of 32 and K of 16 plus the fp32
+    result within MDOT_LDS."""
     t = _static_type(ctx, x)
     if t not in ("float16", "bfloat16") or _static_type(ctx, y) != t:
         return False
@@ -1058,8 +1059,8 @@ def _mdot_fits(ctx, x, y, tx, ty):
         return False
     m, k = (sx[1], sx[0]) if tx else sx
     k2, n = (sy[1], sy[0]) if ty else sy
-    return (k == k2 and m % 32 == 0 and n % 32 == 0 and k % 16 == 0
-            and (m + n) * (k + 8) * 2 + m * n * 4 <= MDOT_LDS)
+    mp, np_, kp = -(-m // 32) * 32, -(-n // 32) * 32, -(-k // 16) * 16
+    return k == k2 and min(m, n, k) > 0 and (mp + np_) * (kp + 8) * 2 + m * n * 4 <= MDOT_LDS
 
 
 def _lower_dots(program, ctx=None):
@@ -1516,20 +1517,23 @@ class TilePlan(GenericPlan):
 
     def _mdot_block(self, em, v):
         """``dot`` on the matrix core: both operands staged into LDS as [row][k] (k
-        contiguous, rows padded by 16 bytes), masked elements as zero; each wave takes 32 x 32
-        output blocks, ``v_mfma_f32_32x32x16`` per 16-deep k slice, into an fp32 LDS array."""
+        contiguous, rows padded by 16 bytes), masked elements as zero, and zero-padded to M, N
+        multiples of 32 and K of 16; each wave takes 32 x 32 output blocks,
+        ``v_mfma_f32_32x32x16`` per 16-deep k slice, and stores their elements inside [M, N]
+        into an fp32 LDS array."""
         k_id = self.red_index[id(v)]
         x, y, tx, ty = v.args
         sx, sy = self.shapes[id(x)], self.shapes[id(y)]
         m, kk = (sx[1], sx[0]) if tx else sx
         n = sy[0] if ty else sy[1]
-        pitch = kk + 8
+        mp, np_, kp = -(-m // 32) * 32, -(-n // 32) * 32, -(-kk // 16) * 16
+        pitch = kp + 8
         a, b, arr = f"da{k_id}", f"db{k_id}", f"red{k_id}"
         lines = [f"    {{  // dot on the matrix core: [{m}, {kk}] x [{kk}, {n}]"]
         t = None
-        for name, val, rows, trans, tag in ((a, x, m, tx, f"ma{k_id}_"), (b, y, n, not ty, f"mb{k_id}_")):
-            # element j of the staged operand: row j / kk, k j % kk
-            r, c = f"(j / {kk}LL)", f"(j % {kk}LL)"
+        for name, val, rows, rows_p, trans, tag in ((a, x, m, mp, tx, f"ma{k_id}_"), (b, y, n, np_, not ty, f"mb{k_id}_")):
+            # element j of the staged (padded) operand: row j / kp, k j % kp; zero past [rows, kk]
+            r, c = f"(j / {kp}LL)", f"(j % {kp}LL)"
             body = em.context(val, (c, r) if trans else (r, c), tag)
             tv = em.type_of(val)
             if t is None:
@@ -1541,27 +1545,32 @@ class TilePlan(GenericPlan):
             value = f"{st}({em.operand(val, t)})"
             if mask:
                 value = f"(({mask}) ? {value} : (unsigned short)0)"
-            lines += [f"      for (long long j = tid; j < {rows * kk}LL; j += 256) {{", *["  " + x for x in body],
-                      f"        {name}[(j / {kk}LL) * {pitch}LL + (j % {kk}LL)] = {value};", "      }"]
-            self.decls.append(f"  __shared__ __attribute__((aligned(16))) unsigned short {name}[{rows * pitch}];")
-            self.lds_bytes += rows * pitch * 2
+            lines += [f"      for (long long j = tid; j < {rows_p * kp}LL; j += 256) {{",
+                      f"        unsigned short staged = 0;",
+                      f"        if ({r} < {rows}LL && {c} < {kk}LL) {{", *["    " + x for x in body],
+                      f"          staged = {value};", "        }",
+                      f"        {name}[(j / {kp}LL) * {pitch}LL + (j % {kp}LL)] = staged;", "      }"]
+            self.decls.append(f"  __shared__ __attribute__((aligned(16))) unsigned short {name}[{rows_p * pitch}];")
+            self.lds_bytes += rows_p * pitch * 2
         frag = "nt_half8" if t == "float16" else "nt_bf16x8"
         mfma = "__builtin_amdgcn_mfma_f32_32x32x16_" + ("f16" if t == "float16" else "bf16")
-        nb = n // 32
+        nb = np_ // 32
         lines += [
             "      __syncthreads();",
             "      {",
             "        const int lane = tid & 63, wave = tid >> 6;",
-            f"        for (int blk = wave; blk < {(m // 32) * nb}; blk += 4) {{",
+            f"        for (int blk = wave; blk < {(mp // 32) * nb}; blk += 4) {{",
             f"          const int bm = blk / {nb}, bn = blk % {nb};",
             "          nt_floatx16 acc = {};",
-            f"          for (int k0 = 0; k0 < {kk}; k0 += 16) {{",
+            f"          for (int k0 = 0; k0 < {kp}; k0 += 16) {{",
             f"            const {frag} fa = *(const {frag}*)({a} + (bm * 32 + (lane & 31)) * {pitch} + k0 + 8 * (lane >> 5));",
             f"            const {frag} fb = *(const {frag}*)({b} + (bn * 32 + (lane & 31)) * {pitch} + k0 + 8 * (lane >> 5));",
             f"            acc = {mfma}(fa, fb, acc, 0, 0, 0);",
             "          }",
-            "          for (int r = 0; r < 16; ++r)",
-            f"            {arr}[(bm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3)) * {n} + bn * 32 + (lane & 31)] = acc[r];",
+            "          for (int r = 0; r < 16; ++r) {",
+            "            const int row = bm * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3), col = bn * 32 + (lane & 31);",
+            f"            if (row < {m} && col < {n}) {arr}[row * {n} + col] = acc[r];",
+            "          }",
             "        }",
             "      }",
             "    }",

@@ -1051,12 +1051,32 @@ def test_matrix_core_dot_programs_compile():
         src = plan.source()
         assert f"__builtin_amdgcn_mfma_f32_32x32x16_{suffix}" in src and "__shared__ float red0[3072]" in src
         assert len(GenericPlan.compile(src)) > 1000
-    # fp32 operands, or shapes off the 32 x 32 x 16 grid, keep the fp32 reduction
+    # shapes off the 32 x 32 x 16 grid run on the matrix core zero-padded to it; fp32 operands
+    # keep the fp32 reduction
     h = ninetoothed.make(dot_arrangement, dot_application, (Tensor(2), Tensor(2), Tensor(2)))
-    for dtype, sw in ((torch.float32, (64, 96)), (torch.float16, (64, 24))):
-        plan = _plan(h, torch.empty((128, 64), dtype=dtype), torch.empty(sw, dtype=dtype), torch.empty(128, sw[1]),
+    for dtype, sw, mfma in ((torch.float32, (64, 96), False), (torch.float16, (64, 24), True),
+                            (torch.bfloat16, (40, 24), True)):
+        plan = _plan(h, torch.empty((128, sw[0]), dtype=dtype), torch.empty(sw, dtype=dtype), torch.empty(128, sw[1]),
                      DOT_BM=32)
-        assert "mfma" not in plan.source()
+        src = plan.source()
+        assert ("mfma" in src) == mfma
+        assert len(GenericPlan.compile(src)) > 1000
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+@pytest.mark.parametrize("shape", ((48, 40, 20), (16, 40, 24), (96, 8, 72)))
+def test_matrix_core_dot_off_the_grid(dtype, shape):
+    # M, N off multiples of 32 and K off 16: operands zero-padded in LDS, results inside [M, N]
+    bm, k, n = shape
+    g = torch.Generator().manual_seed(29)
+    x = (torch.randn(2 * bm, k, generator=g) / 4).to(dtype).cuda()
+    w = (torch.randn(k, n, generator=g) / 4).to(dtype).cuda()
+    o = torch.full((2 * bm, n), float("nan"), dtype=torch.float32, device="cuda")
+    h = ninetoothed.make(dot_arrangement, dot_application, (Tensor(2), Tensor(2), Tensor(2)))
+    assert "mfma" in _plan(h, x, w, o, DOT_BM=bm).source()
+    h(x, w, o, DOT_BM=bm)
+    torch.testing.assert_close(o, x.float() @ w.float(), rtol=1e-4, atol=1e-4)  # exact products, fp32 sums
 
 
 @pytest.mark.gpu
