@@ -272,7 +272,22 @@ class Lowerer:
             return
         frame.env[name] = value
 
+    @staticmethod
+    def _is_param_binding(frame, name):
+        """Whether ``name`` still names an application parameter: assigning it stores into
+        the parameter (never a loop-carried local)."""
+        v = frame.env.get(name)
+        return name in frame.param_names and isinstance(v, Value) and v.op == "param"
+
     def _store(self, param, value):
+        if self._loop_stack:
+            # a whole arranged output assigned inside a loop that stays a loop: every iteration
+            # stores its tile, as the reference's loop body does; a later read of the parameter
+            # reads the tensor (a program that also reads it is refused by the tile kernels)
+            self.effects.append(("view_store", self.b.make("param", param), self.data(value)))
+            self.store_order.append(param)
+            self.written.pop(param, None)
+            return
         self.stores[param] = self.data(value)
         self.store_order.append(param)
         self.written[param] = self.stores[param]
@@ -360,7 +375,8 @@ class Lowerer:
             # unrolled: the body runs `count` times with the loop variable a constant.  Values
             # carried from one iteration to the next are wrapped in `unmask` at every boundary:
             # like the results of a loop, they carry no load mask into later reductions.
-            carried = [n for n in sorted(_assigned_names(s.body)) if isinstance(frame.env.get(n), Value)]
+            carried = [n for n in sorted(_assigned_names(s.body))
+                       if isinstance(frame.env.get(n), Value) and not self._is_param_binding(frame, n)]
 
             def boundary():
                 for n in carried:
@@ -376,7 +392,8 @@ class Lowerer:
         loop_id = self._loop_ids
         self._loop_ids += 1
         assigned = _assigned_names(s.body)
-        carried = [n for n in sorted(assigned) if n in frame.env and not isinstance(frame.env[n], (_Alias,))]
+        carried = [n for n in sorted(assigned) if n in frame.env and not isinstance(frame.env[n], (_Alias,))
+                   and not self._is_param_binding(frame, n)]
         alias_carried = [n for n in sorted(assigned) if isinstance(frame.env.get(n), _Alias) and frame.env[n].kind == "local"]
         loop = Loop(loop_id, s.target.id, trip, parent=self._loop_stack[-1] if self._loop_stack else None)
         saved = {}

@@ -164,15 +164,27 @@ def test_dot_of_two_transposed_tiles_is_a_tile_program():
 
 
 def test_unsupported_program_is_rejected():
-    # a whole arranged output assigned inside a loop: neither a family nor the generic kernels
+    # a value computed inside a loop with a run-time trip count, stored after it: neither a
+    # family nor the generic kernels (they store a loop's carried results after it)
+    def app(lhs, n, output):
+        for i in range(n):
+            y = lhs * i
+        output = y  # noqa: F841
+
+    h = ninetoothed.make(lambda a, n, c: (a.tile((16, 16)), n, c.tile((16, 16))), app,
+                         (Tensor(2), Tensor(0), Tensor(2)))
+    with pytest.raises(LoweringError):
+        _specialize(h, _h((16, 16)), 3, _h((16, 16)))
+
+
+def test_output_assigned_in_an_unrolled_loop_keeps_the_last_store():
     def app(lhs, rhs, output):
         for i in range(3):
             output = lhs * i + rhs  # noqa: F841
 
     h = ninetoothed.make(lambda a, b, c: (a.tile((16, 16)), b.tile((16, 16)), c.tile((16, 16))), app,
                          (Tensor(2), Tensor(2), Tensor(2)))
-    with pytest.raises(LoweringError):
-        _specialize(h, _h((16, 16)), _h((16, 16)), _h((16, 16)))
+    assert _specialize(h, _h((16, 16)), _h((16, 16)), _h((16, 16)))["family"] in ("generic", "add")
 
 
 def test_data_dependent_if_is_rejected():

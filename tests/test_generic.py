@@ -1157,3 +1157,47 @@ def test_overlapping_k_tiles_matmul_runs_as_written():
     torch.testing.assert_close(out.float().cpu(), torch.from_numpy(ref), rtol=1e-2, atol=1e-2)
     five = sum(a[:, 8 * t:8 * t + 16].float() @ b[8 * t:8 * t + 16, :].float() for t in range(5))
     torch.testing.assert_close(out.float(), five.half().float(), rtol=1e-2, atol=1e-2)
+
+
+# ------------------------------------------------------------------ a whole output assigned inside a real loop
+def assigned_each_iteration(x, n, out):
+    for i in range(n):
+        out = x * 2.0 + i  # noqa: F841  (every iteration stores; the last one stays)
+
+
+def _assigned_each_iteration():
+    return ninetoothed.make(lambda x, n, out: (x.tile((BS,)), n, out.tile((BS,))), assigned_each_iteration,
+                            (Tensor(1), Tensor(0), Tensor(1)))
+
+
+def test_output_assigned_inside_a_loop_compiles():
+    plan = _plan(_assigned_each_iteration(), torch.empty(1000), 5, torch.empty(1000), BS=256)
+    assert plan.describe()["family"] == "generic" and plan.nest is not None
+    src = plan.source()
+    assert "store into out[]" in src and len(GenericPlan.compile(src)) > 1000
+
+
+@pytest.mark.gpu
+def test_output_assigned_inside_a_loop():
+    kernel = _assigned_each_iteration()
+    x = torch.randn(1000, device="cuda")
+    for n in (0, 1, 7):
+        out = torch.full_like(x, -3.0)
+        kernel(x, n, out, BS=256)
+        expected = torch.full_like(x, -3.0) if n == 0 else x * 2.0 + (n - 1)
+        torch.testing.assert_close(out, expected)
+
+
+def assigned_in_unrolled_loop(x, out):
+    for i in range(3):
+        out = x * 2.0 + i  # noqa: F841
+
+
+@pytest.mark.gpu
+def test_output_assigned_in_an_unrolled_loop():
+    kernel = ninetoothed.make(lambda x, out: (x.tile((BS,)), out.tile((BS,))), assigned_in_unrolled_loop,
+                              (Tensor(1), Tensor(1)))
+    x = torch.randn(1000, device="cuda")
+    out = torch.empty_like(x)
+    kernel(x, out, BS=128)
+    torch.testing.assert_close(out, x * 2.0 + 2)
