@@ -272,7 +272,11 @@ int nt_conv2d_bf16(const void* x, const int64_t* x_strides, const void* w, const
  * the reduction of a small output), C*R*S >= 96 with C rounded up to 32, y of the input
  * type; 2 = the re-laid input through the N-H-W-C kernel:
  * the workspace; 3 = the direct kernel, no workspace; 4 = the re-laid input through the
- * DMA kernel of 224-position tiles, as 1 but never splitting the reduction).  A forced path whose
+ * DMA kernel of 224-position tiles, as 1 but never splitting the reduction; 5 = the input
+ * read in place, N-C-H-W, by the 224-position strip kernel, only the filter re-laid into the
+ * workspace: stride and dilation 1, C % 32 == 0, Q dividing 224 and 224 / Q dividing P,
+ * unit w stride, W % 8 == 0, 16-byte aligned input rows, W + pw and Q + S - 1 at most
+ * Q + 16, y of the input type).  A forced path whose
  * conditions do not hold returns NT_ERR_INVALID before launching.  Replaces the
  * per-configuration launchers the reference's auto-tuner times
  * (src/ninetoothed/compiler/driver.py:975-1031, tests/test_conv2d.py:109-113). */

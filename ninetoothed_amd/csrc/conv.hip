@@ -845,6 +845,94 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     finish(std::integral_constant<int, NT_DTYPE_NONE>{});
 }
 
+// Epilogue of the 224-position kernels (conv_dma224_kernel, conv_strip224_kernel): wave `wave`
+// holds channels 64 (wave % 4) .. + 63 by positions 128 (wave / 4) .. + 32 NB - 1 of the tile
+// whose first output channel is k0t and first position m0t.
+template <typename T, int NB>
+__device__ __forceinline__ void conv224_store(char* lds, floatx16 (&acc)[2][NB], const ConvArgs& g, int wave, int lane,
+                                              int m0t, int k0t) {
+  const int wk = wave & 3, wm = wave >> 2;
+  uint16_t* Y = (uint16_t*)g.y;
+  // Once every wave has left the k-loop the LDS ring and the staging area are
+  // free: each wave owns 20 KiB of them and stages one 32-channel block of its tile at a
+  // time (32 rows of its PW positions in fp32; a row stride of PW + 8 floats keeps the two
+  // lane halves, four rows apart, on different banks), then each lane stores 16-byte runs
+  // of 8 positions: positions 8 (lane % 16) .. + 7 of rows lane / 16 + 4 t.  One LDS round
+  // trip per 32 channels, and eight stores per lane issued back to back.
+  __syncthreads();
+  constexpr int PW = NB * 32, SW = PW + 8;
+  float* stage = (float*)(lds + wave * 20480);
+  const int cp = (lane & 15) * 8;
+  const int mpos = m0t + wm * 128 + cp;
+  const bool m_ok = cp < PW && mpos < g.M;
+  int64_t ybase = 0;
+  int64_t yoff[8];
+  uint32_t yvalid = 0;  // bit u: position mpos + u < M (an offset may be negative for flipped views)
+  if (m_ok) {
+    const int q = mpos % (int)g.Q, t = mpos / (int)g.Q;
+    const int p = t % (int)g.P, n = t / (int)g.P;
+    ybase = n * g.ys[0] + p * g.ys[2] + q;
+  }
+  if (!g.qvec) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t m = mpos + u;
+      const int64_t q = m % g.Q, t = m / g.Q;
+      yoff[u] = (t / g.P) * g.ys[0] + (t % g.P) * g.ys[2] + q * g.ys[3];
+      yvalid |= (m < g.M ? 1u : 0u) << u;
+    }
+  }
+  auto finish = [&](auto round_c) {
+    constexpr int ROUND = decltype(round_c)::value;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      wave_lds_order();  // the previous block's reads come first
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) stage[acc_row(r, lane) * SW + j * 32 + (lane & 31)] = acc[i][j][r];
+      wave_lds_order();  // every lane's writes before any lane reads
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const int rr = (lane >> 4) + 4 * t;
+        const int k = k0t + wk * 64 + i * 32 + rr;
+        const float4 v0 = *(const float4*)(stage + rr * SW + cp);
+        const float4 v1 = *(const float4*)(stage + rr * SW + cp + 4);
+        const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        u32x4 ow;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          float a = v[2 * d], b = v[2 * d + 1];
+          if constexpr (ROUND == NT_DTYPE_F16) {
+            a = f16_bits_to_float(float_to_f16_bits(a));
+            b = f16_bits_to_float(float_to_f16_bits(b));
+          }
+          if constexpr (ROUND == NT_DTYPE_BF16) {
+            a = bf16_bits_to_float(float_to_bf16_bits(a));
+            b = bf16_bits_to_float(float_to_bf16_bits(b));
+          }
+          ow[d] = (uint32_t)elem<T>::from_float(a) | ((uint32_t)elem<T>::from_float(b) << 16);
+        }
+        if (m_ok && k < g.K) {
+          if (g.qvec) {
+            __builtin_nontemporal_store(ow, (u32x4*)(Y + ybase + (int64_t)k * g.ys[1]));
+          } else {
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+              if ((yvalid >> u) & 1u) Y[yoff[u] + (int64_t)k * g.ys[1]] = (uint16_t)(ow[u >> 1] >> (16 * (u & 1)));
+          }
+        }
+      }
+    }
+  };
+  if (g.round_dtype == NT_DTYPE_F16)
+    finish(std::integral_constant<int, NT_DTYPE_F16>{});
+  else if (g.round_dtype == NT_DTYPE_BF16)
+    finish(std::integral_constant<int, NT_DTYPE_BF16>{});
+  else
+    finish(std::integral_constant<int, NT_DTYPE_NONE>{});
+}
+
 // conv_dma_kernel with tiles of 224 positions (seven 32-position blocks) by 256 channels,
 // for outputs whose 256 x 256 tiles leave CUs idle: [16,256,56,56] has 196 such tiles for
 // 256 CUs, and 224 of these.  Waves w and w + 4 of a workgroup run on one SIMD; wave w
@@ -900,7 +988,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       cdma::load_lds16(rsX, lds0 + cdma::B0 + st + 2048 * wave + 1024 * q, vx[q], xo);
   };
   const int wk = wave & 3, wm = wave >> 2;
-  uint16_t* Y = (uint16_t*)g.y;
 
   auto body = [&](auto nb_c) {
     constexpr int NB = decltype(nb_c)::value;  // 32-position blocks of this wave
@@ -975,89 +1062,281 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     step(T1{}, F1{}, V0{}, kt + 1);
     step(F1{}, F1{}, VN{}, kt + 2);
 
-    // Epilogue.  Once every wave has left the loop the LDS ring and the staging area are
-    // free: each wave owns 20 KiB of them and stages one 32-channel block of its tile at a
-    // time (32 rows of its PW positions in fp32; a row stride of PW + 8 floats keeps the two
-    // lane halves, four rows apart, on different banks), then each lane stores 16-byte runs
-    // of 8 positions: positions 8 (lane % 16) .. + 7 of rows lane / 16 + 4 t.  One LDS round
-    // trip per 32 channels, and eight stores per lane issued back to back.
-    __syncthreads();
-    constexpr int PW = NB * 32, SW = PW + 8;
-    float* stage = (float*)(lds + wave * 20480);
-    const int cp = (lane & 15) * 8;
-    const int mpos = m0t + wm * 128 + cp;
-    const bool m_ok = cp < PW && mpos < g.M;
-    int64_t ybase = 0;
-    int64_t yoff[8];
-    uint32_t yvalid = 0;  // bit u: position mpos + u < M (an offset may be negative for flipped views)
-    if (m_ok) {
-      const int q = mpos % (int)g.Q, t = mpos / (int)g.Q;
-      const int p = t % (int)g.P, n = t / (int)g.P;
-      ybase = n * g.ys[0] + p * g.ys[2] + q;
-    }
-    if (!g.qvec) {
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int64_t m = mpos + u;
-        const int64_t q = m % g.Q, t = m / g.Q;
-        yoff[u] = (t / g.P) * g.ys[0] + (t % g.P) * g.ys[2] + q * g.ys[3];
-        yvalid |= (m < g.M ? 1u : 0u) << u;
-      }
-    }
-    auto finish = [&](auto round_c) {
-      constexpr int ROUND = decltype(round_c)::value;
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        wave_lds_order();  // the previous block's reads come first
-#pragma unroll
-        for (int j = 0; j < NB; ++j)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) stage[acc_row(r, lane) * SW + j * 32 + (lane & 31)] = acc[i][j][r];
-        wave_lds_order();  // every lane's writes before any lane reads
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-          const int rr = (lane >> 4) + 4 * t;
-          const int k = k0t + wk * 64 + i * 32 + rr;
-          const float4 v0 = *(const float4*)(stage + rr * SW + cp);
-          const float4 v1 = *(const float4*)(stage + rr * SW + cp + 4);
-          const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-          u32x4 ow;
-#pragma unroll
-          for (int d = 0; d < 4; ++d) {
-            float a = v[2 * d], b = v[2 * d + 1];
-            if constexpr (ROUND == NT_DTYPE_F16) {
-              a = f16_bits_to_float(float_to_f16_bits(a));
-              b = f16_bits_to_float(float_to_f16_bits(b));
-            }
-            if constexpr (ROUND == NT_DTYPE_BF16) {
-              a = bf16_bits_to_float(float_to_bf16_bits(a));
-              b = bf16_bits_to_float(float_to_bf16_bits(b));
-            }
-            ow[d] = (uint32_t)elem<T>::from_float(a) | ((uint32_t)elem<T>::from_float(b) << 16);
-          }
-          if (m_ok && k < g.K) {
-            if (g.qvec) {
-              __builtin_nontemporal_store(ow, (u32x4*)(Y + ybase + (int64_t)k * g.ys[1]));
-            } else {
-#pragma unroll
-              for (int u = 0; u < 8; ++u)
-                if ((yvalid >> u) & 1u) Y[yoff[u] + (int64_t)k * g.ys[1]] = (uint16_t)(ow[u >> 1] >> (16 * (u & 1)));
-            }
-          }
-        }
-      }
-    };
-    if (g.round_dtype == NT_DTYPE_F16)
-      finish(std::integral_constant<int, NT_DTYPE_F16>{});
-    else if (g.round_dtype == NT_DTYPE_BF16)
-      finish(std::integral_constant<int, NT_DTYPE_BF16>{});
-    else
-      finish(std::integral_constant<int, NT_DTYPE_NONE>{});
+    conv224_store<T, NB>(lds, acc, g, wave, lane, m0t, k0t);
   };
   if (wm == 0)
     body(std::integral_constant<int, 4>{});
   else
     body(std::integral_constant<int, 3>{});
+}
+
+// conv_dma224_kernel for 3 x 3 filters reading the N-C-H-W input itself, with no re-laid copy
+// of it.  A tile is TR = 224 / Q whole output rows of one image (stride 1, dilation 1), so
+// for one 32-channel block every tap (r, s) reads a window of the same srows = TR + 2 input
+// rows.  The workgroup keeps that block's rows in LDS as a strip [srows][pitch][32 channels],
+// zero outside the input (input column c at strip column c + pw), and reads the position
+// operand of tap (r, s) for output (t, w) at strip position (t + r) * pitch + w + s.  A strip
+// position takes 80 bytes (64 of data, 16 of padding) so that the 16 consecutive positions
+// of one ds_read_b128 pass land on distinct banks; pitch = Q + 16 keeps that so across a row
+// change.  Strips are double-buffered: during the nine k-tiles (taps) of block cb, block
+// cb + 1's rows arrive by DMA as NP raw pieces (512 lanes x 16 bytes of channel rows, w
+// fastest, so a wave reads runs of whole rows) on taps 0 .. NP - 1, and tap NP + 1 transposes
+// them into the other strip (per lane 8 positions x 2 channels: two ds_read_b128, eight
+// v_perm, eight ds_write_b32).  The filter operand (K-(C/32)-R-S-32, re-laid by
+// filter_cb_kernel before this kernel) runs through conv_dma224_kernel's four-stage DMA ring,
+// with its waits and barriers.  The nine taps of a block are unrolled, so tap offsets, piece
+// and transposition steps and the vmcnt budget of each barrier (2 filter loads per k-tile,
+// plus 1 after a k-tile that issued a piece) are constants: no division and no branch inside
+// a block.  LDS: filter ring [0, 64 KiB), two strips, NP raw pieces; the epilogue
+// (conv224_store) reuses all of it.
+namespace cstrip {
+constexpr int RING = 65536;   // the filter ring: four 16 KiB stages
+constexpr int SPOS = 80;      // bytes per strip position
+constexpr int PIECE = 8192;   // one raw piece: 512 lanes x 16 bytes
+constexpr int MAX_PIECES = 3;
+constexpr int LDS_BYTES = cdma::EPI + 8 * 4096;
+}  // namespace cstrip
+
+template <typename T, int NP>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void conv_strip224_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wt, ConvArgs g, int pitch, int srows) {
+  constexpr int TAPS = 9;
+  __shared__ __attribute__((aligned(1024))) char lds[cstrip::LDS_BYTES];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tile = (int)xcd_order(blockIdx.x, (int64_t)g.tiles_k * g.tiles_m);
+  const int tk = tile % g.tiles_k, tmi = tile / g.tiles_k;
+  const int k0t = tk * CB_K, m0t = tmi * CB_M224;
+  const int Q = (int)g.Q, PQ = (int)(g.P * g.Q);
+  const int n_img = m0t / PQ, p0 = (m0t - n_img * PQ) / Q;
+  const int KG = (int)g.KG, ncb = (int)g.C / 32;
+  const int wch = (int)g.W / 8, ntask = srows * 32 * wch;
+  const int row_bytes = pitch * cstrip::SPOS;
+  const int strip_bytes = srows * row_bytes;
+  const int strip0 = cstrip::RING, raw0 = cstrip::RING + 2 * strip_bytes;
+  // Byte offset of tap j's window inside a strip.
+  auto tap = [&](int j) { return (j / 3) * row_bytes + (j % 3) * cstrip::SPOS; };
+
+  // Filter ring loads, as conv_dma224_kernel's: rows 32 wave + 16 q + lane / 4, chunk lane % 4.
+  const u32x4 rsW = cdma::rsrc(wt + (int64_t)k0t * KG, (uint32_t)((g.K - k0t) * KG * 2));
+  int vw[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int row = 32 * wave + 16 * q + (lane >> 2);
+    vw[q] = (row * KG + cdma::asw(row, lane & 3) * 8) * 2;
+  }
+  auto load_filter = [&](int q, int kt) {
+    cdma::load_lds16(rsW, lds0 + (kt & 3) * cdma::STAGE + 2048 * wave + 1024 * q, vw[q], kt * 64);
+  };
+  // Raw pieces: lane tid of piece j fetches chunk e = 512 j + tid, e = ((row * 32 + c) * wch + wc),
+  // input row p0 - ph + row, channel 32 cb + c (cb in the scalar offset), w 8 wc .. 8 wc + 7;
+  // rows outside the input (and e past the strip) point at the resource's end and read zeros.
+  const uint32_t img_bytes = (uint32_t)(((g.C - 1) * g.xs[1] + (g.H - 1) * g.xs[2] + g.W) * 2);
+  const u32x4 rsX = cdma::rsrc(x + (int64_t)n_img * g.xs[0], img_bytes);
+  const int cb_bytes = (int)(32 * g.xs[1] * 2);
+  int vp[NP];
+#pragma unroll
+  for (int j = 0; j < NP; ++j) {
+    const int e = j * 512 + tid;
+    vp[j] = (int)img_bytes;
+    if (e < ntask) {
+      const int wc = e % wch, rc = e / wch;
+      const int c = rc & 31, in_row = p0 - (int)g.ph + (rc >> 5);
+      if (in_row >= 0 && in_row < (int)g.H) vp[j] = (int)((c * g.xs[1] + in_row * g.xs[2] + wc * 8) * 2);
+    }
+  }
+  auto load_piece = [&](int j, int cb) {
+    cdma::load_lds16(rsX, lds0 + raw0 + j * cstrip::PIECE + 1024 * wave, vp[j], cb * cb_bytes);
+  };
+  // Transposition: task u = tid + 512 h (h = 0, 1) of ntask / 2 takes channels 2 cp, 2 cp + 1 of
+  // strip row `row`, w 8 wc .. 8 wc + 7 (cp fastest, so 16 lanes fill one position's 64 bytes).
+  int tr_raw[2], tr_dst[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int u = tid + 512 * h;
+    tr_raw[h] = tr_dst[h] = -1;
+    if (u < ntask / 2) {
+      const int cp = u & 15, rw = u >> 4;
+      const int wc = rw % wch, row = rw / wch;
+      tr_raw[h] = raw0 + ((row * 32 + 2 * cp) * wch + wc) * 16;
+      tr_dst[h] = (row * pitch + (int)g.pw + wc * 8) * cstrip::SPOS + cp * 4;
+    }
+  }
+  auto tr_read = [&](int h, u32x4& a, u32x4& b) {
+    if (tr_raw[h] >= 0) {
+      a = *(const u32x4*)(lds + tr_raw[h]);
+      b = *(const u32x4*)(lds + tr_raw[h] + wch * 16);
+    }
+  };
+  auto tr_write = [&](int h, const u32x4& a, const u32x4& b, int strip) {
+    if (tr_dst[h] >= 0) {
+      char* d = lds + strip + tr_dst[h];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        *(uint32_t*)(d + i * cstrip::SPOS) =
+            __builtin_amdgcn_perm(b[i >> 1], a[i >> 1], (i & 1) ? 0x07060302u : 0x05040100u);
+    }
+  };
+
+  // Prologue: strip 0's pieces, filter tiles 0..2; pieces and tile 0 landed (vmcnt 4: tiles 1
+  // and 2 may still fly); strip 0 transposed, the pad columns of both strips zeroed.
+#pragma unroll
+  for (int j = 0; j < NP; ++j) load_piece(j, 0);
+  for (int kt = 0; kt < 3; ++kt) {
+    load_filter(0, kt);
+    load_filter(1, kt);
+  }
+  asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  {
+    u32x4 a = {0u, 0u, 0u, 0u}, b = a;
+    tr_read(0, a, b);
+    tr_write(0, a, b, strip0);
+    tr_read(1, a, b);
+    tr_write(1, a, b, strip0);
+  }
+  {
+    const int padc = pitch - (int)g.W, chunks = 2 * srows * padc * 4;
+    for (int e = tid; e < chunks; e += 512) {
+      const int ch = e & 3, rest = e >> 2;
+      const int col = rest % padc, rb = rest / padc;  // rb = strip buffer * srows + row
+      const int c = col < (int)g.pw ? col : col + (int)g.W;
+      const int buf = rb / srows, row = rb - buf * srows;
+      *(u32x4*)(lds + strip0 + buf * strip_bytes + (row * pitch + c) * cstrip::SPOS + ch * 16) = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  __syncthreads();
+
+  const int wk = wave & 3, wm = wave >> 2;
+  auto body = [&](auto nb_c) {
+    constexpr int NB = decltype(nb_c)::value;  // 32-position blocks of this wave
+    // Fragment reads: filter rows 64 wk + 32 i + lane % 32 of the ring; positions 128 wm +
+    // 32 j + lane % 32 = output (t, w) of the strip, channels 16 s2 + 8 (lane / 32) .. + 7.
+    int a_rd[2], pb[NB];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const int ra = wk * 64 + (lane & 31);
+      a_rd[s2] = ra * 64 + cdma::asw(ra, 2 * s2 + (lane >> 5)) * 16;
+    }
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int m = wm * 128 + 32 * j + (lane & 31);
+      const int t = m / Q, w = m - t * Q;
+      pb[j] = (t * pitch + w) * cstrip::SPOS + (lane >> 5) * 16;
+    }
+    typedef typename mfma_traits<T>::frag frag;
+    frag fa[2][2], fb[2][NB];
+    // Unit u (0..NB+1) of slice s2 of the k-tile at ring stage st and position offset po:
+    // a0, b0 .. b(NB-1), a1.
+    auto read_unit = [&](int u, int s2, int st, int po) {
+      if (u == 0)
+        fa[s2][0] = *(const frag*)(lds + a_rd[s2] + st);
+      else if (u == NB + 1)
+        fa[s2][1] = *(const frag*)(lds + a_rd[s2] + st + 2048);
+      else
+        fb[s2][u - 1] = *(const frag*)(lds + pb[u - 1] + po + s2 * 32);
+    };
+    floatx16 acc[2][NB];
+    zero_acc(acc);
+#pragma unroll
+    for (int u = 0; u < NB + 2; ++u) read_unit(u, 0, 0, strip0);
+
+#define NT_CFENCE() __builtin_amdgcn_sched_barrier(0)
+    // Tap J of channel block cb (k-tile kt = 9 cb + J).  HAS1 reads slice 0 of the next k-tile
+    // during slice 1, LOAD fetches filter tile kt + 3, VM is the number of loads allowed in
+    // flight at the barrier (-1: the last k-tile, no wait and no barrier), NEXT: a block
+    // follows whose strip this block fetches and transposes.
+    auto step = [&](auto j_c, auto has1_c, auto load_c, auto vm_c, auto next_c, int cb) {
+      constexpr int J = decltype(j_c)::value, VM = decltype(vm_c)::value;
+      constexpr bool HAS1 = decltype(has1_c)::value, LOAD = decltype(load_c)::value;
+      constexpr bool NEXT = decltype(next_c)::value;
+      constexpr bool PIECE = NEXT && J < NP, TRANS = NEXT && J == NP + 1;
+      const int kt = cb * TAPS + J;
+      const int st = (kt & 3) * cdma::STAGE, st1 = ((kt + 1) & 3) * cdma::STAGE;
+      const int sb = strip0 + (cb & 1) * strip_bytes, sbn = strip0 + ((cb + 1) & 1) * strip_bytes;
+      const int po = sb + tap(J), po1 = J + 1 < TAPS ? sb + tap(J + 1) : sbn;
+      u32x4 ta = {0u, 0u, 0u, 0u}, tb = ta;
+      static_for<0, 4 * NB>([&](auto m_c) {
+        constexpr int m = decltype(m_c)::value;
+        constexpr int s2 = m / (2 * NB), x = m % (2 * NB);
+        if constexpr (m == 2 * NB && VM >= 0) {
+          NT_CFENCE();
+          if constexpr (VM == 3) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
+          if constexpr (VM == 2) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+          if constexpr (VM == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+          __builtin_amdgcn_s_barrier();
+          NT_CFENCE();
+        }
+        acc[x / NB][x % NB] = mfma_traits<T>::mma(fa[s2][x / NB], fb[s2][x % NB], acc[x / NB][x % NB]);
+        NT_CFENCE();
+        if constexpr (x < NB + 2) {
+          if constexpr (s2 == 0)
+            read_unit(x, 1, st, po);
+          else if constexpr (HAS1)
+            read_unit(x, 0, st1, po1);
+        }
+        if constexpr (s2 == 1 && LOAD && x < 2) load_filter(x, kt + 3);
+        if constexpr (s2 == 1 && PIECE && x == 2) load_piece(J, cb + 1);
+        if constexpr (s2 == 1 && TRANS && (x == 0 || x == 3)) tr_read(x == 0 ? 0 : 1, ta, tb);
+        if constexpr (s2 == 1 && TRANS && x == 2) tr_write(0, ta, tb, sbn);
+        if constexpr (s2 == 1 && TRANS && x == 5) {
+          tr_write(1, ta, tb, sbn);
+          // The next barrier can come before any LDS read issued after these writes has
+          // been waited for, and a barrier alone does not wait for LDS operations.
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        }
+        NT_CFENCE();
+      });
+    };
+#undef NT_CFENCE
+    using T1 = std::integral_constant<bool, true>;
+    using F1 = std::integral_constant<bool, false>;
+    using V3 = std::integral_constant<int, 3>;
+    using V2 = std::integral_constant<int, 2>;
+    using V0 = std::integral_constant<int, 0>;
+    using VN = std::integral_constant<int, -1>;
+    int cb = 0;
+    for (; cb + 1 < ncb; ++cb) {
+      static_for<0, TAPS>([&](auto j_c) {
+        constexpr int J = decltype(j_c)::value;
+        // taps 1 .. NP follow a tap that issued a piece
+        using VM = std::conditional_t<(J >= 1 && J <= NP), V3, V2>;
+        step(j_c, T1{}, T1{}, VM{}, T1{}, cb);
+      });
+    }
+    static_for<0, TAPS - 3>([&](auto j_c) { step(j_c, T1{}, T1{}, V2{}, F1{}, cb); });
+    step(std::integral_constant<int, TAPS - 3>{}, T1{}, F1{}, V2{}, F1{}, cb);
+    step(std::integral_constant<int, TAPS - 2>{}, T1{}, F1{}, V0{}, F1{}, cb);
+    step(std::integral_constant<int, TAPS - 1>{}, F1{}, F1{}, VN{}, F1{}, cb);
+    conv224_store<T, NB>(lds, acc, g, wave, lane, m0t, k0t);
+  };
+  if (wm == 0)
+    body(std::integral_constant<int, 4>{});
+  else
+    body(std::integral_constant<int, 3>{});
+}
+
+// The filter w (K-C-R-S, any strides) into K-(C/32)-R-S-32 for the strip kernel (C % 32 == 0):
+// one lane per 8 consecutive values of the destination (one output channel k, channel block
+// cb, tap rs, channels 8 (e % 4) .. + 7 of the block), gathered with eight loads and stored
+// as one 16-byte vector.  One round of loads per lane: the kernel is as short as its latency.
+template <typename T>
+__global__ __launch_bounds__(256) void filter_cb_kernel(const uint16_t* __restrict__ w, uint16_t* __restrict__ wt,
+                                                        ConvArgs g) {
+  const int KG8 = (int)(g.KG / 8), RS = (int)(g.R * g.S), S = (int)g.S;
+  const int64_t chunks = g.K * KG8;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < chunks; e += (int64_t)gridDim.x * 256) {
+    const int64_t k = e / KG8;
+    const int ce = (int)(e - k * KG8), cbrs = ce >> 2;
+    const int cb = cbrs / RS, rs = cbrs - cb * RS;
+    const int c = cb * 32 + (ce & 3) * 8, r = rs / S, s = rs - r * S;
+    const uint16_t* src = w + k * g.ws[0] + c * g.ws[1] + r * g.ws[2] + s * g.ws[3];
+    uint16_t v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = src[i * g.ws[1]];
+    *(u32x4*)(wt + e * 8) = *(const u32x4*)v;
+  }
 }
 
 // Sum of conv_dma_kernel's split partials: one lane per 8 consecutive output positions of
@@ -1145,9 +1424,10 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
                        int config = 0) {
   // config: 0 = the fastest path whose conditions hold; 1 = re-laid input through the DMA
   // kernel, 2 = re-laid input through conv_nhwc_kernel, 3 = the direct kernel (no
-  // workspace), 4 = re-laid input through the DMA kernel of 224-position tiles.  A forced
-  // path whose conditions do not hold is rejected before launching.
-  if (config < 0 || config > 4) return NT_ERR_INVALID;
+  // workspace), 4 = re-laid input through the DMA kernel of 224-position tiles, 5 = the
+  // input read in place by conv_strip224_kernel (only the filter re-laid).  A forced path
+  // whose conditions do not hold is rejected before launching.
+  if (config < 0 || config > 5) return NT_ERR_INVALID;
   if (N < 0 || C < 0 || H < 0 || W < 0 || K < 0 || R < 0 || S < 0 || P < 0 || Q < 0 || ph < 0 || pw < 0 || sh <= 0 ||
       sw <= 0 || dh <= 0 || dw <= 0)
     return NT_ERR_INVALID;
@@ -1189,6 +1469,48 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
   // Its output as 16-byte runs of 8 positions of one channel, or else element by element.
   g.qvec = Q % 8 == 0 && ys[3] == 1 && ys[0] % 8 == 0 && ys[1] % 8 == 0 && ys[2] % 8 == 0 && (uintptr_t)y % 16 == 0;
   g.Mp = cdiv(g.M, 8) * 8;
+  // conv_strip224_kernel: a 3 x 3 filter, whole output rows per 224-position tile (Q divides
+  // 224, the tile's TR rows divide P), stride and dilation 1, 32-channel blocks, input rows of
+  // unit w stride in 16-byte chunks (W % 8 == 0, 16-byte aligned), a strip row of Q + 16
+  // positions that holds the padded input row, two or three raw pieces per strip, strips and
+  // pieces inside LDS beside the filter ring, 32-bit offsets; the re-laid filter in the
+  // workspace.
+  const int64_t strip_pitch = Q + 16;
+  const int64_t strip_rows = Q > 0 && 224 % Q == 0 ? 224 / Q + R - 1 : 0;
+  int64_t strip_np = 0;
+  const bool strip = [&] {
+    if (R != 3 || S != 3 || strip_rows == 0 || P % (224 / Q) != 0 || sh != 1 || sw != 1 || dh != 1 || dw != 1)
+      return false;
+    if (C % 32 != 0 || y_dtype != elem<T>::code) return false;
+    if (xs[3] != 1 || W % 8 != 0 || (uintptr_t)x % 16 != 0 || xs[0] < 0 || xs[1] < 0 || xs[2] < 0 || xs[0] % 8 != 0 ||
+        xs[1] % 8 != 0 || xs[2] % 8 != 0)
+      return false;
+    if (Q + S - 1 > strip_pitch || pw + W > strip_pitch) return false;
+    strip_np = cdiv(strip_rows * 32 * (W / 8), 512);
+    if (strip_np < 2 || strip_np > cstrip::MAX_PIECES) return false;
+    if (cstrip::RING + 2 * strip_rows * strip_pitch * cstrip::SPOS + strip_np * cstrip::PIECE > cstrip::LDS_BYTES)
+      return false;
+    if (((C - 1) * xs[1] + (H - 1) * xs[2] + W) * 2 >= 0x7fffffffLL || K * C * R * S * 2 >= 0x7fffffffLL ||
+        g.M >= 0x7fffffffLL || tiles_k * (g.M / 224) > 0x7fffffffLL)
+      return false;
+    return workspace != nullptr && (uintptr_t)workspace % 256 == 0 && workspace_bytes >= K * C * R * S * 2;
+  }();
+  if (config == 5 && !strip) return NT_ERR_INVALID;
+  if (strip && (config == 0 || config == 5)) {
+    g.cb_order = 1;
+    g.tiles_m = (int)(g.M / 224);
+    uint16_t* wt = (uint16_t*)workspace;
+    const int64_t fchunks = K * (g.KG / 8), fblocks = cdiv(fchunks, 256) < 16384 ? cdiv(fchunks, 256) : 16384;
+    hipLaunchKernelGGL(filter_cb_kernel<T>, dim3((unsigned)fblocks), dim3(256), 0, stream, (const uint16_t*)w, wt, g);
+    const dim3 grid((unsigned)(tiles_k * g.tiles_m));
+    if (strip_np == 2)
+      hipLaunchKernelGGL((conv_strip224_kernel<T, 2>), grid, dim3(512), 0, stream, (const uint16_t*)x,
+                         (const uint16_t*)wt, g, (int)strip_pitch, (int)strip_rows);
+    else
+      hipLaunchKernelGGL((conv_strip224_kernel<T, 3>), grid, dim3(512), 0, stream, (const uint16_t*)x,
+                         (const uint16_t*)wt, g, (int)strip_pitch, (int)strip_rows);
+    return launch_status();
+  }
   const int64_t C32 = dma_channels(C, R, S), C64 = cdiv(C, 64) * 64;
   const bool dma = config != 2 && dma_fits(C32);
   const int64_t Cl = dma ? C32 : C64;

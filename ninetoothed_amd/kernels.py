@@ -376,8 +376,8 @@ def conv2d_workspace_bytes(x, w, padding=(0, 0)):
 # Paths of the 16-bit convolution that ``config`` can force (0: the fastest whose conditions
 # hold): re-laid input through the DMA kernel, re-laid input through the N-H-W-C kernel,
 # the direct kernel (no workspace), re-laid input through the DMA kernel of 224-position
-# tiles.
-CONV_CONFIGS = (1, 2, 3, 4)
+# tiles, the input read in place by the 224-position strip kernel (only the filter re-laid).
+CONV_CONFIGS = (1, 2, 3, 4, 5)
 
 
 def check_conv2d(x, w, y, round_dtype=None, config=0):

@@ -705,18 +705,91 @@ def test_conv2d_dma224(case, dtype):
 
 def test_conv2d_headline_takes_224_tiles():
     # [16,256,56,56] * [256,256,3,3]: 196 tiles of 256 positions or 224 of 224, one round of
-    # 256 CUs either way; the default path takes the 224-position kernel and agrees with
-    # the 256-position one bit for bit (same k order, same fp32 sums).
+    # 256 CUs either way; the default path takes the 224-position strip kernel (input read
+    # in place) and agrees bit for bit with the 224- and 256-position kernels over the
+    # re-laid input (same k order, same fp32 sums).
     x = _randn((16, 256, 56, 56), torch.float16, 43)
     w = _randn((256, 256, 3, 3), torch.float16, 44, 1.0 / math.sqrt(256 * 9))
     ws = _workspace(x, w, (1, 1))
-    y0, y1, y4 = (torch.empty_like(x) for _ in range(3))
+    y0, y1, y4, y5 = (torch.empty_like(x) for _ in range(4))
     kernels.conv2d(x, w, y0, padding=(1, 1), workspace=ws)
     kernels.conv2d(x, w, y1, padding=(1, 1), workspace=ws, config=1)
     kernels.conv2d(x, w, y4, padding=(1, 1), workspace=ws, config=4)
-    assert torch.equal(y0, y4) and torch.equal(y1, y4)
+    kernels.conv2d(x, w, y5, padding=(1, 1), workspace=ws, config=5)
+    assert torch.equal(y0, y5) and torch.equal(y1, y4) and torch.equal(y4, y5)
     ref = F.conv2d(x.float(), w.float(), padding=1)
-    assert torch.allclose(y4.float(), ref, atol=1e-2, rtol=1e-2)
+    assert torch.allclose(y5.float(), ref, atol=1e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+@pytest.mark.parametrize("case", (
+    # (N, C, H, W), K, padding, input channel offset in a wider tensor, filter layout: the
+    # strip kernel (config 5, 3 x 3 filters) against torch and, bit for bit, the re-laid
+    # 224-position kernel (config 4).  Q = 56 / 16 / 32 (4, 14 and 7 output rows per tile),
+    # two and three raw pieces per strip, one channel block, K no multiple of 256, no row
+    # padding and two rows of it, an input that is a channel slice of a wider tensor (image
+    # stride past C * H * W), and a filter whose rows are not contiguous (re-laid by gathers).
+    ((3, 96, 56, 56), 64, (1, 1), 0, "dense"),
+    ((2, 64, 14, 16), 96, (1, 1), 0, "dense"),
+    ((1, 32, 14, 32), 200, (1, 1), 0, "dense"),
+    ((2, 64, 58, 56), 32, (0, 1), 0, "dense"),
+    ((1, 64, 54, 56), 40, (2, 1), 0, "dense"),
+    ((2, 64, 56, 56), 300, (1, 1), 32, "dense"),
+    ((2, 64, 56, 56), 96, (1, 1), 0, "krsc"),
+))
+def test_conv2d_strip224(case, dtype):
+    (n, c, h, w_), k, padding, c_off, layout = case
+    big = _randn((n, c + 2 * c_off, h, w_), dtype, 45)
+    x = big[:, c_off:c_off + c]
+    if layout == "dense":
+        w = _randn((k, c, 3, 3), dtype, 46, 1.0 / math.sqrt(c * 9))
+    else:
+        w = _randn((k, 3, 3, c), dtype, 46, 1.0 / math.sqrt(c * 9)).permute(0, 3, 1, 2)
+    ref = F.conv2d(x.float(), w.float(), padding=padding)
+    ws = _workspace(x, w, padding)
+    y5 = torch.full(ref.shape, 7.0, dtype=dtype, device=DEV)
+    y4 = torch.full(ref.shape, 7.0, dtype=dtype, device=DEV)
+    kernels.conv2d(x, w, y5, padding=padding, workspace=ws, config=5)
+    kernels.conv2d(x, w, y4, padding=padding, workspace=ws, config=4)
+    assert torch.allclose(y5.float(), ref, atol=2e-2, rtol=1e-2)
+    assert torch.equal(y5, y4)
+
+
+def test_conv2d_strip224_reads_each_calls_filter():
+    # Calls that reuse one workspace (which holds the re-laid filter) with a new filter each
+    # time, back to back on one stream, must each see their own filter.
+    x = _randn((16, 256, 56, 56), torch.float16, 50)
+    ws = _workspace(x, torch.empty((256, 256, 3, 3), dtype=torch.float16, device=DEV), (1, 1))
+    filters = [_randn((256, 256, 3, 3), torch.float16, 51 + i, 1.0 / math.sqrt(256 * 9)) for i in range(3)]
+    ys = [torch.empty_like(x) for _ in filters]
+    for w, y in zip(filters, ys):
+        kernels.conv2d(x, w, y, padding=(1, 1), workspace=ws, config=5)
+    for w, y in zip(filters, ys):
+        y4 = torch.empty_like(x)
+        kernels.conv2d(x, w, y4, padding=(1, 1), workspace=ws, config=4)
+        assert torch.equal(y, y4)
+
+
+def test_conv2d_strip224_rejects_unfit_calls():
+    from ninetoothed_amd.errors import KernelLaunchError
+
+    def call(xshape, wshape, padding=(1, 1), stride=(1, 1), x=None):
+        x = _randn(xshape, torch.float16, 47) if x is None else x
+        w = _randn((wshape[0], x.shape[1], *wshape[1:]), torch.float16, 48, 0.05)
+        ref_shape = F.conv2d(x[:1, :, :, :].float().cpu(), w.float().cpu(), padding=padding, stride=stride).shape
+        y = torch.full((x.shape[0], *ref_shape[1:]), 7.0, dtype=torch.float16, device=DEV)
+        with pytest.raises(KernelLaunchError):
+            kernels.conv2d(x, w, y, padding=padding, stride=stride, workspace=_workspace(x, w, padding), config=5)
+        assert torch.all(y == 7.0)
+
+    call((2, 64, 16, 16), (32, 3, 3))               # Q = 16, 14 rows per tile do not divide P = 16
+    call((2, 48, 56, 56), (32, 3, 3))               # C % 32 != 0
+    call((2, 64, 58, 58), (32, 3, 3), (0, 0))       # Q = 56, but W = 58 is no multiple of 8
+    call((2, 64, 112, 112), (32, 3, 3), stride=(2, 2))  # stride 2
+    call((1, 64, 56, 56), (32, 5, 5), (2, 2))       # a 5 x 5 filter
+    call((1, 64, 56, 56), (32, 1, 1), (0, 0))       # a 1 x 1 filter
+    xt = _randn((2, 64, 56, 56), torch.float16, 49).transpose(2, 3)  # w stride 56
+    call(None, (32, 3, 3), x=xt)
 
 
 @pytest.mark.parametrize("flip", ("w", "h"))
@@ -795,7 +868,7 @@ def test_conv2d_forced_path_rejects_unfit_call():
     x = _randn((2, 24, 16, 16), torch.float16, 62)  # no workspace: no re-laid path
     w = _randn((40, 24, 3, 3), torch.float16, 63, 0.1)
     y = torch.full((2, 40, 14, 14), 7.0, dtype=torch.float16, device=DEV)
-    for config in (1, 2, 4):
+    for config in (1, 2, 4, 5):
         with pytest.raises(KernelLaunchError):
             kernels.conv2d(x, w, y, config=config)
     assert torch.all(y == 7.0)
