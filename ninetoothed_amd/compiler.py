@@ -17,7 +17,7 @@ import copy
 import inspect
 from dataclasses import dataclass, field, replace
 
-from ninetoothed_amd import families, frontend
+from ninetoothed_amd import families, frontend, jagged
 from ninetoothed_amd.backends import default_registry
 from ninetoothed_amd.backends.materializers import materializer_for
 from ninetoothed_amd.errors import LoweringError
@@ -55,6 +55,7 @@ class ParamSpec:
     constexpr: bool
     shape_symbols: tuple  # (symbol name or None) per source dim
     constexpr_value: object = None  # fixed at definition (``Tensor(0, constexpr=True, value=...)``)
+    jagged_dim: object = None  # the ragged dim of a jagged source (ninetoothed_amd.jagged), else None
 
 
 @dataclass
@@ -175,7 +176,9 @@ class KernelProgram:
         for spec in self.param_specs:
             if spec.source_ndim == 0:
                 continue
-            for name, size in zip(spec.shape_symbols, public[spec.name].shape):
+            value = public[spec.name]
+            shape = jagged.padded_shape(value) if jagged.is_jagged(value) else value.shape
+            for name, size in zip(spec.shape_symbols, shape):
                 if name is not None:
                     env[name] = int(size)
         shape_names = set(env)
@@ -356,6 +359,7 @@ def compile_kernel(request):
             constexpr=bool(source.constexpr),
             shape_symbols=_shape_symbol_names(source),
             constexpr_value=source.value if source.constexpr else None,
+            jagged_dim=getattr(source, "jagged_dim", None),
         ))
         if source.ndim:
             symbols.update(t.symbols())

@@ -25,6 +25,7 @@ import math
 
 import numpy as np
 
+from ninetoothed_amd import jagged
 from ninetoothed_amd.errors import LoweringError
 from ninetoothed_amd.frontend import Value
 
@@ -1026,6 +1027,15 @@ def match_generic(ctx):
 FAMILIES = (match_attention, match_gemm, match_softmax, match_max_pool2d, match_add, match_generic)
 
 
+def _families_for(ctx):
+    """The families a call may take: a call with a jagged tensor takes the generic kernels,
+    whose index tables follow each batch's rows (ninetoothed_amd.jagged); the hand-written
+    kernels address strided tensors only."""
+    if any(jagged.is_jagged(v) for v in ctx.values.values()):
+        return (match_generic,)
+    return FAMILIES
+
+
 def candidates(ctx):
     """Every family plan whose pattern and geometry fit, in the order ``select`` tries them.
 
@@ -1041,7 +1051,7 @@ def candidates(ctx):
     from ninetoothed_amd import kernels
 
     plans = []
-    for matcher in FAMILIES:
+    for matcher in _families_for(ctx):
         try:
             plan = matcher(ctx)
             if plan is not None:
@@ -1137,7 +1147,7 @@ def select(ctx):
     declined too; the next families are still tried (an elementwise program the add kernel
     cannot take runs on the generic kernels) and the reasons are reported if none fits."""
     tried, reasons = [], []
-    for matcher in FAMILIES:
+    for matcher in _families_for(ctx):
         name = matcher.__name__[len("match_"):]
         try:
             plan = matcher(ctx)

@@ -45,7 +45,7 @@ import threading
 
 import numpy as np
 
-from ninetoothed_amd import _lib
+from ninetoothed_amd import _lib, jagged
 from ninetoothed_amd.errors import KernelLaunchError, LoweringError
 from ninetoothed_amd.frontend import Value, effect_targets
 from ninetoothed_amd.frontend import pointer_param as frontend_pointer_param
@@ -582,9 +582,12 @@ class GenericPlan:
     def _table(self, name, tensor, maps=None):
         idx, mask, shape = maps or self._maps(name)
         total = int(np.prod(shape)) if shape else 1
-        off = np.zeros((), dtype=np.int64)
-        for i, st in zip(idx, tensor.stride()):
-            off = off + np.asarray(i, dtype=np.int64) * int(st)
+        if jagged.is_jagged(tensor):  # offsets into values(), masked past each batch's rows
+            off, mask = jagged.element_offsets(tensor, idx, mask)
+        else:
+            off = np.zeros((), dtype=np.int64)
+            for i, st in zip(idx, tensor.stride()):
+                off = off + np.asarray(i, dtype=np.int64) * int(st)
         off = np.broadcast_to(np.where(mask, off, -1), shape).reshape(-1)
         if off.size and off.max() >= 2**31:
             raise LoweringError("the generic kernels address at most 2^31 elements of a tensor")
@@ -680,7 +683,7 @@ class GenericPlan:
 
         def launch(args):
             for p, slot in ptrs:
-                slot.value = args[p].data_ptr()
+                slot.value = jagged.data_ptr(args[p])
             for p, slot, kind in svals.values():
                 v = args[p]
                 v = v.item() if hasattr(v, "item") else v
@@ -1687,10 +1690,7 @@ class TilePlan(GenericPlan):
 
     def extent(self, name):
         """Elements from a tensor's first to one past its last element (its storage span)."""
-        t = self.ctx.values[name]
-        if t.numel() == 0:
-            return 0
-        return 1 + sum((int(n) - 1) * int(st) for n, st in zip(t.shape, t.stride()))
+        return jagged.storage_extent(self.ctx.values[name])
 
     _ATOMIC = {"float32": "float", "float64": "double", "int32": "int"}
 

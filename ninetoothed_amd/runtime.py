@@ -24,6 +24,7 @@ to the bound launcher (which reads data pointers, scalars and the current stream
 
 import threading
 
+from ninetoothed_amd import jagged
 from ninetoothed_amd.dtype import normalize_dtype
 
 try:  # the call key in C++ (csrc/fastkey.cpp, built by ninetoothed_amd._build); else built in Python
@@ -116,6 +117,8 @@ class Handle:
             if not self._all_tensors:
                 key = (key, tuple([v if kind == 1 else type(v) for v, kind in zip(args, self._kinds) if kind != 0]))
         else:
+            if any(getattr(args[i], "is_nested", False) for i in self._tensor_pos):
+                raise TypeError("a nested tensor")  # jagged calls take the full path every time
             key = tuple([
                 (v.dtype, v.shape, v.stride(), v.get_device(), v.data_ptr() & 15) if kind == 0
                 else (v if kind == 1 else type(v))
@@ -159,6 +162,14 @@ class Handle:
                 raise TypeError(f"Kernel argument `{spec.name}` must be a tensor.")
             if len(shape) != spec.source_ndim:
                 raise TypeError(f"Kernel argument `{spec.name}` has rank {len(shape)}; expected {spec.source_ndim}.")
+            if jagged.is_jagged(value) or getattr(value, "is_nested", False) or spec.jagged_dim is not None:
+                if spec.jagged_dim is None or not jagged.is_jagged(value) or jagged.ragged_dim(value) != spec.jagged_dim:
+                    raise TypeError(
+                        f"Kernel argument `{spec.name}` must be "
+                        + (f"a jagged nested tensor ragged in dimension {spec.jagged_dim}." if spec.jagged_dim is not None
+                           else "a strided tensor (its Tensor has no `jagged_dim`).")
+                    )
+                shape = jagged.padded_shape(value)
             for axis, (actual, expected) in enumerate(zip(shape, spec.static_shape)):
                 if expected is not None and actual != expected:
                     raise TypeError(
@@ -183,6 +194,9 @@ class Handle:
             v = public[spec.name]
             if spec.source_ndim == 0:
                 parts.append((spec.name, v if spec.constexpr else type(v).__name__))
+            elif jagged.is_jagged(v):
+                # the plan depends on the padded shape; index tables are built per call
+                parts.append((spec.name, v.dtype, "jagged", jagged.padded_shape(v), v.values().stride()))
             else:
                 parts.append((spec.name, v.dtype, tuple(v.shape), v.stride()))
         parts.append(tuple(sorted(meta.items())))

@@ -148,9 +148,12 @@ class Tensor:
             for i, (size, opts) in enumerate(zip(shape, shape_options))
         )
         self.dtype = dtype
+        # A jagged source (reference src/ninetoothed/tensor.py:17-45): dim `jagged_dim` varies
+        # across the batch (dim 0); it is bound to a torch nested tensor of the jagged layout
+        # (ninetoothed_amd.jagged), its size to the call's longest batch.
+        if jagged_dim is not None and not (isinstance(jagged_dim, int) and 1 <= jagged_dim < ndim):
+            raise ValueError("`jagged_dim` must be a dimension after the batch dimension (1 .. ndim - 1).")
         self.jagged_dim = jagged_dim
-        if jagged_dim is not None:
-            raise NotImplementedError("jagged tensors are outside the MI355X backend's hot path")
         self.other = other
         if constexpr and self.ndim != 0:
             raise ValueError("The `constexpr` option can only be set for zero-dimensional tensors.")
