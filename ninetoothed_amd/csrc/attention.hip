@@ -423,23 +423,33 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
   const uint16_t* Q = (const uint16_t*)g.q + b * g.qs[0] + h * g.qs[1];
 
   // Q^T fragments of this lane's queries (one per block), pre-scaled and rounded to the
-  // input type.
+  // input type.  The raw rows are loaded here and scaled only once the first key tile's
+  // loads are in flight too, so that the two fetches share one memory latency.
   int qpos[QB];
   frag qf[QB][G::DSUB];
+  u32x4 qraw[QB][G::DSUB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     qpos[qb] = qw + qb * 32 + (lane & 31);
 #pragma unroll
     for (int dd = 0; dd < G::DSUB; ++dd) {
-      u32x4 raw = {0u, 0u, 0u, 0u};
-      if (qpos[qb] < g.Sq && dd * 16 + half * 8 < D) raw = *(const u32x4*)(Q + (int64_t)qpos[qb] * g.qs[2] + dd * 16 + half * 8);
-      uint16_t tmp[8];
-      const uint16_t* hv = (const uint16_t*)&raw;
-#pragma unroll
-      for (int u = 0; u < 8; ++u) tmp[u] = elem<T>::from_float(elem<T>::to_float(hv[u]) * g.q_scale);
-      qf[qb][dd] = __builtin_bit_cast(frag, *(const u32x4*)tmp);
+      qraw[qb][dd] = u32x4{0u, 0u, 0u, 0u};
+      if (qpos[qb] < g.Sq && dd * 16 + half * 8 < D)
+        qraw[qb][dd] = *(const u32x4*)(Q + (int64_t)qpos[qb] * g.qs[2] + dd * 16 + half * 8);
     }
   }
+  auto scale_q = [&]() {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+      for (int dd = 0; dd < G::DSUB; ++dd) {
+        uint16_t tmp[8];
+        const uint16_t* hv = (const uint16_t*)&qraw[qb][dd];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) tmp[u] = elem<T>::from_float(elem<T>::to_float(hv[u]) * g.q_scale);
+        qf[qb][dd] = __builtin_bit_cast(frag, *(const u32x4*)tmp);
+      }
+  };
 
   // Tile loaders, 256 lanes per operand: with four waves every lane fetches both K and V;
   // with eight, waves 0-3 fetch K and waves 4-7 fetch V (lane index lt within the 256).
@@ -528,8 +538,9 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
   int nkt = (Sk + AT_BN - 1) / AT_BN;
   if (g.causal) nkt = min(nkt, (q0 + BM - 1) / AT_BN + 1);
 
+  if (nkt > 0) load_tile(0);
+  scale_q();
   if (nkt > 0) {
-    load_tile(0);
     store_tile(0);
     if (nkt > 1) load_tile(1);
   }
@@ -673,7 +684,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 #pragma unroll
         for (int r = 0; r < 16; ++r)
           stage[(lane & 31) * ST + jb * 32 + acc_row(r, lane)] = o_acc[qb][ps * 2 + jb][r] * inv;
-      __syncthreads();
+      wave_lds_order();  // a wave reads back only its own staging rows
 #pragma unroll
       for (int e0 = 0; e0 < 32 * 16; e0 += 64) {
         const int e = e0 + lane;
@@ -691,7 +702,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
           }
         }
       }
-      __syncthreads();
+      wave_lds_order();  // the next slice rewrites the staging rows after these reads
     }
   }
 }
