@@ -137,7 +137,8 @@ class _Alias:
 
 _NTL_BY_ID = {id(getattr(ntl, name)): name for name in ntl._FUNCTIONS}
 _NTL_BY_ID.update({id(getattr(ntl.libdevice, name)): f"libdevice.{name}" for name in ntl.libdevice.FUNCTIONS})
-_DTYPE_NAMES = {"float16", "bfloat16", "float32", "float64", "int8", "int16", "int32", "int64", "uint8"}
+_DTYPE_NAMES = {"float8_e4m3fn", "float8_e5m2", "float16", "bfloat16", "float32", "float64", "int8", "int16", "int32",
+                "int64", "uint8"}
 
 _BINOPS = {ast.Add: "add", ast.Sub: "sub", ast.Mult: "mul", ast.Div: "div", ast.FloorDiv: "floordiv", ast.Mod: "mod"}
 _CMPOPS = {ast.Lt: "lt", ast.LtE: "le", ast.Gt: "gt", ast.GtE: "ge", ast.Eq: "eq", ast.NotEq: "ne"}

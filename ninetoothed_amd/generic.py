@@ -65,11 +65,14 @@ _ALLOWED = {"load", "const", "param", "add", "sub", "mul", "div", "floordiv", "m
 
 _FLOAT = ("float16", "bfloat16", "float32", "float64")
 _INT = ("int8", "int16", "int32", "int64", "uint8")
-_RANK = {"bool": 0, "int8": 1, "uint8": 1, "int16": 2, "int32": 3, "int64": 4, "float16": 6, "bfloat16": 6,
-         "float32": 7, "float64": 8}
+_RANK = {"bool": 0, "int8": 1, "uint8": 1, "int16": 2, "int32": 3, "int64": 4, "float8_e4m3fn": 5, "float8_e5m2": 5,
+         "float16": 6, "bfloat16": 6, "float32": 7, "float64": 8}
+_FP8 = ("float8_e4m3fn", "float8_e5m2")
 
 # storage C type, working C type, load expression, store expression (of `v`)
 _STORAGE = {
+    "float8_e4m3fn": ("unsigned char", "float", "ld_e4m3({})", "st_e4m3({})"),
+    "float8_e5m2": ("unsigned char", "float", "ld_e5m2({})", "st_e5m2({})"),
     "float16": ("unsigned short", "float", "ld_f16({})", "st_f16({})"),
     "bfloat16": ("unsigned short", "float", "ld_bf16({})", "st_bf16({})"),
     "float32": ("float", "float", "{}", "{}"),
@@ -124,6 +127,42 @@ typedef _Float16 nt_half8 __attribute__((ext_vector_type(8)));
 typedef __bf16 nt_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float nt_floatx16 __attribute__((ext_vector_type(16)));
 __device__ __forceinline__ unsigned short st_bf16(float x) { return (unsigned short)(__builtin_bit_cast(unsigned, r_bf16(x)) >> 16); }
+// fp8 (OCP formats, as torch's float8_e4m3fn and float8_e5m2): round to nearest, ties to
+// even, on the exact value; e4m3fn has no infinity, so magnitudes from 480 (the midpoint
+// past its largest value, 448) and NaN encode as NaN (0x7f with the sign); e5m2 rounds
+// magnitudes from 61440 (the midpoint past 57344) to infinity.  Below the smallest normal
+// the step is the subnormal quantum (2^-9 and 2^-16); a step that carries into the next
+// binade gives that binade's first code, as the encodings are consecutive.
+__device__ __forceinline__ unsigned char st_e4m3(float x) {
+  const unsigned char sign = (unsigned char)((__builtin_bit_cast(unsigned, x) >> 24) & 0x80u);
+  const float a = __builtin_fabsf(x);
+  if (!(a < 480.0f)) return sign | 0x7f;
+  if (a < 0.015625f) return sign | (unsigned char)__builtin_rintf(a * 512.0f);
+  int e;
+  const float m = __builtin_frexpf(a, &e);  // a = m 2^e, m in [0.5, 1)
+  return sign | (unsigned char)((e + 6) * 8 + (int)__builtin_rintf((2.0f * m - 1.0f) * 8.0f));
+}
+__device__ __forceinline__ unsigned char st_e5m2(float x) {
+  const unsigned char sign = (unsigned char)((__builtin_bit_cast(unsigned, x) >> 24) & 0x80u);
+  const float a = __builtin_fabsf(x);
+  if (a != a) return sign | 0x7f;
+  if (a >= 61440.0f) return sign | 0x7c;
+  if (a < 6.103515625e-05f) return sign | (unsigned char)__builtin_rintf(a * 65536.0f);
+  int e;
+  const float m = __builtin_frexpf(a, &e);
+  return sign | (unsigned char)((e + 14) * 4 + (int)__builtin_rintf((2.0f * m - 1.0f) * 4.0f));
+}
+__device__ __forceinline__ float ld_e4m3(unsigned char b) {
+  const int E = (b >> 3) & 15, M = b & 7;
+  const float v = (E == 15 && M == 7) ? __builtin_nanf("") : (E == 0 ? __builtin_ldexpf((float)M, -9)
+                                                                    : __builtin_ldexpf((float)(8 + M), E - 10));
+  return (b & 0x80) ? -v : v;
+}
+__device__ __forceinline__ float ld_e5m2(unsigned char b) {  // the top byte of an fp16
+  return (float)__builtin_bit_cast(_Float16, (unsigned short)((unsigned)b << 8));
+}
+__device__ __forceinline__ float r_e4m3(float x) { return ld_e4m3(st_e4m3(x)); }
+__device__ __forceinline__ float r_e5m2(float x) { return ld_e5m2(st_e5m2(x)); }
 """
 
 # ntl math functions (unary) and libdevice functions: C names for float / double
@@ -226,6 +265,10 @@ class _Emitter:
             return f"r_f16({expr})"
         if t == "bfloat16":
             return f"r_bf16({expr})"
+        if t == "float8_e4m3fn":
+            return f"r_e4m3({expr})"
+        if t == "float8_e5m2":
+            return f"r_e5m2({expr})"
         return expr
 
     def const_value(self, v):
@@ -1046,12 +1089,22 @@ def _static_type(ctx, v):
 MDOT_LDS = 48 * 1024  # LDS a matrix-core dot may take (staged operands and the fp32 result)
 
 
+def _mdot_stage_type(tx, ty):
+    """The 16-bit type both operands of a matrix-core dot are staged in, or None: bf16 with
+    bf16; fp16 and fp8 (e4m3fn, e5m2) in any mix as fp16, which holds every fp8 value exactly,
+    so the products and their fp32 sums are those of an fp8 matrix multiply."""
+    if tx == ty == "bfloat16":
+        return "bfloat16"
+    if tx in ("float16",) + _FP8 and ty in ("float16",) + _FP8:
+        return "float16"
+    return None
+
+
 def _mdot_fits(ctx, x, y, tx, ty):
     """Whether ``dot`` of (inner) operands x, y runs on the matrix core: both 16-bit floats
     of one type, and the operands padded to M, N multiples of 32 and K of 16 plus the fp32
     result within MDOT_LDS."""
-    t = _static_type(ctx, x)
-    if t not in ("float16", "bfloat16") or _static_type(ctx, y) != t:
+    if _mdot_stage_type(_static_type(ctx, x), _static_type(ctx, y)) is None:
         return False
     try:
         shp = _shapes(ctx, _walk([x, y]), _Emitter(ctx).const_value, {})
@@ -1538,14 +1591,13 @@ class TilePlan(GenericPlan):
             # element j of the staged (padded) operand: row j / kp, k j % kp; zero past [rows, kk]
             r, c = f"(j / {kp}LL)", f"(j % {kp}LL)"
             body = em.context(val, (c, r) if trans else (r, c), tag)
-            tv = em.type_of(val)
             if t is None:
-                t = tv
-            if tv != t or t not in ("float16", "bfloat16"):
-                raise LoweringError("a matrix-core dot needs two operands of one 16-bit float type")
+                t = _mdot_stage_type(_static_type(self.ctx, x), _static_type(self.ctx, y))
+                if t is None:
+                    raise LoweringError("a matrix-core dot needs 16-bit or fp8 float operands (bf16 with bf16)")
             st = "st_f16" if t == "float16" else "st_bf16"
             mask = em.mask_of(val)
-            value = f"{st}({em.operand(val, t)})"
+            value = f"{st}({em.operand(val, em.type_of(val))})"
             if mask:
                 value = f"(({mask}) ? {value} : (unsigned short)0)"
             lines += [f"      for (long long j = tid; j < {rows_p * kp}LL; j += 256) {{",
@@ -1778,6 +1830,8 @@ class TilePlan(GenericPlan):
                 ident = "(-9223372036854775807LL - 1)" if kind == "max" else "9223372036854775807LL"
             return ident, ("({b} > {a} ? {b} : {a})" if kind == "max" else "({b} < {a} ? {b} : {a})")
         inf = "__builtin_huge_val()" if w == "double" else "__builtin_huge_valf()"
+        if t == "float8_e4m3fn":  # no infinity: its largest magnitude (reference ssa.py:2187-2192)
+            inf = "448.0f"
         f = ("fmax" if kind == "max" else "fmin") + ("" if w == "double" else "f")
         return (f"(-{inf})" if kind == "max" else inf), f + "({a}, {b})"
 

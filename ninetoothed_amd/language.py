@@ -14,6 +14,8 @@ int16 = "int16"
 int32 = "int32"
 int64 = "int64"
 uint8 = "uint8"
+float8_e4m3fn = "float8_e4m3fn"
+float8_e5m2 = "float8_e5m2"
 
 
 def _parsed_only(name):
