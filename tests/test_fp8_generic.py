@@ -10,10 +10,7 @@ fp8 arithmetic and a matrix-core dot of fp8 tiles against torch.
 """
 
 import ctypes
-import re
 import subprocess
-import tempfile
-from pathlib import Path
 
 import numpy as np
 import pytest
@@ -31,7 +28,7 @@ CLANG = "/opt/rocm/llvm/bin/clang++"
 
 # ------------------------------------------------------------------ the conversions, on the host
 @pytest.fixture(scope="module")
-def host_fp8():
+def host_fp8(tmp_path_factory):
     body = generic._PRELUDE
     start = body.index("__device__ __forceinline__ unsigned char st_e4m3")
     end = body.index("__device__ __forceinline__ float r_e4m3")
@@ -45,7 +42,7 @@ extern "C" void enc_many(const float* x, unsigned char* out, long n, int e5m2) {
   for (long i = 0; i < n; ++i) out[i] = e5m2 ? st_e5m2(x[i]) : st_e4m3(x[i]);
 }
 """
-    tmp = Path(tempfile.mkdtemp())
+    tmp = tmp_path_factory.mktemp("fp8")
     (tmp / "fp8.cpp").write_text(src)
     subprocess.run([CLANG, "-O2", "-shared", "-fPIC", str(tmp / "fp8.cpp"), "-o", str(tmp / "libfp8.so")], check=True)
     lib = ctypes.CDLL(str(tmp / "libfp8.so"))
