@@ -728,7 +728,8 @@ def test_conv2d_headline_takes_224_tiles():
     # 224-position kernel (config 4).  Q = 56 / 16 / 32 (4, 14 and 7 output rows per tile),
     # two and three raw pieces per strip, one channel block, K no multiple of 256, no row
     # padding and two rows of it, an input that is a channel slice of a wider tensor (image
-    # stride past C * H * W), and a filter whose rows are not contiguous (re-laid by gathers).
+    # stride past C * H * W), a filter whose rows are not contiguous (re-laid by gathers), and
+    # 75 32-channel filter blocks (the contiguous re-layout's last workgroup takes three of four).
     ((3, 96, 56, 56), 64, (1, 1), 0, "dense"),
     ((2, 64, 14, 16), 96, (1, 1), 0, "dense"),
     ((1, 32, 14, 32), 200, (1, 1), 0, "dense"),
@@ -736,6 +737,7 @@ def test_conv2d_headline_takes_224_tiles():
     ((1, 64, 54, 56), 40, (2, 1), 0, "dense"),
     ((2, 64, 56, 56), 300, (1, 1), 32, "dense"),
     ((2, 64, 56, 56), 96, (1, 1), 0, "krsc"),
+    ((2, 32, 28, 56), 75, (1, 1), 0, "dense"),
 ))
 def test_conv2d_strip224(case, dtype):
     (n, c, h, w_), k, padding, c_off, layout = case
