@@ -69,6 +69,9 @@ def _args():
                    help="only run the matrix-core ceiling probe (fp16 MFMAs back to back, zero and random operands)")
     p.add_argument("--ceiling-iters", type=int, default=400_000,
                    help="loop iterations of the ceiling probe (8 MFMAs per wave each)")
+    p.add_argument("--power-probe", action="store_true",
+                   help="only run the sustained-load probe: addmm 4096^3 through the Handle after the GPU idled, "
+                        "time per call in groups of consecutive calls, random and all-zero operands")
     p.add_argument("--trace-summary", default="",
                    help="only summarise a rocprofv3 --kernel-trace CSV of one configuration (--only) run with the "
                         "same --warmup/--steps: per-kernel durations over the K timed steps (no GPU used)")
@@ -507,6 +510,10 @@ def main():
     import ninetoothed_amd as ninetoothed
     import programs as pg
 
+    if args.power_probe:
+        _power_probe(torch, ninetoothed, pg)
+        return
+
     configs = _configs(torch, ninetoothed, pg, cold=args.cold)
     only = set(filter(None, args.only.split(",")))
     traffic = _traffic()
@@ -666,6 +673,52 @@ def _mfma_ceiling(torch, iters, runs):
                 "implied_clock_ghz": tflops * 1e12 / (1024 * 1024) / 1e9}
         print(json.dumps(line), flush=True)
         lines.append(line)
+    return lines
+
+
+def _power_probe(torch, ninetoothed, pg, groups=80, per=5, idle_s=1.0):
+    """The board's clock under sustained matrix-core load: the headline addmm (4096^3, fp16 and
+    bf16, the bench's Handle and its 0.5 * C + A @ B) after one second idle, timed in groups of
+    ``per`` consecutive calls between HIP events, once with N(0,1)/sqrt(K) operands and once
+    with all-zero operands (the same instructions and memory traffic; only the operand bits,
+    and so the power drawn, differ)."""
+    k = ninetoothed.make(pg.addmm_arrangement, pg.addmm_application, pg.addmm_tensors())
+    flops = 2 * 4096**3
+    lines = []
+    for dtype in (torch.float16, torch.bfloat16):
+        for operands in ("random", "zero"):
+            g = torch.Generator("cpu").manual_seed(0)
+
+            def make():
+                if operands == "zero":
+                    return torch.zeros((4096, 4096), dtype=dtype, device="cuda")
+                return (torch.randn((4096, 4096), generator=g) / 64).to(dtype).to("cuda")
+
+            c, a, b = make(), make(), make()
+            o = torch.empty_like(c)
+            k(c, a, b, 0.5, 1.0, o)
+            torch.cuda.synchronize()
+            time.sleep(idle_s)
+            events = [torch.cuda.Event(enable_timing=True) for _ in range(groups + 1)]
+            events[0].record()
+            for i in range(groups):
+                for _ in range(per):
+                    k(c, a, b, 0.5, 1.0, o)
+                events[i + 1].record()
+            torch.cuda.synchronize()
+            us = [events[i].elapsed_time(events[i + 1]) / per * 1e3 for i in range(groups)]
+
+            def rate(part):
+                return flops / (sum(part) / len(part) * 1e-6) / 1e12
+
+            line = {"probe": "power", "dtype": "fp16" if dtype == torch.float16 else "bf16", "operands": operands,
+                    "idle_s": idle_s, "calls_per_group": per, "us_per_call_by_group": [round(u, 1) for u in us],
+                    # calls 6-25: the window a run with --warmup 5 --steps 20 times
+                    "tflops_calls_6_25": rate(us[1:5]), "tflops_last_100_calls": rate(us[-100 // per:]),
+                    "max_us": max(us), "settled_us": sum(us[-100 // per:]) / (100 // per)}
+            print(json.dumps(line), flush=True)
+            lines.append(line)
+            del c, a, b, o
     return lines
 
 
