@@ -676,49 +676,61 @@ def _mfma_ceiling(torch, iters, runs):
     return lines
 
 
-def _power_probe(torch, ninetoothed, pg, groups=80, per=5, idle_s=1.0):
+def _power_probe(torch, ninetoothed, pg, per=5, idle_s=1.0):
     """The board's clock under sustained matrix-core load: the headline addmm (4096^3, fp16 and
-    bf16, the bench's Handle and its 0.5 * C + A @ B) after one second idle, timed in groups of
-    ``per`` consecutive calls between HIP events, once with N(0,1)/sqrt(K) operands and once
-    with all-zero operands (the same instructions and memory traffic; only the operand bits,
-    and so the power drawn, differ)."""
-    k = ninetoothed.make(pg.addmm_arrangement, pg.addmm_application, pg.addmm_tensors())
-    flops = 2 * 4096**3
-    lines = []
+    bf16, the bench's Handle and its 0.5 * C + A @ B; 400 calls) and the bench's attention
+    (fp16, B=4 H=32 S=4096 D=128, non-causal and causal; 100 calls), each after one second
+    idle, timed in groups of ``per`` consecutive calls between HIP events, once with the
+    bench's random operands and once with all-zero operands (the same instructions and memory
+    traffic; only the operand bits, and so the power drawn, differ)."""
+    addmm = ninetoothed.make(pg.addmm_arrangement, pg.addmm_application, pg.addmm_tensors())
+    attn = ninetoothed.make(pg.attention_arrangement, pg.attention_application_scaled, pg.attention_tensors())
+    cases = []
     for dtype in (torch.float16, torch.bfloat16):
+        cases.append(("addmm", dtype, (4096, 4096), 3, 400, 2 * 4096**3,
+                      lambda t: addmm(t[0], t[1], t[2], 0.5, 1.0, t[3]), 1 / 64))
+    for causal in (False, True):
+        cases.append(("attention_causal" if causal else "attention_noncausal", torch.float16, (4, 32, 4096, 128), 3,
+                      100, 4 * 4 * 32 * 4096 * 4096 * 128 // (2 if causal else 1),
+                      lambda t, causal=causal: attn(t[0], t[1], t[2], causal, t[3]), 1.0))
+    lines = []
+    for name, dtype, shape, n_in, calls, flops, call, scale in cases:
         for operands in ("random", "zero"):
             g = torch.Generator("cpu").manual_seed(0)
 
             def make():
                 if operands == "zero":
-                    return torch.zeros((4096, 4096), dtype=dtype, device="cuda")
-                return (torch.randn((4096, 4096), generator=g) / 64).to(dtype).to("cuda")
+                    return torch.zeros(shape, dtype=dtype, device="cuda")
+                return (torch.randn(shape, generator=g) * scale).to(dtype).to("cuda")
 
-            c, a, b = make(), make(), make()
-            o = torch.empty_like(c)
-            k(c, a, b, 0.5, 1.0, o)
+            t = [make() for _ in range(n_in)]
+            t.append(torch.empty_like(t[0]))
+            call(t)
             torch.cuda.synchronize()
             time.sleep(idle_s)
+            groups = calls // per
             events = [torch.cuda.Event(enable_timing=True) for _ in range(groups + 1)]
             events[0].record()
             for i in range(groups):
                 for _ in range(per):
-                    k(c, a, b, 0.5, 1.0, o)
+                    call(t)
                 events[i + 1].record()
             torch.cuda.synchronize()
             us = [events[i].elapsed_time(events[i + 1]) / per * 1e3 for i in range(groups)]
+            tail = us[-(groups // 4):]
 
             def rate(part):
                 return flops / (sum(part) / len(part) * 1e-6) / 1e12
 
-            line = {"probe": "power", "dtype": "fp16" if dtype == torch.float16 else "bf16", "operands": operands,
-                    "idle_s": idle_s, "calls_per_group": per, "us_per_call_by_group": [round(u, 1) for u in us],
+            line = {"probe": "power", "case": name, "dtype": "fp16" if dtype == torch.float16 else "bf16",
+                    "operands": operands, "idle_s": idle_s, "calls_per_group": per,
+                    "us_per_call_by_group": [round(u, 1) for u in us],
                     # calls 6-25: the window a run with --warmup 5 --steps 20 times
-                    "tflops_calls_6_25": rate(us[1:5]), "tflops_last_100_calls": rate(us[-100 // per:]),
-                    "max_us": max(us), "settled_us": sum(us[-100 // per:]) / (100 // per)}
+                    "tflops_calls_6_25": rate(us[1:5]), "tflops_last_quarter": rate(tail),
+                    "max_us": max(us), "settled_us": sum(tail) / len(tail)}
             print(json.dumps(line), flush=True)
             lines.append(line)
-            del c, a, b, o
+            del t
     return lines
 
 
