@@ -1,7 +1,7 @@
 """Benchmark of the MI355X backend on BASELINE.json's configurations (one GPU).
 
-A step is one call of the hot path (one kernel through the drop-in ``make``/``jit``
-Handle) on inputs already resident in HBM.  The headline line is configs[1]: fp16
+A step is one call of the hot path through the drop-in ``make``/``jit`` Handle (one
+kernel; two for conv2d: the filter re-layout, then the strip GEMM) on inputs already resident in HBM.  The headline line is configs[1]: fp16
 addmm out = 0.5*C + 1.0*(A@B), M=N=K=4096.  The same JSON line carries every other
 configuration under "configs", each with its own roofline fraction and CPU baseline.
 
@@ -18,7 +18,8 @@ configurations (softmax, max_pool2d, add) rotate through buffer sets whose total
 the 256 MB Infinity Cache, so every step reads its inputs from HBM.
 
 roofline.achieved = algorithmic work per launch / average launch duration over the K
-steps; peaks are MI355X's published figures (HBM 8 TB/s; dense fp16/bf16 MFMA 2.5 PFLOP/s,
+steps (for conv2d both of a step's kernels count: the GEMM kernel alone is faster, see
+profiles/kernel_durations.md); peaks are MI355X's published figures (HBM 8 TB/s; dense fp16/bf16 MFMA 2.5 PFLOP/s,
 fp8 5.0; fp32 157.3 TFLOP/s).  roofline.traffic is the HBM bytes per launch from the
 rocprofv3 FETCH_SIZE/WRITE_SIZE runs recorded in profiles/hbm_traffic.json (its
 ``source`` says which run), not measured by this process.
