@@ -13,7 +13,7 @@ launched on (torch's current stream, which the launchers pass to the library) ->
 of events -> ``median_ms`` and the 10th/90th percentiles (the spread).  Configurations under
 30 us per step also report ``graph_ms_per_step`` / ``graph_value``: K calls captured once in a
 HIP graph and replayed, i.e. the kernels' rate without the host path of a Handle call (about
-8 us per call, which sets the pace of the direct calls for kernels of a few microseconds).  The bandwidth-bound
+4 us per call for the GEMM, which sets the pace of the direct calls for kernels of a few microseconds).  The bandwidth-bound
 configurations (softmax, max_pool2d, add) rotate through buffer sets whose total exceeds
 the 256 MB Infinity Cache, so every step reads its inputs from HBM.
 
