@@ -729,7 +729,8 @@ def test_conv2d_headline_takes_224_tiles():
     # two and three raw pieces per strip, one channel block, K no multiple of 256, no row
     # padding and two rows of it, an input that is a channel slice of a wider tensor (image
     # stride past C * H * W), a filter whose rows are not contiguous (re-laid by gathers), and
-    # 75 32-channel filter blocks (the contiguous re-layout's last workgroup takes three of four).
+    # 75 32-channel filter blocks (the contiguous re-layout's last workgroup takes three of four),
+    # and a contiguous filter starting 2 bytes past a 16-byte boundary (re-laid by gathers).
     ((3, 96, 56, 56), 64, (1, 1), 0, "dense"),
     ((2, 64, 14, 16), 96, (1, 1), 0, "dense"),
     ((1, 32, 14, 32), 200, (1, 1), 0, "dense"),
@@ -738,6 +739,7 @@ def test_conv2d_headline_takes_224_tiles():
     ((2, 64, 56, 56), 300, (1, 1), 32, "dense"),
     ((2, 64, 56, 56), 96, (1, 1), 0, "krsc"),
     ((2, 32, 28, 56), 75, (1, 1), 0, "dense"),
+    ((2, 64, 28, 56), 48, (1, 1), 0, "offset"),
 ))
 def test_conv2d_strip224(case, dtype):
     (n, c, h, w_), k, padding, c_off, layout = case
@@ -745,6 +747,9 @@ def test_conv2d_strip224(case, dtype):
     x = big[:, c_off:c_off + c]
     if layout == "dense":
         w = _randn((k, c, 3, 3), dtype, 46, 1.0 / math.sqrt(c * 9))
+    elif layout == "offset":
+        w = _randn((k * c * 9 + 1,), dtype, 46, 1.0 / math.sqrt(c * 9))[1:].view(k, c, 3, 3)
+        assert w.is_contiguous() and w.data_ptr() % 16 == 2
     else:
         w = _randn((k, 3, 3, c), dtype, 46, 1.0 / math.sqrt(c * 9)).permute(0, 3, 1, 2)
     ref = F.conv2d(x.float(), w.float(), padding=padding)
