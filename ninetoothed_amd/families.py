@@ -570,18 +570,27 @@ def _fit_conv(ctx, vx, vw, vy):
     _require(np.array_equal(ko, ko2), family, "filter rows do not follow output channels")
     _require(np.array_equal(c, c2), family, "input and filter channels differ")
 
-    def fit(out_pos, win, coord):
-        A = np.stack([out_pos, win, np.ones_like(out_pos)], axis=1).astype(np.float64)
-        sol, *_ = np.linalg.lstsq(A, coord.astype(np.float64), rcond=None)
-        st, dl, off = (int(round(x)) for x in sol)
-        _require(np.array_equal(out_pos * st + win * dl + off, coord), family, "window positions are not affine")
-        return st, dl, -off
-
-    sh, dh, ph = fit(p, r, h)
-    sw, dw, pw = fit(q, s, w)
     N, K, P, Q = vy.source_shape
     _, C, H, W = vx.source_shape
     K2, C2, R, S = vw.source_shape
+
+    def fit(out_pos, win, coord, n_out, n_win):
+        # coord = out_pos * stride + win * dilation - padding.  An axis of one output position
+        # (P or Q of 1) leaves the stride free, a filter axis of one tap (R or S of 1) the
+        # dilation: such an index is 0 throughout, so its coefficient is taken as 1 and only
+        # the others are fitted.
+        free_st, free_dl = n_out == 1, n_win == 1
+        cols = [c for c, free in ((out_pos, free_st), (win, free_dl)) if not free]
+        A = np.stack(cols + [np.ones_like(out_pos)], axis=1).astype(np.float64)
+        sol = iter(int(round(x)) for x in np.linalg.lstsq(A, coord.astype(np.float64), rcond=None)[0])
+        st = 1 if free_st else next(sol)
+        dl = 1 if free_dl else next(sol)
+        off = next(sol)
+        _require(np.array_equal(out_pos * st + win * dl + off, coord), family, "window positions are not affine")
+        return st, dl, -off
+
+    sh, dh, ph = fit(p, r, h, P, R)
+    sw, dw, pw = fit(q, s, w, Q, S)
     _require(K2 == K and C2 == C, family, "filter shape does not match the input/output channels")
     _require(sh > 0 and sw > 0 and dh > 0 and dw > 0 and ph >= 0 and pw >= 0, family, "unsupported stride/padding")
     for src, mask, view in ((y_src, y_mask, vy), (w_src, w_mask, vw), (x_src, x_mask, vx)):

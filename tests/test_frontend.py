@@ -70,6 +70,23 @@ def test_conv2d_geometry_is_recovered(padding):
     assert h._kernel.granularity == _granularity("conv2d")
 
 
+@pytest.mark.parametrize("case", (
+    # (H, W, R, S, padding): a filter axis of one tap, an output axis of one position, both
+    ((16, 16, 1, 1, (0, 0)), (16, 16, 1, 3, (0, 1)), (16, 16, 5, 1, (2, 0)), (2, 14, 2, 4, (0, 0)),
+     (1, 24, 1, 5, (0, 2)), (3, 3, 3, 3, (0, 0)), (1, 1, 1, 1, (0, 0)))
+))
+def test_conv2d_geometry_with_axes_of_one(case):
+    # One tap (R or S of 1) leaves that axis' dilation undetermined by the index maps, one
+    # output position (P or Q of 1) its stride: both are taken as 1, so these calls stay on
+    # the conv2d kernels instead of the generic ones.
+    h_, w_, r, s, (ph, pw) = case
+    p, q = h_ + 2 * ph - r + 1, w_ + 2 * pw - s + 1
+    d = _specialize(pg.make_conv2d(), _h((2, 32, h_, w_)), _h((40, 32, r, s)), _h((2, 40, p, q)), padding_h=ph,
+                    padding_w=pw)
+    assert d["family"] == "conv2d" and d["padding"] == (ph, pw)
+    assert d["stride"] == (1, 1) and d["dilation"] == (1, 1)
+
+
 @pytest.mark.parametrize("causal", (False, True))
 def test_attention_matches(causal):
     h = ninetoothed.make(pg.attention_arrangement, pg.attention_application, pg.attention_tensors())
