@@ -5,11 +5,12 @@ The fixed cases elsewhere pin the reference's own tests and each kernel's edge c
 sweep draws sizes that are no multiple of anything (and some that are), transposed operand
 layouts, strided views and mixed output types, so that a path a fixed case never reaches is
 still checked.  Every draw is seeded (the case id is the seed), so a failure names a case that
-can be run again alone.
+can be run again alone.  ``NT_SWEEP_CASES`` sets the number of draws per family (16).
 """
 
 import functools
 import math
+import os
 import random
 
 import pytest
@@ -22,7 +23,7 @@ import programs as pg
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
-CASES = range(16)
+CASES = range(int(os.environ.get("NT_SWEEP_CASES", "16")))
 
 
 @pytest.fixture(autouse=True)
@@ -42,8 +43,16 @@ def _randn(shape, dtype, g, scale=1.0):
 
 
 def _layout(t, rng):
-    """The same values as ``t`` (2-D), stored row-major or column-major."""
-    return t if rng.random() < 0.5 else t.t().contiguous().t()
+    """The same values as ``t`` (2-D), stored row-major, column-major or as every other
+    column of a wider row-major tensor."""
+    u = rng.random()
+    if u < 0.4:
+        return t
+    if u < 0.8:
+        return t.t().contiguous().t()
+    wide = torch.empty((t.shape[0], 2 * t.shape[1]), dtype=t.dtype, device=t.device)
+    wide[:, ::2] = t
+    return wide[:, ::2]
 
 
 def _size(rng, hi):
@@ -184,3 +193,37 @@ def test_max_pool2d_random(seed):
     y = torch.full(ref.shape, float("nan"), dtype=dtype, device=DEV)
     _pool_handle(ceil_mode)(x, y, WINDOW_HEIGHT=wh, WINDOW_WIDTH=ww)
     assert torch.equal(y, ref), (x.shape, wh, ww, ceil_mode, dtype)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_matmul_random_large(seed):
+    # sizes the 256 x 256 DMA kernels take (and ragged ones around them)
+    rng, g = random.Random(7000 + seed), _gen(7000 + seed)
+    m = rng.choice((256 * rng.randint(1, 10), rng.randint(300, 2600)))
+    n = 8 * rng.randint(32, 320)
+    k = 8 * rng.randint(8, 320)
+    dtype = rng.choice((torch.float16, torch.bfloat16))
+    a = _randn((m, k), dtype, g, 1 / math.sqrt(k))
+    b = _layout(_randn((k, n), dtype, g), rng)
+    out = torch.full((m, n), float("nan"), dtype=torch.float16, device=DEV)
+    _handle("matmul")(a, b, out)
+    ref = (a.float() @ b.float()).half().float()
+    assert torch.allclose(out.float(), ref, atol=1e-2, rtol=1e-2), (m, n, k, dtype, b.stride())
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_conv2d_random_large(seed):
+    # 3 x 3 and 1 x 1 filters over 32-channel multiples at ResNet-like sizes: the strip and
+    # re-laid DMA kernels
+    rng, g = random.Random(8000 + seed), _gen(8000 + seed)
+    r = rng.choice((1, 3))
+    pad = (r - 1) // 2
+    n, c, k = rng.randint(1, 4), 32 * rng.randint(1, 8), rng.choice((8 * rng.randint(1, 40), rng.randint(1, 300)))
+    hw = rng.choice((7, 14, 28, 56, rng.randint(8, 60)))
+    dtype = rng.choice((torch.float16, torch.bfloat16))
+    x = _randn((n, c, hw, hw), dtype, g)
+    wt = _randn((k, c, r, r), dtype, g, 1 / math.sqrt(c * r * r))
+    ref = F.conv2d(x.float(), wt.float(), padding=pad)
+    y = torch.full(ref.shape, float("nan"), dtype=torch.float16, device=DEV)
+    _handle("conv2d")(x, wt, y, padding_h=pad, padding_w=pad)
+    assert torch.allclose(y.float(), ref.half().float(), atol=2e-2, rtol=1e-2), (x.shape, wt.shape, dtype)
