@@ -455,9 +455,10 @@ __device__ __forceinline__ void load_lds16(u32x4 rs, uint32_t lds_addr, int voff
 // The DMA kernels' fast epilogue (16-bit out, c absent or of out's type, unit column
 // stride, 16-byte aligned rows; the launcher's c_pre).  acc holds a wave's 128 x (32 WJ)
 // block as 4 x WJ tiles of 32 x 32 (the 32x32 MFMA accumulator layout); lds + EPI +
-// 2 KiB * WJ * wave is the wave's staging.
-template <int WJ = 2, bool BOUNDED = false>
-__device__ __forceinline__ void dma_fast_epilogue(const GemmArgs& g, const floatx16 (&acc)[4][WJ], char* lds, int wave,
+// 2 KiB * WJ * wave is the wave's staging.  NI: the wave's 32-row slabs (4: 128 rows; 2 in
+// gemm_dma128_kernel, whose staging starts at EPI_AT).
+template <int WJ = 2, bool BOUNDED = false, int NI = 4, int EPI_AT = dma::EPI>
+__device__ __forceinline__ void dma_fast_epilogue(const GemmArgs& g, const floatx16 (&acc)[NI][WJ], char* lds, int wave,
                                                   int lane, int64_t row_base, int64_t col_base) {
   // Fast epilogue: the accumulators go through this wave's staging (never touched by the k
   // loop: no barrier) 16 rows at a time; a lane finishes rows t * (64 / CPR) + lane / CPR
@@ -472,9 +473,10 @@ __device__ __forceinline__ void dma_fast_epilogue(const GemmArgs& g, const float
   // BOUNDED: rows and columns of this wave's block inside out (ragged M and N; N is a
   // multiple of 8, so each lane's 8 columns are all inside or all outside).  Otherwise the
   // launcher has checked that every tile is whole.
-  int rows_v = 128, cols_v = COLS;
+  constexpr int ROWS = 32 * NI;
+  int rows_v = ROWS, cols_v = COLS;
   if constexpr (BOUNDED) {
-    rows_v = (int)(g.M - row_base < 128 ? g.M - row_base : 128);
+    rows_v = (int)(g.M - row_base < ROWS ? g.M - row_base : ROWS);
     cols_v = (int)(g.N - col_base < COLS ? g.N - col_base : COLS);
     if (rows_v <= 0 || cols_v <= 0) return;
   }
@@ -499,7 +501,7 @@ __device__ __forceinline__ void dma_fast_epilogue(const GemmArgs& g, const float
       for (int t = 0; t < WJ; ++t)
         cv[i & 1][h][t] = __builtin_amdgcn_raw_buffer_load_b128(rsC, vc, (i * 32 + h * 16 + t * RPP) * c_row, 0);
   };
-  float* stage = (float*)(lds + dma::EPI + wave * (2048 * WJ));
+  float* stage = (float*)(lds + EPI_AT + wave * (2048 * WJ));
   auto finish = [&](auto out_f16_c, auto round_c, int i, int h) {
     constexpr bool OUT_F16 = decltype(out_f16_c)::value;
     constexpr int ROUND = decltype(round_c)::value;
@@ -548,10 +550,10 @@ __device__ __forceinline__ void dma_fast_epilogue(const GemmArgs& g, const float
     load_c(0);
     load_c(1);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NI; ++i) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) finish(out_f16_c, round_c, i, h);
-      if (i + 2 < 4) load_c(i + 2);
+      if (i + 2 < NI) load_c(i + 2);
     }
   };
   const bool out_f16 = g.out_dtype == NT_DTYPE_F16;
@@ -765,6 +767,169 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     return;
   }
   dma_fast_epilogue<2, true>(g, acc, lds, wave, lane, row_base, col_base);
+}
+
+// gemm_dma_kernel's pipeline on 128 x 128 tiles, for outputs with too few 256 x 256 tiles to
+// fill the chip (2048^2 has 64 of those for 256 CUs, 256 of these).  Four waves of 64 x 64
+// (2 x 2 blocks of 32 x 32) per workgroup and 80 KiB of LDS (ring 64 KiB, staging 16 KiB),
+// so two workgroups share a CU.  The ring holds four 32-deep k-tiles of 8 KiB of a and 8 KiB
+// of b, filled by DMA with each wave's two loads of each operand per k-tile as in the
+// 256-wide kernel: a rows 32 wave + 16 q + lane / 4 (64-byte rows, XOR chunk swizzle); b
+// rows 8 wave + 4 q + lane / 16 (256-byte rows of 128 columns; 32-column group g of row k
+// stored at group g ^ (k % 4), so the transposing reads of 32 lanes, rows r = 0..3 of one
+// group each, hit 4 x 16 distinct banks), or b^T rows as a's (BT).  Per k-tile a wave issues
+// eight MFMAs (its 2 x 2 blocks, two 16-deep slices) with the next slice's four fragment
+// reads between them, one barrier per k-tile, and the fast epilogue on 2 slabs of 32 rows.
+// Only for calls whose epilogue is the fast one (the launcher's c_pre).
+namespace dma128 {
+constexpr int STAGE = 8192, B0 = 32768, EPI = 65536, LDS = EPI + 4 * 4096;
+__device__ __forceinline__ int bsw(int k) { return k & 3; }
+}  // namespace dma128
+
+template <typename T, bool BT = false>
+__global__ __launch_bounds__(256) void gemm_dma128_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(1024))) char lds[dma128::LDS];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  constexpr int TM = 128, TN = 128;
+  int tm, tn;
+  tile_of(blockIdx.x, g.tiles_m, g.tiles_n, tm, tn);
+  const int64_t m0 = (int64_t)tm * TM, n0 = (int64_t)tn * TN;
+  const int nk = (int)((g.K + 31) / 32);
+
+  // Buffer resources end at each panel's last valid element, as in gemm_dma_kernel: rows of a
+  // past M and rows of b past K read zeros; the chunks of a (and b^T) past K in the last
+  // k-tile are fetched from the resource's end.
+  const int rows_a = (int)(g.M - m0 < TM ? g.M - m0 : TM), cols_b = (int)(g.N - n0 < TN ? g.N - n0 : TN);
+  const uint32_t a_end = (uint32_t)(((rows_a - 1) * g.sa_m + g.K) * 2);
+  const u32x4 rsA = dma::rsrc((const uint16_t*)g.a + m0 * g.sa_m, a_end);
+  const uint32_t b_end = BT ? (uint32_t)(((cols_b - 1) * g.sb_n + g.K) * 2) : (uint32_t)(((g.K - 1) * g.sb_k + cols_b) * 2);
+  const u32x4 rsB = dma::rsrc((const uint16_t*)g.b + (BT ? n0 * g.sb_n : n0), b_end);
+  int va[2], vb[2], va_last[2], vb_last[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int ra = 32 * wave + 16 * q + (lane >> 2);
+    va[q] = (int)(ra * g.sa_m * 2) + dma::asw(ra, lane & 3) * 16;
+    va_last[q] = (nk - 1) * 32 + dma::asw(ra, lane & 3) * 8 < g.K ? va[q] : (int)a_end;
+    if constexpr (BT) {
+      vb[q] = (int)(ra * g.sb_n * 2) + dma::asw(ra, lane & 3) * 16;
+      vb_last[q] = (nk - 1) * 32 + dma::asw(ra, lane & 3) * 8 < g.K ? vb[q] : (int)b_end;
+    } else {
+      const int kb = 8 * wave + 4 * q + (lane >> 4);
+      const int nb = 32 * (((lane & 15) >> 2) ^ dma128::bsw(kb)) + 8 * (lane & 3);
+      vb[q] = (int)(kb * g.sb_k * 2) + nb * 2;
+      vb_last[q] = vb[q];
+    }
+  }
+  const int b_kstep = BT ? 64 : (int)(32 * g.sb_k * 2);
+  // Load u (0..3) of tile kt into its stage: a q0, b q0, a q1, b q1 (1 KiB each).
+  auto load_unit = [&](int u, int kt) {
+    const int st = (kt % dma::STAGES) * dma128::STAGE, q = u >> 1;
+    if ((u & 1) == 0)
+      dma::load_lds16(rsA, lds0 + st + 2048 * wave + 1024 * q, kt == nk - 1 ? va_last[q] : va[q], kt * 64);
+    else
+      dma::load_lds16(rsB, lds0 + dma128::B0 + st + 2048 * wave + 1024 * q, kt == nk - 1 ? vb_last[q] : vb[q],
+                      kt * b_kstep);
+  };
+
+  // Fragment reads.  a: row 64 wm + 32 i + lane % 32 (i at + 2048 i), chunk 2 s + lane / 32.
+  // b: lane (group gq = lane / 16, r, q) reads row 16 s + 8 (gq / 2) + 4 half + r at columns
+  // 64 wn + 32 j + 16 (gq % 2) + 4 q .. + 3 (rows 16 s at + 4096 s, the half at + 1024).
+  int a_rd[2], b_rd[2];
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2) {
+    const int row = wm * 64 + (lane & 31);
+    a_rd[s2] = row * 64 + dma::asw(row, 2 * s2 + (lane >> 5)) * 16;
+  }
+  if constexpr (BT) {
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const int row = wn * 64 + (lane & 31);
+      b_rd[s2] = dma128::B0 + row * 64 + dma::asw(row, 2 * s2 + (lane >> 5)) * 16;
+    }
+  } else {
+    const int gq = lane >> 4, r = (lane & 15) >> 2, q = lane & 3;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      b_rd[j] = dma128::B0 + (8 * (gq >> 1) + r) * 256 + (((2 * wn + j) ^ r) * 64) + (16 * (gq & 1) + 4 * q) * 2;
+  }
+  typedef typename mfma_traits<T>::frag frag;
+  frag fa[2][2], fb[2][2];
+  // Unit x (0..3) of slice s2 of the tile at stage offset st, in the order the slice's MFMAs
+  // consume them: a0, b0, b1, a1.
+  auto read_unit = [&](int x, int s2, int st) {
+    if (x == 0 || x == 3) {
+      const int i = x == 0 ? 0 : 1;
+      fa[s2][i] = *(const frag*)(lds + a_rd[s2] + st + i * 2048);
+    } else if constexpr (BT) {
+      const int j = x - 1;
+      fb[s2][j] = *(const frag*)(lds + b_rd[s2] + st + j * 2048);
+    } else {
+      const int j = x - 1;
+      const char* p = lds + b_rd[j] + st + s2 * 4096;
+      const dma::v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) dma::v4i16*)p);
+      const dma::v4i16 hi =
+          __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) dma::v4i16*)(p + 1024));
+      const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+      fb[s2][j] = __builtin_bit_cast(frag, u32x4{l2[0], l2[1], h2[0], h2[1]});
+    }
+  };
+
+  floatx16 acc[2][2];
+  zero_acc(acc);
+
+  // nk >= 3 (the launcher checks): tiles 0..2 in flight, wait for tile 0.
+  for (int kt = 0; kt < 3; ++kt)
+    for (int u = 0; u < 4; ++u) load_unit(u, kt);
+  asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+#pragma unroll
+  for (int x = 0; x < 4; ++x) read_unit(x, 0, 0);
+
+#define NT_FENCE() __builtin_amdgcn_sched_barrier(0)
+  // One k-tile, as gemm_dma_kernel's: HAS1 reads the next tile's slice 0 during slice 1, LOAD
+  // fetches tile kt + 3 into the stage of tile kt - 1, VM the loads left in flight at the
+  // barrier (-1: the last tile, no wait and no barrier).
+  auto step = [&](auto has1_c, auto load_c, auto vm_c, int kt) {
+    constexpr bool HAS1 = decltype(has1_c)::value, LOAD = decltype(load_c)::value;
+    constexpr int VM = decltype(vm_c)::value;
+    const int st = (kt % dma::STAGES) * dma128::STAGE, st1 = ((kt + 1) % dma::STAGES) * dma128::STAGE;
+    static_for<0, 8>([&](auto m_c) {
+      constexpr int m = decltype(m_c)::value;
+      constexpr int s2 = m >> 2, x = m & 3;
+      if constexpr (m == 4 && VM >= 0) {
+        NT_FENCE();
+        if constexpr (VM == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+        if constexpr (VM == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        NT_FENCE();
+      }
+      acc[x >> 1][x & 1] = mfma_traits<T>::mma(fa[s2][x >> 1], fb[s2][x & 1], acc[x >> 1][x & 1]);
+      NT_FENCE();
+      if constexpr (s2 == 0)
+        read_unit(x, 1, st);
+      else if constexpr (HAS1)
+        read_unit(x, 0, st1);
+      if constexpr (s2 == 1 && LOAD) load_unit(x, kt + 3);
+      NT_FENCE();
+    });
+  };
+#undef NT_FENCE
+  using T1 = std::integral_constant<bool, true>;
+  using F1 = std::integral_constant<bool, false>;
+  using V4 = std::integral_constant<int, 4>;
+  using V0 = std::integral_constant<int, 0>;
+  using VN = std::integral_constant<int, -1>;
+  int kt = 0;
+  for (; kt + 3 < nk; ++kt) step(T1{}, T1{}, V4{}, kt);
+  step(T1{}, F1{}, V4{}, kt);
+  step(T1{}, F1{}, V0{}, kt + 1);
+  step(F1{}, F1{}, VN{}, kt + 2);
+
+  dma_fast_epilogue<2, true, 2, dma128::EPI>(g, acc, lds, wave, lane, m0 + wm * 64, n0 + wn * 64);
 }
 
 // ----------------------------------------------------------------------------- fp32
@@ -1137,11 +1302,16 @@ __global__ void gemm_k0_kernel(GemmArgs g) {
 }
 
 // config: 0 = the fastest kernel whose conditions hold; 1 = the DMA kernel, 2 = the
-// register-staged eight-wave kernel, 3 = the element-wise loader kernel (any strides): a
-// forced kernel whose conditions do not hold is rejected before anything is launched.
+// register-staged eight-wave kernel, 3 = the element-wise loader kernel (any strides), 4 =
+// the DMA kernel on 128 x 128 tiles: a forced kernel whose conditions do not hold is
+// rejected before anything is launched.  Config 0 takes the 128 x 128 tiles when they fit
+// and the output has fewer than DMA128_BELOW tiles of 256 x 256: measured fp16, the
+// 128-wide kernel wins up to 128 such tiles (2048^3 729 against 412 TFLOP/s, 8192 x 1024 x
+// 8192 814 against 770) and loses from 144 (3072^3 681 against 849).
+constexpr int64_t DMA128_BELOW = 136;
 template <typename T>
 static int gemm16_launch(GemmArgs g, hipStream_t stream, int config = 0) {
-  if (config < 0 || config > 3) return NT_ERR_INVALID;
+  if (config < 0 || config > 4) return NT_ERR_INVALID;
   if (int e = gemm_check(g)) return e;
   if (!valid_dtype(g.c_dtype)) return NT_ERR_INVALID;  // an fp8 c goes with fp8 operands
   if (g.M == 0 || g.N == 0) return 0;
@@ -1177,7 +1347,27 @@ static int gemm16_launch(GemmArgs g, hipStream_t stream, int config = 0) {
                        (uintptr_t)g.out % 16 == 0;
   const bool c_vec = !g.c || (g.c_dtype == g.out_dtype && g.sc_n == 1 && g.sc_m >= 0 && g.sc_m % 8 == 0 && (uintptr_t)g.c % 16 == 0 &&
                               127 * g.sc_m + 128 <= 0x3fffffffLL);
-  if ((config == 1 && !dma_ok) || (config == 2 && !fast)) return NT_ERR_INVALID;
+  // gemm_dma128_kernel: the same conditions on 128 x 128 tiles, with the fast epilogue only.
+  const bool dma128_nn = aligned && g.N % 8 == 0 && g.K % 8 == 0 && 127 * g.sa_m + g.K <= 0x3fffffffLL &&
+                         (g.K - 1) * g.sb_k + 128 <= 0x3fffffffLL && g.K >= 3 * 32;
+  const bool dma128_bt = g.sa_k == 1 && g.sb_k == 1 && g.sa_m >= 0 && (uintptr_t)g.a % 16 == 0 &&
+                         (uintptr_t)g.b % 16 == 0 && (g.sa_m * 2) % 16 == 0 && (g.sb_n * 2) % 16 == 0 && g.sb_n > 0 &&
+                         g.K % 8 == 0 && 127 * g.sa_m + g.K <= 0x3fffffffLL && 127 * g.sb_n + g.K <= 0x3fffffffLL &&
+                         g.K >= 3 * 32 && !dma128_nn;
+  const int64_t tiles128 = cdiv(g.M, 128) * cdiv(g.N, 128);
+  const bool ok128 = (dma128_nn || dma128_bt) && out_vec && c_vec && g.N % 8 == 0 && tiles128 <= 0x7fffffffLL;
+  if ((config == 1 && !dma_ok) || (config == 2 && !fast) || (config == 4 && !ok128)) return NT_ERR_INVALID;
+  if (config == 4 || (config == 0 && ok128 && tiles_m * tiles_n < DMA128_BELOW)) {
+    g.tiles_m = (int)cdiv(g.M, 128);
+    g.tiles_n = (int)cdiv(g.N, 128);
+    g.c_pre = 1;
+    const dim3 grid128((unsigned)tiles128);
+    if (dma128_bt)
+      hipLaunchKernelGGL((gemm_dma128_kernel<T, true>), grid128, dim3(256), 0, stream, g);
+    else
+      hipLaunchKernelGGL((gemm_dma128_kernel<T, false>), grid128, dim3(256), 0, stream, g);
+    return launch_status();
+  }
   const bool use_dma = config == 0 ? dma_ok : config == 1;
   const bool use_fast8 = config == 0 ? fast && !dma_ok : config == 2;
   g.c_pre = use_dma && out_vec && c_vec && g.N % 8 == 0;

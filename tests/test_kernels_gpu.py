@@ -356,8 +356,9 @@ def test_gemm_dma_ragged(mnk, dtype):
     assert torch.allclose(out32, a.float() @ b.float(), atol=tol, rtol=1e-3)
 
 
+@pytest.mark.parametrize("config", (1, 4))
 @pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
-def test_gemm_dma_ragged_reads_nothing_past_the_matrix(dtype):
+def test_gemm_dma_ragged_reads_nothing_past_the_matrix(dtype, config):
     # a and b are views of larger buffers filled with inf past K (a's columns, b's rows) and
     # past N (b's columns); out is a view whose neighbours must stay untouched.  A value
     # past K reaching the product would give inf * 0 = nan; one past N, a wrong column.
@@ -370,22 +371,63 @@ def test_gemm_dma_ragged_reads_nothing_past_the_matrix(dtype):
     a, b = abuf[:, :k], bbuf[:k, :n]
     obuf = torch.full((m + 1, n + 8), 7.0, dtype=dtype, device=DEV)
     out = obuf[:m, :n]
-    kernels.gemm(a, b, out, config=1)
+    kernels.gemm(a, b, out, config=config)
     assert torch.isfinite(out).all()
     assert torch.allclose(out.float(), a.float() @ b.float(), atol=2e-2, rtol=1e-2)
     assert torch.all(obuf[:, n:] == 7.0) and torch.all(obuf[m:] == 7.0)
 
 
+@pytest.mark.parametrize("config", (1, 4))
 @pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
-def test_gemm_dma_ragged_broadcast_bias(dtype):
+def test_gemm_dma_ragged_broadcast_bias(dtype, config):
     # c broadcast along rows (row stride 0) on a ragged shape: the fast epilogue's c resource.
     m, n, k = 777, 520, 264
     a, b = _randn((m, k), dtype, 65), _randn((k, n), dtype, 66)
     c = _randn((n,), dtype, 67).expand(m, n)
     out = torch.empty((m, n), dtype=dtype, device=DEV)
-    kernels.gemm(a, b, out, c=c, alpha=1.0, beta=0.5, config=1)
+    kernels.gemm(a, b, out, c=c, alpha=1.0, beta=0.5, config=config)
     ref = _gemm_ref(a, b, c, 1.0, 0.5, None)
     assert torch.allclose(out.float(), ref.float(), atol=2e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("bt", (False, True))
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+@pytest.mark.parametrize("mnk", ((2048, 2048, 2048), (1000, 1024, 512), (264, 776, 1000), (300, 264, 104),
+                                 (520, 2056, 96), (128, 128, 96), (1, 8, 96)))
+def test_gemm_dma128(mnk, dtype, bt):
+    # The DMA kernel on 128 x 128 tiles (forced): ragged M, N and K multiples of 8 with a
+    # partial last k-tile (1000, 104), b row-major or k-contiguous, with and without c; out is
+    # a view whose neighbouring columns and row must stay untouched.
+    m, n, k = mnk
+    a = _randn((m, k), dtype, 90)
+    b = _randn((n, k), dtype, 91).t() if bt else _randn((k, n), dtype, 91)
+    c = _randn((m, n), dtype, 92)
+    rd = torch.float16 if dtype == torch.float16 else None
+    obuf = torch.full((m + 1, n + 8), 7.0, dtype=dtype, device=DEV)
+    out = obuf[:m, :n]
+    kernels.gemm(a, b, out, c=c, alpha=0.5, beta=2.0, round_dtype=rd, config=4)
+    ref = _gemm_ref(a, b.contiguous(), c, 0.5, 2.0, rd)
+    tol = 1e-2 * max(1.0, math.sqrt(k) / 8)
+    assert torch.allclose(out.float(), ref.float(), atol=tol, rtol=1e-2)
+    assert torch.all(obuf[:, n:] == 7.0) and torch.all(obuf[m:] == 7.0)
+    out2 = torch.empty((m, n), dtype=dtype, device=DEV)
+    kernels.gemm(a, b, out2, config=4)
+    assert torch.allclose(out2.float(), a.float() @ b.float(), atol=tol, rtol=1e-2)
+
+
+def test_gemm_dma128_rejects_what_its_epilogue_cannot_store():
+    from ninetoothed_amd.errors import KernelLaunchError
+
+    a, b = _randn((256, 128), torch.float16, 93), _randn((128, 256), torch.float16, 94)
+    out32 = torch.full((256, 256), 7.0, dtype=torch.float32, device=DEV)
+    with pytest.raises(KernelLaunchError):  # fp32 out: the element-wise epilogue only
+        kernels.gemm(a, b, out32, config=4)
+    assert torch.all(out32 == 7.0)
+    b_odd = _randn((128, 260), torch.float16, 95)[:, :252]  # N % 8 != 0
+    out = torch.full((256, 252), 7.0, dtype=torch.float16, device=DEV)
+    with pytest.raises(KernelLaunchError):
+        kernels.gemm(a, b_odd, out, config=4)
+    assert torch.all(out == 7.0)
 
 
 def test_gemm_forced_config_rejects_unfit_call():
@@ -393,9 +435,9 @@ def test_gemm_forced_config_rejects_unfit_call():
 
     a, b = _randn((300, 100), torch.float16, 53), _randn((100, 200), torch.float16, 54)
     out = torch.full((300, 200), 7.0, dtype=torch.float16, device=DEV)
-    # K = 100 (rows of a not 16-byte aligned) fits neither the DMA kernel nor (M, N not
+    # K = 100 (rows of a not 16-byte aligned) fits neither the DMA kernels nor (M, N not
     # multiples of 256) the register-staged one: rejected before launching
-    for config in (1, 2):
+    for config in (1, 2, 4):
         with pytest.raises(KernelLaunchError):
             kernels.gemm(a, b, out, config=config)
     assert torch.all(out == 7.0)
@@ -467,16 +509,18 @@ def test_gemm_negative_row_strides():
     assert torch.allclose(out.float(), ref, atol=1e-2, rtol=1e-2), (out.float() - ref).abs().max()
 
 
+@pytest.mark.parametrize("config", (1, 4))
 @pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
-def test_gemm_dma_b_transposed_reads_nothing_past_k(dtype):
+def test_gemm_dma_b_transposed_reads_nothing_past_k(dtype, config):
     # b^T rows are a view of a wider buffer holding inf past K: those values must not
-    # reach the product (the last k-tile's chunks past K read zeros).
-    m, n, k = 264, 300, 200
+    # reach the product (the last k-tile's chunks past K read zeros).  N = 300 on the 256-wide
+    # kernel (any N with b^T), 296 on the 128-wide one (its epilogue stores 8 columns a lane).
+    m, n, k = 264, 300 if config == 1 else 296, 200
     bt_buf = torch.full((n, k + 8), float("inf"), dtype=dtype, device=DEV)
     bt_buf[:, :k] = _randn((n, k), dtype, 73)
     a, b = _randn((m, k), dtype, 74), bt_buf[:, :k].t()
     out = torch.empty((m, n), dtype=dtype, device=DEV)
-    kernels.gemm(a, b, out, config=1)
+    kernels.gemm(a, b, out, config=config)
     assert torch.isfinite(out).all()
     assert torch.allclose(out.float(), a.float() @ b.float(), atol=2e-2, rtol=1e-2)
 
