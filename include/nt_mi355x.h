@@ -279,7 +279,10 @@ int nt_conv2d_bf16(const void* x, const int64_t* x_strides, const void* w, const
  * read in place, N-C-H-W, by the 224-position strip kernel, only the filter re-laid into the
  * workspace: stride and dilation 1, C % 32 == 0, Q dividing 224 and 224 / Q dividing P,
  * unit w stride, W % 8 == 0, 16-byte aligned input rows, W + pw and Q + S - 1 at most
- * Q + 16, y of the input type).  A forced path whose
+ * Q + 16, y of the input type; 6 = 1 x 1 filters at stride 1 without padding as a batch of
+ * N products (filter [K, C] times image [C, H W]) on the 128 x 128-tile GEMM kernel, no
+ * workspace: unit C stride of the filter, H W positions back to back in x and y with
+ * 16-byte aligned rows, H W and C multiples of 8, C >= 96, a 16-bit y).  A forced path whose
  * conditions do not hold returns NT_ERR_INVALID before launching.  Replaces the
  * per-configuration launchers the reference's auto-tuner times
  * (src/ninetoothed/compiler/driver.py:975-1031, tests/test_conv2d.py:109-113). */

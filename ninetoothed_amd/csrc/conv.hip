@@ -1449,9 +1449,10 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
   // config: 0 = the fastest path whose conditions hold; 1 = re-laid input through the DMA
   // kernel, 2 = re-laid input through conv_nhwc_kernel, 3 = the direct kernel (no
   // workspace), 4 = re-laid input through the DMA kernel of 224-position tiles, 5 = the
-  // input read in place by conv_strip224_kernel (only the filter re-laid).  A forced path
-  // whose conditions do not hold is rejected before launching.
-  if (config < 0 || config > 5) return NT_ERR_INVALID;
+  // input read in place by conv_strip224_kernel (only the filter re-laid), 6 = 1 x 1 filters
+  // as a batch of products on gemm_dma128_kernel.  A forced path whose conditions do not
+  // hold is rejected before launching.
+  if (config < 0 || config > 6) return NT_ERR_INVALID;
   if (N < 0 || C < 0 || H < 0 || W < 0 || K < 0 || R < 0 || S < 0 || P < 0 || Q < 0 || ph < 0 || pw < 0 || sh <= 0 ||
       sw <= 0 || dh <= 0 || dw <= 0)
     return NT_ERR_INVALID;
@@ -1478,6 +1479,19 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
   if (tiles_k * tiles_m > 0x7fffffffLL) return NT_ERR_INVALID;
   g.tiles_k = (int)tiles_k;
   g.tiles_m = (int)tiles_m;
+  // 1 x 1 filters at stride 1 without padding, over images whose H W positions are back to
+  // back (unit w stride, rows adjacent) into an output laid out alike: output image n
+  // [K, P Q] is the filter [K, C] times input image n [C, H W], so the N products run as one
+  // batch on gemm_dma128_kernel, the input read in place (gemm16_batch128 checks alignment,
+  // strides and sizes and declines, launching nothing, what it does not take).
+  if (config == 0 || config == 6) {
+    const bool one_by_one = R == 1 && S == 1 && ph == 0 && pw == 0 && sh == 1 && sw == 1 && dh == 1 && dw == 1 &&
+                            xs[3] == 1 && xs[2] == W && ys[3] == 1 && ys[2] == Q && ws[1] == 1 && N <= 65535;
+    const int e = one_by_one ? gemm16_batch128(elem<T>::code, w, ws[0], 0, x, xs[1], xs[0], y, ys[1], ys[0], y_dtype, K,
+                                               P * Q, C, N, round_dtype, stream)
+                             : NT_ERR_INVALID;
+    if (e != NT_ERR_INVALID || config == 6) return e;
+  }
   const int64_t Hp = H + 2 * ph, Wp = W + 2 * pw;
   // The re-laid input and filter carry Cl channels: C rounded up to 32 for the DMA kernel
   // (its 32-deep k-tiles stay inside one filter tap), to 64 for conv_nhwc_kernel (64-deep

@@ -41,6 +41,9 @@ struct GemmArgs {
   int tiles_m, tiles_n;
   int c_pre;  // gemm_dma_kernel's fast epilogue: 16-bit out (and c) with unit column stride,
               // 16-byte aligned rows, out and c panel offsets within 32 bits
+  // gemm_dma128_kernel only: product blockIdx.y of a batch, its a, b and out at these element
+  // strides from the first's (0 outside a batch).
+  int64_t sa_b, sb_b, so_b;
 };
 
 // Map a linear workgroup id to an output tile so that consecutive ids on one XCD
@@ -789,6 +792,11 @@ __device__ __forceinline__ int bsw(int k) { return k & 3; }
 template <typename T, bool BT = false>
 __global__ __launch_bounds__(256) void gemm_dma128_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(1024))) char lds[dma128::LDS];
+  if (blockIdx.y) {  // product blockIdx.y of a batch (no c)
+    g.a = (const uint16_t*)g.a + blockIdx.y * g.sa_b;
+    g.b = (const uint16_t*)g.b + blockIdx.y * g.sb_b;
+    g.out = (uint16_t*)g.out + blockIdx.y * g.so_b;
+  }
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1623,6 +1631,43 @@ static int gemm32_launch(GemmArgs g, hipStream_t stream) {
     hipLaunchKernelGGL(gemm_f32_kernel<true>, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, stream, g);
   else
     hipLaunchKernelGGL(gemm_f32_kernel<false>, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, stream, g);
+  return launch_status();
+}
+
+// A batch of 16-bit products out_i = round(a_i @ b_i) (a_i = a + i sa_b, and so on; no c,
+// alpha 1) on gemm_dma128_kernel: conv2d's 1 x 1 filters over N-C-H-W images, a = the filter
+// [K, C], b_i = image i [C, H W], out_i = output image i [K, P Q].  a k-contiguous, b and out
+// row-major with 16-byte aligned rows, N and K multiples of 8, K at least 96, 16-bit out;
+// NT_ERR_INVALID (nothing launched) otherwise.
+int gemm16_batch128(int dtype, const void* a, int64_t sa_m, int64_t sa_b, const void* b, int64_t sb_k, int64_t sb_b,
+                    void* out, int64_t so_m, int64_t so_b, int out_dtype, int64_t M, int64_t N, int64_t K,
+                    int64_t batch, int round_dtype, hipStream_t stream) {
+  if (dtype != NT_DTYPE_F16 && dtype != NT_DTYPE_BF16) return NT_ERR_INVALID;
+  if (out_dtype != NT_DTYPE_F16 && out_dtype != NT_DTYPE_BF16) return NT_ERR_INVALID;
+  if (M <= 0 || N <= 0 || K < 3 * 32 || batch <= 0 || batch > 65535) return NT_ERR_INVALID;
+  if (!a || !b || !out || N % 8 || K % 8 || sa_m < 0 || sb_k < 0 || so_m < 0 || sa_b < 0 || sb_b < 0 || so_b < 0)
+    return NT_ERR_INVALID;
+  if ((uintptr_t)a % 16 || (uintptr_t)b % 16 || (uintptr_t)out % 16 || sa_m % 8 || sb_k % 8 || so_m % 8 ||
+      sa_b % 8 || sb_b % 8 || so_b % 8)
+    return NT_ERR_INVALID;
+  if (127 * sa_m + K > 0x3fffffffLL || (K - 1) * sb_k + 128 > 0x3fffffffLL) return NT_ERR_INVALID;
+  const int64_t tiles = cdiv(M, 128) * cdiv(N, 128);
+  if (tiles > 0x7fffffffLL) return NT_ERR_INVALID;
+  GemmArgs g{};
+  g.a = a; g.b = b; g.out = out;
+  g.sa_m = sa_m; g.sa_k = 1; g.sb_k = sb_k; g.sb_n = 1; g.so_m = so_m; g.so_n = 1;
+  g.sa_b = sa_b; g.sb_b = sb_b; g.so_b = so_b;
+  g.M = M; g.N = N; g.K = K;
+  g.alpha = 1.0f; g.beta = 0.0f;
+  g.out_dtype = out_dtype; g.c_dtype = out_dtype; g.round_dtype = round_dtype;
+  g.tiles_m = (int)cdiv(M, 128);
+  g.tiles_n = (int)cdiv(N, 128);
+  g.c_pre = 1;
+  const dim3 grid((unsigned)tiles, (unsigned)batch);
+  if (dtype == NT_DTYPE_F16)
+    hipLaunchKernelGGL((gemm_dma128_kernel<f16_t, false>), grid, dim3(256), 0, stream, g);
+  else
+    hipLaunchKernelGGL((gemm_dma128_kernel<bf16_t, false>), grid, dim3(256), 0, stream, g);
   return launch_status();
 }
 

@@ -806,6 +806,51 @@ def test_conv2d_strip224(case, dtype):
     assert torch.equal(y5, y4)
 
 
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+@pytest.mark.parametrize("case", (
+    # (N, C, H, W), K: 1 x 1 filters as a batch of products on the 128 x 128-tile GEMM kernel
+    # (config 6): ResNet's bottleneck shapes, one image, a K no multiple of 8 (ragged M of the
+    # products), C = 96 (three 32-deep k-tiles), H W = 8 (one 128-wide tile, mostly past N).
+    ((4, 256, 56, 56), 64), ((4, 128, 56, 56), 256), ((8, 512, 28, 28), 128), ((1, 128, 16, 24), 200),
+    ((3, 96, 4, 2), 37), ((2, 1024, 28, 28), 256),
+))
+def test_conv2d_1x1_as_batched_gemm(case, dtype):
+    (n, c, h, w_), k = case
+    x = _randn((n, c, h, w_), dtype, 96)
+    w = _randn((k, c, 1, 1), dtype, 97, 1.0 / math.sqrt(c))
+    ref = F.conv2d(x.float(), w.float())
+    ybuf = torch.full((n, k + 1, h, w_), 7.0, dtype=dtype, device=DEV)
+    y6 = ybuf[:, :k]  # image stride past K * H * W; the extra channel must stay untouched
+    kernels.conv2d(x, w, y6, config=6)
+    y0 = torch.empty(ref.shape, dtype=dtype, device=DEV)
+    kernels.conv2d(x, w, y0)  # the default takes the same path
+    tol = 2e-2 if dtype == torch.bfloat16 else 1e-2
+    assert torch.allclose(y6.float(), ref, atol=tol, rtol=tol)
+    assert torch.equal(y0, y6)
+    assert torch.all(ybuf[:, k:] == 7.0)
+
+
+def test_conv2d_1x1_path_declines_what_it_cannot_take():
+    from ninetoothed_amd.errors import KernelLaunchError
+
+    def forced(xshape, wshape, padding=(0, 0), x=None):
+        x = _randn(xshape, torch.float16, 98) if x is None else x
+        w = _randn(wshape, torch.float16, 99, 0.05)
+        ref = F.conv2d(x.float(), w.float(), padding=padding)
+        y = torch.full(ref.shape, 7.0, dtype=torch.float16, device=DEV)
+        with pytest.raises(KernelLaunchError):
+            kernels.conv2d(x, w, y, padding=padding, config=6)
+        assert torch.all(y == 7.0)
+        kernels.conv2d(x, w, y, padding=padding, workspace=_workspace(x, w, padding))  # the default runs elsewhere
+        assert torch.allclose(y.float(), ref, atol=2e-2, rtol=1e-2)
+
+    forced((2, 128, 14, 14), (64, 128, 1, 1))               # H W = 196, no multiple of 8
+    forced((2, 64, 16, 16), (64, 64, 1, 1))                 # C = 64 < 96
+    forced((2, 128, 16, 16), (64, 128, 3, 3), (1, 1))       # a 3 x 3 filter
+    forced((2, 128, 16, 16), (64, 128, 1, 1), (1, 1))       # padding
+    forced(None, (64, 128, 1, 1), x=_randn((2, 128, 16, 16), torch.float16, 100).transpose(2, 3))  # w stride 16
+
+
 def test_conv2d_strip224_reads_each_calls_filter():
     # Calls that reuse one workspace (which holds the re-laid filter) with a new filter each
     # time, back to back on one stream, must each see their own filter.
