@@ -1363,6 +1363,36 @@ __global__ __launch_bounds__(144) void filter_cb9_kernel(const uint16_t* __restr
   }
 }
 
+// conv2d's 1 x 1 path when H W is no multiple of 8: each input image's rows [C][H W] copied
+// into [N][C][HWp] (HWp = H W rounded up to 8, zeros past H W), so that the batch of products
+// reads 16-byte aligned rows; one lane per 8 destination elements, one 16-byte store.
+__global__ __launch_bounds__(256) void rows_pad8_kernel(const uint16_t* __restrict__ x, int64_t xs0, int64_t xs1,
+                                                        uint16_t* __restrict__ dst, int64_t N, int64_t C, int64_t HW,
+                                                        int64_t HWp) {
+  const int64_t per_row = HWp / 8, total = N * C * per_row;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int64_t row = e / per_row, j0 = (e - row * per_row) * 8;
+    const int64_t n = row / C, c = row - n * C;
+    const uint16_t* src = x + n * xs0 + c * xs1;
+    uint16_t v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = j0 + i < HW ? src[j0 + i] : (uint16_t)0;
+    *(u32x4*)(dst + row * HWp + j0) = *(const u32x4*)v;
+  }
+}
+
+// ... and the products' [N][K][HWp] back into y's images: y[n][k][j] for j < H W.
+__global__ __launch_bounds__(256) void rows_unpad_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ y,
+                                                         int64_t ys0, int64_t ys1, int64_t N, int64_t K, int64_t HW,
+                                                         int64_t HWp) {
+  const int64_t total = N * K * HW;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int64_t row = e / HW, j = e - row * HW;
+    const int64_t n = row / K, k = row - n * K;
+    y[n * ys0 + k * ys1 + j] = src[row * HWp + j];
+  }
+}
+
 // Sum of conv_dma_kernel's split partials: one lane per 8 consecutive output positions of
 // one channel, rounded and stored as one 16-byte vector when they share an output row
 // (qvec), else element by element.
@@ -1484,12 +1514,33 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
   // [K, P Q] is the filter [K, C] times input image n [C, H W], so the N products run as one
   // batch on gemm_dma128_kernel, the input read in place (gemm16_batch128 checks alignment,
   // strides and sizes and declines, launching nothing, what it does not take).
+  // When H W is no multiple of 8, the images go through the workspace with rows padded to
+  // a multiple of 8 (zeros past H W, whose products are dropped on the way back).
   if (config == 0 || config == 6) {
     const bool one_by_one = R == 1 && S == 1 && ph == 0 && pw == 0 && sh == 1 && sw == 1 && dh == 1 && dw == 1 &&
                             xs[3] == 1 && xs[2] == W && ys[3] == 1 && ys[2] == Q && ws[1] == 1 && N <= 65535;
-    const int e = one_by_one ? gemm16_batch128(elem<T>::code, w, ws[0], 0, x, xs[1], xs[0], y, ys[1], ys[0], y_dtype, K,
-                                               P * Q, C, N, round_dtype, stream)
-                             : NT_ERR_INVALID;
+    int e = one_by_one ? gemm16_batch128(elem<T>::code, w, ws[0], 0, x, xs[1], xs[0], y, ys[1], ys[0], y_dtype, K,
+                                         P * Q, C, N, round_dtype, stream)
+                       : NT_ERR_INVALID;
+    const int64_t HW = H * W, HWp = cdiv(HW, 8) * 8;
+    const int64_t xb = cdiv(N * C * HWp * 2, 256) * 256, yb = N * K * HWp * 2;
+    if (e == NT_ERR_INVALID && one_by_one && HW % 8 != 0 && workspace && (uintptr_t)workspace % 256 == 0 &&
+        workspace_bytes >= xb + yb) {
+      uint16_t* xp = (uint16_t*)workspace;
+      uint16_t* yp = (uint16_t*)((char*)workspace + xb);
+      if (gemm16_batch128(elem<T>::code, w, ws[0], 0, xp, HWp, C * HWp, yp, HWp, K * HWp, y_dtype, K, HWp, C, N,
+                          round_dtype, stream, true) == 0) {
+        const int64_t pad_blocks = cdiv(N * C * (HWp / 8), 256), back_blocks = cdiv(N * K * HW, 256);
+        hipLaunchKernelGGL(rows_pad8_kernel, dim3((unsigned)(pad_blocks < 16384 ? pad_blocks : 16384)), dim3(256), 0,
+                           stream, (const uint16_t*)x, xs[0], xs[1], xp, N, C, HW, HWp);
+        e = gemm16_batch128(elem<T>::code, w, ws[0], 0, xp, HWp, C * HWp, yp, HWp, K * HWp, y_dtype, K, HWp, C, N,
+                            round_dtype, stream);
+        if (e) return e;
+        hipLaunchKernelGGL(rows_unpad_kernel, dim3((unsigned)(back_blocks < 16384 ? back_blocks : 16384)), dim3(256),
+                           0, stream, (const uint16_t*)yp, (uint16_t*)y, ys[0], ys[1], N, K, HW, HWp);
+        return launch_status();
+      }
+    }
     if (e != NT_ERR_INVALID || config == 6) return e;
   }
   const int64_t Hp = H + 2 * ph, Wp = W + 2 * pw;
@@ -1650,7 +1701,14 @@ extern "C" int64_t nt_conv2d_workspace_size(int64_t N, int64_t C, int64_t H, int
   int64_t per = 0;
   const int64_t sp = nt::conv_splits(nt::cdiv(K, nt::CB_K) * nt::cdiv(M, nt::CB_M), cd * R * S / 32, K, M, INT64_MAX,
                                      &per);
-  return base + (sp > 1 ? sp * K * M * 4 : 0);
+  const int64_t relaid = base + (sp > 1 ? sp * K * M * 4 : 0);
+  // 1 x 1 filters over H W no multiple of 8: the padded images and products
+  if (R == 1 && S == 1 && ph == 0 && pw == 0 && (H * W) % 8 != 0) {
+    const int64_t HWp = nt::cdiv(H * W, 8) * 8;
+    const int64_t padded = nt::cdiv(N * C * HWp * 2, 256) * 256 + N * K * HWp * 2;
+    return padded > relaid ? padded : relaid;
+  }
+  return relaid;
 }
 
 #define NT_CONV_ENTRY(NAME, T)                                                                                       \

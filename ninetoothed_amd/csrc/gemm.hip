@@ -1638,10 +1638,11 @@ static int gemm32_launch(GemmArgs g, hipStream_t stream) {
 // alpha 1) on gemm_dma128_kernel: conv2d's 1 x 1 filters over N-C-H-W images, a = the filter
 // [K, C], b_i = image i [C, H W], out_i = output image i [K, P Q].  a k-contiguous, b and out
 // row-major with 16-byte aligned rows, N and K multiples of 8, K at least 96, 16-bit out;
-// NT_ERR_INVALID (nothing launched) otherwise.
+// NT_ERR_INVALID (nothing launched) otherwise.  check_only: 0 when it would launch, and no
+// launch.
 int gemm16_batch128(int dtype, const void* a, int64_t sa_m, int64_t sa_b, const void* b, int64_t sb_k, int64_t sb_b,
                     void* out, int64_t so_m, int64_t so_b, int out_dtype, int64_t M, int64_t N, int64_t K,
-                    int64_t batch, int round_dtype, hipStream_t stream) {
+                    int64_t batch, int round_dtype, hipStream_t stream, bool check_only) {
   if (dtype != NT_DTYPE_F16 && dtype != NT_DTYPE_BF16) return NT_ERR_INVALID;
   if (out_dtype != NT_DTYPE_F16 && out_dtype != NT_DTYPE_BF16) return NT_ERR_INVALID;
   if (M <= 0 || N <= 0 || K < 3 * 32 || batch <= 0 || batch > 65535) return NT_ERR_INVALID;
@@ -1653,6 +1654,7 @@ int gemm16_batch128(int dtype, const void* a, int64_t sa_m, int64_t sa_b, const 
   if (127 * sa_m + K > 0x3fffffffLL || (K - 1) * sb_k + 128 > 0x3fffffffLL) return NT_ERR_INVALID;
   const int64_t tiles = cdiv(M, 128) * cdiv(N, 128);
   if (tiles > 0x7fffffffLL) return NT_ERR_INVALID;
+  if (check_only) return 0;
   GemmArgs g{};
   g.a = a; g.b = b; g.out = out;
   g.sa_m = sa_m; g.sa_k = 1; g.sb_k = sb_k; g.sb_n = 1; g.so_m = so_m; g.so_n = 1;

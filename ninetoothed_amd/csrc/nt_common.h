@@ -128,9 +128,10 @@ inline bool valid_round(int d) { return d == NT_DTYPE_NONE || d == NT_DTYPE_F16 
 inline int launch_status() { return (int)hipGetLastError(); }
 
 // gemm.hip: a batch of 16-bit products on gemm_dma128_kernel (conv2d's 1 x 1 filters);
-// NT_ERR_INVALID, with nothing launched, for a call it does not take.
+// NT_ERR_INVALID, with nothing launched, for a call it does not take; with check_only, 0
+// for one it would take, launching nothing either way.
 int gemm16_batch128(int dtype, const void* a, int64_t sa_m, int64_t sa_b, const void* b, int64_t sb_k, int64_t sb_b,
                     void* out, int64_t so_m, int64_t so_b, int out_dtype, int64_t M, int64_t N, int64_t K,
-                    int64_t batch, int round_dtype, hipStream_t stream);
+                    int64_t batch, int round_dtype, hipStream_t stream, bool check_only = false);
 
 }  // namespace nt

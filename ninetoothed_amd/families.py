@@ -355,7 +355,7 @@ class ConvPlan(Plan):
         from ninetoothed_amd import kernels
 
         x, w, y = values[self.x], values[self.w], values[self.y]
-        nbytes = 0 if self.config in (3, 6) else kernels.conv2d_workspace_bytes(x, w, self.padding)
+        nbytes = 0 if self.config == 3 else kernels.conv2d_workspace_bytes(x, w, self.padding)
         launch = kernels.bind_conv2d(x, w, y, padding=self.padding, stride=self.stride, dilation=self.dilation,
                                      round_dtype=self.round_dtype, workspace_bytes=nbytes, config=self.config)
         ix, iw, iy = index[self.x], index[self.w], index[self.y]

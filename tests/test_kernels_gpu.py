@@ -813,6 +813,8 @@ def test_conv2d_strip224(case, dtype):
     # products), C = 96 (three 32-deep k-tiles), H W = 8 (one 128-wide tile, mostly past N).
     ((4, 256, 56, 56), 64), ((4, 128, 56, 56), 256), ((8, 512, 28, 28), 128), ((1, 128, 16, 24), 200),
     ((3, 96, 4, 2), 37), ((2, 1024, 28, 28), 256),
+    # H W no multiple of 8: the images through the workspace with rows padded to 8
+    ((4, 1024, 14, 14), 256), ((8, 2048, 7, 7), 512), ((2, 96, 3, 5), 40), ((1, 256, 1, 1), 24),
 ))
 def test_conv2d_1x1_as_batched_gemm(case, dtype):
     (n, c, h, w_), k = case
@@ -821,9 +823,10 @@ def test_conv2d_1x1_as_batched_gemm(case, dtype):
     ref = F.conv2d(x.float(), w.float())
     ybuf = torch.full((n, k + 1, h, w_), 7.0, dtype=dtype, device=DEV)
     y6 = ybuf[:, :k]  # image stride past K * H * W; the extra channel must stay untouched
-    kernels.conv2d(x, w, y6, config=6)
+    ws = _workspace(x, w, (0, 0)) if (h * w_) % 8 else None
+    kernels.conv2d(x, w, y6, workspace=ws, config=6)
     y0 = torch.empty(ref.shape, dtype=dtype, device=DEV)
-    kernels.conv2d(x, w, y0)  # the default takes the same path
+    kernels.conv2d(x, w, y0, workspace=ws)  # the default takes the same path
     tol = 2e-2 if dtype == torch.bfloat16 else 1e-2
     assert torch.allclose(y6.float(), ref, atol=tol, rtol=tol)
     assert torch.equal(y0, y6)
@@ -844,7 +847,7 @@ def test_conv2d_1x1_path_declines_what_it_cannot_take():
         kernels.conv2d(x, w, y, padding=padding, workspace=_workspace(x, w, padding))  # the default runs elsewhere
         assert torch.allclose(y.float(), ref, atol=2e-2, rtol=1e-2)
 
-    forced((2, 128, 14, 14), (64, 128, 1, 1))               # H W = 196, no multiple of 8
+    forced((2, 128, 14, 14), (64, 128, 1, 1))               # H W = 196, no multiple of 8, and no workspace
     forced((2, 64, 16, 16), (64, 64, 1, 1))                 # C = 64 < 96
     forced((2, 128, 16, 16), (64, 128, 3, 3), (1, 1))       # a 3 x 3 filter
     forced((2, 128, 16, 16), (64, 128, 1, 1), (1, 1))       # padding
