@@ -282,7 +282,10 @@ int nt_conv2d_bf16(const void* x, const int64_t* x_strides, const void* w, const
  * Q + 16, y of the input type; 6 = 1 x 1 filters at stride 1 without padding as a batch of
  * N products (filter [K, C] times image [C, H W]) on the 128 x 128-tile GEMM kernel, no
  * workspace: unit C stride of the filter, H W positions back to back in x and y with
- * 16-byte aligned rows, H W and C multiples of 8, C >= 96, a 16-bit y).  A forced path whose
+ * 16-byte aligned rows, H W and C multiples of 8, C >= 96, a 16-bit y; H W no multiple of 8
+ * through the workspace with rows padded to 8); 7 = the re-laid input through the DMA kernel
+ * of 128 x 128 tiles (four waves, two workgroups per CU), as 1 otherwise; the default for
+ * outputs of fewer than 136 tiles of 256 x 256).  A forced path whose
  * conditions do not hold returns NT_ERR_INVALID before launching.  Replaces the
  * per-configuration launchers the reference's auto-tuner times
  * (src/ninetoothed/compiler/driver.py:975-1031, tests/test_conv2d.py:109-113). */

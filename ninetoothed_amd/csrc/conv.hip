@@ -608,18 +608,23 @@ __device__ __forceinline__ void load_lds16(u32x4 rs, uint32_t lds_addr, int voff
 }
 }  // namespace cdma
 
-template <typename T>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void conv_dma_kernel(
+template <typename T, int TW = 256>
+__global__ __launch_bounds__(TW * 2) __attribute__((amdgpu_waves_per_eu(2, 2))) void conv_dma_kernel(
     const uint16_t* __restrict__ xp, const uint16_t* __restrict__ wt, ConvArgs g, int64_t Hp, int64_t Wp) {
-  __shared__ __attribute__((aligned(1024))) char lds[cdma::EPI + 8 * 4096];
+  // TW: the tile, TW channels x TW positions (256: eight waves of 128 x 64; 128: four waves
+  // of 64 x 64, 80 KiB of LDS, two workgroups per CU, for outputs of few 256 x 256 tiles).
+  static_assert(TW == 256 || TW == 128, "256 or 128 wide tiles");
+  constexpr int NW = TW / 32, NI = TW / 64;  // waves; 32-row filter blocks per wave
+  constexpr int STAGE = TW * 64, B0 = 4 * STAGE, EPI = 8 * STAGE;
+  __shared__ __attribute__((aligned(1024))) char lds[EPI + NW * 4096];
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wk = wave >> 2, wm = wave & 3;
+  const int wk = wave / (NW / 2), wm = wave % (NW / 2);
   const int ntile = g.tiles_k * g.tiles_m;
   const int split = (int)blockIdx.x / ntile, tile = (int)blockIdx.x - split * ntile;
   const int tk = tile % g.tiles_k, tmi = tile / g.tiles_k;
-  const int k0t = tk * CB_K, m0t = tmi * CB_M;
+  const int k0t = tk * TW, m0t = tmi * TW;
   const int KG = (int)g.KG, C = (int)g.C;
   // This workgroup's k-tiles [kt0, kt1): all of them, or one split's (at least 3).
   const int kt0 = split * g.kt_per, kt1 = min(KG / 32, kt0 + g.kt_per);
@@ -653,25 +658,25 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   };
   // Load u (0..3) of tile kt into its stage: filter q0, im2col q0, filter q1, im2col q1.
   auto load_unit = [&](int u, int kt, int xo) {
-    const int st = (kt & 3) * cdma::STAGE, q = u >> 1;
+    const int st = (kt & 3) * STAGE, q = u >> 1;
     if ((u & 1) == 0)
       cdma::load_lds16(rsW, lds0 + st + 2048 * wave + 1024 * q, vw[q], kt * 64);
     else
-      cdma::load_lds16(rsX, lds0 + cdma::B0 + st + 2048 * wave + 1024 * q, vx[q], xo);
+      cdma::load_lds16(rsX, lds0 + B0 + st + 2048 * wave + 1024 * q, vx[q], xo);
   };
 
-  // Fragment reads: filter rows 128 wk + 32 i + lane % 32, im2col rows 64 wm + 32 j + lane % 32,
+  // Fragment reads: filter rows 32 NI wk + 32 i + lane % 32, im2col rows 64 wm + 32 j + lane % 32,
   // chunk 2 s + lane / 32 (the swizzle depends on lane % 32 only).
   int a_rd[2], b_rd[2];
 #pragma unroll
   for (int s2 = 0; s2 < 2; ++s2) {
-    const int ra = wk * 128 + (lane & 31), rb = wm * 64 + (lane & 31);
+    const int ra = wk * 32 * NI + (lane & 31), rb = wm * 64 + (lane & 31);
     a_rd[s2] = ra * 64 + cdma::asw(ra, 2 * s2 + (lane >> 5)) * 16;
-    b_rd[s2] = cdma::B0 + rb * 64 + cdma::asw(rb, 2 * s2 + (lane >> 5)) * 16;
+    b_rd[s2] = B0 + rb * 64 + cdma::asw(rb, 2 * s2 + (lane >> 5)) * 16;
   }
   typedef typename mfma_traits<T>::frag frag;
-  frag fa[2][4], fb[2][2];
-  // Read unit x (0..5) of slice s2 of the tile at stage byte offset st: a0, b0, b1, a1, a2, a3.
+  frag fa[2][NI], fb[2][2];
+  // Read unit x (0..NI+1) of slice s2 of the tile at stage byte offset st: a0, b0, b1, a1, ..
   auto read_unit = [&](int x, int s2, int st) {
     if (x == 0 || x >= 3) {
       const int i = x == 0 ? 0 : x - 2;
@@ -682,7 +687,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
   };
 
-  floatx16 acc[4][2];
+  floatx16 acc[NI][2];
   zero_acc(acc);
 
   // kt1 - kt0 >= 3 (the launcher checks): tiles kt0..kt0+2 in flight, wait for kt0.
@@ -693,7 +698,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
   __builtin_amdgcn_s_barrier();
 #pragma unroll
-  for (int x = 0; x < 6; ++x) read_unit(x, 0, (kt0 & 3) * cdma::STAGE);
+  for (int x = 0; x < NI + 2; ++x) read_unit(x, 0, (kt0 & 3) * STAGE);
 
 #define NT_CFENCE() __builtin_amdgcn_sched_barrier(0)
   // One k-tile, as gemm_dma_kernel's: HAS1 reads slice 0 of tile kt+1 during slice 1, LOAD
@@ -702,12 +707,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   auto step = [&](auto has1_c, auto load_c, auto vm_c, int kt) {
     constexpr bool HAS1 = decltype(has1_c)::value, LOAD = decltype(load_c)::value;
     constexpr int VM = decltype(vm_c)::value;
-    const int st = (kt & 3) * cdma::STAGE, st1 = ((kt + 1) & 3) * cdma::STAGE;
+    const int st = (kt & 3) * STAGE, st1 = ((kt + 1) & 3) * STAGE;
     const int xo3 = LOAD ? x_off(kt + 3) : 0;
-    static_for<0, 16>([&](auto m_c) {
+    static_for<0, 4 * NI>([&](auto m_c) {
       constexpr int m = decltype(m_c)::value;
-      constexpr int s2 = m >> 3, x = m & 7;
-      if constexpr (m == 8 && VM >= 0) {
+      constexpr int s2 = m / (2 * NI), x = m % (2 * NI);
+      if constexpr (m == 2 * NI && VM >= 0) {
         NT_CFENCE();
         if constexpr (VM == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
         if constexpr (VM == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -716,7 +721,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
       acc[x >> 1][x & 1] = mfma_traits<T>::mma(fa[s2][x >> 1], fb[s2][x & 1], acc[x >> 1][x & 1]);
       NT_CFENCE();
-      if constexpr (x < 6) {
+      if constexpr (x < NI + 2) {
         if constexpr (s2 == 0)
           read_unit(x, 1, st);
         else if constexpr (HAS1)
@@ -740,7 +745,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   // Epilogue: this lane's 8 output positions (columns (lane % 8) * 8 .. + 7 of the wave's 64)
   // and their (n, p, q); channels rows t * 8 + lane / 8 of each 16-row half.
-  float* stage = (float*)(lds + cdma::EPI + wave * 4096);
+  float* stage = (float*)(lds + EPI + wave * 4096);
   const int cg = (lane & 7) * 8;
   const int mpos = m0t + wm * 64 + cg;
   const bool m_ok = mpos < g.M;
@@ -768,7 +773,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // A split's partial tile, fp32, unrounded: conv_splitk_reduce_kernel sums the splits.
     float* P = g.part + (int64_t)split * g.K * g.Mp;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NI; ++i)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         wave_lds_order();
@@ -781,7 +786,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           const int rr = t * 8 + (lane >> 3);
-          const int k = k0t + wk * 128 + i * 32 + h * 16 + rr;
+          const int k = k0t + wk * 32 * NI + i * 32 + h * 16 + rr;
           if (m_ok && k < g.K) {
             float* dst = P + (int64_t)k * g.Mp + mpos;
             *(float4*)dst = *(const float4*)(stage + rr * 64 + cg);
@@ -794,7 +799,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   auto finish = [&](auto round_c) {
     constexpr int ROUND = decltype(round_c)::value;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NI; ++i)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         wave_lds_order();  // the previous half's reads come first
@@ -807,7 +812,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           const int rr = t * 8 + (lane >> 3);
-          const int k = k0t + wk * 128 + i * 32 + h * 16 + rr;
+          const int k = k0t + wk * 32 * NI + i * 32 + h * 16 + rr;
           const float4 v0 = *(const float4*)(stage + rr * 64 + cg);
           const float4 v1 = *(const float4*)(stage + rr * 64 + cg + 4);
           const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
@@ -1454,6 +1459,12 @@ static int64_t dma_channels(int64_t C, int64_t R, int64_t S) {
 // give about 256 workgroups, at most 16, each with at least 4 k-tiles (the last at least
 // 3), and no more than `room` bytes of fp32 partials (K x M each).  Returns the number of
 // splits and sets *per to the k-tiles of each.
+// The re-laid DMA path takes 128 x 128 tiles by default below this many 256 x 256 tiles:
+// measured fp16 3 x 3, it wins up to 98 such tiles ([32,128,28,28] x 128 36.7 against 64.3 us
+// on the 256-wide kernel; [4,256,56,56] x 256 36.6 against 45.6 on the strip kernel) and
+// loses at 196 (the headline, 103.8 against the strip kernel's 60.8).
+constexpr int64_t CONV128_BELOW = 136;
+
 static int64_t conv_splits(int64_t tiles, int64_t nk, int64_t K, int64_t M, int64_t room, int64_t* per) {
   *per = nk;
   if (tiles >= 128) return 1;
@@ -1480,9 +1491,10 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
   // kernel, 2 = re-laid input through conv_nhwc_kernel, 3 = the direct kernel (no
   // workspace), 4 = re-laid input through the DMA kernel of 224-position tiles, 5 = the
   // input read in place by conv_strip224_kernel (only the filter re-laid), 6 = 1 x 1 filters
-  // as a batch of products on gemm_dma128_kernel.  A forced path whose conditions do not
-  // hold is rejected before launching.
-  if (config < 0 || config > 6) return NT_ERR_INVALID;
+  // as a batch of products on gemm_dma128_kernel, 7 = re-laid input through the DMA kernel
+  // of 128 x 128 tiles.  A forced path whose conditions do not hold is rejected before
+  // launching.
+  if (config < 0 || config > 7) return NT_ERR_INVALID;
   if (N < 0 || C < 0 || H < 0 || W < 0 || K < 0 || R < 0 || S < 0 || P < 0 || Q < 0 || ph < 0 || pw < 0 || sh <= 0 ||
       sw <= 0 || dh <= 0 || dw <= 0)
     return NT_ERR_INVALID;
@@ -1564,6 +1576,13 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
   // positions that holds the padded input row, two or three raw pieces per strip, strips and
   // pieces inside LDS beside the filter ring, 32-bit offsets; the re-laid filter in the
   // workspace.
+  // Config 0 takes the re-laid input on 128 x 128 tiles for outputs of fewer than
+  // CONV128_BELOW tiles of 256 x 256, where the strip kernel's one 224-position tile per CU
+  // leaves most of the chip idle, when that path can run here.
+  const bool prefer128 = config == 0 && tiles_k * tiles_m < CONV128_BELOW && R * S > 0 &&
+                         dma_fits(dma_channels(C, R, S)) && workspace != nullptr && (uintptr_t)workspace % 256 == 0 &&
+                         workspace_bytes >= nhwc_bytes(N, dma_channels(C, R, S), H, W, K, R, S, ph, pw) &&
+                         (P - 1) * sh + (R - 1) * dh < Hp && (Q - 1) * sw + (S - 1) * dw < Wp;
   const int64_t strip_pitch = Q + 16;
   const int64_t strip_rows = Q > 0 && 224 % Q == 0 ? 224 / Q + R - 1 : 0;
   int64_t strip_np = 0;
@@ -1585,7 +1604,7 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
     return workspace != nullptr && (uintptr_t)workspace % 256 == 0 && workspace_bytes >= K * C * R * S * 2;
   }();
   if (config == 5 && !strip) return NT_ERR_INVALID;
-  if (strip && (config == 0 || config == 5)) {
+  if (strip && (config == 5 || (config == 0 && !prefer128))) {
     g.cb_order = 1;
     g.tiles_m = (int)(g.M / 224);
     uint16_t* wt = (uint16_t*)workspace;
@@ -1613,19 +1632,23 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
   // (an empty filter, R or S zero, sums nothing: the direct kernel writes the zeros)
   const bool nhwc = config != 3 && R * S > 0 && workspace != nullptr && workspace_bytes >= need && (uintptr_t)workspace % 256 == 0 &&
                     (P - 1) * sh + (R - 1) * dh < Hp && (Q - 1) * sw + (S - 1) * dw < Wp;
-  if (((config == 1 || config == 4) && !(nhwc && dma)) || (config == 2 && !nhwc)) return NT_ERR_INVALID;
+  if (((config == 1 || config == 4 || config == 7) && !(nhwc && dma)) || (config == 2 && !nhwc)) return NT_ERR_INVALID;
   if (nhwc) {
     g.C = Cl;
     g.KG = Cl * R * S;
     g.cb_order = dma ? 1 : 0;
     // Few output tiles: the DMA kernel splits the reduction, partials after the re-layout.
     const int64_t part_at = cdiv(need, 256) * 256;
+    // 128 x 128 tiles (conv_dma_kernel<T, 128>) for outputs of few 256 x 256 tiles: four
+    // times as many workgroups, two per CU, and fewer splits.
+    const bool t128 = dma && (config == 7 || (config == 0 && tiles_k * tiles_m < CONV128_BELOW));
+    const int64_t tk = t128 ? cdiv(K, 128) : tiles_k, tm = t128 ? cdiv(g.M, 128) : tiles_m;
     int64_t per = g.KG / 32;
-    const int64_t sp = dma && config != 4 ? conv_splits(tiles_k * tiles_m, g.KG / 32, K, g.Mp, workspace_bytes - part_at, &per) : 1;
+    const int64_t sp = dma && config != 4 ? conv_splits(tk * tm, g.KG / 32, K, g.Mp, workspace_bytes - part_at, &per) : 1;
     // 224-position tiles when, without a split, they leave fewer CUs idle: per CU and round
     // of 256 workgroups, a workgroup's time goes with its positions (224 or 256).
     const int64_t tiles_m224 = cdiv(g.M, CB_M224);
-    const bool m224 = dma && sp == 1 && tiles_k * tiles_m224 <= 0x7fffffffLL &&
+    const bool m224 = dma && !t128 && sp == 1 && tiles_k * tiles_m224 <= 0x7fffffffLL &&
                       (config == 4 || (config == 0 && cdiv(tiles_k * tiles_m224, 256) * 224 * 100 <
                                                           cdiv(tiles_k * tiles_m, 256) * 256 * 97));
     g.splits = (int)sp;
@@ -1663,8 +1686,15 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
       hipLaunchKernelGGL(conv_dma224_kernel<T>, dim3((unsigned)(tiles_k * tiles_m224)), dim3(512), 0, stream,
                          (const uint16_t*)xp, (const uint16_t*)wt, g, Hp, Wp);
     } else if (dma) {
-      hipLaunchKernelGGL(conv_dma_kernel<T>, dim3((unsigned)(sp * tiles_k * tiles_m)), dim3(512), 0, stream,
-                         (const uint16_t*)xp, (const uint16_t*)wt, g, Hp, Wp);
+      g.tiles_k = (int)tk;
+      g.tiles_m = (int)tm;
+      if (sp * tk * tm > 0x7fffffffLL) return NT_ERR_INVALID;
+      if (t128)
+        hipLaunchKernelGGL((conv_dma_kernel<T, 128>), dim3((unsigned)(sp * tk * tm)), dim3(256), 0, stream,
+                           (const uint16_t*)xp, (const uint16_t*)wt, g, Hp, Wp);
+      else
+        hipLaunchKernelGGL(conv_dma_kernel<T>, dim3((unsigned)(sp * tk * tm)), dim3(512), 0, stream,
+                           (const uint16_t*)xp, (const uint16_t*)wt, g, Hp, Wp);
       if (sp > 1) {
         const int64_t vecs = K * (g.Mp / 8);
         hipLaunchKernelGGL(conv_splitk_reduce_kernel<T>, dim3((unsigned)(cdiv(vecs, 256) < 4096 ? cdiv(vecs, 256) : 4096)),

@@ -377,8 +377,9 @@ def conv2d_workspace_bytes(x, w, padding=(0, 0)):
 # hold): re-laid input through the DMA kernel, re-laid input through the N-H-W-C kernel,
 # the direct kernel (no workspace), re-laid input through the DMA kernel of 224-position
 # tiles, the input read in place by the 224-position strip kernel (only the filter re-laid),
-# 1 x 1 filters as a batch of products on the 128 x 128-tile GEMM kernel (no workspace).
-CONV_CONFIGS = (1, 2, 3, 4, 5, 6)
+# 1 x 1 filters as a batch of products on the 128 x 128-tile GEMM kernel, re-laid input
+# through the DMA kernel of 128 x 128 tiles.
+CONV_CONFIGS = (1, 2, 3, 4, 5, 6, 7)
 
 
 def check_conv2d(x, w, y, round_dtype=None, config=0):

@@ -255,7 +255,8 @@ def test_conv_plans_expand_into_paths():
     ctx = h._kernel.context(dict(zip(names, (x, w, y))), {"padding_h": 1, "padding_w": 1})
     described = [p.describe() for p in families.candidates(ctx)]
     assert [(d["family"], d["config"]) for d in described] == [("conv2d", 1), ("conv2d", 2), ("conv2d", 3),
-                                                                ("conv2d", 4), ("conv2d", 5), ("conv2d", 6)]
+                                                                ("conv2d", 4), ("conv2d", 5), ("conv2d", 6),
+                                                                ("conv2d", 7)]
 
 
 @pytest.mark.gpu

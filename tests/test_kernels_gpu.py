@@ -642,10 +642,11 @@ def test_conv2d_relayout_dma(case, dtype):
     assert torch.allclose(y.float(), ref.to(torch.float16).float(), atol=2e-2, rtol=1e-2)
 
 
-@pytest.mark.parametrize("config", (1, 2, 3, 4))
+@pytest.mark.parametrize("config", (1, 2, 3, 4, 7))
 def test_conv2d_paths(config):
     # Each forced path (re-laid + DMA kernel, re-laid + N-H-W-C kernel, direct kernel,
-    # re-laid + DMA kernel of 224-position tiles) on a call all four admit.
+    # re-laid + DMA kernel of 224-position tiles, re-laid + DMA kernel of 128 x 128 tiles) on a
+    # call all five admit.
     x = _randn((2, 64, 16, 16), torch.float16, 60)
     w = _randn((96, 64, 3, 3), torch.float16, 61, 1.0 / math.sqrt(64 * 9))
     y = torch.empty((2, 96, 16, 16), dtype=torch.float16, device=DEV)
@@ -692,13 +693,14 @@ def test_conv2d_padded_channels(case, dtype):
     ((32, 512, 7, 7), (512, 3, 3), (1, 1)),   # Q = 7: partials of M rounded up to 8, stores one by one
     ((3, 96, 14, 14), (200, 3, 3), (1, 1)),
 ))
-def test_conv2d_split_reduction(case, dtype):
+@pytest.mark.parametrize("config", (1, 7))
+def test_conv2d_split_reduction(case, dtype, config):
     (n, c, h, w_), (k, r, s), padding = case
     x = _randn((n, c, h, w_), dtype, 37)
     w = _randn((k, c, r, s), dtype, 38, 1.0 / math.sqrt(c * r * s))
     ref = F.conv2d(x.float(), w.float(), padding=padding)
     y = torch.full(ref.shape, 7.0, dtype=dtype, device=DEV)
-    kernels.conv2d(x, w, y, padding=padding, workspace=_workspace(x, w, padding), config=1)
+    kernels.conv2d(x, w, y, padding=padding, workspace=_workspace(x, w, padding), config=config)
     assert torch.allclose(y.float(), ref, atol=2e-2, rtol=1e-2)
 
 
@@ -712,14 +714,15 @@ def test_conv2d_split_reduction(case, dtype):
     ((8, 64, 28, 21), (128, 1, 1), (0, 0), (1, 1)),  # C*R*S = 64: re-laid with 96 channels
     ((4, 40, 9, 11), (72, 1, 1), (0, 0), (1, 1)),
 ))
-def test_conv2d_dma_any_q(case, dtype):
+@pytest.mark.parametrize("config", (1, 7))
+def test_conv2d_dma_any_q(case, dtype, config):
     (n, c, h, w_), (k, r, s), padding, stride = case
     x = _randn((n, c, h, w_), dtype, 39)
     w = _randn((k, c, r, s), dtype, 40, 1.0 / math.sqrt(c * r * s))
     ref = F.conv2d(x.float(), w.float(), padding=padding, stride=stride)
     assert ref.shape[3] % 8 != 0
     y = torch.full(ref.shape, 7.0, dtype=dtype, device=DEV)
-    kernels.conv2d(x, w, y, padding=padding, stride=stride, workspace=_workspace(x, w, padding), config=1)
+    kernels.conv2d(x, w, y, padding=padding, stride=stride, workspace=_workspace(x, w, padding), config=config)
     assert torch.allclose(y.float(), ref, atol=2e-2, rtol=1e-2)
 
 
@@ -892,7 +895,7 @@ def test_conv2d_strip224_rejects_unfit_calls():
 
 
 @pytest.mark.parametrize("flip", ("w", "h"))
-@pytest.mark.parametrize("config", (0, 1, 3, 4))
+@pytest.mark.parametrize("config", (0, 1, 3, 4, 7))
 @pytest.mark.parametrize("xshape", ((4, 64, 15, 13), (17, 64, 45, 45)))
 def test_conv2d_flipped_output(flip, config, xshape):
     """An output flipped along w (q stride -1) or h (p stride -Q) through the C ABI, with
