@@ -1527,7 +1527,10 @@ static int conv_launch(const void* x, const int64_t* xs, const void* w, const in
   // batch on gemm_dma128_kernel, the input read in place (gemm16_batch128 checks alignment,
   // strides and sizes and declines, launching nothing, what it does not take).
   // When H W is no multiple of 8, the images go through the workspace with rows padded to
-  // a multiple of 8 (zeros past H W, whose products are dropped on the way back).
+  // a multiple of 8 (zeros past H W, whose products are dropped on the way back), if it
+  // holds them: nt_conv2d_workspace_size asks for no more than the re-laid path needs, which
+  // covers the padded images wherever that path splits the reduction (small outputs, where
+  // this one pays); elsewhere the call goes on to the re-laid path.
   if (config == 0 || config == 6) {
     const bool one_by_one = R == 1 && S == 1 && ph == 0 && pw == 0 && sh == 1 && sw == 1 && dh == 1 && dw == 1 &&
                             xs[3] == 1 && xs[2] == W && ys[3] == 1 && ys[2] == Q && ws[1] == 1 && N <= 65535;
@@ -1731,14 +1734,7 @@ extern "C" int64_t nt_conv2d_workspace_size(int64_t N, int64_t C, int64_t H, int
   int64_t per = 0;
   const int64_t sp = nt::conv_splits(nt::cdiv(K, nt::CB_K) * nt::cdiv(M, nt::CB_M), cd * R * S / 32, K, M, INT64_MAX,
                                      &per);
-  const int64_t relaid = base + (sp > 1 ? sp * K * M * 4 : 0);
-  // 1 x 1 filters over H W no multiple of 8: the padded images and products
-  if (R == 1 && S == 1 && ph == 0 && pw == 0 && (H * W) % 8 != 0) {
-    const int64_t HWp = nt::cdiv(H * W, 8) * 8;
-    const int64_t padded = nt::cdiv(N * C * HWp * 2, 256) * 256 + N * K * HWp * 2;
-    return padded > relaid ? padded : relaid;
-  }
-  return relaid;
+  return base + (sp > 1 ? sp * K * M * 4 : 0);
 }
 
 #define NT_CONV_ENTRY(NAME, T)                                                                                       \
