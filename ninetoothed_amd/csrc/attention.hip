@@ -1255,9 +1255,15 @@ static int attention_launch(const void* q, const int64_t* qs, const void* k, con
   const bool fast_fits = fast_ok(dm), pipe_fits = D == 128 && fast_fits;
   if ((config == 1 && !pipe_fits) || (config == 2 && !fast_fits)) return NT_ERR_INVALID;
   // The eight-wave kernel is the default: measured on MI355X at B=4, H=32, S=4096, D=128
-  // it runs 1,090-1,130 us non-causal against 1,140-1,270 us for the pipelined kernel.
+  // it runs 1,090-1,130 us non-causal against 1,140-1,270 us for the pipelined kernel.  Up
+  // to 128 queries a head with at least 512 heads (B H), the four-wave kernel's 128-query
+  // blocks waste half or less of what the eight-wave kernel's 256 do while the heads alone
+  // fill the chip: [16,32,64,4096,128] 250 against 302 us, [32,32,32,4096,128] 452 against
+  // 556 (fp16, interleaved medians); with fewer heads or longer queries the eight-wave one
+  // wins ([4,32,128,4096,128] 120 against 144, [16,32,256,4096,128] 347 against 472).
   const bool pipe = config == 1;
-  const bool fast = config == 2 || (config == 0 && fast_fits);
+  const bool few_queries = Sq <= AT_BM && B * H >= 512;
+  const bool fast = config == 2 || (config == 0 && fast_fits && !few_queries);
   static_assert(ap::BM == NW * 32, "both fast kernels take 256 queries per workgroup");
   const int64_t bm = pipe || fast ? NW * 32 : AT_BM;
   const int64_t qblocks = cdiv(Sq, bm);
