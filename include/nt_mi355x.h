@@ -200,7 +200,10 @@ int nt_gemm_bf16(const void* a, int64_t sa_m, int64_t sa_k, const void* b, int64
  *   3 = the element-wise loader kernel: anything;
  *   4 = the DMA kernel on 128 x 128 tiles (four waves, two workgroups per CU): the
  *       conditions of 1, and an out (and c) of the operands' 16-bit type with unit column
- *       stride and 16-byte aligned rows.
+ *       stride and 16-byte aligned rows;
+ *   5 = the few-rows kernel (the default where it fits with M <= 32, or N <= 4096): M <= 64,
+ *       a and b k-contiguous (b^T rows, x @ w.t()) with 16-byte aligned rows, K a multiple
+ *       of 8; any N, out.
  * A forced configuration whose conditions do not hold returns NT_ERR_INVALID before
  * launching.  Replaces the per-configuration launchers the reference's auto-tuner times
  * (src/ninetoothed/compiler/driver.py:975-1031, src/ninetoothed/auto_tuner.py:14-202). */

@@ -940,6 +940,89 @@ __global__ __launch_bounds__(256) void gemm_dma128_kernel(GemmArgs g) {
   dma_fast_epilogue<2, true, 2, dma128::EPI>(g, acc, lds, wave, lane, m0 + wm * 64, n0 + wn * 64);
 }
 
+// Few rows (M <= 64) against k-contiguous b (b^T rows, x @ w.t(): a linear layer on a few
+// tokens).  The product reads b once and is bound by streaming it, which the 128-wide tiles
+// spread over too few workgroups (N / 128).  Here a workgroup owns 32 columns (32 rows of
+// b^T) and every row of a; its eight waves take contiguous eighths of K and load their MFMA
+// fragments straight from memory (a lane's row of a, or column of b, at k 8 (lane / 32) ..
+// + 7 of each 16-deep step: 16 bytes per operand), MB 32-row blocks of a against the one
+// block of b^T per step, four steps in flight.  The eight partial 32 x 32 tiles are then
+// summed through LDS and finished element by element (alpha, round, beta c, any out type).
+namespace skinny {
+constexpr int NW = 8, STEPS = 4;
+}  // namespace skinny
+
+template <typename T, int MB>
+__global__ __launch_bounds__(64 * skinny::NW) void gemm_skinny_kernel(GemmArgs g) {
+  __shared__ float part[skinny::NW * MB * 16 * 64];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t n0 = (int64_t)blockIdx.x * 32;
+  const int nsteps = (int)((g.K + 15) / 16);
+  const int per = (nsteps + skinny::NW - 1) / skinny::NW;
+  const int s0 = wave * per, s1 = min(nsteps, s0 + per);
+  const int kl = 8 * (lane >> 5);
+  const int64_t n = n0 + (lane & 31);
+  const bool n_ok = n < g.N;
+  const uint16_t* brow = (const uint16_t*)g.b + (n_ok ? n : 0) * g.sb_n + kl;
+  const uint16_t* arow[MB];
+  bool m_ok[MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) {
+    const int64_t m = 32 * i + (lane & 31);
+    m_ok[i] = m < g.M;
+    arow[i] = (const uint16_t*)g.a + (m_ok[i] ? m : 0) * g.sa_m + kl;
+  }
+  typedef typename mfma_traits<T>::frag frag;
+  // Step s: this lane's 8 k of a row of each a block and of a column of b (zeros past M, N, K;
+  // K is a multiple of 8, so a lane's 8 k are all inside or all outside).
+  auto load = [&](int st, frag (&fa)[MB], frag& fb) {
+    const int64_t k = (int64_t)st * 16;
+    const bool k_ok = k + kl < g.K;
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    fb = __builtin_bit_cast(frag, n_ok && k_ok ? *(const u32x4*)(brow + k) : z);
+#pragma unroll
+    for (int i = 0; i < MB; ++i) fa[i] = __builtin_bit_cast(frag, m_ok[i] && k_ok ? *(const u32x4*)(arow[i] + k) : z);
+  };
+  floatx16 acc[MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
+  frag fa[skinny::STEPS][MB], fb[skinny::STEPS];
+#pragma unroll
+  for (int j = 0; j < skinny::STEPS; ++j)
+    if (s0 + j < s1) load(s0 + j, fa[j], fb[j]);
+  for (int st = s0; st < s1; st += skinny::STEPS) {
+#pragma unroll
+    for (int j = 0; j < skinny::STEPS; ++j) {
+      if (st + j < s1) {
+#pragma unroll
+        for (int i = 0; i < MB; ++i) acc[i] = mfma_traits<T>::mma(fa[j][i], fb[j], acc[i]);
+        if (st + j + skinny::STEPS < s1) load(st + j + skinny::STEPS, fa[j], fb[j]);
+      }
+    }
+  }
+  // Sum the eight waves' partial tiles: acc[i][r] of lane l is C[32 i + acc_row(r, l)][n0 + l % 32].
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) part[((wave * MB + i) * 16 + r) * 64 + lane] = acc[i][r];
+  __syncthreads();
+  for (int e = tid; e < MB * 16 * 64; e += 64 * skinny::NW) {
+    const int l = e & 63, ir = e >> 6, i = ir >> 4, r = ir & 15;
+    float v = 0.0f;
+#pragma unroll
+    for (int w = 0; w < skinny::NW; ++w) v += part[((w * MB + i) * 16 + r) * 64 + l];
+    const int64_t row = 32 * i + acc_row(r, l), col = n0 + (l & 31);
+    if (row < g.M && col < g.N) {
+      float out = g.alpha * round_through(v, g.round_dtype);
+      if (g.c) out += g.beta * load_c<false>(g, row * g.sc_m + col * g.sc_n);
+      store_from_float(g.out, row * g.so_m + col * g.so_n, g.out_dtype, out);
+    }
+  }
+}
+
 // ----------------------------------------------------------------------------- fp32
 constexpr int F32_TM = 32, F32_TN = 32, F32_KC = 256;
 constexpr int F32_AS = F32_KC + 4;  // a chunk row stride (floats): 16-byte aligned rows
@@ -1311,15 +1394,15 @@ __global__ void gemm_k0_kernel(GemmArgs g) {
 
 // config: 0 = the fastest kernel whose conditions hold; 1 = the DMA kernel, 2 = the
 // register-staged eight-wave kernel, 3 = the element-wise loader kernel (any strides), 4 =
-// the DMA kernel on 128 x 128 tiles: a forced kernel whose conditions do not hold is
-// rejected before anything is launched.  Config 0 takes the 128 x 128 tiles when they fit
+// the DMA kernel on 128 x 128 tiles, 5 = the few-rows kernel (M <= 64, b^T rows): a forced
+// kernel whose conditions do not hold is rejected before anything is launched.  Config 0 takes the 128 x 128 tiles when they fit
 // and the output has fewer than DMA128_BELOW tiles of 256 x 256: measured fp16, the
 // 128-wide kernel wins up to 128 such tiles (2048^3 729 against 412 TFLOP/s, 8192 x 1024 x
 // 8192 814 against 770) and loses from 144 (3072^3 681 against 849).
 constexpr int64_t DMA128_BELOW = 136;
 template <typename T>
 static int gemm16_launch(GemmArgs g, hipStream_t stream, int config = 0) {
-  if (config < 0 || config > 4) return NT_ERR_INVALID;
+  if (config < 0 || config > 5) return NT_ERR_INVALID;
   if (int e = gemm_check(g)) return e;
   if (!valid_dtype(g.c_dtype)) return NT_ERR_INVALID;  // an fp8 c goes with fp8 operands
   if (g.M == 0 || g.N == 0) return 0;
@@ -1364,7 +1447,25 @@ static int gemm16_launch(GemmArgs g, hipStream_t stream, int config = 0) {
                          g.K >= 3 * 32 && !dma128_nn;
   const int64_t tiles128 = cdiv(g.M, 128) * cdiv(g.N, 128);
   const bool ok128 = (dma128_nn || dma128_bt) && out_vec && c_vec && g.N % 8 == 0 && tiles128 <= 0x7fffffffLL;
-  if ((config == 1 && !dma_ok) || (config == 2 && !fast) || (config == 4 && !ok128)) return NT_ERR_INVALID;
+  // gemm_skinny_kernel: at most 64 rows, a and b^T rows k-contiguous with 16-byte aligned rows.
+  const bool skinny = g.M <= 64 && g.sa_k == 1 && g.sb_k == 1 && g.sa_m >= 0 && g.sb_n > 0 && (uintptr_t)g.a % 16 == 0 &&
+                      (uintptr_t)g.b % 16 == 0 && g.sa_m % 8 == 0 && g.sb_n % 8 == 0 && g.K % 8 == 0 &&
+                      cdiv(g.N, 32) <= 0x7fffffffLL;
+  if ((config == 1 && !dma_ok) || (config == 2 && !fast) || (config == 4 && !ok128) || (config == 5 && !skinny))
+    return NT_ERR_INVALID;
+  // Default: up to 32 rows, or up to 64 with N <= 4096.  At 64 rows every workgroup re-reads
+  // a panel of a as large as its share of b, and the 128-wide tiles win for wide N (fp16,
+  // interleaved medians, few-rows / 128-wide / torch: 1 x 4096 x 4096 11.6 / 29.4 / 21.4 us;
+  // 16 x 4096 x 4096 14.7 / 30.7 / 21.3; 8 x 11008 x 4096 26.9 / 32.1 / 21.6; 64 x 4096 x 4096
+  // 26.6 / 32.6 / 21.4; 64 x 11008 x 4096 52.5 / 33.9 / 21.5).
+  if (config == 5 || (config == 0 && skinny && (g.M <= 32 || g.N <= 4096))) {
+    const dim3 gridS((unsigned)cdiv(g.N, 32));
+    if (g.M <= 32)
+      hipLaunchKernelGGL((gemm_skinny_kernel<T, 1>), gridS, dim3(64 * skinny::NW), 0, stream, g);
+    else
+      hipLaunchKernelGGL((gemm_skinny_kernel<T, 2>), gridS, dim3(64 * skinny::NW), 0, stream, g);
+    return launch_status();
+  }
   if (config == 4 || (config == 0 && ok128 && tiles_m * tiles_n < DMA128_BELOW)) {
     g.tiles_m = (int)cdiv(g.M, 128);
     g.tiles_n = (int)cdiv(g.N, 128);

@@ -277,8 +277,8 @@ def max_pool2d(x, y, window, stride=None, padding=(0, 0), dilation=(1, 1), confi
 # ------------------------------------------------------------------------ gemm
 # Kernel configurations of the 16-bit GEMM that ``config`` can force (0: the fastest whose
 # conditions hold): the DMA kernel, the register-staged eight-wave kernel, the element-wise
-# loader kernel, the DMA kernel on 128 x 128 tiles.
-GEMM_CONFIGS = (1, 2, 3, 4)
+# loader kernel, the DMA kernel on 128 x 128 tiles, the few-rows kernel (M <= 64, b^T rows).
+GEMM_CONFIGS = (1, 2, 3, 4, 5)
 
 
 def check_gemm(a, b, out, c=None, round_dtype=None, config=0):

@@ -206,8 +206,8 @@ def test_gemm_plans_expand_into_kernel_configs():
     t = torch.empty(512, 512, dtype=torch.float16)
     ctx = h._kernel.context({"lhs": t, "rhs": t, "output": t}, {})
     described = [p.describe() for p in families.candidates(ctx)]
-    assert [d["family"] for d in described] == ["gemm"] * 4
-    assert [d["config"] for d in described] == [1, 2, 3, 4]
+    assert [d["family"] for d in described] == ["gemm"] * 5
+    assert [d["config"] for d in described] == [1, 2, 3, 4, 5]
     assert "config" not in families.select(ctx).describe()  # untuned: the library picks
 
 

@@ -415,6 +415,44 @@ def test_gemm_dma128(mnk, dtype, bt):
     assert torch.allclose(out2.float(), a.float() @ b.float(), atol=tol, rtol=1e-2)
 
 
+@pytest.mark.parametrize("dtype", (torch.float16, torch.bfloat16))
+@pytest.mark.parametrize("mnk", ((1, 4096, 4096), (7, 100, 72), (32, 4096, 11008), (33, 256, 8), (64, 1000, 520),
+                                 (2, 32, 4104)))
+def test_gemm_few_rows(mnk, dtype):
+    # The few-rows kernel (forced; also the default here): M <= 64 against b^T rows, ragged N
+    # and K (multiples of 8, a last 16-deep step half past K), with c, alpha and beta, and an
+    # fp32 out; out a view whose neighbours must stay untouched.
+    m, n, k = mnk
+    a = _randn((m, k), dtype, 110, 1.0 / math.sqrt(k))
+    b = _randn((n, k), dtype, 111).t()
+    c = _randn((m, n), dtype, 112)
+    rd = torch.float16 if dtype == torch.float16 else None
+    obuf = torch.full((m + 1, n + 3), 7.0, dtype=dtype, device=DEV)
+    out = obuf[:m, :n]
+    kernels.gemm(a, b, out, c=c, alpha=0.5, beta=2.0, round_dtype=rd, config=5)
+    ref = _gemm_ref(a, b.contiguous(), c, 0.5, 2.0, rd)
+    assert torch.allclose(out.float(), ref.float(), atol=2e-2, rtol=1e-2)
+    assert torch.all(obuf[:, n:] == 7.0) and torch.all(obuf[m:] == 7.0)
+    out0 = torch.empty((m, n), dtype=dtype, device=DEV)
+    kernels.gemm(a, b, out0, c=c, alpha=0.5, beta=2.0, round_dtype=rd)
+    assert torch.equal(out0, out)
+    out32 = torch.empty((m, n), dtype=torch.float32, device=DEV)
+    kernels.gemm(a, b, out32, config=5)
+    assert torch.allclose(out32, a.float() @ b.float(), atol=1e-3, rtol=1e-3)
+
+
+def test_gemm_few_rows_rejects_unfit_calls():
+    from ninetoothed_amd.errors import KernelLaunchError
+
+    a, bt = _randn((65, 256), torch.float16, 113), _randn((128, 256), torch.float16, 114)
+    out = torch.full((65, 128), 7.0, dtype=torch.float16, device=DEV)
+    with pytest.raises(KernelLaunchError):  # 65 rows
+        kernels.gemm(a, bt.t(), out, config=5)
+    with pytest.raises(KernelLaunchError):  # b row-major
+        kernels.gemm(a[:64], _randn((256, 128), torch.float16, 115), out[:64], config=5)
+    assert torch.all(out == 7.0)
+
+
 def test_gemm_dma128_rejects_what_its_epilogue_cannot_store():
     from ninetoothed_amd.errors import KernelLaunchError
 
