@@ -943,18 +943,22 @@ __global__ __launch_bounds__(256) void gemm_dma128_kernel(GemmArgs g) {
 // Few rows (M <= 64) against k-contiguous b (b^T rows, x @ w.t(): a linear layer on a few
 // tokens).  The product reads b once and is bound by streaming it, which the 128-wide tiles
 // spread over too few workgroups (N / 128).  Here a workgroup owns 32 columns (32 rows of
-// b^T) and every row of a; its eight waves take contiguous eighths of K and load their MFMA
-// fragments straight from memory (a lane's row of a, or column of b, at k 8 (lane / 32) ..
-// + 7 of each 16-deep step: 16 bytes per operand), MB 32-row blocks of a against the one
-// block of b^T per step, four steps in flight.  The eight partial 32 x 32 tiles are then
-// summed through LDS and finished element by element (alpha, round, beta c, any out type).
+// b^T) and one 32-row block of a (blockIdx.y); its eight waves take contiguous eighths of K
+// and load their MFMA fragments straight from memory (a lane's row of a, or column of b, at
+// k 8 (lane / 32) .. + 7 of each 16-deep step: 16 bytes per operand), four steps in flight.
+// The eight partial 32 x 32 tiles are then summed through LDS and finished element by
+// element (alpha, round, beta c, any out type).  One row block per workgroup rather than
+// both in one: 64 x 4096 x 4096 fp16 18.8 against 26.9 us (more workgroups, half the work
+// each).
 namespace skinny {
 constexpr int NW = 8, STEPS = 4;
 }  // namespace skinny
 
-template <typename T, int MB>
+template <typename T>
 __global__ __launch_bounds__(64 * skinny::NW) void gemm_skinny_kernel(GemmArgs g) {
+  constexpr int MB = 1;  // 32-row blocks of a per workgroup
   __shared__ float part[skinny::NW * MB * 16 * 64];
+  const int64_t m0 = 32 * (int64_t)blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t n0 = (int64_t)blockIdx.x * 32;
@@ -969,7 +973,7 @@ __global__ __launch_bounds__(64 * skinny::NW) void gemm_skinny_kernel(GemmArgs g
   bool m_ok[MB];
 #pragma unroll
   for (int i = 0; i < MB; ++i) {
-    const int64_t m = 32 * i + (lane & 31);
+    const int64_t m = m0 + 32 * i + (lane & 31);
     m_ok[i] = m < g.M;
     arow[i] = (const uint16_t*)g.a + (m_ok[i] ? m : 0) * g.sa_m + kl;
   }
@@ -1014,7 +1018,7 @@ __global__ __launch_bounds__(64 * skinny::NW) void gemm_skinny_kernel(GemmArgs g
     float v = 0.0f;
 #pragma unroll
     for (int w = 0; w < skinny::NW; ++w) v += part[((w * MB + i) * 16 + r) * 64 + l];
-    const int64_t row = 32 * i + acc_row(r, l), col = n0 + (l & 31);
+    const int64_t row = m0 + 32 * i + acc_row(r, l), col = n0 + (l & 31);
     if (row < g.M && col < g.N) {
       float out = g.alpha * round_through(v, g.round_dtype);
       if (g.c) out += g.beta * load_c<false>(g, row * g.sc_m + col * g.sc_n);
@@ -1453,17 +1457,14 @@ static int gemm16_launch(GemmArgs g, hipStream_t stream, int config = 0) {
                       cdiv(g.N, 32) <= 0x7fffffffLL;
   if ((config == 1 && !dma_ok) || (config == 2 && !fast) || (config == 4 && !ok128) || (config == 5 && !skinny))
     return NT_ERR_INVALID;
-  // Default: up to 32 rows, or up to 64 with N <= 4096.  At 64 rows every workgroup re-reads
-  // a panel of a as large as its share of b, and the 128-wide tiles win for wide N (fp16,
-  // interleaved medians, few-rows / 128-wide / torch: 1 x 4096 x 4096 11.6 / 29.4 / 21.4 us;
-  // 16 x 4096 x 4096 14.7 / 30.7 / 21.3; 8 x 11008 x 4096 26.9 / 32.1 / 21.6; 64 x 4096 x 4096
-  // 26.6 / 32.6 / 21.4; 64 x 11008 x 4096 52.5 / 33.9 / 21.5).
+  // Default: up to 32 rows, or up to 64 with N <= 4096; past 32 rows with wide N the 128-wide
+  // tiles win (fp16, interleaved medians, few-rows / 128-wide / torch: 1 x 4096 x 4096
+  // 11.6 / 29.4 / 21.4 us; 16 x 4096 x 4096 14.8 / 30.3 / 19.9; 8 x 11008 x 4096 26.9 / 32.1 /
+  // 21.6; 64 x 4096 x 4096 18.8 / 32.6 / 21.4; 64 x 4096 x 11008 48.2 / 84.2 / 30.5; 33 x 11008 x
+  // 4096 47.6 / 33.1 / 21.7).
   if (config == 5 || (config == 0 && skinny && (g.M <= 32 || g.N <= 4096))) {
-    const dim3 gridS((unsigned)cdiv(g.N, 32));
-    if (g.M <= 32)
-      hipLaunchKernelGGL((gemm_skinny_kernel<T, 1>), gridS, dim3(64 * skinny::NW), 0, stream, g);
-    else
-      hipLaunchKernelGGL((gemm_skinny_kernel<T, 2>), gridS, dim3(64 * skinny::NW), 0, stream, g);
+    const dim3 gridS((unsigned)cdiv(g.N, 32), (unsigned)cdiv(g.M, 32));
+    hipLaunchKernelGGL((gemm_skinny_kernel<T>), gridS, dim3(64 * skinny::NW), 0, stream, g);
     return launch_status();
   }
   if (config == 4 || (config == 0 && ok128 && tiles_m * tiles_n < DMA128_BELOW)) {
