@@ -34,6 +34,9 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only name,...] [--
        [--cold] [--no-graph]
        python bench.py --trace-summary <rocprofv3 kernel_trace.csv> --only <config> --warmup W --steps K
        (per-kernel durations over the K timed steps of a traced run of that configuration)
+       python bench.py --mfma-ceiling   (bare MFMAs back to back, zero and random operands)
+       python bench.py --power-probe    (the headline addmm and attention over sustained calls after idle,
+                                         random and zero operands: the power limit's share of their rates)
 """
 
 import argparse
